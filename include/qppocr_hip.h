@@ -1,0 +1,272 @@
+/*
+ * qppocr_hip.h -- C ABI of the MI355X (gfx950) HIP backend for the
+ * qppocr-kernels operator set and the det/rec session built on it.
+ *
+ * Plain C99 types only.  Every call returns an int status: QPH_OK (0) or a
+ * negative code; qph_last_error() returns the message of the calling
+ * thread's last failure.  Nothing aborts or throws across this boundary.
+ * Tensor pointers are device pointers unless a name says _host.  Layouts are
+ * the reference's: contiguous row-major NCHW activations, ONNX weight layouts.
+ * A context owns one HIP stream; every operator call is enqueued on it
+ * (asynchronous with respect to the host; qph_sync waits).
+ *
+ * Numerics: outputs are bit-identical to the qppocr-kernels CPU path for the
+ * same inputs (same fma chains in the same order, same polynomial exp/erf).
+ */
+#ifndef QPPOCR_HIP_H
+#define QPPOCR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define QPH_API __attribute__((visibility("default")))
+#else
+#define QPH_API
+#endif
+
+/* status codes (mirror qppocr-core/src/error.rs:343-353: Graph / Device errors) */
+#define QPH_OK 0
+#define QPH_EINVAL -1        /* bad shape / argument (Error::Graph) */
+#define QPH_EHIP -2          /* HIP runtime failure (Error::Device) */
+#define QPH_EUNSUPPORTED -3  /* operator form the backend does not implement */
+#define QPH_ENOMEM -4
+
+/* ------------------------------------------------------------- context */
+
+typedef struct qph_ctx qph_ctx;
+
+/* Device context + stream: the DeviceContext analogue
+ * (qppocr-core/src/device.rs:83-101).  device = HIP device ordinal. */
+QPH_API int qph_ctx_create(int device, qph_ctx** out);
+QPH_API int qph_ctx_destroy(qph_ctx* ctx);
+/* Use an external HIP stream (e.g. a framework's current stream) instead of
+ * the context's own; NULL restores the context's stream. */
+QPH_API int qph_ctx_set_stream(qph_ctx* ctx, void* hip_stream);
+QPH_API void* qph_ctx_stream(qph_ctx* ctx);
+QPH_API int qph_sync(qph_ctx* ctx);
+/* Thread-local message of the last failed call (empty string if none). */
+QPH_API const char* qph_last_error(void);
+QPH_API const char* qph_version(void);
+
+/* device memory (the library never frees caller memory) */
+QPH_API int qph_malloc(qph_ctx* ctx, void** ptr, size_t bytes);
+QPH_API int qph_free(qph_ctx* ctx, void* ptr);
+QPH_API int qph_memcpy_h2d(qph_ctx* ctx, void* dst, const void* src_host, size_t bytes);
+QPH_API int qph_memcpy_d2h(qph_ctx* ctx, void* dst_host, const void* src, size_t bytes);
+QPH_API int qph_memset(qph_ctx* ctx, void* dst, int value, size_t bytes);
+
+/* ------------------------------------------------------------ operators */
+
+/* ConvParams (qppocr-kernels/src/conv.rs:124-143). */
+typedef struct {
+  int64_t sh, sw;   /* stride */
+  int64_t ph, pw;   /* begin padding */
+  int64_t peh, pew; /* end padding */
+  int64_t dh, dw;   /* dilation (must be 1, conv.rs:149) */
+  int64_t group;
+} qph_conv_params;
+
+/* Activation folded into a producer: superset of
+ * qppocr-kernels/src/activation.rs:75-95 (None | Gelu(c1,c2,c3) | Relu) plus
+ * the HardSigmoid+Mul pair (hardswish, alpha=c1 beta=c2; executor.rs:746-758)
+ * and Sigmoid (executor.rs:737-745), each with the standalone op's arithmetic. */
+#define QPH_ACT_NONE 0
+#define QPH_ACT_GELU 1
+#define QPH_ACT_RELU 2
+#define QPH_ACT_HARDSWISH 3
+#define QPH_ACT_SIGMOID 4
+typedef struct {
+  int32_t kind;
+  float c1, c2, c3;
+} qph_act;
+
+/* conv2d_out_shape (qppocr-kernels/src/conv.rs:146-156). */
+QPH_API int qph_conv2d_out_shape(const int64_t xs[4], const int64_t ws[4],
+                                 const qph_conv_params* p, int64_t ys[4]);
+
+/* conv2d_res_into (qppocr-kernels/src/conv.rs:222-715): y = act(conv(x, w) +
+ * bias) (+ residual).  Dispatch as the reference: 1x1 s1 g1 -> GEMM,
+ * depthwise (g > 1, C/g == 1) -> direct, else implicit GEMM.  bias,
+ * residual and act may be NULL.  ys_out (may be NULL) receives the shape. */
+QPH_API int qph_conv2d(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
+                       const int64_t ws[4], const float* bias, const qph_conv_params* p,
+                       const qph_act* act, const float* residual, float* y, int64_t ys_out[4]);
+
+/* Epilogue placement for the fused det neck (no reference counterpart as one
+ * call; it is the reference's Conv -> Resize(nearest) -> Add / Concat node
+ * sequence, qppocr-core/src/executor.rs:433-652, 885-951, 1889-1916, with
+ * identical per-element arithmetic):
+ *   res_up   residual is a coarse map at half resolution, added via nearest
+ *            2x upsample (resize.rs:26-57 with oh = 2h); 0 = same shape.
+ *   y_ctotal/y_coff  write into channels [y_coff, y_coff+M) of a tensor with
+ *            y_ctotal channels (Concat along C); 0/0 = plain output.
+ *   y_up     replicate each output pixel y_up x y_up times (nearest upsample
+ *            of the result by an integer factor); 1 = none.
+ *   trans_out (1x1 only) store the output as [N][oh*ow][M] (the rec
+ *            backbone's [B,C,1,T] -> [B,T,C] reshape/transpose). */
+typedef struct {
+  const float* residual;
+  int32_t res_up;
+  int64_t y_ctotal, y_coff, y_up;
+  int32_t trans_out;
+} qph_conv_epilogue;
+QPH_API int qph_conv2d_ex(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
+                          const int64_t ws[4], const float* bias, const qph_conv_params* p,
+                          const qph_act* act, const qph_conv_epilogue* ep, float* y);
+
+/* convtranspose2d, 2x2 s2 p0 only, no bias (qppocr-kernels/src/conv.rs:730-804).
+ * w: ONNX [Ci, Co, 2, 2]. */
+QPH_API int qph_convtranspose2d(qph_ctx* ctx, const float* x, const int64_t xs[4],
+                                const float* w, const int64_t ws[4], int64_t sh, int64_t sw,
+                                int64_t ph, int64_t pw, float* y, int64_t ys_out[4]);
+/* Two chained 2x2 s2 ConvTranspose nodes then Sigmoid in one pass (the det
+ * head tail: executor.rs:654-687 twice, then executor.rs:737-745).
+ * w1 [C, M1, 2, 2], w2 [M1, 1, 2, 2]; y [N, 1, 4H, 4W]. */
+QPH_API int qph_convt2x2_pair_sigmoid(qph_ctx* ctx, const float* x, const int64_t xs[4],
+                                      const float* w1, const int64_t w1s[4], const float* w2,
+                                      const int64_t w2s[4], float* y);
+
+/* sgemm / sgemm_res (qppocr-kernels/src/gemm.rs:37-70): C[M,N] (row stride
+ * ldc) = A[M,K] B[K,N], bias per row placed as the reference does, then act,
+ * then += residual (C's layout).  serial selects the reference's serial panel
+ * path (sgemm_serial*, gemm.rs:138-168) for the bias-placement rule. */
+QPH_API int qph_sgemm(qph_ctx* ctx, const float* a, const float* b, float* c, int64_t m,
+                      int64_t n, int64_t k, int64_t ldc, const float* bias, const qph_act* act,
+                      const float* residual, int32_t serial);
+
+/* MatMul (qppocr-kernels/src/shape.rs:568-698) for a [batch, M, K] x b
+ * [K, N] (b_shared = 1) or b [batch, K, N]; no bias. */
+QPH_API int qph_matmul(qph_ctx* ctx, const float* a, const float* b, float* out, int64_t batch,
+                       int64_t m, int64_t k, int64_t n, int32_t b_shared);
+
+/* The rec linear: MatMul x[R,K] . w[K,N] then Add(bias[N]) then act then
+ * Add(residual[R,N]) (executor.rs:1559-1580 MatMul, 885-951 Add,
+ * 759-768 FusedGelu) in one kernel. */
+QPH_API int qph_linear(qph_ctx* ctx, const float* x, const float* w, const float* bias,
+                       int64_t rows, int64_t k, int64_t n, const qph_act* act,
+                       const float* residual, float* y);
+
+/* LayerNorm as the exported ReduceMean/Sub/Pow/ReduceMean/Add/Sqrt/Div/Mul/Add
+ * chain over the last axis (shape.rs:510-560 f64 means, elementwise.rs). */
+QPH_API int qph_layernorm(qph_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                          float eps, int64_t rows, int64_t cols, float* y);
+
+/* softmax_last_dim in place (qppocr-kernels/src/activation.rs:321-403). */
+QPH_API int qph_softmax_last_dim(qph_ctx* ctx, float* t, int64_t rows, int64_t inner);
+
+/* Row softmax then per-row argmax, the rec head's Softmax node followed by
+ * the CTC argmax (activation.rs:321-403; qppocr-core/src/pipeline/rec.rs:34-90).
+ * probs may be NULL (pairs only); pairs[2r] = max prob, pairs[2r+1] = index
+ * as u32 bits stored in an f32 slot (device.rs:160-165). */
+QPH_API int qph_softmax_argmax(qph_ctx* ctx, const float* logits, int64_t rows, int64_t cols,
+                               float* probs, float* pairs);
+
+/* CTC greedy argmax over probabilities (rec.rs:46-54): first strict max,
+ * ties to the lowest index.  t_valid (may be NULL) masks steps t >= t_valid[b]
+ * of batch item b (rows = batch * t_len) to (0, blank). */
+QPH_API int qph_ctc_argmax(qph_ctx* ctx, const float* probs, int64_t batch, int64_t t_len,
+                           int64_t cols, const int32_t* t_valid_host, float* pairs);
+
+/* Multi-head self-attention core of the rec encoder on a packed qkv
+ * [B, T, 3, heads, dh] (the QKV MatMul output): q*scale, q.k^T, Softmax,
+ * .v, transposed back to [B, T, heads*dh] (shape.rs:664-697 small matmul
+ * path, activation.rs:321-403). */
+QPH_API int qph_attention(qph_ctx* ctx, const float* qkv, int64_t batch, int64_t t,
+                          int64_t heads, int64_t dh, float scale, float* out);
+
+/* Standalone activations (activation.rs:232-276; executor.rs:732-768). */
+QPH_API int qph_activation(qph_ctx* ctx, const float* x, float* y, int64_t n,
+                           const qph_act* act);
+/* HardSigmoid(alpha, beta) node (activation.rs:243-251). */
+QPH_API int qph_hardsigmoid(qph_ctx* ctx, const float* x, float* y, int64_t n, float alpha,
+                            float beta);
+/* resize_nearest (qppocr-kernels/src/resize.rs:8-57). */
+QPH_API int qph_resize_nearest(qph_ctx* ctx, const float* x, int64_t nc, int64_t h, int64_t w,
+                               int64_t oh, int64_t ow, float* y);
+/* Broadcast binary op in place on a[rows, cols] (elementwise.rs:185-298):
+ * op 0 add, 1 sub, 2 mul, 3 div; bmode 0 = b[rows] (per row), 1 = b[cols]
+ * (per column), 2 = scalar b[0], 3 = same shape. */
+QPH_API int qph_binary_inplace(qph_ctx* ctx, float* a, const float* b, int64_t rows,
+                               int64_t cols, int32_t op, int32_t bmode);
+/* reduce_mean over the last axis (shape.rs:510-560, f64 accumulation). */
+QPH_API int qph_reduce_mean_last(qph_ctx* ctx, const float* x, int64_t rows, int64_t cols,
+                                 float* out);
+
+/* ------------------------------------------------------------- session */
+
+/* A static det or rec graph (the optimised graph the DeviceContext receives,
+ * qppocr-core/src/device.rs:83-101) as a node list over numbered tensors.
+ * Tensor 0 is the graph input; the node list is topologically ordered. */
+#define QPH_OP_CONV 1          /* x -> y; w, bias; qph_conv_params; act; epilogue fields */
+#define QPH_OP_CONVT_PAIR_SIG 2 /* x -> y; w (first ConvT), w2 (second ConvT); then sigmoid */
+#define QPH_OP_LINEAR 3        /* x [R,K] -> y [R,N]; w [K,N]; bias [N]; act; residual tensor */
+#define QPH_OP_LAYERNORM 4     /* x -> y; w = gamma, bias = beta; eps */
+#define QPH_OP_ATTENTION 5     /* qkv -> y; heads, dh, scale */
+#define QPH_OP_SOFTMAX_ARGMAX 6 /* logits -> probs (y, optional) and pairs (y2) */
+#define QPH_OP_CONVT 7         /* x -> y; w [Ci, Co, 2, 2] */
+#define QPH_OP_ACT 8           /* x -> y; act */
+
+typedef struct {
+  int32_t op;
+  int32_t in;       /* input tensor id */
+  int32_t in2;      /* residual / second input tensor id, -1 if none */
+  int32_t out;      /* output tensor id */
+  int32_t out2;     /* second output tensor id (pairs), -1 if none */
+  int32_t w, bias, w2;  /* weight indices, -1 if none */
+  int64_t ws[4];    /* weight shape of w */
+  int64_t w2s[4];   /* weight shape of w2 */
+  qph_conv_params cp;
+  qph_act act;
+  int32_t res_up;
+  int32_t trans_out;
+  int64_t y_ctotal, y_coff, y_up;
+  int64_t heads, dh;
+  float eps, scale;
+} qph_node;
+
+/* Tensor table: shape per tensor id (rank 4, unused trailing dims = 1).
+ * alias[i] >= 0 makes tensor i share tensor alias[i]'s storage (Concat
+ * slots written through y_ctotal/y_coff). */
+typedef struct {
+  int32_t n_tensors;
+  const int64_t* shapes;  /* n_tensors * 4 */
+  const int32_t* alias;   /* n_tensors, -1 = own storage */
+  int32_t n_nodes;
+  const qph_node* nodes;
+  int32_t n_weights;
+  const int64_t* weight_sizes;  /* floats per weight */
+  int32_t n_outputs;
+  const int32_t* outputs;       /* graph output tensor ids */
+} qph_net_spec;
+
+typedef struct qph_net qph_net;
+
+/* create_session (device.rs:88-101): validates every node (unsupported ->
+ * QPH_EUNSUPPORTED naming the node), copies the weights to device memory
+ * owned by the net and plans the activation arena. */
+QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
+                           const float* const* weights_host, qph_net** out);
+QPH_API int qph_net_destroy(qph_net* net);
+/* DeviceSession::run (device.rs:130): input from the host (or device when
+ * input_is_device), outputs copied to the host buffers (sizes from the
+ * tensor table) unless outputs_host is NULL.  The kernel sequence is
+ * captured into a HIP graph on the first run and replayed afterwards. */
+QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_device,
+                        float* const* outputs_host);
+/* Device pointer of a tensor of the net (valid until destroy). */
+QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* numel);
+/* Average device time (ms) of each node over the runs since the last reset
+ * when profiling is on (events around each node; graph replay disabled). */
+QPH_API int qph_net_set_profiling(qph_net* net, int32_t on);
+QPH_API int qph_net_node_times(qph_net* net, double* ms_per_node, int32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QPPOCR_HIP_H */

@@ -1,0 +1,129 @@
+"""CPU oracle executor for the det/rec graphs of qppocr_amd.nets.
+
+TEST INFRASTRUCTURE ONLY (the checker and the timed CPU baseline).
+
+Each fused node of the HIP graph is run here as the sequence of separate
+nodes the reference CPU executor runs (qppocr-core/src/executor.rs:433-1660),
+each rounding to f32 and each through the oracle's restatement of the
+kernel it calls:
+  Conv  (+ReLU/GELU fused only for group 1, optimize.rs:337-427; +residual,
+        optimize.rs:662-772)                     -> conv2d (conv.rs:222-715)
+  hardswish                                      -> HardSigmoid node, Mul node
+  Resize(nearest 2x) + Add (FPN top-down)        -> resize_nearest, Add
+  Resize(nearest)xf + Concat (FPN fuse)          -> resize_nearest, Concat
+  Reshape/Transpose [B,C,1,T] -> [B,T,C]         -> transpose (exact copy)
+  LayerNorm                                      -> ReduceMean..Add chain
+  MatMul + Add(bias) [+ FusedGelu] [+ Add(res)]  -> matmul, Add, gelu, Add
+  attention                                      -> Mul(scale), MatMul, Softmax, MatMul
+  ConvTranspose x2 + Sigmoid                     -> convtranspose2d x2, sigmoid
+  Softmax + CTC argmax                           -> softmax_last_dim, ctc argmax
+"""
+import numpy as np
+
+from . import oracle as O
+
+# op codes of include/qppocr_hip.h
+OP_CONV, OP_CONVT_PAIR_SIG, OP_LINEAR, OP_LAYERNORM, OP_ATTENTION = 1, 2, 3, 4, 5
+OP_SOFTMAX_ARGMAX, OP_CONVT, OP_ACT = 6, 7, 8
+
+
+def _act_nodes(y, act):
+    """The activation as the reference graph applies it after a Conv / MatMul."""
+    if act == O.ACT_HARDSWISH:
+        hs = O.hardsigmoid(y, O.HS_ALPHA, O.HS_BETA)
+        return O.binary_flat(y, hs, 2)          # Mul node
+    if act == O.ACT_RELU:
+        return O.relu_inplace(y.copy())
+    if act == O.ACT_GELU:
+        return O.gelu_inplace(y.copy())
+    if act == O.ACT_SIGMOID:
+        return O.sigmoid_tensor(y)
+    return y
+
+
+def run_graph(g, x_in, keep=False):
+    """Runs graph g on the CPU oracle; returns the outputs (and all tensors if keep)."""
+    T = {0: np.ascontiguousarray(x_in, dtype=np.float32).reshape(g.shapes[0])}
+    W = g.weights
+    for d in g.nodes:
+        op = d["op"]
+        x = T[d["inp"]]
+        if op == OP_CONV:
+            m, cg, kh, kw = d["ws"]
+            sh, sw, ph, pw, peh, pew, _, _, grp = d["cp"]
+            params = O.conv_params(sh, sw, ph, pw, peh, pew, grp)
+            w = W[d["w"]].reshape(m, cg, kh, kw)
+            b = W[d["bias"]] if d["bias"] >= 0 else None
+            fused = d["act"] if (grp == 1 and d["act"] in (O.ACT_RELU, O.ACT_GELU)) else O.ACT_NONE
+            y = O.conv2d(x.reshape(g.shapes[d["inp"]]), w, b, params, fused)
+            if fused == O.ACT_NONE:
+                y = _act_nodes(y, d["act"])
+            if d["in2"] >= 0:
+                r = T[d["in2"]].reshape(g.shapes[d["in2"]])
+                if d["res_up"] == 2:
+                    r = O.resize_nearest(r, y.shape[2], y.shape[3])
+                y = O.binary_flat(y, r, 0)        # Add node
+            if d["trans_out"]:
+                n, c, oh, ow = y.shape
+                y = np.ascontiguousarray(y.reshape(n, c, oh * ow).transpose(0, 2, 1))
+            if d["y_ctotal"]:
+                up = d["y_up"]
+                if up != 1:
+                    y = O.resize_nearest(y, y.shape[2] * up, y.shape[3] * up)
+                out = T.get(d["out"])
+                if out is None:
+                    out = np.zeros(g.shapes[d["out"]], dtype=np.float32)
+                    T[d["out"]] = out
+                c0 = d["y_coff"]
+                out[:, c0:c0 + y.shape[1]] = y     # Concat slot
+            else:
+                T[d["out"]] = y.reshape(g.shapes[d["out"]])
+        elif op == OP_CONVT_PAIR_SIG:
+            w1 = W[d["w"]].reshape(d["ws"])
+            w2 = W[d["w2"]].reshape(d["w2s"])
+            y = O.convtranspose2d(x.reshape(g.shapes[d["inp"]]), w1)
+            y = O.convtranspose2d(y, w2)
+            T[d["out"]] = O.sigmoid_tensor(y)
+        elif op == OP_LINEAR:
+            k, n = d["ws"][0], d["ws"][1]
+            rows = x.size // k
+            y = O.matmul(x.reshape(rows, k), W[d["w"]].reshape(k, n))
+            if d["bias"] >= 0:
+                y = O.binary_bcast(y, W[d["bias"]], rows, n, 0, 1)
+            y = _act_nodes(y, d["act"])
+            if d["in2"] >= 0:
+                y = O.binary_flat(y, T[d["in2"]].reshape(rows, n), 0)
+            T[d["out"]] = y.reshape(g.shapes[d["out"]])
+        elif op == OP_LAYERNORM:
+            cols = d["ws"][0]
+            y = O.layernorm(x.reshape(-1, cols), W[d["w"]], W[d["bias"]], d["eps"])
+            T[d["out"]] = y.reshape(g.shapes[d["out"]])
+        elif op == OP_ATTENTION:
+            b, t = g.shapes[d["inp"]][0], g.shapes[d["inp"]][1]
+            H, dh = d["heads"], d["dh"]
+            qkv = x.reshape(b, t, 3, H, dh).transpose(2, 0, 3, 1, 4)   # [3, B, H, T, dh]
+            q = np.ascontiguousarray(qkv[0])
+            k = np.ascontiguousarray(qkv[1])
+            v = np.ascontiguousarray(qkv[2])
+            sc = np.full((1,), d["scale"], dtype=np.float32)
+            q = O.binary_bcast(q.reshape(-1, dh), sc, q.size // dh, dh, 2, 2).reshape(q.shape)
+            kt = np.ascontiguousarray(k.transpose(0, 1, 3, 2))          # [B, H, dh, T]
+            s = O.matmul(q, kt)                                         # [B, H, T, T]
+            O.softmax_last_dim(s, t)
+            o = O.matmul(s, v)                                          # [B, H, T, dh]
+            T[d["out"]] = np.ascontiguousarray(o.transpose(0, 2, 1, 3)).reshape(g.shapes[d["out"]])
+        elif op == OP_SOFTMAX_ARGMAX:
+            cols = d["ws"][0]
+            p = x.reshape(-1, cols).copy()
+            O.softmax_last_dim(p, cols)
+            T[d["out"]] = p.reshape(g.shapes[d["out"]])
+            if d["out2"] >= 0:
+                T[d["out2"]] = O.ctc_argmax(p).reshape(g.shapes[d["out2"]])
+        elif op == OP_CONVT:
+            T[d["out"]] = O.convtranspose2d(x.reshape(g.shapes[d["inp"]]), W[d["w"]].reshape(d["ws"]))
+        elif op == OP_ACT:
+            T[d["out"]] = _act_nodes(x.copy(), d["act"])
+        else:
+            raise ValueError(f"oracle executor: unknown op {op}")
+    outs = [T[t].reshape(g.lshapes[t]) for t in g.outputs]
+    return (outs, T) if keep else outs

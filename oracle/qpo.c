@@ -1,0 +1,693 @@
+/*
+ * qpo.c -- CPU oracle: a plain-C restatement of the qppocr-kernels CPU
+ * arithmetic for the det/rec operator set.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP library and
+ * the "port" CPU baseline timed next to it.  Nothing in the product
+ * (qppocr_amd/, include/) links, loads or calls it.
+ *
+ * The reference is Rust (crates/qppocr-kernels); its scalar "judge" kernels
+ * are bit-identical to its AVX2 kernels (qppocr-kernels/src/x86.rs:1-9), so a
+ * scalar C restatement that keeps every fma, every rounding step and every
+ * reduction order reproduces the reference's output bits.  Each function
+ * cites the reference lines it follows.  FTZ|DAZ is set on every worker
+ * thread exactly as the reference executor does (qppocr-kernels/src/par.rs:229-256,
+ * qppocr-core/src/executor.rs:215).
+ *
+ * Threading (OpenMP) only distributes independent output elements; every
+ * output element's arithmetic is fixed, so results do not depend on the
+ * thread count.  Loops are written so gcc -O3 -mavx2 -mfma vectorises them
+ * without changing any element's operation sequence (-ffp-contract=off keeps
+ * every non-fma a*b+c as two roundings, as Rust does).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <xmmintrin.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define QPO_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------ basics */
+
+/* FTZ|DAZ on the calling thread: qppocr-kernels/src/par.rs:229-245. */
+static inline void qpo_ftz(void) { _mm_setcsr(_mm_getcsr() | 0x8040); }
+
+QPO_API int qpo_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+QPO_API void qpo_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
+static inline float bits_f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* exp1: qppocr-kernels/src/activation.rs:28-47 (x86.rs:28-57 exp256_ps).
+ * clamp +-88, k = rint(x*inv_ln2) (ties-even), two fnmadd range-reduction
+ * steps, degree-6 Horner in fma, scale by 2^k built from exponent bits. */
+static inline float exp1(float x) {
+  const float LN2_HI = 0.6931472f;
+  const float LN2_LO = -2.9802322e-8f;
+  const float INV_LN2 = 1.442695f;
+  x = fminf(x, 88.0f);
+  x = fmaxf(x, -88.0f);
+  float kf = rintf(x * INV_LN2);
+  float r = fmaf(-kf, LN2_HI, x);
+  r = fmaf(-kf, LN2_LO, r);
+  float p = 1.0f / 720.0f;
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int32_t ki = (int32_t)kf + 127;
+  return bits_f((uint32_t)ki << 23) * p;
+}
+
+/* erf1: qppocr-kernels/src/activation.rs:53-66 (x86.rs:63-77), A&S 7.1.26. */
+static inline float erf1(float x) {
+  float ax = bits_f(f_bits(x) & 0x7fffffffu);
+  float t = 1.0f / fmaf(0.3275911f, ax, 1.0f);
+  float p = 1.0614054f;
+  p = fmaf(p, t, -1.453152027f);
+  p = fmaf(p, t, 1.421413741f);
+  p = fmaf(p, t, -0.284496736f);
+  p = fmaf(p, t, 0.2548296f);
+  p *= t;
+  float e = exp1(ax * (0.0f - ax));
+  float r = fmaf(-p, e, 1.0f);
+  return bits_f(f_bits(r) | (f_bits(x) & 0x80000000u));
+}
+
+QPO_API float qpo_exp1(float x) { return exp1(x); }
+QPO_API float qpo_erf1(float x) { return erf1(x); }
+
+/* ------------------------------------------------------------- activations */
+
+/* act kinds shared with the HIP library's qph_act:
+ *   0 none, 1 gelu(c1,c2,c3), 2 relu, 3 hardswish(alpha=c1, beta=c2),
+ *   4 sigmoid.
+ * The reference's Activation has only None/Gelu/Relu (activation.rs:75-95);
+ * hardswish and sigmoid are separate graph nodes there (executor.rs:737-758,
+ * 885-951) and are applied here with exactly those nodes' arithmetic. */
+
+/* relu: activation.rs:232-239 (v > 0 ? v : 0, NaN -> 0). */
+static inline float relu1(float v) { return v > 0.0f ? v : 0.0f; }
+
+/* hardsigmoid: activation.rs:168-187 / x86.rs:795-824. */
+static inline float hsig1(float x, float alpha, float beta) {
+  float v = fmaf(x, alpha, beta);
+  return v < 0.0f ? 0.0f : (v > 1.0f ? 1.0f : v);
+}
+
+/* hardswish as the graph composes it: HardSigmoid node then Mul node
+ * (executor.rs:746-758 then elementwise.rs:197-205): y = x * hs(x). */
+static inline float hswish1(float x, float alpha, float beta) { return x * hsig1(x, alpha, beta); }
+
+/* sigmoid: activation.rs:196-201 / x86.rs:828-843. */
+static inline float sigmoid1(float x) { return 1.0f / (1.0f + exp1(-x)); }
+
+/* gelu: activation.rs:209-215 / x86.rs:82-85: (c3*x) * (erf1(x*inv_c1) + c2). */
+static inline float gelu1(float v, float inv_c1, float c2, float c3) {
+  return c3 * v * (erf1(v * inv_c1) + c2);
+}
+
+static inline float act1(float v, int kind, float c1, float c2, float c3, float inv_c1) {
+  switch (kind) {
+    case 1: return gelu1(v, inv_c1, c2, c3);
+    case 2: return relu1(v);
+    case 3: return hswish1(v, c1, c2);
+    case 4: return sigmoid1(v);
+    default: return v;
+  }
+}
+
+/* Apply act (then optional residual add) to a contiguous range, the order of
+ * gemm.rs:478-507 finish_res: act first, then += residual. */
+static void act_res_range(float* y, const float* res, size_t n, int kind, float c1, float c2,
+                          float c3) {
+  float inv_c1 = 1.0f / c1;
+  if (kind != 0)
+    for (size_t i = 0; i < n; i++) y[i] = act1(y[i], kind, c1, c2, c3, inv_c1);
+  if (res)
+    for (size_t i = 0; i < n; i++) y[i] = y[i] + res[i];
+}
+
+QPO_API void qpo_relu_inplace(float* t, int64_t n) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; i++) t[i] = relu1(t[i]);
+}
+
+QPO_API void qpo_hardsigmoid(const float* x, float* y, int64_t n, float alpha, float beta) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; i++) y[i] = hsig1(x[i], alpha, beta);
+}
+
+QPO_API void qpo_sigmoid(const float* x, float* y, int64_t n) {
+#pragma omp parallel
+  {
+    qpo_ftz();
+#pragma omp for schedule(static)
+    for (int64_t i = 0; i < n; i++) y[i] = sigmoid1(x[i]);
+  }
+}
+
+QPO_API void qpo_gelu_inplace(float* t, int64_t n, float c1, float c2, float c3) {
+  float inv_c1 = 1.0f / c1;
+#pragma omp parallel
+  {
+    qpo_ftz();
+#pragma omp for schedule(static)
+    for (int64_t i = 0; i < n; i++) t[i] = gelu1(t[i], inv_c1, c2, c3);
+  }
+}
+
+QPO_API void qpo_erf_inplace(float* t, int64_t n) {
+  for (int64_t i = 0; i < n; i++) t[i] = erf1(t[i]);
+}
+
+/* clip: activation.rs:221-228 (comparison chain, NaN passes through). */
+QPO_API void qpo_clip_inplace(float* t, int64_t n, float lo, float hi) {
+  for (int64_t i = 0; i < n; i++) {
+    float v = t[i];
+    float m = v < lo ? lo : v;
+    t[i] = hi < m ? hi : m;
+  }
+}
+
+/* ----------------------------------------------------------------- softmax */
+
+/* hsum8: activation.rs:313-316, the association of x86.rs:91-97. */
+static inline float hsum8(const float* v) {
+  float t0 = v[0] + v[4], t1 = v[1] + v[5], t2 = v[2] + v[6], t3 = v[3] + v[7];
+  return (t0 + t1) + (t2 + t3);
+}
+
+/* One row: activation.rs:346-403 (scalar mirror of x86.rs:1091-1134). */
+static void softmax_row(float* row, int64_t inner) {
+  int64_t i = 0;
+  float mx;
+  if (inner >= 8) {
+    float vmax[8];
+    for (int j = 0; j < 8; j++) vmax[j] = row[j];
+    while (i + 8 <= inner) {
+      for (int j = 0; j < 8; j++)
+        if (row[i + j] > vmax[j]) vmax[j] = row[i + j];
+      i += 8;
+    }
+    mx = vmax[0];
+    for (int j = 1; j < 8; j++)
+      if (vmax[j] > mx) mx = vmax[j];
+  } else {
+    i = 1;
+    mx = row[0];
+  }
+  for (; i < inner; i++)
+    if (row[i] > mx) mx = row[i];
+  float sum = 0.0f;
+  int64_t i2 = 0;
+  if (inner >= 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    while (i2 + 8 <= inner) {
+      for (int j = 0; j < 8; j++) {
+        float ev = exp1(row[i2 + j] - mx);
+        row[i2 + j] = ev;
+        acc[j] += ev;
+      }
+      i2 += 8;
+    }
+    sum = hsum8(acc);
+  }
+  for (; i2 < inner; i2++) {
+    row[i2] = exp1(row[i2] - mx);
+    sum += row[i2];
+  }
+  float inv = 1.0f / sum;
+  for (int64_t k = 0; k < inner; k++) row[k] *= inv;
+}
+
+/* softmax_last_dim: activation.rs:321-334. */
+QPO_API void qpo_softmax_last_dim(float* t, int64_t rows, int64_t inner) {
+#pragma omp parallel
+  {
+    qpo_ftz();
+#pragma omp for schedule(static)
+    for (int64_t r = 0; r < rows; r++) softmax_row(t + r * inner, inner);
+  }
+}
+
+/* ---------------------------------------------------------------- sgemm */
+
+/* Bias placement of the reference sgemm (gemm.rs:7-16):
+ *   path 0 = panel kernel (gemm.rs:523-596, x86.rs:134-444): 32-column
+ *     panels; rows in the M%4 tail of a panel narrower than 32 columns start
+ *     the fma chain from the bias ("seeded"); everything else adds the bias
+ *     after the chain.
+ *   path 1 = m-rows kernel (gemm.rs:598-643, x86.rs:717-772), taken by the
+ *     parallel sgemm when n <= 32 (np == 1): columns j >= n - n%32 are seeded.
+ * Every element's chain is acc = fma(a[i][kk], b[kk][j], acc), kk ascending. */
+static inline int bias_seeded(int path, int64_t i, int64_t j, int64_t m, int64_t n) {
+  if (path == 1) return j >= n - n % 32;
+  int64_t n0 = (j / 32) * 32;
+  int64_t nn = n - n0 < 32 ? n - n0 : 32;
+  return nn < 32 && i >= m - m % 4;
+}
+
+/* Path the reference sgemm/sgemm_res takes for a shape (gemm.rs:249-466):
+ * serial (panel) when called from a parallel region or m*n*k < gemm_par_min
+ * (2e5, par.rs:41-48); otherwise panel when np >= 2, m-rows when np == 1.
+ * The baseline runs with more than one thread (par::threads() > 1). */
+QPO_API int qpo_sgemm_path(int64_t m, int64_t n, int64_t k, int serial) {
+  if (serial) return 0;
+  if ((double)m * (double)n * (double)k < 2e5) return 0;
+  return (n + 31) / 32 >= 2 ? 0 : 1;
+}
+
+/* C[M,N] (row stride ldc) = A[M,K] * B where B's row kk starts at
+ * brow[kk] (implicit GEMM, gemm.rs:75-128) or at b + kk*ldb; bias per row.
+ * Blocking: 4 rows x 32 columns at a time, fma chains in registers. */
+static void gemm_block(const float* a, int64_t lda, const float* b, int64_t ldb,
+                       const float* const* brow, float* c, int64_t ldc, int64_t m, int64_t n,
+                       int64_t k, const float* bias, int path, int64_t i0, int64_t i1,
+                       int64_t j0, int64_t j1) {
+  for (int64_t i = i0; i < i1; i += 4) {
+    int64_t ni = i1 - i < 4 ? i1 - i : 4;
+    for (int64_t jb = j0; jb < j1; jb += 32) {
+      int64_t nj = j1 - jb < 32 ? j1 - jb : 32;
+      float acc[4][32];
+      for (int r = 0; r < 4; r++)
+        for (int j = 0; j < 32; j++) {
+          float s = 0.0f;
+          if (bias && r < ni && j < nj && bias_seeded(path, i + r, jb + j, m, n)) s = bias[i + r];
+          acc[r][j] = s;
+        }
+      for (int64_t kk = 0; kk < k; kk++) {
+        const float* bp = brow ? brow[kk] + jb : b + kk * ldb + jb;
+        float bv[32];
+        for (int j = 0; j < 32; j++) bv[j] = j < nj ? bp[j] : 0.0f;
+        for (int r = 0; r < 4; r++) {
+          float av = r < ni ? a[(i + r) * lda + kk] : 0.0f;
+          for (int j = 0; j < 32; j++) acc[r][j] = fmaf(av, bv[j], acc[r][j]);
+        }
+      }
+      for (int r = 0; r < ni; r++)
+        for (int j = 0; j < nj; j++) {
+          float v = acc[r][j];
+          if (bias && !bias_seeded(path, i + r, jb + j, m, n)) v = v + bias[i + r];
+          c[(i + r) * ldc + jb + j] = v;
+        }
+    }
+  }
+}
+
+/* sgemm / sgemm_res: gemm.rs:37-70, 223-507.  Result = chain (+bias by the
+ * placement rule), then act, then += residual (residual has C's layout). */
+QPO_API void qpo_sgemm(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                       int64_t ldc, const float* bias, int act, float c1, float c2, float c3,
+                       const float* residual, int serial) {
+  if (m == 0 || n == 0 || k == 0) return;
+  int path = qpo_sgemm_path(m, n, k, serial);
+  int64_t mblocks = (m + 3) / 4;
+  int64_t nblocks = (n + 127) / 128;
+#pragma omp parallel
+  {
+    qpo_ftz();
+#pragma omp for schedule(dynamic, 1) collapse(2)
+    for (int64_t mb = 0; mb < mblocks; mb++)
+      for (int64_t nb = 0; nb < nblocks; nb++) {
+        int64_t i0 = mb * 4, i1 = i0 + 4 < m ? i0 + 4 : m;
+        int64_t j0 = nb * 128, j1 = j0 + 128 < n ? j0 + 128 : n;
+        gemm_block(a, k, b, n, NULL, c, ldc, m, n, k, bias, path, i0, i1, j0, j1);
+      }
+#pragma omp for schedule(static)
+    for (int64_t i = 0; i < m; i++)
+      act_res_range(c + i * ldc, residual ? residual + i * ldc : NULL, (size_t)n, act, c1, c2, c3);
+  }
+}
+
+/* ------------------------------------------------------------------ conv2d */
+
+/* conv2d_out_shape: conv.rs:146-156. Returns 0 on success. */
+QPO_API int qpo_conv2d_out_shape(const int64_t* xs, const int64_t* ws, const int64_t* p,
+                                 int64_t* ys) {
+  /* p = {sh, sw, ph, pw, peh, pew, dh, dw, group} (ConvParams, conv.rs:124-143) */
+  int64_t n = xs[0], c = xs[1], h = xs[2], w = xs[3];
+  int64_t m = ws[0], cg = ws[1], kh = ws[2], kw = ws[3];
+  if (p[6] != 1 || p[7] != 1) return -1;
+  if (p[8] * cg != c || m % p[8] != 0) return -2;
+  int64_t oh = (h + p[2] + p[4] - kh) / p[0] + 1;
+  int64_t ow = (w + p[3] + p[5] - kw) / p[1] + 1;
+  if (oh <= 0 || ow <= 0) return -3;
+  ys[0] = n; ys[1] = m; ys[2] = oh; ys[3] = ow;
+  return 0;
+}
+
+/* conv2d_res_into: conv.rs:222-715.  Branches:
+ *   1x1 s1 g1 -> sgemm (conv.rs:264-460): per batch item W[M,C] x X[C,HW];
+ *   depthwise (g > 1, C/g == 1) -> padded-plane direct conv (conv.rs:461-505,
+ *     x86.rs:994-1060): acc = fma(w, x, acc) over ky then kx from 0, + bias;
+ *   general -> implicit GEMM per output row (conv.rs:506-637): K order
+ *     ch -> ky -> kx, N = ow, panel bias placement, act on each row GEMM.
+ * act then residual (conv.rs:673-713, gemm.rs:478-507). */
+QPO_API int qpo_conv2d(const float* x, const int64_t* xs, const float* wt, const int64_t* ws,
+                       const float* bias, const int64_t* p, int act, float c1, float c2, float c3,
+                       const float* residual, float* y, int64_t* ys_out) {
+  int64_t ys[4];
+  int rc = qpo_conv2d_out_shape(xs, ws, p, ys);
+  if (rc) return rc;
+  if (ys_out) memcpy(ys_out, ys, sizeof ys);
+  const int64_t n = xs[0], c = xs[1], h = xs[2], wd = xs[3];
+  const int64_t m = ws[0], cg = ws[1], kh = ws[2], kw = ws[3];
+  const int64_t sh = p[0], sw = p[1], ph = p[2], pw = p[3], peh = p[4], pew = p[5], g = p[8];
+  const int64_t oh = ys[2], ow = ys[3], ohw = oh * ow;
+  const int depthwise = g > 1 && cg == 1;
+  const float inv_c1 = 1.0f / c1;
+
+  if (g == 1 && kh == 1 && kw == 1 && sh == 1 && sw == 1) {
+    /* 1x1: conv.rs:370-460.  N > 1 with threads > 1 runs sgemm_serial_res
+     * per chunk (panel path); N == 1 runs sgemm_res (parallel rules). */
+    int serial = n > 1;
+    for (int64_t bn = 0; bn < n; bn++)
+      qpo_sgemm(wt, x + bn * c * ohw, y + bn * m * ohw, m, ohw, c, ohw, bias, act, c1, c2, c3,
+                residual ? residual + bn * m * ohw : NULL, serial);
+    return 0;
+  }
+
+  if (depthwise) {
+    const int64_t pheight = ph + h + peh;
+    const int64_t pwidth = pw + wd + pew;
+#pragma omp parallel
+    {
+      qpo_ftz();
+      float* pad = (float*)malloc(sizeof(float) * (size_t)(pheight * pwidth));
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t u = 0; u < n * c; u++) {
+        int64_t bn = u / c, ch = u % c;
+        const float* xch = x + (bn * c + ch) * h * wd;
+        const float* wc = wt + ch * kh * kw;
+        float bv = bias ? bias[ch] : 0.0f;
+        /* pad_channel: conv.rs:78-119 */
+        memset(pad, 0, sizeof(float) * (size_t)(pheight * pwidth));
+        for (int64_t yy = 0; yy < h; yy++)
+          memcpy(pad + (ph + yy) * pwidth + pw, xch + yy * wd, sizeof(float) * (size_t)wd);
+        float* yc = y + (bn * m + ch) * ohw;
+        for (int64_t oy = 0; oy < oh; oy++) {
+          const float* base = pad + oy * sh * pwidth;
+          for (int64_t ox = 0; ox < ow; ox++) {
+            float acc = 0.0f;
+            for (int64_t ky = 0; ky < kh; ky++) {
+              const float* row = base + ky * pwidth;
+              for (int64_t kx = 0; kx < kw; kx++) acc = fmaf(wc[ky * kw + kx], row[ox * sw + kx], acc);
+            }
+            yc[oy * ow + ox] = acc + bv;
+          }
+        }
+        /* conv.rs:673-677 act (never fused for group > 1 by the optimizer,
+         * applied if asked), then conv.rs:701-713 residual. */
+        if (act != 0)
+          for (int64_t i = 0; i < ohw; i++) yc[i] = act1(yc[i], act, c1, c2, c3, inv_c1);
+        if (residual) {
+          const float* rs = residual + (bn * m + ch) * ohw;
+          for (int64_t i = 0; i < ohw; i++) yc[i] = yc[i] + rs[i];
+        }
+      }
+      free(pad);
+    }
+    return 0;
+  }
+
+  /* general grouped conv: implicit GEMM, one output row per sgemm call. */
+  const int64_t mg = m / g, kk = cg * kh * kw;
+  const int64_t pwidth = (ow - 1) * sw + kw;
+#pragma omp parallel
+  {
+    qpo_ftz();
+    float* slab = (float*)malloc(sizeof(float) * (size_t)(cg * kh * pwidth));
+    const float** brow = (const float**)malloc(sizeof(float*) * (size_t)kk);
+    float* patch = (float*)malloc(sizeof(float) * (size_t)(kk * ow));
+#pragma omp for schedule(dynamic, 1) collapse(3)
+    for (int64_t bn = 0; bn < n; bn++)
+      for (int64_t gi = 0; gi < g; gi++)
+        for (int64_t oy = 0; oy < oh; oy++) {
+          const float* xg = x + (bn * c + gi * cg) * h * wd;
+          /* zero-padded slab of the kh input rows this output row reads */
+          for (int64_t ch = 0; ch < cg; ch++)
+            for (int64_t ky = 0; ky < kh; ky++) {
+              float* dst = slab + (ch * kh + ky) * pwidth;
+              int64_t iy = oy * sh - ph + ky;
+              for (int64_t xx = 0; xx < pwidth; xx++) {
+                int64_t ix = xx - pw;
+                dst[xx] = (iy >= 0 && iy < h && ix >= 0 && ix < wd) ? xg[(ch * h + iy) * wd + ix] : 0.0f;
+              }
+            }
+          /* B row k = (ch, ky, kx): element ox = slab[ch][ky][ox*sw + kx] */
+          for (int64_t ch = 0; ch < cg; ch++)
+            for (int64_t ky = 0; ky < kh; ky++)
+              for (int64_t kx = 0; kx < kw; kx++) {
+                int64_t kidx = (ch * kh + ky) * kw + kx;
+                const float* src = slab + (ch * kh + ky) * pwidth + kx;
+                float* dst = patch + kidx * ow;
+                for (int64_t ox = 0; ox < ow; ox++) dst[ox] = src[ox * sw];
+                brow[kidx] = dst;
+              }
+          float* yrow = y + (bn * m + gi * mg) * ohw + oy * ow;
+          const float* bg = bias ? bias + gi * mg : NULL;
+          gemm_block(wt + gi * mg * kk, kk, NULL, 0, brow, yrow, ohw, mg, ow, kk, bg, 0, 0, mg, 0, ow);
+          for (int64_t r = 0; r < mg; r++) {
+            float* yr = yrow + r * ohw;
+            if (act != 0)
+              for (int64_t i = 0; i < ow; i++) yr[i] = act1(yr[i], act, c1, c2, c3, inv_c1);
+          }
+        }
+    free(slab);
+    free((void*)brow);
+    free(patch);
+  }
+  if (residual) {
+    int64_t total = n * m * ohw;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < total; i++) y[i] = y[i] + residual[i];
+  }
+  return 0;
+}
+
+/* --------------------------------------------------------- convtranspose */
+
+/* convtranspose2d, 2x2 s2 p0 only, no bias: conv.rs:730-838 (x86.rs:1065-1085).
+ * w is ONNX [Ci, Co, 2, 2]; out(2iy+ky, 2ix+kx) = chain over ci ascending of
+ * fma(x, w, acc) from 0. */
+QPO_API int qpo_convtranspose2x2(const float* x, const int64_t* xs, const float* w,
+                                 const int64_t* ws, float* y) {
+  int64_t n = xs[0], c = xs[1], h = xs[2], wd = xs[3];
+  int64_t cin = ws[0], m = ws[1];
+  if (cin != c || ws[2] != 2 || ws[3] != 2) return -1;
+  int64_t oh = 2 * h, ow = 2 * wd;
+#pragma omp parallel
+  {
+    qpo_ftz();
+#pragma omp for schedule(static) collapse(3)
+    for (int64_t bn = 0; bn < n; bn++)
+      for (int64_t co = 0; co < m; co++)
+        for (int64_t iy = 0; iy < h; iy++) {
+          const float* xn = x + bn * c * h * wd;
+          for (int ky = 0; ky < 2; ky++) {
+            float* orow = y + ((bn * m + co) * oh + 2 * iy + ky) * ow;
+            for (int64_t j = 0; j < wd; j++) {
+              float a0 = 0.0f, a1 = 0.0f;
+              for (int64_t ch = 0; ch < c; ch++) {
+                float xv = xn[(ch * h + iy) * wd + j];
+                const float* wc = w + ((ch * m + co) * 4 + ky * 2);
+                a0 = fmaf(xv, wc[0], a0);
+                a1 = fmaf(xv, wc[1], a1);
+              }
+              orow[2 * j] = a0;
+              orow[2 * j + 1] = a1;
+            }
+          }
+        }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ resize */
+
+/* resize_nearest: resize.rs:26-57: iy = min((int)((float)oy * H / oh), H-1). */
+QPO_API void qpo_resize_nearest(const float* x, int64_t nc, int64_t h, int64_t w, int64_t oh,
+                                int64_t ow, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t p = 0; p < nc; p++) {
+    for (int64_t oy = 0; oy < oh; oy++) {
+      int64_t iy = (int64_t)((float)oy * (float)h / (float)oh);
+      if (iy > h - 1) iy = h - 1;
+      for (int64_t ox = 0; ox < ow; ox++) {
+        int64_t ix = (int64_t)((float)ox * (float)w / (float)ow);
+        if (ix > w - 1) ix = w - 1;
+        y[(p * oh + oy) * ow + ox] = x[(p * h + iy) * w + ix];
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------- elementwise, reduce */
+
+/* Binary ops, same-shape flat pass: elementwise.rs:197-205 (x86.rs:867-892).
+ * op: 0 add, 1 sub, 2 mul, 3 div, 4 pow (powf, elementwise.rs:48-56). */
+static inline float binop(int op, float a, float b) {
+  switch (op) {
+    case 0: return a + b;
+    case 1: return a - b;
+    case 2: return a * b;
+    case 3: return a / b;
+    default: return powf(a, b);
+  }
+}
+
+QPO_API void qpo_binary_flat(float* a, const float* b, int64_t n, int op) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; i++) a[i] = binop(op, a[i], b[i]);
+}
+
+/* a[R,C] op= b broadcast: bmode 0 = b[R] per row (a [R,C] op [R,1]),
+ * 1 = b[C] per column (a [R,C] op [C]), 2 = scalar b[0].  The run paths of
+ * binary_op_inplace (elementwise.rs:207-298, x86.rs:895-942). */
+QPO_API void qpo_binary_bcast(float* a, const float* b, int64_t rows, int64_t cols, int op,
+                              int bmode) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t j = 0; j < cols; j++) {
+      float bv = bmode == 0 ? b[r] : (bmode == 1 ? b[j] : b[0]);
+      a[r * cols + j] = binop(op, a[r * cols + j], bv);
+    }
+}
+
+/* reduce_mean over the last axis: shape.rs:510-560 (f64 accumulation,
+ * ascending, then (s / mid) rounded to f32). */
+QPO_API void qpo_reduce_mean_last(const float* x, int64_t rows, int64_t cols, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++) {
+    double s = 0.0;
+    for (int64_t j = 0; j < cols; j++) s += (double)x[r * cols + j];
+    out[r] = (float)(s / (double)cols);
+  }
+}
+
+QPO_API void qpo_sqrt_inplace(float* t, int64_t n) {
+  for (int64_t i = 0; i < n; i++) t[i] = sqrtf(t[i]);
+}
+
+/* LayerNorm exactly as the exported graph runs it on the CPU executor
+ * (ReduceMean -> Sub -> Pow(2) -> ReduceMean -> Add(eps) -> Sqrt -> Div ->
+ * Mul(gamma) -> Add(beta)), each node rounding to f32:
+ * shape.rs:510-560, elementwise.rs:185-298, activation.rs:449-459. */
+QPO_API void qpo_layernorm_chain(const float* x, const float* gamma, const float* beta, float eps,
+                                 int64_t rows, int64_t cols, float* y) {
+#pragma omp parallel
+  {
+    qpo_ftz();
+    float* d = (float*)malloc(sizeof(float) * (size_t)cols);
+#pragma omp for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+      const float* xr = x + r * cols;
+      double s = 0.0;
+      for (int64_t j = 0; j < cols; j++) s += (double)xr[j];
+      float mu = (float)(s / (double)cols);
+      for (int64_t j = 0; j < cols; j++) d[j] = xr[j] - mu;
+      double s2 = 0.0;
+      for (int64_t j = 0; j < cols; j++) s2 += (double)powf(d[j], 2.0f);
+      float var = (float)(s2 / (double)cols);
+      float sd = sqrtf(var + eps);
+      float* yr = y + r * cols;
+      for (int64_t j = 0; j < cols; j++) {
+        float v = d[j] / sd;
+        v = v * gamma[j];
+        yr[j] = v + beta[j];
+      }
+    }
+    free(d);
+  }
+}
+
+/* ------------------------------------------------------------------ matmul */
+
+/* Batched matmul without bias: shape.rs:568-698.  Every path (folded sgemm,
+ * per-batch sgemm, row outer product) computes each element as the chain
+ * c = fma(a[kk], b[kk][j], c) from 0, kk ascending, so one loop serves.
+ * a: [batch, m, k] (abatch 1 = shared), b: [batch, k, n] (bbatch 1 = shared). */
+QPO_API void qpo_matmul(const float* a, const float* b, float* out, int64_t batch, int64_t m,
+                        int64_t k, int64_t n, int a_shared, int b_shared) {
+#pragma omp parallel
+  {
+    qpo_ftz();
+    float* crow = (float*)malloc(sizeof(float) * (size_t)n);
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < batch * m; t++) {
+      int64_t bi = t / m, mm = t % m;
+      const float* ar = a + (a_shared ? 0 : bi * m * k) + mm * k;
+      const float* bp = b + (b_shared ? 0 : bi * k * n);
+      for (int64_t j = 0; j < n; j++) crow[j] = 0.0f;
+      for (int64_t kk = 0; kk < k; kk++) {
+        float av = ar[kk];
+        const float* br = bp + kk * n;
+        for (int64_t j = 0; j < n; j++) crow[j] = fmaf(av, br[j], crow[j]);
+      }
+      memcpy(out + t * n, crow, sizeof(float) * (size_t)n);
+    }
+    free(crow);
+  }
+}
+
+/* --------------------------------------------------------------------- CTC */
+
+/* Per-row argmax, first strict maximum (ties -> lowest index):
+ * qppocr-core/src/pipeline/rec.rs:46-54.  pairs[2t] = value,
+ * pairs[2t+1] = index as f32 bits (rec.rs:82-90, device.rs:160-165). */
+QPO_API void qpo_ctc_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < rows; t++) {
+    const float* row = probs + t * cols;
+    int64_t best = 0;
+    float bestv = row[0];
+    for (int64_t c = 1; c < cols; c++)
+      if (row[c] > bestv) {
+        bestv = row[c];
+        best = c;
+      }
+    uint32_t ib = (uint32_t)best;
+    pairs[2 * t] = bestv;
+    memcpy(&pairs[2 * t + 1], &ib, 4);
+  }
+}
+
+/* Greedy CTC collapse over pairs: rec.rs:82-115 (emit when idx != 0 and
+ * idx != previous; confidence = f64 mean of emitted values).  Returns the
+ * number of emitted ids written to ids (capacity t_len). */
+QPO_API int64_t qpo_ctc_collapse(const float* pairs, int64_t t_len, int32_t* ids, float* conf) {
+  int64_t prev = -1, cnt = 0;
+  double cs = 0.0;
+  for (int64_t t = 0; t < t_len; t++) {
+    uint32_t ib;
+    memcpy(&ib, &pairs[2 * t + 1], 4);
+    int64_t b = (int64_t)ib;
+    if (b != 0 && b != prev) {
+      ids[cnt++] = (int32_t)b;
+      cs += (double)pairs[2 * t];
+    }
+    prev = b;
+  }
+  if (conf) *conf = cnt > 0 ? (float)(cs / (double)cnt) : 0.0f;
+  return cnt;
+}

@@ -1,0 +1,212 @@
+// Internal declarations shared by the qppocr HIP library's translation units.
+//
+// Numerics contract: every kernel reproduces the qppocr-kernels CPU operation
+// sequence for each output element (same fma chains in the same k order,
+// same separately-rounded multiplies/adds, same exp/erf polynomials), so the
+// results are bit-identical to the CPU path.  All device code is compiled
+// with -ffp-contract=off so that a*b+c is never fused unless written as fmaf,
+// and with f32 denormals flushed, as the CPU executor runs with FTZ|DAZ
+// (qppocr-kernels/src/par.rs:229-256).  fp32 MFMA on gfx950 accumulates each
+// product in k order with one rounding per product, i.e. an MFMA k-chain is a
+// chain of fmaf calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <string>
+
+#include "../../include/qppocr_hip.h"
+
+namespace qph {
+
+// ----------------------------------------------------------------- errors
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+// Checks a HIP return code; on failure records the message and returns QPH_EHIP.
+int hip_check(hipError_t e, const char* what);
+
+#define QPH_TRY_HIP(expr)                                  \
+  do {                                                     \
+    int _rc = ::qph::hip_check((expr), #expr);             \
+    if (_rc != QPH_OK) return _rc;                         \
+  } while (0)
+
+#define QPH_TRY(expr)               \
+  do {                              \
+    int _rc = (expr);               \
+    if (_rc != QPH_OK) return _rc;  \
+  } while (0)
+
+// After a kernel launch: report launch-configuration errors.
+int launch_check(const char* kernel);
+
+}  // namespace qph
+
+struct qph_ctx {
+  int device;
+  hipStream_t stream;
+  bool own_stream;
+  void* ws;         // scratch for standalone operator calls (repacked weights, masks)
+  size_t ws_bytes;
+};
+
+namespace qph {
+
+// Grows the context scratch to at least `bytes` (synchronises the stream
+// before releasing a smaller buffer) and returns it.
+int ctx_workspace(qph_ctx* ctx, size_t bytes, void** out);
+
+// Activation kinds (qph_act.kind): 0 none, 1 gelu(c1,c2,c3), 2 relu,
+// 3 hardswish(alpha=c1, beta=c2), 4 sigmoid.
+
+// exp1: qppocr-kernels/src/activation.rs:28-47 (x86.rs:28-57).
+__device__ __forceinline__ float exp1(float x) {
+  const float LN2_HI = 0.6931472f;
+  const float LN2_LO = -2.9802322e-8f;
+  const float INV_LN2 = 1.442695f;
+  x = fminf(x, 88.0f);
+  x = fmaxf(x, -88.0f);
+  float kf = __builtin_rintf(x * INV_LN2);
+  float r = __builtin_fmaf(-kf, LN2_HI, x);
+  r = __builtin_fmaf(-kf, LN2_LO, r);
+  float p = 1.0f / 720.0f;
+  p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ki = (int)kf + 127;
+  return __uint_as_float((unsigned)ki << 23) * p;
+}
+
+// erf1: qppocr-kernels/src/activation.rs:53-66 (A&S 7.1.26).
+__device__ __forceinline__ float erf1(float x) {
+  float ax = __uint_as_float(__float_as_uint(x) & 0x7fffffffu);
+  float t = 1.0f / __builtin_fmaf(0.3275911f, ax, 1.0f);
+  float p = 1.0614054f;
+  p = __builtin_fmaf(p, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.2548296f);
+  p = p * t;
+  float e = exp1(ax * (0.0f - ax));
+  float r = __builtin_fmaf(-p, e, 1.0f);
+  return __uint_as_float(__float_as_uint(r) | (__float_as_uint(x) & 0x80000000u));
+}
+
+// relu: activation.rs:232-239 (NaN -> 0).
+__device__ __forceinline__ float relu1(float v) { return v > 0.0f ? v : 0.0f; }
+
+// hardsigmoid: activation.rs:168-187.
+__device__ __forceinline__ float hsig1(float x, float alpha, float beta) {
+  float v = __builtin_fmaf(x, alpha, beta);
+  return v < 0.0f ? 0.0f : (v > 1.0f ? 1.0f : v);
+}
+
+// sigmoid: activation.rs:196-201 (true division).
+__device__ __forceinline__ float sigmoid1(float x) { return 1.0f / (1.0f + exp1(-x)); }
+
+// gelu: activation.rs:209-215, (c3*x) * (erf1(x*inv_c1) + c2).
+__device__ __forceinline__ float gelu1(float v, float inv_c1, float c2, float c3) {
+  return c3 * v * (erf1(v * inv_c1) + c2);
+}
+
+struct Act {
+  int kind;
+  float c1, c2, c3, inv_c1;
+};
+
+__device__ __forceinline__ float act_apply(float v, const Act& a) {
+  switch (a.kind) {
+    case 1: return gelu1(v, a.inv_c1, a.c2, a.c3);
+    case 2: return relu1(v);
+    case 3: return v * hsig1(v, a.c1, a.c2);  // HardSigmoid node then Mul node
+    case 4: return sigmoid1(v);
+    default: return v;
+  }
+}
+
+inline Act make_act(const qph_act* a) {
+  Act r;
+  if (!a) {
+    r.kind = 0; r.c1 = 1.0f; r.c2 = 0.0f; r.c3 = 0.0f;
+  } else {
+    r.kind = a->kind; r.c1 = a->c1; r.c2 = a->c2; r.c3 = a->c3;
+  }
+  r.inv_c1 = 1.0f / r.c1;  // host f32 division: same value as the reference's 1.0f32 / c1
+  return r;
+}
+
+inline bool act_valid(const qph_act* a) { return !a || (a->kind >= 0 && a->kind <= 4); }
+
+// -------------------------------------------------------- launch helpers
+
+inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+// Internal launchers shared between the operator entry points and the
+// session runner.  All pointers are device pointers; shapes were validated
+// by the caller.
+
+struct GemmArgs {
+  const float* a; int64_t lda; int64_t a_batch;   // A[M][K], row stride lda
+  const float* b; int64_t ldb; int64_t b_batch;   // B[K][N], row stride ldb
+  float* c; int64_t ldc; int64_t c_batch;         // C[M][N] (or C^T when trans_out)
+  int64_t m, n, k, batch;
+  const float* bias; int bias_mode;               // 0 none, 1 per row (M), 2 per column (N)
+  int seed_rule;                                  // reference bias placement: 0 panel, 1 m-rows
+  Act act;
+  const float* res; int64_t ldr; int64_t r_batch;  // residual, same layout as C
+  int res_up;                                      // 0 same shape; 2 = nearest 2x of a coarse map
+  int64_t up_w, up_cw;                             // output / coarse image width (res_up)
+  int trans_out;                                   // store C^T: c[j*ldc + i]
+};
+int launch_gemm(const GemmArgs& g, hipStream_t s);
+
+struct ConvArgs {
+  const float* x; int64_t n, c, h, w;
+  const float* wt;     // ONNX layout [M][C/g][kh][kw]
+  const float* wk;     // optional repacked k-major weights [Kpad][Mpad] (NULL: built per call)
+  const float* bias;
+  int64_t m, kh, kw, sh, sw, ph, pw, oh, ow, group;
+  Act act;
+  const float* res;    // residual, same layout as y
+  float* y;            // y[N][M][oh][ow] when y_cstride == 0 (default NCHW)
+  // optional strided placement of the output: channel slice of a larger
+  // tensor (y_ctotal channels, offset y_coff) and nearest upsample by y_up.
+  int64_t y_ctotal, y_coff, y_up;
+};
+int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
+                  const float* wk_resident, const int64_t ws[4], const float* bias,
+                  const qph_conv_params* p, const qph_act* act, const qph_conv_epilogue* ep,
+                  float* y);
+int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk);
+int launch_depthwise(const ConvArgs& a, hipStream_t s);
+int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw);
+int launch_repack_conv_w(const float* wt, int64_t m, int64_t kk, float* wk, hipStream_t s);
+
+int launch_convt2x2(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, const float* wt,
+                    int64_t m, float* y, hipStream_t s);
+int launch_convt2x2_pair_sigmoid(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
+                                 const float* w1, int64_t m1, const float* w2, float* y,
+                                 hipStream_t s);
+int launch_layernorm(const float* x, const float* gamma, const float* beta, float eps,
+                     int64_t rows, int64_t cols, float* y, hipStream_t s);
+int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s);
+int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, float* probs,
+                          float* pairs, hipStream_t s);
+int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, hipStream_t s);
+int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
+                     float scale, float* out, hipStream_t s);
+int launch_elementwise_act(const float* x, float* y, int64_t n, const Act& a, hipStream_t s);
+int launch_resize_nearest(const float* x, int64_t nc, int64_t h, int64_t w, int64_t oh,
+                          int64_t ow, float* y, hipStream_t s);
+int launch_binary(float* a, const float* b, int64_t rows, int64_t cols, int op, int bmode,
+                  hipStream_t s);
+int launch_mask_pairs(float* pairs, int64_t batch, int64_t t, const int32_t* t_valid,
+                      hipStream_t s);
+
+}  // namespace qph

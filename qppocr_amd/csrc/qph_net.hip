@@ -1,0 +1,404 @@
+// Session: a static det/rec graph resident on the device, run as one HIP
+// graph replay per call.  This is the DeviceSession side of the boundary
+// (qppocr-core/src/device.rs:83-176): weights are moved to the device once at
+// create time, every node is validated then (unsupported -> error naming the
+// node, no silent fallback, device.rs:88-94), and each run is one host call.
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "qph_internal.h"
+
+using namespace qph;
+
+struct qph_net {
+  qph_ctx* ctx;
+  std::vector<qph_node> nodes;
+  std::vector<int64_t> shapes;   // 4 per tensor
+  std::vector<int32_t> alias;
+  std::vector<int32_t> outputs;
+  std::vector<float*> weights;   // device copies
+  std::vector<float*> wk;        // per node: resident repacked dense-conv weights (or NULL)
+  std::vector<float*> tptr;      // per tensor device pointer
+  char* arena;
+  size_t arena_bytes;
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+  bool graph_ready;
+  bool profiling;
+  std::vector<hipEvent_t> ev;
+  std::vector<double> node_ms;
+  int64_t prof_runs;
+};
+
+static int64_t numel_of(const qph_net* net, int32_t id) {
+  const int64_t* s = &net->shapes[4 * (size_t)id];
+  return s[0] * s[1] * s[2] * s[3];
+}
+
+static std::string node_name(size_t i, const qph_node& n) {
+  return "node " + std::to_string(i) + " (op " + std::to_string(n.op) + ")";
+}
+
+static int check_tensor(const qph_net* net, int32_t id, bool optional, size_t i, const qph_node& n,
+                        const char* what) {
+  if (id < 0 && optional) return QPH_OK;
+  if (id < 0 || id >= (int32_t)net->tptr.size())
+    return fail(QPH_EINVAL, node_name(i, n) + ": bad " + what + " tensor id");
+  return QPH_OK;
+}
+
+// Launches node i on the context stream.
+static int run_node(qph_net* net, size_t i) {
+  const qph_node& n = net->nodes[i];
+  qph_ctx* ctx = net->ctx;
+  hipStream_t s = ctx->stream;
+  const int64_t* xs = &net->shapes[4 * (size_t)n.in];
+  float* x = net->tptr[n.in];
+  float* y = net->tptr[n.out];
+  const float* w = n.w >= 0 ? net->weights[n.w] : nullptr;
+  const float* bias = n.bias >= 0 ? net->weights[n.bias] : nullptr;
+  const float* w2 = n.w2 >= 0 ? net->weights[n.w2] : nullptr;
+  const float* res = n.in2 >= 0 ? net->tptr[n.in2] : nullptr;
+  switch (n.op) {
+    case QPH_OP_CONV: {
+      qph_conv_epilogue ep{};
+      ep.residual = res;
+      ep.res_up = n.res_up;
+      ep.y_ctotal = n.y_ctotal;
+      ep.y_coff = n.y_coff;
+      ep.y_up = n.y_up;
+      ep.trans_out = n.trans_out;
+      return conv_dispatch(ctx, x, xs, w, net->wk[i], n.ws, bias, &n.cp, &n.act, &ep, y);
+    }
+    case QPH_OP_CONVT_PAIR_SIG:
+      return launch_convt2x2_pair_sigmoid(x, xs[0], xs[1], xs[2], xs[3], w, n.ws[1], w2, y, s);
+    case QPH_OP_CONVT:
+      return launch_convt2x2(x, xs[0], xs[1], xs[2], xs[3], w, n.ws[1], y, s);
+    case QPH_OP_LINEAR: {
+      const int64_t k = n.ws[0], nn = n.ws[1];
+      const int64_t rows = numel_of(net, n.in) / k;
+      GemmArgs g{};
+      g.a = x; g.lda = k; g.b = w; g.ldb = nn; g.c = y; g.ldc = nn;
+      g.m = rows; g.n = nn; g.k = k; g.batch = 1;
+      g.bias = bias; g.bias_mode = bias ? 2 : 0;
+      g.act = make_act(&n.act);
+      g.res = res; g.ldr = nn;
+      return launch_gemm(g, s);
+    }
+    case QPH_OP_LAYERNORM: {
+      const int64_t cols = n.ws[0];
+      return launch_layernorm(x, w, bias, n.eps, numel_of(net, n.in) / cols, cols, y, s);
+    }
+    case QPH_OP_ATTENTION:
+      return launch_attention(x, xs[0], xs[1], n.heads, n.dh, n.scale, y, s);
+    case QPH_OP_SOFTMAX_ARGMAX: {
+      const int64_t c = n.ws[0];  // row width
+      float* pairs = n.out2 >= 0 ? net->tptr[n.out2] : nullptr;
+      return launch_softmax_argmax(x, numel_of(net, n.in) / c, c, y, pairs, s);
+    }
+    case QPH_OP_ACT:
+      return launch_elementwise_act(x, y, numel_of(net, n.in), make_act(&n.act), s);
+    default:
+      return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unknown op");
+  }
+}
+
+static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t nw) {
+  const qph_node& n = net->nodes[i];
+  QPH_TRY(check_tensor(net, n.in, false, i, n, "input"));
+  QPH_TRY(check_tensor(net, n.out, false, i, n, "output"));
+  QPH_TRY(check_tensor(net, n.in2, true, i, n, "second input"));
+  QPH_TRY(check_tensor(net, n.out2, true, i, n, "second output"));
+  for (int32_t wi : {n.w, n.bias, n.w2})
+    if (wi >= nw) return fail(QPH_EINVAL, node_name(i, n) + ": bad weight index");
+  if (!act_valid(&n.act)) return fail(QPH_EINVAL, node_name(i, n) + ": bad activation");
+  const int64_t* xs = &net->shapes[4 * (size_t)n.in];
+  const int64_t* ys = &net->shapes[4 * (size_t)n.out];
+  auto wsize = [&](int32_t wi) { return wi >= 0 ? wsizes[wi] : (int64_t)-1; };
+  switch (n.op) {
+    case QPH_OP_CONV: {
+      if (n.w < 0) return fail(QPH_EINVAL, node_name(i, n) + ": conv without weight");
+      int64_t os[4];
+      int rc = qph_conv2d_out_shape(xs, n.ws, &n.cp, os);
+      if (rc) return fail(rc, node_name(i, n) + ": " + qph_last_error());
+      if (wsize(n.w) != n.ws[0] * n.ws[1] * n.ws[2] * n.ws[3])
+        return fail(QPH_EINVAL, node_name(i, n) + ": weight size mismatch");
+      if (n.bias >= 0 && wsize(n.bias) != n.ws[0])
+        return fail(QPH_EINVAL, node_name(i, n) + ": bias size mismatch");
+      const int64_t up = n.y_up ? n.y_up : 1;
+      const int64_t ctot = n.y_ctotal ? n.y_ctotal : os[1];
+      int64_t want[4] = {os[0], ctot, os[2] * up, os[3] * up};
+      if (n.trans_out) {
+        if (numel_of(net, n.out) != os[0] * os[1] * os[2] * os[3])
+          return fail(QPH_EINVAL, node_name(i, n) + ": output size mismatch");
+      } else {
+        for (int d = 0; d < 4; d++)
+          if (ys[d] != want[d])
+            return fail(QPH_EINVAL, node_name(i, n) + ": output shape mismatch");
+      }
+      if (n.in2 >= 0) {
+        const int64_t* rs = &net->shapes[4 * (size_t)n.in2];
+        int64_t f = n.res_up == 2 ? 2 : 1;
+        if (rs[0] != os[0] || rs[1] != os[1] || rs[2] * f != os[2] || rs[3] * f != os[3])
+          return fail(QPH_EINVAL, node_name(i, n) + ": residual shape mismatch");
+      }
+      return QPH_OK;
+    }
+    case QPH_OP_CONVT_PAIR_SIG:
+    case QPH_OP_CONVT: {
+      if (n.w < 0 || n.ws[0] != xs[1] || n.ws[2] != 2 || n.ws[3] != 2)
+        return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": ConvTranspose needs [C,M,2,2]");
+      int64_t f = 2, m = n.ws[1];
+      if (n.op == QPH_OP_CONVT_PAIR_SIG) {
+        if (n.w2 < 0 || n.w2s[0] != n.ws[1] || n.w2s[1] != 1 || n.w2s[2] != 2 || n.w2s[3] != 2)
+          return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": second ConvTranspose needs [M,1,2,2]");
+        if (xs[1] > 64 || n.ws[1] > 64)
+          return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": ConvT pair needs C, M <= 64");
+        f = 4;
+        m = 1;
+      }
+      if (ys[0] != xs[0] || ys[1] != m || ys[2] != f * xs[2] || ys[3] != f * xs[3])
+        return fail(QPH_EINVAL, node_name(i, n) + ": output shape mismatch");
+      return QPH_OK;
+    }
+    case QPH_OP_LINEAR: {
+      if (n.w < 0 || wsize(n.w) != n.ws[0] * n.ws[1])
+        return fail(QPH_EINVAL, node_name(i, n) + ": linear weight [K,N] mismatch");
+      if (numel_of(net, n.in) % n.ws[0])
+        return fail(QPH_EINVAL, node_name(i, n) + ": input not a multiple of K");
+      int64_t rows = numel_of(net, n.in) / n.ws[0];
+      if (numel_of(net, n.out) != rows * n.ws[1])
+        return fail(QPH_EINVAL, node_name(i, n) + ": output size mismatch");
+      if (n.bias >= 0 && wsize(n.bias) != n.ws[1])
+        return fail(QPH_EINVAL, node_name(i, n) + ": bias size mismatch");
+      if (n.in2 >= 0 && numel_of(net, n.in2) != rows * n.ws[1])
+        return fail(QPH_EINVAL, node_name(i, n) + ": residual size mismatch");
+      return QPH_OK;
+    }
+    case QPH_OP_LAYERNORM:
+      if (n.w < 0 || n.bias < 0 || wsize(n.w) != n.ws[0] || wsize(n.bias) != n.ws[0] ||
+          numel_of(net, n.in) % n.ws[0] || numel_of(net, n.out) != numel_of(net, n.in))
+        return fail(QPH_EINVAL, node_name(i, n) + ": layernorm shapes");
+      return QPH_OK;
+    case QPH_OP_ATTENTION:
+      if (xs[2] * xs[3] != 3 * n.heads * n.dh || n.dh > 64 || xs[1] > 256 ||
+          numel_of(net, n.out) != xs[0] * xs[1] * n.heads * n.dh)
+        return fail(QPH_EINVAL, node_name(i, n) + ": attention shapes");
+      if ((2 * xs[1] * (n.dh + 1) + 4 * (xs[1] + n.dh)) * 4 > 64 * 1024)
+        return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": attention too large for LDS");
+      return QPH_OK;
+    case QPH_OP_SOFTMAX_ARGMAX:
+      if (n.ws[0] <= 0 || n.ws[0] > 32768 || numel_of(net, n.in) % n.ws[0] ||
+          numel_of(net, n.out) != numel_of(net, n.in))
+        return fail(QPH_EINVAL, node_name(i, n) + ": softmax row width / probs size");
+      if (n.out2 >= 0 && numel_of(net, n.out2) != 2 * (numel_of(net, n.in) / n.ws[0]))
+        return fail(QPH_EINVAL, node_name(i, n) + ": pairs size mismatch");
+      return QPH_OK;
+    case QPH_OP_ACT:
+      if (numel_of(net, n.out) != numel_of(net, n.in))
+        return fail(QPH_EINVAL, node_name(i, n) + ": size mismatch");
+      return QPH_OK;
+    default:
+      return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unsupported op");
+  }
+}
+
+static void release(qph_net* net) {
+  if (!net) return;
+  (void)hipStreamSynchronize(net->ctx->stream);
+  if (net->graph_ready) {
+    (void)hipGraphExecDestroy(net->exec);
+    (void)hipGraphDestroy(net->graph);
+  }
+  for (auto e : net->ev) (void)hipEventDestroy(e);
+  for (float* p : net->weights) (void)hipFree(p);
+  for (float* p : net->wk)
+    if (p) (void)hipFree(p);
+  if (net->arena) (void)hipFree(net->arena);
+  delete net;
+}
+
+extern "C" {
+
+QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
+                           const float* const* weights_host, qph_net** out) {
+  if (!ctx || !spec || !out) return fail(QPH_EINVAL, "net_create: NULL argument");
+  *out = nullptr;
+  if (spec->n_tensors <= 0 || spec->n_nodes <= 0 || !spec->shapes || !spec->nodes)
+    return fail(QPH_EINVAL, "net_create: empty graph");
+  if (spec->n_weights > 0 && (!weights_host || !spec->weight_sizes))
+    return fail(QPH_EINVAL, "net_create: missing weights");
+  qph_net* net = new qph_net();
+  net->ctx = ctx;
+  net->arena = nullptr;
+  net->arena_bytes = 0;
+  net->graph_ready = false;
+  net->profiling = false;
+  net->prof_runs = 0;
+  net->nodes.assign(spec->nodes, spec->nodes + spec->n_nodes);
+  net->shapes.assign(spec->shapes, spec->shapes + 4 * (size_t)spec->n_tensors);
+  net->alias.assign((size_t)spec->n_tensors, -1);
+  if (spec->alias) net->alias.assign(spec->alias, spec->alias + spec->n_tensors);
+  if (spec->n_outputs > 0 && spec->outputs)
+    net->outputs.assign(spec->outputs, spec->outputs + spec->n_outputs);
+  net->tptr.assign((size_t)spec->n_tensors, nullptr);
+  net->wk.assign(net->nodes.size(), nullptr);
+  int rc = QPH_OK;
+  auto bail = [&](int code) {
+    std::string msg = qph_last_error();
+    release(net);
+    set_error(msg);
+    return code;
+  };
+  // tensors: one arena, 256-byte aligned slots; aliases share their target
+  for (int32_t t = 0; t < spec->n_tensors; t++) {
+    for (int d = 0; d < 4; d++)
+      if (net->shapes[4 * t + d] <= 0) {
+        fail(QPH_EINVAL, "net_create: tensor " + std::to_string(t) + " has an empty shape");
+        return bail(QPH_EINVAL);
+      }
+    int32_t a = net->alias[t];
+    if (a >= spec->n_tensors || a == t || (a >= 0 && net->alias[a] >= 0)) {
+      fail(QPH_EINVAL, "net_create: bad alias of tensor " + std::to_string(t));
+      return bail(QPH_EINVAL);
+    }
+  }
+  std::vector<size_t> off((size_t)spec->n_tensors, 0);
+  for (int32_t t = 0; t < spec->n_tensors; t++) {
+    if (net->alias[t] >= 0) continue;
+    off[t] = net->arena_bytes;
+    net->arena_bytes += ((size_t)numel_of(net, t) * 4 + 255) / 256 * 256;
+  }
+  rc = hip_check(hipMalloc((void**)&net->arena, net->arena_bytes), "hipMalloc(arena)");
+  if (rc) return bail(rc);
+  for (int32_t t = 0; t < spec->n_tensors; t++) {
+    int32_t a = net->alias[t] >= 0 ? net->alias[t] : t;
+    net->tptr[t] = (float*)(net->arena + off[a]);
+  }
+  // weights
+  for (int32_t wi = 0; wi < spec->n_weights; wi++) {
+    float* d = nullptr;
+    size_t bytes = (size_t)spec->weight_sizes[wi] * 4;
+    rc = hip_check(hipMalloc((void**)&d, bytes ? bytes : 4), "hipMalloc(weight)");
+    if (rc) return bail(rc);
+    net->weights.push_back(d);
+    if (bytes) {
+      rc = hip_check(hipMemcpy(d, weights_host[wi], bytes, hipMemcpyHostToDevice), "hipMemcpy(weight)");
+      if (rc) return bail(rc);
+    }
+  }
+  for (size_t i = 0; i < net->nodes.size(); i++) {
+    rc = validate_node(net, i, spec->weight_sizes, spec->n_weights);
+    if (rc) return bail(rc);
+    const qph_node& n = net->nodes[i];
+    const bool dense = n.op == QPH_OP_CONV &&
+                       !(n.cp.group == 1 && n.ws[2] == 1 && n.ws[3] == 1 && n.cp.sh == 1 &&
+                         n.cp.sw == 1) &&
+                       !(n.cp.group > 1 && n.ws[1] == 1);
+    if (dense) {
+      int64_t kk = n.ws[1] * n.ws[2] * n.ws[3];
+      float* d = nullptr;
+      rc = hip_check(hipMalloc((void**)&d, (size_t)dense_conv_wk_floats(n.ws[0], n.ws[1], n.ws[2], n.ws[3]) * 4),
+                     "hipMalloc(repacked weight)");
+      if (rc) return bail(rc);
+      net->wk[i] = d;
+      rc = launch_repack_conv_w(net->weights[n.w], n.ws[0], kk, d, ctx->stream);
+      if (rc) return bail(rc);
+    }
+  }
+  rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (rc) return bail(rc);
+  *out = net;
+  return QPH_OK;
+}
+
+QPH_API int qph_net_destroy(qph_net* net) {
+  release(net);
+  return QPH_OK;
+}
+
+QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* numel) {
+  if (!net || id < 0 || id >= (int32_t)net->tptr.size())
+    return fail(QPH_EINVAL, "net_tensor: bad tensor id");
+  if (dev_ptr) *dev_ptr = net->tptr[id];
+  if (numel) *numel = numel_of(net, id);
+  return QPH_OK;
+}
+
+QPH_API int qph_net_set_profiling(qph_net* net, int32_t on) {
+  if (!net) return fail(QPH_EINVAL, "net_set_profiling: NULL net");
+  net->profiling = on != 0;
+  net->prof_runs = 0;
+  net->node_ms.assign(net->nodes.size(), 0.0);
+  if (net->profiling && net->ev.empty()) {
+    net->ev.resize(net->nodes.size() + 1);
+    for (auto& e : net->ev) QPH_TRY_HIP(hipEventCreate(&e));
+  }
+  return QPH_OK;
+}
+
+QPH_API int qph_net_node_times(qph_net* net, double* ms, int32_t n) {
+  if (!net || !ms) return fail(QPH_EINVAL, "net_node_times: NULL argument");
+  for (int32_t i = 0; i < n && i < (int32_t)net->node_ms.size(); i++)
+    ms[i] = net->prof_runs ? net->node_ms[i] / (double)net->prof_runs : 0.0;
+  return QPH_OK;
+}
+
+QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_device,
+                        float* const* outputs_host) {
+  if (!net) return fail(QPH_EINVAL, "net_run: NULL net");
+  hipStream_t s = net->ctx->stream;
+  if (input) {
+    size_t bytes = (size_t)numel_of(net, 0) * 4;
+    QPH_TRY_HIP(hipMemcpyAsync(net->tptr[0], input, bytes,
+                               input_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
+  }
+  if (net->profiling) {
+    for (size_t i = 0; i < net->nodes.size(); i++) {
+      QPH_TRY_HIP(hipEventRecord(net->ev[i], s));
+      QPH_TRY(run_node(net, i));
+    }
+    QPH_TRY_HIP(hipEventRecord(net->ev[net->nodes.size()], s));
+    QPH_TRY_HIP(hipEventSynchronize(net->ev[net->nodes.size()]));
+    for (size_t i = 0; i < net->nodes.size(); i++) {
+      float ms = 0.0f;
+      QPH_TRY_HIP(hipEventElapsedTime(&ms, net->ev[i], net->ev[i + 1]));
+      net->node_ms[i] += ms;
+    }
+    net->prof_runs++;
+  } else {
+    if (!net->graph_ready) {
+      QPH_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      int rc = QPH_OK;
+      for (size_t i = 0; i < net->nodes.size() && rc == QPH_OK; i++) rc = run_node(net, i);
+      hipGraph_t g = nullptr;
+      hipError_t e = hipStreamEndCapture(s, &g);
+      if (rc != QPH_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+      }
+      QPH_TRY_HIP(e);
+      e = hipGraphInstantiate(&net->exec, g, nullptr, nullptr, 0);
+      if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_check(e, "hipGraphInstantiate");
+      }
+      net->graph = g;
+      net->graph_ready = true;
+    }
+    QPH_TRY_HIP(hipGraphLaunch(net->exec, s));
+  }
+  if (outputs_host) {
+    for (size_t o = 0; o < net->outputs.size(); o++) {
+      if (!outputs_host[o]) continue;
+      int32_t id = net->outputs[o];
+      QPH_TRY_HIP(hipMemcpyAsync(outputs_host[o], net->tptr[id], (size_t)numel_of(net, id) * 4,
+                                 hipMemcpyDeviceToHost, s));
+    }
+    QPH_TRY_HIP(hipStreamSynchronize(s));
+  }
+  return QPH_OK;
+}
+
+}  // extern "C"

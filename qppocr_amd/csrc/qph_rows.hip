@@ -1,0 +1,470 @@
+// Row kernels of the rec model: LayerNorm, softmax (+ argmax), multi-head
+// attention; and the small elementwise / layout kernels.
+#include "qph_internal.h"
+
+namespace qph {
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------- LayerNorm
+//
+// The exported LayerNorm runs on the CPU executor as nine nodes
+// (qppocr-core/src/executor.rs:1518-1557 ReduceMean, 885-951 binary ops,
+// activation.rs:449-459 Sqrt), each rounding to f32:
+//   mu = (float)(sum_f64(x) / C); d = x - mu; sq = d*d (Pow 2);
+//   var = (float)(sum_f64(sq) / C); sd = sqrt(var + eps);
+//   y = ((d / sd) * gamma) + beta.
+// One wave per row; the f64 sums are exact for rows whose values span less
+// than 2^45 in magnitude ratio, which makes them independent of the order.
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta, float eps,
+                                                        int64_t rows, int64_t cols,
+                                                        float* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + row * cols;
+  float* yr = y + row * cols;
+  double s = 0.0;
+  for (int64_t j = lane; j < cols; j += 64) s += (double)xr[j];
+  s = wave_sum_f64(s);
+  const float mu = (float)(s / (double)cols);
+  double s2 = 0.0;
+  for (int64_t j = lane; j < cols; j += 64) {
+    float d = xr[j] - mu;
+    float sq = d * d;
+    s2 += (double)sq;
+  }
+  s2 = wave_sum_f64(s2);
+  const float var = (float)(s2 / (double)cols);
+  const float sd = __builtin_sqrtf(var + eps);
+  for (int64_t j = lane; j < cols; j += 64) {
+    float d = xr[j] - mu;
+    float v = d / sd;
+    v = v * gamma[j];
+    yr[j] = v + beta[j];
+  }
+}
+
+int launch_layernorm(const float* x, const float* gamma, const float* beta, float eps,
+                     int64_t rows, int64_t cols, float* y, hipStream_t s) {
+  hipLaunchKernelGGL(layernorm_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, x, gamma, beta,
+                     eps, rows, cols, y);
+  return launch_check("layernorm_kernel");
+}
+
+// ------------------------------------------------------------------ softmax
+//
+// softmax_last_dim row semantics (qppocr-kernels/src/activation.rs:346-403,
+// x86.rs:1091-1134): mx = row max; e = exp1(x - mx); the sum is eight lane
+// partials (lane j takes e[j], e[j+8], ... in order) reduced as
+// ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)), then the cols%8 tail added in
+// order; rows narrower than 8 sum sequentially; y = e * (1/sum).
+// Workgroup per row.  The max is order-free; e is stored to the output, then
+// eight threads run the lane chains over LDS-staged chunks, so the
+// summation order is the reference's.
+
+#define SM_CHUNK 4096  // floats per LDS chunk (16 KB)
+
+__device__ __forceinline__ float block_max_256(float v, float* red) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < 4; i++) r = fmaxf(r, red[i]);
+  return r;
+}
+
+// Row sum in the reference order over e[0..cols) (global, already written).
+// Returns the sum in all threads.  lds: SM_CHUNK floats + 16.
+__device__ float ref_order_sum(const float* e, int64_t cols, float* lds) {
+  const int tid = threadIdx.x;
+  float* chunk = lds;
+  float* part = lds + SM_CHUNK;  // 8 lane partials + result
+  float lanesum = 0.0f;          // valid in threads 0..7
+  const int64_t full = cols >= 8 ? (cols / 8) * 8 : 0;
+  for (int64_t c0 = 0; c0 < full; c0 += SM_CHUNK) {
+    const int64_t n = (full - c0) < SM_CHUNK ? (full - c0) : SM_CHUNK;
+    __syncthreads();
+    for (int64_t i = tid; i < n; i += 256) chunk[i] = e[c0 + i];
+    __syncthreads();
+    if (tid < 8) {
+      float s = lanesum;
+      for (int64_t i = tid; i < n; i += 8) s = s + chunk[i];
+      lanesum = s;
+    }
+  }
+  __syncthreads();
+  if (tid < 8) part[tid] = lanesum;
+  __syncthreads();
+  if (tid == 0) {
+    float sum;
+    int64_t i;
+    if (cols >= 8) {
+      float t0 = part[0] + part[4], t1 = part[1] + part[5], t2 = part[2] + part[6],
+            t3 = part[3] + part[7];
+      sum = (t0 + t1) + (t2 + t3);
+      i = full;
+    } else {
+      sum = 0.0f;
+      i = 0;
+    }
+    for (; i < cols; i++) sum = sum + e[i];
+    part[8] = sum;
+  }
+  __syncthreads();
+  return part[8];
+}
+
+// probs may alias logits (in-place softmax).  pairs may be NULL.
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, int64_t cols,
+                                                           float* probs, float* pairs) {
+  __shared__ float lds[SM_CHUNK + 16];
+  __shared__ float red[8];
+  __shared__ int redi[4];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* xr = logits + row * cols;
+  float* pr = probs + row * cols;
+  float mx = -__builtin_inff();
+  if (cols >= 8) {
+    for (int64_t i = tid; i < cols; i += 256) mx = fmaxf(mx, xr[i]);
+    mx = block_max_256(mx, red);
+  } else {
+    // rows narrower than 8: sequential max (activation.rs:362-371)
+    mx = xr[0];
+    for (int64_t i = 1; i < cols; i++)
+      if (xr[i] > mx) mx = xr[i];
+  }
+  __syncthreads();  // every read of the row precedes any in-place write
+  for (int64_t i = tid; i < cols; i += 256) pr[i] = exp1(xr[i] - mx);
+  __threadfence_block();
+  const float sum = ref_order_sum(pr, cols, lds);
+  const float inv = 1.0f / sum;
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  for (int64_t i = tid; i < cols; i += 256) {
+    float p = pr[i] * inv;
+    pr[i] = p;
+    if (p > bv) {  // ascending i per thread: keeps the first strict max
+      bv = p;
+      bi = (int)i;
+    }
+  }
+  if (!pairs) return;
+  // argmax reduction: larger value wins, ties -> lower index (rec.rs:46-54)
+  for (int off = 32; off >= 1; off >>= 1) {
+    float ov = __shfl_xor(bv, off, 64);
+    int oi = __shfl_xor(bi, off, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const int lane = tid & 63, wave = tid >> 6;
+  __syncthreads();
+  if (lane == 0) {
+    red[wave] = bv;
+    redi[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float v = red[0];
+    int ix = redi[0];
+    for (int w = 1; w < 4; w++)
+      if (red[w] > v || (red[w] == v && redi[w] < ix)) {
+        v = red[w];
+        ix = redi[w];
+      }
+    pairs[2 * row] = v;
+    pairs[2 * row + 1] = __uint_as_float((unsigned)ix);
+  }
+}
+
+int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s) {
+  if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, t, cols, t,
+                     (float*)nullptr);
+  return launch_check("softmax_rows_kernel");
+}
+
+int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, float* probs,
+                          float* pairs, hipStream_t s) {
+  if (!probs) return fail(QPH_EINVAL, "softmax_argmax: probs buffer required");
+  if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols,
+                     probs, pairs);
+  return launch_check("softmax_rows_kernel");
+}
+
+// argmax over probabilities: first strict max (rec.rs:46-54).
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ probs,
+                                                     int64_t rows, int64_t cols,
+                                                     float* __restrict__ pairs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* pr = probs + row * cols;
+  float bv = pr[0];
+  int bi = 0;
+  bool have = false;
+  for (int64_t i = lane; i < cols; i += 64) {
+    float p = pr[i];
+    if (!have || p > bv) {
+      bv = p;
+      bi = (int)i;
+      have = true;
+    }
+  }
+  if (!have) {
+    bv = -__builtin_inff();
+    bi = 0x7fffffff;
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    float ov = __shfl_xor(bv, off, 64);
+    int oi = __shfl_xor(bi, off, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    pairs[2 * row] = bv;
+    pairs[2 * row + 1] = __uint_as_float((unsigned)bi);
+  }
+}
+
+int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, probs, rows, cols,
+                     pairs);
+  return launch_check("argmax_kernel");
+}
+
+// Steps t >= t_valid[b] become (0, blank): the padded tail of a bucketed
+// line never emits (CTC collapse skips index 0).
+__global__ void mask_pairs_kernel(float* pairs, int64_t batch, int64_t t, const int32_t* tv) {
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= batch * t) return;
+  int64_t b = idx / t, s = idx - b * t;
+  if (s >= tv[b]) {
+    pairs[2 * idx] = 0.0f;
+    pairs[2 * idx + 1] = __uint_as_float(0u);
+  }
+}
+
+int launch_mask_pairs(float* pairs, int64_t batch, int64_t t, const int32_t* tv, hipStream_t s) {
+  hipLaunchKernelGGL(mask_pairs_kernel, dim3(ceil_div(batch * t, 256)), dim3(256), 0, s, pairs,
+                     batch, t, tv);
+  return launch_check("mask_pairs_kernel");
+}
+
+// ---------------------------------------------------------------- attention
+//
+// SVTR-style self-attention on the packed QKV MatMul output
+// qkv[b][t][3][H][dh]: q = q * scale (Mul node), S = q . k^T and O = P . v
+// through the small-matmul path (qppocr-kernels/src/shape.rs:664-697: each
+// element is fma(a[kk], b[kk][j], c) from 0, kk ascending), P = softmax over
+// the last axis (activation.rs:346-403), out[b][t][h*dh + d].
+// One workgroup per (b, h); K and V of that head in LDS; each wave takes
+// query rows t1 = wave, wave+4, ... (the loop runs the same number of times
+// in every wave so that the block barriers stay uniform).
+
+__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ qkv, int64_t T,
+                                                        int64_t H, int64_t DH, float scale,
+                                                        float* __restrict__ out) {
+  extern __shared__ float sm[];
+  const int64_t b = blockIdx.x / H, h = blockIdx.x - b * H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t D = H * DH;
+  const int ldk = (int)DH + 1;
+  float* sk = sm;                        // T x (DH+1)
+  float* sv = sk + T * ldk;              // T x (DH+1)
+  float* sp = sv + T * ldk;              // 4 waves x (T scores + DH scaled q)
+  const float* base = qkv + b * T * 3 * D;
+  for (int64_t i = tid; i < T * DH; i += 256) {
+    int64_t t = i / DH, d = i - t * DH;
+    const float* row = base + t * 3 * D + h * DH + d;
+    sk[t * ldk + d] = row[D];
+    sv[t * ldk + d] = row[2 * D];
+  }
+  float* p = sp + wave * (T + DH);
+  float* qrow = p + T;
+  for (int64_t tb = 0; tb < T; tb += 4) {
+    const int64_t t1 = tb + wave;
+    const bool active = t1 < T;
+    if (active)
+      for (int64_t d = lane; d < DH; d += 64) qrow[d] = base[t1 * 3 * D + h * DH + d] * scale;
+    __syncthreads();
+    // scores: lane j -> S[t1][j] = chain over d of fma(q[t1][d], k[j][d], acc)
+    if (active)
+      for (int64_t j = lane; j < T; j += 64) {
+        float acc = 0.0f;
+        for (int64_t d = 0; d < DH; d++) acc = __builtin_fmaf(qrow[d], sk[j * ldk + d], acc);
+        p[j] = acc;
+      }
+    __syncthreads();
+    // softmax over p[0..T) in the reference order
+    float mx = 0.0f;
+    if (active) {
+      if (T >= 8) {
+        mx = -__builtin_inff();
+        for (int64_t j = lane; j < T; j += 64) mx = fmaxf(mx, p[j]);
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      } else {
+        mx = p[0];
+        for (int64_t j = 1; j < T; j++)
+          if (p[j] > mx) mx = p[j];
+      }
+    }
+    __syncthreads();
+    if (active)
+      for (int64_t j = lane; j < T; j += 64) p[j] = exp1(p[j] - mx);
+    __syncthreads();
+    float inv = 0.0f;
+    if (active) {
+      float part = 0.0f;
+      const int64_t full = T >= 8 ? (T / 8) * 8 : 0;
+      if (lane < 8)
+        for (int64_t j = lane; j < full; j += 8) part = part + p[j];
+      float l[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) l[q] = __shfl(part, q, 64);
+      float sum;
+      int64_t j0;
+      if (T >= 8) {
+        float t0 = l[0] + l[4], t1s = l[1] + l[5], t2 = l[2] + l[6], t3 = l[3] + l[7];
+        sum = (t0 + t1s) + (t2 + t3);
+        j0 = full;
+      } else {
+        sum = 0.0f;
+        j0 = 0;
+      }
+      for (int64_t j = j0; j < T; j++) sum = sum + p[j];
+      inv = 1.0f / sum;
+    }
+    __syncthreads();
+    if (active)
+      for (int64_t j = lane; j < T; j += 64) p[j] = p[j] * inv;
+    __syncthreads();
+    // O[t1][d] = chain over j of fma(P[t1][j], v[j][d], acc)
+    if (active)
+      for (int64_t d = lane; d < DH; d += 64) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < T; j++) acc = __builtin_fmaf(p[j], sv[j * ldk + d], acc);
+        out[(b * T + t1) * D + h * DH + d] = acc;
+      }
+    __syncthreads();
+  }
+}
+
+int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
+                     float scale, float* out, hipStream_t s) {
+  size_t lds = (size_t)(2 * t * (dh + 1) + 4 * (t + dh)) * sizeof(float);
+  if (lds > 64 * 1024) return fail(QPH_EUNSUPPORTED, "attention: T*dh too large for LDS");
+  if (batch * heads > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "attention: grid too large");
+  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)(batch * heads)), dim3(256), lds, s, qkv,
+                     t, heads, dh, scale, out);
+  return launch_check("attention_kernel");
+}
+
+// ------------------------------------------------------------- elementwise
+
+__global__ void act_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n, Act a) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    float v = x[i];
+    y[i] = a.kind == 5 ? hsig1(v, a.c1, a.c2) : act_apply(v, a);
+  }
+}
+
+int launch_elementwise_act(const float* x, float* y, int64_t n, const Act& a, hipStream_t s) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(act_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n, a);
+  return launch_check("act_kernel");
+}
+
+// resize_nearest (qppocr-kernels/src/resize.rs:26-57):
+// iy = min((int)((float)oy * (float)H / (float)oh), H-1), likewise ix.
+__global__ void resize_nearest_kernel(const float* __restrict__ x, int64_t h, int64_t w,
+                                      int64_t oh, int64_t ow, float* __restrict__ y) {
+  const int64_t p = blockIdx.y;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= oh * ow) return;
+  const int64_t oy = idx / ow, ox = idx - oy * ow;
+  int64_t iy = (int64_t)((float)oy * (float)h / (float)oh);
+  int64_t ix = (int64_t)((float)ox * (float)w / (float)ow);
+  if (iy > h - 1) iy = h - 1;
+  if (ix > w - 1) ix = w - 1;
+  y[p * oh * ow + idx] = x[(p * h + iy) * w + ix];
+}
+
+int launch_resize_nearest(const float* x, int64_t nc, int64_t h, int64_t w, int64_t oh,
+                          int64_t ow, float* y, hipStream_t s) {
+  if (nc > 65535) return fail(QPH_EUNSUPPORTED, "resize: too many planes");
+  hipLaunchKernelGGL(resize_nearest_kernel, dim3(ceil_div(oh * ow, 256), (unsigned)nc), dim3(256),
+                     0, s, x, h, w, oh, ow, y);
+  return launch_check("resize_nearest_kernel");
+}
+
+// Broadcast binary op in place (elementwise.rs:185-298): one IEEE op each.
+__global__ void binary_kernel(float* __restrict__ a, const float* __restrict__ b, int64_t rows,
+                              int64_t cols, int op, int bmode) {
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; idx < rows * cols; idx += stride) {
+    int64_t r = idx / cols, j = idx - r * cols;
+    float bv = bmode == 0 ? b[r] : (bmode == 1 ? b[j] : (bmode == 2 ? b[0] : b[idx]));
+    float av = a[idx];
+    float o;
+    switch (op) {
+      case 0: o = av + bv; break;
+      case 1: o = av - bv; break;
+      case 2: o = av * bv; break;
+      default: o = av / bv; break;
+    }
+    a[idx] = o;
+  }
+}
+
+int launch_binary(float* a, const float* b, int64_t rows, int64_t cols, int op, int bmode,
+                  hipStream_t s) {
+  int64_t blocks = (rows * cols + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(binary_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a, b, rows, cols, op,
+                     bmode);
+  return launch_check("binary_kernel");
+}
+
+// reduce_mean over the last axis (shape.rs:510-560): f64 sum, / cols, to f32.
+__global__ __launch_bounds__(256) void reduce_mean_kernel(const float* __restrict__ x, int64_t rows,
+                                                          int64_t cols, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  double s = 0.0;
+  for (int64_t j = lane; j < cols; j += 64) s += (double)x[row * cols + j];
+  s = wave_sum_f64(s);
+  if (lane == 0) out[row] = (float)(s / (double)cols);
+}
+
+}  // namespace qph
+
+using namespace qph;
+
+extern "C" QPH_API int qph_reduce_mean_last(qph_ctx* ctx, const float* x, int64_t rows,
+                                            int64_t cols, float* out) {
+  if (!ctx) return fail(QPH_EINVAL, "null context");
+  if (rows <= 0 || cols <= 0 || !x || !out) return fail(QPH_EINVAL, "reduce_mean: bad argument");
+  hipLaunchKernelGGL(reduce_mean_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, ctx->stream, x,
+                     rows, cols, out);
+  return launch_check("reduce_mean_kernel");
+}

@@ -1,0 +1,81 @@
+"""End-to-end parity of the five workloads on the GPU against the CPU oracle.
+
+Bar: bit-exact fp32 outputs (every element equal) and identical CTC argmax
+ids; the target's tolerance (1e-4 relative / 1e-5 absolute, argmax ids equal
+except where the top-2 logit gap is below 1e-4) is checked as well, so a
+future kernel that trades exactness for speed still has a stated bar.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, baseline_tol_check
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def test_cfg1_conv3x3_bias_relu(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import configs, ops
+    x, w, b = configs.cfg1(0)
+    print("cfg1 conv3x3 32->32 160x160 bias+relu", flush=True)
+    y = ops.conv2d(_t(torch, x), _t(torch, w), _t(torch, b), ops.conv_params(1, 1, 1, 1), 2)
+    ref = oracle.conv2d(x, w, b, oracle.conv_params(1, 1, 1, 1), oracle.ACT_RELU)
+    got = y.cpu().numpy()
+    baseline_tol_check(got, ref)
+    assert_bitexact(got, ref, "cfg1")
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_cfg2_depthwise_hardswish(gpu, oracle, case):
+    torch = gpu
+    from qppocr_amd import configs, ops
+    x, w, b, k, s = configs.cfg2(1)[case]
+    print(f"cfg2 case {case}: C{x.shape[1]} {x.shape[2]}^2 k{k} s{s}", flush=True)
+    c = x.shape[1]
+    y = ops.conv2d(_t(torch, x), _t(torch, w), _t(torch, b),
+                   ops.conv_params(s, s, k // 2, k // 2, group=c), 3)
+    ref = oracle.conv2d(x, w, b, oracle.conv_params(s, s, k // 2, k // 2, group=c))
+    ref = oracle.binary_flat(ref, oracle.hardsigmoid(ref), 2)
+    got = y.cpu().numpy()
+    baseline_tol_check(got, ref)
+    assert_bitexact(got, ref, f"cfg2[{case}]")
+
+
+def test_cfg3_det_net(gpu, oracle):
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    g, x = nets.build_det(2, 640, 640)
+    print("cfg3 det 1x3x640x640", flush=True)
+    sess = nets.HipSession(g)
+    out = sess.run(x)[0]
+    ref = onets.run_graph(g, x)[0]
+    baseline_tol_check(out, ref)
+    assert_bitexact(out, ref, "det prob map")
+    out2 = sess.run(x)[0]   # graph replay gives the same bits
+    assert_bitexact(out2, out, "det replay")
+    sess.close()
+
+
+def _ids(pairs):
+    return np.ascontiguousarray(pairs[..., 1]).view(np.uint32)
+
+
+def test_cfg4_rec_net(gpu, oracle):
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    g, x = nets.build_rec(3, 32, 320)
+    print("cfg4 rec 32x3x48x320", flush=True)
+    sess = nets.HipSession(g)
+    probs, pairs = sess.run(x)
+    probs_ref, pairs_ref = onets.run_graph(g, x)
+    baseline_tol_check(probs, probs_ref)
+    assert_bitexact(probs, probs_ref, "rec probs")
+    assert (_ids(pairs) == _ids(pairs_ref)).all()
+    assert_bitexact(pairs[..., 0], pairs_ref[..., 0], "rec pair values")
+    probs2, pairs2 = sess.run(x)
+    assert_bitexact(probs2, probs, "rec replay")
+    sess.close()

@@ -1,0 +1,361 @@
+"""Parity of every HIP operator with the CPU oracle (bit-exact), through the C ABI.
+
+The oracle restates the qppocr-kernels CPU arithmetic; the HIP kernels keep
+each element's operation sequence, so outputs must be identical element for
+element.  Shapes follow the reference's own kernel test cases
+(qppocr-kernels/tests/kernels.rs:162-590, 638-683, 1038-1141, 1143-1260,
+1422-1467).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, baseline_tol_check
+
+pytestmark = pytest.mark.gpu
+
+# (name, n, c, m, h, w, kh, kw, sh, sw, ph, pw, group, bias)  kernels.rs:162-590
+CONV_CASES = [
+    ("1x1 conv (gemm path)", 1, 16, 24, 32, 32, 1, 1, 1, 1, 0, 0, 1, True),
+    ("3x3 s1 p1", 1, 3, 16, 64, 64, 3, 3, 1, 1, 1, 1, 1, True),
+    ("3x3 s2 p1", 1, 3, 16, 65, 65, 3, 3, 2, 2, 1, 1, 1, True),
+    ("5x5 s1 p2", 1, 8, 16, 33, 33, 5, 5, 1, 1, 2, 2, 1, False),
+    ("5x5 s2 p2", 1, 8, 16, 64, 64, 5, 5, 2, 2, 2, 2, 1, True),
+    ("depthwise 3x3 s1 p1", 1, 16, 16, 64, 64, 3, 3, 1, 1, 1, 1, 16, True),
+    ("depthwise 3x3 on 1x1", 1, 4, 4, 1, 1, 3, 3, 1, 1, 1, 1, 4, False),
+    ("depthwise 3x3 s2 p1", 1, 32, 32, 65, 65, 3, 3, 2, 2, 1, 1, 32, True),
+    ("depthwise 5x5 s1 p2", 1, 24, 24, 40, 40, 5, 5, 1, 1, 2, 2, 24, True),
+    ("depthwise 5x5 s2 p2", 1, 24, 24, 40, 40, 5, 5, 2, 2, 2, 2, 24, False),
+    ("depthwise 3x3 s[1,2]", 1, 32, 32, 40, 40, 3, 3, 1, 2, 1, 1, 32, True),
+    ("depthwise 3x3 s[2,1]", 1, 32, 32, 40, 40, 3, 3, 2, 1, 1, 1, 32, True),
+    ("depthwise 5x5 s[1,2]", 1, 24, 24, 40, 40, 5, 5, 1, 2, 2, 2, 24, True),
+    ("3x3 s[1,2] p1", 1, 8, 16, 40, 40, 3, 3, 1, 2, 1, 1, 1, True),
+    ("3x3 s[2,1] p1", 1, 8, 16, 40, 40, 3, 3, 2, 1, 1, 1, 1, True),
+    ("depthwise 7x7 s1 p3", 1, 32, 32, 40, 40, 7, 7, 1, 1, 3, 3, 32, True),
+    ("depthwise 7x7 s2 p3", 1, 32, 32, 40, 40, 7, 7, 2, 2, 3, 3, 32, True),
+    ("batch=2 3x3", 2, 8, 16, 24, 24, 3, 3, 1, 1, 1, 1, 1, True),
+    ("M=17 N=713 (tail rows)", 1, 8, 17, 30, 24, 1, 1, 1, 1, 0, 0, 1, True),
+    ("M=3 3x3 (all tail)", 1, 4, 3, 16, 16, 3, 3, 1, 1, 1, 1, 1, True),
+    ("dense 96->24 3x3 (neck)", 1, 96, 24, 20, 20, 3, 3, 1, 1, 1, 1, 1, True),
+    ("dense 32->40 3x3 wide M", 2, 32, 40, 19, 37, 3, 3, 1, 1, 1, 1, 1, True),
+    ("1x1 batch=3 M%4", 3, 20, 13, 7, 9, 1, 1, 1, 1, 0, 0, 1, True),
+]
+
+
+def _t(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def _n(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=[c[0] for c in CONV_CASES])
+@pytest.mark.parametrize("act", [0, 2, 3])
+def test_conv2d(gpu, oracle, case, act):
+    torch = gpu
+    from qppocr_amd import ops
+    name, n, c, m, h, w, kh, kw, sh, sw, ph, pw, g, has_b = case
+    rng = np.random.default_rng(abs(hash(name)) % (1 << 32))
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = rng.uniform(-1, 1, (m, c // g, kh, kw)).astype(np.float32)
+    b = rng.uniform(-1, 1, (m,)).astype(np.float32) if has_b else None
+    params = oracle.conv_params(sh, sw, ph, pw, group=g)
+    # the reference graph fuses only ReLU into group-1 convs; hardswish is the
+    # HardSigmoid + Mul pair applied to the conv output
+    y_ref = oracle.conv2d(x, wt, b, params, act if act != 3 else 0)
+    if act == 3:
+        y_ref = oracle.binary_flat(y_ref, oracle.hardsigmoid(y_ref), 2)
+    y = ops.conv2d(_t(torch, x), _t(torch, wt), None if b is None else _t(torch, b),
+                   ops.conv_params(sh, sw, ph, pw, group=g), act)
+    assert_bitexact(_n(y), y_ref, name)
+
+
+def test_conv2d_residual(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(5)
+    for (c, m, k, s, g) in [(8, 16, 3, 1, 1), (16, 32, 1, 1, 1), (24, 24, 5, 1, 24)]:
+        x = rng.standard_normal((2, c, 21, 23)).astype(np.float32)
+        wt = rng.standard_normal((m, c // g, k, k)).astype(np.float32)
+        b = rng.standard_normal((m,)).astype(np.float32)
+        p = oracle.conv_params(s, s, k // 2, k // 2, group=g)
+        ys = oracle.conv_out_shape(x.shape, wt.shape, p)
+        r = rng.standard_normal(ys).astype(np.float32)
+        act = 2 if g == 1 else 0
+        y_ref = oracle.conv2d(x, wt, b, p, act, residual=r)
+        y = ops.conv2d(_t(torch, x), _t(torch, wt), _t(torch, b),
+                       ops.conv_params(s, s, k // 2, k // 2, group=g), act, residual=_t(torch, r))
+        assert_bitexact(_n(y), y_ref, f"residual c{c} m{m} k{k} g{g}")
+
+
+def test_conv1x1_upsample_add_and_transposed_out(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((1, 32, 20, 20)).astype(np.float32)
+    wt = rng.standard_normal((96, 32, 1, 1)).astype(np.float32)
+    b = rng.standard_normal((96,)).astype(np.float32)
+    coarse = rng.standard_normal((1, 96, 10, 10)).astype(np.float32)
+    y_ref = oracle.conv2d(x, wt, b)
+    y_ref = oracle.binary_flat(y_ref, oracle.resize_nearest(coarse, 20, 20), 0)
+    y = ops.conv2d(_t(torch, x), _t(torch, wt), _t(torch, b), residual=_t(torch, coarse), res_up=2)
+    assert_bitexact(_n(y), y_ref, "lateral + up2")
+    # [B, C, 1, T] -> [B, T, C]
+    x = rng.standard_normal((4, 64, 1, 40)).astype(np.float32)
+    wt = rng.standard_normal((48, 64, 1, 1)).astype(np.float32)
+    y_ref = oracle.conv2d(x, wt, b[:48], act=0)
+    y_ref = oracle.binary_flat(y_ref, oracle.hardsigmoid(y_ref), 2)
+    y_ref = y_ref.reshape(4, 48, 40).transpose(0, 2, 1)
+    y = ops.conv2d(_t(torch, x), _t(torch, wt), _t(torch, b[:48]), act_kind=3, trans_out=True)
+    assert_bitexact(_n(y), y_ref, "trans_out")
+
+
+def test_conv3x3_placed_output(gpu, oracle):
+    """Smoothing conv written upsampled into a channel slot of the neck concat."""
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(7)
+    out = torch.full((1, 96, 40, 40), float("nan"), device="cuda")
+    ref = np.zeros((1, 96, 40, 40), dtype=np.float32)
+    for slot, hw in enumerate([5, 10, 20, 40]):
+        x = rng.standard_normal((1, 96, hw, hw)).astype(np.float32)
+        wt = rng.standard_normal((24, 96, 3, 3)).astype(np.float32)
+        b = rng.standard_normal((24,)).astype(np.float32)
+        y = oracle.conv2d(x, wt, b, oracle.conv_params(1, 1, 1, 1))
+        ref[:, 24 * slot:24 * slot + 24] = oracle.resize_nearest(y, 40, 40)
+        ops.conv2d(_t(torch, x), _t(torch, wt), _t(torch, b), ops.conv_params(1, 1, 1, 1),
+                   out=out, y_ctotal=96, y_coff=24 * slot, y_up=40 // hw)
+    assert_bitexact(_n(out), ref, "concat slots")
+
+
+def test_grouped_conv_unsupported(gpu):
+    torch = gpu
+    from qppocr_amd import ops
+    from qppocr_amd._lib import QphError
+    x = torch.zeros((1, 16, 8, 8), device="cuda")
+    w = torch.zeros((24, 4, 3, 3), device="cuda")
+    with pytest.raises(QphError) as e:
+        ops.conv2d(x, w, params=ops.conv_params(1, 1, 1, 1, group=4))
+    assert e.value.code == -3
+
+
+SGEMM_SHAPES = [(1, 1, 1), (64, 64, 64), (1, 500, 300), (17, 33, 129), (256, 96, 384),
+                (1, 368, 368 * 9), (17, 713, 77), (5, 37, 13)]
+
+
+@pytest.mark.parametrize("mnk", SGEMM_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in SGEMM_SHAPES])
+@pytest.mark.parametrize("serial", [False, True])
+def test_sgemm(gpu, oracle, mnk, serial):
+    torch = gpu
+    from qppocr_amd import ops
+    m, n, k = mnk
+    rng = np.random.default_rng(m * 1000 + n + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    bias = rng.uniform(-1, 1, (m,)).astype(np.float32)
+    c_ref = oracle.sgemm(a, b, m, n, k, bias, serial=serial)
+    c = ops.sgemm(_t(torch, a), _t(torch, b), m, n, k, _t(torch, bias), serial=serial)
+    assert_bitexact(_n(c), c_ref, f"sgemm {mnk}")
+    ref64 = a.astype(np.float64) @ b + bias
+    from conftest import rel_check
+    rel_check(_n(c), ref64)
+
+
+def test_sgemm_bias_placement(gpu, oracle):
+    """Bias seeded vs added after the chain: with a = [1, 1], b rows [1], [2^24]
+    and bias 1, the after-chain order gives 2^24 and the seeded order 2^24 + 2."""
+    torch = gpu
+    from qppocr_amd import ops
+    for (m, n, k) in [(5, 5, 2), (64, 16, 4000)]:
+        a = np.zeros((m, k), np.float32)
+        a[:, :2] = 1.0
+        b = np.zeros((k, n), np.float32)
+        b[0] = 1.0
+        b[1] = 2.0 ** 24
+        bias = np.ones(m, np.float32)
+        c_ref = oracle.sgemm(a, b, m, n, k, bias)
+        c = _n(ops.sgemm(_t(torch, a), _t(torch, b), m, n, k, _t(torch, bias)))
+        assert_bitexact(c, c_ref, f"bias placement {m}x{n}x{k}")
+
+
+def test_linear_epilogues(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(11)
+    for (rows, k, n, act, res) in [(1280, 256, 768, 0, False), (1280, 256, 1024, 1, False),
+                                   (1280, 1024, 256, 0, True), (37, 256, 18709, 0, False),
+                                   (100, 77, 130, 2, True)]:
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        w = (rng.standard_normal((k, n)) * math.sqrt(2 / k)).astype(np.float32)
+        b = (rng.standard_normal((n,)) * 0.1).astype(np.float32)
+        r = rng.standard_normal((rows, n)).astype(np.float32) if res else None
+        y_ref = oracle.matmul(x, w)
+        y_ref = oracle.binary_bcast(y_ref, b, rows, n, 0, 1)
+        if act == 1:
+            y_ref = oracle.gelu_inplace(y_ref)
+        elif act == 2:
+            y_ref = oracle.relu_inplace(y_ref)
+        if res:
+            y_ref = oracle.binary_flat(y_ref, r, 0)
+        y = ops.linear(_t(torch, x), _t(torch, w), _t(torch, b), act,
+                       None if r is None else _t(torch, r))
+        assert_bitexact(_n(y), y_ref, f"linear {rows}x{k}x{n}")
+
+
+def test_matmul_batched(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(12)
+    a = rng.uniform(-1, 1, (2, 3, 40, 80)).astype(np.float32)   # kernels.rs shape_op_tests
+    b = rng.uniform(-1, 1, (80, 101)).astype(np.float32)
+    assert_bitexact(_n(ops.matmul(_t(torch, a), _t(torch, b))), oracle.matmul(a, b), "shared B")
+    a = rng.uniform(-1, 1, (16, 40, 32)).astype(np.float32)
+    b = rng.uniform(-1, 1, (16, 32, 40)).astype(np.float32)
+    assert_bitexact(_n(ops.matmul(_t(torch, a), _t(torch, b))), oracle.matmul(a, b), "batched B")
+
+
+@pytest.mark.parametrize("inner", [1, 4, 7, 8, 13, 40, 100, 4099, 18709])
+def test_softmax_last_dim(gpu, oracle, inner):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(inner)
+    rows = 37
+    t = (rng.standard_normal((rows, inner)) * 3).astype(np.float32)
+    ref = oracle.softmax_last_dim(t.copy(), inner)
+    g = _t(torch, t)
+    ops.softmax_last_dim(g, inner)
+    assert_bitexact(_n(g), ref, f"softmax {inner}")
+
+
+def test_softmax_argmax_and_ties(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(13)
+    logits = (rng.standard_normal((64, 18709)) * 2).astype(np.float32)
+    logits[3, 100] = logits[3, 50] = 40.0        # tie: lowest index wins
+    logits[5, :] = 0.0                           # all equal: index 0
+    logits[7, 18708] = 30.0                      # last column
+    probs, pairs = ops.softmax_argmax(_t(torch, logits))
+    p_ref = oracle.softmax_last_dim(logits.copy(), 18709)
+    pr_ref = oracle.ctc_argmax(p_ref)
+    assert_bitexact(_n(probs), p_ref, "probs")
+    assert_bitexact(_n(pairs)[:, 0], pr_ref[:, 0], "pair values")
+    ids = ops.pairs_ids(pairs).cpu().numpy()
+    ids_ref = oracle.pairs_ids(pr_ref)
+    assert (ids == ids_ref).all()
+    assert ids[3] == 50 and ids[5] == 0 and ids[7] == 18708
+
+
+def test_ctc_argmax_masked(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(14)
+    probs = rng.random((4, 20, 97)).astype(np.float32)
+    probs[0, 2, 10] = probs[0, 2, 20] = 2.0
+    tv = [20, 10, 0, 5]
+    pairs = _n(ops.ctc_argmax(_t(torch, probs), tv))
+    ref = oracle.ctc_argmax(probs)
+    ids = pairs[..., 1].copy().view(np.uint32)
+    ids_ref = ref[..., 1].copy().view(np.uint32)
+    for b in range(4):
+        assert (ids[b, :tv[b]] == ids_ref[b, :tv[b]]).all()
+        assert (ids[b, tv[b]:] == 0).all()
+    assert ids[0, 2] == 10
+
+
+def test_layernorm(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(15)
+    for rows, cols in [(1280, 256), (7, 33), (3, 1000)]:
+        x = (rng.standard_normal((rows, cols)) * 2 + 0.5).astype(np.float32)
+        g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+        b = (0.1 * rng.standard_normal(cols)).astype(np.float32)
+        ref = oracle.layernorm(x, g, b, 1e-6)
+        y = ops.layernorm(_t(torch, x), _t(torch, g), _t(torch, b), 1e-6)
+        assert_bitexact(_n(y), ref, f"layernorm {rows}x{cols}")
+
+
+@pytest.mark.parametrize("t", [40, 20, 5, 160])
+def test_attention(gpu, oracle, t):
+    torch = gpu
+    from qppocr_amd import ops, nets
+    from oracle import nets as onets
+    rng = np.random.default_rng(t)
+    b, heads, dh = 3, 8, 32
+    qkv = rng.standard_normal((b, t, 3 * heads * dh)).astype(np.float32)
+    g = nets.Graph((b, t, 3 * heads * dh))
+    o = g.attention(0, heads, dh, 1.0 / math.sqrt(dh))
+    g.outputs = [o]
+    ref = onets.run_graph(g, qkv)[0].reshape(b, t, heads * dh)
+    y = ops.attention(_t(torch, qkv), heads, dh, 1.0 / math.sqrt(dh))
+    assert_bitexact(_n(y), ref, f"attention T={t}")
+
+
+def test_convtranspose(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(16)
+    x = rng.uniform(-1, 1, (2, 24, 17, 19)).astype(np.float32)
+    w1 = rng.uniform(-1, 1, (24, 24, 2, 2)).astype(np.float32)
+    w2 = rng.uniform(-1, 1, (24, 1, 2, 2)).astype(np.float32)
+    y1 = oracle.convtranspose2d(x, w1)
+    assert_bitexact(_n(ops.convtranspose2d(_t(torch, x), _t(torch, w1))), y1, "convT")
+    ref = oracle.sigmoid_tensor(oracle.convtranspose2d(y1, w2))
+    got = _n(ops.convt_pair_sigmoid(_t(torch, x), _t(torch, w1), _t(torch, w2)))
+    assert_bitexact(got, ref, "convT pair + sigmoid")
+    # generic-size path of the pair kernel
+    x = rng.uniform(-1, 1, (1, 5, 6, 7)).astype(np.float32)
+    w1 = rng.uniform(-1, 1, (5, 3, 2, 2)).astype(np.float32)
+    w2 = rng.uniform(-1, 1, (3, 1, 2, 2)).astype(np.float32)
+    ref = oracle.sigmoid_tensor(oracle.convtranspose2d(oracle.convtranspose2d(x, w1), w2))
+    got = _n(ops.convt_pair_sigmoid(_t(torch, x), _t(torch, w1), _t(torch, w2)))
+    assert_bitexact(got, ref, "convT pair generic")
+
+
+def test_elementwise_activations(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(17)
+    x = rng.uniform(-1, 1, 4096).astype(np.float32)
+    special = np.array([0.0, -0.0, 3.0, -3.0, 88.0, -88.0, 100.0, -100.0, 1e-30, -1e-30, 6.0,
+                        -6.0, 1e6, -1e6], np.float32)
+    x = np.concatenate([x, x * 10, special])
+    gx = _t(torch, x)
+    assert_bitexact(_n(ops.sigmoid_tensor(gx)), oracle.sigmoid_tensor(x), "sigmoid")
+    assert_bitexact(_n(ops.hardsigmoid(gx)), oracle.hardsigmoid(x), "hardsigmoid")
+    assert_bitexact(_n(ops.relu_inplace(gx.clone())), oracle.relu_inplace(x.copy()), "relu")
+    assert_bitexact(_n(ops.gelu_inplace(gx.clone())), oracle.gelu_inplace(x.copy()), "gelu")
+    hs = oracle.binary_flat(x, oracle.hardsigmoid(x), 2)
+    assert_bitexact(_n(ops.activation(gx, 3)), hs, "hardswish")
+    er = oracle.erf_inplace(x.copy())
+    # erf via gelu identity is not exposed; check exp1/erf1 through sigmoid/gelu above
+    assert np.isfinite(er).all()
+
+
+def test_resize_nearest(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(18)
+    x = rng.uniform(-1, 1, (2, 3, 20, 30)).astype(np.float32)   # kernels.rs:1203-1219
+    for oh, ow in [(33, 47), (40, 60), (10, 15)]:
+        assert_bitexact(_n(ops.resize_nearest(_t(torch, x), oh, ow)),
+                        oracle.resize_nearest(x, oh, ow), f"resize {oh}x{ow}")
+
+
+def test_reduce_mean_and_binary(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(19)
+    x = rng.standard_normal((100, 256)).astype(np.float32)
+    assert_bitexact(_n(ops.reduce_mean_last(_t(torch, x))), oracle.reduce_mean_last(x), "mean")
+    b = rng.standard_normal(256).astype(np.float32)
+    for op in range(4):
+        got = _n(ops.binary_inplace(_t(torch, x), _t(torch, b), op, 1))
+        assert_bitexact(got, oracle.binary_bcast(x, b, 100, 256, op, 1), f"binary {op}")
+
+
+def test_baseline_tolerance_helper():
+    baseline_tol_check(np.array([1.0, 0.0]), np.array([1.00005, 5e-6]))
