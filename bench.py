@@ -1,0 +1,160 @@
+"""Throughput of the HIP backend on the det + rec workload, one JSON line.
+
+A step is one det forward on 1x3x640x640 plus one rec forward on a batch of
+32 lines of 3x48x320 (the det image and the 32 text lines of one page), both
+as replayed HIP graphs with their inputs already resident in HBM.  value =
+steps per second = det images per second with 32 recognised lines each;
+det_img_per_s and rec_lines_per_s are the stage-isolated rates from HIP
+events recorded on the session stream inside the timed region.
+
+roofline: the dominant kernel is the rec head GEMM (1280 x 18709 x 256,
+12.26 GFLOP of the step's 20.86).  Its average launch time comes from HIP
+events around each node of the rec graph (eager launches on the same stream),
+over the same number of steps, after the timed region.
+
+cpu_baseline: the CPU oracle (plain-C restatement of the qppocr-kernels
+AVX2 path, OpenMP over all host threads) on a bounded sample of the same
+workload, timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+REC_BATCH = 32
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-steps", type=int, default=6, help="CPU baseline sample (steps)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the det/rec path "
+                          "shards by image / rec batch with no exchange (see DESIGN.md), "
+                          "multi-GPU runs are not part of it", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from qppocr_amd import nets, ops
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    ctx = ops.context(0)
+    lib = ops._lib.load()
+    stream_ptr = lib.qph_ctx_stream(ctx)
+    stream = torch.cuda.ExternalStream(stream_ptr)
+
+    det_g, det_x = nets.build_det(2, 640, 640)
+    rec_g, rec_x = nets.build_rec(3, REC_BATCH, 320)
+    det = nets.HipSession(det_g)
+    rec = nets.HipSession(rec_g)
+    # inputs resident in HBM: copied once, then every step reuses them
+    det.run(det_x, outputs=False)
+    rec.run(rec_x, outputs=False)
+    det.sync()
+
+    for _ in range(args.warmup):
+        det.run(None, outputs=False)
+        rec.run(None, outputs=False)
+    det.sync()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    t0 = time.perf_counter()
+    for i in range(K):
+        ev[i][0].record(stream)
+        det.run(None, outputs=False)
+        ev[i][1].record(stream)
+        rec.run(None, outputs=False)
+        ev[i][2].record(stream)
+    det.sync()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / K
+    det_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / K
+    rec_ms = sum(b.elapsed_time(c) for _, b, c in ev) / K
+
+    # dominant kernel: rec head GEMM, events around each node (eager launches)
+    rec.set_profiling(True)
+    for _ in range(K):
+        rec.run(None, outputs=False)
+    rec.sync()
+    node_ms = rec.node_times()
+    rec.set_profiling(False)
+    head = len(rec_g.nodes) - 2        # linear 256 -> 18709
+    head_ms = node_ms[head]
+    d = rec_g.nodes[head]
+    rows = rec_g.numel(d["inp"]) // d["ws"][0]
+    head_flops = 2 * rows * d["ws"][0] * d["ws"][1]
+    achieved = head_flops / (head_ms * 1e-3) / 1e12
+
+    det_flops = nets.flops(det_g)
+    rec_flops = nets.flops(rec_g)
+    result = {
+        "metric": "det img/s @1x3x640x640 + rec lines/s @48x320 b32, fp32; % of roofline",
+        "value": round(1e3 / ms_step, 3),
+        "unit": "img/s (1 det image 1x3x640x640 + 32 rec lines 3x48x320 per step)",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded inputs, random-init weights)",
+        "config": {"workload": "det 1x3x640x640 (config 3) + rec 32x3x48x320 (config 4) per step",
+                   "det_gflop": round(det_flops / 1e9, 3), "rec_gflop": round(rec_flops / 1e9, 3)},
+        "det_img_per_s": round(1e3 / det_ms, 2),
+        "rec_lines_per_s": round(REC_BATCH * 1e3 / rec_ms, 1),
+        "det_ms": round(det_ms, 4),
+        "rec_ms": round(rec_ms, 4),
+        "roofline": {"bound": "mfma", "kernel": "rec head GEMM 1280x18709x256 (gemm_mfma_kernel)",
+                     "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": None, "avg_launch_ms": round(head_ms, 5)},
+    }
+
+    if not args.no_cpu:
+        from oracle import nets as onets
+        from oracle import oracle as O
+        O.lib()
+        onets.run_graph(det_g, det_x)          # warm-up (page-in, thread pool)
+        c0 = time.perf_counter()
+        for _ in range(args.cpu_steps):
+            onets.run_graph(det_g, det_x)
+            onets.run_graph(rec_g, rec_x)
+        c1 = time.perf_counter()
+        cpu_step = (c1 - c0) / args.cpu_steps
+        result["cpu_baseline"] = {
+            "value": round(1.0 / cpu_step, 4),
+            "unit": result["unit"],
+            "cores": O.threads(),
+            "kind": "port",
+            "sample": f"{args.cpu_steps} steps of det 1x3x640x640 + rec 32x3x48x320, "
+                      f"{cpu_step:.3f} s/step, C oracle -O3 -mavx2 -mfma, OpenMP",
+        }
+    print(json.dumps(result))
+    det.close()
+    rec.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -158,7 +158,7 @@ def test_sgemm(gpu, oracle, mnk, serial):
     c_ref = oracle.sgemm(a, b, m, n, k, bias, serial=serial)
     c = ops.sgemm(_t(torch, a), _t(torch, b), m, n, k, _t(torch, bias), serial=serial)
     assert_bitexact(_n(c), c_ref, f"sgemm {mnk}")
-    ref64 = a.astype(np.float64) @ b + bias
+    ref64 = a.astype(np.float64) @ b + bias[:, None]
     from conftest import rel_check
     rel_check(_n(c), ref64)
 
