@@ -592,7 +592,12 @@ QPO_API void qpo_sqrt_inplace(float* t, int64_t n) {
 /* LayerNorm exactly as the exported graph runs it on the CPU executor
  * (ReduceMean -> Sub -> Pow(2) -> ReduceMean -> Add(eps) -> Sqrt -> Div ->
  * Mul(gamma) -> Add(beta)), each node rounding to f32:
- * shape.rs:510-560, elementwise.rs:185-298, activation.rs:449-459. */
+ * shape.rs:510-560, elementwise.rs:185-298, activation.rs:449-459.
+ * Pow(d, 2) is the correctly rounded square d*d, as the reference's GPU plan
+ * lowers it (qppocr-gpu/src/plan.rs:2319-2330, shaders/n_elem.comp:61); the
+ * CPU executor calls the platform libm powf (elementwise.rs:32-34, "ulp-level
+ * differences across implementations"), which under glibc 2.35 returns the
+ * neighbouring float for about 0.07% of inputs. */
 QPO_API void qpo_layernorm_chain(const float* x, const float* gamma, const float* beta, float eps,
                                  int64_t rows, int64_t cols, float* y) {
 #pragma omp parallel
@@ -607,7 +612,7 @@ QPO_API void qpo_layernorm_chain(const float* x, const float* gamma, const float
       float mu = (float)(s / (double)cols);
       for (int64_t j = 0; j < cols; j++) d[j] = xr[j] - mu;
       double s2 = 0.0;
-      for (int64_t j = 0; j < cols; j++) s2 += (double)powf(d[j], 2.0f);
+      for (int64_t j = 0; j < cols; j++) s2 += (double)(d[j] * d[j]);
       float var = (float)(s2 / (double)cols);
       float sd = sqrtf(var + eps);
       float* yr = y + r * cols;

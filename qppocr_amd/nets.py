@@ -121,7 +121,7 @@ class Graph:
 
     def layernorm(self, x, g, b, eps):
         cols = self.weights[g].shape[0]
-        out = self.tensor(self.shapes[x])
+        out = self.tensor(self.lshapes[x])
         self.nodes.append(dict(op=OP_LAYERNORM, inp=x, in2=-1, out=out, out2=-1, w=g, bias=b,
                                w2=-1, ws=(cols, 1, 1, 1), w2s=(0, 0, 0, 0), cp=(1,) * 9,
                                act=ACT_NONE, res_up=0, trans_out=0, y_ctotal=0, y_coff=0, y_up=1,
@@ -139,7 +139,7 @@ class Graph:
 
     def softmax_argmax(self, logits, cols):
         s = self.shapes[logits]
-        probs = self.tensor(s)
+        probs = self.tensor(self.lshapes[logits])
         rows = self.numel(logits) // cols
         pairs = self.tensor((s[0], rows // s[0], 2))
         self.nodes.append(dict(op=OP_SOFTMAX_ARGMAX, inp=logits, in2=-1, out=probs, out2=pairs,
