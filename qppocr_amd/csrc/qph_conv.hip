@@ -15,16 +15,20 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // bias added after the chain (seeded in the M%4 tail of partial 32-column
 // panels), then the activation.
 //
-// Kernel: a 256-thread workgroup owns WM*16 output channels x a TH x TW
-// block of output pixels.  The input halo of the block (all or a chunk of
-// the input channels) sits in LDS, zero-filled outside the image, so every
-// tap is a plain LDS read.  Waves issue v_mfma_f32_16x16x4f32 (16 channels x
-// 16 pixels, 4 k per instruction, each k its own fma in order).  Weights
-// come from a k-major repack wk[Kpad][Mpad] (zero rows past K), so a lane
-// reads W[co][k] as one coalesced word.
+// Kernel: a 256-thread workgroup owns MB = 16*WM output channels x a TH x TW
+// block of output pixels.  Input channels are taken in chunks (multiples of
+// 4): the input halo of the block and the chunk's weights (a k-major repack
+// wk[Kpad][Mpad], Kpad = ceil(C/4)*4*T, zero past the real extent) are
+// staged in LDS with direct buffer->LDS loads, all of a chunk in flight at
+// once; lanes past the image edge or past C use an out-of-range buffer
+// offset and read 0, which is the zero padding.  The waves then run
+// v_mfma_f32_16x16x4f32 (16 channels x 16 pixels, 4 consecutive k per
+// instruction, each k its own rounding, in order) from LDS only.  k advances
+// over groups of four input channels: a group holds 4*T k values (T = kh*kw
+// taps), i.e. T MFMA k-steps, and the LDS offset of each (step, lane) inside
+// a group is a per-lane constant computed once.
 
-#define CONV_LDS_FLOATS 12288  // 48 KB halo budget per workgroup
-#define CONV_KOFF_MAX 4096
+#define CONV_LDS_FLOATS 16320  // 63.75 KB per workgroup: halo tile + weight slice
 
 // wk[k][mo] = w[mo][k] for k < kk, mo < m; zero elsewhere (Kpad x Mpad).
 __global__ void repack_conv_w_kernel(const float* __restrict__ w, int64_t m, int64_t kk,
@@ -35,18 +39,19 @@ __global__ void repack_conv_w_kernel(const float* __restrict__ w, int64_t m, int
   wk[idx] = (k < kk && mo < m) ? w[mo * kk + k] : 0.0f;
 }
 
-static inline int64_t kpad_of(int64_t kk) { return (kk + 3) / 4 * 4; }
 static inline int64_t mpad_of(int64_t m) { return (m + 31) / 32 * 32; }
+static inline int64_t kpad_of(int64_t cg, int64_t khkw) { return (cg + 3) / 4 * 4 * khkw; }
 
 int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw) {
-  return kpad_of(cg * kh * kw) * mpad_of(m);
+  return kpad_of(cg, kh * kw) * mpad_of(m);
 }
 
-int launch_repack_conv_w(const float* wt, int64_t m, int64_t kk, float* wk, hipStream_t s) {
-  int64_t kpad = kpad_of(kk), mpad = mpad_of(m);
+int launch_repack_conv_w_taps(const float* wt, int64_t m, int64_t cg, int64_t khkw, float* wk,
+                              hipStream_t s) {
+  int64_t kpad = kpad_of(cg, khkw), mpad = mpad_of(m);
   int64_t total = kpad * mpad;
   hipLaunchKernelGGL(repack_conv_w_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, wt, m,
-                     kk, kpad, mpad, wk);
+                     cg * khkw, kpad, mpad, wk);
   return launch_check("repack_conv_w_kernel");
 }
 
@@ -56,34 +61,55 @@ struct DenseConvK {
   const float* bias;
   const float* res;
   float* y;
-  int64_t c, h, w, m, mpad, kh, kw, sh, sw, ph, pw, oh, ow;
+  int64_t c, h, w, m, mpad, kpad, kh, kw, sh, sw, ph, pw, oh, ow;
   int64_t y_ctotal, y_coff, y_up;
-  int tw, th;          // pixel block: th rows x tw cols (th * tw = pixels per workgroup)
-  int cchunk;          // input channels per LDS fill
+  int tw, th;          // pixel block: th rows x tw cols
+  int cchunk;          // input channels per LDS fill (multiple of 4)
   int rt, ct;          // halo rows / cols
   int tiles_x;         // pixel blocks along ow
   Act act;
 };
 
+// Writes v to the up x up block of output pixel (oy, ox) (nearest upsample
+// by an integer factor); rows as 16-byte stores when up is 4 or 8.
+__device__ __forceinline__ void store_replicated(float* yb, int64_t yow, int64_t oy, int64_t ox,
+                                                 int up, float v) {
+  if (up == 1) {
+    yb[oy * yow + ox] = v;
+    return;
+  }
+  for (int dy = 0; dy < up; dy++) {
+    float* r = yb + (oy * up + dy) * yow + ox * up;
+    if (up % 4 == 0) {
+      const float4 q = make_float4(v, v, v, v);
+      for (int dx = 0; dx < up; dx += 4) *(float4*)(r + dx) = q;
+    } else if (up == 2) {
+      *(float2*)r = make_float2(v, v);
+    } else {
+      for (int dx = 0; dx < up; dx++) r[dx] = v;
+    }
+  }
+}
+
 // WM: waves along M (1: 16 channels, 4 waves along pixels; 2: 32 channels,
-// 2 waves along pixels).  NT: 16-pixel MFMA tiles per wave.
-template <int WM, int NT>
+// 2 waves along pixels).  NT: 16-pixel MFMA tiles per wave.  T: taps (kh*kw).
+template <int WM, int NT, int T>
 __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
-  constexpr int WP = 4 / WM;             // waves along pixels
-  constexpr int PIX = WP * NT * 16;      // pixels per workgroup
-  __shared__ float tile[CONV_LDS_FLOATS];
-  __shared__ int koff[CONV_KOFF_MAX];
+  constexpr int MB = 16 * WM;            // output channels per workgroup (4/WM waves along pixels)
+  __shared__ float lds[CONV_LDS_FLOATS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wp = wave / WM;
+  const int lg = lane >> 4, l16 = lane & 15;
   const int64_t bn = blockIdx.z;
-  const int64_t m0 = (int64_t)blockIdx.y * (16 * WM) + 16 * wm;
+  const int64_t mblk0 = (int64_t)blockIdx.y * MB;
+  const int64_t m0 = mblk0 + 16 * wm;
   const int tyb = blockIdx.x / p.tiles_x, txb = blockIdx.x - tyb * p.tiles_x;
   const int64_t oy0 = (int64_t)tyb * p.th, ox0 = (int64_t)txb * p.tw;
-  const int64_t iy0 = oy0 * p.sh - p.ph, ix0 = ox0 * p.sw - p.pw;
-  const int khkw = (int)(p.kh * p.kw);
-  const int kk_total = (int)(p.c * khkw);
+  const int iy0 = (int)(oy0 * p.sh - p.ph), ix0 = (int)(ox0 * p.sw - p.pw);
   const int plane = p.rt * p.ct;
+  const int kw = (int)p.kw;
+  const int H = (int)p.h, W = (int)p.w;
 
   // per-lane pixel offsets into the halo tile for each of this wave's tiles
   int poff[NT];
@@ -91,17 +117,26 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
   int64_t poy[NT], pox[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
-    int pix = (wp * NT + t) * 16 + (lane & 15);
+    int pix = (wp * NT + t) * 16 + l16;
     int py = pix / p.tw, px = pix - py * p.tw;
     poy[t] = oy0 + py;
     pox[t] = ox0 + px;
-    pval[t] = pix < PIX && py < p.th && poy[t] < p.oh && pox[t] < p.ow;
+    pval[t] = py < p.th && poy[t] < p.oh && pox[t] < p.ow;
     poff[t] = pval[t] ? (int)(py * p.sh * p.ct + px * p.sw) : 0;
+  }
+  // per-lane offset of k-step s inside a group of four channels:
+  // k_local = 4 s + lg -> channel k_local / T, tap k_local % T
+  int goff[T];
+#pragma unroll
+  for (int s = 0; s < T; s++) {
+    int kl = 4 * s + lg;
+    int ci = kl / T, tap = kl - ci * T;
+    int ky = tap / kw, kx = tap - ky * kw;
+    goff[s] = ci * plane + ky * p.ct + kx;
   }
 
   // accumulators (bias-seeded where the reference seeds)
   f32x4 acc[NT];
-  const int lg = lane >> 4;
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll
@@ -115,44 +150,75 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
       acc[t][v] = s0;
     }
 
+  // input image and repacked weights as buffer resources: offsets past the
+  // end read as 0
   const float* xn = p.x + bn * p.c * p.h * p.w;
-  for (int c0 = 0; c0 < p.c; c0 += p.cchunk) {
-    const int cc = (int)((p.c - c0) < p.cchunk ? (p.c - c0) : p.cchunk);
-    const int kloc = cc * khkw;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)xn, 0, (int)(p.c * p.h * p.w * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.wk, 0, (int)(p.kpad * p.mpad * 4), 0x00020000);
+  const unsigned OOB = 0x80000000u;
+
+  const int cpad = (int)((p.c + 3) / 4 * 4);
+  for (int c0 = 0; c0 < cpad; c0 += p.cchunk) {
+    const int cc = (cpad - c0) < p.cchunk ? (cpad - c0) : p.cchunk;  // multiple of 4
+    float* tile = lds;
+    float* wsl = lds + ((cc * plane + 63) & ~63);     // [cc*T][MB]
     __syncthreads();
-    // halo fill: cc channels x rt rows x ct cols, zero outside the image
-    for (int idx = tid; idx < cc * plane; idx += 256) {
-      int ci = idx / plane, r = idx - ci * plane;
-      int ry = r / p.ct, rx = r - ry * p.ct;
-      int64_t iy = iy0 + ry, ix = ix0 + rx;
-      float v = 0.0f;
-      if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w) v = xn[((c0 + ci) * p.h + iy) * p.w + ix];
-      tile[idx] = v;
-    }
-    for (int k = tid; k < ((kloc + 3) & ~3); k += 256) {
-      int off = 0;
-      if (k < kloc) {
-        int ci = k / khkw, r = k - ci * khkw;
-        int ky = r / (int)p.kw, kx = r - ky * (int)p.kw;
-        off = ci * plane + ky * p.ct + kx;
+    // halo fill: cc channels x rt rows, one buffer->LDS load per 64 columns
+    const int nrows = cc * p.rt;
+    for (int rr = wave; rr < nrows; rr += 4) {
+      const int ci = rr / p.rt, ry = rr - ci * p.rt;
+      const int iy = iy0 + ry;
+      const bool rowok = c0 + ci < p.c && iy >= 0 && iy < H;
+      const unsigned rowbase = (unsigned)(((c0 + ci) * H + iy) * W);
+      float* dst = tile + rr * p.ct;
+      for (int x0 = 0; x0 < p.ct; x0 += 64) {
+        if (lane < p.ct - x0) {
+          const int ix = ix0 + x0 + lane;
+          const unsigned off =
+              (rowok && ix >= 0 && ix < W) ? (rowbase + (unsigned)ix) * 4u : OOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              xr, (__attribute__((address_space(3))) void*)(dst + x0), 4, off, 0, 0, 0);
+        }
       }
-      koff[k] = off;
     }
+    // weight slice: rows c0*T .. (c0+cc)*T of wk, columns mblk0 .. +MB; one
+    // load moves 64/MB consecutive rows
+    {
+      constexpr int RPL = 64 / MB;   // rows per load
+      const int nkr = cc * T;
+      const int kr0 = c0 * T;
+      const int lr = lane / MB, lc = lane - lr * MB;
+      for (int r0 = wave * RPL; r0 < nkr; r0 += 4 * RPL) {
+        const int kr = r0 + lr;
+        const unsigned off = kr < nkr
+                                 ? (unsigned)(((int64_t)(kr0 + kr) * p.mpad + mblk0 + lc) * 4)
+                                 : OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wr, (__attribute__((address_space(3))) void*)(wsl + r0 * MB), 4, off, 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const int kbase = c0 * khkw;
-    const float* wkp = p.wk + (int64_t)kbase * p.mpad + m0 + (lane & 15);
-    for (int k0 = 0; k0 < kloc; k0 += 4) {
-      const int kl = k0 + lg;
-      const float a = wkp[(int64_t)kl * p.mpad];  // zero past K (repack)
-      const int ko = koff[kl];
+    const float* wl = wsl + 16 * wm + l16;
+    for (int q = 0; q < cc / 4; q++) {
+      const float* tq = tile + q * 4 * plane;
+      const float* wq = wl + q * 4 * T * MB;
+      float a[T], b[T][NT];
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        float b = tile[ko + poff[t]];
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[t], 0, 0, 0);
+      for (int s = 0; s < T; s++) {
+        a[s] = wq[(4 * s + lg) * MB];
+#pragma unroll
+        for (int t = 0; t < NT; t++) b[s][t] = tq[goff[s] + poff[t]];
       }
+#pragma unroll
+      for (int s = 0; s < T; s++)
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s][t], acc[t], 0, 0, 0);
     }
   }
-  (void)kk_total;
 
   // epilogue
   const int64_t yoh = p.oh * p.y_up, yow = p.ow * p.y_up;
@@ -172,19 +238,28 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
       xv = act_apply(xv, p.act);
       if (p.res) xv = xv + p.res[((bn * p.m + co) * p.oh + poy[t]) * p.ow + pox[t]];
       float* yb = p.y + ((bn * p.y_ctotal + p.y_coff + co) * yoh) * yow;
-      for (int dy = 0; dy < p.y_up; dy++)
-        for (int dx = 0; dx < p.y_up; dx++)
-          yb[(poy[t] * p.y_up + dy) * yow + pox[t] * p.y_up + dx] = xv;
+      store_replicated(yb, yow, poy[t], pox[t], (int)p.y_up, xv);
     }
   }
 }
 
+template <int T>
+static int launch_dense_t(const DenseConvK& p, bool wide_m, dim3 grid, hipStream_t s) {
+  if (wide_m)
+    hipLaunchKernelGGL((dense_conv_kernel<2, 2, T>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((dense_conv_kernel<1, 2, T>), grid, dim3(256), 0, s, p);
+  return launch_check("dense_conv_kernel");
+}
+
 int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
-  const int64_t kk = a.c * a.kh * a.kw;
+  const int64_t khkw = a.kh * a.kw;
+  if (khkw != 9 && khkw != 25 && khkw != 1 && khkw != 4)
+    return fail(QPH_EUNSUPPORTED, "dense conv: kernel sizes with kh*kw in {1, 4, 9, 25} only");
   const float* wk = a.wk;
   if (!wk) {
     if (!scratch_wk) return fail(QPH_EINVAL, "dense conv: no repacked weights");
-    QPH_TRY(launch_repack_conv_w(a.wt, a.m, kk, scratch_wk, s));
+    QPH_TRY(launch_repack_conv_w_taps(a.wt, a.m, a.c, khkw, scratch_wk, s));
     wk = scratch_wk;
   }
   DenseConvK p{};
@@ -195,6 +270,7 @@ int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
   p.y_ctotal = a.y_ctotal; p.y_coff = a.y_coff; p.y_up = a.y_up;
   p.act = a.act;
   const bool wide_m = a.m > 16;
+  const int mb = wide_m ? 32 : 16;
   // 2 MFMA tiles per wave; pixels per workgroup: 64 (WM=2) or 128 (WM=1)
   const int pix = wide_m ? 64 : 128;
   p.tw = a.ow >= 32 ? 32 : 16;
@@ -202,29 +278,30 @@ int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
   p.rt = (int)((p.th - 1) * a.sh + a.kh);
   p.ct = (int)((p.tw - 1) * a.sw + a.kw);
   const int plane = p.rt * p.ct;
-  // channel chunk: fits the halo budget, and each chunk's K is a multiple
-  // of 4 so that MFMA k-groups never straddle two fills
-  int khkw = (int)(a.kh * a.kw);
-  int cch = CONV_LDS_FLOATS / plane;
-  if (cch > CONV_KOFF_MAX / khkw) cch = CONV_KOFF_MAX / khkw;
-  if (cch >= a.c) {
-    cch = (int)a.c;
-  } else {
-    while (cch > 0 && (cch * khkw) % 4 != 0) cch--;
-  }
-  if (cch <= 0) return fail(QPH_EUNSUPPORTED, "dense conv: kernel too large for the LDS tile");
-  p.cchunk = cch;
+  if (p.ct > 128) return fail(QPH_EUNSUPPORTED, "dense conv: halo row wider than 128");
+  if (a.c * a.h * a.w * 4 >= (int64_t)0x80000000)
+    return fail(QPH_EUNSUPPORTED, "dense conv: input image larger than 2 GB");
+  // channel chunk (multiple of 4): halo + weight slice within the LDS budget
+  const int per4 = 4 * (plane + (int)khkw * mb);
+  int groups = (CONV_LDS_FLOATS - 64) / per4;
+  const int64_t cpad = (a.c + 3) / 4 * 4;
+  if (groups <= 0) return fail(QPH_EUNSUPPORTED, "dense conv: kernel too large for the LDS tile");
+  if ((int64_t)groups * 4 > cpad) groups = (int)(cpad / 4);
+  p.cchunk = 4 * groups;
+  p.kpad = kpad_of(a.c, khkw);
+  if (p.kpad * p.mpad * 4 >= (int64_t)0x80000000)
+    return fail(QPH_EUNSUPPORTED, "dense conv: weights larger than 2 GB");
   p.tiles_x = (int)ceil_div(a.ow, p.tw);
   const int tiles_y = (int)ceil_div(a.oh, p.th);
-  const int64_t mblk = wide_m ? 32 : 16;
-  dim3 grid((unsigned)(p.tiles_x * tiles_y), ceil_div(a.m, mblk), (unsigned)a.n);
+  dim3 grid((unsigned)(p.tiles_x * tiles_y), ceil_div(a.m, mb), (unsigned)a.n);
   if (a.n > 65535 || (int64_t)p.tiles_x * tiles_y > (1ll << 31))
     return fail(QPH_EUNSUPPORTED, "dense conv: grid too large");
-  if (wide_m)
-    hipLaunchKernelGGL((dense_conv_kernel<2, 2>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((dense_conv_kernel<1, 2>), grid, dim3(256), 0, s, p);
-  return launch_check("dense_conv_kernel");
+  switch (khkw) {
+    case 9: return launch_dense_t<9>(p, wide_m, grid, s);
+    case 25: return launch_dense_t<25>(p, wide_m, grid, s);
+    case 4: return launch_dense_t<4>(p, wide_m, grid, s);
+    default: return launch_dense_t<1>(p, wide_m, grid, s);
+  }
 }
 
 // --------------------------------------------------------------- depthwise
@@ -261,13 +338,35 @@ __global__ __launch_bounds__(256) void depthwise_kernel(DwK p) {
   const int64_t oy0 = (int64_t)tyb * p.th, ox0 = (int64_t)txb * p.tw;
   const int64_t iy0 = oy0 * p.sh - p.ph, ix0 = ox0 * p.sw - p.pw;
   const float* xp = p.x + plane_id * p.h * p.w_;
-  const int tot = p.rt * p.ct;
-  for (int idx = tid; idx < tot; idx += 256) {
-    int ry = idx / p.ct, rx = idx - ry * p.ct;
-    int64_t iy = iy0 + ry, ix = ix0 + rx;
-    float v = 0.0f;
-    if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w_) v = xp[iy * p.w_ + ix];
-    tile[idx] = v;
+  // halo fill: each wave takes whole rows (lanes along x, up to 192 wide),
+  // two rows' loads in flight before their stores
+  {
+    const int lane = tid & 63, wave = tid >> 6;
+    for (int r0 = wave * 2; r0 < p.rt; r0 += 8) {
+      float v[2][3];
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int ry = r0 + u;
+        const int64_t iy = iy0 + ry;
+        const bool rowok = ry < p.rt && iy >= 0 && iy < p.h;
+#pragma unroll
+        for (int hx = 0; hx < 3; hx++) {
+          const int rx = lane + 64 * hx;
+          const int64_t ix = ix0 + rx;
+          v[u][hx] = (rowok && rx < p.ct && ix >= 0 && ix < p.w_) ? xp[iy * p.w_ + ix] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int ry = r0 + u;
+        if (ry >= p.rt) break;
+#pragma unroll
+        for (int hx = 0; hx < 3; hx++) {
+          const int rx = lane + 64 * hx;
+          if (rx < p.ct) tile[ry * p.ct + rx] = v[u][hx];
+        }
+      }
+    }
   }
   float wr[KH * KW];
 #pragma unroll
@@ -319,6 +418,7 @@ int launch_depthwise(const ConvArgs& a, hipStream_t s) {
       return fail(QPH_EUNSUPPORTED, "depthwise: kernel too large for the LDS tile");
     }
   }
+  if (p.ct > 192) return fail(QPH_EUNSUPPORTED, "depthwise: halo row wider than 192");
   p.tiles_x = (int)ceil_div(a.ow, p.tw);
   const int64_t tiles = (int64_t)p.tiles_x * ceil_div(a.oh, p.th);
   const int64_t planes = a.n * a.c;
@@ -385,6 +485,15 @@ __global__ __launch_bounds__(256) void convt_pair_sigmoid_kernel(const float* __
                                                                  const float* __restrict__ w1,
                                                                  const float* __restrict__ w2,
                                                                  float* __restrict__ y) {
+  // weights staged once per workgroup; every lane reads the same LDS word
+  // (broadcast), four taps at a time
+  __shared__ f32x4 sw1[C * M1];
+  __shared__ f32x4 sw2[M1];
+  for (int i = threadIdx.x; i < C * M1; i += blockDim.x)
+    sw1[i] = f32x4{w1[4 * i], w1[4 * i + 1], w1[4 * i + 2], w1[4 * i + 3]};
+  for (int i = threadIdx.x; i < M1; i += blockDim.x)
+    sw2[i] = f32x4{w2[4 * i], w2[4 * i + 1], w2[4 * i + 2], w2[4 * i + 3]};
+  __syncthreads();
   const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t bn = blockIdx.y;
   if (pix >= h * w) return;
@@ -393,26 +502,40 @@ __global__ __launch_bounds__(256) void convt_pair_sigmoid_kernel(const float* __
   const float* xn = x + bn * C * h * w + pix;
 #pragma unroll
   for (int ci = 0; ci < C; ci++) xv[ci] = xn[ci * h * w];
+  // first ConvT: mid[co][q] = chain over ci of fma(x[ci], w1[ci][co][q], acc)
+  f32x4 mid[M1];
+#pragma unroll
+  for (int co = 0; co < M1; co++) {
+    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ci = 0; ci < C; ci++) {
+      const f32x4 wv = sw1[ci * M1 + co];
+      a[0] = __builtin_fmaf(xv[ci], wv[0], a[0]);
+      a[1] = __builtin_fmaf(xv[ci], wv[1], a[1]);
+      a[2] = __builtin_fmaf(xv[ci], wv[2], a[2]);
+      a[3] = __builtin_fmaf(xv[ci], wv[3], a[3]);
+    }
+    mid[co] = a;
+  }
+  // second ConvT on each of the four intermediate pixels, then Sigmoid
   const int64_t ow = 4 * w;
   float* yo = y + (bn * 4 * h + 4 * iy) * ow + 4 * ix;
 #pragma unroll
-  for (int q = 0; q < 4; q++) {  // (ky, kx) of the first ConvT
+  for (int q = 0; q < 4; q++) {
     const int ky = q >> 1, kx = q & 1;
-    float mid[M1];
+    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int co = 0; co < M1; co++) {
-      float a = 0.0f;
-#pragma unroll
-      for (int ci = 0; ci < C; ci++) a = __builtin_fmaf(xv[ci], w1[(ci * M1 + co) * 4 + q], a);
-      mid[co] = a;
+      const f32x4 wv = sw2[co];
+      a[0] = __builtin_fmaf(mid[co][q], wv[0], a[0]);
+      a[1] = __builtin_fmaf(mid[co][q], wv[1], a[1]);
+      a[2] = __builtin_fmaf(mid[co][q], wv[2], a[2]);
+      a[3] = __builtin_fmaf(mid[co][q], wv[3], a[3]);
     }
 #pragma unroll
     for (int q2 = 0; q2 < 4; q2++) {
-      float a = 0.0f;
-#pragma unroll
-      for (int co = 0; co < M1; co++) a = __builtin_fmaf(mid[co], w2[co * 4 + q2], a);
       const int oy = 2 * ky + (q2 >> 1), ox = 2 * kx + (q2 & 1);
-      yo[oy * ow + ox] = sigmoid1(a);
+      yo[oy * ow + ox] = sigmoid1(a[q2]);
     }
   }
 }

@@ -18,6 +18,7 @@
 namespace qph {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define GEMM_BK 16
 
@@ -175,6 +176,143 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
       }
 }
 
+// ------------------------------------------------------------ skinny tiles
+//
+// For GEMMs whose 128x128 tiling leaves most of the chip idle (the rec
+// linears, 1280 x {256..1024} x {256, 1024}; the pointwise convs): a
+// workgroup owns 32x32 outputs, each wave one 16x16 block accumulated with
+// v_mfma_f32_16x16x4f32 (4 k per instruction in order), so a K-deep chain
+// takes K/4 dependent MFMAs and the grid has M*N/256 waves.  K advances in
+// slabs of 64 through double-buffered LDS; A is staged row-major (stride
+// 66: a 16-row x 2-k read hits 32 distinct banks), B row-major (stride 48).
+
+#define SK_BK 64
+#define SK_PA (SK_BK + 2)
+#define SK_PB 48
+
+__device__ __forceinline__ void epilogue_store(const GemmArgs& g, float* C, const float* R,
+                                               int64_t i, int64_t j, float x) {
+  const int64_t M = g.m, N = g.n;
+  if (g.bias_mode == 1) {
+    if (!bias_seeded(g.seed_rule, i, j, M, N)) x = x + g.bias[i];
+  } else if (g.bias_mode == 2) {
+    x = x + g.bias[j];
+  }
+  x = act_apply(x, g.act);
+  if (R) {
+    float r;
+    if (g.res_up == 2) {
+      int64_t oy = j / g.up_w, ox = j - oy * g.up_w;
+      r = R[i * g.ldr + (oy >> 1) * g.up_cw + (ox >> 1)];
+    } else {
+      r = R[i * g.ldr + j];
+    }
+    x = x + r;
+  }
+  if (g.trans_out)
+    C[j * g.ldc + i] = x;
+  else
+    C[i * g.ldc + j] = x;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
+  __shared__ float sA[2][32 * SK_PA];
+  __shared__ float sB[2][SK_BK * SK_PB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lg = lane >> 4, l16 = lane & 15;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int64_t bz = blockIdx.z;
+  const int64_t i0 = (int64_t)blockIdx.y * 32;
+  const int64_t j0 = (int64_t)blockIdx.x * 32;
+  const float* A = g.a + bz * g.a_batch;
+  const float* B = g.b + bz * g.b_batch;
+  const int64_t M = g.m, N = g.n, K = g.k;
+
+  // staging: A slab 32 rows x 64 k (thread: row tid/8, k 8*(tid%8) .. +8),
+  // B slab 64 k x 32 cols (thread: k row tid/4, cols 8*(tid%4) .. +8)
+  const int ar = tid >> 3, ak = (tid & 7) * 8;
+  const int br = tid >> 2, bc = (tid & 3) * 8;
+  float ra[8], rb[8];
+  auto load = [&](int64_t k0) {
+    const int64_t ia = i0 + ar, ka = k0 + ak;
+    const int64_t kb = k0 + br, jb = j0 + bc;
+    if (VEC && ia < M && ka + 8 <= K) {
+      const float4* pa = (const float4*)(A + ia * g.lda + ka);
+      float4 v0 = pa[0], v1 = pa[1];
+      ra[0] = v0.x; ra[1] = v0.y; ra[2] = v0.z; ra[3] = v0.w;
+      ra[4] = v1.x; ra[5] = v1.y; ra[6] = v1.z; ra[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; u++) ra[u] = (ia < M && ka + u < K) ? A[ia * g.lda + ka + u] : 0.0f;
+    }
+    if (VEC && kb < K && jb + 8 <= N) {
+      const float4* pb = (const float4*)(B + kb * g.ldb + jb);
+      float4 v0 = pb[0], v1 = pb[1];
+      rb[0] = v0.x; rb[1] = v0.y; rb[2] = v0.z; rb[3] = v0.w;
+      rb[4] = v1.x; rb[5] = v1.y; rb[6] = v1.z; rb[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; u++) rb[u] = (kb < K && jb + u < N) ? B[kb * g.ldb + jb + u] : 0.0f;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) sA[buf][ar * SK_PA + ak + u] = ra[u];
+#pragma unroll
+    for (int u = 0; u < 8; u++) sB[buf][br * SK_PB + bc + u] = rb[u];
+  };
+
+  const int64_t ii = i0 + wm * 16;     // this wave's 16x16 block
+  const int64_t jj = j0 + wn * 16;
+  f32x4 acc;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    float s0 = 0.0f;
+    if (g.bias_mode == 1) {
+      int64_t i = ii + 4 * lg + v, j = jj + l16;
+      if (i < M && j < N && bias_seeded(g.seed_rule, i, j, M, N)) s0 = g.bias[i];
+    }
+    acc[v] = s0;
+  }
+
+  const int64_t nk = (K + SK_BK - 1) / SK_BK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int64_t t = 0; t < nk; t++) {
+    const int buf = (int)(t & 1);
+    if (t + 1 < nk) load((t + 1) * SK_BK);
+    const float* a_s = sA[buf] + (wm * 16 + l16) * SK_PA + lg;
+    const float* b_s = sB[buf] + lg * SK_PB + wn * 16 + l16;
+#pragma unroll
+    for (int kk = 0; kk < SK_BK; kk += 4)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a_s[kk], b_s[kk * SK_PB], acc, 0, 0, 0);
+    if (t + 1 < nk) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  float* C = g.c + bz * g.c_batch;
+  const float* R = g.res ? g.res + bz * g.r_batch : nullptr;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    int64_t i = ii + 4 * lg + v, j = jj + l16;
+    if (i < M && j < N) epilogue_store(g, C, R, i, j, acc[v]);
+  }
+}
+
+static int launch_skinny(const GemmArgs& g, hipStream_t s) {
+  dim3 grid(ceil_div(g.n, 32), ceil_div(g.m, 32), (unsigned)g.batch);
+  const bool vec = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (g.a_batch % 4 == 0) &&
+                   (g.b_batch % 4 == 0) && ((uintptr_t)g.a % 16 == 0) &&
+                   ((uintptr_t)g.b % 16 == 0);
+  if (vec)
+    hipLaunchKernelGGL(gemm_skinny_kernel<true>, grid, dim3(256), 0, s, g);
+  else
+    hipLaunchKernelGGL(gemm_skinny_kernel<false>, grid, dim3(256), 0, s, g);
+  return launch_check("gemm_skinny_kernel");
+}
+
 template <int MI, int NI>
 static int launch_cfg(const GemmArgs& g, hipStream_t s) {
   constexpr int BM = 64 * MI, BN = 64 * NI;
@@ -193,8 +331,7 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
     return (double)ceil_div(g.m, bm) * (double)ceil_div(g.n, bn) * (double)g.batch;
   };
   if (g.m >= 128 && g.n >= 128 && tiles(128, 128) >= 512) return launch_cfg<2, 2>(g, s);
-  if (g.n >= 128 && tiles(64, 128) >= 512) return launch_cfg<1, 2>(g, s);
-  return launch_cfg<1, 1>(g, s);
+  return launch_skinny(g, s);
 }
 
 }  // namespace qph

@@ -186,7 +186,10 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
 int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk);
 int launch_depthwise(const ConvArgs& a, hipStream_t s);
 int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw);
-int launch_repack_conv_w(const float* wt, int64_t m, int64_t kk, float* wk, hipStream_t s);
+// wk[Kpad][Mpad] k-major copy of an ONNX [M][cg][kh][kw] weight, Kpad =
+// ceil(cg/4)*4*khkw, Mpad = ceil(M/32)*32, zero-filled past the real extent.
+int launch_repack_conv_w_taps(const float* wt, int64_t m, int64_t cg, int64_t khkw, float* wk,
+                              hipStream_t s);
 
 int launch_convt2x2(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, const float* wt,
                     int64_t m, float* y, hipStream_t s);
@@ -201,6 +204,8 @@ int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, float
 int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, hipStream_t s);
 int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
                      float scale, float* out, hipStream_t s);
+int launch_attention_generic(const float* qkv, int64_t batch, int64_t t, int64_t heads,
+                             int64_t dh, float scale, float* out, hipStream_t s);
 int launch_elementwise_act(const float* x, float* y, int64_t n, const Act& a, hipStream_t s);
 int launch_resize_nearest(const float* x, int64_t nc, int64_t h, int64_t w, int64_t oh,
                           int64_t ow, float* y, hipStream_t s);

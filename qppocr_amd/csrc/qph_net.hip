@@ -297,13 +297,13 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
                          n.cp.sw == 1) &&
                        !(n.cp.group > 1 && n.ws[1] == 1);
     if (dense) {
-      int64_t kk = n.ws[1] * n.ws[2] * n.ws[3];
       float* d = nullptr;
       rc = hip_check(hipMalloc((void**)&d, (size_t)dense_conv_wk_floats(n.ws[0], n.ws[1], n.ws[2], n.ws[3]) * 4),
                      "hipMalloc(repacked weight)");
       if (rc) return bail(rc);
       net->wk[i] = d;
-      rc = launch_repack_conv_w(net->weights[n.w], n.ws[0], kk, d, ctx->stream);
+      rc = launch_repack_conv_w_taps(net->weights[n.w], n.ws[0], n.ws[1], n.ws[2] * n.ws[3], d,
+                                     ctx->stream);
       if (rc) return bail(rc);
     }
   }

@@ -65,11 +65,12 @@ int launch_layernorm(const float* x, const float* gamma, const float* beta, floa
 // partials (lane j takes e[j], e[j+8], ... in order) reduced as
 // ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)), then the cols%8 tail added in
 // order; rows narrower than 8 sum sequentially; y = e * (1/sum).
-// Workgroup per row.  The max is order-free; e is stored to the output, then
-// eight threads run the lane chains over LDS-staged chunks, so the
-// summation order is the reference's.
+// Workgroup per row.  The max is order-free (no NaN inputs).  The row is
+// walked in LDS chunks, double-buffered: waves 1-3 compute e for chunk c+1
+// (stored to LDS and to the output) while lanes 0-7 of wave 0 run the eight
+// lane chains over chunk c, so the summation order is the reference's.
 
-#define SM_CHUNK 4096  // floats per LDS chunk (16 KB)
+#define SM_CHUNK 4096  // floats per LDS chunk (16 KB), a multiple of 8
 
 __device__ __forceinline__ float block_max_256(float v, float* red) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
@@ -82,80 +83,122 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
   return r;
 }
 
-// Row sum in the reference order over e[0..cols) (global, already written).
-// Returns the sum in all threads.  lds: SM_CHUNK floats + 16.
-__device__ float ref_order_sum(const float* e, int64_t cols, float* lds) {
-  const int tid = threadIdx.x;
-  float* chunk = lds;
-  float* part = lds + SM_CHUNK;  // 8 lane partials + result
-  float lanesum = 0.0f;          // valid in threads 0..7
-  const int64_t full = cols >= 8 ? (cols / 8) * 8 : 0;
-  for (int64_t c0 = 0; c0 < full; c0 += SM_CHUNK) {
-    const int64_t n = (full - c0) < SM_CHUNK ? (full - c0) : SM_CHUNK;
-    __syncthreads();
-    for (int64_t i = tid; i < n; i += 256) chunk[i] = e[c0 + i];
-    __syncthreads();
-    if (tid < 8) {
-      float s = lanesum;
-      for (int64_t i = tid; i < n; i += 8) s = s + chunk[i];
-      lanesum = s;
+// probs may alias logits (in-place softmax).  pairs may be NULL.
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, int64_t cols,
+                                                           float* probs, float* pairs) {
+  __shared__ float buf[2][SM_CHUNK];
+  __shared__ float part[16];
+  __shared__ float red[8];
+  __shared__ int redi[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const float* xr = logits + row * cols;
+  float* pr = probs + row * cols;
+
+  // max over the row, eight loads in flight per thread
+  float mx = -__builtin_inff();
+  for (int64_t i0 = tid; i0 < cols; i0 += 256 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      int64_t i = i0 + 256 * u;
+      v[u] = i < cols ? xr[i] : -__builtin_inff();
     }
+#pragma unroll
+    for (int u = 0; u < 8; u++) mx = fmaxf(mx, v[u]);
   }
+  mx = block_max_256(mx, red);
+  __syncthreads();  // every read of the row precedes any in-place write
+
+  const int64_t full = cols >= 8 ? (cols / 8) * 8 : 0;
+  const int64_t nch = (cols + SM_CHUNK - 1) / SM_CHUNK;
+  // e for chunk c by waves 1-3 (192 threads)
+  auto compute = [&](int64_t c) {
+    const int64_t base = c * SM_CHUNK;
+    const int64_t n = (cols - base) < SM_CHUNK ? (cols - base) : SM_CHUNK;
+    float* bb = buf[c & 1];
+    for (int64_t j0 = tid - 64; j0 < n; j0 += 192 * 4) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        int64_t j = j0 + 192 * u;
+        v[u] = j < n ? xr[base + j] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        int64_t j = j0 + 192 * u;
+        if (j < n) {
+          float e = exp1(v[u] - mx);
+          bb[j] = e;
+          pr[base + j] = e;
+        }
+      }
+    }
+  };
+  if (wave != 0) compute(0);
   __syncthreads();
-  if (tid < 8) part[tid] = lanesum;
+  float lanesum = 0.0f;  // lanes 0..7 of wave 0
+  for (int64_t c = 0; c < nch; c++) {
+    if (wave == 0) {
+      if (lane < 8) {
+        const int64_t base = c * SM_CHUNK;
+        const int64_t n = full - base < SM_CHUNK ? full - base : SM_CHUNK;  // full part only
+        const float* bb = buf[c & 1];
+        float s = lanesum;
+        int64_t i = lane;
+        for (; i + 8 * 31 < n; i += 8 * 32) {
+          float v[32];
+#pragma unroll
+          for (int u = 0; u < 32; u++) v[u] = bb[i + 8 * u];
+#pragma unroll
+          for (int u = 0; u < 32; u++) s = s + v[u];
+        }
+        for (; i < n; i += 8) s = s + bb[i];
+        lanesum = s;
+      }
+    } else if (c + 1 < nch) {
+      compute(c + 1);
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && lane < 8) part[lane] = lanesum;
   __syncthreads();
   if (tid == 0) {
     float sum;
-    int64_t i;
     if (cols >= 8) {
       float t0 = part[0] + part[4], t1 = part[1] + part[5], t2 = part[2] + part[6],
             t3 = part[3] + part[7];
       sum = (t0 + t1) + (t2 + t3);
-      i = full;
     } else {
       sum = 0.0f;
-      i = 0;
     }
-    for (; i < cols; i++) sum = sum + e[i];
+    for (int64_t i = full; i < cols; i++) sum = sum + pr[i];   // tail, in order
     part[8] = sum;
   }
   __syncthreads();
-  return part[8];
-}
+  const float inv = 1.0f / part[8];
 
-// probs may alias logits (in-place softmax).  pairs may be NULL.
-__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, int64_t cols,
-                                                           float* probs, float* pairs) {
-  __shared__ float lds[SM_CHUNK + 16];
-  __shared__ float red[8];
-  __shared__ int redi[4];
-  const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const float* xr = logits + row * cols;
-  float* pr = probs + row * cols;
-  float mx = -__builtin_inff();
-  if (cols >= 8) {
-    for (int64_t i = tid; i < cols; i += 256) mx = fmaxf(mx, xr[i]);
-    mx = block_max_256(mx, red);
-  } else {
-    // rows narrower than 8: sequential max (activation.rs:362-371)
-    mx = xr[0];
-    for (int64_t i = 1; i < cols; i++)
-      if (xr[i] > mx) mx = xr[i];
-  }
-  __syncthreads();  // every read of the row precedes any in-place write
-  for (int64_t i = tid; i < cols; i += 256) pr[i] = exp1(xr[i] - mx);
-  __threadfence_block();
-  const float sum = ref_order_sum(pr, cols, lds);
-  const float inv = 1.0f / sum;
+  // normalise (+ argmax of the probabilities)
   float bv = -__builtin_inff();
   int bi = 0x7fffffff;
-  for (int64_t i = tid; i < cols; i += 256) {
-    float p = pr[i] * inv;
-    pr[i] = p;
-    if (p > bv) {  // ascending i per thread: keeps the first strict max
-      bv = p;
-      bi = (int)i;
+  for (int64_t i0 = tid; i0 < cols; i0 += 256 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      int64_t i = i0 + 256 * u;
+      v[u] = i < cols ? pr[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      int64_t i = i0 + 256 * u;
+      if (i < cols) {
+        float p = v[u] * inv;
+        pr[i] = p;
+        if (p > bv) {  // ascending i per thread: keeps the first strict max
+          bv = p;
+          bi = (int)i;
+        }
+      }
     }
   }
   if (!pairs) return;
@@ -168,7 +211,6 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, 
       bi = oi;
     }
   }
-  const int lane = tid & 63, wave = tid >> 6;
   __syncthreads();
   if (lane == 0) {
     red[wave] = bv;
@@ -364,8 +406,131 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   }
 }
 
+// Head dimension known at compile time: the block of RB query rows is
+// processed by all 256 threads at once.  Scores (RB x T): one chain of DH
+// fmas each; softmax: 16 threads per row (max, exp1 spread over the 16;
+// lanes 0-7 of the group run the eight reference lane chains, then the tree
+// and the tail); P.V (RB x DH): one chain of T fmas each.
+#define ATT_RB 16
+
+template <int DH>
+__global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restrict__ qkv,
+                                                           int64_t T, int64_t H, float scale,
+                                                           float* __restrict__ out) {
+  extern __shared__ float sm[];
+  constexpr int LD = DH + 1;
+  const int64_t b = blockIdx.x / H, h = blockIdx.x - b * H;
+  const int tid = threadIdx.x;
+  const int64_t D = H * DH;
+  const int t = (int)T;
+  const int ldp = t + 1;
+  float* sk = sm;                 // T x LD
+  float* sv = sk + t * LD;        // T x LD
+  float* sq = sv + t * LD;        // RB x LD (scaled q of the block)
+  float* sp = sq + ATT_RB * LD;   // RB x (T+1) scores / probabilities
+  float* ssum = sp + ATT_RB * ldp;  // RB x 16 (lane partials, inv)
+  const float* base = qkv + b * T * 3 * D + h * DH;
+  for (int i = tid; i < t * DH; i += 256) {
+    int r = i / DH, d = i - r * DH;
+    const float* row = base + (int64_t)r * 3 * D + d;
+    sk[r * LD + d] = row[D];
+    sv[r * LD + d] = row[2 * D];
+  }
+  const int g = tid >> 4, u = tid & 15;   // softmax: row g of the block, thread u of 16
+  for (int r0 = 0; r0 < t; r0 += ATT_RB) {
+    const int rb = (t - r0) < ATT_RB ? (t - r0) : ATT_RB;
+    for (int i = tid; i < rb * DH; i += 256) {
+      int r = i / DH, d = i - r * DH;
+      sq[r * LD + d] = base[(int64_t)(r0 + r) * 3 * D + d] * scale;   // Mul node
+    }
+    __syncthreads();
+    // scores S[r][j] = chain over d of fma(q[r][d], k[j][d], acc)
+    for (int i = tid; i < rb * t; i += 256) {
+      int r = i / t, j = i - r * t;
+      const float* qr = sq + r * LD;
+      const float* kj = sk + j * LD;
+      float acc = 0.0f;
+#pragma unroll
+      for (int d = 0; d < DH; d++) acc = __builtin_fmaf(qr[d], kj[d], acc);
+      sp[r * ldp + j] = acc;
+    }
+    __syncthreads();
+    // softmax of row g (reference order), 16 threads per row
+    float mx = -__builtin_inff();
+    const bool rowok = g < rb;
+    float* pr = sp + g * ldp;
+    if (rowok)
+      for (int j = u; j < t; j += 16) mx = fmaxf(mx, pr[j]);
+    for (int off = 8; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
+    if (t < 8 && rowok) {   // narrow rows: sequential max from the first element
+      mx = pr[0];
+      for (int j = 1; j < t; j++)
+        if (pr[j] > mx) mx = pr[j];
+    }
+    __syncthreads();
+    if (rowok)
+      for (int j = u; j < t; j += 16) pr[j] = exp1(pr[j] - mx);
+    __syncthreads();
+    const int full = t >= 8 ? (t / 8) * 8 : 0;
+    if (rowok && u < 8) {
+      float s = 0.0f;
+      for (int j = u; j < full; j += 8) s = s + pr[j];
+      ssum[g * 16 + u] = s;
+    }
+    __syncthreads();
+    if (rowok && u == 0) {
+      const float* l = ssum + g * 16;
+      float sum;
+      if (t >= 8) {
+        float t0 = l[0] + l[4], t1 = l[1] + l[5], t2 = l[2] + l[6], t3 = l[3] + l[7];
+        sum = (t0 + t1) + (t2 + t3);
+      } else {
+        sum = 0.0f;
+      }
+      for (int j = full; j < t; j++) sum = sum + pr[j];
+      ssum[g * 16 + 8] = 1.0f / sum;
+    }
+    __syncthreads();
+    if (rowok) {
+      const float inv = ssum[g * 16 + 8];
+      for (int j = u; j < t; j += 16) pr[j] = pr[j] * inv;
+    }
+    __syncthreads();
+    // O[r][d] = chain over j of fma(P[r][j], v[j][d], acc)
+    for (int i = tid; i < rb * DH; i += 256) {
+      int r = i / DH, d = i - r * DH;
+      const float* p = sp + r * ldp;
+      float acc = 0.0f;
+      for (int j = 0; j < t; j++) acc = __builtin_fmaf(p[j], sv[j * LD + d], acc);
+      out[(b * T + r0 + r) * D + h * DH + d] = acc;
+    }
+    __syncthreads();
+  }
+}
+
+static size_t attention_dh_lds(int64_t t, int64_t dh) {
+  return (size_t)(2 * t * (dh + 1) + ATT_RB * (dh + 1) + ATT_RB * (t + 1) + ATT_RB * 16) *
+         sizeof(float);
+}
+
 int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
                      float scale, float* out, hipStream_t s) {
+  if ((dh == 32 || dh == 64) && attention_dh_lds(t, dh) <= 64 * 1024) {
+    if (batch * heads > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "attention: grid too large");
+    size_t lds = attention_dh_lds(t, dh);
+    if (dh == 32)
+      hipLaunchKernelGGL(attention_dh_kernel<32>, dim3((unsigned)(batch * heads)), dim3(256), lds,
+                         s, qkv, t, heads, scale, out);
+    else
+      hipLaunchKernelGGL(attention_dh_kernel<64>, dim3((unsigned)(batch * heads)), dim3(256), lds,
+                         s, qkv, t, heads, scale, out);
+    return launch_check("attention_dh_kernel");
+  }
+  return launch_attention_generic(qkv, batch, t, heads, dh, scale, out, s);
+}
+
+int launch_attention_generic(const float* qkv, int64_t batch, int64_t t, int64_t heads,
+                             int64_t dh, float scale, float* out, hipStream_t s) {
   size_t lds = (size_t)(2 * t * (dh + 1) + 4 * (t + dh)) * sizeof(float);
   if (lds > 64 * 1024) return fail(QPH_EUNSUPPORTED, "attention: T*dh too large for LDS");
   if (batch * heads > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "attention: grid too large");
