@@ -40,6 +40,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-steps", type=int, default=6, help="CPU baseline sample (steps)")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (a kernel of "
+                         "known traffic for scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the det/rec path "
@@ -58,6 +61,13 @@ def main():
     lib = ops._lib.load()
     stream_ptr = lib.qph_ctx_stream(ctx)
     stream = torch.cuda.ExternalStream(stream_ptr)
+    if args.copy_calibration_mb > 0:
+        n = args.copy_calibration_mb * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     det_g, det_x = nets.build_det(2, 640, 640)
     rec_g, rec_x = nets.build_rec(3, REC_BATCH, 320)

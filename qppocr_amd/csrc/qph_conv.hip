@@ -220,27 +220,44 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
     }
   }
 
-  // epilogue
+  // epilogue: operands (bias, residual) first, then finish and store (the
+  // stores may alias the operands as far as the compiler knows)
   const int64_t yoh = p.oh * p.y_up, yow = p.ow * p.y_up;
+  float badd[NT][4], rv[NT][4];
+  bool hadd[NT][4], ok[NT][4];
 #pragma unroll
-  for (int t = 0; t < NT; t++) {
-    if (!pval[t]) continue;
+  for (int t = 0; t < NT; t++)
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      int64_t co = m0 + 4 * lg + v;
-      if (co >= p.m) continue;
-      float xv = acc[t][v];
+      const int64_t co = m0 + 4 * lg + v;
+      ok[t][v] = pval[t] && co < p.m;
+      hadd[t][v] = false;
+      badd[t][v] = 0.0f;
+      rv[t][v] = 0.0f;
+      if (!ok[t][v]) continue;
       if (p.bias) {
         int64_t n0 = (pox[t] >> 5) << 5;
         bool seeded = (p.ow - n0) < 32 && co >= p.m - p.m % 4;
-        if (!seeded) xv = xv + p.bias[co];
+        if (!seeded) {
+          badd[t][v] = p.bias[co];
+          hadd[t][v] = true;
+        }
       }
+      if (p.res) rv[t][v] = p.res[((bn * p.m + co) * p.oh + poy[t]) * p.ow + pox[t]];
+    }
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      if (!ok[t][v]) continue;
+      const int64_t co = m0 + 4 * lg + v;
+      float xv = acc[t][v];
+      if (hadd[t][v]) xv = xv + badd[t][v];
       xv = act_apply(xv, p.act);
-      if (p.res) xv = xv + p.res[((bn * p.m + co) * p.oh + poy[t]) * p.ow + pox[t]];
+      if (p.res) xv = xv + rv[t][v];
       float* yb = p.y + ((bn * p.y_ctotal + p.y_coff + co) * yoh) * yow;
       store_replicated(yb, yow, poy[t], pox[t], (int)p.y_up, xv);
     }
-  }
 }
 
 template <int T>

@@ -31,6 +31,52 @@ __device__ __forceinline__ bool bias_seeded(int rule, int64_t i, int64_t j, int6
   return (n - n0) < 32 && i >= m - m % 4;
 }
 
+// Epilogue in two phases: every operand the outputs need (bias, residual)
+// is loaded first, then the values are finished and stored.  The stores to C
+// may alias those operands as far as the compiler knows, so interleaving
+// them would serialise one load round trip per output.
+struct EpiIn {
+  float add;   // bias term (added when has_add)
+  float res;   // residual term
+  bool has_add, ok;
+};
+
+__device__ __forceinline__ EpiIn epilogue_gather(const GemmArgs& g, const float* R, int64_t i,
+                                                 int64_t j) {
+  EpiIn e{0.0f, 0.0f, false, i < g.m && j < g.n};
+  if (!e.ok) return e;
+  if (g.bias_mode == 1) {
+    if (!bias_seeded(g.seed_rule, i, j, g.m, g.n)) {
+      e.add = g.bias[i];
+      e.has_add = true;
+    }
+  } else if (g.bias_mode == 2) {
+    e.add = g.bias[j];
+    e.has_add = true;
+  }
+  if (R) {
+    if (g.res_up == 2) {
+      int64_t oy = j / g.up_w, ox = j - oy * g.up_w;
+      e.res = R[i * g.ldr + (oy >> 1) * g.up_cw + (ox >> 1)];
+    } else {
+      e.res = R[i * g.ldr + j];
+    }
+  }
+  return e;
+}
+
+__device__ __forceinline__ void epilogue_put(const GemmArgs& g, float* C, bool has_res,
+                                             const EpiIn& e, int64_t i, int64_t j, float x) {
+  if (!e.ok) return;
+  if (e.has_add) x = x + e.add;
+  x = act_apply(x, g.act);
+  if (has_res) x = x + e.res;
+  if (g.trans_out)
+    C[j * g.ldc + i] = x;
+  else
+    C[i * g.ldc + j] = x;
+}
+
 template <int MI, int NI>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
   constexpr int BM = 64 * MI, BN = 64 * NI;
@@ -144,36 +190,17 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
   for (int mi = 0; mi < MI; mi++)
 #pragma unroll
-    for (int ni = 0; ni < NI; ni++)
+    for (int ni = 0; ni < NI; ni++) {
+      EpiIn e[16];
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        int64_t i = i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-        int64_t j = j0 + wn0 + ni * 32 + lr;
-        if (i >= M || j >= N) continue;
-        float x = acc[mi][ni][v];
-        if (g.bias_mode == 1) {
-          if (!bias_seeded(g.seed_rule, i, j, M, N)) x = x + g.bias[i];
-        } else if (g.bias_mode == 2) {
-          x = x + g.bias[j];
-        }
-        x = act_apply(x, g.act);
-        if (R) {
-          float r;
-          if (g.res_up == 2) {
-            // nearest 2x upsample of a coarse map: row stride ldr (channel
-            // plane), coarse width up_cw, output width up_w.
-            int64_t oy = j / g.up_w, ox = j - oy * g.up_w;
-            r = R[i * g.ldr + (oy >> 1) * g.up_cw + (ox >> 1)];
-          } else {
-            r = R[i * g.ldr + j];
-          }
-          x = x + r;
-        }
-        if (g.trans_out)
-          C[j * g.ldc + i] = x;
-        else
-          C[i * g.ldc + j] = x;
-      }
+      for (int v = 0; v < 16; v++)
+        e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                               j0 + wn0 + ni * 32 + lr);
+#pragma unroll
+      for (int v = 0; v < 16; v++)
+        epilogue_put(g, C, R != nullptr, e[v], i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                     j0 + wn0 + ni * 32 + lr, acc[mi][ni][v]);
+    }
 }
 
 // ------------------------------------------------------------ skinny tiles
@@ -189,31 +216,6 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 #define SK_BK 64
 #define SK_PA (SK_BK + 2)
 #define SK_PB 48
-
-__device__ __forceinline__ void epilogue_store(const GemmArgs& g, float* C, const float* R,
-                                               int64_t i, int64_t j, float x) {
-  const int64_t M = g.m, N = g.n;
-  if (g.bias_mode == 1) {
-    if (!bias_seeded(g.seed_rule, i, j, M, N)) x = x + g.bias[i];
-  } else if (g.bias_mode == 2) {
-    x = x + g.bias[j];
-  }
-  x = act_apply(x, g.act);
-  if (R) {
-    float r;
-    if (g.res_up == 2) {
-      int64_t oy = j / g.up_w, ox = j - oy * g.up_w;
-      r = R[i * g.ldr + (oy >> 1) * g.up_cw + (ox >> 1)];
-    } else {
-      r = R[i * g.ldr + j];
-    }
-    x = x + r;
-  }
-  if (g.trans_out)
-    C[j * g.ldc + i] = x;
-  else
-    C[i * g.ldc + j] = x;
-}
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
@@ -294,11 +296,11 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
 
   float* C = g.c + bz * g.c_batch;
   const float* R = g.res ? g.res + bz * g.r_batch : nullptr;
+  EpiIn e[4];
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    int64_t i = ii + 4 * lg + v, j = jj + l16;
-    if (i < M && j < N) epilogue_store(g, C, R, i, j, acc[v]);
-  }
+  for (int v = 0; v < 4; v++) e[v] = epilogue_gather(g, R, ii + 4 * lg + v, jj + l16);
+#pragma unroll
+  for (int v = 0; v < 4; v++) epilogue_put(g, C, R != nullptr, e[v], ii + 4 * lg + v, jj + l16, acc[v]);
 }
 
 static int launch_skinny(const GemmArgs& g, hipStream_t s) {
@@ -321,6 +323,159 @@ static int launch_cfg(const GemmArgs& g, hipStream_t s) {
   return launch_check("gemm_mfma_kernel");
 }
 
+// ------------------------------------------------------------- wide tiles
+//
+// The large GEMMs (the rec head, 1280 x 18709 x 256): 128x128 tiles, 4 waves
+// of 64x64 (2x2 v_mfma_f32_32x32x2f32 accumulators each), K slabs of 32
+// through double-buffered LDS with 16-byte global loads (needs lda, ldb
+// multiples of 4 and 16-byte aligned bases: the session pads the head
+// weight rows).  Tile order is XCD-aware: workgroup b runs on XCD b % 8
+// (round-robin dispatch), and each XCD gets a contiguous range of tiles in
+// column-block-major order, so one B column block stays in that XCD's L2
+// while all row blocks pass over it, and A (small) is read once per XCD.
+
+#define WB_BK 32
+#define WB_PA (128 + 1)
+#define WB_PB (128 + 4)
+#define NUM_XCD 8
+
+__global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int nb,
+                                                        int tiles_per_xcd) {
+  __shared__ float sA[2][WB_BK * WB_PA];
+  __shared__ __attribute__((aligned(16))) float sB[2][WB_BK * WB_PB];
+  const int b = blockIdx.x;
+  const int tile = (b % NUM_XCD) * tiles_per_xcd + b / NUM_XCD;
+  if (tile >= mb * nb) return;
+  const int nblk = tile / mb, mblk = tile - nblk * mb;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave & 1) * 64, wn0 = (wave >> 1) * 64;
+  const int64_t i0 = (int64_t)mblk * 128, j0 = (int64_t)nblk * 128;
+  const int64_t bz = blockIdx.z;
+  const float* A = g.a + bz * g.a_batch;
+  const float* B = g.b + bz * g.b_batch;
+  const int64_t M = g.m, N = g.n, K = g.k;
+
+  // A slab 128 x 32: thread -> rows t/8 + 32 r, k 4*(t%8); B slab 32 x 128:
+  // thread -> k rows t/32 + 8 r, columns 4*(t%32)
+  const int ar = tid >> 3, ak = (tid & 7) * 4;
+  const int br = tid >> 5, bc = (tid & 31) * 4;
+  float4 ra[4], rb[4];
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t i = i0 + ar + 32 * r, k = k0 + ak;
+      if (i < M && k + 4 <= K) {
+        ra[r] = *(const float4*)(A + i * g.lda + k);
+      } else {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = (i < M && k + u < K) ? A[i * g.lda + k + u] : 0.0f;
+        ra[r] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t k = k0 + br + 8 * r, j = j0 + bc;
+      if (k < K && j + 4 <= N) {
+        rb[r] = *(const float4*)(B + k * g.ldb + j);
+      } else {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = (k < K && j + u < N) ? B[k * g.ldb + j + u] : 0.0f;
+        rb[r] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float* d = sA[buf] + ak * WB_PA + ar + 32 * r;   // transposed: [k][m]
+      d[0] = ra[r].x;
+      d[WB_PA] = ra[r].y;
+      d[2 * WB_PA] = ra[r].z;
+      d[3 * WB_PA] = ra[r].w;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) *(float4*)(sB[buf] + (br + 8 * r) * WB_PB + bc) = rb[r];
+  };
+
+  const int lr = lane & 31, lh = lane >> 5;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        float s0 = 0.0f;
+        if (g.bias_mode == 1) {
+          int64_t i = i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          int64_t j = j0 + wn0 + ni * 32 + lr;
+          if (i < M && j < N && bias_seeded(g.seed_rule, i, j, M, N)) s0 = g.bias[i];
+        }
+        acc[mi][ni][v] = s0;
+      }
+
+  const int64_t nk = (K + WB_BK - 1) / WB_BK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int64_t t = 0; t < nk; t++) {
+    const int buf = (int)(t & 1);
+    if (t + 1 < nk) load((t + 1) * WB_BK);
+    const float* a_s = sA[buf] + lh * WB_PA + wm0 + lr;
+    const float* b_s = sB[buf] + lh * WB_PB + wn0 + lr;
+    // operands of k-step kk+2 are read before the MFMAs of k-step kk issue
+    float op[2][4];
+    op[0][0] = a_s[0];
+    op[0][1] = a_s[32];
+    op[0][2] = b_s[0];
+    op[0][3] = b_s[32];
+#pragma unroll
+    for (int kk = 0; kk < WB_BK; kk += 2) {
+      const int cur = (kk >> 1) & 1, nxt = cur ^ 1;
+      if (kk + 2 < WB_BK) {
+        op[nxt][0] = a_s[(kk + 2) * WB_PA];
+        op[nxt][1] = a_s[(kk + 2) * WB_PA + 32];
+        op[nxt][2] = b_s[(kk + 2) * WB_PB];
+        op[nxt][3] = b_s[(kk + 2) * WB_PB + 32];
+      }
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][0], op[cur][2], acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][0], op[cur][3], acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][1], op[cur][2], acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][1], op[cur][3], acc[1][1], 0, 0, 0);
+    }
+    if (t + 1 < nk) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  float* C = g.c + bz * g.c_batch;
+  const float* R = g.res ? g.res + bz * g.r_batch : nullptr;
+#pragma unroll
+  for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+      EpiIn e[16];
+#pragma unroll
+      for (int v = 0; v < 16; v++)
+        e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                               j0 + wn0 + ni * 32 + lr);
+#pragma unroll
+      for (int v = 0; v < 16; v++)
+        epilogue_put(g, C, R != nullptr, e[v], i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                     j0 + wn0 + ni * 32 + lr, acc[mi][ni][v]);
+    }
+}
+
+static int launch_wide(const GemmArgs& g, hipStream_t s) {
+  const int mb = (int)ceil_div(g.m, 128), nb = (int)ceil_div(g.n, 128);
+  const int tiles = mb * nb;
+  const int per = (tiles + NUM_XCD - 1) / NUM_XCD;
+  dim3 grid((unsigned)(per * NUM_XCD), 1, (unsigned)g.batch);
+  hipLaunchKernelGGL(gemm_wide_kernel, grid, dim3(256), 0, s, g, mb, nb, per);
+  return launch_check("gemm_wide_kernel");
+}
+
 int launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (g.m <= 0 || g.n <= 0 || g.k <= 0 || g.batch <= 0) return QPH_OK;
   if (g.m > (1ll << 31) || g.n > (1ll << 31) || g.batch > 65535)
@@ -330,7 +485,13 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
   auto tiles = [&](int bm, int bn) {
     return (double)ceil_div(g.m, bm) * (double)ceil_div(g.n, bn) * (double)g.batch;
   };
-  if (g.m >= 128 && g.n >= 128 && tiles(128, 128) >= 512) return launch_cfg<2, 2>(g, s);
+  if (g.m >= 128 && g.n >= 128 && tiles(128, 128) >= 512) {
+    const bool vec = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (g.a_batch % 4 == 0) &&
+                     (g.b_batch % 4 == 0) && ((uintptr_t)g.a % 16 == 0) &&
+                     ((uintptr_t)g.b % 16 == 0);
+    if (vec && tiles(128, 128) < (1u << 30)) return launch_wide(g, s);
+    return launch_cfg<2, 2>(g, s);
+  }
   return launch_skinny(g, s);
 }
 

@@ -79,7 +79,10 @@ static int run_node(qph_net* net, size_t i) {
       const int64_t k = n.ws[0], nn = n.ws[1];
       const int64_t rows = numel_of(net, n.in) / k;
       GemmArgs g{};
-      g.a = x; g.lda = k; g.b = w; g.ldb = nn; g.c = y; g.ldc = nn;
+      // weights resident with rows padded to a multiple of 4 floats
+      g.a = x; g.lda = k; g.b = net->wk[i] ? net->wk[i] : w; g.ldb = (nn + 3) / 4 * 4;
+      if (!net->wk[i]) g.ldb = nn;
+      g.c = y; g.ldc = nn;
       g.m = rows; g.n = nn; g.k = k; g.batch = 1;
       g.bias = bias; g.bias_mode = bias ? 2 : 0;
       g.act = make_act(&n.act);
@@ -304,6 +307,22 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
       net->wk[i] = d;
       rc = launch_repack_conv_w_taps(net->weights[n.w], n.ws[0], n.ws[1], n.ws[2] * n.ws[3], d,
                                      ctx->stream);
+      if (rc) return bail(rc);
+    }
+    if (n.op == QPH_OP_LINEAR && n.ws[1] % 4 != 0) {
+      // [K][N] -> [K][N4] with zero columns past N (16-byte aligned rows)
+      const int64_t k = n.ws[0], nn = n.ws[1], n4 = (nn + 3) / 4 * 4;
+      float* d = nullptr;
+      rc = hip_check(hipMalloc((void**)&d, (size_t)(k * n4) * 4), "hipMalloc(padded weight)");
+      if (rc) return bail(rc);
+      net->wk[i] = d;
+      rc = hip_check(hipMemset2DAsync(d, (size_t)n4 * 4, 0, (size_t)n4 * 4, (size_t)k, ctx->stream),
+                     "hipMemset2DAsync");
+      if (rc == QPH_OK)
+        rc = hip_check(hipMemcpy2DAsync(d, (size_t)n4 * 4, net->weights[n.w], (size_t)nn * 4,
+                                        (size_t)nn * 4, (size_t)k, hipMemcpyDeviceToDevice,
+                                        ctx->stream),
+                       "hipMemcpy2DAsync");
       if (rc) return bail(rc);
     }
   }

@@ -20,6 +20,8 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 //   y = ((d / sd) * gamma) + beta.
 // One wave per row; the f64 sums are exact for rows whose values span less
 // than 2^45 in magnitude ratio, which makes them independent of the order.
+// The row (cols <= 64*V) stays in registers across the three passes.
+template <int V>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x,
                                                         const float* __restrict__ gamma,
                                                         const float* __restrict__ beta, float eps,
@@ -30,31 +32,53 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
   if (row >= rows) return;
   const float* xr = x + row * cols;
   float* yr = y + row * cols;
+  float xv[V], gv[V], bv[V];
+#pragma unroll
+  for (int u = 0; u < V; u++) {
+    const int64_t j = lane + 64 * u;
+    const bool in = j < cols;
+    xv[u] = in ? xr[j] : 0.0f;
+    gv[u] = in ? gamma[j] : 0.0f;
+    bv[u] = in ? beta[j] : 0.0f;
+  }
   double s = 0.0;
-  for (int64_t j = lane; j < cols; j += 64) s += (double)xr[j];
+#pragma unroll
+  for (int u = 0; u < V; u++)
+    if (lane + 64 * u < cols) s += (double)xv[u];
   s = wave_sum_f64(s);
   const float mu = (float)(s / (double)cols);
   double s2 = 0.0;
-  for (int64_t j = lane; j < cols; j += 64) {
-    float d = xr[j] - mu;
-    float sq = d * d;
-    s2 += (double)sq;
-  }
+#pragma unroll
+  for (int u = 0; u < V; u++)
+    if (lane + 64 * u < cols) {
+      float d = xv[u] - mu;
+      float sq = d * d;
+      s2 += (double)sq;
+    }
   s2 = wave_sum_f64(s2);
   const float var = (float)(s2 / (double)cols);
   const float sd = __builtin_sqrtf(var + eps);
-  for (int64_t j = lane; j < cols; j += 64) {
-    float d = xr[j] - mu;
-    float v = d / sd;
-    v = v * gamma[j];
-    yr[j] = v + beta[j];
+#pragma unroll
+  for (int u = 0; u < V; u++) {
+    const int64_t j = lane + 64 * u;
+    if (j < cols) {
+      float d = xv[u] - mu;
+      float v = d / sd;
+      v = v * gv[u];
+      yr[j] = v + bv[u];
+    }
   }
 }
 
 int launch_layernorm(const float* x, const float* gamma, const float* beta, float eps,
                      int64_t rows, int64_t cols, float* y, hipStream_t s) {
-  hipLaunchKernelGGL(layernorm_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, x, gamma, beta,
-                     eps, rows, cols, y);
+  dim3 grid(ceil_div(rows, 4));
+  if (cols <= 256)
+    hipLaunchKernelGGL(layernorm_kernel<4>, grid, dim3(256), 0, s, x, gamma, beta, eps, rows, cols, y);
+  else if (cols <= 1024)
+    hipLaunchKernelGGL(layernorm_kernel<16>, grid, dim3(256), 0, s, x, gamma, beta, eps, rows, cols, y);
+  else
+    hipLaunchKernelGGL(layernorm_kernel<64>, grid, dim3(256), 0, s, x, gamma, beta, eps, rows, cols, y);
   return launch_check("layernorm_kernel");
 }
 
