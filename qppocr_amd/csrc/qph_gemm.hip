@@ -326,153 +326,251 @@ static int launch_cfg(const GemmArgs& g, hipStream_t s) {
 // ------------------------------------------------------------- wide tiles
 //
 // The large GEMMs (the rec head, 1280 x 18709 x 256): 128x128 tiles, 4 waves
-// of 64x64 (2x2 v_mfma_f32_32x32x2f32 accumulators each), K slabs of 32
-// through double-buffered LDS with 16-byte global loads (needs lda, ldb
-// multiples of 4 and 16-byte aligned bases: the session pads the head
-// weight rows).  Tile order is XCD-aware: workgroup b runs on XCD b % 8
-// (round-robin dispatch), and each XCD gets a contiguous range of tiles in
-// column-block-major order, so one B column block stays in that XCD's L2
-// while all row blocks pass over it, and A (small) is read once per XCD.
+// of 64x64 (2x2 v_mfma_f32_32x32x2f32 accumulators each), K slabs of 16
+// (K must be a multiple of 16).
+//
+// Slabs go from global memory straight into LDS (buffer loads with the LDS
+// bit, one word per lane, no staging registers), double-buffered, the next
+// slab in flight while the current one is multiplied.  Every LDS position is
+// one lane of one load, so the layout is whatever the per-lane offsets say:
+//   A slab: [m][h][s], row pitch 20 words (16 + 4 pad), element k = 2s + h.
+//     A lane of the MFMA needs A[m][2s + h] for s = 0..7 (h = lane / 32), so
+//     one ds_read_b128 brings four k-steps; 20-word rows keep the eight
+//     lanes of one b128 read on distinct banks.
+//   B slab: rows r = 8h + s hold B[k0 + 2s + h][j0 .. j0 + 127].
+// The buffer resources start at the tile's (row, k0) and (k0, column)
+// corner, so the per-lane offsets are the same for every slab and tile.
+// Range checks give the edges: A rows past M and B rows past K lie beyond
+// the range and read 0; B columns past N read the next row's words, which
+// only reach output columns past N (never stored).
+//
+// Persistent: each workgroup walks its tiles; workgroup b runs on XCD b % 8
+// (round-robin dispatch) and every XCD owns a contiguous range of tiles in
+// column-block-major order, so a B column block stays in that XCD's L2
+// while the row blocks pass over it.  The first slab of a workgroup's next
+// tile is loaded while the current tile's epilogue runs.
 
-#define WB_BK 32
-#define WB_PA (128 + 1)
-#define WB_PB (128 + 4)
+#define WB_BK 16
+#define WB_PA 20
+#define WB_A (128 * WB_PA)
+#define WB_B (WB_BK * 128)
+#define WB_STAGE (WB_A + WB_B)
+#define WB_AL 10   // A-slab loads per wave (128 * 20 words / 64 lanes / 4 waves)
+#define WB_BL 8    // B-slab loads per wave
 #define NUM_XCD 8
 
+// PLAIN: column bias or none, no activation, residual or transposed store
+// (the rec head); accumulators then start at 0 and the epilogue is one add
+// and a store, which keeps the register budget small.
+template <bool PLAIN>
 __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int nb,
-                                                        int tiles_per_xcd) {
-  __shared__ float sA[2][WB_BK * WB_PA];
-  __shared__ __attribute__((aligned(16))) float sB[2][WB_BK * WB_PB];
-  const int b = blockIdx.x;
-  const int tile = (b % NUM_XCD) * tiles_per_xcd + b / NUM_XCD;
-  if (tile >= mb * nb) return;
-  const int nblk = tile / mb, mblk = tile - nblk * mb;
+                                                        int ntiles, int per_xcd, int wg_xcd) {
+  __shared__ __attribute__((aligned(16))) float lds[2 * WB_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm0 = (wave & 1) * 64, wn0 = (wave >> 1) * 64;
-  const int64_t i0 = (int64_t)mblk * 128, j0 = (int64_t)nblk * 128;
-  const int64_t bz = blockIdx.z;
-  const float* A = g.a + bz * g.a_batch;
-  const float* B = g.b + bz * g.b_batch;
-  const int64_t M = g.m, N = g.n, K = g.k;
-
-  // A slab 128 x 32: thread -> rows t/8 + 32 r, k 4*(t%8); B slab 32 x 128:
-  // thread -> k rows t/32 + 8 r, columns 4*(t%32)
-  const int ar = tid >> 3, ak = (tid & 7) * 4;
-  const int br = tid >> 5, bc = (tid & 31) * 4;
-  float4 ra[4], rb[4];
-  auto load = [&](int64_t k0) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int64_t i = i0 + ar + 32 * r, k = k0 + ak;
-      if (i < M && k + 4 <= K) {
-        ra[r] = *(const float4*)(A + i * g.lda + k);
-      } else {
-        float v[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = (i < M && k + u < K) ? A[i * g.lda + k + u] : 0.0f;
-        ra[r] = make_float4(v[0], v[1], v[2], v[3]);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int64_t k = k0 + br + 8 * r, j = j0 + bc;
-      if (k < K && j + 4 <= N) {
-        rb[r] = *(const float4*)(B + k * g.ldb + j);
-      } else {
-        float v[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = (k < K && j + u < N) ? B[k * g.ldb + j + u] : 0.0f;
-        rb[r] = make_float4(v[0], v[1], v[2], v[3]);
-      }
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      float* d = sA[buf] + ak * WB_PA + ar + 32 * r;   // transposed: [k][m]
-      d[0] = ra[r].x;
-      d[WB_PA] = ra[r].y;
-      d[2 * WB_PA] = ra[r].z;
-      d[3 * WB_PA] = ra[r].w;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) *(float4*)(sB[buf] + (br + 8 * r) * WB_PB + bc) = rb[r];
-  };
+  const int xcd = (int)(blockIdx.x % NUM_XCD), wl = (int)(blockIdx.x / NUM_XCD);
+  const int t_end = min(xcd * per_xcd + per_xcd, ntiles);
+  int tile = xcd * per_xcd + wl;
+  if (tile >= t_end) return;
 
   const int lr = lane & 31, lh = lane >> 5;
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-    for (int ni = 0; ni < 2; ni++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        float s0 = 0.0f;
-        if (g.bias_mode == 1) {
-          int64_t i = i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-          int64_t j = j0 + wn0 + ni * 32 + lr;
-          if (i < M && j < N && bias_seeded(g.seed_rule, i, j, M, N)) s0 = g.bias[i];
-        }
-        acc[mi][ni][v] = s0;
-      }
+  const int wm0 = (wave & 1) * 64, wn0 = (wave >> 1) * 64;
+  // all word offsets below fit 31 bits (checked by the launcher)
+  const int M = (int)g.m, N = (int)g.n, K = (int)g.k;
+  const int lda = (int)g.lda, ldb = (int)g.ldb;
+  const int nk = K / WB_BK;
+  const int a_words = (M - 1) * lda + K, b_words = (K - 1) * ldb + N;
 
-  const int64_t nk = (K + WB_BK - 1) / WB_BK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int64_t t = 0; t < nk; t++) {
-    const int buf = (int)(t & 1);
-    if (t + 1 < nk) load((t + 1) * WB_BK);
-    const float* a_s = sA[buf] + lh * WB_PA + wm0 + lr;
-    const float* b_s = sB[buf] + lh * WB_PB + wn0 + lr;
-    // operands of k-step kk+2 are read before the MFMAs of k-step kk issue
-    float op[2][4];
-    op[0][0] = a_s[0];
-    op[0][1] = a_s[32];
-    op[0][2] = b_s[0];
-    op[0][3] = b_s[32];
+  unsigned aoff[WB_AL], boff[WB_BL];
 #pragma unroll
-    for (int kk = 0; kk < WB_BK; kk += 2) {
-      const int cur = (kk >> 1) & 1, nxt = cur ^ 1;
-      if (kk + 2 < WB_BK) {
-        op[nxt][0] = a_s[(kk + 2) * WB_PA];
-        op[nxt][1] = a_s[(kk + 2) * WB_PA + 32];
-        op[nxt][2] = b_s[(kk + 2) * WB_PB];
-        op[nxt][3] = b_s[(kk + 2) * WB_PB + 32];
-      }
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][0], op[cur][2], acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][0], op[cur][3], acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][1], op[cur][2], acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(op[cur][1], op[cur][3], acc[1][1], 0, 0, 0);
-    }
-    if (t + 1 < nk) store(buf ^ 1);
-    __syncthreads();
+  for (int r = 0; r < WB_AL; r++) {
+    const int p = (wave + 4 * r) * 64 + lane;
+    const int m = p / WB_PA, q = p - m * WB_PA;
+    aoff[r] = q < 16 ? (unsigned)(m * lda + 2 * (q & 7) + (q >> 3)) * 4u : 0x80000000u;
+  }
+#pragma unroll
+  for (int r = 0; r < WB_BL; r++) {
+    const int p = (wave + 4 * r) * 64 + lane;
+    const int row = p >> 7;
+    boff[r] = (unsigned)((2 * (row & 7) + (row >> 3)) * ldb + (p & 127)) * 4u;
   }
 
-  float* C = g.c + bz * g.c_batch;
-  const float* R = g.res ? g.res + bz * g.r_batch : nullptr;
+  // tile t -> batch, row block, column block
+  auto corner = [&](int t, int& bz, int& i0, int& j0) {
+    const int per_b = mb * nb;
+    bz = t / per_b;
+    const int tt = t - bz * per_b;
+    const int nblk = tt / mb;
+    i0 = (tt - nblk * mb) * 128;
+    j0 = nblk * 128;
+  };
+  // loads of slab kt of the tile at (bz, i0, j0) into LDS stage st
+  auto issue = [&](int bz, int i0, int j0, int kt, int st) {
+    const int k0 = kt * WB_BK;
+    const int ab = i0 * lda + k0, bb = k0 * ldb + j0;
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.a + bz * g.a_batch + ab), 0, (a_words - ab) * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.b + bz * g.b_batch + bb), 0, (b_words - bb) * 4, 0x00020000);
+    float* sa = lds + st * WB_STAGE;
+    float* sb = sa + WB_A;
 #pragma unroll
-  for (int mi = 0; mi < 2; mi++)
+    for (int r = 0; r < WB_AL; r++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ar, (__attribute__((address_space(3))) void*)(sa + (wave + 4 * r) * 64), 4, aoff[r],
+          0, 0, 0);
 #pragma unroll
-    for (int ni = 0; ni < 2; ni++) {
-      EpiIn e[16];
+    for (int r = 0; r < WB_BL; r++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          br, (__attribute__((address_space(3))) void*)(sb + (wave + 4 * r) * 64), 4, boff[r],
+          0, 0, 0);
+  };
+
+  int bz, i0, j0;
+  corner(tile, bz, i0, j0);
+  int st = 0;
+  issue(bz, i0, j0, 0, st);
+  while (true) {
+    // accumulators start at 0, or at the bias where the reference seeds it
+    // (row bias only; the seeded region is whole 32-column panels)
+    f32x16 acc[2][2];
 #pragma unroll
-      for (int v = 0; v < 16; v++)
-        e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
-                               j0 + wn0 + ni * 32 + lr);
+    for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-      for (int v = 0; v < 16; v++)
-        epilogue_put(g, C, R != nullptr, e[v], i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
-                     j0 + wn0 + ni * 32 + lr, acc[mi][ni][v]);
+      for (int ni = 0; ni < 2; ni++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[mi][ni][v] = 0.0f;
+        const int n0 = j0 + wn0 + ni * 32;
+        if (!PLAIN && g.bias_mode == 1 && n0 < N &&
+            (g.seed_rule == 1 ? n0 >= N - N % 32 : N - n0 < 32)) {
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            const int i = i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+            if (i < M && n0 + lr < N && bias_seeded(g.seed_rule, i, n0 + lr, M, N))
+              acc[mi][ni][v] = g.bias[i];
+          }
+        }
+      }
+
+    const int next = tile + wg_xcd;
+    int nbz = 0, ni0 = 0, nj0 = 0;
+    if (next < t_end) corner(next, nbz, ni0, nj0);
+    for (int kt = 0; kt < nk; kt++) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      // every wave is past slab kt-1, whose stage now takes slab kt+1 (or
+      // the next tile's first slab)
+      if (kt + 1 < nk)
+        issue(bz, i0, j0, kt + 1, st ^ 1);
+      else if (next < t_end)
+        issue(nbz, ni0, nj0, 0, st ^ 1);
+      const float* sa = lds + st * WB_STAGE + (wm0 + lr) * WB_PA + lh * 8;
+      const float* sb = lds + st * WB_STAGE + WB_A + lh * 8 * 128 + wn0 + lr;
+      f32x4 ga[2][2];
+      float gb[2][2][4];
+#pragma unroll
+      for (int gp = 0; gp < 2; gp++) {
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) ga[gp][mi] = *(const f32x4*)(sa + mi * 32 * WB_PA + gp * 4);
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+          for (int u = 0; u < 4; u++) gb[gp][ni][u] = sb[(gp * 4 + u) * 128 + ni * 32];
+      }
+#pragma unroll
+      for (int gp = 0; gp < 2; gp++)
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+          for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++)
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(ga[gp][mi][u], gb[gp][ni][u],
+                                                                 acc[mi][ni], 0, 0, 0);
+      // all of the slab's operand reads go out before its 32 MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+      st ^= 1;
     }
+
+    float* C = g.c + (int64_t)bz * g.c_batch;
+    if (PLAIN) {
+      // column bias or none (a term of -0.0 leaves every value unchanged)
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+          const int j = j0 + wn0 + ni * 32 + lr;
+          const int ib = i0 + wm0 + mi * 32 + 4 * lh;
+          if (j < N) {
+            const float badd = g.bias_mode == 2 ? g.bias[j] : -0.0f;
+            float* cj = C + j;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+              const int i = ib + 8 * (v >> 2) + (v & 3);
+              if (i < M) cj[(int64_t)i * g.ldc] = acc[mi][ni][v] + badd;
+            }
+          }
+        }
+    } else {
+      const float* R = g.res ? g.res + (int64_t)bz * g.r_batch : nullptr;
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+          EpiIn e[16];
+#pragma unroll
+          for (int v = 0; v < 16; v++)
+            e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                                   j0 + wn0 + ni * 32 + lr);
+#pragma unroll
+          for (int v = 0; v < 16; v++)
+            epilogue_put(g, C, R != nullptr, e[v],
+                         i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                         j0 + wn0 + ni * 32 + lr, acc[mi][ni][v]);
+        }
+    }
+    if (next >= t_end) break;
+    tile = next;
+    bz = nbz;
+    i0 = ni0;
+    j0 = nj0;
+  }
+}
+
+// K in whole slabs, operands within the 32-bit buffer offsets.
+static bool wide_fits(const GemmArgs& g) {
+  const int64_t ab = ((g.m - 1) * g.lda + g.k) * 4, bb = ((g.k - 1) * g.ldb + g.n) * 4;
+  return g.k % WB_BK == 0 && ab < (1ll << 31) && bb < (1ll << 31) &&
+         (g.k * g.ldb + 128) * 4 < (1ll << 31) && (128 * g.lda + g.k) * 4 < (1ll << 31);
 }
 
 static int launch_wide(const GemmArgs& g, hipStream_t s) {
+  static int occ_dev[2][64], cus_dev[64];
+  const bool plain = g.act.kind == 0 && g.res == nullptr && !g.trans_out && g.bias_mode != 1;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(QPH_EHIP, "gemm: no current device (or index past 63)");
+  if (occ_dev[plain][dev] == 0) {
+    int occ = 0, cus = 0;
+    const void* fn = plain ? (const void*)gemm_wide_kernel<true> : (const void*)gemm_wide_kernel<false>;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 256, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        occ <= 0 || cus <= 0)
+      return fail(QPH_EHIP, "gemm: occupancy query failed");
+    cus_dev[dev] = cus;
+    occ_dev[plain][dev] = occ;
+  }
   const int mb = (int)ceil_div(g.m, 128), nb = (int)ceil_div(g.n, 128);
-  const int tiles = mb * nb;
-  const int per = (tiles + NUM_XCD - 1) / NUM_XCD;
-  dim3 grid((unsigned)(per * NUM_XCD), 1, (unsigned)g.batch);
-  hipLaunchKernelGGL(gemm_wide_kernel, grid, dim3(256), 0, s, g, mb, nb, per);
+  const int ntiles = mb * nb * (int)g.batch;
+  const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
+  const int wg_xcd =
+      std::max(1, std::min(per_xcd, occ_dev[plain][dev] * cus_dev[dev] / NUM_XCD));
+  if (plain)
+    hipLaunchKernelGGL(gemm_wide_kernel<true>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(256), 0,
+                       s, g, mb, nb, ntiles, per_xcd, wg_xcd);
+  else
+    hipLaunchKernelGGL(gemm_wide_kernel<false>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(256), 0,
+                       s, g, mb, nb, ntiles, per_xcd, wg_xcd);
   return launch_check("gemm_wide_kernel");
 }
 
@@ -486,10 +584,7 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
     return (double)ceil_div(g.m, bm) * (double)ceil_div(g.n, bn) * (double)g.batch;
   };
   if (g.m >= 128 && g.n >= 128 && tiles(128, 128) >= 512) {
-    const bool vec = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (g.a_batch % 4 == 0) &&
-                     (g.b_batch % 4 == 0) && ((uintptr_t)g.a % 16 == 0) &&
-                     ((uintptr_t)g.b % 16 == 0);
-    if (vec && tiles(128, 128) < (1u << 30)) return launch_wide(g, s);
+    if (wide_fits(g) && tiles(128, 128) < (1u << 30)) return launch_wide(g, s);
     return launch_cfg<2, 2>(g, s);
   }
   return launch_skinny(g, s);

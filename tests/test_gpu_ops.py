@@ -204,6 +204,41 @@ def test_linear_epilogues(gpu, oracle):
         assert_bitexact(_n(y), y_ref, f"linear {rows}x{k}x{n}")
 
 
+def test_gemm_wide_tiles(gpu, oracle):
+    """Shapes with >= 512 128x128 tiles take the persistent wide-tile kernel:
+    ragged M / N edges, unpadded odd ldb, both bias-seeding rules (row bias),
+    GELU + residual epilogue, batched B, and K not a multiple of 16 (which
+    falls back to the 128x128 staged kernel)."""
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(21)
+    for (m, n, k, serial) in [(1300, 6500, 48, False), (1300, 6500, 48, True),
+                              (1290, 6531, 50, False)]:
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+        bias = rng.uniform(-1, 1, (m,)).astype(np.float32)
+        c_ref = oracle.sgemm(a, b, m, n, k, bias, serial=serial)
+        c = ops.sgemm(_t(torch, a), _t(torch, b), m, n, k, _t(torch, bias), serial=serial)
+        assert_bitexact(_n(c), c_ref, f"wide sgemm {m}x{n}x{k} serial={serial}")
+    for (rows, k, n, act, res) in [(1290, 32, 8195, 0, False), (1280, 64, 8200, 1, True)]:
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        w = (rng.standard_normal((k, n)) * math.sqrt(2 / k)).astype(np.float32)
+        b = (rng.standard_normal((n,)) * 0.1).astype(np.float32)
+        r = rng.standard_normal((rows, n)).astype(np.float32) if res else None
+        y_ref = oracle.binary_bcast(oracle.matmul(x, w), b, rows, n, 0, 1)
+        if act == 1:
+            y_ref = oracle.gelu_inplace(y_ref)
+        if res:
+            y_ref = oracle.binary_flat(y_ref, r, 0)
+        y = ops.linear(_t(torch, x), _t(torch, w), _t(torch, b), act,
+                       None if r is None else _t(torch, r))
+        assert_bitexact(_n(y), y_ref, f"wide linear {rows}x{k}x{n} act={act}")
+    a = rng.uniform(-1, 1, (6, 300, 32)).astype(np.float32)
+    b = rng.uniform(-1, 1, (6, 32, 4100)).astype(np.float32)
+    assert_bitexact(_n(ops.matmul(_t(torch, a), _t(torch, b))), oracle.matmul(a, b),
+                    "wide batched matmul")
+
+
 def test_matmul_batched(gpu, oracle):
     torch = gpu
     from qppocr_amd import ops
