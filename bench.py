@@ -10,7 +10,9 @@ events recorded on the session stream inside the timed region.
 roofline: the dominant kernel is the rec head GEMM (1280 x 18709 x 256,
 12.26 GFLOP of the step's 20.86).  Its average launch time comes from HIP
 events around each node of the rec graph (eager launches on the same stream),
-over the same number of steps, after the timed region.
+over the same number of steps, after the timed region.  traffic (HBM bytes
+per launch) is the calibrated FETCH_SIZE + WRITE_SIZE figure recorded in
+profiles/rec_head_gemm_traffic.md (rocprofv3 counter runs of this script).
 
 cpu_baseline: the CPU oracle (plain-C restatement of the qppocr-kernels
 AVX2 path, OpenMP over all host threads) on a bounded sample of the same
@@ -33,6 +35,44 @@ PEAK_HBM_GBS = 8000.0
 REC_BATCH = 32
 
 
+def head_traffic_bytes():
+    """HBM bytes per launch of the rec head GEMM from the committed counter
+    summary, or None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "rec_head_gemm_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
+OP_NAMES = {1: "conv", 2: "convt_pair_sigmoid", 3: "linear", 4: "layernorm", 5: "attention",
+            6: "softmax_argmax", 7: "convt", 8: "act"}
+
+
+def write_node_report(path, nets, graphs):
+    """Per node: average launch time (HIP events, eager launches) and the
+    fraction of its roofline (fp32 MFMA peak for products, HBM peak else)."""
+    rows = []
+    for name, g, node_ms in graphs:
+        for i, d in enumerate(g.nodes):
+            fl, by, bound = nets.node_cost(g, d)
+            ms = node_ms[i]
+            row = {"graph": name, "node": i, "op": OP_NAMES.get(d["op"], str(d["op"])),
+                   "in": list(g.lshapes[d["inp"]]), "w": list(d["ws"]), "us": round(ms * 1e3, 2),
+                   "gflop": round(fl / 1e9, 4), "mb": round(by / 1e6, 3), "bound": bound}
+            if ms > 0:
+                tf, gbs = fl / (ms * 1e-3) / 1e12, by / (ms * 1e-3) / 1e9
+                row["tflops"], row["gbs"] = round(tf, 2), round(gbs, 1)
+                row["frac"] = round(tf / PEAK_FP32_MFMA_TFLOPS if bound == "mfma"
+                                    else gbs / PEAK_HBM_GBS, 4)
+            rows.append(row)
+    with open(path, "w") as f:
+        json.dump(rows, f, indent=0)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -40,6 +80,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-steps", type=int, default=6, help="CPU baseline sample (steps)")
+    ap.add_argument("--node-report", default="",
+                    help="also write per-node times and roofline fractions (JSON) to this path")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a kernel of "
                          "known traffic for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -101,6 +143,22 @@ def main():
     det_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / K
     rec_ms = sum(b.elapsed_time(c) for _, b, c in ev) / K
 
+    # the same step with host buffers at the boundary: det input up, det map
+    # down, rec input up, rec (val, idx) pairs down (pageable host memory)
+    pairs_id = rec_g.outputs[-1]
+    pairs_ptr, pairs_n = rec.tensor_ptr(pairs_id)
+    pairs_host = np.empty(pairs_n, np.float32)
+    torch.cuda.synchronize()
+    h0 = time.perf_counter()
+    for _ in range(K):
+        det.run(det_x, outputs=True)
+        rec.run(rec_x, outputs=False)
+        ops.check(lib.qph_memcpy_d2h(ctx, pairs_host.ctypes.data_as(ctypes.c_void_p),
+                                     ctypes.c_void_p(pairs_ptr), pairs_n * 4))
+    det.sync()
+    h1 = time.perf_counter()
+    host_ms_step = (h1 - h0) * 1e3 / K
+
     # dominant kernel: rec head GEMM, events around each node (eager launches)
     rec.set_profiling(True)
     for _ in range(K):
@@ -114,6 +172,16 @@ def main():
     rows = rec_g.numel(d["inp"]) // d["ws"][0]
     head_flops = 2 * rows * d["ws"][0] * d["ws"][1]
     achieved = head_flops / (head_ms * 1e-3) / 1e12
+
+    if args.node_report:
+        det.set_profiling(True)
+        for _ in range(K):
+            det.run(None, outputs=False)
+        det.sync()
+        det_node_ms = det.node_times()
+        det.set_profiling(False)
+        write_node_report(args.node_report, nets, [("det", det_g, det_node_ms),
+                                                   ("rec", rec_g, node_ms)])
 
     det_flops = nets.flops(det_g)
     rec_flops = nets.flops(rec_g)
@@ -136,10 +204,11 @@ def main():
         "rec_lines_per_s": round(REC_BATCH * 1e3 / rec_ms, 1),
         "det_ms": round(det_ms, 4),
         "rec_ms": round(rec_ms, 4),
-        "roofline": {"bound": "mfma", "kernel": "rec head GEMM 1280x18709x256 (gemm_mfma_kernel)",
+        "pcie_inclusive_img_per_s": round(1e3 / host_ms_step, 3),
+        "roofline": {"bound": "mfma", "kernel": "rec head GEMM 1280x18709x256 (gemm_wide_kernel)",
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": None, "avg_launch_ms": round(head_ms, 5)},
+                     "traffic": head_traffic_bytes(), "avg_launch_ms": round(head_ms, 5)},
     }
 
     if not args.no_cpu:

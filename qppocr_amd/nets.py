@@ -327,29 +327,61 @@ def build_rec(seed=3, batch=32, w=320, h=48):
     return g, x_in
 
 
+def node_cost(g, d):
+    """Algorithmic work of one node: (flops, bytes, bound).  flops = 2 x MACs
+    of the mathematical op (activations not counted); bytes = compulsory fp32
+    traffic, each input, weight and output counted once (an output written
+    up x up times by a fused nearest upsample counts at its written size).
+    bound: "mfma" for conv / linear / attention products, "hbm" otherwise."""
+    f32 = 4
+    op = d["op"]
+    if op == OP_CONV:
+        n = g.shapes[d["inp"]][0]
+        m, cg, kh, kw = d["ws"]
+        sh, sw, ph, pw, peh, pew = d["cp"][:6]
+        group = d["cp"][8]
+        h, w = g.shapes[d["inp"]][2], g.shapes[d["inp"]][3]
+        oh = (h + ph + peh - kh) // sh + 1
+        ow = (w + pw + pew - kw) // sw + 1
+        fl = 2 * n * m * cg * kh * kw * oh * ow
+        by = g.numel(d["inp"]) + m * cg * kh * kw + (m if d["bias"] >= 0 else 0)
+        by += n * m * oh * ow * d["y_up"] ** 2
+        if d["in2"] >= 0:
+            by += g.numel(d["in2"])
+        bound = "hbm" if group > 1 and cg == 1 else "mfma"
+        return fl, by * f32, bound
+    if op == OP_LINEAR:
+        k, nn = d["ws"][0], d["ws"][1]
+        rows = g.numel(d["inp"]) // k
+        by = rows * k + k * nn + nn + rows * nn + (rows * nn if d["in2"] >= 0 else 0)
+        return 2 * rows * k * nn, by * f32, "mfma"
+    if op == OP_ATTENTION:
+        b, t = g.shapes[d["inp"]][0], g.shapes[d["inp"]][1]
+        hd = d["heads"] * d["dh"]
+        return 2 * 2 * b * d["heads"] * t * t * d["dh"], (b * t * 3 * hd + b * t * hd) * f32, "mfma"
+    if op == OP_CONVT_PAIR_SIG:
+        n, c, h, w = g.shapes[d["inp"]]
+        m1 = d["ws"][1]
+        fl = 2 * n * h * w * 4 * (c * m1 + m1 * 4)
+        by = g.numel(d["inp"]) + c * m1 * 4 + m1 * 4 + n * 16 * h * w
+        return fl, by * f32, "hbm"
+    if op == OP_CONVT:
+        n, c, h, w = g.shapes[d["inp"]]
+        m1 = d["ws"][1]
+        return 2 * n * h * w * 4 * c * m1, (g.numel(d["inp"]) + c * m1 * 4 + n * m1 * 4 * h * w) * f32, "hbm"
+    if op == OP_SOFTMAX_ARGMAX:
+        cols = d["ws"][0]
+        rows = g.numel(d["inp"]) // cols
+        return 0, (2 * rows * cols + 2 * rows) * f32, "hbm"
+    if op == OP_LAYERNORM:
+        cols = d["ws"][0]
+        return 0, (2 * g.numel(d["inp"]) + 2 * cols) * f32, "hbm"
+    return 0, 2 * g.numel(d["inp"]) * f32, "hbm"
+
+
 def flops(g):
     """Algorithmic FLOPs of a graph: 2 x MACs of conv / linear / attention matmuls."""
-    total = 0
-    for d in g.nodes:
-        if d["op"] == OP_CONV:
-            n = g.shapes[d["inp"]][0]
-            m, cg, kh, kw = d["ws"]
-            sh, sw, ph, pw, peh, pew = d["cp"][:6]
-            h, w = g.shapes[d["inp"]][2], g.shapes[d["inp"]][3]
-            oh = (h + ph + peh - kh) // sh + 1
-            ow = (w + pw + pew - kw) // sw + 1
-            total += 2 * n * m * cg * kh * kw * oh * ow
-        elif d["op"] == OP_LINEAR:
-            k, nn = d["ws"][0], d["ws"][1]
-            total += 2 * (g.numel(d["inp"]) // k) * k * nn
-        elif d["op"] == OP_ATTENTION:
-            b, t = g.shapes[d["inp"]][0], g.shapes[d["inp"]][1]
-            total += 2 * 2 * b * d["heads"] * t * t * d["dh"]
-        elif d["op"] == OP_CONVT_PAIR_SIG:
-            n, c, h, w = g.shapes[d["inp"]]
-            m1 = d["ws"][1]
-            total += 2 * n * h * w * 4 * (c * m1 + m1 * 4)
-    return total
+    return sum(node_cost(g, d)[0] for d in g.nodes)
 
 
 # ------------------------------------------------------------------ session
