@@ -260,6 +260,285 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
     }
 }
 
+// ------------------------------------------------------- direct 3x3 conv
+//
+// The 3x3 dense convs of the det neck/head and the stems (C up to a few
+// hundred, M <= 64, any stride and padding): the same k-ascending fma chain
+// per output as the implicit-GEMM kernel above (k = (ci, ky, kx), bias after
+// the chain or seeded by the same panel rule), with no LDS at all.
+//
+// One wave owns MT 16-channel blocks x NPX runs of 16 consecutive output
+// pixels (row-major over oh x ow) and walks k in groups of four input
+// channels (36 k = 9 v_mfma_f32_16x16x4f32 steps).  Lane (n = lane % 16,
+// g = lane / 16) supplies k = 4s + g of step s: its input word is read
+// straight from HBM / L2 with a buffer load whose per-lane offset is fixed
+// for the whole K loop (the buffer base moves by four channels per group),
+// and out-of-image taps or channels past C carry an offset past the buffer
+// range, which reads 0 -- the zero padding.  Weights come from the k-major
+// repack wk[Kpad][Mpad] (one 64-byte row segment per lane group).  The next
+// group's operands are loaded into registers while the current group's
+// MFMAs run, and every wave is independent (no barriers), so the many waves
+// of a launch hide the load latency for each other.
+
+struct DirectConvK {
+  const float* x;
+  const float* wk;
+  const float* bias;
+  const float* res;
+  float* y;
+  int c, h, w, m, mpad, sh, sw, ph, pw, oh, ow;
+  int64_t y_ctotal, y_coff, y_up;
+  int units_m, units_px, units;
+  Act act;
+};
+
+// Work unit u (a wave-uniform index) of the conv described by p.
+template <int MT, int NPX, int D>
+__device__ __forceinline__ void direct3x3_unit(const DirectConvK& p, int u, int lane) {
+  const int mu = u % p.units_m, rest = u / p.units_m;
+  const int pu = rest % p.units_px, img = rest / p.units_px;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int m0 = mu * 16 * MT;
+  const int npx = p.oh * p.ow, HW = p.h * p.w;
+  const unsigned OOB = 0x80000000u;
+
+  int poy[NPX], pox[NPX];
+  bool pval[NPX];
+  unsigned voff[NPX][9];
+#pragma unroll
+  for (int t = 0; t < NPX; t++) {
+    const int pix = (pu * NPX + t) * 16 + l16;
+    pval[t] = pix < npx;
+    poy[t] = pix / p.ow;
+    pox[t] = pix - poy[t] * p.ow;
+#pragma unroll
+    for (int s = 0; s < 9; s++) {
+      const int kl = 4 * s + lg, cl = kl / 9, tap = kl - 9 * cl;
+      const int ky = tap / 3, kx = tap - 3 * ky;
+      const int iy = poy[t] * p.sh - p.ph + ky, ix = pox[t] * p.sw - p.pw + kx;
+      const bool ok = pval[t] && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+      // offsets of 2^31 and up lie past every range (the image is < 2 GB)
+      const int64_t off = ((int64_t)cl * HW + (int64_t)iy * p.w + ix) * 4;
+      voff[t][s] = ok && off < (int64_t)OOB ? (unsigned)off : OOB;
+    }
+  }
+
+  // accumulators, bias-seeded where the reference seeds (M%4 tail rows of a
+  // partial 32-column panel of the output row)
+  f32x4 acc[MT][NPX];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int t = 0; t < NPX; t++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        float s0 = 0.0f;
+        const int co = m0 + mt * 16 + 4 * lg + v;
+        if (p.bias && co < p.m && pval[t]) {
+          const int n0 = (pox[t] >> 5) << 5;
+          if ((p.ow - n0) < 32 && co >= p.m - p.m % 4) s0 = p.bias[co];
+        }
+        acc[mt][t][v] = s0;
+      }
+
+  const float* xi = p.x + (int64_t)img * p.c * HW;
+  const unsigned woff = (unsigned)(lg * p.mpad + m0 + l16) * 4u;
+  const int ng = (p.c + 3) / 4;
+  const int w_words = ng * 36 * p.mpad;
+  // D register buffers: the loads of groups g+1 .. g+D-1 are in flight
+  // while group g's MFMAs run
+  float ab[D][MT][9], bb[D][NPX][9];
+  auto load = [&](int g, float (&a)[MT][9], float (&b)[NPX][9]) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(xi + (int64_t)g * 4 * HW), 0, (p.c - 4 * g) * HW * 4, 0x00020000);
+#pragma unroll
+    for (int s = 0; s < 9; s++)
+#pragma unroll
+      for (int t = 0; t < NPX; t++)
+        b[t][s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff[t][s], 0, 0));
+    // weights: the lane part of the offset is fixed, the step part uniform
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.wk + g * 36 * p.mpad), 0, (w_words - g * 36 * p.mpad) * 4, 0x00020000);
+#pragma unroll
+    for (int s = 0; s < 9; s++)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+        a[mt][s] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(wr, woff, (4 * s * p.mpad + mt * 16) * 4, 0));
+  };
+  auto mma = [&](const float (&a)[MT][9], const float (&b)[NPX][9]) {
+#pragma unroll
+    for (int s = 0; s < 9; s++)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < NPX; t++)
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][s], b[t][s], acc[mt][t], 0, 0, 0);
+  };
+
+  // Loads are issued unconditionally (groups past the end reload the last
+  // group, unused) so that every path has the same loads in flight and the
+  // waits before each group's MFMAs stay partial.
+#pragma unroll
+  for (int j = 0; j < D - 1; j++) load(min(j, ng - 1), ab[j], bb[j]);
+  for (int g = 0; g < ng; g += D) {
+#pragma unroll
+    for (int j = 0; j < D; j++) {
+      load(min(g + j + D - 1, ng - 1), ab[(j + D - 1) % D], bb[(j + D - 1) % D]);
+      if (g + j < ng) mma(ab[j], bb[j]);
+    }
+  }
+
+  // epilogue: operands (bias, residual) first, then finish and store
+  const int64_t yoh = (int64_t)p.oh * p.y_up, yow = (int64_t)p.ow * p.y_up;
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    float badd[NPX][4], rv[NPX][4];
+    bool hadd[NPX][4], ok[NPX][4];
+#pragma unroll
+    for (int t = 0; t < NPX; t++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int co = m0 + mt * 16 + 4 * lg + v;
+        ok[t][v] = pval[t] && co < p.m;
+        hadd[t][v] = false;
+        badd[t][v] = 0.0f;
+        rv[t][v] = 0.0f;
+        if (!ok[t][v]) continue;
+        if (p.bias) {
+          const int n0 = (pox[t] >> 5) << 5;
+          const bool seeded = (p.ow - n0) < 32 && co >= p.m - p.m % 4;
+          if (!seeded) {
+            badd[t][v] = p.bias[co];
+            hadd[t][v] = true;
+          }
+        }
+        if (p.res) rv[t][v] = p.res[(((int64_t)img * p.m + co) * p.oh + poy[t]) * p.ow + pox[t]];
+      }
+#pragma unroll
+    for (int t = 0; t < NPX; t++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        if (!ok[t][v]) continue;
+        const int co = m0 + mt * 16 + 4 * lg + v;
+        float xv = acc[mt][t][v];
+        if (hadd[t][v]) xv = xv + badd[t][v];
+        xv = act_apply(xv, p.act);
+        if (p.res) xv = xv + rv[t][v];
+        float* yb = p.y + (((int64_t)img * p.y_ctotal + p.y_coff + co) * yoh) * yow;
+        store_replicated(yb, yow, poy[t], pox[t], (int)p.y_up, xv);
+      }
+  }
+}
+
+template <int MT, int NPX, int D>
+__global__ __launch_bounds__(256) void conv3x3_direct_kernel(DirectConvK p) {
+  // wave index as a scalar: everything derived from it (image, channel
+  // block, buffer bases) stays in SGPRs
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int u = blockIdx.x * 4 + wave;
+  if (u >= p.units) return;
+  direct3x3_unit<MT, NPX, D>(p, u, lane);
+}
+
+// Up to four independent 3x3 convs in one launch (the det neck's four
+// smoothing convs, which read different levels and write disjoint channel
+// slots of the concat): waves [start[i], start[i+1]) work on conv i.
+#define DIRECT_GROUP_MAX 4
+struct DirectConvGroup {
+  DirectConvK k[DIRECT_GROUP_MAX];
+  int start[DIRECT_GROUP_MAX + 1];
+  int n;
+};
+
+__global__ __launch_bounds__(256) void conv3x3_direct_group_kernel(DirectConvGroup g) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int u = blockIdx.x * 4 + wave;
+  if (u >= g.start[g.n]) return;
+  if (u < g.start[1]) direct3x3_unit<1, 1, 4>(g.k[0], u, lane);
+  else if (u < g.start[2]) direct3x3_unit<1, 1, 4>(g.k[1], u - g.start[1], lane);
+  else if (u < g.start[3]) direct3x3_unit<1, 1, 4>(g.k[2], u - g.start[2], lane);
+  else direct3x3_unit<1, 1, 4>(g.k[3], u - g.start[3], lane);
+}
+
+static void direct_params(const ConvArgs& a, const float* wk, DirectConvK& p) {
+  p = DirectConvK{};
+  p.x = a.x; p.wk = wk; p.bias = a.bias; p.res = a.res; p.y = a.y;
+  p.c = (int)a.c; p.h = (int)a.h; p.w = (int)a.w; p.m = (int)a.m; p.mpad = (int)mpad_of(a.m);
+  p.sh = (int)a.sh; p.sw = (int)a.sw; p.ph = (int)a.ph; p.pw = (int)a.pw;
+  p.oh = (int)a.oh; p.ow = (int)a.ow;
+  p.y_ctotal = a.y_ctotal; p.y_coff = a.y_coff; p.y_up = a.y_up;
+  p.act = a.act;
+}
+
+bool direct3x3_eligible(const ConvArgs& a) {
+  return a.kh == 3 && a.kw == 3 && a.group == 1 &&
+         a.c * a.h * a.w * 4 < (int64_t)0x80000000 && a.oh * a.ow < (1ll << 30) &&
+         kpad_of(a.c, 9) * mpad_of(a.m) * 4 < (int64_t)0x80000000 &&
+         (int64_t)ceil_div(a.m, 16) * ceil_div(a.oh * a.ow, 16) * a.n < (1ll << 29);
+}
+
+int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s) {
+  if (n < 1 || n > DIRECT_GROUP_MAX) return fail(QPH_EINVAL, "conv group: 1 to 4 convs");
+  DirectConvGroup g{};
+  g.n = n;
+  int64_t total = 0;
+  for (int i = 0; i < n; i++) {
+    if (!a[i].wk || !direct3x3_eligible(a[i]) || a[i].c <= 4)
+      return fail(QPH_EUNSUPPORTED, "conv group: member is not a resident direct 3x3 conv");
+    direct_params(a[i], a[i].wk, g.k[i]);
+    g.k[i].units_m = (int)ceil_div(a[i].m, 16);
+    g.k[i].units_px = (int)ceil_div(a[i].oh * a[i].ow, 16);
+    g.k[i].units = (int)(g.k[i].units_m * (int64_t)g.k[i].units_px * a[i].n);
+    g.start[i] = (int)total;
+    total += g.k[i].units;
+  }
+  for (int i = n; i <= DIRECT_GROUP_MAX; i++) g.start[i] = (int)total;
+  if (total >= (1ll << 30)) return fail(QPH_EUNSUPPORTED, "conv group: grid too large");
+  hipLaunchKernelGGL(conv3x3_direct_group_kernel, dim3((unsigned)ceil_div(total, 4)), dim3(256),
+                     0, s, g);
+  return launch_check("conv3x3_direct_group_kernel");
+}
+
+// Launches the direct kernel for a 3x3 conv, choosing the per-wave tile so
+// that the launch has enough waves to hide load latency.
+static int launch_direct3x3(const ConvArgs& a, const float* wk, hipStream_t s) {
+  DirectConvK p;
+  direct_params(a, wk, p);
+  const int64_t npx = a.oh * a.ow;
+  auto waves = [&](int mt, int npxu) {
+    return (int64_t)ceil_div(a.m, 16 * mt) * ceil_div(npx, 16 * npxu) * a.n;
+  };
+  int mt = 1, nt = 1;
+  if (a.m > 16 && waves(2, 2) >= 4096) { mt = 2; nt = 2; }
+  else if (a.m > 16 && waves(2, 1) >= 2048) { mt = 2; nt = 1; }
+  else if (waves(1, 2) >= 4096) { mt = 1; nt = 2; }
+  p.units_m = (int)ceil_div(a.m, 16 * mt);
+  p.units_px = (int)ceil_div(npx, 16 * nt);
+  const int64_t units = waves(mt, nt);
+  if (units >= (1ll << 31) - 4) return fail(QPH_EUNSUPPORTED, "dense conv: grid too large");
+  p.units = (int)units;
+  dim3 grid((unsigned)ceil_div(units, 4));
+  // one group of four channels (the stems): nothing to prefetch
+  const bool one = a.c <= 4;
+  if (mt == 2 && nt == 2) {
+    if (one) hipLaunchKernelGGL((conv3x3_direct_kernel<2, 2, 1>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((conv3x3_direct_kernel<2, 2, 2>), grid, dim3(256), 0, s, p);
+  } else if (mt == 2) {
+    if (one) hipLaunchKernelGGL((conv3x3_direct_kernel<2, 1, 1>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((conv3x3_direct_kernel<2, 1, 3>), grid, dim3(256), 0, s, p);
+  } else if (nt == 2) {
+    if (one) hipLaunchKernelGGL((conv3x3_direct_kernel<1, 2, 1>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((conv3x3_direct_kernel<1, 2, 3>), grid, dim3(256), 0, s, p);
+  } else {
+    if (one) hipLaunchKernelGGL((conv3x3_direct_kernel<1, 1, 1>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((conv3x3_direct_kernel<1, 1, 4>), grid, dim3(256), 0, s, p);
+  }
+  return launch_check("conv3x3_direct_kernel");
+}
+
 template <int T>
 static int launch_dense_t(const DenseConvK& p, bool wide_m, dim3 grid, hipStream_t s) {
   if (wide_m)
@@ -279,6 +558,8 @@ int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
     QPH_TRY(launch_repack_conv_w_taps(a.wt, a.m, a.c, khkw, scratch_wk, s));
     wk = scratch_wk;
   }
+  // 3x3: direct kernel (input and weight buffers within 32-bit offsets)
+  if (direct3x3_eligible(a)) return launch_direct3x3(a, wk, s);
   DenseConvK p{};
   p.x = a.x; p.wk = wk; p.bias = a.bias; p.res = a.res; p.y = a.y;
   p.c = a.c; p.h = a.h; p.w = a.w; p.m = a.m; p.mpad = mpad_of(a.m);

@@ -179,11 +179,16 @@ struct ConvArgs {
   // tensor (y_ctotal channels, offset y_coff) and nearest upsample by y_up.
   int64_t y_ctotal, y_coff, y_up;
 };
+// plan != NULL: a dense conv with resident weights is not launched; its
+// arguments are returned in *plan (other conv kinds fail with EUNSUPPORTED).
 int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
                   const float* wk_resident, const int64_t ws[4], const float* bias,
                   const qph_conv_params* p, const qph_act* act, const qph_conv_epilogue* ep,
-                  float* y);
+                  float* y, ConvArgs* plan = nullptr);
 int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk);
+// 3x3 convs the direct kernel takes; up to four independent ones in one launch
+bool direct3x3_eligible(const ConvArgs& a);
+int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s);
 int launch_depthwise(const ConvArgs& a, hipStream_t s);
 int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw);
 // wk[Kpad][Mpad] k-major copy of an ONNX [M][cg][kh][kw] weight, Kpad =

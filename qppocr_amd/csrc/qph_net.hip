@@ -19,6 +19,8 @@ struct qph_net {
   std::vector<int32_t> outputs;
   std::vector<float*> weights;   // device copies
   std::vector<float*> wk;        // per node: resident repacked dense-conv weights (or NULL)
+  std::vector<ConvArgs> plan;    // per node: launch arguments of a dense 3x3 conv
+  std::vector<int> group_len;    // > 1: first of that many independent 3x3 convs, one launch
   std::vector<float*> tptr;      // per tensor device pointer
   char* arena;
   size_t arena_bytes;
@@ -104,6 +106,61 @@ static int run_node(qph_net* net, size_t i) {
       return launch_elementwise_act(x, y, numel_of(net, n.in), make_act(&n.act), s);
     default:
       return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unknown op");
+  }
+}
+
+static int32_t storage_of(const qph_net* net, int32_t t) {
+  return t >= 0 && net->alias[(size_t)t] >= 0 ? net->alias[(size_t)t] : t;
+}
+
+// Consecutive dense 3x3 convs (up to four) of which none reads another's
+// output run as one launch of the direct kernel: the det neck's smoothing
+// convs at 20, 40, 80 and 160 px each leave most of the chip idle alone.
+static void plan_conv_groups(qph_net* net) {
+  const size_t nn = net->nodes.size();
+  net->plan.assign(nn, ConvArgs{});
+  net->group_len.assign(nn, 1);
+  std::vector<bool> ok(nn, false);
+  for (size_t i = 0; i < nn; i++) {
+    const qph_node& n = net->nodes[i];
+    if (n.op != QPH_OP_CONV || !net->wk[i] || n.ws[2] != 3 || n.ws[3] != 3 || n.cp.group != 1)
+      continue;
+    qph_conv_epilogue ep{};
+    ep.residual = n.in2 >= 0 ? net->tptr[n.in2] : nullptr;
+    ep.res_up = n.res_up;
+    ep.y_ctotal = n.y_ctotal;
+    ep.y_coff = n.y_coff;
+    ep.y_up = n.y_up;
+    ep.trans_out = n.trans_out;
+    ConvArgs pl{};
+    const float* bias = n.bias >= 0 ? net->weights[n.bias] : nullptr;
+    if (conv_dispatch(net->ctx, net->tptr[n.in], &net->shapes[4 * (size_t)n.in],
+                      net->weights[n.w], net->wk[i], n.ws, bias, &n.cp, &n.act, &ep,
+                      net->tptr[n.out], &pl) != QPH_OK)
+      continue;
+    if (!direct3x3_eligible(pl) || pl.c <= 4) continue;
+    net->plan[i] = pl;
+    ok[i] = true;
+  }
+  auto reads_output_of = [&](size_t a, size_t b) {
+    const qph_node& na = net->nodes[a];
+    const int32_t out = storage_of(net, net->nodes[b].out);
+    return storage_of(net, na.in) == out || (na.in2 >= 0 && storage_of(net, na.in2) == out);
+  };
+  for (size_t i = 0; i < nn;) {
+    size_t j = i;
+    if (ok[i]) {
+      j = i + 1;
+      while (j < nn && j - i < 4 && ok[j]) {
+        bool indep = true;
+        for (size_t k = i; k < j && indep; k++)
+          indep = !reads_output_of(j, k) && !reads_output_of(k, j);
+        if (!indep) break;
+        j++;
+      }
+      if (j - i >= 2) net->group_len[i] = (int)(j - i);
+    }
+    i = j > i ? j : i + 1;
   }
 }
 
@@ -326,6 +383,7 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
       if (rc) return bail(rc);
     }
   }
+  plan_conv_groups(net);
   rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   if (rc) return bail(rc);
   *out = net;
@@ -390,7 +448,14 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
     if (!net->graph_ready) {
       QPH_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
       int rc = QPH_OK;
-      for (size_t i = 0; i < net->nodes.size() && rc == QPH_OK; i++) rc = run_node(net, i);
+      for (size_t i = 0; i < net->nodes.size() && rc == QPH_OK;) {
+        if (net->group_len[i] > 1) {
+          rc = launch_dense_conv_group(&net->plan[i], net->group_len[i], s);
+          i += (size_t)net->group_len[i];
+        } else {
+          rc = run_node(net, i++);
+        }
+      }
       hipGraph_t g = nullptr;
       hipError_t e = hipStreamEndCapture(s, &g);
       if (rc != QPH_OK) {

@@ -193,7 +193,7 @@ namespace qph {
 int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
                   const float* wk_resident, const int64_t ws[4], const float* bias,
                   const qph_conv_params* p, const qph_act* act, const qph_conv_epilogue* ep,
-                  float* y) {
+                  float* y, ConvArgs* plan) {
   CTX_CHECK(ctx);
   if (!x || !w || !y) return fail(QPH_EINVAL, "conv2d: NULL tensor");
   if (!act_valid(act)) return fail(QPH_EINVAL, "conv2d: bad activation kind");
@@ -219,6 +219,8 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
   const bool plain_out = y_ctotal == m && y_coff == 0 && y_up == 1;
   Act a = make_act(act);
 
+  if (plan && (pointwise || depthwise || g != 1 || !wk_resident))
+    return fail(QPH_EUNSUPPORTED, "conv2d: only resident dense convs are planned");
   if (pointwise) {
     if (!plain_out) return fail(QPH_EUNSUPPORTED, "conv2d 1x1: channel-slice output not supported");
     if (trans && res_up) return fail(QPH_EUNSUPPORTED, "conv2d 1x1: trans_out with res_up");
@@ -263,6 +265,10 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
   if (res && !plain_out) return fail(QPH_EUNSUPPORTED, "conv2d: residual with placed output");
   if (wk_resident) {
     ca.wk = wk_resident;
+    if (plan) {
+      *plan = ca;
+      return QPH_OK;
+    }
     return launch_dense_conv(ca, ctx->stream, nullptr);
   }
   // standalone call: k-major repacked weights go to the context scratch

@@ -130,6 +130,37 @@ def test_conv3x3_placed_output(gpu, oracle):
     assert_bitexact(_n(out), ref, "concat slots")
 
 
+# 3x3 convs on the direct kernel: each per-wave tile shape (16/32 channels x
+# 16/32 pixels), a channel count that ends inside a group of four, M with a
+# partial last block and a bias-seeded M%4 tail (partial 32-column panel),
+# stride (2, 1) with uneven padding.
+DIRECT_CASES = [
+    # n, c, m, h, w, sh, sw, ph, pw, peh, pew
+    (1, 96, 24, 40, 40, 1, 1, 1, 1, 1, 1),
+    (2, 5, 22, 37, 40, 1, 1, 1, 1, 1, 1),
+    (2, 32, 32, 128, 128, 1, 1, 1, 1, 1, 1),
+    (8, 8, 32, 128, 128, 1, 1, 1, 1, 1, 1),
+    (8, 8, 16, 128, 128, 1, 1, 1, 1, 1, 1),
+    (8, 3, 16, 128, 128, 2, 2, 1, 1, 1, 1),
+    (3, 12, 40, 33, 47, 2, 1, 0, 1, 2, 0),
+]
+
+
+@pytest.mark.parametrize("case", DIRECT_CASES, ids=[str(c) for c in DIRECT_CASES])
+def test_conv3x3_direct_tiles(gpu, oracle, case):
+    torch = gpu
+    from qppocr_amd import ops
+    n, c, m, h, w, sh, sw, ph, pw, peh, pew = case
+    rng = np.random.default_rng(sum(case))
+    x = rng.standard_normal((n, c, h, w)).astype(np.float32)
+    wt = rng.standard_normal((m, c, 3, 3)).astype(np.float32)
+    b = rng.standard_normal((m,)).astype(np.float32)
+    y_ref = oracle.conv2d(x, wt, b, oracle.conv_params(sh, sw, ph, pw, peh, pew), 2)
+    y = ops.conv2d(_t(torch, x), _t(torch, wt), _t(torch, b),
+                   ops.conv_params(sh, sw, ph, pw, peh, pew), 2)
+    assert_bitexact(_n(y), y_ref, f"direct 3x3 {case}")
+
+
 def test_grouped_conv_unsupported(gpu):
     torch = gpu
     from qppocr_amd import ops
