@@ -73,6 +73,40 @@ def write_node_report(path, nets, graphs):
         json.dump(rows, f, indent=0)
 
 
+def time_mixed_page(steps, warmup, stream):
+    """det 1x3x1536x1536 + 128 rec lines (widths {80..1280}, buckets of 160,
+    <= 64 lines per batch), inputs resident: det img/s, rec lines/s and the
+    wall time of one whole page, from HIP events on the session stream."""
+    import torch
+    from qppocr_amd import pipeline
+    det_g, det_x, rw, lines, widths = pipeline.mixed_page(4, 1536, 128)
+    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths)
+    page.upload()
+    for _ in range(warmup):
+        page.run()
+    page.sync()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        page.run_det()
+        ev[i][1].record(stream)
+        page.run_rec()
+        ev[i][2].record(stream)
+    page.sync()
+    torch.cuda.synchronize()
+    det_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / steps
+    rec_ms = sum(b.elapsed_time(c) for _, b, c in ev) / steps
+    out = {"workload": "det 1x3x1536x1536 + 128 rec lines 3x48x{80..1280}, buckets of 160, "
+                       "<= 64 lines/batch, CTC masked past w/8",
+           "rec_batches": [[bw, len(idx)] for bw, idx in page.plan],
+           "det_img_per_s": round(1e3 / det_ms, 2),
+           "rec_lines_per_s": round(len(widths) * 1e3 / rec_ms, 1),
+           "page_ms": round(det_ms + rec_ms, 4), "det_ms": round(det_ms, 4),
+           "rec_ms": round(rec_ms, 4)}
+    page.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -80,6 +114,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-steps", type=int, default=6, help="CPU baseline sample (steps)")
+    ap.add_argument("--mixed-page", action="store_true",
+                    help="also time the mixed-shape page (det 1536^2 + 128 bucketed rec lines)")
     ap.add_argument("--node-report", default="",
                     help="also write per-node times and roofline fractions (JSON) to this path")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -210,6 +246,9 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": head_traffic_bytes(), "avg_launch_ms": round(head_ms, 5)},
     }
+
+    if args.mixed_page:
+        result["mixed_page"] = time_mixed_page(K, args.warmup, stream)
 
     if not args.no_cpu:
         from oracle import nets as onets

@@ -8,7 +8,8 @@
 3  det forward 1x3x640x640 (nets.build_det, seed 2).
 4  rec forward 32x3x48x320 (nets.build_rec, seed 3).
 5  det at 1536^2 + 128 rec lines of widths {80, 88, ..., 1280}, bucketed to
-   multiples of 160, <= 64 lines per batch, CTC masked past w/8 (seed 4).
+   multiples of 160, <= 64 lines per batch, CTC masked past w/8 (seed 4):
+   pipeline.mixed_page and pipeline.PageRunner.
 """
 import math
 
@@ -60,29 +61,3 @@ def cfg2_bytes_flops(c, hw, k, s):
     oh = conv_out_hw(hw, k, s, k // 2)
     bytes_ = 4 * (c * hw * hw + c * k * k + c + c * oh * oh)
     return bytes_, 2 * c * k * k * oh * oh
-
-
-CFG5_BUCKET = 160
-CFG5_MAX_BATCH = 64
-
-
-def cfg5_widths(seed=4, n=128):
-    """Line widths drawn uniformly from {80, 88, ..., 1280}."""
-    rng = np.random.Generator(np.random.PCG64(seed))
-    choices = np.arange(80, 1281, 8)
-    return rng.choice(choices, size=n).astype(np.int64)
-
-
-def cfg5_plan(widths, bucket=CFG5_BUCKET, max_batch=CFG5_MAX_BATCH):
-    """Width bucketing and batching of the rec lines: bucket width =
-    ceil(w / bucket) * bucket; lines of one bucket (in input order) are cut
-    into batches of at most max_batch.  Returns [(bucket_width, [line idx])].
-    (The reference engine sorts lines by width and rounds batch widths up to
-    the session's bucket grain, qppocr-core/src/pipeline/engine.rs:1211-1290.)"""
-    bw = ((np.asarray(widths) + bucket - 1) // bucket) * bucket
-    plan = []
-    for w in sorted(set(int(v) for v in bw)):
-        idx = [i for i in range(len(widths)) if bw[i] == w]
-        for s in range(0, len(idx), max_batch):
-            plan.append((w, idx[s:s + max_batch]))
-    return plan

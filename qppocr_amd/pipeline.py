@@ -1,0 +1,151 @@
+"""Page-level det + rec over the HIP sessions (the mixed-shape workload).
+
+One page: a det forward on the page image, then its text lines recognised in
+width buckets.  As the reference engine does (qppocr-core/src/pipeline/
+engine.rs:1211-1290 batching, 1450-1493 rec run and decode), lines of one
+bucket width run together as one batch, zero-padded on the right to the
+bucket width; every (batch, bucket width) shape has its own session (its own
+HIP graph), created once and replayed.  The rec sessions export (val, idx)
+pairs (DeviceSession::rec_argmax_pairs, device.rs:160-165) and the host
+collapses them with ctc_decode_pairs (rec.rs:82-115), reading only the
+steps t < w_i / 8 of a line of width w_i (the padding is masked out).
+"""
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from .nets import HipSession, build_det, build_rec_graph, rec_weights, WeightRng
+
+REC_H = 48
+REC_STRIDE = 8          # rec time steps per input column: T = w / 8
+BUCKET = 160
+MAX_BATCH = 64
+
+
+def ctc_decode_pairs(pairs, t_len):
+    """Greedy CTC collapse of (val, idx-bits) pairs over the first t_len
+    steps (qppocr-core/src/pipeline/rec.rs:82-115): a step emits its index
+    when it is not blank (0) and differs from the previous step's index;
+    the confidence is the f64 mean of the emitted values (0 if none)."""
+    pairs = np.ascontiguousarray(pairs, dtype=np.float32).reshape(-1, 2)
+    idx = pairs[:, 1].view(np.uint32)
+    ids = []
+    conf_sum = 0.0
+    prev = -1
+    for t in range(int(t_len)):
+        b = int(idx[t])
+        if b != 0 and b != prev:
+            ids.append(b)
+            conf_sum += float(pairs[t, 0])
+        prev = b
+    conf = np.float32(conf_sum / len(ids)) if ids else np.float32(0.0)
+    return ids, float(conf)
+
+
+def bucket_plan(widths, bucket=BUCKET, max_batch=MAX_BATCH):
+    """[(bucket_width, [line indices])]: bucket width = ceil(w / bucket) *
+    bucket; the lines of one bucket, in input order, cut into batches of at
+    most max_batch."""
+    bw = ((np.asarray(widths) + bucket - 1) // bucket) * bucket
+    plan = []
+    for w in sorted(set(int(v) for v in bw)):
+        idx = [i for i in range(len(widths)) if bw[i] == w]
+        for s in range(0, len(idx), max_batch):
+            plan.append((w, idx[s:s + max_batch]))
+    return plan
+
+
+def pack_lines(lines, idx, bucket_width):
+    """[B, 3, 48, bucket_width] batch of the given lines, zero-padded right."""
+    out = np.zeros((len(idx), 3, REC_H, bucket_width), dtype=np.float32)
+    for b, i in enumerate(idx):
+        out[b, :, :, :lines[i].shape[-1]] = lines[i]
+    return out
+
+
+class PageRunner:
+    """det on one page size plus rec sessions for a fixed set of line
+    widths; inputs are uploaded once (resident in HBM), run() replays the
+    det graph and every rec batch graph on one stream."""
+
+    def __init__(self, det_graph, det_input, rec_w, lines, widths, device=0):
+        self.det = HipSession(det_graph, device)
+        self.det_input = det_input
+        self.widths = np.asarray(widths, dtype=np.int64)
+        self.plan = bucket_plan(self.widths)
+        self.rec = []
+        for bw, idx in self.plan:
+            g = build_rec_graph(rec_w, len(idx), bw, REC_H)
+            sess = HipSession(g, device)
+            self.rec.append((bw, idx, g, sess, pack_lines(lines, idx, bw)))
+        self.lib = _lib.load()
+
+    def upload(self):
+        """Inputs to HBM (one copy per session) and one run to build the graphs."""
+        self.det.run(self.det_input, outputs=False)
+        for _, _, _, sess, x in self.rec:
+            sess.run(x, outputs=False)
+        self.sync()
+
+    def run(self):
+        """One page: det + every rec batch, inputs already resident."""
+        self.det.run(None, outputs=False)
+        for _, _, _, sess, _ in self.rec:
+            sess.run(None, outputs=False)
+
+    def run_det(self):
+        self.det.run(None, outputs=False)
+
+    def run_rec(self):
+        for _, _, _, sess, _ in self.rec:
+            sess.run(None, outputs=False)
+
+    def sync(self):
+        self.det.sync()
+
+    def det_map(self):
+        g = self.det.graph
+        ptr, n = self.det.tensor_ptr(g.outputs[0])
+        return self._d2h(ptr, n).reshape(g.lshapes[g.outputs[0]])
+
+    def rec_pairs(self):
+        """Per line: its [T_bucket, 2] pairs (unmasked)."""
+        out = [None] * len(self.widths)
+        for bw, idx, g, sess, _ in self.rec:
+            ptr, n = sess.tensor_ptr(g.outputs[-1])
+            pairs = self._d2h(ptr, n).reshape(len(idx), bw // REC_STRIDE, 2)
+            for b, i in enumerate(idx):
+                out[i] = pairs[b]
+        return out
+
+    def decode(self):
+        """Per line: (ids, confidence) over its unpadded steps."""
+        return [ctc_decode_pairs(p, int(w) // REC_STRIDE)
+                for p, w in zip(self.rec_pairs(), self.widths)]
+
+    def _d2h(self, ptr, n):
+        host = np.empty(n, dtype=np.float32)
+        _lib.check(self.lib.qph_memcpy_d2h(self.det.ctx, host.ctypes.data_as(ctypes.c_void_p),
+                                           ctypes.c_void_p(ptr), n * 4))
+        return host
+
+    def close(self):
+        self.det.close()
+        for _, _, _, sess, _ in self.rec:
+            sess.close()
+
+
+def mixed_page(seed=4, det_hw=1536, n_lines=128):
+    """The mixed-shape workload: a det_hw^2 page (det architecture and
+    input normalisation of the 640^2 workload; its input and weights from
+    build_det(seed)) and n_lines rec lines of height 48 with widths uniform
+    on {80, 88, ..., 1280} and U[-1, 1) pixels.  One PCG64(seed) stream
+    draws the widths, then the line pixels in line order, then the rec
+    weights."""
+    r = WeightRng(seed)
+    widths = r.rng.choice(np.arange(80, 1281, 8), size=n_lines).astype(np.int64)
+    det_g, det_x = build_det(seed, det_hw, det_hw)
+    lines = [r.uniform((3, REC_H, int(w)), -1.0, 1.0) for w in widths]
+    rw = rec_weights(r)
+    return det_g, det_x, rw, lines, widths

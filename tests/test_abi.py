@@ -95,3 +95,4 @@ def test_ops_refuse_host_tensors(lib):
 
 def test_version(lib):
     assert b"gfx950" in lib.qph_version()
+

@@ -79,3 +79,32 @@ def test_cfg4_rec_net(gpu, oracle):
     probs2, pairs2 = sess.run(x)
     assert_bitexact(probs2, probs, "rec replay")
     sess.close()
+
+
+def test_cfg5_mixed_page(gpu, oracle):
+    """det 1536^2 + 128 rec lines in width buckets, CTC masked past w/8:
+    det map and every batch's pairs bit-exact with the oracle, and each
+    line's decoded ids equal to the oracle's collapse of the oracle pairs."""
+    from qppocr_amd import pipeline
+    from oracle import nets as onets
+    det_g, det_x, rw, lines, widths = pipeline.mixed_page(4, 1536, 128)
+    print("cfg5 det 1536^2 + 128 lines", flush=True)
+    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths)
+    page.upload()
+    page.run()
+    page.sync()
+    det_ref = onets.run_graph(det_g, det_x)[0]
+    assert_bitexact(page.det_map(), det_ref, "cfg5 det map")
+    got = page.rec_pairs()
+    decoded = page.decode()
+    for bw, idx, g, _, x in page.rec:
+        print(f"cfg5 rec batch {len(idx)}x{bw}", flush=True)
+        _, pairs_ref = onets.run_graph(g, x)
+        for b, i in enumerate(idx):
+            assert (_ids(got[i]) == _ids(pairs_ref[b])).all(), f"line {i}"
+            assert_bitexact(got[i][..., 0], pairs_ref[b][..., 0], f"line {i} values")
+            t_valid = int(widths[i]) // pipeline.REC_STRIDE
+            ref_ids, ref_conf = oracle.ctc_collapse(pairs_ref[b][:t_valid], t_valid)
+            assert decoded[i][0] == [int(v) for v in ref_ids], f"line {i} ids"
+            assert np.float32(decoded[i][1]) == np.float32(ref_conf)
+    page.close()
