@@ -16,7 +16,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqppocr_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["qph_runtime.hip", "qph_gemm.hip", "qph_conv.hip", "qph_rows.hip", "qph_net.hip"]
+SOURCES = ["qph_runtime.hip", "qph_gemm.hip", "qph_conv.hip", "qph_block.hip", "qph_rows.hip",
+           "qph_net.hip"]
 
 CFLAGS = [
     "--offload-arch=gfx950",

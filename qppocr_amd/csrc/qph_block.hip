@@ -1,0 +1,246 @@
+// Fused backbone block: depthwise conv (+ bias + activation) straight into
+// the pointwise 1x1 conv (+ bias + activation), one launch, the depthwise
+// output never written to HBM.
+//
+// Reference: the two Conv nodes of a block (qppocr-core/src/executor.rs:
+// 433-652), each followed by its HardSigmoid + Mul pair (746-758, 885-951):
+// depthwise as conv.rs:461-505 / x86.rs:994-1060 (acc = 0; for ky, kx:
+// acc = fma(w, xpad, acc); y = acc + bias), pointwise as the 1x1 GEMM path
+// conv.rs:264-460 (k = input channel ascending, bias after the chain or
+// seeded by the same placement rule).  Every element keeps those operation
+// sequences; only where the intermediate lives changes.
+//
+// A workgroup owns 16 consecutive output pixels of one output row of one
+// image and a 64-channel slice of M (one 16-channel block per wave).
+// Phase 1: one burst of buffer->LDS loads brings the input halo of those
+// pixels for all C channels (KH rows x (15*sw + KW) columns; out-of-image
+// taps carry an out-of-range offset and read 0, the zero padding) and the
+// k-major weight rows of the slice.  Phase 2: the depthwise outputs of all
+// C channels for the 16 pixels, from the halo, into LDS (t[c][16]).
+// Phase 3: each wave runs the pointwise chain of its 16 channels with
+// v_mfma_f32_16x16x4f32, both operands from LDS.  LDS is sized per launch.
+#include "qph_internal.h"
+
+namespace qph {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define DWPW_MAX_C 256
+#define DWPW_MAX_HALO 16384   // floats of input halo per workgroup (64 KB)
+#define DWPW_MSLICE 64        // output channels per workgroup
+
+struct DwPwK {
+  const float* x;
+  const float* wd;
+  const float* bd;
+  int c, h, w, sh, sw, ph, pw, oh, ow;
+  Act act_d;
+  const float* wk;   // pointwise weights, k-major [cpad][mpad], zero-padded
+  const float* bp;
+  int m, mpad, cpad, seed_rule;
+  Act act_p;
+  float* y;
+  int trans_out;
+  int ct;            // halo columns: 15 * sw + kw
+  int tiles_x;       // 16-pixel tiles per output row
+  int slices;        // 64-channel slices of M
+  int halo, wrows;   // LDS floats of the halo and of the weight slice
+  int wdl_pad;       // LDS floats of the depthwise weights (rounded to 64)
+  int pcp;           // LDS floats per channel of the halo (KH * ct rounded to 64)
+};
+
+template <int KH, int KW>
+__global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
+  extern __shared__ float lds[];
+  float* halo = lds;                 // [c][KH][ct]
+  float* wsl = lds + p.halo;         // [cpad][64]
+  float* t = wsl + p.wrows;          // [cpad][16]
+  float* wdl = t + p.cpad * 16;      // depthwise weights [c][KH*KW], then bias [c]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int img = blockIdx.z;
+  const int slice = blockIdx.y;
+  const int oy = blockIdx.x / p.tiles_x;
+  const int ox0 = (blockIdx.x - oy * p.tiles_x) * 16;
+  const int64_t plane = (int64_t)p.h * p.w;
+  const unsigned OOB = 0x80000000u;
+
+  // phase 1: halo and weight slice, all loads in flight at once
+  {
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.x + (int64_t)img * p.c * plane), 0, (int)(p.c * plane * 4), 0x00020000);
+    // lane -> a fixed (row, column) of a channel's halo (one or two loads
+    // per channel); the channel moves the scalar offset only, so the loop
+    // issues no vector instructions.  Out-of-image taps keep an
+    // out-of-range vector offset (read 0) whatever the scalar offset.
+    const int iy0 = oy * p.sh - p.ph, ix0 = ox0 * p.sw - p.pw;
+    const int per_c = KH * p.ct;
+    unsigned voff[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int q = 64 * j + lane;
+      const int r = q / p.ct, col = q - r * p.ct;
+      const int iy = iy0 + r, ix = ix0 + col;
+      const bool ok = q < per_c && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+      voff[j] = ok ? (unsigned)((iy * p.w + ix) * 4) : OOB;
+    }
+    for (int ci = wave; ci < p.c; ci += 4) {
+      const int soff = (int)(ci * plane * 4);
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        if (64 * j < per_c)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              xr, (__attribute__((address_space(3))) void*)(halo + ci * p.pcp + 64 * j), 4,
+              voff[j], soff, 0, 0);
+    }
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.wk, 0, p.cpad * p.mpad * 4, 0x00020000);
+    const int m0 = slice * DWPW_MSLICE;
+    const unsigned woff = m0 + lane < p.mpad ? (unsigned)((m0 + lane) * 4) : OOB;
+    for (int k = wave; k < p.cpad; k += 4)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wr, (__attribute__((address_space(3))) void*)(wsl + k * 64), 4, woff,
+          k * p.mpad * 4, 0, 0);
+    // depthwise weights and bias (contiguous [c][KH*KW] and [c])
+    const int nwd = p.c * KH * KW;
+    const __amdgpu_buffer_rsrc_t dwr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.wd, 0, nwd * 4, 0x00020000);
+    for (int base = wave * 64; base < nwd; base += 256)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          dwr, (__attribute__((address_space(3))) void*)(wdl + base), 4, (unsigned)lane * 4u,
+          base * 4, 0, 0);
+    if (p.bd) {
+      const __amdgpu_buffer_rsrc_t br =
+          __builtin_amdgcn_make_buffer_rsrc((void*)p.bd, 0, p.c * 4, 0x00020000);
+      for (int base = wave * 64; base < p.c; base += 256)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            br, (__attribute__((address_space(3))) void*)(wdl + p.wdl_pad + base), 4,
+            (unsigned)lane * 4u, base * 4, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // phase 2: depthwise outputs of every channel for the 16 pixels
+  const int npx = p.oh * p.ow;
+  for (int e = tid; e < p.cpad * 16; e += 256) {
+    const int ci = e >> 4, pi = e & 15;
+    float v = 0.0f;
+    if (ci < p.c && ox0 + pi < p.ow) {
+      const float* hp = halo + ci * p.pcp + pi * p.sw;
+      const float* wp = wdl + ci * KH * KW;
+      float acc = 0.0f;
+#pragma unroll
+      for (int ky = 0; ky < KH; ky++)
+#pragma unroll
+        for (int kx = 0; kx < KW; kx++)
+          acc = __builtin_fmaf(wp[ky * KW + kx], hp[ky * p.ct + kx], acc);
+      v = acc + (p.bd ? wdl[p.wdl_pad + ci] : 0.0f);
+      v = act_apply(v, p.act_d);
+    }
+    t[e] = v;
+  }
+  __syncthreads();
+
+  // phase 3: pointwise chain of this wave's 16 channels
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int mb = slice * 4 + wave;            // 16-channel block index
+  if (mb * 16 >= p.m) return;
+  const int px = oy * p.ow + ox0 + l16;
+  const bool pok = ox0 + l16 < p.ow;
+  f32x4 acc;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mb * 16 + 4 * lg + v;
+    float s0 = 0.0f;
+    if (p.bp && mo < p.m && pok && bias_seeded(p.seed_rule, mo, px, p.m, npx)) s0 = p.bp[mo];
+    acc[v] = s0;
+  }
+  const float* al = wsl + lg * 64 + wave * 16 + l16;
+  const float* bl = t + lg * 16 + l16;
+  const int nsteps = p.cpad >> 2;
+  int s = 0;
+  for (; s + 4 <= nsteps; s += 4) {
+    float av[4], bv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      av[u] = al[(s + u) * 256];
+      bv[u] = bl[(s + u) * 64];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u], acc, 0, 0, 0);
+  }
+  for (; s < nsteps; s++)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(al[s * 256], bl[s * 64], acc, 0, 0, 0);
+
+  // epilogue: bias terms first, then finish and store
+  float badd[4];
+  bool hadd[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mb * 16 + 4 * lg + v;
+    hadd[v] = p.bp && mo < p.m && pok && !bias_seeded(p.seed_rule, mo, px, p.m, npx);
+    badd[v] = hadd[v] ? p.bp[mo] : 0.0f;
+  }
+  if (!pok) return;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mb * 16 + 4 * lg + v;
+    if (mo >= p.m) continue;
+    float r = acc[v];
+    if (hadd[v]) r = r + badd[v];
+    r = act_apply(r, p.act_p);
+    if (p.trans_out)
+      p.y[((int64_t)img * npx + px) * p.m + mo] = r;
+    else
+      p.y[((int64_t)img * p.m + mo) * npx + px] = r;
+  }
+}
+
+// halo per channel: KH rows of 15 * sw + KW columns, in one or two loads
+static int halo_per_c(const DwPwArgs& a) { return (int)(a.kh * (15 * a.sw + a.kw)); }
+static int halo_floats(const DwPwArgs& a) {
+  return (int)(a.c * ((halo_per_c(a) + 63) / 64 * 64));
+}
+
+bool dwpw_eligible(const DwPwArgs& a) {
+  return ((a.kh == 3 && a.kw == 3) || (a.kh == 5 && a.kw == 5)) && a.c > 0 &&
+         a.c <= DWPW_MAX_C && a.m > 0 && a.n <= 65535 && a.sw <= 4 && halo_per_c(a) <= 128 &&
+         halo_floats(a) <= DWPW_MAX_HALO && a.c * a.h * a.w * 4 < (int64_t)0x80000000 &&
+         a.oh * a.ow < (1ll << 30) && (a.m + 31) / 32 * 32 * ((a.c + 3) / 4 * 4) * 4 < (1ll << 31);
+}
+
+int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
+  if (!dwpw_eligible(a) || !a.wk) return fail(QPH_EUNSUPPORTED, "dw+pw block: unsupported shape");
+  DwPwK p{};
+  p.x = a.x; p.wd = a.wd; p.bd = a.bd;
+  p.c = (int)a.c; p.h = (int)a.h; p.w = (int)a.w; p.sh = (int)a.sh; p.sw = (int)a.sw;
+  p.ph = (int)a.ph; p.pw = (int)a.pw; p.oh = (int)a.oh; p.ow = (int)a.ow;
+  p.act_d = a.act_d;
+  p.wk = a.wk; p.bp = a.bp;
+  p.m = (int)a.m; p.mpad = (int)((a.m + 31) / 32 * 32); p.cpad = (int)((a.c + 3) / 4 * 4);
+  p.seed_rule = a.seed_rule;
+  p.act_p = a.act_p;
+  p.y = a.y; p.trans_out = a.trans_out;
+  p.ct = (int)(15 * a.sw + a.kw);
+  p.tiles_x = (int)ceil_div(a.ow, 16);
+  p.slices = (int)ceil_div(a.m, DWPW_MSLICE);
+  p.pcp = (halo_per_c(a) + 63) / 64 * 64;
+  p.halo = halo_floats(a);
+  p.wrows = p.cpad * 64;
+  p.wdl_pad = (int)((a.c * a.kh * a.kw + 63) / 64 * 64);
+  const size_t lds =
+      (size_t)(p.halo + p.wrows + p.cpad * 16 + p.wdl_pad + (a.c + 63) / 64 * 64) * 4;
+  const int64_t tiles = (int64_t)p.tiles_x * a.oh;
+  if (tiles >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "dw+pw block: grid too large");
+  dim3 grid((unsigned)tiles, (unsigned)p.slices, (unsigned)a.n);
+  const void* fn = a.kh == 3 ? (const void*)dwpw_kernel<3, 3> : (const void*)dwpw_kernel<5, 5>;
+  QPH_TRY_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  if (a.kh == 3)
+    hipLaunchKernelGGL((dwpw_kernel<3, 3>), grid, dim3(256), lds, s, p);
+  else
+    hipLaunchKernelGGL((dwpw_kernel<5, 5>), grid, dim3(256), lds, s, p);
+  return launch_check("dwpw_kernel");
+}
+
+}  // namespace qph

@@ -22,15 +22,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define GEMM_BK 16
 
-// Reference bias placement (gemm.rs:7-16): rule 0 (panel kernel): seeded
-// when row is in the M%4 tail and the 32-column panel is partial; rule 1
-// (m-rows kernel): seeded for columns j >= n - n%32.
-__device__ __forceinline__ bool bias_seeded(int rule, int64_t i, int64_t j, int64_t m, int64_t n) {
-  if (rule == 1) return j >= n - n % 32;
-  int64_t n0 = (j >> 5) << 5;
-  return (n - n0) < 32 && i >= m - m % 4;
-}
-
 // Epilogue in two phases: every operand the outputs need (bias, residual)
 // is loaded first, then the values are finished and stored.  The stores to C
 // may alias those operands as far as the compiler knows, so interleaving

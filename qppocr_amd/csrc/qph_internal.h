@@ -166,6 +166,15 @@ struct GemmArgs {
 };
 int launch_gemm(const GemmArgs& g, hipStream_t s);
 
+// Reference bias placement (gemm.rs:7-16): rule 0 (panel kernel): seeded
+// when row is in the M%4 tail and the 32-column panel is partial; rule 1
+// (m-rows kernel): seeded for columns j >= n - n%32.
+__device__ __forceinline__ bool bias_seeded(int rule, int64_t i, int64_t j, int64_t m, int64_t n) {
+  if (rule == 1) return j >= n - n % 32;
+  int64_t n0 = (j >> 5) << 5;
+  return (n - n0) < 32 && i >= m - m % 4;
+}
+
 struct ConvArgs {
   const float* x; int64_t n, c, h, w;
   const float* wt;     // ONNX layout [M][C/g][kh][kw]
@@ -186,6 +195,22 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
                   const qph_conv_params* p, const qph_act* act, const qph_conv_epilogue* ep,
                   float* y, ConvArgs* plan = nullptr);
 int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk);
+// Depthwise conv (+ bias + act) feeding a 1x1 conv (+ bias + act) in one
+// kernel; wk = the 1x1 weights repacked k-major [ceil(C/4)*4][ceil(M/32)*32].
+struct DwPwArgs {
+  const float* x; int64_t n, c, h, w;
+  const float* wd; const float* bd;
+  int64_t kh, kw, sh, sw, ph, pw, oh, ow;
+  Act act_d;
+  const float* wk; const float* bp;
+  int64_t m;
+  int seed_rule;
+  Act act_p;
+  int trans_out;
+  float* y;
+};
+bool dwpw_eligible(const DwPwArgs& a);
+int launch_dwpw(const DwPwArgs& a, hipStream_t s);
 // 3x3 convs the direct kernel takes; up to four independent ones in one launch
 bool direct3x3_eligible(const ConvArgs& a);
 int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s);

@@ -21,6 +21,8 @@ struct qph_net {
   std::vector<float*> wk;        // per node: resident repacked dense-conv weights (or NULL)
   std::vector<ConvArgs> plan;    // per node: launch arguments of a dense 3x3 conv
   std::vector<int> group_len;    // > 1: first of that many independent 3x3 convs, one launch
+  std::vector<DwPwArgs> dwpw;    // per node: fused depthwise + pointwise launch
+  std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1 with it)
   std::vector<float*> tptr;      // per tensor device pointer
   char* arena;
   size_t arena_bytes;
@@ -164,6 +166,64 @@ static void plan_conv_groups(qph_net* net) {
   }
 }
 
+// Depthwise conv node i feeding 1x1 conv node i + 1 (the backbone blocks):
+// one launch, the depthwise output kept on chip.  Needs plain outputs (the
+// 1x1 may store transposed), no residuals, and no other reader of the
+// intermediate tensor.  The 1x1 weights are repacked k-major here.
+static int plan_dwpw(qph_net* net) {
+  const size_t nn = net->nodes.size();
+  net->dwpw.assign(nn, DwPwArgs{});
+  net->fused.assign(nn, false);
+  std::vector<int> readers(net->tptr.size(), 0);
+  for (const qph_node& n : net->nodes) {
+    readers[(size_t)storage_of(net, n.in)]++;
+    if (n.in2 >= 0) readers[(size_t)storage_of(net, n.in2)]++;
+  }
+  for (int32_t o : net->outputs) readers[(size_t)storage_of(net, o)]++;
+  for (size_t i = 0; i + 1 < nn; i++) {
+    if (i > 0 && net->fused[i - 1]) continue;
+    const qph_node& d = net->nodes[i];
+    const qph_node& q = net->nodes[i + 1];
+    if (d.op != QPH_OP_CONV || q.op != QPH_OP_CONV) continue;
+    const int64_t* xs = &net->shapes[4 * (size_t)d.in];
+    const bool dw = d.cp.group > 1 && d.ws[1] == 1 && d.ws[0] == xs[1] && d.cp.group == xs[1] &&
+                    d.in2 < 0 && d.res_up == 0 && d.trans_out == 0 &&
+                    (d.y_ctotal == 0 || d.y_ctotal == d.ws[0]) && d.y_coff == 0 && d.y_up <= 1;
+    const bool pw = q.cp.group == 1 && q.ws[2] == 1 && q.ws[3] == 1 && q.cp.sh == 1 &&
+                    q.cp.sw == 1 && q.cp.ph == 0 && q.cp.pw == 0 && q.cp.peh == 0 &&
+                    q.cp.pew == 0 && q.in2 < 0 && q.res_up == 0 &&
+                    (q.y_ctotal == 0 || q.y_ctotal == q.ws[0]) && q.y_coff == 0 && q.y_up <= 1;
+    if (!dw || !pw || q.in != d.out || q.ws[1] != d.ws[0]) continue;
+    if (storage_of(net, d.out) != d.out || readers[(size_t)d.out] != 1) continue;
+    int64_t ys[4];
+    if (qph_conv2d_out_shape(xs, d.ws, &d.cp, ys) != QPH_OK) continue;
+    DwPwArgs f{};
+    f.x = net->tptr[d.in]; f.n = xs[0]; f.c = xs[1]; f.h = xs[2]; f.w = xs[3];
+    f.wd = net->weights[d.w]; f.bd = d.bias >= 0 ? net->weights[d.bias] : nullptr;
+    f.kh = d.ws[2]; f.kw = d.ws[3]; f.sh = d.cp.sh; f.sw = d.cp.sw; f.ph = d.cp.ph; f.pw = d.cp.pw;
+    f.oh = ys[2]; f.ow = ys[3];
+    f.act_d = make_act(&d.act);
+    f.bp = q.bias >= 0 ? net->weights[q.bias] : nullptr;
+    f.m = q.ws[0];
+    // the 1x1 path's bias-placement rule (as conv_dispatch picks it)
+    const double fl = (double)f.m * (double)(f.oh * f.ow) * (double)f.c;
+    f.seed_rule = (f.n > 1 || fl < 2e5 || (f.oh * f.ow + 31) / 32 >= 2) ? 0 : 1;
+    f.act_p = make_act(&q.act);
+    f.trans_out = q.trans_out;
+    f.y = net->tptr[q.out];
+    if (!dwpw_eligible(f)) continue;
+    float* wk = nullptr;
+    QPH_TRY(hip_check(hipMalloc((void**)&wk, (size_t)dense_conv_wk_floats(f.m, f.c, 1, 1) * 4),
+                      "hipMalloc(repacked 1x1 weight)"));
+    net->wk[i + 1] = wk;
+    QPH_TRY(launch_repack_conv_w_taps(net->weights[q.w], f.m, f.c, 1, wk, net->ctx->stream));
+    f.wk = wk;
+    net->dwpw[i] = f;
+    net->fused[i] = true;
+  }
+  return QPH_OK;
+}
+
 static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t nw) {
   const qph_node& n = net->nodes[i];
   QPH_TRY(check_tensor(net, n.in, false, i, n, "input"));
@@ -262,6 +322,31 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
     default:
       return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unsupported op");
   }
+}
+
+// Every node in order, fused launches where planned.  With profiling on,
+// an event precedes each node; the nodes a fused launch covers after its
+// first get their events right after it (so their time reads 0).
+static int run_all(qph_net* net) {
+  hipStream_t s = net->ctx->stream;
+  const size_t nn = net->nodes.size();
+  for (size_t i = 0; i < nn;) {
+    if (net->profiling) QPH_TRY_HIP(hipEventRecord(net->ev[i], s));
+    size_t step = 1;
+    if (net->group_len[i] > 1) {
+      QPH_TRY(launch_dense_conv_group(&net->plan[i], net->group_len[i], s));
+      step = (size_t)net->group_len[i];
+    } else if (net->fused[i]) {
+      QPH_TRY(launch_dwpw(net->dwpw[i], s));
+      step = 2;
+    } else {
+      QPH_TRY(run_node(net, i));
+    }
+    if (net->profiling)
+      for (size_t k = i + 1; k < i + step; k++) QPH_TRY_HIP(hipEventRecord(net->ev[k], s));
+    i += step;
+  }
+  return QPH_OK;
 }
 
 static void release(qph_net* net) {
@@ -384,6 +469,8 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     }
   }
   plan_conv_groups(net);
+  rc = plan_dwpw(net);
+  if (rc) return bail(rc);
   rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   if (rc) return bail(rc);
   *out = net;
@@ -432,10 +519,7 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
                                input_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
   }
   if (net->profiling) {
-    for (size_t i = 0; i < net->nodes.size(); i++) {
-      QPH_TRY_HIP(hipEventRecord(net->ev[i], s));
-      QPH_TRY(run_node(net, i));
-    }
+    QPH_TRY(run_all(net));
     QPH_TRY_HIP(hipEventRecord(net->ev[net->nodes.size()], s));
     QPH_TRY_HIP(hipEventSynchronize(net->ev[net->nodes.size()]));
     for (size_t i = 0; i < net->nodes.size(); i++) {
@@ -447,15 +531,7 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
   } else {
     if (!net->graph_ready) {
       QPH_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      int rc = QPH_OK;
-      for (size_t i = 0; i < net->nodes.size() && rc == QPH_OK;) {
-        if (net->group_len[i] > 1) {
-          rc = launch_dense_conv_group(&net->plan[i], net->group_len[i], s);
-          i += (size_t)net->group_len[i];
-        } else {
-          rc = run_node(net, i++);
-        }
-      }
+      int rc = run_all(net);
       hipGraph_t g = nullptr;
       hipError_t e = hipStreamEndCapture(s, &g);
       if (rc != QPH_OK) {

@@ -108,3 +108,39 @@ def test_cfg5_mixed_page(gpu, oracle):
             assert decoded[i][0] == [int(v) for v in ref_ids], f"line {i} ids"
             assert np.float32(decoded[i][1]) == np.float32(ref_conf)
     page.close()
+
+
+def test_session_fusion_rules(gpu, oracle):
+    """The session fuses a depthwise conv into the following 1x1 conv only
+    when nothing else reads the intermediate: here one block's intermediate
+    is also a graph output (kept separate), the next block is fused, and
+    four independent 3x3 convs share one launch; everything bit-exact."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    r = nets.WeightRng(11)
+    g = nets.Graph((2, 16, 24, 40))
+    wd = g.weight(r.kaiming((16, 1, 3, 3), 9))
+    bd = g.weight(r.normal((16,), 0.1))
+    t1 = g.conv(0, wd, bd, pad=(1, 1, 1, 1), group=16, act=nets.ACT_HARDSWISH)
+    wp = g.weight(r.kaiming((32, 16, 1, 1), 16))
+    bp = g.weight(r.normal((32,), 0.1))
+    y1 = g.conv(t1, wp, bp, act=nets.ACT_HARDSWISH)
+    wd2 = g.weight(r.kaiming((32, 1, 5, 5), 25))
+    bd2 = g.weight(r.normal((32,), 0.1))
+    t2 = g.conv(y1, wd2, bd2, stride=(2, 2), pad=(2, 2, 2, 2), group=32, act=nets.ACT_HARDSWISH)
+    wp2 = g.weight(r.kaiming((48, 32, 1, 1), 32))
+    bp2 = g.weight(r.normal((48,), 0.1))
+    y2 = g.conv(t2, wp2, bp2, act=nets.ACT_HARDSWISH)
+    outs = [t1, y2]
+    for k in range(4):
+        w3 = g.weight(r.kaiming((8, 48, 3, 3), 48 * 9))
+        b3 = g.weight(r.normal((8,), 0.1))
+        outs.append(g.conv(y2, w3, b3, pad=(1, 1, 1, 1), act=nets.ACT_RELU))
+    g.outputs = outs
+    x = r.normal((2, 16, 24, 40), 1.0)
+    sess = nets.HipSession(g)
+    got = sess.run(x)
+    ref = onets.run_graph(g, x)
+    for i, (a, b) in enumerate(zip(got, ref)):
+        assert_bitexact(a, b, f"output {i}")
+    sess.close()
