@@ -107,15 +107,15 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         __builtin_amdgcn_make_buffer_rsrc((void*)p.wd, 0, nwd * 4, 0x00020000);
     for (int base = wave * 64; base < nwd; base += 256)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          dwr, (__attribute__((address_space(3))) void*)(wdl + base), 4, (unsigned)lane * 4u,
-          base * 4, 0, 0);
+          dwr, (__attribute__((address_space(3))) void*)(wdl + base), 4,
+          (unsigned)(base + lane) * 4u, 0, 0, 0);
     if (p.bd) {
       const __amdgpu_buffer_rsrc_t br =
           __builtin_amdgcn_make_buffer_rsrc((void*)p.bd, 0, p.c * 4, 0x00020000);
       for (int base = wave * 64; base < p.c; base += 256)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             br, (__attribute__((address_space(3))) void*)(wdl + p.wdl_pad + base), 4,
-            (unsigned)lane * 4u, base * 4, 0, 0);
+            (unsigned)(base + lane) * 4u, 0, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();

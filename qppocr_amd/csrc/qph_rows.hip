@@ -1,8 +1,12 @@
 // Row kernels of the rec model: LayerNorm, softmax (+ argmax), multi-head
 // attention; and the small elementwise / layout kernels.
+#include <algorithm>
+
 #include "qph_internal.h"
 
 namespace qph {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -254,20 +258,185 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, 
   }
 }
 
-int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s) {
+// Rows of up to 20480 floats (the rec head, 18709): each of the 512 threads
+// keeps its elements (i = tid + 512 u) in registers, so the row is read from
+// HBM once and the probabilities written once, and a workgroup needs only a
+// small LDS window: several rows are resident per CU.  The eight lane chains
+// run in lanes 0-7 of wave 0 over windows of 2048 elements that all threads
+// write transposed (element j + 8t of the window at j * 264 + t: one
+// ds_read_b128 gives a chain lane four of its terms, and a wave's writes hit
+// 64 distinct banks), double-buffered so the chains of one window overlap
+// the writes of the next.  Same operation sequence as above.
+#define SM_REG_MAX_COLS 20480
+#define SM_REG_PER_THREAD 40     // SM_REG_MAX_COLS / 512
+#define SM_WIN 2048              // elements per chain window (4 per thread)
+#define SM_WIN_PITCH 264         // floats per chain lane in a window (8 mod 64)
+
+__device__ __forceinline__ float block_max_512(float v, float* red) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < 8; i++) r = fmaxf(r, red[i]);
+  return r;
+}
+
+__global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, int cols,
+                                                          float* probs, float* pairs) {
+  __shared__ __attribute__((aligned(16))) float win[2][8 * SM_WIN_PITCH];
+  __shared__ float part[16];
+  __shared__ float red[8];
+  __shared__ int redi[8];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t row = blockIdx.x;
+  const int nu = (cols - tid + 511) >> 9;   // this thread's elements: u < nu
+  // row to registers (out-of-range reads give 0 and are never used)
+  float e[SM_REG_PER_THREAD];
+  {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(logits + row * cols), 0, cols * 4, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < SM_REG_PER_THREAD; u++)
+      e[u] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(r, (unsigned)(tid + 512 * u) * 4u, 0, 0));
+  }
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < SM_REG_PER_THREAD; u++) mx = u < nu ? fmaxf(mx, e[u]) : mx;
+  mx = block_max_512(mx, red);
+#pragma unroll
+  for (int u = 0; u < SM_REG_PER_THREAD; u++) e[u] = exp1(e[u] - mx);
+
+  const int full = cols >= 8 ? (cols / 8) * 8 : 0;
+  const int t8 = full / 8;
+  const int nwin = (full + SM_WIN - 1) / SM_WIN;
+  // window w holds elements [w * 2048, w * 2048 + 2048) of the full part:
+  // this thread's u = 4w .. 4w + 3
+  auto put = [&](int w) {
+    float* b = win[w & 1];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+      for (int u = 0; u < SM_REG_PER_THREAD; u++) {
+        if (u != 4 * w + q) continue;
+        const int il = tid + 512 * q;      // index inside the window
+        if (w * SM_WIN + il < full) b[(il & 7) * SM_WIN_PITCH + (il >> 3)] = e[u];
+      }
+    }
+  };
+  float s = 0.0f;   // chain of lane j = lane (lanes 0-7 of wave 0)
+  if (nwin > 0) put(0);
+  __syncthreads();
+  for (int w = 0; w < nwin; w++) {
+    if (w + 1 < nwin) put(w + 1);
+    if (wave == 0 && lane < 8) {
+      const float* ej = win[w & 1] + lane * SM_WIN_PITCH;
+      const int nt = min(t8 - w * (SM_WIN / 8), SM_WIN / 8);   // terms in this window
+      int t = 0;
+      for (; t + 32 <= nt; t += 32) {
+        f32x4 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = *(const f32x4*)(ej + t + 4 * q);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          s = s + v[q][0];
+          s = s + v[q][1];
+          s = s + v[q][2];
+          s = s + v[q][3];
+        }
+      }
+      for (; t < nt; t++) s = s + ej[t];
+    }
+    __syncthreads();
+  }
+  // tail elements (full <= i < cols) to LDS for the in-order tail sum
+#pragma unroll
+  for (int u = 0; u < SM_REG_PER_THREAD; u++) {
+    const int i = tid + 512 * u;
+    if (i >= full && u < nu) win[0][i - full] = e[u];
+  }
+  if (wave == 0 && lane < 8) part[lane] = s;
+  __syncthreads();
+  if (tid == 0) {
+    float sum;
+    if (cols >= 8) {
+      float a0 = part[0] + part[4], a1 = part[1] + part[5], a2 = part[2] + part[6],
+            a3 = part[3] + part[7];
+      sum = (a0 + a1) + (a2 + a3);
+    } else {
+      sum = 0.0f;
+    }
+    for (int i = 0; i < cols - full; i++) sum = sum + win[0][i];   // tail, in order
+    part[8] = sum;
+  }
+  __syncthreads();
+  const float inv = 1.0f / part[8];
+  float* pr = probs + row * cols;
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < SM_REG_PER_THREAD; u++) {
+    if (u < nu) {
+      const int i = tid + 512 * u;
+      const float p = e[u] * inv;
+      pr[i] = p;
+      if (p > bv) {  // ascending i per thread: keeps the first strict max
+        bv = p;
+        bi = i;
+      }
+    }
+  }
+  if (!pairs) return;
+  for (int off = 32; off >= 1; off >>= 1) {
+    float ov = __shfl_xor(bv, off, 64);
+    int oi = __shfl_xor(bi, off, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    red[wave] = bv;
+    redi[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float v = red[0];
+    int ix = redi[0];
+    for (int w = 1; w < 8; w++)
+      if (red[w] > v || (red[w] == v && redi[w] < ix)) {
+        v = red[w];
+        ix = redi[w];
+      }
+    pairs[2 * row] = v;
+    pairs[2 * row + 1] = __uint_as_float((unsigned)ix);
+  }
+}
+
+static int launch_softmax(const float* logits, int64_t rows, int64_t cols, float* probs,
+                          float* pairs, hipStream_t s) {
   if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
-  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, t, cols, t,
-                     (float*)nullptr);
+  if (cols <= SM_REG_MAX_COLS) {
+    hipLaunchKernelGGL(softmax_reg_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
+                       (int)cols, probs, pairs);
+    return launch_check("softmax_reg_kernel");
+  }
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols,
+                     probs, pairs);
   return launch_check("softmax_rows_kernel");
+}
+
+int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s) {
+  return launch_softmax(t, rows, cols, t, nullptr, s);
 }
 
 int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, float* probs,
                           float* pairs, hipStream_t s) {
   if (!probs) return fail(QPH_EINVAL, "softmax_argmax: probs buffer required");
-  if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
-  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols,
-                     probs, pairs);
-  return launch_check("softmax_rows_kernel");
+  return launch_softmax(logits, rows, cols, probs, pairs, s);
 }
 
 // argmax over probabilities: first strict max (rec.rs:46-54).
