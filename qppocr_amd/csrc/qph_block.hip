@@ -235,7 +235,7 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
   if (tiles >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "dw+pw block: grid too large");
   dim3 grid((unsigned)tiles, (unsigned)p.slices, (unsigned)a.n);
   const void* fn = a.kh == 3 ? (const void*)dwpw_kernel<3, 3> : (const void*)dwpw_kernel<5, 5>;
-  QPH_TRY_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  QPH_TRY(allow_full_lds(fn));
   if (a.kh == 3)
     hipLaunchKernelGGL((dwpw_kernel<3, 3>), grid, dim3(256), lds, s, p);
   else

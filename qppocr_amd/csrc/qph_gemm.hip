@@ -201,16 +201,18 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 // workgroup owns 32x32 outputs, each wave one 16x16 block accumulated with
 // v_mfma_f32_16x16x4f32 (4 k per instruction in order), so a K-deep chain
 // takes K/4 dependent MFMAs and the grid has M*N/256 waves.  K advances in
-// slabs of 64 through double-buffered LDS; A is staged row-major (stride
-// 66: a 16-row x 2-k read hits 32 distinct banks), B row-major (stride 48).
+// slabs of 64 through double-buffered LDS.  A is staged k-deinterleaved,
+// [m][g][s] with k = 4s + g (row pitch 68), so a lane's 16 k-steps of a
+// slab are four ds_read_b128; B row-major (stride 48).  All of a slab's
+// operand reads are issued before its 16 MFMAs.
 
 #define SK_BK 64
-#define SK_PA (SK_BK + 2)
+#define SK_PA 68
 #define SK_PB 48
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
-  __shared__ float sA[2][32 * SK_PA];
+  __shared__ __attribute__((aligned(16))) float sA[2][32 * SK_PA];
   __shared__ float sB[2][SK_BK * SK_PB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lg = lane >> 4, l16 = lane & 15;
@@ -251,7 +253,10 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) sA[buf][ar * SK_PA + ak + u] = ra[u];
+    for (int u = 0; u < 8; u++) {
+      const int k = ak + u;
+      sA[buf][ar * SK_PA + (k & 3) * 16 + (k >> 2)] = ra[u];
+    }
 #pragma unroll
     for (int u = 0; u < 8; u++) sB[buf][br * SK_PB + bc + u] = rb[u];
   };
@@ -276,11 +281,17 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
   for (int64_t t = 0; t < nk; t++) {
     const int buf = (int)(t & 1);
     if (t + 1 < nk) load((t + 1) * SK_BK);
-    const float* a_s = sA[buf] + (wm * 16 + l16) * SK_PA + lg;
+    const float* a_s = sA[buf] + (wm * 16 + l16) * SK_PA + lg * 16;
     const float* b_s = sB[buf] + lg * SK_PB + wn * 16 + l16;
+    f32x4 av[4];
+    float bv[16];
 #pragma unroll
-    for (int kk = 0; kk < SK_BK; kk += 4)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a_s[kk], b_s[kk * SK_PB], acc, 0, 0, 0);
+    for (int q = 0; q < 4; q++) av[q] = *(const f32x4*)(a_s + 4 * q);
+#pragma unroll
+    for (int st = 0; st < 16; st++) bv[st] = b_s[4 * st * SK_PB];
+#pragma unroll
+    for (int st = 0; st < 16; st++)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st >> 2][st & 3], bv[st], acc, 0, 0, 0);
     if (t + 1 < nk) store(buf ^ 1);
     __syncthreads();
   }

@@ -209,6 +209,9 @@ struct DwPwArgs {
   int trans_out;
   float* y;
 };
+// Lets kernel fn take up to the whole 160 KB of a CU's LDS as dynamic
+// shared memory; the attribute is set once per kernel and device.
+int allow_full_lds(const void* fn);
 bool dwpw_eligible(const DwPwArgs& a);
 int launch_dwpw(const DwPwArgs& a, hipStream_t s);
 // 3x3 convs the direct kernel takes; up to four independent ones in one launch

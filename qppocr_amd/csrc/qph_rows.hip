@@ -599,17 +599,19 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   }
 }
 
-// Head dimension known at compile time: the block of RB query rows is
-// processed by all 256 threads at once.  Scores (RB x T): one chain of DH
-// fmas each; softmax: 16 threads per row (max, exp1 spread over the 16;
-// lanes 0-7 of the group run the eight reference lane chains, then the tree
-// and the tail); P.V (RB x DH): one chain of T fmas each.
-#define ATT_RB 16
+// Head dimension known at compile time: one workgroup per (batch, head);
+// q (times scale: the Mul node), k and v of all T rows arrive in LDS in one
+// burst of loads, then the query rows go in blocks (all rows up to 64).  Scores: one chain of DH fmas per
+// (row, key).  Softmax: eight threads per row, thread j owning elements
+// j, j+8, ... -- its max part, its exp1 values and exactly the reference's
+// lane-j chain -- then the ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree and the
+// tail in order within the group of eight (no workgroup barrier).  P.V:
+// one chain of T fmas per (row, d).
 
 template <int DH>
 __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restrict__ qkv,
                                                            int64_t T, int64_t H, float scale,
-                                                           float* __restrict__ out) {
+                                                           int blk, float* __restrict__ out) {
   extern __shared__ float sm[];
   constexpr int LD = DH + 1;
   const int64_t b = blockIdx.x / H, h = blockIdx.x - b * H;
@@ -617,30 +619,42 @@ __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restri
   const int64_t D = H * DH;
   const int t = (int)T;
   const int ldp = t + 1;
-  float* sk = sm;                 // T x LD
+  float* sq = sm;                 // T x LD (scaled q)
+  float* sk = sq + t * LD;        // T x LD
   float* sv = sk + t * LD;        // T x LD
-  float* sq = sv + t * LD;        // RB x LD (scaled q of the block)
-  float* sp = sq + ATT_RB * LD;   // RB x (T+1) scores / probabilities
-  float* ssum = sp + ATT_RB * ldp;  // RB x 16 (lane partials, inv)
+  float* sp = sv + t * LD;        // blk x (T+1) scores / probabilities
   const float* base = qkv + b * T * 3 * D + h * DH;
-  for (int i = tid; i < t * DH; i += 256) {
-    int r = i / DH, d = i - r * DH;
-    const float* row = base + (int64_t)r * 3 * D + d;
-    sk[r * LD + d] = row[D];
-    sv[r * LD + d] = row[2 * D];
-  }
-  const int g = tid >> 4, u = tid & 15;   // softmax: row g of the block, thread u of 16
-  for (int r0 = 0; r0 < t; r0 += ATT_RB) {
-    const int rb = (t - r0) < ATT_RB ? (t - r0) : ATT_RB;
-    for (int i = tid; i < rb * DH; i += 256) {
-      int r = i / DH, d = i - r * DH;
-      sq[r * LD + d] = base[(int64_t)(r0 + r) * 3 * D + d] * scale;   // Mul node
+  for (int i0 = tid; i0 < t * DH; i0 += 256 * 4) {
+    float q[4], k[4], v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int i = i0 + 256 * u;
+      if (i < t * DH) {
+        const float* row = base + (int64_t)(i / DH) * 3 * D + (i % DH);
+        q[u] = row[0];
+        k[u] = row[D];
+        v[u] = row[2 * D];
+      }
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int i = i0 + 256 * u;
+      if (i < t * DH) {
+        const int r = i / DH, d = i - r * DH;
+        sq[r * LD + d] = q[u] * scale;   // Mul node
+        sk[r * LD + d] = k[u];
+        sv[r * LD + d] = v[u];
+      }
+    }
+  }
+  __syncthreads();
+  const int full = t >= 8 ? (t / 8) * 8 : 0;
+  for (int r0 = 0; r0 < t; r0 += blk) {
+    const int rb = (t - r0) < blk ? (t - r0) : blk;
     // scores S[r][j] = chain over d of fma(q[r][d], k[j][d], acc)
     for (int i = tid; i < rb * t; i += 256) {
-      int r = i / t, j = i - r * t;
-      const float* qr = sq + r * LD;
+      const int r = i / t, j = i - r * t;
+      const float* qr = sq + (r0 + r) * LD;
       const float* kj = sk + j * LD;
       float acc = 0.0f;
 #pragma unroll
@@ -648,75 +662,90 @@ __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restri
       sp[r * ldp + j] = acc;
     }
     __syncthreads();
-    // softmax of row g (reference order), 16 threads per row
-    float mx = -__builtin_inff();
-    const bool rowok = g < rb;
-    float* pr = sp + g * ldp;
-    if (rowok)
-      for (int j = u; j < t; j += 16) mx = fmaxf(mx, pr[j]);
-    for (int off = 8; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
-    if (t < 8 && rowok) {   // narrow rows: sequential max from the first element
-      mx = pr[0];
-      for (int j = 1; j < t; j++)
-        if (pr[j] > mx) mx = pr[j];
-    }
-    __syncthreads();
-    if (rowok)
-      for (int j = u; j < t; j += 16) pr[j] = exp1(pr[j] - mx);
-    __syncthreads();
-    const int full = t >= 8 ? (t / 8) * 8 : 0;
-    if (rowok && u < 8) {
-      float s = 0.0f;
-      for (int j = u; j < full; j += 8) s = s + pr[j];
-      ssum[g * 16 + u] = s;
-    }
-    __syncthreads();
-    if (rowok && u == 0) {
-      const float* l = ssum + g * 16;
-      float sum;
-      if (t >= 8) {
-        float t0 = l[0] + l[4], t1 = l[1] + l[5], t2 = l[2] + l[6], t3 = l[3] + l[7];
-        sum = (t0 + t1) + (t2 + t3);
-      } else {
-        sum = 0.0f;
+    // softmax, eight threads per row (groups never straddle a wave)
+    for (int g0 = 0; g0 < rb; g0 += 32) {
+      const int r = g0 + (tid >> 3), lj = tid & 7;
+      const bool rowok = r < rb;
+      float* pr = sp + (rowok ? r : 0) * ldp;
+      float mx = -__builtin_inff();
+      if (rowok)
+        for (int j = lj; j < t; j += 8) mx = fmaxf(mx, pr[j]);
+      for (int off = 4; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 8));
+      if (t < 8 && rowok) {   // narrow rows: sequential max from the first element
+        mx = pr[0];
+        for (int j = 1; j < t; j++)
+          if (pr[j] > mx) mx = pr[j];
       }
-      for (int j = full; j < t; j++) sum = sum + pr[j];
-      ssum[g * 16 + 8] = 1.0f / sum;
+      float s = 0.0f;
+      if (rowok)
+        for (int j = lj; j < t; j += 8) {
+          const float e = exp1(pr[j] - mx);
+          pr[j] = e;
+          if (j < full) s = s + e;   // lane lj's chain, ascending j
+        }
+      // tree of the eight lane chains, then the tail in order (lane 0)
+      const int gb = (threadIdx.x & 63) & ~7;
+      const float l0 = __shfl(s, gb + 0, 64), l1 = __shfl(s, gb + 1, 64);
+      const float l2 = __shfl(s, gb + 2, 64), l3 = __shfl(s, gb + 3, 64);
+      const float l4 = __shfl(s, gb + 4, 64), l5 = __shfl(s, gb + 5, 64);
+      const float l6 = __shfl(s, gb + 6, 64), l7 = __shfl(s, gb + 7, 64);
+      float sum = 0.0f;
+      if (rowok && lj == 0) {
+        if (t >= 8) sum = ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7));
+        for (int j = full; j < t; j++) sum = sum + pr[j];
+      }
+      sum = __shfl(sum, gb, 64);
+      const float inv = 1.0f / sum;
+      if (rowok)
+        for (int j = lj; j < t; j += 8) pr[j] = pr[j] * inv;
     }
     __syncthreads();
-    if (rowok) {
-      const float inv = ssum[g * 16 + 8];
-      for (int j = u; j < t; j += 16) pr[j] = pr[j] * inv;
-    }
-    __syncthreads();
-    // O[r][d] = chain over j of fma(P[r][j], v[j][d], acc)
+    // O[r][d] = chain over j of fma(P[r][j], v[j][d], acc); operands read
+    // eight j at a time so their LDS reads are in flight together
     for (int i = tid; i < rb * DH; i += 256) {
-      int r = i / DH, d = i - r * DH;
+      const int r = i / DH, d = i - r * DH;
       const float* p = sp + r * ldp;
+      const float* vd = sv + d;
       float acc = 0.0f;
-      for (int j = 0; j < t; j++) acc = __builtin_fmaf(p[j], sv[j * LD + d], acc);
+      int j = 0;
+      for (; j + 8 <= t; j += 8) {
+        float pv[8], vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          pv[u] = p[j + u];
+          vv[u] = vd[(j + u) * LD];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = __builtin_fmaf(pv[u], vv[u], acc);
+      }
+      for (; j < t; j++) acc = __builtin_fmaf(p[j], vd[j * LD], acc);
       out[(b * T + r0 + r) * D + h * DH + d] = acc;
     }
     __syncthreads();
   }
 }
 
-static size_t attention_dh_lds(int64_t t, int64_t dh) {
-  return (size_t)(2 * t * (dh + 1) + ATT_RB * (dh + 1) + ATT_RB * (t + 1) + ATT_RB * 16) *
-         sizeof(float);
+static size_t attention_dh_lds(int64_t t, int64_t dh, int64_t blk) {
+  return (size_t)(3 * t * (dh + 1) + blk * (t + 1)) * sizeof(float);
 }
 
 int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
                      float scale, float* out, hipStream_t s) {
-  if ((dh == 32 || dh == 64) && attention_dh_lds(t, dh) <= 64 * 1024) {
+  // query rows per block: all of them up to 64, else 64 or 32 as LDS allows
+  int64_t blk = t <= 64 ? t : 64;
+  if (attention_dh_lds(t, dh, blk) > 160 * 1024) blk = 32;
+  if ((dh == 32 || dh == 64) && attention_dh_lds(t, dh, blk) <= 160 * 1024) {
     if (batch * heads > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "attention: grid too large");
-    size_t lds = attention_dh_lds(t, dh);
+    const size_t lds = attention_dh_lds(t, dh, blk);
+    const void* fn = dh == 32 ? (const void*)attention_dh_kernel<32>
+                              : (const void*)attention_dh_kernel<64>;
+    QPH_TRY(allow_full_lds(fn));
     if (dh == 32)
       hipLaunchKernelGGL(attention_dh_kernel<32>, dim3((unsigned)(batch * heads)), dim3(256), lds,
-                         s, qkv, t, heads, scale, out);
+                         s, qkv, t, heads, scale, (int)blk, out);
     else
       hipLaunchKernelGGL(attention_dh_kernel<64>, dim3((unsigned)(batch * heads)), dim3(256), lds,
-                         s, qkv, t, heads, scale, out);
+                         s, qkv, t, heads, scale, (int)blk, out);
     return launch_check("attention_dh_kernel");
   }
   return launch_attention_generic(qkv, batch, t, heads, dh, scale, out, s);

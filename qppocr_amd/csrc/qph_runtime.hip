@@ -5,6 +5,10 @@
 #include <cstring>
 #include <string>
 
+#include <mutex>
+#include <set>
+#include <utility>
+
 #include "qph_internal.h"
 
 namespace qph {
@@ -188,6 +192,18 @@ QPH_API int qph_conv2d_out_shape(const int64_t xs[4], const int64_t ws[4],
 }  // extern "C"
 
 namespace qph {
+int allow_full_lds(const void* fn) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  QPH_TRY_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({fn, dev})) return QPH_OK;
+  QPH_TRY_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  done.insert({fn, dev});
+  return QPH_OK;
+}
+
 // Validates a conv node and launches its kernel.  wk: resident k-major
 // repacked weights of a dense conv (NULL: repacked into the context scratch).
 int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,

@@ -344,7 +344,7 @@ def test_layernorm(gpu, oracle):
         assert_bitexact(_n(y), ref, f"layernorm {rows}x{cols}")
 
 
-@pytest.mark.parametrize("t", [40, 20, 5, 160])
+@pytest.mark.parametrize("t", [40, 20, 5, 13, 64, 160])
 def test_attention(gpu, oracle, t):
     torch = gpu
     from qppocr_amd import ops, nets
