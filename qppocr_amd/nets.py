@@ -392,10 +392,12 @@ class HipSession:
     rec graph exports both the probability tensor and the (val, idx) argmax
     pairs (rec_argmax_pairs, device.rs:160-165)."""
 
-    def __init__(self, graph, device=0):
+    def __init__(self, graph, device=0, ctx=None):
+        """ctx: the context (and so the stream) to run on; default: the
+        device's shared context (ops.context)."""
         from . import ops
         self.lib = _lib.load()
-        self.ctx = ops.context(device)
+        self.ctx = ctx if ctx is not None else ops.context(device)
         self.graph = graph
         spec, self._keep = graph.to_c()
         self._spec = spec

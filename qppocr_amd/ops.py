@@ -35,6 +35,20 @@ def context(device=0):
     return _ctx[device]
 
 
+def new_context(device=0):
+    """A further context of a HIP device, with its own stream: sessions on
+    different contexts run concurrently (e.g. det of one page while rec of
+    the previous page).  Destroy it with close_context."""
+    lib = _lib.load()
+    p = ctypes.c_void_p()
+    check(lib.qph_ctx_create(int(device), ctypes.byref(p)))
+    return p
+
+
+def close_context(ctx):
+    check(_lib.load().qph_ctx_destroy(ctx))
+
+
 def _dev(t):
     return t.device.index if t.device.index is not None else torch.cuda.current_device()
 

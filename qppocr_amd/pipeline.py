@@ -67,17 +67,22 @@ def pack_lines(lines, idx, bucket_width):
 class PageRunner:
     """det on one page size plus rec sessions for a fixed set of line
     widths; inputs are uploaded once (resident in HBM), run() replays the
-    det graph and every rec batch graph on one stream."""
+    det graph and every rec batch graph.  contexts (optional): the det runs
+    on contexts[0] and the rec batches round-robin on the others (each
+    context is one stream, so they run concurrently); by default everything
+    runs on the device's shared context."""
 
-    def __init__(self, det_graph, det_input, rec_w, lines, widths, device=0):
-        self.det = HipSession(det_graph, device)
+    def __init__(self, det_graph, det_input, rec_w, lines, widths, device=0, contexts=None):
+        ctxs = list(contexts) if contexts else [None]
+        rec_ctxs = ctxs[1:] or ctxs[:1]
+        self.det = HipSession(det_graph, device, ctx=ctxs[0])
         self.det_input = det_input
         self.widths = np.asarray(widths, dtype=np.int64)
         self.plan = bucket_plan(self.widths)
         self.rec = []
-        for bw, idx in self.plan:
+        for k, (bw, idx) in enumerate(self.plan):
             g = build_rec_graph(rec_w, len(idx), bw, REC_H)
-            sess = HipSession(g, device)
+            sess = HipSession(g, device, ctx=rec_ctxs[k % len(rec_ctxs)])
             self.rec.append((bw, idx, g, sess, pack_lines(lines, idx, bw)))
         self.lib = _lib.load()
 
@@ -103,6 +108,8 @@ class PageRunner:
 
     def sync(self):
         self.det.sync()
+        for _, _, _, sess, _ in self.rec:
+            sess.sync()
 
     def det_map(self):
         g = self.det.graph
@@ -125,6 +132,7 @@ class PageRunner:
                 for p, w in zip(self.rec_pairs(), self.widths)]
 
     def _d2h(self, ptr, n):
+        self.sync()
         host = np.empty(n, dtype=np.float32)
         _lib.check(self.lib.qph_memcpy_d2h(self.det.ctx, host.ctypes.data_as(ctypes.c_void_p),
                                            ctypes.c_void_p(ptr), n * 4))
