@@ -5,6 +5,7 @@ hipcc cross-compiles for gfx950 without a GPU.  Device code is built with
 step matches the CPU path) and f32 denormal flushing (the CPU executor runs
 with FTZ|DAZ).  Packed-fp32 instruction selection is disabled.
 """
+import ctypes
 import os
 import subprocess
 import sys
@@ -54,6 +55,13 @@ def build(verbose=False):
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
+    # every symbol must resolve (a kernel whose host stub was dropped shows
+    # up here, not at the first launch)
+    try:
+        ctypes.CDLL(os.path.abspath(tmp), mode=os.RTLD_NOW)
+    except OSError as e:
+        os.remove(tmp)
+        raise RuntimeError(f"built library does not load: {e}")
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)

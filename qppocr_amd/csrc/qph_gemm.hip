@@ -13,6 +13,8 @@
 // K advances in slabs of 16 staged through LDS (A transposed to [k][m] so a
 // wave's 32 rows at one k are 32 consecutive words), with the next slab's
 // global loads issued before the current slab's MFMAs.
+#include <type_traits>
+
 #include "qph_internal.h"
 
 namespace qph {
@@ -576,20 +578,291 @@ static int launch_wide(const GemmArgs& g, hipStream_t s) {
   return launch_check("gemm_wide_kernel");
 }
 
+// Tile choice: 128x128 tiles when they still yield about two workgroups per
+// CU (256 CUs) for the whole launch, else the 32x32 kernels.
+bool gemm_takes_wide(int64_t m, int64_t n, int64_t batch) {
+  const double tiles = (double)ceil_div(m, 128) * (double)ceil_div(n, 128) * (double)batch;
+  return m >= 128 && n >= 128 && tiles >= 512;
+}
+
 int launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (g.m <= 0 || g.n <= 0 || g.k <= 0 || g.batch <= 0) return QPH_OK;
   if (g.m > (1ll << 31) || g.n > (1ll << 31) || g.batch > 65535)
     return fail(QPH_EUNSUPPORTED, "gemm: dimension too large");
-  // Tile choice: the largest tile that still yields about two workgroups
-  // per CU (256 CUs) for the whole launch.
-  auto tiles = [&](int bm, int bn) {
-    return (double)ceil_div(g.m, bm) * (double)ceil_div(g.n, bn) * (double)g.batch;
-  };
-  if (g.m >= 128 && g.n >= 128 && tiles(128, 128) >= 512) {
-    if (wide_fits(g) && tiles(128, 128) < (1u << 30)) return launch_wide(g, s);
+  if (gemm_takes_wide(g.m, g.n, g.batch)) {
+    const double tiles = (double)ceil_div(g.m, 128) * (double)ceil_div(g.n, 128) * (double)g.batch;
+    if (wide_fits(g) && tiles < (double)(1u << 30)) return launch_wide(g, s);
     return launch_cfg<2, 2>(g, s);
   }
   return launch_skinny(g, s);
+}
+
+// ------------------------------------------------- linears, resident W^T
+//
+// The session's linears below the 128x128 size (the rec QKV, projection and
+// MLP, 1280 x {256..1024} x {256, 1024}) keep their weight transposed,
+// Wt[N][K], so both operands are k-contiguous rows.  A workgroup owns TM x TN
+// outputs (TM, TN in {32, 64}) as 2 x 2 waves; a wave holds
+// (TM/32) x (TN/32) 16x16 blocks, each accumulated with v_mfma_f32_16x16x4f32
+// (four k per instruction, in order), so a K-deep output is K/4 dependent
+// MFMAs and a wave interleaves the chains of its blocks.  On these shapes
+// the cost is the MFMA chains plus the operand traffic from L2, which the
+// tile shape trades against each other (larger tiles: fewer bytes per
+// FLOP, fewer waves to spread the chains over); the launcher picks it.
+//
+// K advances in slabs of 64 through a ring of NS LDS stages filled by
+// 16-byte buffer->LDS loads (no staging registers; one instruction moves
+// four 256-byte slab rows); NS - 1 slabs are in flight while one is
+// multiplied.  Each stage's A and Wt slabs are __shared__ arrays of their
+// own and the loop is unrolled over the ring, so the compiler can tell the
+// loads into one slab from the reads of another (and places no wait of its
+// own before the operand reads).
+// Slab rows are 64 words (16 chunks of 4 k) with the chunks XOR-swizzled by
+// the row: chunk c of row r sits at chunk position c ^ (r % 16).  A load lane
+// picks its source chunk to match, and the MFMA lane that needs k = 4s + g of
+// row r reads word 4 (s ^ (r % 16)) + g: the 64 lanes of one read (16 rows x
+// 4 g) then hit 64 distinct banks.  Rows past M or N read 0 through the
+// buffer range check (their outputs are not stored).
+//
+// Workgroup b runs on XCD b % 8; XCD x takes the contiguous tile range
+// [x * per_xcd, (x + 1) * per_xcd) in row-block-major order, so its L2 holds
+// a few A row blocks and the whole (small) Wt, instead of every A row block
+// for a few Wt column blocks.
+
+#define LT_BK 64
+
+// 16-byte buffer->LDS load: lane L's four words land at dst + 4L.  (A plain
+// function, so that only the device compile checks the builtin's size.)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, float* dst, unsigned voff,
+                                           int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, soff, 0, 0);
+}
+
+// NK > 0: K / 64 fixed at compile time, so the slab loop unrolls completely
+// (and each stage's loads and reads stay distinguishable to the compiler's
+// wait placement across the whole chain); NK = 0: any K / 64, run-time loop.
+template <int TM, int TN, int NS, int NK>
+__global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, int per_xcd) {
+  static_assert((TM == 32 || TM == 64) && (TN == 32 || TN == 64) && (NS == 3 || NS == 4), "");
+  constexpr int BM = TM / 32, BN = TN / 32;   // 16x16 blocks per wave
+  constexpr int LA = TM / 16, LB = TN / 16;   // loads per wave per slab
+  constexpr int L = LA + LB;
+  // stage s: A slab in sN, Wt slab in tN
+  __shared__ __attribute__((aligned(16))) float s0[TM * LT_BK], s1[TM * LT_BK], s2[TM * LT_BK],
+      s3[TM * LT_BK];
+  __shared__ __attribute__((aligned(16))) float t0[TN * LT_BK], t1[TN * LT_BK], t2[TN * LT_BK],
+      t3[TN * LT_BK];
+  const int tid = threadIdx.x, lane = tid & 63;
+  // "& 3" bounds the wave index for the compiler: with it the LDS offsets of
+  // every load and read have known ranges, which is what lets the compiler
+  // see that a stage's reads do not touch the stages still loading
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & 3;
+  const int lg = lane >> 4, l16 = lane & 15;
+  const int wm = wave & 1, wn = wave >> 1;
+  // all word offsets fit 31 bits (checked by the launcher)
+  const int M = (int)g.m, N = (int)g.n, K = (int)g.k, lda = (int)g.lda;
+  const int nb = (N + TN - 1) / TN;
+  const int tile = (int)(blockIdx.x % NUM_XCD) * per_xcd + (int)(blockIdx.x / NUM_XCD);
+  if (tile >= ntiles) return;
+  const int i0 = (tile / nb) * TM, j0 = (tile % nb) * TN;
+  const int nk = NK > 0 ? NK : K / LT_BK;
+
+  const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)g.a, 0, ((M - 1) * lda + K) * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)g.wt, 0, N * K * 4, 0x00020000);
+  // this wave loads slab rows [wave * TM/4, (wave + 1) * TM/4) of A (and the
+  // same for Wt with TN), four rows per instruction: lane L -> row
+  // wave * TM/4 + 4u + L/16, chunk position L % 16
+  unsigned aoff[LA], boff[LB];
+#pragma unroll
+  for (int u = 0; u < LA; u++) {
+    const int rl = wave * (TM / 4) + 4 * u + (lane >> 4);
+    const int r = i0 + rl;
+    aoff[u] = r < M ? (unsigned)(r * lda + 4 * ((lane & 15) ^ (rl & 15))) * 4u : 0x80000000u;
+  }
+#pragma unroll
+  for (int u = 0; u < LB; u++) {
+    const int rl = wave * (TN / 4) + 4 * u + (lane >> 4);
+    const int n = j0 + rl;
+    boff[u] = n < N ? (unsigned)(n * K + 4 * ((lane & 15) ^ (rl & 15))) * 4u : 0x80000000u;
+  }
+
+  auto stage_a = [&](auto st) -> float* {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return s0;
+    else if constexpr (S == 1) return s1;
+    else if constexpr (S == 2) return s2;
+    else return s3;
+  };
+  auto stage_b = [&](auto st) -> float* {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return t0;
+    else if constexpr (S == 1) return t1;
+    else if constexpr (S == 2) return t2;
+    else return t3;
+  };
+  // slab kt -> stage S: L loads per wave (k offset in the scalar offset)
+  auto issue = [&](auto st, int kt) {
+    float* a = stage_a(st) + wave * (TM / 4) * LT_BK;
+    float* b = stage_b(st) + wave * (TN / 4) * LT_BK;
+    const int so = kt * LT_BK * 4;
+#pragma unroll
+    for (int u = 0; u < LA; u++) lds_load16(ar, a + 4 * u * LT_BK, aoff[u], so);
+#pragma unroll
+    for (int u = 0; u < LB; u++) lds_load16(br, b + 4 * u * LT_BK, boff[u], so);
+  };
+  f32x4 acc[BM][BN];
+#pragma unroll
+  for (int bm = 0; bm < BM; bm++)
+#pragma unroll
+    for (int bn = 0; bn < BN; bn++) acc[bm][bn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float av[BM][16], bv[BN][16];
+  // operands of a slab: lane (g, l16) takes k = 4s + g of its rows, s = 0..15
+  auto fetch = [&](auto st) {
+#pragma unroll
+    for (int bm = 0; bm < BM; bm++) {
+      const float* a = stage_a(st) + (wm * (TM / 2) + bm * 16 + l16) * LT_BK + lg;
+#pragma unroll
+      for (int s = 0; s < 16; s++) av[bm][s] = a[4 * (s ^ l16)];
+    }
+#pragma unroll
+    for (int bn = 0; bn < BN; bn++) {
+      const float* b = stage_b(st) + (wn * (TN / 2) + bn * 16 + l16) * LT_BK + lg;
+#pragma unroll
+      for (int s = 0; s < 16; s++) bv[bn][s] = b[4 * (s ^ l16)];
+    }
+  };
+  auto mfmas = [&]() {
+#pragma unroll
+    for (int s = 0; s < 16; s++)
+#pragma unroll
+      for (int bm = 0; bm < BM; bm++)
+#pragma unroll
+        for (int bn = 0; bn < BN; bn++)
+          acc[bm][bn] =
+              __builtin_amdgcn_mfma_f32_16x16x4f32(av[bm][s], bv[bn][s], acc[bm][bn], 0, 0, 0);
+  };
+  // workgroup barrier that leaves the loads in flight: only this wave's
+  // LDS reads must be back (lgkmcnt 0) before a stage it read is refilled
+  auto barrier = [&]() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+
+  issue(S0{}, 0);
+  if (nk > 1) issue(S1{}, 1);
+  if constexpr (NS > 3)
+    if (nk > 2) issue(S2{}, 2);
+  // slab t: wait until it is in (at most the NS - 2 slabs after it still
+  // loading), then refill the stage freed by slab t - 1 with slab t + NS - 1
+  auto step = [&](auto st, int t) {
+    constexpr int S = decltype(st)::value;
+    const int ahead = min(NS - 2, nk - 1 - t);
+    if (ahead >= 2) wait_vmcnt<2 * L>();
+    else if (ahead == 1) wait_vmcnt<L>();
+    else wait_vmcnt<0>();
+    barrier();
+    // the operand reads go out before the refill, so they wait on no load
+    fetch(st);
+    if (t + NS - 1 < nk) issue(std::integral_constant<int, (S + NS - 1) % NS>{}, t + NS - 1);
+    mfmas();
+  };
+  auto ring = [&](int t) {
+    step(S0{}, t);
+    if (t + 1 < nk) step(S1{}, t + 1);
+    if (t + 2 < nk) step(S2{}, t + 2);
+    if constexpr (NS > 3)
+      if (t + 3 < nk) step(S3{}, t + 3);
+  };
+  if constexpr (NK > 0) {
+#pragma unroll
+    for (int t = 0; t < NK; t += NS) ring(t);
+  } else {
+    for (int t = 0; t < nk; t += NS) ring(t);
+  }
+
+  // epilogue: MatMul, then + bias (a term of -0.0 leaves a value unchanged),
+  // activation, then + residual; operands gathered before any store
+#pragma unroll
+  for (int bn = 0; bn < BN; bn++) {
+    const int j = j0 + wn * (TN / 2) + bn * 16 + l16;
+    if (j >= N) continue;
+    const float badd = g.bias ? g.bias[j] : -0.0f;
+    float r[BM][4];
+#pragma unroll
+    for (int bm = 0; bm < BM; bm++) {
+      const int ib = i0 + wm * (TM / 2) + bm * 16 + 4 * lg;
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        r[bm][v] = (g.res && ib + v < M) ? g.res[(int64_t)(ib + v) * N + j] : 0.0f;
+    }
+#pragma unroll
+    for (int bm = 0; bm < BM; bm++) {
+      const int ib = i0 + wm * (TM / 2) + bm * 16 + 4 * lg;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        if (ib + v >= M) continue;
+        float x = acc[bm][bn][v] + badd;
+        x = act_apply(x, g.act);
+        if (g.res) x = x + r[bm][v];
+        g.c[(int64_t)(ib + v) * N + j] = x;
+      }
+    }
+  }
+}
+
+bool linear_nt_eligible(int64_t m, int64_t n, int64_t k, int64_t lda) {
+  if (m <= 0 || n <= 0 || k < LT_BK || k % LT_BK != 0 || lda < k) return false;
+  return ((m - 1) * lda + k) * 4 < (1ll << 31) && n * k * 4 < (1ll << 31) &&
+         m * n < (1ll << 31) && (double)ceil_div(m, 32) * (double)ceil_div(n, 32) < 1e9;
+}
+
+template <int TM, int TN, int NS>
+static void launch_lt(const LinArgs& g, hipStream_t s) {
+  const int ntiles = (int)(ceil_div(g.n, TN) * ceil_div(g.m, TM));
+  const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
+  const dim3 grid((unsigned)(per_xcd * NUM_XCD));
+  const int64_t nk = g.k / LT_BK;
+  if (nk == 4)
+    hipLaunchKernelGGL((linear_nt_kernel<TM, TN, NS, 4>), grid, dim3(256), 0, s, g, ntiles, per_xcd);
+  else if (nk == 16)
+    hipLaunchKernelGGL((linear_nt_kernel<TM, TN, NS, 16>), grid, dim3(256), 0, s, g, ntiles,
+                       per_xcd);
+  else
+    hipLaunchKernelGGL((linear_nt_kernel<TM, TN, NS, 0>), grid, dim3(256), 0, s, g, ntiles, per_xcd);
+}
+
+// Tile shape and ring depth as measured on the rec linears (1280 rows, K
+// 256 / 1024, N 256..1024): 32x32 tiles with three stages (48 KB, three
+// workgroups per CU) beat 64x32 and 64x64 on all four, and three stages beat
+// four (two workgroups per CU).
+int launch_linear_nt(const LinArgs& g, hipStream_t s) {
+  if (!linear_nt_eligible(g.m, g.n, g.k, g.lda))
+    return fail(QPH_EUNSUPPORTED, "linear: shape outside the resident-weight kernel");
+  launch_lt<32, 32, 3>(g, s);
+  return launch_check("linear_nt_kernel");
+}
+
+__global__ void transpose_kernel(const float* __restrict__ w, int64_t k, int64_t n,
+                                 float* __restrict__ wt) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= k * n) return;
+  const int64_t j = e / k, i = e - j * k;
+  wt[e] = w[i * n + j];
+}
+
+int launch_transpose(const float* w, int64_t k, int64_t n, float* wt, hipStream_t s) {
+  if (k <= 0 || n <= 0) return QPH_OK;
+  hipLaunchKernelGGL(transpose_kernel, dim3(ceil_div(k * n, 256)), dim3(256), 0, s, w, k, n, wt);
+  return launch_check("transpose_kernel");
 }
 
 }  // namespace qph

@@ -166,6 +166,33 @@ struct GemmArgs {
 };
 int launch_gemm(const GemmArgs& g, hipStream_t s);
 
+// The session's linears: C[M][N] = act(A[M][K] * Wt[N][K]^T + bias) (+ res),
+// Wt the weight held transposed (k contiguous).
+struct LinArgs {
+  const float* a; int64_t lda;
+  const float* wt;
+  float* c;
+  int64_t m, n, k;
+  const float* bias;          // per column, or NULL
+  Act act;
+  const float* res;           // [M][N], or NULL
+};
+bool linear_nt_eligible(int64_t m, int64_t n, int64_t k, int64_t lda);
+int launch_linear_nt(const LinArgs& g, hipStream_t s);
+// true when launch_gemm takes the 128x128 persistent kernel for this shape
+bool gemm_takes_wide(int64_t m, int64_t n, int64_t batch);
+// wt[j][i] = w[i][j] for a [k][n] row-major w
+int launch_transpose(const float* w, int64_t k, int64_t n, float* wt, hipStream_t s);
+
+// s_waitcnt that waits until at most N vector-memory operations of this
+// wave are outstanding (N < 64); the export and LDS/scalar counters are left
+// at their maxima (no wait).  Encoding: vmcnt bits [3:0] and [15:14].
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+
 // Reference bias placement (gemm.rs:7-16): rule 0 (panel kernel): seeded
 // when row is in the M%4 tail and the 32-column panel is partial; rule 1
 // (m-rows kernel): seeded for columns j >= n - n%32.

@@ -23,6 +23,7 @@ struct qph_net {
   std::vector<int> group_len;    // > 1: first of that many independent 3x3 convs, one launch
   std::vector<DwPwArgs> dwpw;    // per node: fused depthwise + pointwise launch
   std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1 with it)
+  std::vector<float*> wt;        // per linear node: resident transposed weight Wt[N][K] (or NULL)
   std::vector<float*> tptr;      // per tensor device pointer
   char* arena;
   size_t arena_bytes;
@@ -50,6 +51,23 @@ static int check_tensor(const qph_net* net, int32_t id, bool optional, size_t i,
   if (id < 0 || id >= (int32_t)net->tptr.size())
     return fail(QPH_EINVAL, node_name(i, n) + ": bad " + what + " tensor id");
   return QPH_OK;
+}
+
+// Linear node i over its resident transposed weight.
+static LinArgs lin_args(const qph_net* net, size_t i) {
+  const qph_node& n = net->nodes[i];
+  LinArgs g{};
+  g.a = net->tptr[n.in];
+  g.lda = n.ws[0];
+  g.wt = net->wt[i];
+  g.c = net->tptr[n.out];
+  g.k = n.ws[0];
+  g.n = n.ws[1];
+  g.m = numel_of(net, n.in) / g.k;
+  g.bias = n.bias >= 0 ? net->weights[n.bias] : nullptr;
+  g.act = make_act(&n.act);
+  g.res = n.in2 >= 0 ? net->tptr[n.in2] : nullptr;
+  return g;
 }
 
 // Launches node i on the context stream.
@@ -82,6 +100,7 @@ static int run_node(qph_net* net, size_t i) {
     case QPH_OP_LINEAR: {
       const int64_t k = n.ws[0], nn = n.ws[1];
       const int64_t rows = numel_of(net, n.in) / k;
+      if (net->wt[i]) return launch_linear_nt(lin_args(net, i), s);
       GemmArgs g{};
       // weights resident with rows padded to a multiple of 4 floats
       g.a = x; g.lda = k; g.b = net->wk[i] ? net->wk[i] : w; g.ldb = (nn + 3) / 4 * 4;
@@ -360,6 +379,8 @@ static void release(qph_net* net) {
   for (float* p : net->weights) (void)hipFree(p);
   for (float* p : net->wk)
     if (p) (void)hipFree(p);
+  for (float* p : net->wt)
+    if (p) (void)hipFree(p);
   if (net->arena) (void)hipFree(net->arena);
   delete net;
 }
@@ -389,6 +410,7 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     net->outputs.assign(spec->outputs, spec->outputs + spec->n_outputs);
   net->tptr.assign((size_t)spec->n_tensors, nullptr);
   net->wk.assign(net->nodes.size(), nullptr);
+  net->wt.assign(net->nodes.size(), nullptr);
   int rc = QPH_OK;
   auto bail = [&](int code) {
     std::string msg = qph_last_error();
@@ -450,6 +472,19 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
       rc = launch_repack_conv_w_taps(net->weights[n.w], n.ws[0], n.ws[1], n.ws[2] * n.ws[3], d,
                                      ctx->stream);
       if (rc) return bail(rc);
+    }
+    if (n.op == QPH_OP_LINEAR) {
+      // below the 128x128 size: weight kept transposed for linear_nt_kernel
+      const int64_t k = n.ws[0], nn = n.ws[1], rows = numel_of(net, n.in) / k;
+      if (!gemm_takes_wide(rows, nn, 1) && linear_nt_eligible(rows, nn, k, k)) {
+        float* d = nullptr;
+        rc = hip_check(hipMalloc((void**)&d, (size_t)(k * nn) * 4), "hipMalloc(transposed weight)");
+        if (rc) return bail(rc);
+        net->wt[i] = d;
+        rc = launch_transpose(net->weights[n.w], k, nn, d, ctx->stream);
+        if (rc) return bail(rc);
+        continue;
+      }
     }
     if (n.op == QPH_OP_LINEAR && n.ws[1] % 4 != 0) {
       // [K][N] -> [K][N4] with zero columns past N (16-byte aligned rows)

@@ -144,3 +144,54 @@ def test_session_fusion_rules(gpu, oracle):
     for i, (a, b) in enumerate(zip(got, ref)):
         assert_bitexact(a, b, f"output {i}")
     sess.close()
+
+
+LINEAR_CASES = [
+    # rows, k, n, layernorm in front, activation, residual, LN output also an output
+    (1280, 256, 768, True, "none", False, False),   # rec QKV: 4 slabs
+    (1280, 1024, 256, False, "none", True, False),  # rec MLP down: 16 slabs + residual
+    (1280, 256, 1024, True, "gelu", False, False),  # rec MLP up + GELU
+    (70, 64, 40, False, "gelu", True, False),        # ragged rows / columns, 1 slab
+    (33, 192, 96, True, "none", True, False),        # 3 slabs, run-time slab loop
+    (64, 128, 200, True, "none", False, True),       # 2 slabs
+    (50, 320, 64, True, "gelu", False, False),       # 5 slabs
+    (96, 448, 37, False, "none", True, False),       # 7 slabs, odd N
+]
+
+
+@pytest.mark.parametrize("case", LINEAR_CASES, ids=lambda c: "x".join(map(str, c[:3])) + f"-{c[3]}{c[4]}{c[5]}{c[6]}")
+def test_session_linear_shapes(gpu, oracle, case):
+    """Session linears below the 128x128 size run over a transposed resident
+    weight (linear_nt_kernel): ragged rows and columns, 1..16 slabs of 64
+    (compile-time and run-time slab loops), GELU and residual epilogues,
+    after a LayerNorm or not; bit-exact against the oracle."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    rows, k, n, ln, act, res, ln_out = case
+    r = nets.WeightRng(rows * 7 + k + n)
+    g = nets.Graph((1, rows, k))
+    x = 0
+    outs = []
+    if ln:
+        gam = g.weight((1.0 + r.normal((k,), 0.1)).astype(np.float32))
+        bet = g.weight(r.normal((k,), 0.1))
+        x = g.layernorm(0, gam, bet, nets.LN_EPS)
+        if ln_out:
+            outs.append(x)
+    resid = -1
+    if res:
+        w0 = g.weight(r.kaiming((k, n), k))
+        b0 = g.weight(r.normal((n,), 0.1))
+        resid = g.linear(0, w0, b0)
+        outs.append(resid)
+    w = g.weight(r.kaiming((k, n), k))
+    b = g.weight(r.normal((n,), 0.1))
+    y = g.linear(x, w, b, act=nets.ACT_GELU if act == "gelu" else nets.ACT_NONE, residual=resid)
+    g.outputs = outs + [y]
+    xin = r.normal((1, rows, k), 1.0)
+    sess = nets.HipSession(g)
+    got = sess.run(xin)
+    ref = onets.run_graph(g, xin)
+    for i, (a, bb) in enumerate(zip(got, ref)):
+        assert_bitexact(a, bb, f"output {i}")
+    sess.close()
