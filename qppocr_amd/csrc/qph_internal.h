@@ -259,8 +259,8 @@ int launch_convt2x2_pair_sigmoid(const float* x, int64_t n, int64_t c, int64_t h
 int launch_layernorm(const float* x, const float* gamma, const float* beta, float eps,
                      int64_t rows, int64_t cols, float* y, hipStream_t s);
 int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s);
-int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, float* probs,
-                          float* pairs, hipStream_t s);
+int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
+                          float* probs, float* pairs, hipStream_t s);
 int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, hipStream_t s);
 int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
                      float scale, float* out, hipStream_t s);

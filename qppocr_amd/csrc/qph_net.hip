@@ -25,6 +25,7 @@ struct qph_net {
   std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1 with it)
   std::vector<float*> wt;        // per linear node: resident transposed weight Wt[N][K] (or NULL)
   std::vector<float*> tptr;      // per tensor device pointer
+  std::vector<int64_t> pitch;    // per tensor: padded row pitch in floats (0: contiguous)
   char* arena;
   size_t arena_bytes;
   hipGraph_t graph;
@@ -105,7 +106,7 @@ static int run_node(qph_net* net, size_t i) {
       // weights resident with rows padded to a multiple of 4 floats
       g.a = x; g.lda = k; g.b = net->wk[i] ? net->wk[i] : w; g.ldb = (nn + 3) / 4 * 4;
       if (!net->wk[i]) g.ldb = nn;
-      g.c = y; g.ldc = nn;
+      g.c = y; g.ldc = net->pitch[n.out] ? net->pitch[n.out] : nn;
       g.m = rows; g.n = nn; g.k = k; g.batch = 1;
       g.bias = bias; g.bias_mode = bias ? 2 : 0;
       g.act = make_act(&n.act);
@@ -121,7 +122,8 @@ static int run_node(qph_net* net, size_t i) {
     case QPH_OP_SOFTMAX_ARGMAX: {
       const int64_t c = n.ws[0];  // row width
       float* pairs = n.out2 >= 0 ? net->tptr[n.out2] : nullptr;
-      return launch_softmax_argmax(x, numel_of(net, n.in) / c, c, y, pairs, s);
+      return launch_softmax_argmax(x, numel_of(net, n.in) / c, c,
+                                   net->pitch[n.in] ? net->pitch[n.in] : c, y, pairs, s);
     }
     case QPH_OP_ACT:
       return launch_elementwise_act(x, y, numel_of(net, n.in), make_act(&n.act), s);
@@ -132,6 +134,38 @@ static int run_node(qph_net* net, size_t i) {
 
 static int32_t storage_of(const qph_net* net, int32_t t) {
   return t >= 0 && net->alias[(size_t)t] >= 0 ? net->alias[(size_t)t] : t;
+}
+
+// A linear on the 128x128 path whose output only a softmax_argmax reads
+// (the rec head, N = 18709) keeps its rows 32 floats (128 bytes) apart: every
+// 32-column segment of the GEMM's stores is then one whole cache line instead
+// of parts of two.  Runs before the arena is laid out; ids are range-checked
+// here because the nodes are validated later.
+static void plan_pitch(qph_net* net) {
+  const size_t nt = net->tptr.size();
+  net->pitch.assign(nt, 0);
+  std::vector<int> readers(nt, 0);
+  std::vector<bool> aliased(nt, false);
+  auto ok = [&](int32_t t) { return t >= 0 && (size_t)t < nt; };
+  for (size_t t = 0; t < nt; t++)
+    if (net->alias[t] >= 0 && (size_t)net->alias[t] < nt) aliased[(size_t)net->alias[t]] = true;
+  for (const qph_node& n : net->nodes) {
+    if (ok(n.in)) readers[(size_t)storage_of(net, n.in)]++;
+    if (ok(n.in2)) readers[(size_t)storage_of(net, n.in2)]++;
+  }
+  for (int32_t o : net->outputs)
+    if (ok(o)) readers[(size_t)storage_of(net, o)] += 1 << 20;   // outputs stay contiguous
+  for (const qph_node& q : net->nodes) {
+    if (q.op != QPH_OP_LINEAR || !ok(q.out) || !ok(q.in) || q.ws[0] <= 0) continue;
+    const int32_t t = q.out;
+    const int64_t nn = q.ws[1], rows = numel_of(net, q.in) / q.ws[0];
+    if (net->alias[(size_t)t] >= 0 || aliased[(size_t)t] || readers[(size_t)t] != 1) continue;
+    if (nn % 32 == 0 || !gemm_takes_wide(rows, nn, 1) || numel_of(net, t) != rows * nn) continue;
+    bool soft = false;
+    for (const qph_node& r : net->nodes)
+      soft = soft || (r.in == t && r.op == QPH_OP_SOFTMAX_ARGMAX && r.ws[0] == nn);
+    if (soft) net->pitch[(size_t)t] = (nn + 31) / 32 * 32;
+  }
 }
 
 // Consecutive dense 3x3 convs (up to four) of which none reads another's
@@ -431,11 +465,19 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
       return bail(QPH_EINVAL);
     }
   }
+  plan_pitch(net);
   std::vector<size_t> off((size_t)spec->n_tensors, 0);
   for (int32_t t = 0; t < spec->n_tensors; t++) {
     if (net->alias[t] >= 0) continue;
     off[t] = net->arena_bytes;
-    net->arena_bytes += ((size_t)numel_of(net, t) * 4 + 255) / 256 * 256;
+    int64_t words = numel_of(net, t);
+    if (net->pitch[(size_t)t]) {
+      const qph_node* q = nullptr;
+      for (const qph_node& n : net->nodes)
+        if (n.out == t) q = &n;
+      words = numel_of(net, q->in) / q->ws[0] * net->pitch[(size_t)t];
+    }
+    net->arena_bytes += ((size_t)words * 4 + 255) / 256 * 256;
   }
   rc = hip_check(hipMalloc((void**)&net->arena, net->arena_bytes), "hipMalloc(arena)");
   if (rc) return bail(rc);

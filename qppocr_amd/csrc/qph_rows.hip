@@ -113,14 +113,14 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
 
 // probs may alias logits (in-place softmax).  pairs may be NULL.
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, int64_t cols,
-                                                           float* probs, float* pairs) {
+                                                           int64_t ld, float* probs, float* pairs) {
   __shared__ float buf[2][SM_CHUNK];
   __shared__ float part[16];
   __shared__ float red[8];
   __shared__ int redi[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
-  const float* xr = logits + row * cols;
+  const float* xr = logits + row * ld;
   float* pr = probs + row * cols;
 
   // max over the row, eight loads in flight per thread
@@ -283,7 +283,7 @@ __device__ __forceinline__ float block_max_512(float v, float* red) {
   return r;
 }
 
-__global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, int cols,
+__global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, int cols, int ld,
                                                           float* probs, float* pairs) {
   __shared__ __attribute__((aligned(16))) float win[2][8 * SM_WIN_PITCH];
   __shared__ float part[16];
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
   float e[SM_REG_PER_THREAD];
   {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(logits + row * cols), 0, cols * 4, 0x00020000);
+        (void*)(logits + row * ld), 0, cols * 4, 0x00020000);
 #pragma unroll
     for (int u = 0; u < SM_REG_PER_THREAD; u++)
       e[u] = __builtin_bit_cast(
@@ -416,27 +416,29 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
   }
 }
 
-static int launch_softmax(const float* logits, int64_t rows, int64_t cols, float* probs,
-                          float* pairs, hipStream_t s) {
+// logits rows ld floats apart (ld >= cols); probs contiguous.
+static int launch_softmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
+                          float* probs, float* pairs, hipStream_t s) {
   if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
-  if (cols <= SM_REG_MAX_COLS) {
+  if (ld < cols) return fail(QPH_EINVAL, "softmax: row pitch below the row width");
+  if (cols <= SM_REG_MAX_COLS && ld < (1ll << 31)) {
     hipLaunchKernelGGL(softmax_reg_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
-                       (int)cols, probs, pairs);
+                       (int)cols, (int)ld, probs, pairs);
     return launch_check("softmax_reg_kernel");
   }
   hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols,
-                     probs, pairs);
+                     ld, probs, pairs);
   return launch_check("softmax_rows_kernel");
 }
 
 int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s) {
-  return launch_softmax(t, rows, cols, t, nullptr, s);
+  return launch_softmax(t, rows, cols, cols, t, nullptr, s);
 }
 
-int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, float* probs,
-                          float* pairs, hipStream_t s) {
+int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
+                          float* probs, float* pairs, hipStream_t s) {
   if (!probs) return fail(QPH_EINVAL, "softmax_argmax: probs buffer required");
-  return launch_softmax(logits, rows, cols, probs, pairs, s);
+  return launch_softmax(logits, rows, cols, ld, probs, pairs, s);
 }
 
 // argmax over probabilities: first strict max (rec.rs:46-54).

@@ -418,7 +418,7 @@ QPH_API int qph_softmax_argmax(qph_ctx* ctx, const float* logits, int64_t rows, 
   if (rows <= 0 || cols <= 0 || !logits || !pairs)
     return fail(QPH_EINVAL, "softmax_argmax: bad argument");
   if (cols > 32768) return fail(QPH_EUNSUPPORTED, "softmax_argmax: cols > 32768");
-  return launch_softmax_argmax(logits, rows, cols, probs, pairs, ctx->stream);
+  return launch_softmax_argmax(logits, rows, cols, cols, probs, pairs, ctx->stream);
 }
 
 QPH_API int qph_ctc_argmax(qph_ctx* ctx, const float* probs, int64_t batch, int64_t t_len,
