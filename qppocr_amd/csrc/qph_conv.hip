@@ -1,5 +1,7 @@
 // Convolution kernels: implicit-GEMM dense conv on fp32 MFMA, depthwise
 // direct conv, 2x2 s2 ConvTranspose (single and the fused det-head pair).
+#include <algorithm>
+
 #include "qph_internal.h"
 
 namespace qph {
@@ -731,6 +733,71 @@ int launch_depthwise(const ConvArgs& a, hipStream_t s) {
   else
     return fail(QPH_EUNSUPPORTED, "depthwise: kernel sizes 3x3, 5x5, 7x7 only");
   return launch_check("depthwise_kernel");
+}
+
+// Depthwise conv over channel-last tensors, x[n][h][w][c] -> y[n][oh][ow][c]
+// (the rec backbone's deeper blocks, whose pointwise half then runs as a
+// row-major GEMM): one thread per output element, channels fastest, so a
+// wave reads and writes 64 consecutive channels of a pixel.  Same operation
+// sequence as depthwise_kernel (out-of-image taps contribute fma(w, 0, acc)).
+
+struct DwClK {
+  const float* x;
+  const float* w;
+  const float* bias;
+  float* y;
+  int n, c, h, w_, sh, sw, ph, pw, oh, ow;
+  Act act;
+};
+
+template <int KH, int KW>
+__global__ __launch_bounds__(256) void depthwise_cl_kernel(DwClK p) {
+  const int total = p.n * p.oh * p.ow * p.c;   // < 2^31 (launcher)
+  for (int e = (int)blockIdx.x * 256 + (int)threadIdx.x; e < total; e += (int)gridDim.x * 256) {
+    const int ch = e % p.c;
+    int q = e / p.c;
+    const int ox = q % p.ow;
+    q /= p.ow;
+    const int oy = q % p.oh, img = q / p.oh;
+    const float* wp = p.w + ch * KH * KW;
+    const float* xb = p.x + (int64_t)img * p.h * p.w_ * p.c + ch;
+    float acc = 0.0f;
+#pragma unroll
+    for (int ky = 0; ky < KH; ky++) {
+      const int iy = oy * p.sh - p.ph + ky;
+#pragma unroll
+      for (int kx = 0; kx < KW; kx++) {
+        const int ix = ox * p.sw - p.pw + kx;
+        const float xv = (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w_)
+                             ? xb[((int64_t)iy * p.w_ + ix) * p.c]
+                             : 0.0f;
+        acc = __builtin_fmaf(wp[ky * KW + kx], xv, acc);
+      }
+    }
+    const float v = acc + (p.bias ? p.bias[ch] : 0.0f);
+    p.y[e] = act_apply(v, p.act);
+  }
+}
+
+int launch_depthwise_cl(const ConvArgs& a, hipStream_t s) {
+  const int64_t total = a.n * a.oh * a.ow * a.c;
+  if (total <= 0) return QPH_OK;
+  if (total >= (1ll << 31) || a.n * a.h * a.w * a.c >= (1ll << 31))
+    return fail(QPH_EUNSUPPORTED, "depthwise (channel-last): tensor too large");
+  DwClK p{};
+  p.x = a.x; p.w = a.wt; p.bias = a.bias; p.y = a.y;
+  p.n = (int)a.n; p.c = (int)a.c; p.h = (int)a.h; p.w_ = (int)a.w;
+  p.sh = (int)a.sh; p.sw = (int)a.sw; p.ph = (int)a.ph; p.pw = (int)a.pw;
+  p.oh = (int)a.oh; p.ow = (int)a.ow;
+  p.act = a.act;
+  const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(total, 256), 1 << 20);
+  if (a.kh == 3 && a.kw == 3)
+    hipLaunchKernelGGL((depthwise_cl_kernel<3, 3>), dim3(grid), dim3(256), 0, s, p);
+  else if (a.kh == 5 && a.kw == 5)
+    hipLaunchKernelGGL((depthwise_cl_kernel<5, 5>), dim3(grid), dim3(256), 0, s, p);
+  else
+    return fail(QPH_EUNSUPPORTED, "depthwise (channel-last): 3x3 and 5x5 only");
+  return launch_check("depthwise_cl_kernel");
 }
 
 // ----------------------------------------------------------- ConvTranspose

@@ -245,6 +245,8 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s);
 bool direct3x3_eligible(const ConvArgs& a);
 int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s);
 int launch_depthwise(const ConvArgs& a, hipStream_t s);
+// depthwise conv with x and y channel-last ([n][h][w][c]); 3x3 and 5x5
+int launch_depthwise_cl(const ConvArgs& a, hipStream_t s);
 int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw);
 // wk[Kpad][Mpad] k-major copy of an ONNX [M][cg][kh][kw] weight, Kpad =
 // ceil(cg/4)*4*khkw, Mpad = ceil(M/32)*32, zero-filled past the real extent.

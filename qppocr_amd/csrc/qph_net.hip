@@ -24,6 +24,9 @@ struct qph_net {
   std::vector<DwPwArgs> dwpw;    // per node: fused depthwise + pointwise launch
   std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1 with it)
   std::vector<float*> wt;        // per linear node: resident transposed weight Wt[N][K] (or NULL)
+  std::vector<bool> cl_dw;       // depthwise conv node run channel-last (in and out)
+  std::vector<bool> cl_pw;       // 1x1 conv node run as a row-major GEMM, channel-last in and out
+  std::vector<bool> cl_out;      // 1x1 conv node storing channel-last (trans_out) for a cl_dw reader
   std::vector<float*> tptr;      // per tensor device pointer
   std::vector<int64_t> pitch;    // per tensor: padded row pitch in floats (0: contiguous)
   char* arena;
@@ -85,13 +88,33 @@ static int run_node(qph_net* net, size_t i) {
   const float* res = n.in2 >= 0 ? net->tptr[n.in2] : nullptr;
   switch (n.op) {
     case QPH_OP_CONV: {
+      if (net->cl_dw[i]) {
+        ConvArgs a{};
+        a.x = x; a.n = xs[0]; a.c = xs[1]; a.h = xs[2]; a.w = xs[3];
+        a.wt = w; a.bias = bias;
+        a.m = n.ws[0]; a.kh = n.ws[2]; a.kw = n.ws[3];
+        a.sh = n.cp.sh; a.sw = n.cp.sw; a.ph = n.cp.ph; a.pw = n.cp.pw;
+        const int64_t* ys = &net->shapes[4 * (size_t)n.out];
+        a.oh = ys[2]; a.ow = ys[3];
+        a.act = make_act(&n.act);
+        a.y = y;
+        return launch_depthwise_cl(a, s);
+      }
+      if (net->cl_pw[i]) {
+        // y[n * h * w][M] = act(x[n * h * w][C] . W[M][C]^T + bias)
+        LinArgs g{};
+        g.a = x; g.lda = n.ws[1]; g.wt = w; g.c = y;
+        g.m = xs[0] * xs[2] * xs[3]; g.n = n.ws[0]; g.k = n.ws[1];
+        g.bias = bias; g.act = make_act(&n.act); g.res = nullptr;
+        return launch_linear_nt(g, s);
+      }
       qph_conv_epilogue ep{};
       ep.residual = res;
       ep.res_up = n.res_up;
       ep.y_ctotal = n.y_ctotal;
       ep.y_coff = n.y_coff;
       ep.y_up = n.y_up;
-      ep.trans_out = n.trans_out;
+      ep.trans_out = n.trans_out || net->cl_out[i];
       return conv_dispatch(ctx, x, xs, w, net->wk[i], n.ws, bias, &n.cp, &n.act, &ep, y);
     }
     case QPH_OP_CONVT_PAIR_SIG:
@@ -219,6 +242,97 @@ static void plan_conv_groups(qph_net* net) {
   }
 }
 
+// The deeper backbone blocks of the rec net (64..256 channels over a few
+// rows of pixels) run channel-last: the depthwise conv as
+// depthwise_cl_kernel, the 1x1 conv as a row-major GEMM (linear_nt_kernel:
+// rows = pixels, k = channels; the ONNX [M][C][1][1] weight is already
+// k-contiguous).  The fused kernel reloads every channel's halo for each
+// 64-channel slice and the weight slice for each 16-pixel tile, which at
+// these shapes costs far more than the intermediate round trip.
+// Structure: a chain of (depthwise -> 1x1) blocks ending in a 1x1 conv that
+// stores [n][pixels][M] (trans_out), every intermediate read only by the
+// next node; the 1x1 conv feeding the chain's first depthwise stores
+// channel-last too (trans_out).  A 1x1 conv joins only if its bias comes
+// after the chain (rule 0 with M % 4 == 0: no seeded accumulators, as in the
+// linear epilogue) and linear_nt_kernel takes the shape (C % 64 == 0).
+static void plan_cl(qph_net* net) {
+  const size_t nn = net->nodes.size(), nt = net->tptr.size();
+  net->cl_dw.assign(nn, false);
+  net->cl_pw.assign(nn, false);
+  net->cl_out.assign(nn, false);
+  std::vector<int> readers(nt, 0);
+  for (const qph_node& n : net->nodes) {
+    readers[(size_t)storage_of(net, n.in)]++;
+    if (n.in2 >= 0) readers[(size_t)storage_of(net, n.in2)]++;
+  }
+  for (int32_t o : net->outputs) readers[(size_t)storage_of(net, o)] += 1 << 20;
+  auto producer = [&](int32_t t) {
+    for (size_t i = 0; i < nn; i++)
+      if (net->nodes[i].out == t) return (int)i;
+    return -1;
+  };
+  auto plain_out = [&](const qph_node& q) {
+    return q.in2 < 0 && q.res_up == 0 && (q.y_ctotal == 0 || q.y_ctotal == q.ws[0]) &&
+           q.y_coff == 0 && q.y_up <= 1;
+  };
+  auto single = [&](int32_t t) { return storage_of(net, t) == t && readers[(size_t)t] == 1; };
+  auto is_pw = [&](const qph_node& q) {
+    return q.op == QPH_OP_CONV && q.cp.group == 1 && q.ws[2] == 1 && q.ws[3] == 1 &&
+           q.cp.sh == 1 && q.cp.sw == 1 && q.cp.ph == 0 && q.cp.pw == 0 && q.cp.peh == 0 &&
+           q.cp.pew == 0 && plain_out(q);
+  };
+  auto is_dw = [&](const qph_node& d) {
+    const int64_t* xs = &net->shapes[4 * (size_t)d.in];
+    return d.op == QPH_OP_CONV && d.cp.group > 1 && d.ws[1] == 1 && d.ws[0] == xs[1] &&
+           d.cp.group == xs[1] && ((d.ws[2] == 3 && d.ws[3] == 3) || (d.ws[2] == 5 && d.ws[3] == 5)) &&
+           d.trans_out == 0 && plain_out(d);
+  };
+  auto pw_ok = [&](const qph_node& q) {
+    const int64_t* xs = &net->shapes[4 * (size_t)q.in];
+    const int64_t m = q.ws[0], c = q.ws[1], px = xs[2] * xs[3];
+    const double fl = (double)m * (double)px * (double)c;
+    const int rule = (xs[0] > 1 || fl < 2e5 || (px + 31) / 32 >= 2) ? 0 : 1;
+    return rule == 0 && m % 4 == 0 && linear_nt_eligible(xs[0] * px, m, c, c);
+  };
+  for (size_t e = 0; e < nn; e++) {
+    const qph_node& last = net->nodes[e];
+    if (!is_pw(last) || !last.trans_out || !pw_ok(last)) continue;
+    // walk back: blocks (dw[k], pw[k]), pw[0] = e; feeder = the 1x1 conv
+    // before the chain's first depthwise
+    std::vector<int> dws, pws;
+    int p = (int)e, feeder = -1;
+    while (true) {
+      const int d = producer(net->nodes[(size_t)p].in);
+      if (d < 0 || !is_dw(net->nodes[(size_t)d]) || !single(net->nodes[(size_t)d].out)) break;
+      const int x = producer(net->nodes[(size_t)d].in);
+      if (x < 0 || !is_pw(net->nodes[(size_t)x]) || net->nodes[(size_t)x].trans_out ||
+          !single(net->nodes[(size_t)x].out))
+        break;
+      dws.push_back(d);
+      pws.push_back(p);
+      if (!pw_ok(net->nodes[(size_t)x])) {
+        feeder = x;
+        break;
+      }
+      p = x;
+      feeder = x;
+    }
+    // the last block taken needs its depthwise input channel-last: the
+    // feeder stores it so; a chain whose walk stopped on a 1x1 conv that
+    // joined as a block gives that conv back as the feeder
+    if (!dws.empty() && feeder >= 0 && feeder == pws.back()) {
+      dws.pop_back();
+      pws.pop_back();
+    }
+    if (dws.empty() || feeder < 0) continue;
+    for (size_t k = 0; k < dws.size(); k++) {
+      net->cl_dw[(size_t)dws[k]] = true;
+      net->cl_pw[(size_t)pws[k]] = true;
+    }
+    net->cl_out[(size_t)feeder] = true;
+  }
+}
+
 // Depthwise conv node i feeding 1x1 conv node i + 1 (the backbone blocks):
 // one launch, the depthwise output kept on chip.  Needs plain outputs (the
 // 1x1 may store transposed), no residuals, and no other reader of the
@@ -247,6 +361,7 @@ static int plan_dwpw(qph_net* net) {
                     q.cp.pew == 0 && q.in2 < 0 && q.res_up == 0 &&
                     (q.y_ctotal == 0 || q.y_ctotal == q.ws[0]) && q.y_coff == 0 && q.y_up <= 1;
     if (!dw || !pw || q.in != d.out || q.ws[1] != d.ws[0]) continue;
+    if (net->cl_dw[i] || net->cl_pw[i + 1]) continue;
     if (storage_of(net, d.out) != d.out || readers[(size_t)d.out] != 1) continue;
     int64_t ys[4];
     if (qph_conv2d_out_shape(xs, d.ws, &d.cp, ys) != QPH_OK) continue;
@@ -262,7 +377,7 @@ static int plan_dwpw(qph_net* net) {
     const double fl = (double)f.m * (double)(f.oh * f.ow) * (double)f.c;
     f.seed_rule = (f.n > 1 || fl < 2e5 || (f.oh * f.ow + 31) / 32 >= 2) ? 0 : 1;
     f.act_p = make_act(&q.act);
-    f.trans_out = q.trans_out;
+    f.trans_out = q.trans_out || net->cl_out[i + 1];
     f.y = net->tptr[q.out];
     if (!dwpw_eligible(f)) continue;
     float* wk = nullptr;
@@ -546,6 +661,7 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     }
   }
   plan_conv_groups(net);
+  plan_cl(net);
   rc = plan_dwpw(net);
   if (rc) return bail(rc);
   rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");

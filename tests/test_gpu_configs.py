@@ -195,3 +195,37 @@ def test_session_linear_shapes(gpu, oracle, case):
     for i, (a, bb) in enumerate(zip(got, ref)):
         assert_bitexact(a, bb, f"output {i}")
     sess.close()
+
+
+def test_session_channel_last_chain(gpu, oracle):
+    """A chain of depthwise -> 1x1 blocks ending in a 1x1 conv that stores
+    [n][pixels][M] runs channel-last (depthwise_cl_kernel + the 1x1 convs as
+    row-major GEMMs) from the first block whose 1x1 conv has C % 64 == 0;
+    the block before it (C = 32) stays fused and stores channel-last.
+    Strides (2,2), (2,1), (3,1), a 5x5 depthwise and an odd width; bit-exact
+    against the oracle."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    r = nets.WeightRng(23)
+    g = nets.Graph((2, 3, 24, 41))
+    ws = g.weight(r.kaiming((32, 3, 3, 3), 27))
+    bs = g.weight(r.normal((32,), 0.1))
+    x = g.conv(0, ws, bs, stride=(2, 2), pad=(1, 1, 1, 1), act=nets.ACT_HARDSWISH)
+    blocks = [  # (dw kernel, stride, pad, cin, cout)
+        (3, (1, 1), (1, 1, 1, 1), 32, 64), (3, (2, 1), (1, 1, 1, 1), 64, 128),
+        (5, (1, 1), (2, 2, 2, 2), 128, 64), (3, (3, 1), (0, 1, 0, 1), 64, 128),
+    ]
+    for i, (k, st, pad, cin, cout) in enumerate(blocks):
+        wd = g.weight(r.kaiming((cin, 1, k, k), k * k))
+        bd = g.weight(r.normal((cin,), 0.1))
+        x = g.conv(x, wd, bd, stride=st, pad=pad, group=cin, act=nets.ACT_HARDSWISH)
+        wp = g.weight(r.kaiming((cout, cin, 1, 1), cin))
+        bp = g.weight(r.normal((cout,), 0.1))
+        x = g.conv(x, wp, bp, act=nets.ACT_HARDSWISH, trans_out=i == len(blocks) - 1)
+    g.outputs = [x]
+    xin = r.uniform((2, 3, 24, 41), -1.0, 1.0)
+    sess = nets.HipSession(g)
+    got = sess.run(xin)
+    ref = onets.run_graph(g, xin)
+    assert_bitexact(got[0], ref[0], "chain output")
+    sess.close()
