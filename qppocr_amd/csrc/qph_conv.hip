@@ -550,7 +550,100 @@ static int launch_dense_t(const DenseConvK& p, bool wide_m, dim3 grid, hipStream
   return launch_check("dense_conv_kernel");
 }
 
+// --------------------------------------------------- few input channels
+//
+// Dense convs with 3 input channels and 16 or 32 outputs (the det and rec
+// stems, 3x3 stride 2): one thread per output pixel keeps its C*KH*KW
+// input taps in registers and runs the output channels' chains on the VALU,
+// four at a time, the weights wave-uniform (scalar loads, ONNX layout).  Per
+// element: acc = 0; for k = c*KH*KW + ky*KW + kx ascending: acc = fma(w[m][k],
+// x_k, acc) -- the implicit-GEMM chain, taps outside the image giving
+// fma(w, 0, acc) -- then + bias (M % 4 == 0: the reference never seeds it),
+// then the activation.  The MFMA kernels spend most of their time on
+// latency at this size.
+
+struct SmallCK {
+  const float* x;
+  const float* w;
+  const float* bias;
+  float* y;
+  int h, w_, m, sh, sw, ph, pw, oh, ow;
+  Act act;
+};
+
+template <int C, int KH, int KW, int M>
+__global__ __launch_bounds__(256) void conv_smallc_kernel(SmallCK p) {
+  constexpr int K = C * KH * KW;
+  // weights transposed to [k][m] in LDS: one broadcast ds_read_b128 gives
+  // tap k of four output channels
+  __shared__ __attribute__((aligned(16))) float wl[K * M];
+  __shared__ float bl[M];
+  const int tid = (int)threadIdx.x;
+  for (int i = tid; i < K * M; i += 256) {
+    const int m = i / K, k = i - m * K;
+    wl[k * M + m] = p.w[i];
+  }
+  if (tid < M) bl[tid] = p.bias ? p.bias[tid] : 0.0f;
+  __syncthreads();
+  const int npx = p.oh * p.ow;
+  const int e = (int)blockIdx.x * 256 + tid;   // pixel of the image
+  const int img = (int)blockIdx.y;
+  if (e >= npx) return;
+  const int oy = e / p.ow, ox = e - oy * p.ow;
+  const float* xb = p.x + (int64_t)img * C * p.h * p.w_;
+  float xv[K];
+#pragma unroll
+  for (int c = 0; c < C; c++)
+#pragma unroll
+    for (int ky = 0; ky < KH; ky++)
+#pragma unroll
+      for (int kx = 0; kx < KW; kx++) {
+        const int iy = oy * p.sh - p.ph + ky, ix = ox * p.sw - p.pw + kx;
+        const bool in = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w_;
+        xv[(c * KH + ky) * KW + kx] = in ? xb[((int64_t)c * p.h + iy) * p.w_ + ix] : 0.0f;
+      }
+  float* yb = p.y + (int64_t)img * M * npx + e;
+#pragma unroll 2
+  for (int m0 = 0; m0 < M; m0 += 4) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+      const f32x4 wv = *(const f32x4*)(wl + k * M + m0);
+#pragma unroll
+      for (int q = 0; q < 4; q++) acc[q] = __builtin_fmaf(wv[q], xv[k], acc[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float v = p.bias ? acc[q] + bl[m0 + q] : acc[q];
+      yb[(int64_t)(m0 + q) * npx] = act_apply(v, p.act);
+    }
+  }
+}
+
+static bool smallc_eligible(const ConvArgs& a) {
+  return a.group == 1 && a.c == 3 && a.kh == 3 && a.kw == 3 && (a.m == 16 || a.m == 32) &&
+         !a.res &&
+         a.y_ctotal == a.m && a.y_coff == 0 && a.y_up == 1 && a.oh * a.ow < (1ll << 31) &&
+         a.n <= 65535 && a.m * a.oh * a.ow < (1ll << 31);
+}
+
+static int launch_smallc(const ConvArgs& a, hipStream_t s) {
+  SmallCK p{};
+  p.x = a.x; p.w = a.wt; p.bias = a.bias; p.y = a.y;
+  p.h = (int)a.h; p.w_ = (int)a.w; p.m = (int)a.m;
+  p.sh = (int)a.sh; p.sw = (int)a.sw; p.ph = (int)a.ph; p.pw = (int)a.pw;
+  p.oh = (int)a.oh; p.ow = (int)a.ow;
+  p.act = a.act;
+  dim3 grid(ceil_div(a.oh * a.ow, 256), (unsigned)a.n);
+  if (a.m == 16)
+    hipLaunchKernelGGL((conv_smallc_kernel<3, 3, 3, 16>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((conv_smallc_kernel<3, 3, 3, 32>), grid, dim3(256), 0, s, p);
+  return launch_check("conv_smallc_kernel");
+}
+
 int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
+  if (smallc_eligible(a)) return launch_smallc(a, s);
   const int64_t khkw = a.kh * a.kw;
   if (khkw != 9 && khkw != 25 && khkw != 1 && khkw != 4)
     return fail(QPH_EUNSUPPORTED, "dense conv: kernel sizes with kh*kw in {1, 4, 9, 25} only");

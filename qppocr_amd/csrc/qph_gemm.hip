@@ -34,8 +34,19 @@ struct EpiIn {
   bool has_add, ok;
 };
 
+// Residual column of output column j: j itself, or for the upsample-add
+// (res_up == 2) the coarse-map offset of pixel j (nearest 2x).  Column
+// indices of an upsampled map fit 32 bits (checked by the launcher's
+// caller), so the division is a 32-bit one; computed once per column.
+__device__ __forceinline__ int64_t res_col(const GemmArgs& g, int64_t j) {
+  if (g.res_up != 2) return j;
+  const unsigned ju = (unsigned)j, w = (unsigned)g.up_w;
+  const unsigned oy = ju / w, ox = ju - oy * w;
+  return (int64_t)(oy >> 1) * g.up_cw + (ox >> 1);
+}
+
 __device__ __forceinline__ EpiIn epilogue_gather(const GemmArgs& g, const float* R, int64_t i,
-                                                 int64_t j) {
+                                                 int64_t j, int64_t rcol) {
   EpiIn e{0.0f, 0.0f, false, i < g.m && j < g.n};
   if (!e.ok) return e;
   if (g.bias_mode == 1) {
@@ -47,14 +58,7 @@ __device__ __forceinline__ EpiIn epilogue_gather(const GemmArgs& g, const float*
     e.add = g.bias[j];
     e.has_add = true;
   }
-  if (R) {
-    if (g.res_up == 2) {
-      int64_t oy = j / g.up_w, ox = j - oy * g.up_w;
-      e.res = R[i * g.ldr + (oy >> 1) * g.up_cw + (ox >> 1)];
-    } else {
-      e.res = R[i * g.ldr + j];
-    }
-  }
+  if (R) e.res = R[i * g.ldr + rcol];
   return e;
 }
 
@@ -185,10 +189,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
     for (int ni = 0; ni < NI; ni++) {
       EpiIn e[16];
+      const int64_t rc = R ? res_col(g, j0 + wn0 + ni * 32 + lr) : 0;
 #pragma unroll
       for (int v = 0; v < 16; v++)
         e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
-                               j0 + wn0 + ni * 32 + lr);
+                               j0 + wn0 + ni * 32 + lr, rc);
 #pragma unroll
       for (int v = 0; v < 16; v++)
         epilogue_put(g, C, R != nullptr, e[v], i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
@@ -301,8 +306,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
   float* C = g.c + bz * g.c_batch;
   const float* R = g.res ? g.res + bz * g.r_batch : nullptr;
   EpiIn e[4];
+  const int64_t rc = R ? res_col(g, jj + l16) : 0;
 #pragma unroll
-  for (int v = 0; v < 4; v++) e[v] = epilogue_gather(g, R, ii + 4 * lg + v, jj + l16);
+  for (int v = 0; v < 4; v++) e[v] = epilogue_gather(g, R, ii + 4 * lg + v, jj + l16, rc);
 #pragma unroll
   for (int v = 0; v < 4; v++) epilogue_put(g, C, R != nullptr, e[v], ii + 4 * lg + v, jj + l16, acc[v]);
 }
@@ -522,10 +528,11 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int 
 #pragma unroll
         for (int ni = 0; ni < 2; ni++) {
           EpiIn e[16];
+          const int64_t rc = R ? res_col(g, j0 + wn0 + ni * 32 + lr) : 0;
 #pragma unroll
           for (int v = 0; v < 16; v++)
             e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
-                                   j0 + wn0 + ni * 32 + lr);
+                                   j0 + wn0 + ni * 32 + lr, rc);
 #pragma unroll
           for (int v = 0; v < 16; v++)
             epilogue_put(g, C, R != nullptr, e[v],

@@ -232,6 +232,8 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
     return fail(QPH_EINVAL, "conv2d: bad output placement");
   if (res_up == 2 && ((oh & 1) || (ow & 1)))
     return fail(QPH_EINVAL, "conv2d: upsample-add needs even output size");
+  if (res_up == 2 && oh * ow >= (1ll << 32))
+    return fail(QPH_EUNSUPPORTED, "conv2d: upsample-add map past 2^32 pixels");
   const bool plain_out = y_ctotal == m && y_coff == 0 && y_up == 1;
   Act a = make_act(act);
 

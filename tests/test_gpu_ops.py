@@ -143,6 +143,10 @@ DIRECT_CASES = [
     (8, 8, 16, 128, 128, 1, 1, 1, 1, 1, 1),
     (8, 3, 16, 128, 128, 2, 2, 1, 1, 1, 1),
     (3, 12, 40, 33, 47, 2, 1, 0, 1, 2, 0),
+    # 3 input channels, M % 4 == 0: the VALU kernel (odd sizes, asymmetric pads)
+    (3, 3, 32, 47, 81, 2, 2, 1, 1, 1, 1),
+    (2, 3, 20, 30, 33, 1, 2, 0, 1, 2, 0),
+    (1, 3, 22, 17, 19, 2, 2, 1, 1, 1, 1),   # M % 4 != 0: MFMA path
 ]
 
 
