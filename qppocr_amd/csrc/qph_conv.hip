@@ -833,43 +833,43 @@ int launch_depthwise(const ConvArgs& a, hipStream_t s) {
 // row-major GEMM): one thread per output element, channels fastest, so a
 // wave reads and writes 64 consecutive channels of a pixel.  Same operation
 // sequence as depthwise_kernel (out-of-image taps contribute fma(w, 0, acc)).
+// C must be a power of two (the rec blocks: 64, 128, 256).
 
 struct DwClK {
   const float* x;
   const float* w;
   const float* bias;
   float* y;
-  int n, c, h, w_, sh, sw, ph, pw, oh, ow;
+  int n, c, lc, h, w_, sh, sw, ph, pw, oh, ow;   // c = 1 << lc
   Act act;
 };
 
 template <int KH, int KW>
 __global__ __launch_bounds__(256) void depthwise_cl_kernel(DwClK p) {
-  const int total = p.n * p.oh * p.ow * p.c;   // < 2^31 (launcher)
-  for (int e = (int)blockIdx.x * 256 + (int)threadIdx.x; e < total; e += (int)gridDim.x * 256) {
-    const int ch = e % p.c;
-    int q = e / p.c;
-    const int ox = q % p.ow;
-    q /= p.ow;
-    const int oy = q % p.oh, img = q / p.oh;
-    const float* wp = p.w + ch * KH * KW;
-    const float* xb = p.x + (int64_t)img * p.h * p.w_ * p.c + ch;
-    float acc = 0.0f;
+  // grid: x over (ox, ch) of one output row, y over (image, oy); C a power
+  // of two, so the channel is a mask and the column a shift
+  const int row = (int)blockIdx.y;
+  const int oy = row % p.oh, img = row / p.oh;
+  const int e = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (e >= p.ow * p.c) return;
+  const int ch = e & (p.c - 1), ox = e >> p.lc;
+  const float* wp = p.w + ch * KH * KW;
+  const float* xb = p.x + (int64_t)img * p.h * p.w_ * p.c + ch;
+  float acc = 0.0f;
 #pragma unroll
-    for (int ky = 0; ky < KH; ky++) {
-      const int iy = oy * p.sh - p.ph + ky;
+  for (int ky = 0; ky < KH; ky++) {
+    const int iy = oy * p.sh - p.ph + ky;
 #pragma unroll
-      for (int kx = 0; kx < KW; kx++) {
-        const int ix = ox * p.sw - p.pw + kx;
-        const float xv = (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w_)
-                             ? xb[((int64_t)iy * p.w_ + ix) * p.c]
-                             : 0.0f;
-        acc = __builtin_fmaf(wp[ky * KW + kx], xv, acc);
-      }
+    for (int kx = 0; kx < KW; kx++) {
+      const int ix = ox * p.sw - p.pw + kx;
+      const float xv = (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w_)
+                           ? xb[((int64_t)iy * p.w_ + ix) * p.c]
+                           : 0.0f;
+      acc = __builtin_fmaf(wp[ky * KW + kx], xv, acc);
     }
-    const float v = acc + (p.bias ? p.bias[ch] : 0.0f);
-    p.y[e] = act_apply(v, p.act);
   }
+  const float v = acc + (p.bias ? p.bias[ch] : 0.0f);
+  p.y[((int64_t)row * p.ow) * p.c + e] = act_apply(v, p.act);
 }
 
 int launch_depthwise_cl(const ConvArgs& a, hipStream_t s) {
@@ -877,17 +877,21 @@ int launch_depthwise_cl(const ConvArgs& a, hipStream_t s) {
   if (total <= 0) return QPH_OK;
   if (total >= (1ll << 31) || a.n * a.h * a.w * a.c >= (1ll << 31))
     return fail(QPH_EUNSUPPORTED, "depthwise (channel-last): tensor too large");
+  if (a.c & (a.c - 1)) return fail(QPH_EUNSUPPORTED, "depthwise (channel-last): C not a power of two");
+  if (a.n * a.oh > 65535) return fail(QPH_EUNSUPPORTED, "depthwise (channel-last): grid too large");
   DwClK p{};
   p.x = a.x; p.w = a.wt; p.bias = a.bias; p.y = a.y;
   p.n = (int)a.n; p.c = (int)a.c; p.h = (int)a.h; p.w_ = (int)a.w;
+  p.lc = 0;
+  while ((1ll << p.lc) < a.c) p.lc++;
   p.sh = (int)a.sh; p.sw = (int)a.sw; p.ph = (int)a.ph; p.pw = (int)a.pw;
   p.oh = (int)a.oh; p.ow = (int)a.ow;
   p.act = a.act;
-  const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(total, 256), 1 << 20);
+  const dim3 grid(ceil_div(a.ow * a.c, 256), (unsigned)(a.n * a.oh));
   if (a.kh == 3 && a.kw == 3)
-    hipLaunchKernelGGL((depthwise_cl_kernel<3, 3>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((depthwise_cl_kernel<3, 3>), grid, dim3(256), 0, s, p);
   else if (a.kh == 5 && a.kw == 5)
-    hipLaunchKernelGGL((depthwise_cl_kernel<5, 5>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((depthwise_cl_kernel<5, 5>), grid, dim3(256), 0, s, p);
   else
     return fail(QPH_EUNSUPPORTED, "depthwise (channel-last): 3x3 and 5x5 only");
   return launch_check("depthwise_cl_kernel");

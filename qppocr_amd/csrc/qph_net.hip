@@ -283,7 +283,9 @@ static void plan_cl(qph_net* net) {
   };
   auto is_dw = [&](const qph_node& d) {
     const int64_t* xs = &net->shapes[4 * (size_t)d.in];
+    const int64_t* ys = &net->shapes[4 * (size_t)d.out];
     return d.op == QPH_OP_CONV && d.cp.group > 1 && d.ws[1] == 1 && d.ws[0] == xs[1] &&
+           (xs[1] & (xs[1] - 1)) == 0 && ys[0] * ys[2] <= 65535 &&
            d.cp.group == xs[1] && ((d.ws[2] == 3 && d.ws[3] == 3) || (d.ws[2] == 5 && d.ws[3] == 5)) &&
            d.trans_out == 0 && plain_out(d);
   };
