@@ -603,14 +603,21 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
 
 // Head dimension known at compile time: one workgroup per (batch, head);
 // q (times scale: the Mul node), k and v of all T rows arrive in LDS in one
-// burst of loads, then the query rows go in blocks (all rows up to 64).  Scores: one chain of DH fmas per
-// (row, key).  Softmax: eight threads per row, thread j owning elements
-// j, j+8, ... -- its max part, its exp1 values and exactly the reference's
-// lane-j chain -- then the ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree and the
-// tail in order within the group of eight (no workgroup barrier).  P.V:
-// one chain of T fmas per (row, d).
+// burst of loads, then the query rows go in blocks (all rows up to 64).
+// Scores: one chain of DH fmas per (row, key).  Softmax: eight threads per
+// row, thread j owning elements j, j+8, ... -- its max part, its exp1 values
+// and exactly the reference's lane-j chain -- then the
+// ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree and the tail in order within the
+// group of eight (no workgroup barrier).  P.V: one chain of T fmas per
+// (row, d).
+// MF (T % 4 == 0): both products on v_mfma_f32_16x16x4f32, whose four k
+// terms per instruction are added in order, so each 16x16 output block is
+// the same fma chains (k = d for the scores, k = j for P.V, each from 0);
+// q, k and v rows are zero-filled up to a multiple of 16 and the score /
+// probability block to 16-row, 16-column tiles, whose extra outputs are
+// never used.
 
-template <int DH>
+template <int DH, bool MF>
 __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restrict__ qkv,
                                                            int64_t T, int64_t H, float scale,
                                                            int blk, float* __restrict__ out) {
@@ -620,17 +627,19 @@ __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restri
   const int tid = threadIdx.x;
   const int64_t D = H * DH;
   const int t = (int)T;
-  const int ldp = t + 1;
-  float* sq = sm;                 // T x LD (scaled q)
-  float* sk = sq + t * LD;        // T x LD
-  float* sv = sk + t * LD;        // T x LD
-  float* sp = sv + t * LD;        // blk x (T+1) scores / probabilities
+  const int tp = MF ? (t + 15) / 16 * 16 : t;     // rows held (zero past t)
+  const int ldp = MF ? tp + 1 : t + 1;
+  float* sq = sm;                 // tp x LD (scaled q)
+  float* sk = sq + tp * LD;       // tp x LD
+  float* sv = sk + tp * LD;       // tp x LD
+  float* sp = sv + tp * LD;       // blk (rounded to 16) x ldp scores / probabilities
   const float* base = qkv + b * T * 3 * D + h * DH;
-  for (int i0 = tid; i0 < t * DH; i0 += 256 * 4) {
+  for (int i0 = tid; i0 < tp * DH; i0 += 256 * 4) {
     float q[4], k[4], v[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int i = i0 + 256 * u;
+      q[u] = k[u] = v[u] = 0.0f;
       if (i < t * DH) {
         const float* row = base + (int64_t)(i / DH) * 3 * D + (i % DH);
         q[u] = row[0];
@@ -641,7 +650,7 @@ __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restri
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int i = i0 + 256 * u;
-      if (i < t * DH) {
+      if (i < tp * DH) {
         const int r = i / DH, d = i - r * DH;
         sq[r * LD + d] = q[u] * scale;   // Mul node
         sk[r * LD + d] = k[u];
@@ -651,17 +660,35 @@ __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restri
   }
   __syncthreads();
   const int full = t >= 8 ? (t / 8) * 8 : 0;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lg = lane >> 4, l16 = lane & 15;
   for (int r0 = 0; r0 < t; r0 += blk) {
     const int rb = (t - r0) < blk ? (t - r0) : blk;
-    // scores S[r][j] = chain over d of fma(q[r][d], k[j][d], acc)
-    for (int i = tid; i < rb * t; i += 256) {
-      const int r = i / t, j = i - r * t;
-      const float* qr = sq + (r0 + r) * LD;
-      const float* kj = sk + j * LD;
-      float acc = 0.0f;
+    if (MF) {
+      // S block (rb x t) in 16x16 tiles over the four waves
+      const int nr = (rb + 15) / 16, nc = tp / 16;
+      for (int tl = wave; tl < nr * nc; tl += 4) {
+        const int br = tl / nc, bc = tl - br * nc;
+        const float* a = sq + (r0 + 16 * br + l16) * LD + lg;
+        const float* bk = sk + (16 * bc + l16) * LD + lg;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int d = 0; d < DH; d++) acc = __builtin_fmaf(qr[d], kj[d], acc);
-      sp[r * ldp + j] = acc;
+        for (int s4 = 0; s4 < DH / 4; s4++)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4], bk[4 * s4], acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) sp[(16 * br + 4 * lg + v) * ldp + 16 * bc + l16] = acc[v];
+      }
+    } else {
+      // scores S[r][j] = chain over d of fma(q[r][d], k[j][d], acc)
+      for (int i = tid; i < rb * t; i += 256) {
+        const int r = i / t, j = i - r * t;
+        const float* qr = sq + (r0 + r) * LD;
+        const float* kj = sk + j * LD;
+        float acc = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DH; d++) acc = __builtin_fmaf(qr[d], kj[d], acc);
+        sp[r * ldp + j] = acc;
+      }
     }
     __syncthreads();
     // softmax, eight threads per row (groups never straddle a wave)
@@ -702,52 +729,82 @@ __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restri
         for (int j = lj; j < t; j += 8) pr[j] = pr[j] * inv;
     }
     __syncthreads();
-    // O[r][d] = chain over j of fma(P[r][j], v[j][d], acc); operands read
-    // eight j at a time so their LDS reads are in flight together
-    for (int i = tid; i < rb * DH; i += 256) {
-      const int r = i / DH, d = i - r * DH;
-      const float* p = sp + r * ldp;
-      const float* vd = sv + d;
-      float acc = 0.0f;
-      int j = 0;
-      for (; j + 8 <= t; j += 8) {
-        float pv[8], vv[8];
+    if (MF) {
+      // O block (rb x DH) = P . v in 16x16 tiles, k = j over exactly t terms
+      const int nr = (rb + 15) / 16;
+      for (int tl = wave; tl < nr * (DH / 16); tl += 4) {
+        const int br = tl / (DH / 16), bc = tl - br * (DH / 16);
+        const float* a = sp + (16 * br + l16) * ldp + lg;
+        const float* bv = sv + lg * LD + 16 * bc + l16;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s4 = 0; s4 < t / 4; s4++)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4], bv[4 * s4 * LD], acc, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-          pv[u] = p[j + u];
-          vv[u] = vd[(j + u) * LD];
+        for (int v = 0; v < 4; v++) {
+          const int r = 16 * br + 4 * lg + v;
+          if (r < rb) out[(b * T + r0 + r) * D + h * DH + 16 * bc + l16] = acc[v];
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++) acc = __builtin_fmaf(pv[u], vv[u], acc);
       }
-      for (; j < t; j++) acc = __builtin_fmaf(p[j], vd[j * LD], acc);
-      out[(b * T + r0 + r) * D + h * DH + d] = acc;
+    } else {
+      // O[r][d] = chain over j of fma(P[r][j], v[j][d], acc); operands read
+      // eight j at a time so their LDS reads are in flight together
+      for (int i = tid; i < rb * DH; i += 256) {
+        const int r = i / DH, d = i - r * DH;
+        const float* p = sp + r * ldp;
+        const float* vd = sv + d;
+        float acc = 0.0f;
+        int j = 0;
+        for (; j + 8 <= t; j += 8) {
+          float pv[8], vv[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            pv[u] = p[j + u];
+            vv[u] = vd[(j + u) * LD];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; u++) acc = __builtin_fmaf(pv[u], vv[u], acc);
+        }
+        for (; j < t; j++) acc = __builtin_fmaf(p[j], vd[j * LD], acc);
+        out[(b * T + r0 + r) * D + h * DH + d] = acc;
+      }
     }
     __syncthreads();
   }
 }
 
-static size_t attention_dh_lds(int64_t t, int64_t dh, int64_t blk) {
-  return (size_t)(3 * t * (dh + 1) + blk * (t + 1)) * sizeof(float);
+static size_t attention_dh_lds(int64_t t, int64_t dh, int64_t blk, bool mf) {
+  const int64_t tp = mf ? (t + 15) / 16 * 16 : t;
+  const int64_t bp = mf ? (blk + 15) / 16 * 16 : blk;
+  return (size_t)(3 * tp * (dh + 1) + bp * (tp + 1)) * sizeof(float);
 }
 
 int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
                      float scale, float* out, hipStream_t s) {
   // query rows per block: all of them up to 64, else 64 or 32 as LDS allows
+  const bool mf = t % 4 == 0;
   int64_t blk = t <= 64 ? t : 64;
-  if (attention_dh_lds(t, dh, blk) > 160 * 1024) blk = 32;
-  if ((dh == 32 || dh == 64) && attention_dh_lds(t, dh, blk) <= 160 * 1024) {
+  if (attention_dh_lds(t, dh, blk, mf) > 160 * 1024) blk = 32;
+  if ((dh == 32 || dh == 64) && attention_dh_lds(t, dh, blk, mf) <= 160 * 1024) {
     if (batch * heads > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "attention: grid too large");
-    const size_t lds = attention_dh_lds(t, dh, blk);
-    const void* fn = dh == 32 ? (const void*)attention_dh_kernel<32>
-                              : (const void*)attention_dh_kernel<64>;
+    const size_t lds = attention_dh_lds(t, dh, blk, mf);
+    const void* fn = dh == 32 ? (mf ? (const void*)attention_dh_kernel<32, true>
+                                    : (const void*)attention_dh_kernel<32, false>)
+                              : (mf ? (const void*)attention_dh_kernel<64, true>
+                                    : (const void*)attention_dh_kernel<64, false>);
     QPH_TRY(allow_full_lds(fn));
-    if (dh == 32)
-      hipLaunchKernelGGL(attention_dh_kernel<32>, dim3((unsigned)(batch * heads)), dim3(256), lds,
-                         s, qkv, t, heads, scale, (int)blk, out);
+    const dim3 grid((unsigned)(batch * heads));
+    if (dh == 32 && mf)
+      hipLaunchKernelGGL((attention_dh_kernel<32, true>), grid, dim3(256), lds, s, qkv, t, heads,
+                         scale, (int)blk, out);
+    else if (dh == 32)
+      hipLaunchKernelGGL((attention_dh_kernel<32, false>), grid, dim3(256), lds, s, qkv, t, heads,
+                         scale, (int)blk, out);
+    else if (mf)
+      hipLaunchKernelGGL((attention_dh_kernel<64, true>), grid, dim3(256), lds, s, qkv, t, heads,
+                         scale, (int)blk, out);
     else
-      hipLaunchKernelGGL(attention_dh_kernel<64>, dim3((unsigned)(batch * heads)), dim3(256), lds,
-                         s, qkv, t, heads, scale, (int)blk, out);
+      hipLaunchKernelGGL((attention_dh_kernel<64, false>), grid, dim3(256), lds, s, qkv, t, heads,
+                         scale, (int)blk, out);
     return launch_check("attention_dh_kernel");
   }
   return launch_attention_generic(qkv, batch, t, heads, dh, scale, out, s);
