@@ -263,7 +263,7 @@ def main():
         "rec_ms": round(rec_ms, 4),
         "serial_ms_per_step": round(det_ms + rec_ms, 4),
         "pcie_inclusive_img_per_s": round(1e3 / host_ms_step, 3),
-        "roofline": {"bound": "mfma", "kernel": "rec head GEMM 1280x18709x256 (gemm_wide_kernel)",
+        "roofline": {"bound": "mfma", "kernel": "rec head GEMM 1280x18709x256 (gemm_wave_kernel)",
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": head_traffic_bytes(), "avg_launch_ms": round(head_ms, 5)},

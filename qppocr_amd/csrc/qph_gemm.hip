@@ -369,10 +369,8 @@ static int launch_cfg(const GemmArgs& g, hipStream_t s) {
 #define WB_BL 8    // B-slab loads per wave
 #define NUM_XCD 8
 
-// PLAIN: column bias or none, no activation, residual or transposed store
-// (the rec head); accumulators then start at 0 and the epilogue is one add
-// and a store, which keeps the register budget small.
-template <bool PLAIN>
+// (The plain case -- column bias or none, no activation, residual or
+// transposed store, the rec head -- runs on gemm_wave_kernel below.)
 __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int nb,
                                                         int ntiles, int per_xcd, int wg_xcd) {
   __shared__ __attribute__((aligned(16))) float lds[2 * WB_STAGE];
@@ -450,7 +448,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int 
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[mi][ni][v] = 0.0f;
         const int n0 = j0 + wn0 + ni * 32;
-        if (!PLAIN && g.bias_mode == 1 && n0 < N &&
+        if (g.bias_mode == 1 && n0 < N &&
             (g.seed_rule == 1 ? n0 >= N - N % 32 : N - n0 < 32)) {
 #pragma unroll
           for (int v = 0; v < 16; v++) {
@@ -503,49 +501,201 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int 
     }
 
     float* C = g.c + (int64_t)bz * g.c_batch;
-    if (PLAIN) {
-      // column bias or none (a term of -0.0 leaves every value unchanged)
+    const float* R = g.res ? g.res + (int64_t)bz * g.r_batch : nullptr;
 #pragma unroll
-      for (int mi = 0; mi < 2; mi++)
+    for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-          const int j = j0 + wn0 + ni * 32 + lr;
-          const int ib = i0 + wm0 + mi * 32 + 4 * lh;
-          if (j < N) {
-            const float badd = g.bias_mode == 2 ? g.bias[j] : -0.0f;
-            float* cj = C + j;
+      for (int ni = 0; ni < 2; ni++) {
+        EpiIn e[16];
+        const int64_t rc = R ? res_col(g, j0 + wn0 + ni * 32 + lr) : 0;
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-              const int i = ib + 8 * (v >> 2) + (v & 3);
-              if (i < M) cj[(int64_t)i * g.ldc] = acc[mi][ni][v] + badd;
-            }
-          }
-        }
-    } else {
-      const float* R = g.res ? g.res + (int64_t)bz * g.r_batch : nullptr;
+        for (int v = 0; v < 16; v++)
+          e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                                 j0 + wn0 + ni * 32 + lr, rc);
 #pragma unroll
-      for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-          EpiIn e[16];
-          const int64_t rc = R ? res_col(g, j0 + wn0 + ni * 32 + lr) : 0;
-#pragma unroll
-          for (int v = 0; v < 16; v++)
-            e[v] = epilogue_gather(g, R, i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
-                                   j0 + wn0 + ni * 32 + lr, rc);
-#pragma unroll
-          for (int v = 0; v < 16; v++)
-            epilogue_put(g, C, R != nullptr, e[v],
-                         i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
-                         j0 + wn0 + ni * 32 + lr, acc[mi][ni][v]);
-        }
-    }
+        for (int v = 0; v < 16; v++)
+          epilogue_put(g, C, R != nullptr, e[v],
+                       i0 + wm0 + mi * 32 + 8 * (v >> 2) + 4 * lh + (v & 3),
+                       j0 + wn0 + ni * 32 + lr, acc[mi][ni][v]);
+      }
     if (next >= t_end) break;
     tile = next;
     bz = nbz;
     i0 = ni0;
     j0 = nj0;
   }
+}
+
+// ------------------------------------------------ one-wave 64x64 tiles
+//
+// The rec head (PLAIN: column bias, no activation / residual / transposed
+// store) on workgroups of a single wave, each owning whole 64x64 tiles: the
+// wave loads its own A and B slabs (the same k-deinterleaved A layout and
+// B rows as gemm_wide_kernel, K in slabs of 16, double-buffered), so no
+// workgroup barrier ties its progress to other waves.  Two such waves per
+// SIMD keep the MFMA pipe fed through each other's slab waits, where the
+// four-wave 128x128 tiles stall together at every slab barrier.  Persistent
+// and XCD-aware like gemm_wide_kernel; tiles of 64.
+
+#define WV_PA 20
+#define WV_A (64 * WV_PA)
+#define WV_B (16 * 64)
+#define WV_STAGE (WV_A + WV_B)
+#define WV_AL (WV_A / 64)   // A-slab loads (words / 64 lanes)
+#define WV_BL (WV_B / 64)   // B-slab loads
+
+__global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int nb, int ntiles,
+                                                       int per_xcd, int wg_xcd) {
+  __shared__ __attribute__((aligned(16))) float lds[2 * WV_STAGE];
+  const int lane = threadIdx.x;
+  const int xcd = (int)(blockIdx.x % NUM_XCD), wl = (int)(blockIdx.x / NUM_XCD);
+  const int t_end = min(xcd * per_xcd + per_xcd, ntiles);
+  int tile = xcd * per_xcd + wl;
+  if (tile >= t_end) return;
+  const int lr = lane & 31, lh = lane >> 5;
+  // all word offsets fit 31 bits (checked by the launcher)
+  const int M = (int)g.m, N = (int)g.n, K = (int)g.k;
+  const int lda = (int)g.lda, ldb = (int)g.ldb;
+  const int nk = K / WB_BK;
+  const int a_words = (M - 1) * lda + K, b_words = (K - 1) * ldb + N;
+  unsigned aoff[WV_AL], boff[WV_BL];
+#pragma unroll
+  for (int r = 0; r < WV_AL; r++) {
+    const int p = r * 64 + lane;
+    const int m = p / WV_PA, q = p - m * WV_PA;
+    aoff[r] = q < 16 ? (unsigned)(m * lda + 2 * (q & 7) + (q >> 3)) * 4u : 0x80000000u;
+  }
+#pragma unroll
+  for (int r = 0; r < WV_BL; r++) {
+    // row r holds B[k0 + 2s + h][j0 .. j0 + 63] for r = 8h + s
+    boff[r] = (unsigned)((2 * (r & 7) + (r >> 3)) * ldb + lane) * 4u;
+  }
+  auto corner = [&](int t, int& bz, int& i0, int& j0) {
+    const int per_b = mb * nb;
+    bz = t / per_b;
+    const int tt = t - bz * per_b;
+    const int nblk = tt / mb;
+    i0 = (tt - nblk * mb) * 64;
+    j0 = nblk * 64;
+  };
+  auto issue = [&](int bz, int i0, int j0, int kt, int st) {
+    const int k0 = kt * WB_BK;
+    const int ab = i0 * lda + k0, bb = k0 * ldb + j0;
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.a + bz * g.a_batch + ab), 0, (a_words - ab) * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.b + bz * g.b_batch + bb), 0, (b_words - bb) * 4, 0x00020000);
+    float* sa = lds + st * WV_STAGE;
+    float* sb = sa + WV_A;
+#pragma unroll
+    for (int r = 0; r < WV_AL; r++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ar, (__attribute__((address_space(3))) void*)(sa + r * 64), 4, aoff[r], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < WV_BL; r++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          br, (__attribute__((address_space(3))) void*)(sb + r * 64), 4, boff[r], 0, 0, 0);
+  };
+
+  int bz, i0, j0;
+  corner(tile, bz, i0, j0);
+  int st = 0;
+  issue(bz, i0, j0, 0, st);
+  while (true) {
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[mi][ni][v] = 0.0f;
+    const int next = tile + wg_xcd;
+    int nbz = 0, ni0 = 0, nj0 = 0;
+    if (next < t_end) corner(next, nbz, ni0, nj0);
+    for (int kt = 0; kt < nk; kt++) {
+      // this wave's loads of slab kt (and its earlier stores) are done; its
+      // reads of slab kt - 1 are done too, so that stage takes slab kt + 1
+      __builtin_amdgcn_s_waitcnt(0);
+      __asm__ volatile("" ::: "memory");
+      if (kt + 1 < nk)
+        issue(bz, i0, j0, kt + 1, st ^ 1);
+      else if (next < t_end)
+        issue(nbz, ni0, nj0, 0, st ^ 1);
+      const float* sa = lds + st * WV_STAGE + lr * WV_PA + lh * 8;
+      const float* sb = lds + st * WV_STAGE + WV_A + lh * 8 * 64 + lr;
+      f32x4 ga[2][2];
+      float gb[2][2][4];
+#pragma unroll
+      for (int gp = 0; gp < 2; gp++) {
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) ga[gp][mi] = *(const f32x4*)(sa + mi * 32 * WV_PA + gp * 4);
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+          for (int u = 0; u < 4; u++) gb[gp][ni][u] = sb[(gp * 4 + u) * 64 + ni * 32];
+      }
+#pragma unroll
+      for (int gp = 0; gp < 2; gp++)
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+          for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++)
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(ga[gp][mi][u], gb[gp][ni][u],
+                                                                 acc[mi][ni], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+      st ^= 1;
+    }
+    // column bias or none (a term of -0.0 leaves every value unchanged)
+    float* C = g.c + (int64_t)bz * g.c_batch;
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++) {
+        const int j = j0 + ni * 32 + lr;
+        const int ib = i0 + mi * 32 + 4 * lh;
+        if (j < N) {
+          const float badd = g.bias_mode == 2 ? g.bias[j] : -0.0f;
+          float* cj = C + j;
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            const int i = ib + 8 * (v >> 2) + (v & 3);
+            if (i < M) cj[(int64_t)i * g.ldc] = acc[mi][ni][v] + badd;
+          }
+        }
+      }
+    if (next >= t_end) break;
+    tile = next;
+    bz = nbz;
+    i0 = ni0;
+    j0 = nj0;
+  }
+}
+
+static int launch_wave(const GemmArgs& g, hipStream_t s) {
+  static int occ_dev[64], cus_dev[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(QPH_EHIP, "gemm: no current device (or index past 63)");
+  if (occ_dev[dev] == 0) {
+    int occ = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)gemm_wave_kernel, 64, 0) !=
+            hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        occ <= 0 || cus <= 0)
+      return fail(QPH_EHIP, "gemm: occupancy query failed");
+    cus_dev[dev] = cus;
+    occ_dev[dev] = occ;
+  }
+  const int mb = (int)ceil_div(g.m, 64), nb = (int)ceil_div(g.n, 64);
+  const int ntiles = mb * nb * (int)g.batch;
+  const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
+  const int wg_xcd = std::max(1, std::min(per_xcd, occ_dev[dev] * cus_dev[dev] / NUM_XCD));
+  hipLaunchKernelGGL(gemm_wave_kernel, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s, g, mb,
+                     nb, ntiles, per_xcd, wg_xcd);
+  return launch_check("gemm_wave_kernel");
 }
 
 // K in whole slabs, operands within the 32-bit buffer offsets.
@@ -556,32 +706,26 @@ static bool wide_fits(const GemmArgs& g) {
 }
 
 static int launch_wide(const GemmArgs& g, hipStream_t s) {
-  static int occ_dev[2][64], cus_dev[64];
-  const bool plain = g.act.kind == 0 && g.res == nullptr && !g.trans_out && g.bias_mode != 1;
+  static int occ_dev[64], cus_dev[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
     return fail(QPH_EHIP, "gemm: no current device (or index past 63)");
-  if (occ_dev[plain][dev] == 0) {
+  if (occ_dev[dev] == 0) {
     int occ = 0, cus = 0;
-    const void* fn = plain ? (const void*)gemm_wide_kernel<true> : (const void*)gemm_wide_kernel<false>;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 256, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)gemm_wide_kernel, 256, 0) !=
+            hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         occ <= 0 || cus <= 0)
       return fail(QPH_EHIP, "gemm: occupancy query failed");
     cus_dev[dev] = cus;
-    occ_dev[plain][dev] = occ;
+    occ_dev[dev] = occ;
   }
   const int mb = (int)ceil_div(g.m, 128), nb = (int)ceil_div(g.n, 128);
   const int ntiles = mb * nb * (int)g.batch;
   const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
-  const int wg_xcd =
-      std::max(1, std::min(per_xcd, occ_dev[plain][dev] * cus_dev[dev] / NUM_XCD));
-  if (plain)
-    hipLaunchKernelGGL(gemm_wide_kernel<true>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(256), 0,
-                       s, g, mb, nb, ntiles, per_xcd, wg_xcd);
-  else
-    hipLaunchKernelGGL(gemm_wide_kernel<false>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(256), 0,
-                       s, g, mb, nb, ntiles, per_xcd, wg_xcd);
+  const int wg_xcd = std::max(1, std::min(per_xcd, occ_dev[dev] * cus_dev[dev] / NUM_XCD));
+  hipLaunchKernelGGL(gemm_wide_kernel, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(256), 0, s, g, mb,
+                     nb, ntiles, per_xcd, wg_xcd);
   return launch_check("gemm_wide_kernel");
 }
 
@@ -598,6 +742,8 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
     return fail(QPH_EUNSUPPORTED, "gemm: dimension too large");
   if (gemm_takes_wide(g.m, g.n, g.batch)) {
     const double tiles = (double)ceil_div(g.m, 128) * (double)ceil_div(g.n, 128) * (double)g.batch;
+    const bool plain = g.act.kind == 0 && g.res == nullptr && !g.trans_out && g.bias_mode != 1;
+    if (plain && wide_fits(g) && tiles < (double)(1u << 28)) return launch_wave(g, s);
     if (wide_fits(g) && tiles < (double)(1u << 30)) return launch_wide(g, s);
     return launch_cfg<2, 2>(g, s);
   }
