@@ -13,10 +13,14 @@
 // A workgroup owns 16 consecutive output pixels of one output row of one
 // image and a 64-channel slice of M (one 16-channel block per wave).
 // Phase 1: one burst of buffer->LDS loads brings the input halo of those
-// pixels for all C channels (KH rows x (15*sw + KW) columns; out-of-image
-// taps carry an out-of-range offset and read 0, the zero padding) and the
-// k-major weight rows of the slice.  Phase 2: the depthwise outputs of all
-// C channels for the 16 pixels, from the halo, into LDS (t[c][16]).
+// pixels for all C channels (KH rows x (15*sw + KW) columns, rows padded to
+// a multiple of 4 columns; out-of-image taps carry an out-of-range offset
+// and read 0, the zero padding) and the k-major weight rows of the slice.
+// Phase 2: the depthwise outputs of all C channels for the 16 pixels into
+// LDS (t[c][16]); a thread computes PX adjacent pixels of one channel with
+// that channel's taps in registers and reads each halo row once (16-byte
+// reads where PX * sw is a multiple of 4; the channel pitch is 4 mod 64
+// floats, so 16 lanes on 16 channels cover the 64 banks once).
 // Phase 3: each wave runs the pointwise chain of its 16 channels with
 // v_mfma_f32_16x16x4f32, both operands from LDS.  LDS is sized per launch.
 #include "qph_internal.h"
@@ -26,7 +30,7 @@ namespace qph {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define DWPW_MAX_C 256
-#define DWPW_MAX_HALO 16384   // floats of input halo per workgroup (64 KB)
+#define DWPW_MAX_HALO 20480   // floats of input halo per workgroup (80 KB)
 #define DWPW_MSLICE 64        // output channels per workgroup
 
 struct DwPwK {
@@ -41,15 +45,16 @@ struct DwPwK {
   Act act_p;
   float* y;
   int trans_out;
-  int ct;            // halo columns: 15 * sw + kw
+  int ct;            // halo row pitch: 15 * sw + kw rounded up to 4
+  int ctr;           // halo columns read from the image: 15 * sw + kw
   int tiles_x;       // 16-pixel tiles per output row
   int slices;        // 64-channel slices of M
   int halo, wrows;   // LDS floats of the halo and of the weight slice
   int wdl_pad;       // LDS floats of the depthwise weights (rounded to 64)
-  int pcp;           // LDS floats per channel of the halo (KH * ct rounded to 64)
+  int pcp;           // LDS floats per channel of the halo (KH * ct rounded to 64, + 4)
 };
 
-template <int KH, int KW>
+template <int KH, int KW, int SW, int PX>
 __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   extern __shared__ float lds[];
   float* halo = lds;                 // [c][KH][ct]
@@ -81,7 +86,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
       const int q = 64 * j + lane;
       const int r = q / p.ct, col = q - r * p.ct;
       const int iy = iy0 + r, ix = ix0 + col;
-      const bool ok = q < per_c && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+      const bool ok = q < per_c && col < p.ctr && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
       voff[j] = ok ? (unsigned)((iy * p.w + ix) * 4) : OOB;
     }
     for (int ci = wave; ci < p.c; ci += 4) {
@@ -121,24 +126,71 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     __syncthreads();
   }
 
-  // phase 2: depthwise outputs of every channel for the 16 pixels
+  // phase 2: depthwise outputs of every channel for the 16 pixels; task e =
+  // (part, channel): pixels part * PX .. part * PX + PX - 1 of channel ci
   const int npx = p.oh * p.ow;
-  for (int e = tid; e < p.cpad * 16; e += 256) {
-    const int ci = e >> 4, pi = e & 15;
-    float v = 0.0f;
-    if (ci < p.c && ox0 + pi < p.ow) {
-      const float* hp = halo + ci * p.pcp + pi * p.sw;
-      const float* wp = wdl + ci * KH * KW;
-      float acc = 0.0f;
+  {
+    constexpr int NC = (PX - 1) * SW + KW;   // halo columns of a task's row
+    constexpr bool V4 = (PX * SW) % 4 == 0;  // row start 16-byte aligned
+    constexpr int NV = (NC + 3) / 4;
+    constexpr int NR = V4 ? 4 * NV : NC;
+    const int ntask = p.cpad * (16 / PX);
+    for (int e = tid; e < ntask; e += 256) {
+      const int part = e / p.cpad;
+      const int ci = e - part * p.cpad;
+      const int px0 = part * PX;
+      float acc[PX];
 #pragma unroll
-      for (int ky = 0; ky < KH; ky++)
+      for (int q = 0; q < PX; q++) acc[q] = 0.0f;
+      if (ci < p.c) {
+        float wv[KH * KW];
+        const float* wp = wdl + ci * KH * KW;
 #pragma unroll
-        for (int kx = 0; kx < KW; kx++)
-          acc = __builtin_fmaf(wp[ky * KW + kx], hp[ky * p.ct + kx], acc);
-      v = acc + (p.bd ? wdl[p.wdl_pad + ci] : 0.0f);
-      v = act_apply(v, p.act_d);
+        for (int j = 0; j < KH * KW; j++) wv[j] = wp[j];
+        const float* hp = halo + ci * p.pcp + px0 * SW;
+#pragma unroll
+        for (int ky = 0; ky < KH; ky++) {
+          float r[NR];
+          const float* rp = hp + ky * p.ct;
+          if constexpr (V4) {
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+              const f32x4 t4 = *(const f32x4*)(rp + 4 * v);
+              r[4 * v] = t4[0];
+              r[4 * v + 1] = t4[1];
+              r[4 * v + 2] = t4[2];
+              r[4 * v + 3] = t4[3];
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < NC; j++) r[j] = rp[j];
+          }
+#pragma unroll
+          for (int kx = 0; kx < KW; kx++)
+#pragma unroll
+            for (int q = 0; q < PX; q++)
+              acc[q] = __builtin_fmaf(wv[ky * KW + kx], r[q * SW + kx], acc[q]);
+        }
+      }
+      float o[PX];
+#pragma unroll
+      for (int q = 0; q < PX; q++) {
+        float v = 0.0f;
+        if (ci < p.c && ox0 + px0 + q < p.ow) {
+          v = acc[q] + (p.bd ? wdl[p.wdl_pad + ci] : 0.0f);
+          v = act_apply(v, p.act_d);
+        }
+        o[q] = v;
+      }
+      float* tp = t + ci * 16 + px0;
+      if constexpr (PX % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < PX; q += 4) *(f32x4*)(tp + q) = f32x4{o[q], o[q + 1], o[q + 2], o[q + 3]};
+      } else {
+#pragma unroll
+        for (int q = 0; q < PX; q++) tp[q] = o[q];
+      }
     }
-    t[e] = v;
   }
   __syncthreads();
 
@@ -197,17 +249,43 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   }
 }
 
-// halo per channel: KH rows of 15 * sw + KW columns, in one or two loads
-static int halo_per_c(const DwPwArgs& a) { return (int)(a.kh * (15 * a.sw + a.kw)); }
-static int halo_floats(const DwPwArgs& a) {
-  return (int)(a.c * ((halo_per_c(a) + 63) / 64 * 64));
-}
+// halo row pitch: 15 * sw + KW columns rounded up to 4 (16-byte rows)
+static int halo_ct(const DwPwArgs& a) { return (int)((15 * a.sw + a.kw + 3) / 4 * 4); }
+// halo per channel: KH rows, in one or two loads
+static int halo_per_c(const DwPwArgs& a) { return (int)(a.kh * halo_ct(a)); }
+// channel pitch 4 mod 64 floats: 16 lanes reading 16 consecutive channels
+// 16 bytes each hit the 64 banks once
+static int halo_pcp(const DwPwArgs& a) { return (halo_per_c(a) + 63) / 64 * 64 + 4; }
+static int halo_floats(const DwPwArgs& a) { return (int)(a.c * halo_pcp(a)); }
+// pixels per depthwise task: about one task per thread
+static int dw_px(int64_t cpad) { return cpad >= 128 ? 8 : cpad >= 64 ? 4 : cpad >= 32 ? 2 : 1; }
 
 bool dwpw_eligible(const DwPwArgs& a) {
   return ((a.kh == 3 && a.kw == 3) || (a.kh == 5 && a.kw == 5)) && a.c > 0 &&
-         a.c <= DWPW_MAX_C && a.m > 0 && a.n <= 65535 && a.sw <= 4 && halo_per_c(a) <= 128 &&
-         halo_floats(a) <= DWPW_MAX_HALO && a.c * a.h * a.w * 4 < (int64_t)0x80000000 &&
-         a.oh * a.ow < (1ll << 30) && (a.m + 31) / 32 * 32 * ((a.c + 3) / 4 * 4) * 4 < (1ll << 31);
+         a.c <= DWPW_MAX_C && a.m > 0 && a.n <= 65535 && (a.sw == 1 || a.sw == 2) &&
+         halo_per_c(a) <= 128 && halo_floats(a) <= DWPW_MAX_HALO &&
+         a.c * a.h * a.w * 4 < (int64_t)0x80000000 && a.oh * a.ow < (1ll << 30) &&
+         (a.m + 31) / 32 * 32 * ((a.c + 3) / 4 * 4) * 4 < (1ll << 31);
+}
+
+template <int KH, int KW, int SW, int PX>
+static int launch_dwpw_t(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
+  // the widest halo row read of a task stays inside its channel's pitch
+  static_assert((16 - PX) * SW + 4 * (((PX - 1) * SW + KW + 3) / 4) <= (15 * SW + KW + 3) / 4 * 4 + 4,
+                "depthwise row reads past the halo row");
+  QPH_TRY(allow_full_lds((const void*)dwpw_kernel<KH, KW, SW, PX>));
+  hipLaunchKernelGGL((dwpw_kernel<KH, KW, SW, PX>), grid, dim3(256), lds, s, p);
+  return launch_check("dwpw_kernel");
+}
+
+template <int KH, int KW, int SW>
+static int launch_dwpw_px(int px, dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
+  switch (px) {
+    case 8: return launch_dwpw_t<KH, KW, SW, 8>(grid, lds, p, s);
+    case 4: return launch_dwpw_t<KH, KW, SW, 4>(grid, lds, p, s);
+    case 2: return launch_dwpw_t<KH, KW, SW, 2>(grid, lds, p, s);
+    default: return launch_dwpw_t<KH, KW, SW, 1>(grid, lds, p, s);
+  }
 }
 
 int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
@@ -222,10 +300,11 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
   p.seed_rule = a.seed_rule;
   p.act_p = a.act_p;
   p.y = a.y; p.trans_out = a.trans_out;
-  p.ct = (int)(15 * a.sw + a.kw);
+  p.ct = halo_ct(a);
+  p.ctr = (int)(15 * a.sw + a.kw);
   p.tiles_x = (int)ceil_div(a.ow, 16);
   p.slices = (int)ceil_div(a.m, DWPW_MSLICE);
-  p.pcp = (halo_per_c(a) + 63) / 64 * 64;
+  p.pcp = halo_pcp(a);
   p.halo = halo_floats(a);
   p.wrows = p.cpad * 64;
   p.wdl_pad = (int)((a.c * a.kh * a.kw + 63) / 64 * 64);
@@ -234,13 +313,10 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
   const int64_t tiles = (int64_t)p.tiles_x * a.oh;
   if (tiles >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "dw+pw block: grid too large");
   dim3 grid((unsigned)tiles, (unsigned)p.slices, (unsigned)a.n);
-  const void* fn = a.kh == 3 ? (const void*)dwpw_kernel<3, 3> : (const void*)dwpw_kernel<5, 5>;
-  QPH_TRY(allow_full_lds(fn));
-  if (a.kh == 3)
-    hipLaunchKernelGGL((dwpw_kernel<3, 3>), grid, dim3(256), lds, s, p);
-  else
-    hipLaunchKernelGGL((dwpw_kernel<5, 5>), grid, dim3(256), lds, s, p);
-  return launch_check("dwpw_kernel");
+  const int px = dw_px(p.cpad);
+  if (a.kh == 5) return launch_dwpw_px<5, 5, 1>(px, grid, lds, p, s);
+  if (a.sw == 1) return launch_dwpw_px<3, 3, 1>(px, grid, lds, p, s);
+  return launch_dwpw_px<3, 3, 2>(px, grid, lds, p, s);
 }
 
 }  // namespace qph

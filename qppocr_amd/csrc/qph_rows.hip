@@ -330,7 +330,10 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
   float s = 0.0f;   // chain of lane j = lane (lanes 0-7 of wave 0)
   if (nwin > 0) put(0);
   __syncthreads();
-  for (int w = 0; w < nwin; w++) {
+  // fully unrolled, so put() picks its registers statically
+#pragma unroll
+  for (int w = 0; w < SM_REG_MAX_COLS / SM_WIN; w++) {
+    if (w >= nwin) continue;   // uniform
     if (w + 1 < nwin) put(w + 1);
     if (wave == 0 && lane < 8) {
       const float* ej = win[w & 1] + lane * SM_WIN_PITCH;
@@ -416,11 +419,143 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
   }
 }
 
+// Rows of up to 19008 floats (the rec head, 18709): registers as in
+// softmax_reg_kernel, but all the exponentials of the full part go to LDS at
+// once, in the chain layout (element 8t + j at j * SM_TP + t; a wave's
+// writes hit 64 distinct banks, a chain lane reads four terms per
+// ds_read_b128), so the eight lane chains run in one pass with a single
+// barrier before it.  Wave 0 then forms the sum itself (the reference's
+// pairwise tree of the chains, then the tail in order).  76 KB of LDS: two
+// workgroups per CU.  Same operation sequence as softmax_rows_kernel.
+#define SM_TP 2376                      // floats per chain lane (8 mod 64)
+#define SM_LDS_MAX_COLS (8 * SM_TP)     // 19008
+#define SM_LDS_PER_THREAD 38            // ceil(SM_LDS_MAX_COLS / 512)
+
+__global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, int cols, int ld,
+                                                          float* probs, float* pairs) {
+  __shared__ __attribute__((aligned(16))) float tr[8 * SM_TP];
+  __shared__ float tail[8];
+  __shared__ float red[8];
+  __shared__ int redi[8];
+  __shared__ float total;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t row = blockIdx.x;
+  const int nu = (cols - tid + 511) >> 9;   // this thread's elements: u < nu
+  float e[SM_LDS_PER_THREAD];
+  {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(logits + row * ld), 0, cols * 4, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < SM_LDS_PER_THREAD; u++)
+      e[u] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(r, (unsigned)(tid + 512 * u) * 4u, 0, 0));
+  }
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < SM_LDS_PER_THREAD; u++) mx = u < nu ? fmaxf(mx, e[u]) : mx;
+  mx = block_max_512(mx, red);
+#pragma unroll
+  for (int u = 0; u < SM_LDS_PER_THREAD; u++) e[u] = exp1(e[u] - mx);
+
+  const int full = cols >= 8 ? (cols / 8) * 8 : 0;
+  const int t8 = full >> 3;
+  {
+    // element i = tid + 512 u: chain lane i & 7 = tid & 7, term i >> 3
+    float* tp = tr + (tid & 7) * SM_TP + (tid >> 3);
+#pragma unroll
+    for (int u = 0; u < SM_LDS_PER_THREAD; u++) {
+      const int i = tid + 512 * u;
+      if (i < full)
+        tp[64 * u] = e[u];
+      else if (u < nu)
+        tail[i - full] = e[u];
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float s = 0.0f;   // chain of lane j = lane (lanes 0-7)
+    if (lane < 8) {
+      const float* ej = tr + lane * SM_TP;
+      int t = 0;
+      for (; t + 32 <= t8; t += 32) {
+        f32x4 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = *(const f32x4*)(ej + t + 4 * q);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          s = s + v[q][0];
+          s = s + v[q][1];
+          s = s + v[q][2];
+          s = s + v[q][3];
+        }
+      }
+      for (; t < t8; t++) s = s + ej[t];
+    }
+    // ((s0 + s4) + (s1 + s5)) + ((s2 + s6) + (s3 + s7)) in lane 0
+    const float a = s + __shfl_down(s, 4, 64);   // lane j < 4: s_j + s_(j+4)
+    const float b = a + __shfl_down(a, 1, 64);   // lane 0: a0 + a1, lane 2: a2 + a3
+    const float c = b + __shfl_down(b, 2, 64);   // lane 0: (a0 + a1) + (a2 + a3)
+    if (lane == 0) {
+      float sum = cols >= 8 ? c : 0.0f;
+      for (int i = 0; i < cols - full; i++) sum = sum + tail[i];   // tail, in order
+      total = sum;
+    }
+  }
+  __syncthreads();
+  const float inv = 1.0f / total;
+  float* pr = probs + row * cols;
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < SM_LDS_PER_THREAD; u++) {
+    if (u < nu) {
+      const int i = tid + 512 * u;
+      const float p = e[u] * inv;
+      pr[i] = p;
+      if (p > bv) {  // ascending i per thread: keeps the first strict max
+        bv = p;
+        bi = i;
+      }
+    }
+  }
+  if (!pairs) return;
+  for (int off = 32; off >= 1; off >>= 1) {
+    float ov = __shfl_xor(bv, off, 64);
+    int oi = __shfl_xor(bi, off, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    red[wave] = bv;
+    redi[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float v = red[0];
+    int ix = redi[0];
+    for (int w = 1; w < 8; w++)
+      if (red[w] > v || (red[w] == v && redi[w] < ix)) {
+        v = red[w];
+        ix = redi[w];
+      }
+    pairs[2 * row] = v;
+    pairs[2 * row + 1] = __uint_as_float((unsigned)ix);
+  }
+}
+
 // logits rows ld floats apart (ld >= cols); probs contiguous.
 static int launch_softmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
                           float* probs, float* pairs, hipStream_t s) {
   if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
   if (ld < cols) return fail(QPH_EINVAL, "softmax: row pitch below the row width");
+  if (cols <= SM_LDS_MAX_COLS && ld < (1ll << 31)) {
+    hipLaunchKernelGGL(softmax_lds_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
+                       (int)cols, (int)ld, probs, pairs);
+    return launch_check("softmax_lds_kernel");
+  }
   if (cols <= SM_REG_MAX_COLS && ld < (1ll << 31)) {
     hipLaunchKernelGGL(softmax_reg_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
                        (int)cols, (int)ld, probs, pairs);

@@ -286,7 +286,7 @@ def test_matmul_batched(gpu, oracle):
     assert_bitexact(_n(ops.matmul(_t(torch, a), _t(torch, b))), oracle.matmul(a, b), "batched B")
 
 
-@pytest.mark.parametrize("inner", [1, 4, 7, 8, 13, 40, 100, 4099, 18709, 40000])
+@pytest.mark.parametrize("inner", [1, 4, 7, 8, 13, 40, 100, 4099, 18709, 19007, 19008, 19009, 20480, 40000])
 def test_softmax_last_dim(gpu, oracle, inner):
     torch = gpu
     from qppocr_amd import ops
