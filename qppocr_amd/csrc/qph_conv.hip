@@ -936,70 +936,73 @@ int launch_convt2x2(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, 
   return launch_check("convt2x2_kernel");
 }
 
-// Det head tail: ConvT(C->M1) -> ConvT(M1->1) -> Sigmoid in one pass.  One
-// thread per input pixel: the 2x2 block of the first ConvT (rounded to f32,
-// as the intermediate tensor is) feeds a 2x2 block each of the second, so
-// one input pixel produces a 4x4 block of the output.  Weights are read with
-// wave-uniform (scalar) loads.
+// Det head tail: ConvT(C->M1) -> ConvT(M1->1) -> Sigmoid in one pass.  An
+// input pixel's first ConvT gives a 2x2 block of the intermediate (rounded to
+// f32, as the intermediate tensor is); each of those four pixels feeds a 2x2
+// block of the second, so one input pixel produces a 4x4 output block.  Wave
+// q of a workgroup takes tap q = 2ky + kx of the first ConvT for 64 input
+// pixels: its weights are then the same for every lane (scalar loads), and
+// it writes the 2x2 output block at (2ky, 2kx) of each pixel's 4x4 block.
 template <int C, int M1>
 __global__ __launch_bounds__(256) void convt_pair_sigmoid_kernel(const float* __restrict__ x,
                                                                  int64_t h, int64_t w,
                                                                  const float* __restrict__ w1,
                                                                  const float* __restrict__ w2,
                                                                  float* __restrict__ y) {
-  // weights staged once per workgroup; every lane reads the same LDS word
-  // (broadcast), four taps at a time
-  __shared__ f32x4 sw1[C * M1];
-  __shared__ f32x4 sw2[M1];
-  for (int i = threadIdx.x; i < C * M1; i += blockDim.x)
-    sw1[i] = f32x4{w1[4 * i], w1[4 * i + 1], w1[4 * i + 2], w1[4 * i + 3]};
-  for (int i = threadIdx.x; i < M1; i += blockDim.x)
-    sw2[i] = f32x4{w2[4 * i], w2[4 * i + 1], w2[4 * i + 2], w2[4 * i + 3]};
+  static_assert(C % 4 == 0, "whole 16-byte weight rows");
+  // weights staged per workgroup as [q][co][ci] (w1, ONNX [ci][co][2][2]) and
+  // [co][q2] (w2): a wave reads its tap's rows with broadcast 16-byte reads
+  __shared__ __attribute__((aligned(16))) float sw1[4 * M1 * C];
+  __shared__ __attribute__((aligned(16))) float sw2[M1 * 4];
+  for (int i = threadIdx.x; i < C * M1 * 4; i += 256) {
+    const int ci = i / (M1 * 4), co = (i >> 2) % M1, tq = i & 3;
+    sw1[(tq * M1 + co) * C + ci] = w1[i];
+  }
+  for (int i = threadIdx.x; i < M1 * 4; i += 256) sw2[i] = w2[i];
   __syncthreads();
-  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t hw = h * w;
+  const int64_t pix = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
   const int64_t bn = blockIdx.y;
-  if (pix >= h * w) return;
+  if (pix >= hw) return;
   const int64_t iy = pix / w, ix = pix - iy * w;
   float xv[C];
-  const float* xn = x + bn * C * h * w + pix;
+  const float* xn = x + bn * C * hw + pix;
 #pragma unroll
-  for (int ci = 0; ci < C; ci++) xv[ci] = xn[ci * h * w];
-  // first ConvT: mid[co][q] = chain over ci of fma(x[ci], w1[ci][co][q], acc)
-  f32x4 mid[M1];
+  for (int ci = 0; ci < C; ci++) xv[ci] = xn[ci * hw];
+  // first ConvT, tap q: mid[co] = chain over ci of fma(x[ci], w1[ci][co][q], acc)
+  float mid[M1];
+  const float* wq = sw1 + q * M1 * C;
 #pragma unroll
   for (int co = 0; co < M1; co++) {
-    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+    float a = 0.0f;
 #pragma unroll
-    for (int ci = 0; ci < C; ci++) {
-      const f32x4 wv = sw1[ci * M1 + co];
-      a[0] = __builtin_fmaf(xv[ci], wv[0], a[0]);
-      a[1] = __builtin_fmaf(xv[ci], wv[1], a[1]);
-      a[2] = __builtin_fmaf(xv[ci], wv[2], a[2]);
-      a[3] = __builtin_fmaf(xv[ci], wv[3], a[3]);
+    for (int c4 = 0; c4 < C; c4 += 4) {
+      const f32x4 wv = *(const f32x4*)(wq + co * C + c4);
+      a = __builtin_fmaf(xv[c4], wv[0], a);
+      a = __builtin_fmaf(xv[c4 + 1], wv[1], a);
+      a = __builtin_fmaf(xv[c4 + 2], wv[2], a);
+      a = __builtin_fmaf(xv[c4 + 3], wv[3], a);
     }
     mid[co] = a;
   }
-  // second ConvT on each of the four intermediate pixels, then Sigmoid
-  const int64_t ow = 4 * w;
-  float* yo = y + (bn * 4 * h + 4 * iy) * ow + 4 * ix;
+  // second ConvT on that intermediate pixel (chain over co), then Sigmoid
+  f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int ky = q >> 1, kx = q & 1;
-    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int co = 0; co < M1; co++) {
-      const f32x4 wv = sw2[co];
-      a[0] = __builtin_fmaf(mid[co][q], wv[0], a[0]);
-      a[1] = __builtin_fmaf(mid[co][q], wv[1], a[1]);
-      a[2] = __builtin_fmaf(mid[co][q], wv[2], a[2]);
-      a[3] = __builtin_fmaf(mid[co][q], wv[3], a[3]);
-    }
-#pragma unroll
-    for (int q2 = 0; q2 < 4; q2++) {
-      const int oy = 2 * ky + (q2 >> 1), ox = 2 * kx + (q2 & 1);
-      yo[oy * ow + ox] = sigmoid1(a[q2]);
-    }
+  for (int co = 0; co < M1; co++) {
+    const f32x4 wv = *(const f32x4*)(sw2 + co * 4);
+    o[0] = __builtin_fmaf(mid[co], wv[0], o[0]);
+    o[1] = __builtin_fmaf(mid[co], wv[1], o[1]);
+    o[2] = __builtin_fmaf(mid[co], wv[2], o[2]);
+    o[3] = __builtin_fmaf(mid[co], wv[3], o[3]);
   }
+  const int ky = q >> 1, kx = q & 1;
+  const int64_t ow = 4 * w;
+  float* yo = y + (bn * 4 * h + 4 * iy + 2 * ky) * ow + 4 * ix + 2 * kx;
+  yo[0] = sigmoid1(o[0]);
+  yo[1] = sigmoid1(o[1]);
+  yo[ow] = sigmoid1(o[2]);
+  yo[ow + 1] = sigmoid1(o[3]);
 }
 
 // generic-size fallback of the pair kernel (C, M1 <= 64)
@@ -1036,11 +1039,15 @@ int launch_convt2x2_pair_sigmoid(const float* x, int64_t n, int64_t c, int64_t h
                                  const float* w1, int64_t m1, const float* w2, float* y,
                                  hipStream_t s) {
   if (n > 65535) return fail(QPH_EUNSUPPORTED, "convT pair: batch too large");
-  dim3 grid(ceil_div(h * w, 256), (unsigned)n);
-  if (c == 24 && m1 == 24)
+  if (c == 24 && m1 == 24) {
+    // 64 input pixels per workgroup, one wave per first-ConvT tap
+    if (ceil_div(h * w, 64) >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "convT pair: grid too large");
+    dim3 grid((unsigned)ceil_div(h * w, 64), (unsigned)n);
     hipLaunchKernelGGL((convt_pair_sigmoid_kernel<24, 24>), grid, dim3(256), 0, s, x, h, w, w1, w2, y);
-  else
+  } else {
+    dim3 grid(ceil_div(h * w, 256), (unsigned)n);
     hipLaunchKernelGGL(convt_pair_sigmoid_generic, grid, dim3(256), 0, s, x, c, h, w, w1, m1, w2, y);
+  }
   return launch_check("convt_pair_sigmoid_kernel");
 }
 
