@@ -281,6 +281,15 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
     acc[v] = s0;
   }
 
+  // epilogue operands (bias, residual) fetched now, their latency under the
+  // k-loop's
+  float* C = g.c + bz * g.c_batch;
+  const float* R = g.res ? g.res + bz * g.r_batch : nullptr;
+  EpiIn e[4];
+  const int64_t rc = R ? res_col(g, jj + l16) : 0;
+#pragma unroll
+  for (int v = 0; v < 4; v++) e[v] = epilogue_gather(g, R, ii + 4 * lg + v, jj + l16, rc);
+
   const int64_t nk = (K + SK_BK - 1) / SK_BK;
   load(0);
   store(0);
@@ -296,19 +305,17 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
     for (int q = 0; q < 4; q++) av[q] = *(const f32x4*)(a_s + 4 * q);
 #pragma unroll
     for (int st = 0; st < 16; st++) bv[st] = b_s[4 * st * SK_PB];
+    // only the k-steps that hold real k (the chain takes no padding terms
+    // while K is a multiple of 4)
+    const int64_t steps = min((int64_t)16, (K - t * SK_BK + 3) / 4);
 #pragma unroll
     for (int st = 0; st < 16; st++)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st >> 2][st & 3], bv[st], acc, 0, 0, 0);
+      if (st < steps)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st >> 2][st & 3], bv[st], acc, 0, 0, 0);
     if (t + 1 < nk) store(buf ^ 1);
     __syncthreads();
   }
 
-  float* C = g.c + bz * g.c_batch;
-  const float* R = g.res ? g.res + bz * g.r_batch : nullptr;
-  EpiIn e[4];
-  const int64_t rc = R ? res_col(g, jj + l16) : 0;
-#pragma unroll
-  for (int v = 0; v < 4; v++) e[v] = epilogue_gather(g, R, ii + 4 * lg + v, jj + l16, rc);
 #pragma unroll
   for (int v = 0; v < 4; v++) epilogue_put(g, C, R != nullptr, e[v], ii + 4 * lg + v, jj + l16, acc[v]);
 }
