@@ -515,7 +515,7 @@ static int launch_direct3x3(const ConvArgs& a, const float* wk, hipStream_t s) {
   };
   int mt = 1, nt = 1;
   if (a.m > 16 && waves(2, 2) >= 4096) { mt = 2; nt = 2; }
-  else if (a.m > 16 && waves(2, 1) >= 2048) { mt = 2; nt = 1; }
+  else if (a.m > 16 && waves(2, 1) >= 512) { mt = 2; nt = 1; }   // det head 96->24 at 160x160: 1600
   else if (waves(1, 2) >= 4096) { mt = 1; nt = 2; }
   p.units_m = (int)ceil_div(a.m, 16 * mt);
   p.units_px = (int)ceil_div(npx, 16 * nt);
