@@ -551,6 +551,9 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int 
 #define WV_AL (WV_A / 64)   // A-slab loads (words / 64 lanes)
 #define WV_BL (WV_B / 64)   // B-slab loads
 
+// ROWS: the row-store epilogue (whole 64-row blocks, 16-byte aligned output
+// rows); otherwise each lane stores its own 64 values.
+template <bool ROWS>
 __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int nb, int ntiles,
                                                        int per_xcd, int wg_xcd) {
   __shared__ __attribute__((aligned(16))) float lds[2 * WV_STAGE];
@@ -608,6 +611,7 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
   corner(tile, bz, i0, j0);
   int st = 0;
   issue(bz, i0, j0, 0, st);
+  bool stored = false;   // the previous tile's 16 row stores follow this slab's loads
   while (true) {
     f32x16 acc[2][2];
 #pragma unroll
@@ -620,9 +624,14 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
     int nbz = 0, ni0 = 0, nj0 = 0;
     if (next < t_end) corner(next, nbz, ni0, nj0);
     for (int kt = 0; kt < nk; kt++) {
-      // this wave's loads of slab kt (and its earlier stores) are done; its
-      // reads of slab kt - 1 are done too, so that stage takes slab kt + 1
-      __builtin_amdgcn_s_waitcnt(0);
+      // this wave's loads of slab kt are done (the previous tile's row
+      // stores, issued after them, may still be draining); its reads of slab
+      // kt - 1 are done too, so that stage takes slab kt + 1
+      if (ROWS && kt == 0 && stored)
+        wait_vmcnt<16>();
+      else
+        wait_vmcnt<0>();
+      __builtin_amdgcn_s_waitcnt(0xC07F);
       __asm__ volatile("" ::: "memory");
       if (kt + 1 < nk)
         issue(bz, i0, j0, kt + 1, st ^ 1);
@@ -655,24 +664,67 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
       __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
       st ^= 1;
     }
-    // column bias or none (a term of -0.0 leaves every value unchanged)
+    // column bias or none (a term of -0.0 leaves every value unchanged).
+    // The tile goes out as rows: each 32-row half through the stage the last
+    // slab came from (pitch 72: a write's two row groups and a read's rows
+    // fall on distinct banks), then 16-byte stores, four rows of 64 columns
+    // per instruction.
     float* C = g.c + (int64_t)bz * g.c_batch;
+    float badd[2];
 #pragma unroll
-    for (int mi = 0; mi < 2; mi++)
+    for (int ni = 0; ni < 2; ni++) {
+      const int j = j0 + ni * 32 + lr;
+      badd[ni] = g.bias_mode == 2 && j < N ? g.bias[j] : -0.0f;
+    }
+    if constexpr (!ROWS) {
 #pragma unroll
-      for (int ni = 0; ni < 2; ni++) {
-        const int j = j0 + ni * 32 + lr;
-        const int ib = i0 + mi * 32 + 4 * lh;
-        if (j < N) {
-          const float badd = g.bias_mode == 2 ? g.bias[j] : -0.0f;
-          float* cj = C + j;
+      for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-          for (int v = 0; v < 16; v++) {
-            const int i = ib + 8 * (v >> 2) + (v & 3);
-            if (i < M) cj[(int64_t)i * g.ldc] = acc[mi][ni][v] + badd;
+        for (int ni = 0; ni < 2; ni++) {
+          const int j = j0 + ni * 32 + lr;
+          const int ib = i0 + mi * 32 + 4 * lh;
+          if (j < N) {
+            float* cj = C + j;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+              const int i = ib + 8 * (v >> 2) + (v & 3);
+              if (i < M) cj[(int64_t)i * g.ldc] = acc[mi][ni][v] + badd[ni];
+            }
+          }
+        }
+    } else {
+    float* sc = lds + (st ^ 1) * WV_STAGE;   // the stage of slab nk - 1
+    const int rr = lane >> 4, c4 = (lane & 15) * 4;
+    const int jc = j0 + c4;
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++) {
+      // (the reads of the previous half / slab are back before the writes)
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+          sc[(8 * (v >> 2) + 4 * lh + (v & 3)) * 72 + ni * 32 + lr] = acc[mi][ni][v] + badd[ni];
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+      for (int it = 0; it < 8; it++) {
+        const int r = 4 * it + rr;
+        const int i = i0 + mi * 32 + r;
+        const f32x4 val = *(const f32x4*)(sc + r * 72 + c4);
+        float* cp = C + (int64_t)i * g.ldc + jc;
+        if (i < M) {
+          if (jc + 4 <= N) {
+            *(f32x4*)cp = val;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+              if (jc + q < N) cp[q] = val[q];
           }
         }
       }
+    }
+    }
+    stored = true;
     if (next >= t_end) break;
     tile = next;
     bz = nbz;
@@ -688,7 +740,7 @@ static int launch_wave(const GemmArgs& g, hipStream_t s) {
     return fail(QPH_EHIP, "gemm: no current device (or index past 63)");
   if (occ_dev[dev] == 0) {
     int occ = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)gemm_wave_kernel, 64, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)gemm_wave_kernel<true>, 64, 0) !=
             hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         occ <= 0 || cus <= 0)
@@ -700,8 +752,16 @@ static int launch_wave(const GemmArgs& g, hipStream_t s) {
   const int ntiles = mb * nb * (int)g.batch;
   const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
   const int wg_xcd = std::max(1, std::min(per_xcd, occ_dev[dev] * cus_dev[dev] / NUM_XCD));
-  hipLaunchKernelGGL(gemm_wave_kernel, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s, g, mb,
-                     nb, ntiles, per_xcd, wg_xcd);
+  // whole 64-row blocks: every tile issues its 16 row stores, which the
+  // next tile's first wait counts on; 16-byte aligned output rows
+  const bool rows = g.m % 64 == 0 && g.ldc % 4 == 0 && (uintptr_t)g.c % 16 == 0 &&
+                    g.c_batch % 4 == 0;
+  if (rows)
+    hipLaunchKernelGGL(gemm_wave_kernel<true>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s,
+                       g, mb, nb, ntiles, per_xcd, wg_xcd);
+  else
+    hipLaunchKernelGGL(gemm_wave_kernel<false>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s,
+                       g, mb, nb, ntiles, per_xcd, wg_xcd);
   return launch_check("gemm_wave_kernel");
 }
 

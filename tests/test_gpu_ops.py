@@ -243,7 +243,9 @@ def test_gemm_wide_tiles(gpu, oracle):
     """Shapes with >= 512 128x128 tiles take the persistent wide-tile kernel:
     ragged M / N edges, unpadded odd ldb, both bias-seeding rules (row bias),
     GELU + residual epilogue, batched B, and K not a multiple of 16 (which
-    falls back to the 128x128 staged kernel)."""
+    falls back to the 128x128 staged kernel); plain ones (column bias or
+    none) take the one-wave kernel, with its row-store epilogue when the
+    rows come in whole 64-row blocks and 16-byte aligned, batched too."""
     torch = gpu
     from qppocr_amd import ops
     rng = np.random.default_rng(21)
@@ -255,7 +257,10 @@ def test_gemm_wide_tiles(gpu, oracle):
         c_ref = oracle.sgemm(a, b, m, n, k, bias, serial=serial)
         c = ops.sgemm(_t(torch, a), _t(torch, b), m, n, k, _t(torch, bias), serial=serial)
         assert_bitexact(_n(c), c_ref, f"wide sgemm {m}x{n}x{k} serial={serial}")
-    for (rows, k, n, act, res) in [(1290, 32, 8195, 0, False), (1280, 64, 8200, 1, True)]:
+    # (1280, 32, 8196): column bias only, whole 64-row blocks, rows 16-byte
+    # aligned -- the one-wave kernel with its row-store epilogue
+    for (rows, k, n, act, res) in [(1290, 32, 8195, 0, False), (1280, 64, 8200, 1, True),
+                                   (1280, 32, 8196, 0, False)]:
         x = rng.standard_normal((rows, k)).astype(np.float32)
         w = (rng.standard_normal((k, n)) * math.sqrt(2 / k)).astype(np.float32)
         b = (rng.standard_normal((n,)) * 0.1).astype(np.float32)
@@ -268,10 +273,13 @@ def test_gemm_wide_tiles(gpu, oracle):
         y = ops.linear(_t(torch, x), _t(torch, w), _t(torch, b), act,
                        None if r is None else _t(torch, r))
         assert_bitexact(_n(y), y_ref, f"wide linear {rows}x{k}x{n} act={act}")
-    a = rng.uniform(-1, 1, (6, 300, 32)).astype(np.float32)
-    b = rng.uniform(-1, 1, (6, 32, 4100)).astype(np.float32)
-    assert_bitexact(_n(ops.matmul(_t(torch, a), _t(torch, b))), oracle.matmul(a, b),
-                    "wide batched matmul")
+    # both plain, so the one-wave kernel; the second with whole 64-row blocks
+    # and 16-byte rows, so its row-store epilogue
+    for (bt, m, k, n) in [(6, 300, 32, 4100), (6, 320, 32, 4100)]:
+        a = rng.uniform(-1, 1, (bt, m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (bt, k, n)).astype(np.float32)
+        assert_bitexact(_n(ops.matmul(_t(torch, a), _t(torch, b))), oracle.matmul(a, b),
+                        f"wide batched matmul {bt}x{m}x{k}x{n}")
 
 
 def test_matmul_batched(gpu, oracle):
