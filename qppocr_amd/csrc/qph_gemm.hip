@@ -533,6 +533,14 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int 
   }
 }
 
+// 16-byte buffer->LDS load: lane L's four words land at dst + 4L.  (A plain
+// function, so that only the device compile checks the builtin's size.)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, float* dst, unsigned voff,
+                                           int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, soff, 0, 0);
+}
+
 // ------------------------------------------------ one-wave 64x64 tiles
 //
 // The rec head (PLAIN: column bias, no activation / residual / transposed
@@ -549,7 +557,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int 
 #define WV_B (16 * 64)
 #define WV_STAGE (WV_A + WV_B)
 #define WV_AL (WV_A / 64)   // A-slab loads (words / 64 lanes)
-#define WV_BL (WV_B / 64)   // B-slab loads
+#define WV_BL (WV_B / 256)  // B-slab loads (16 bytes a lane: four 64-column rows each)
 
 // ROWS: the row-store epilogue (whole 64-row blocks, 16-byte aligned output
 // rows); otherwise each lane stores its own 64 values.
@@ -576,9 +584,11 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
     aoff[r] = q < 16 ? (unsigned)(m * lda + 2 * (q & 7) + (q >> 3)) * 4u : 0x80000000u;
   }
 #pragma unroll
-  for (int r = 0; r < WV_BL; r++) {
-    // row r holds B[k0 + 2s + h][j0 .. j0 + 63] for r = 8h + s
-    boff[r] = (unsigned)((2 * (r & 7) + (r >> 3)) * ldb + lane) * 4u;
+  for (int u = 0; u < WV_BL; u++) {
+    // row r holds B[k0 + 2s + h][j0 .. j0 + 63] for r = 8h + s; load u
+    // brings rows 4u .. 4u + 3, lane L four columns of row 4u + L / 16
+    const int r = 4 * u + (lane >> 4);
+    boff[u] = (unsigned)((2 * (r & 7) + (r >> 3)) * ldb + 4 * (lane & 15)) * 4u;
   }
   auto corner = [&](int t, int& bz, int& i0, int& j0) {
     const int per_b = mb * nb;
@@ -602,9 +612,7 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           ar, (__attribute__((address_space(3))) void*)(sa + r * 64), 4, aoff[r], 0, 0, 0);
 #pragma unroll
-    for (int r = 0; r < WV_BL; r++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          br, (__attribute__((address_space(3))) void*)(sb + r * 64), 4, boff[r], 0, 0, 0);
+    for (int u = 0; u < WV_BL; u++) lds_load16(br, sb + u * 256, boff[u], 0);
   };
 
   int bz, i0, j0;
@@ -851,13 +859,6 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
 
 #define LT_BK 64
 
-// 16-byte buffer->LDS load: lane L's four words land at dst + 4L.  (A plain
-// function, so that only the device compile checks the builtin's size.)
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, float* dst, unsigned voff,
-                                           int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
-                                           voff, soff, 0, 0);
-}
 
 // NK > 0: K / 64 fixed at compile time, so the slab loop unrolls completely
 // (and each stage's loads and reads stay distinguishable to the compiler's
