@@ -545,18 +545,23 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, float* dst,
 //
 // The rec head (PLAIN: column bias, no activation / residual / transposed
 // store) on workgroups of a single wave, each owning whole 64x64 tiles: the
-// wave loads its own A and B slabs (the same k-deinterleaved A layout and
-// B rows as gemm_wide_kernel, K in slabs of 16, double-buffered), so no
-// workgroup barrier ties its progress to other waves.  Two such waves per
+// wave loads its own A and B slabs (K in slabs of 16, double-buffered), so
+// no workgroup barrier ties its progress to other waves.  Two such waves per
 // SIMD keep the MFMA pipe fed through each other's slab waits, where the
 // four-wave 128x128 tiles stall together at every slab barrier.  Persistent
 // and XCD-aware like gemm_wide_kernel; tiles of 64.
+//
+// Slabs arrive by 16-byte buffer->LDS loads (a slab is 5 + 4 instructions):
+// A as its rows, k in order, 20 words a row (the fifth four-word chunk of a
+// row is padding and reads 0); B as the rows of gemm_wide_kernel (r = 8h + s
+// holds k = 2s + h).  A lane reads its A terms k = 2s + h two words apart
+// (ds_read2) and its B terms one word each.
 
 #define WV_PA 20
 #define WV_A (64 * WV_PA)
 #define WV_B (16 * 64)
 #define WV_STAGE (WV_A + WV_B)
-#define WV_AL (WV_A / 64)   // A-slab loads (words / 64 lanes)
+#define WV_AL (WV_A / 256)  // A-slab loads (16 bytes a lane)
 #define WV_BL (WV_B / 256)  // B-slab loads (16 bytes a lane: four 64-column rows each)
 
 // ROWS: the row-store epilogue (whole 64-row blocks, 16-byte aligned output
@@ -578,10 +583,12 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
   const int a_words = (M - 1) * lda + K, b_words = (K - 1) * ldb + N;
   unsigned aoff[WV_AL], boff[WV_BL];
 #pragma unroll
-  for (int r = 0; r < WV_AL; r++) {
-    const int p = r * 64 + lane;
-    const int m = p / WV_PA, q = p - m * WV_PA;
-    aoff[r] = q < 16 ? (unsigned)(m * lda + 2 * (q & 7) + (q >> 3)) * 4u : 0x80000000u;
+  for (int u = 0; u < WV_AL; u++) {
+    // four-word chunk c = 64u + lane: row c / 5, k 4 (c % 5) .. + 3 (the
+    // fifth chunk of a row is its padding: out of range, reads 0)
+    const int c = u * 64 + lane;
+    const int m = c / 5, q = c - m * 5;
+    aoff[u] = q < 4 ? (unsigned)(m * lda + 4 * q) * 4u : 0x80000000u;
   }
 #pragma unroll
   for (int u = 0; u < WV_BL; u++) {
@@ -608,9 +615,7 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
     float* sa = lds + st * WV_STAGE;
     float* sb = sa + WV_A;
 #pragma unroll
-    for (int r = 0; r < WV_AL; r++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ar, (__attribute__((address_space(3))) void*)(sa + r * 64), 4, aoff[r], 0, 0, 0);
+    for (int u = 0; u < WV_AL; u++) lds_load16(ar, sa + u * 256, aoff[u], 0);
 #pragma unroll
     for (int u = 0; u < WV_BL; u++) lds_load16(br, sb + u * 256, boff[u], 0);
   };
@@ -645,14 +650,16 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
         issue(bz, i0, j0, kt + 1, st ^ 1);
       else if (next < t_end)
         issue(nbz, ni0, nj0, 0, st ^ 1);
-      const float* sa = lds + st * WV_STAGE + lr * WV_PA + lh * 8;
+      const float* sa = lds + st * WV_STAGE + lr * WV_PA + lh;
       const float* sb = lds + st * WV_STAGE + WV_A + lh * 8 * 64 + lr;
       f32x4 ga[2][2];
       float gb[2][2][4];
 #pragma unroll
       for (int gp = 0; gp < 2; gp++) {
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) ga[gp][mi] = *(const f32x4*)(sa + mi * 32 * WV_PA + gp * 4);
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+          for (int u = 0; u < 4; u++) ga[gp][mi][u] = sa[mi * 32 * WV_PA + 2 * (4 * gp + u)];
 #pragma unroll
         for (int ni = 0; ni < 2; ni++)
 #pragma unroll
@@ -818,7 +825,10 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (gemm_takes_wide(g.m, g.n, g.batch)) {
     const double tiles = (double)ceil_div(g.m, 128) * (double)ceil_div(g.n, 128) * (double)g.batch;
     const bool plain = g.act.kind == 0 && g.res == nullptr && !g.trans_out && g.bias_mode != 1;
-    if (plain && wide_fits(g) && tiles < (double)(1u << 28)) return launch_wave(g, s);
+    // (16-byte aligned A rows for the one-wave kernel's slab loads)
+    if (plain && wide_fits(g) && g.lda % 4 == 0 && (uintptr_t)g.a % 16 == 0 &&
+        g.a_batch % 4 == 0 && tiles < (double)(1u << 28))
+      return launch_wave(g, s);
     if (wide_fits(g) && tiles < (double)(1u << 30)) return launch_wide(g, s);
     return launch_cfg<2, 2>(g, s);
   }
