@@ -23,6 +23,19 @@
 // floats, so 16 lanes on 16 channels cover the 64 banks once).
 // Phase 3: each wave runs the pointwise chain of its 16 channels with
 // v_mfma_f32_16x16x4f32, both operands from LDS.  LDS is sized per launch.
+//
+// With the stem in front (STEM, the first block of both nets: stem conv
+// 3 -> C, 3x3 stride 2 pad 1, then a 3x3 stride-2 pad-1 depthwise), the halo
+// is not loaded but computed: phase 1 brings the 3 x 7 x 67 input pixels the
+// tile's 3 x 33 stem outputs read, phase S runs the stem chains on
+// v_mfma_f32_16x16x4f32 (16 stem pixels x 16 channels a block, k = c*9 +
+// ky*3 + kx ascending after one leading 0 * 0 term, so each output is the
+// reference's chain acc = 0; acc = fma(w, x, acc) exactly; taps outside the
+// image read 0), adds the bias, applies the activation and writes the halo,
+// with exact zeros where the depthwise reads its own zero padding.  The stem
+// output never reaches HBM.  Reference for the stem: the Conv node of
+// qppocr-core/src/executor.rs:433-652 over conv.rs:264-460 (the implicit
+// GEMM; bias after the chain), its HardSigmoid + Mul pair as above.
 #include "qph_internal.h"
 
 namespace qph {
@@ -52,15 +65,45 @@ struct DwPwK {
   int halo, wrows;   // LDS floats of the halo and of the weight slice
   int wdl_pad;       // LDS floats of the depthwise weights (rounded to 64)
   int pcp;           // LDS floats per channel of the halo (KH * ct rounded to 64, + 4)
+  // stem (STEM launches only)
+  const float* xin;
+  const float* wst;
+  const float* bst;
+  int hin, win;
+  Act act_s;
 };
 
-template <int KH, int KW, int SW, int PX>
+// stem input region of a tile: 3 channels x 7 rows x 67 columns, rows 68
+// floats apart (a row arrives as a 64-lane load and a 3-lane load: only
+// active lanes write LDS); the stem tile is 3 rows x 33 columns of stem
+// outputs
+#define ST_RR 7
+#define ST_RP 68
+#define ST_IN (3 * ST_RR * ST_RP)
+#define ST_K 28            // 27 taps after one leading zero term
+#define ST_PX 99           // 3 x 33 stem outputs
+#define ST_PB 7            // 16-pixel blocks covering them
+
+// AK = 3: every activation of the launch is the HardSigmoid + Mul pair
+// (both nets' blocks), applied inline; AK = 0: any, through act_apply
+template <int AK>
+__device__ __forceinline__ float act_k(float v, const Act& a) {
+  if constexpr (AK == 3) return v * hsig1(v, a.c1, a.c2);
+  else return act_apply(v, a);
+}
+
+template <int KH, int KW, int SW, int PX, bool STEM, int AK>
 __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   extern __shared__ float lds[];
   float* halo = lds;                 // [c][KH][ct]
   float* wsl = lds + p.halo;         // [cpad][64]
   float* t = wsl + p.wrows;          // [cpad][16]
   float* wdl = t + p.cpad * 16;      // depthwise weights [c][KH*KW], then bias [c]
+  // STEM: input region [3][7][68], stem weights [c][27] (28 c floats of
+  // room), bias [c] (64 floats of room)
+  float* xin = wdl + p.wdl_pad + (p.c + 63) / 64 * 64;
+  float* wsm = xin + ST_IN;
+  float* bsm = wsm + ST_K * p.c;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int img = blockIdx.z;
@@ -79,24 +122,62 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     // issues no vector instructions.  Out-of-image taps keep an
     // out-of-range vector offset (read 0) whatever the scalar offset.
     const int iy0 = oy * p.sh - p.ph, ix0 = ox0 * p.sw - p.pw;
-    const int per_c = KH * p.ct;
-    unsigned voff[2];
+    if constexpr (STEM) {
+      // input rows 2 * iy0 - 1 .., columns 2 * ix0 - 1 .. (the stem is
+      // stride 2, pad 1); a row per (channel, region row), columns 0-63
+      // and 64-66
+      const int64_t iplane = (int64_t)p.hin * p.win;
+      const __amdgpu_buffer_rsrc_t ir = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(p.xin + (int64_t)img * 3 * iplane), 0, (int)(3 * iplane * 4), 0x00020000);
+      const int jy0 = 2 * iy0 - 1, jx0 = 2 * ix0 - 1;
+      for (int cr = wave; cr < 3 * ST_RR; cr += 4) {
+        const int c = cr / ST_RR, rr = cr - c * ST_RR;
+        const int iy = jy0 + rr;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int q = 64 * j + lane;
-      const int r = q / p.ct, col = q - r * p.ct;
-      const int iy = iy0 + r, ix = ix0 + col;
-      const bool ok = q < per_c && col < p.ctr && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
-      voff[j] = ok ? (unsigned)((iy * p.w + ix) * 4) : OOB;
-    }
-    for (int ci = wave; ci < p.c; ci += 4) {
-      const int soff = (int)(ci * plane * 4);
+        for (int j = 0; j < 2; j++) {
+          const int col = 64 * j + lane, ix = jx0 + col;
+          const bool ok = iy >= 0 && iy < p.hin && ix >= 0 && ix < p.win;
+          if (j == 0 || lane < 3)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ir, (__attribute__((address_space(3))) void*)(xin + cr * ST_RP + 64 * j), 4,
+                ok ? (unsigned)(((c * p.hin + iy) * p.win + ix) * 4) : OOB, 0, 0, 0);
+        }
+      }
+      // stem weights in their ONNX layout [c][27] (27 c <= 28 c floats in
+      // whole 64-word loads), the bias in one load (64 floats of room)
+      const int nws = 27 * p.c;
+      const __amdgpu_buffer_rsrc_t swr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)p.wst, 0, nws * 4, 0x00020000);
+      for (int base = wave * 64; base < nws; base += 256)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            swr, (__attribute__((address_space(3))) void*)(wsm + base), 4,
+            (unsigned)(base + lane) * 4u, 0, 0, 0);
+      if (p.bst && wave == 0) {
+        const __amdgpu_buffer_rsrc_t sbr =
+            __builtin_amdgcn_make_buffer_rsrc((void*)p.bst, 0, p.c * 4, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(sbr, (__attribute__((address_space(3))) void*)bsm,
+                                                 4, (unsigned)lane * 4u, 0, 0, 0);
+      }
+    } else {
+      const int per_c = KH * p.ct;
+      unsigned voff[2];
 #pragma unroll
-      for (int j = 0; j < 2; j++)
-        if (64 * j < per_c)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              xr, (__attribute__((address_space(3))) void*)(halo + ci * p.pcp + 64 * j), 4,
-              voff[j], soff, 0, 0);
+      for (int j = 0; j < 2; j++) {
+        const int q = 64 * j + lane;
+        const int r = q / p.ct, col = q - r * p.ct;
+        const int iy = iy0 + r, ix = ix0 + col;
+        const bool ok = q < per_c && col < p.ctr && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+        voff[j] = ok ? (unsigned)((iy * p.w + ix) * 4) : OOB;
+      }
+      for (int ci = wave; ci < p.c; ci += 4) {
+        const int soff = (int)(ci * plane * 4);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          if (64 * j < per_c)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void*)(halo + ci * p.pcp + 64 * j), 4,
+                voff[j], soff, 0, 0);
+      }
     }
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)p.wk, 0, p.cpad * p.mpad * 4, 0x00020000);
@@ -123,6 +204,54 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
             (unsigned)(base + lane) * 4u, 0, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // phase S: the stem outputs of the halo, block (pixel block pb, channel
+  // block cb) per wave task; lane (g, l) feeds stem pixel 16 pb + l's tap
+  // k' = 4 s + g and takes outputs (pixel 16 pb + 4 g + v, channel 16 cb + l)
+  if constexpr (STEM) {
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int sy0 = oy * p.sh - p.ph, sx0 = ox0 * p.sw - p.pw;
+    // tap offsets in the input region, k = k' - 1 = c * 9 + ky * 3 + kx
+    int koff[ST_K / 4];
+#pragma unroll
+    for (int s = 0; s < ST_K / 4; s++) {
+      const int k = 4 * s + lg - 1;
+      const int c = k / 9, ky = (k - 9 * c) / 3, kx = k - 9 * c - 3 * ky;
+      koff[s] = k < 0 ? -1 : (c * ST_RR + ky) * ST_RP + kx;
+    }
+    const int ntask = ST_PB * (p.c / 16);
+    for (int task = wave; task < ntask; task += 4) {
+      const int pb = task % ST_PB, cb = task / ST_PB;
+      const int q = pb * 16 + l16;
+      const int qr = q / 33, qc = q - 33 * qr;
+      const int poff = 2 * qr * ST_RP + 2 * qc;
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < ST_K / 4; s++) {
+        const float a = (koff[s] >= 0 && q < ST_PX) ? xin[koff[s] + poff] : 0.0f;
+        // weight (k', channel): 0 for the leading term, else w[ch][k' - 1]
+        // (27 words apart over the 16 channels: no bank conflict)
+        const float b = koff[s] >= 0 ? wsm[(cb * 16 + l16) * 27 + 4 * s + lg - 1] : 0.0f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+      }
+      const int ch = cb * 16 + l16;
+      const float bias = bsm[ch];
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int qo = pb * 16 + 4 * lg + v;
+        if (qo >= ST_PX) continue;
+        const int ro = qo / 33, co = qo - 33 * ro;
+        const int sy = sy0 + ro, sx = sx0 + co;
+        float val = 0.0f;   // the depthwise's zero padding
+        if (sy >= 0 && sy < p.h && sx >= 0 && sx < p.w) {
+          val = p.bst ? acc[v] + bias : acc[v];
+          val = act_k<AK>(val, p.act_s);
+        }
+        halo[ch * p.pcp + ro * p.ct + co] = val;
+      }
+    }
     __syncthreads();
   }
 
@@ -178,7 +307,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         float v = 0.0f;
         if (ci < p.c && ox0 + px0 + q < p.ow) {
           v = acc[q] + (p.bd ? wdl[p.wdl_pad + ci] : 0.0f);
-          v = act_apply(v, p.act_d);
+          v = act_k<AK>(v, p.act_d);
         }
         o[q] = v;
       }
@@ -241,7 +370,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     if (mo >= p.m) continue;
     float r = acc[v];
     if (hadd[v]) r = r + badd[v];
-    r = act_apply(r, p.act_p);
+    r = act_k<AK>(r, p.act_p);
     if (p.trans_out)
       p.y[((int64_t)img * npx + px) * p.m + mo] = r;
     else
@@ -268,15 +397,23 @@ bool dwpw_eligible(const DwPwArgs& a) {
          (a.m + 31) / 32 * 32 * ((a.c + 3) / 4 * 4) * 4 < (1ll << 31);
 }
 
-template <int KH, int KW, int SW, int PX>
-static int launch_dwpw_t(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
+template <int KH, int KW, int SW, int PX, bool STEM, int AK>
+static int launch_dwpw_a(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
   // the widest halo row read of a task stays inside its channel's pitch
   static_assert((16 - PX) * SW + 4 * (((PX - 1) * SW + KW + 3) / 4) <= (15 * SW + KW + 3) / 4 * 4 + 4,
                 "depthwise row reads past the halo row");
-  QPH_TRY(allow_full_lds((const void*)dwpw_kernel<KH, KW, SW, PX>));
-  hipLaunchKernelGGL((dwpw_kernel<KH, KW, SW, PX>), grid, dim3(256), lds, s, p);
+  QPH_TRY(allow_full_lds((const void*)dwpw_kernel<KH, KW, SW, PX, STEM, AK>));
+  hipLaunchKernelGGL((dwpw_kernel<KH, KW, SW, PX, STEM, AK>), grid, dim3(256), lds, s, p);
   return launch_check("dwpw_kernel");
 }
+
+template <int KH, int KW, int SW, int PX, bool STEM = false>
+static int launch_dwpw_t(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
+  const bool hs = p.act_d.kind == 3 && p.act_p.kind == 3 && (!STEM || p.act_s.kind == 3);
+  return hs ? launch_dwpw_a<KH, KW, SW, PX, STEM, 3>(grid, lds, p, s)
+            : launch_dwpw_a<KH, KW, SW, PX, STEM, 0>(grid, lds, p, s);
+}
+
 
 template <int KH, int KW, int SW>
 static int launch_dwpw_px(int px, dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
@@ -286,6 +423,12 @@ static int launch_dwpw_px(int px, dim3 grid, size_t lds, const DwPwK& p, hipStre
     case 2: return launch_dwpw_t<KH, KW, SW, 2>(grid, lds, p, s);
     default: return launch_dwpw_t<KH, KW, SW, 1>(grid, lds, p, s);
   }
+}
+
+bool dwpw_stem_eligible(const DwPwArgs& a) {
+  return a.stem && a.xin && a.wst && (a.c == 16 || a.c == 32) && a.kh == 3 && a.kw == 3 &&
+         a.sh == 2 && a.sw == 2 && a.ph == 1 && a.pw == 1 && a.h == (a.hin - 1) / 2 + 1 &&
+         a.w == (a.win - 1) / 2 + 1 && 3 * a.hin * a.win * 4 < (int64_t)0x80000000;
 }
 
 int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
@@ -308,12 +451,20 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
   p.halo = halo_floats(a);
   p.wrows = p.cpad * 64;
   p.wdl_pad = (int)((a.c * a.kh * a.kw + 63) / 64 * 64);
-  const size_t lds =
-      (size_t)(p.halo + p.wrows + p.cpad * 16 + p.wdl_pad + (a.c + 63) / 64 * 64) * 4;
+  size_t lds = (size_t)(p.halo + p.wrows + p.cpad * 16 + p.wdl_pad + (a.c + 63) / 64 * 64) * 4;
   const int64_t tiles = (int64_t)p.tiles_x * a.oh;
   if (tiles >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "dw+pw block: grid too large");
   dim3 grid((unsigned)tiles, (unsigned)p.slices, (unsigned)a.n);
   const int px = dw_px(p.cpad);
+  if (a.stem) {
+    if (!dwpw_stem_eligible(a)) return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: unsupported shape");
+    p.xin = a.xin; p.wst = a.wst; p.bst = a.bst; p.act_s = a.act_s;
+    p.hin = (int)a.hin; p.win = (int)a.win;
+    lds += (size_t)(ST_IN + ST_K * a.c + 64) * 4;
+    // cpad 16 -> 1 pixel per depthwise task, 32 -> 2
+    if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true>(grid, lds, p, s);
+    return launch_dwpw_t<3, 3, 2, 1, true>(grid, lds, p, s);
+  }
   if (a.kh == 5) return launch_dwpw_px<5, 5, 1>(px, grid, lds, p, s);
   if (a.sw == 1) return launch_dwpw_px<3, 3, 1>(px, grid, lds, p, s);
   return launch_dwpw_px<3, 3, 2>(px, grid, lds, p, s);

@@ -235,11 +235,21 @@ struct DwPwArgs {
   Act act_p;
   int trans_out;
   float* y;
+  // stem in front (stem != 0): x is then the stem's output, never stored;
+  // the kernel computes it from xin ([n][3][hin][win]) with the 3x3
+  // stride-2 pad-1 conv wst ([c][3][3][3]) + bst, then act_s
+  int stem;
+  const float* xin; int64_t hin, win;
+  const float* wst; const float* bst;
+  Act act_s;
 };
 // Lets kernel fn take up to the whole 160 KB of a CU's LDS as dynamic
 // shared memory; the attribute is set once per kernel and device.
 int allow_full_lds(const void* fn);
 bool dwpw_eligible(const DwPwArgs& a);
+// the stem conv that can run inside the dw + pw launch of a (3 -> a.c
+// channels, 3x3, stride 2, pad 1, into a 3x3 stride-2 pad-1 depthwise)
+bool dwpw_stem_eligible(const DwPwArgs& a);
 int launch_dwpw(const DwPwArgs& a, hipStream_t s);
 // 3x3 convs the direct kernel takes; up to four independent ones in one launch
 bool direct3x3_eligible(const ConvArgs& a);

@@ -22,7 +22,7 @@ struct qph_net {
   std::vector<ConvArgs> plan;    // per node: launch arguments of a dense 3x3 conv
   std::vector<int> group_len;    // > 1: first of that many independent 3x3 convs, one launch
   std::vector<DwPwArgs> dwpw;    // per node: fused depthwise + pointwise launch
-  std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1 with it)
+  std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1, and i + 2 for a stem, with it)
   std::vector<float*> wt;        // per linear node: resident transposed weight Wt[N][K] (or NULL)
   std::vector<bool> cl_dw;       // depthwise conv node run channel-last (in and out)
   std::vector<bool> cl_pw;       // 1x1 conv node run as a row-major GEMM, channel-last in and out
@@ -382,14 +382,40 @@ static int plan_dwpw(qph_net* net) {
     f.trans_out = q.trans_out || net->cl_out[i + 1];
     f.y = net->tptr[q.out];
     if (!dwpw_eligible(f)) continue;
+    // the stem conv in front (3 -> c channels, 3x3 stride 2 pad 1), its
+    // output read by this depthwise only: computed inside the launch
+    size_t at = i;
+    if (i > 0 && storage_of(net, d.in) == d.in && readers[(size_t)d.in] == 1 &&
+        !(i > 1 && net->fused[i - 2])) {
+      const qph_node& st = net->nodes[i - 1];
+      const int64_t* ss = &net->shapes[4 * (size_t)st.in];
+      const bool sok = st.op == QPH_OP_CONV && st.out == d.in && st.cp.group == 1 && ss[1] == 3 &&
+                       st.ws[1] == 3 && st.ws[0] == f.c && st.ws[2] == 3 && st.ws[3] == 3 &&
+                       st.cp.sh == 2 && st.cp.sw == 2 && st.cp.ph == 1 && st.cp.pw == 1 &&
+                       st.cp.dh <= 1 && st.cp.dw <= 1 && st.in2 < 0 && st.res_up == 0 &&
+                       st.trans_out == 0 && !net->cl_out[i - 1] &&
+                       (st.y_ctotal == 0 || st.y_ctotal == st.ws[0]) && st.y_coff == 0 &&
+                       st.y_up <= 1 && net->group_len[i - 1] <= 1;
+      if (sok) {
+        DwPwArgs g = f;
+        g.stem = 1;
+        g.xin = net->tptr[st.in]; g.hin = ss[2]; g.win = ss[3];
+        g.wst = net->weights[st.w]; g.bst = st.bias >= 0 ? net->weights[st.bias] : nullptr;
+        g.act_s = make_act(&st.act);
+        if (ss[0] == f.n && dwpw_stem_eligible(g)) {
+          f = g;
+          at = i - 1;
+        }
+      }
+    }
     float* wk = nullptr;
     QPH_TRY(hip_check(hipMalloc((void**)&wk, (size_t)dense_conv_wk_floats(f.m, f.c, 1, 1) * 4),
                       "hipMalloc(repacked 1x1 weight)"));
     net->wk[i + 1] = wk;
     QPH_TRY(launch_repack_conv_w_taps(net->weights[q.w], f.m, f.c, 1, wk, net->ctx->stream));
     f.wk = wk;
-    net->dwpw[i] = f;
-    net->fused[i] = true;
+    net->dwpw[at] = f;
+    net->fused[at] = true;
   }
   return QPH_OK;
 }
@@ -508,7 +534,7 @@ static int run_all(qph_net* net) {
       step = (size_t)net->group_len[i];
     } else if (net->fused[i]) {
       QPH_TRY(launch_dwpw(net->dwpw[i], s));
-      step = 2;
+      step = net->dwpw[i].stem ? 3 : 2;
     } else {
       QPH_TRY(run_node(net, i));
     }

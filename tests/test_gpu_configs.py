@@ -197,6 +197,47 @@ def test_session_linear_shapes(gpu, oracle, case):
     sess.close()
 
 
+STEM_CASES = [
+    # n, h, w, stem channels, pw channels, activations (stem, dw, pw), stem bias, stem output read elsewhere
+    (2, 30, 50, 16, 24, ("relu", "none", "relu"), False, False),   # odd sizes, generic activations
+    (1, 48, 100, 32, 64, ("hs", "hs", "hs"), True, False),         # rec-like, partial last tile
+    (1, 48, 100, 32, 64, ("hs", "hs", "hs"), True, True),          # stem output also an output: not fused
+    (3, 7, 9, 16, 16, ("hs", "hs", "hs"), True, False),            # tiny maps
+]
+
+
+@pytest.mark.parametrize("case", STEM_CASES, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}-{c[3]}-{c[4]}-{c[5][0]}-{c[6]}{c[7]}")
+def test_session_stem_fusion(gpu, oracle, case):
+    """A 3-channel 3x3 stride-2 stem conv in front of a 3x3 stride-2
+    depthwise + 1x1 block runs inside the block's launch (its output
+    computed in LDS, never stored) unless something else reads it: odd
+    map sizes, partial tiles, no stem bias, generic and hardswish
+    activations; bit-exact against the oracle."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    n, h, w, cs, m, acts, sbias, shared = case
+    kind = {"relu": nets.ACT_RELU, "none": nets.ACT_NONE, "hs": nets.ACT_HARDSWISH}
+    r = nets.WeightRng(n * 131 + h * 7 + w + cs + m)
+    g = nets.Graph((n, 3, h, w))
+    ws = g.weight(r.kaiming((cs, 3, 3, 3), 27))
+    bs = g.weight(r.normal((cs,), 0.1)) if sbias else -1
+    s0 = g.conv(0, ws, bs, stride=(2, 2), pad=(1, 1, 1, 1), act=kind[acts[0]])
+    wd = g.weight(r.kaiming((cs, 1, 3, 3), 9))
+    bd = g.weight(r.normal((cs,), 0.1))
+    t = g.conv(s0, wd, bd, stride=(2, 2), pad=(1, 1, 1, 1), group=cs, act=kind[acts[1]])
+    wp = g.weight(r.kaiming((m, cs, 1, 1), cs))
+    bp = g.weight(r.normal((m,), 0.1))
+    y = g.conv(t, wp, bp, act=kind[acts[2]])
+    g.outputs = [s0, y] if shared else [y]
+    x = r.normal((n, 3, h, w), 1.0)
+    sess = nets.HipSession(g)
+    got = sess.run(x)
+    ref = onets.run_graph(g, x)
+    for i, (a, b) in enumerate(zip(got, ref)):
+        assert_bitexact(a, b, f"output {i}")
+    sess.close()
+
+
 def test_session_channel_last_chain(gpu, oracle):
     """A chain of depthwise -> 1x1 blocks ending in a 1x1 conv that stores
     [n][pixels][M] runs channel-last (depthwise_cl_kernel + the 1x1 convs as
