@@ -875,7 +875,7 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
 // wait placement across the whole chain); NK = 0: any K / 64, run-time loop.
 template <int TM, int TN, int NS, int NK>
 __global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, int per_xcd) {
-  static_assert((TM == 32 || TM == 64) && (TN == 32 || TN == 64) && (NS == 3 || NS == 4), "");
+  static_assert((TM == 32 || TM == 64) && (TN == 32 || TN == 64) && (NS >= 2 && NS <= 4), "");
   constexpr int BM = TM / 32, BN = TN / 32;   // 16x16 blocks per wave
   constexpr int LA = TM / 16, LB = TN / 16;   // loads per wave per slab
   constexpr int L = LA + LB;
@@ -989,14 +989,15 @@ __global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, i
   using S3 = std::integral_constant<int, 3>;
 
   issue(S0{}, 0);
-  if (nk > 1) issue(S1{}, 1);
+  if constexpr (NS > 2)
+    if (nk > 1) issue(S1{}, 1);
   if constexpr (NS > 3)
     if (nk > 2) issue(S2{}, 2);
   // slab t: wait until it is in (at most the NS - 2 slabs after it still
   // loading), then refill the stage freed by slab t - 1 with slab t + NS - 1
   auto step = [&](auto st, int t) {
     constexpr int S = decltype(st)::value;
-    const int ahead = min(NS - 2, nk - 1 - t);
+    const int ahead = NS == 2 ? 0 : min(NS - 2, nk - 1 - t);
     if (ahead >= 2) wait_vmcnt<2 * L>();
     else if (ahead == 1) wait_vmcnt<L>();
     else wait_vmcnt<0>();
@@ -1009,7 +1010,8 @@ __global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, i
   auto ring = [&](int t) {
     step(S0{}, t);
     if (t + 1 < nk) step(S1{}, t + 1);
-    if (t + 2 < nk) step(S2{}, t + 2);
+    if constexpr (NS > 2)
+      if (t + 2 < nk) step(S2{}, t + 2);
     if constexpr (NS > 3)
       if (t + 3 < nk) step(S3{}, t + 3);
   };
@@ -1072,13 +1074,31 @@ static void launch_lt(const LinArgs& g, hipStream_t s) {
 }
 
 // Tile shape and ring depth as measured on the rec linears (1280 rows, K
-// 256 / 1024, N 256..1024): 32x32 tiles with three stages (48 KB, three
-// workgroups per CU) beat 64x32 and 64x64 on all four, and three stages beat
-// four (two workgroups per CU).
+// 256 / 1024, N 256..1024) and 1x1 convs (K 64..256): 32x32 tiles beat 64x32
+// and 64x64 on all of them.  Three stages (48 KB, three workgroups per CU)
+// beat four (two per CU) and, where the slabs are many or the tiles fill
+// three workgroups per CU, two; two stages (32 KB) win for K <= 128 and when
+// the tiles need two rounds at three per CU but one at four (QKV: 960).
 int launch_linear_nt(const LinArgs& g, hipStream_t s) {
   if (!linear_nt_eligible(g.m, g.n, g.k, g.lda))
     return fail(QPH_EUNSUPPORTED, "linear: shape outside the resident-weight kernel");
-  launch_lt<32, 32, 3>(g, s);
+  static int cus_dev[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(QPH_EHIP, "linear: no current device (or index past 63)");
+  if (cus_dev[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      return fail(QPH_EHIP, "linear: device query failed");
+    cus_dev[dev] = cus;
+  }
+  const int64_t tiles = (int64_t)ceil_div(g.m, 32) * ceil_div(g.n, 32);
+  const int64_t cus = cus_dev[dev];
+  if (g.k <= 128 || (tiles > 3 * cus && tiles <= 4 * cus))
+    launch_lt<32, 32, 2>(g, s);
+  else
+    launch_lt<32, 32, 3>(g, s);
   return launch_check("linear_nt_kernel");
 }
 
