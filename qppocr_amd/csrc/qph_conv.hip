@@ -465,6 +465,196 @@ __global__ __launch_bounds__(256) void conv3x3_direct_group_kernel(DirectConvGro
   else direct3x3_unit<1, 1, 4>(g.k[3], u - g.start[3], lane);
 }
 
+// ---------------------------------------------- LDS-staged 3x3 conv
+//
+// Stride 1, pad 1, M <= 32, C a multiple of 8 (the det neck smoothing convs
+// and the det head conv, 96 -> 24): the same chain as direct3x3_unit (k =
+// ci * 9 + ky * 3 + kx ascending, four per v_mfma_f32_16x16x4f32 step, bias
+// after the chain or seeded by the panel rule, then the activation, the
+// residual and the replicated store), but with both operands out of LDS.
+// A workgroup owns 2 output rows x 32 columns: wave w the 16 pixels of row
+// w / 2 from column 16 (w % 2), both 16-channel blocks of M.  K advances in
+// chunks of 8 input channels (72 k = 18 steps) through a ring of three LDS
+// stages, two chunks in flight while one is multiplied: the chunk's input
+// halo (8 x 4 rows x 34 columns, out-of-image words read 0 = the zero
+// padding) and its 72 weight rows of the k-major repack (32 floats each,
+// 16-float halves swapped on rows with k & 2 so that the four k rows of one
+// step hit distinct banks) arrive by buffer->LDS loads, 14 per wave per
+// chunk, so each wait counts exactly the chunks still loading.  Each direct3x3_unit step costs two vector-memory
+// loads per lane; here a step is three LDS reads and two MFMAs.
+
+#define LC_CC 8                         // input channels per chunk
+#define LC_HP 34                        // halo row pitch (32 + 2 columns)
+#define LC_HALO 1280                    // 8 x 4 x 34 = 1088 floats, in 20 loads
+#define LC_NST 3                        // ring stages
+#define LC_WROWS (LC_CC * 9)            // 72 weight rows per chunk
+#define LC_W (LC_WROWS * 32)            // 2304 floats
+#define LC_STAGE (LC_HALO + LC_W)
+#define LC_HL (LC_HALO / 64)            // 20 halo loads per chunk (5 a wave)
+#define LC_WL (LC_W / 64)               // 36 weight loads per chunk
+
+struct LdsConvGroup {
+  DirectConvK k[DIRECT_GROUP_MAX];
+  int tiles_x[DIRECT_GROUP_MAX];
+  int start[DIRECT_GROUP_MAX + 1];
+  int n;
+};
+
+// The ring stages are three __shared__ arrays of their own, picked at compile
+// time (the chunk loop is unrolled over the ring): that is what lets the
+// compiler tell the loads into one stage from the reads of another and place
+// no wait of its own before the operand reads.
+__device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x, int tile,
+                                              float* s0, float* s1, float* s2, int wave,
+                                              int lane) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int per_img = tiles_x * ((p.oh + 1) / 2);
+  const int img = tile / per_img, rem = tile - img * per_img;
+  const int oy0 = (rem / tiles_x) * 2, ox0 = (rem % tiles_x) * 32;
+  const int HW = p.h * p.w;
+  const unsigned OOB = 0x80000000u;
+  const int r = wave >> 1, c = (wave & 1) * 16 + l16;   // this lane's pixel in the tile
+  const int poy = oy0 + r, pox = ox0 + c;
+  const bool pval = poy < p.oh && pox < p.ow;
+
+  // chunk-invariant load offsets: halo word f = 64 q + lane of this wave's
+  // loads q = wave, wave + 4, ... (channel part in the scalar offset)
+  unsigned hoff[LC_HL / 4], woff[LC_WL / 4];
+#pragma unroll
+  for (int j = 0; j < LC_HL / 4; j++) {
+    const int f = 64 * (wave + 4 * j) + lane;
+    const int cl = f / (4 * LC_HP), rr = (f / LC_HP) % 4, cc = f % LC_HP;
+    const int iy = oy0 - 1 + rr, ix = ox0 - 1 + cc;
+    const bool ok = f < LC_CC * 4 * LC_HP && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+    hoff[j] = ok ? (unsigned)((cl * HW + iy * p.w + ix) * 4) : OOB;
+  }
+#pragma unroll
+  for (int j = 0; j < LC_WL / 4; j++) {
+    const int f = 64 * (wave + 4 * j) + lane;
+    const int kr = f >> 5, mc = (f & 31) ^ (((kr >> 1) & 1) << 4);
+    woff[j] = (unsigned)((kr * p.mpad + mc) * 4);
+  }
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + (int64_t)img * p.c * HW), 0, p.c * HW * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wk, 0, p.c * 9 * p.mpad * 4, 0x00020000);
+  auto issue = [&](int ch, float* st) {
+#pragma unroll
+    for (int j = 0; j < LC_HL / 4; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xr, (__attribute__((address_space(3))) void*)(st + 64 * (wave + 4 * j)), 4, hoff[j],
+          ch * LC_CC * HW * 4, 0, 0);
+#pragma unroll
+    for (int j = 0; j < LC_WL / 4; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wr, (__attribute__((address_space(3))) void*)(st + LC_HALO + 64 * (wave + 4 * j)), 4,
+          woff[j], ch * LC_WROWS * p.mpad * 4, 0, 0);
+  };
+  // per-step operand offsets inside a stage: k = 4 s + g of the chunk
+  int boff[LC_WROWS / 4];
+#pragma unroll
+  for (int s = 0; s < LC_WROWS / 4; s++) {
+    const int k = 4 * s + lg, cl = k / 9, tap = k - 9 * cl;
+    const int ky = tap / 3, kx = tap - 3 * ky;
+    boff[s] = cl * 4 * LC_HP + (r + ky) * LC_HP + c + kx;
+  }
+
+  // accumulators, bias-seeded where the reference seeds
+  f32x4 acc[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float s0 = 0.0f;
+      const int co = mt * 16 + 4 * lg + v;
+      if (p.bias && co < p.m && pval) {
+        const int n0 = (pox >> 5) << 5;
+        if ((p.ow - n0) < 32 && co >= p.m - p.m % 4) s0 = p.bias[co];
+      }
+      acc[mt][v] = s0;
+    }
+
+  constexpr int PER = (LC_HL + LC_WL) / 4;   // loads per wave per chunk
+  const int nch = p.c / LC_CC;
+  auto stage = [&](auto st) -> float* {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return s0;
+    else if constexpr (S == 1) return s1;
+    else return s2;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  issue(0, s0);
+  if (nch > 1) issue(1, s1);
+  auto body = [&](auto sti, int ch) {
+    constexpr int S = decltype(sti)::value;
+    // this chunk in (the next one may still load); then a barrier with no
+    // fence, which leaves the loads in flight, after which every wave is
+    // done with the stage of chunk ch - 1, refilled with chunk ch + 2
+    if (ch + 1 < nch)
+      wait_vmcnt<PER>();
+    else
+      wait_vmcnt<0>();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    if (ch + 2 < nch) issue(ch + 2, stage(std::integral_constant<int, (S + 2) % LC_NST>{}));
+    const float* st = stage(sti);
+    const float* wst = st + LC_HALO;
+#pragma unroll
+    for (int s = 0; s < LC_WROWS / 4; s++) {
+      const int k = 4 * s + lg;
+      const float b = st[boff[s]];
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++) {
+        const float a = wst[k * 32 + ((mt * 16 + l16) ^ (((k >> 1) & 1) << 4))];
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[mt], 0, 0, 0);
+      }
+    }
+  };
+  for (int ch = 0; ch < nch; ch += LC_NST) {
+    body(S0{}, ch);
+    if (ch + 1 < nch) body(S1{}, ch + 1);
+    if (ch + 2 < nch) body(S2{}, ch + 2);
+  }
+
+  // epilogue as in direct3x3_unit
+  const int64_t yoh = (int64_t)p.oh * p.y_up, yow = (int64_t)p.ow * p.y_up;
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = mt * 16 + 4 * lg + v;
+      if (!pval || co >= p.m) continue;
+      float xv = acc[mt][v];
+      if (p.bias) {
+        const int n0 = (pox >> 5) << 5;
+        const bool seeded = (p.ow - n0) < 32 && co >= p.m - p.m % 4;
+        if (!seeded) xv = xv + p.bias[co];
+      }
+      xv = act_apply(xv, p.act);
+      if (p.res) xv = xv + p.res[(((int64_t)img * p.m + co) * p.oh + poy) * p.ow + pox];
+      float* yb = p.y + (((int64_t)img * p.y_ctotal + p.y_coff + co) * yoh) * yow;
+      store_replicated(yb, yow, poy, pox, (int)p.y_up, xv);
+    }
+}
+
+__global__ __launch_bounds__(256) void conv3x3_lds_kernel(LdsConvGroup g) {
+  __shared__ __attribute__((aligned(16))) float s0[LC_STAGE], s1[LC_STAGE], s2[LC_STAGE];
+  const int lane = threadIdx.x & 63;
+  // "& 3" bounds the wave index, so that the LDS offsets of the loads and
+  // reads have known ranges
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+  const int t = blockIdx.x;
+  if (t >= g.start[g.n]) return;
+  if (t < g.start[1]) lds_conv_tile(g.k[0], g.tiles_x[0], t, s0, s1, s2, wave, lane);
+  else if (t < g.start[2]) lds_conv_tile(g.k[1], g.tiles_x[1], t - g.start[1], s0, s1, s2, wave, lane);
+  else if (t < g.start[3]) lds_conv_tile(g.k[2], g.tiles_x[2], t - g.start[2], s0, s1, s2, wave, lane);
+  else lds_conv_tile(g.k[3], g.tiles_x[3], t - g.start[3], s0, s1, s2, wave, lane);
+}
+
 static void direct_params(const ConvArgs& a, const float* wk, DirectConvK& p) {
   p = DirectConvK{};
   p.x = a.x; p.wk = wk; p.bias = a.bias; p.res = a.res; p.y = a.y;
@@ -482,8 +672,33 @@ bool direct3x3_eligible(const ConvArgs& a) {
          (int64_t)ceil_div(a.m, 16) * ceil_div(a.oh * a.ow, 16) * a.n < (1ll << 29);
 }
 
+static bool lds3x3_eligible(const ConvArgs& a) {
+  return direct3x3_eligible(a) && a.sh == 1 && a.sw == 1 && a.ph == 1 && a.pw == 1 &&
+         a.m <= 32 && a.c % LC_CC == 0 && a.c > 0 && mpad_of(a.m) == 32 &&
+         a.c * a.h * a.w * 4 < (int64_t)0x80000000;
+}
+
+static int launch_lds3x3(const ConvArgs* a, int n, hipStream_t s) {
+  LdsConvGroup g{};
+  g.n = n;
+  int64_t total = 0;
+  for (int i = 0; i < n; i++) {
+    direct_params(a[i], a[i].wk, g.k[i]);
+    g.tiles_x[i] = (int)ceil_div(a[i].ow, 32);
+    g.start[i] = (int)total;
+    total += (int64_t)g.tiles_x[i] * ceil_div(a[i].oh, 2) * a[i].n;
+  }
+  for (int i = n; i <= DIRECT_GROUP_MAX; i++) g.start[i] = (int)total;
+  if (total >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "conv: grid too large");
+  hipLaunchKernelGGL(conv3x3_lds_kernel, dim3((unsigned)total), dim3(256), 0, s, g);
+  return launch_check("conv3x3_lds_kernel");
+}
+
 int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s) {
   if (n < 1 || n > DIRECT_GROUP_MAX) return fail(QPH_EINVAL, "conv group: 1 to 4 convs");
+  bool lds = true;
+  for (int i = 0; i < n; i++) lds = lds && a[i].wk && lds3x3_eligible(a[i]);
+  if (lds) return launch_lds3x3(a, n, s);
   DirectConvGroup g{};
   g.n = n;
   int64_t total = 0;
@@ -507,6 +722,11 @@ int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s) {
 // Launches the direct kernel for a 3x3 conv, choosing the per-wave tile so
 // that the launch has enough waves to hide load latency.
 static int launch_direct3x3(const ConvArgs& a, const float* wk, hipStream_t s) {
+  if (lds3x3_eligible(a)) {
+    ConvArgs b = a;
+    b.wk = wk;
+    return launch_lds3x3(&b, 1, s);
+  }
   DirectConvK p;
   direct_params(a, wk, p);
   const int64_t npx = a.oh * a.ow;
