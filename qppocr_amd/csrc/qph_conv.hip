@@ -1092,6 +1092,65 @@ __global__ __launch_bounds__(256) void depthwise_cl_kernel(DwClK p) {
   p.y[((int64_t)row * p.ow) * p.c + e] = act_apply(v, p.act);
 }
 
+// PX adjacent output columns per thread (stride SW along x, 3x3): the taps
+// of the channel sit in registers and the KH rows of (PX - 1) * SW + 3 input
+// columns are read once for all PX outputs; each output keeps the chain
+// above (acc = fma(w, x, acc) over ky, kx, then + bias, then the
+// activation).  AK = 3: HardSigmoid + Mul inline.
+template <int SW, int PX, int AK>
+__global__ __launch_bounds__(256) void depthwise_cl_px_kernel(DwClK p) {
+  constexpr int NC = (PX - 1) * SW + 3;
+  const int row = (int)blockIdx.y;
+  const int oy = row % p.oh, img = row / p.oh;
+  const int ngx = (p.ow + PX - 1) / PX;
+  const int e = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (e >= ngx * p.c) return;
+  const int ch = e & (p.c - 1), ox0 = (e >> p.lc) * PX;
+  float w[9];
+#pragma unroll
+  for (int j = 0; j < 9; j++) w[j] = p.w[ch * 9 + j];
+  const float bias = p.bias ? p.bias[ch] : 0.0f;
+  const float* xb = p.x + (int64_t)img * p.h * p.w_ * p.c + ch;
+  float acc[PX];
+#pragma unroll
+  for (int q = 0; q < PX; q++) acc[q] = 0.0f;
+#pragma unroll
+  for (int ky = 0; ky < 3; ky++) {
+    const int iy = oy * p.sh - p.ph + ky;
+    const bool rok = iy >= 0 && iy < p.h;
+    float xv[NC];
+#pragma unroll
+    for (int c2 = 0; c2 < NC; c2++) {
+      const int ix = ox0 * SW - p.pw + c2;
+      xv[c2] = (rok && ix >= 0 && ix < p.w_) ? xb[((int64_t)iy * p.w_ + ix) * p.c] : 0.0f;
+    }
+#pragma unroll
+    for (int kx = 0; kx < 3; kx++)
+#pragma unroll
+      for (int q = 0; q < PX; q++) acc[q] = __builtin_fmaf(w[ky * 3 + kx], xv[q * SW + kx], acc[q]);
+  }
+  float* yb = p.y + ((int64_t)row * p.ow) * p.c + ch;
+#pragma unroll
+  for (int q = 0; q < PX; q++) {
+    if (ox0 + q >= p.ow) break;
+    float v = acc[q] + (p.bias ? bias : 0.0f);
+    if constexpr (AK == 3) v = v * hsig1(v, p.act.c1, p.act.c2);
+    else v = act_apply(v, p.act);
+    yb[(int64_t)(ox0 + q) * p.c] = v;
+  }
+}
+
+template <int SW>
+static int launch_dwcl_px(const DwClK& p, hipStream_t s) {
+  const int ngx = (p.ow + 3) / 4;
+  const dim3 grid(ceil_div((int64_t)ngx * p.c, 256), (unsigned)(p.n * p.oh));
+  if (p.act.kind == 3)
+    hipLaunchKernelGGL((depthwise_cl_px_kernel<SW, 4, 3>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((depthwise_cl_px_kernel<SW, 4, 0>), grid, dim3(256), 0, s, p);
+  return launch_check("depthwise_cl_px_kernel");
+}
+
 int launch_depthwise_cl(const ConvArgs& a, hipStream_t s) {
   const int64_t total = a.n * a.oh * a.ow * a.c;
   if (total <= 0) return QPH_OK;
@@ -1107,6 +1166,8 @@ int launch_depthwise_cl(const ConvArgs& a, hipStream_t s) {
   p.sh = (int)a.sh; p.sw = (int)a.sw; p.ph = (int)a.ph; p.pw = (int)a.pw;
   p.oh = (int)a.oh; p.ow = (int)a.ow;
   p.act = a.act;
+  if (a.kh == 3 && a.kw == 3 && a.ow >= 8 && (a.sw == 1 || a.sw == 2))
+    return a.sw == 1 ? launch_dwcl_px<1>(p, s) : launch_dwcl_px<2>(p, s);
   const dim3 grid(ceil_div(a.ow * a.c, 256), (unsigned)(a.n * a.oh));
   if (a.kh == 3 && a.kw == 3)
     hipLaunchKernelGGL((depthwise_cl_kernel<3, 3>), grid, dim3(256), 0, s, p);
