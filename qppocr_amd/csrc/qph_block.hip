@@ -108,6 +108,17 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int img = blockIdx.z;
   const int slice = blockIdx.y;
+  // STEM (one 64-channel slice, cpad = 16 PX): this lane's pointwise A terms
+  // W[m = 16 wave + l][k = 4 s + g] of the k-major repack, loaded first so
+  // that their latency hides under phase 1; read by phase 3 from registers
+  constexpr int WS = STEM ? 4 * PX : 1;
+  float wreg[WS];
+  if constexpr (STEM) {
+    const int col = wave * 16 + (lane & 15);
+#pragma unroll
+    for (int u = 0; u < WS; u++)
+      wreg[u] = col < p.mpad ? p.wk[(4 * u + (lane >> 4)) * p.mpad + col] : 0.0f;
+  }
   const int oy = blockIdx.x / p.tiles_x;
   const int ox0 = (blockIdx.x - oy * p.tiles_x) * 16;
   const int64_t plane = (int64_t)p.h * p.w;
@@ -183,7 +194,8 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         (void*)p.wk, 0, p.cpad * p.mpad * 4, 0x00020000);
     const int m0 = slice * DWPW_MSLICE;
     const unsigned woff = m0 + lane < p.mpad ? (unsigned)((m0 + lane) * 4) : OOB;
-    for (int k = wave; k < p.cpad; k += 4)
+    // (STEM: the pointwise weights go to registers below, not to LDS)
+    for (int k = wave; k < (STEM ? 0 : p.cpad); k += 4)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           wr, (__attribute__((address_space(3))) void*)(wsl + k * 64), 4, woff,
           k * p.mpad * 4, 0, 0);
@@ -341,6 +353,12 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   const float* bl = t + lg * 16 + l16;
   const int nsteps = p.cpad >> 2;
   int s = 0;
+  if constexpr (STEM) {
+#pragma unroll
+    for (int u = 0; u < WS; u++)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wreg[u], bl[u * 64], acc, 0, 0, 0);
+    s = nsteps;
+  }
   for (; s + 4 <= nsteps; s += 4) {
     float av[4], bv[4];
 #pragma unroll
@@ -460,6 +478,10 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
     if (!dwpw_stem_eligible(a)) return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: unsupported shape");
     p.xin = a.xin; p.wst = a.wst; p.bst = a.bst; p.act_s = a.act_s;
     p.hin = (int)a.hin; p.win = (int)a.win;
+    if (p.cpad != 16 * px || p.slices != 1)
+      return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: unsupported shape");
+    lds -= (size_t)p.wrows * 4;   // pointwise weights in registers
+    p.wrows = 0;
     lds += (size_t)(ST_IN + ST_K * a.c + 64) * 4;
     // cpad 16 -> 1 pixel per depthwise task, 32 -> 2
     if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true>(grid, lds, p, s);
