@@ -141,6 +141,12 @@ DIRECT_CASES = [
     (2, 32, 32, 128, 128, 1, 1, 1, 1, 1, 1),
     (8, 8, 32, 128, 128, 1, 1, 1, 1, 1, 1),
     (8, 8, 16, 128, 128, 1, 1, 1, 1, 1, 1),
+    # LDS-staged kernel (stride 1, pad 1, C % 8 == 0, M <= 32): two chunks with
+    # bias-seeded rows (M % 4 tail, partial last 32-column panel) and partial
+    # tiles; three chunks, M = 8, odd sizes; five chunks (the ring wraps)
+    (1, 16, 22, 19, 45, 1, 1, 1, 1, 1, 1),
+    (2, 24, 8, 9, 70, 1, 1, 1, 1, 1, 1),
+    (1, 40, 32, 7, 33, 1, 1, 1, 1, 1, 1),
     (8, 3, 16, 128, 128, 2, 2, 1, 1, 1, 1),
     (3, 12, 40, 33, 47, 2, 1, 0, 1, 2, 0),
     # 3 input channels, M % 4 == 0: the VALU kernel (odd sizes, asymmetric pads)
