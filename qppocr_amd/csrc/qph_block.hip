@@ -382,17 +382,28 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     badd[v] = hadd[v] ? p.bp[mo] : 0.0f;
   }
   if (!pok) return;
+  float r[4];
 #pragma unroll
   for (int v = 0; v < 4; v++) {
-    const int mo = mb * 16 + 4 * lg + v;
+    r[v] = acc[v];
+    if (hadd[v]) r[v] = r[v] + badd[v];
+    r[v] = act_k<AK>(r[v], p.act_p);
+  }
+  const int mo0 = mb * 16 + 4 * lg;
+  // channel-last: this lane's four channels of the pixel are adjacent, one
+  // 16-byte store when they are all inside M and 16-byte aligned
+  if (p.trans_out && mo0 + 3 < p.m && p.m % 4 == 0 && ((uintptr_t)p.y & 15) == 0) {
+    *(f32x4*)(p.y + ((int64_t)img * npx + px) * p.m + mo0) = f32x4{r[0], r[1], r[2], r[3]};
+    return;
+  }
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mo0 + v;
     if (mo >= p.m) continue;
-    float r = acc[v];
-    if (hadd[v]) r = r + badd[v];
-    r = act_k<AK>(r, p.act_p);
     if (p.trans_out)
-      p.y[((int64_t)img * npx + px) * p.m + mo] = r;
+      p.y[((int64_t)img * npx + px) * p.m + mo] = r[v];
     else
-      p.y[((int64_t)img * p.m + mo) * npx + px] = r;
+      p.y[((int64_t)img * p.m + mo) * npx + px] = r[v];
   }
 }
 
