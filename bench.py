@@ -131,9 +131,9 @@ def main():
                          "known traffic for scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; the det/rec path "
-                          "shards by image / rec batch with no exchange (see DESIGN.md), "
-                          "multi-GPU runs are not part of it", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this benchmark runs on one GPU only; the det/rec path "
+                          "shards by image / rec batch with no exchange between GPUs, "
+                          "and multi-GPU runs are not part of it", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import numpy as np
