@@ -261,7 +261,10 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
 /* Device pointer of a tensor of the net (valid until destroy). */
 QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* numel);
 /* Average device time (ms) of each node over the runs since the last reset
- * when profiling is on (events around each node; graph replay disabled). */
+ * when profiling is on (events around each node; graph replay disabled).
+ * A launch that covers several nodes (a depthwise + 1x1 block, a stem conv
+ * run inside the first block, a group of independent 3x3 convs) is booked
+ * on its first node; the nodes it covers read only the event overhead. */
 QPH_API int qph_net_set_profiling(qph_net* net, int32_t on);
 QPH_API int qph_net_node_times(qph_net* net, double* ms_per_node, int32_t n);
 
