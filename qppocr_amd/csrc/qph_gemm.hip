@@ -988,6 +988,22 @@ __global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, i
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
 
+  // epilogue operands (bias, residual) loaded now, their latency under the
+  // slab loop's
+  float badd[BN], rres[BM][BN][4];
+#pragma unroll
+  for (int bn = 0; bn < BN; bn++) {
+    const int j = j0 + wn * (TN / 2) + bn * 16 + l16;
+    badd[bn] = (g.bias && j < N) ? g.bias[j] : -0.0f;
+#pragma unroll
+    for (int bm = 0; bm < BM; bm++) {
+      const int ib = i0 + wm * (TM / 2) + bm * 16 + 4 * lg;
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        rres[bm][bn][v] = (g.res && j < N && ib + v < M) ? g.res[(int64_t)(ib + v) * N + j] : 0.0f;
+    }
+  }
+
   issue(S0{}, 0);
   if constexpr (NS > 2)
     if (nk > 1) issue(S1{}, 1);
@@ -1023,29 +1039,20 @@ __global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, i
   }
 
   // epilogue: MatMul, then + bias (a term of -0.0 leaves a value unchanged),
-  // activation, then + residual; operands gathered before any store
+  // activation, then + residual
 #pragma unroll
   for (int bn = 0; bn < BN; bn++) {
     const int j = j0 + wn * (TN / 2) + bn * 16 + l16;
     if (j >= N) continue;
-    const float badd = g.bias ? g.bias[j] : -0.0f;
-    float r[BM][4];
-#pragma unroll
-    for (int bm = 0; bm < BM; bm++) {
-      const int ib = i0 + wm * (TM / 2) + bm * 16 + 4 * lg;
-#pragma unroll
-      for (int v = 0; v < 4; v++)
-        r[bm][v] = (g.res && ib + v < M) ? g.res[(int64_t)(ib + v) * N + j] : 0.0f;
-    }
 #pragma unroll
     for (int bm = 0; bm < BM; bm++) {
       const int ib = i0 + wm * (TM / 2) + bm * 16 + 4 * lg;
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         if (ib + v >= M) continue;
-        float x = acc[bm][bn][v] + badd;
+        float x = acc[bm][bn][v] + badd[bn];
         x = act_apply(x, g.act);
-        if (g.res) x = x + r[bm][v];
+        if (g.res) x = x + rres[bm][bn][v];
         g.c[(int64_t)(ib + v) * N + j] = x;
       }
     }
