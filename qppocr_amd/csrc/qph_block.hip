@@ -112,6 +112,14 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   // W[m = 16 wave + l][k = 4 s + g] of the k-major repack, loaded first so
   // that their latency hides under phase 1; read by phase 3 from registers
   constexpr int WS = STEM ? 4 * PX : 1;
+  // the pointwise bias of this lane's four output channels, loaded now
+  // (latency under phase 1)
+  float bpre[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = (slice * 4 + wave) * 16 + 4 * (lane >> 4) + v;
+    bpre[v] = (p.bp && mo < p.m) ? p.bp[mo] : 0.0f;
+  }
   float wreg[WS];
   if constexpr (STEM) {
     const int col = wave * 16 + (lane & 15);
@@ -346,7 +354,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   for (int v = 0; v < 4; v++) {
     const int mo = mb * 16 + 4 * lg + v;
     float s0 = 0.0f;
-    if (p.bp && mo < p.m && pok && bias_seeded(p.seed_rule, mo, px, p.m, npx)) s0 = p.bp[mo];
+    if (p.bp && mo < p.m && pok && bias_seeded(p.seed_rule, mo, px, p.m, npx)) s0 = bpre[v];
     acc[v] = s0;
   }
   const float* al = wsl + lg * 64 + wave * 16 + l16;
@@ -379,7 +387,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   for (int v = 0; v < 4; v++) {
     const int mo = mb * 16 + 4 * lg + v;
     hadd[v] = p.bp && mo < p.m && pok && !bias_seeded(p.seed_rule, mo, px, p.m, npx);
-    badd[v] = hadd[v] ? p.bp[mo] : 0.0f;
+    badd[v] = hadd[v] ? bpre[v] : 0.0f;
   }
   if (!pok) return;
   float r[4];

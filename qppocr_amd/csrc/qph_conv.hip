@@ -574,6 +574,15 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
       acc[mt][v] = s0;
     }
 
+  // the epilogue's bias terms, loaded now (latency under the chunk loop)
+  float bterm[2][4];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = mt * 16 + 4 * lg + v;
+      bterm[mt][v] = (p.bias && co < p.m) ? p.bias[co] : 0.0f;
+    }
   constexpr int PER = (LC_HL + LC_WL) / 4;   // loads per wave per chunk
   const int nch = p.c / LC_CC;
   auto stage = [&](auto st) -> float* {
@@ -632,7 +641,7 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
       if (p.bias) {
         const int n0 = (pox >> 5) << 5;
         const bool seeded = (p.ow - n0) < 32 && co >= p.m - p.m % 4;
-        if (!seeded) xv = xv + p.bias[co];
+        if (!seeded) xv = xv + bterm[mt][v];
       }
       xv = act_apply(xv, p.act);
       if (p.res) xv = xv + p.res[(((int64_t)img * p.m + co) * p.oh + poy) * p.ow + pox];
