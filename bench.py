@@ -1,32 +1,48 @@
-"""Throughput of the HIP backend on the det + rec workload, one JSON line.
+"""Throughput of the HIP backend on the det + rec workload, one JSON line,
+with every synthetic config measured beside it.
 
-A step is one det forward on 1x3x640x640 plus one rec forward on a batch of
-32 lines of 3x48x320 (the det image and the 32 text lines of one page), both
-as replayed HIP graphs with their inputs already resident in HBM.  The det
-and rec sessions run on two contexts (two streams), as a page pipeline runs
-the det of one page next to the rec of another: value = steps per second =
-det images per second with 32 recognised lines each, over the wall time of
-K steps with both streams busy.  det_img_per_s and rec_lines_per_s are the
-stage-isolated rates (HIP events around each session alone, on its own
-stream) and serial_ms_per_step their sum, the step time on one stream.
+Headline step: one det forward on 1x3x640x640 plus one rec forward on a
+batch of 32 lines of 3x48x320 (the det image and the 32 text lines of one
+page), both as replayed HIP graphs with their inputs already resident in
+HBM.  The rec session ends in the CTC exit of the reference's GPU sessions
+(rec_argmax_pairs, qppocr-core/src/device.rs:160-165): softmax + argmax
+emit the (value, index) pairs the decoder reads; the probability tensor is
+not stored (rec_lines_per_s_with_probs is the same graph exporting it too).
+The det and rec sessions run on two contexts (two streams), as a page
+pipeline runs the det of one page next to the rec of another: value = steps
+per second = det images per second with 32 recognised lines each, over the
+wall time of K steps with both streams busy.  det_img_per_s and
+rec_lines_per_s are the stage-isolated rates (HIP events around each
+session alone, on its own stream).
 
-roofline: the dominant kernel is the rec head GEMM (1280 x 18709 x 256,
+roofline: the dominant kernel, the rec head GEMM (1280 x 18709 x 256,
 12.26 GFLOP of the step's 20.86).  Its average launch time comes from HIP
-events around each node of the rec graph (eager launches on the same stream),
-over the same number of steps, after the timed region.  traffic (HBM bytes
-per launch) is the calibrated FETCH_SIZE + WRITE_SIZE figure recorded in
-profiles/rec_head_gemm_traffic.md (rocprofv3 counter runs of this script).
+events around each node of the rec graph (eager launches on the session
+stream) over the same number of steps.  traffic (HBM bytes per launch) is
+the calibrated FETCH_SIZE + WRITE_SIZE figure in
+profiles/rec_head_gemm_traffic.md.
 
-cpu_baseline: the CPU oracle (plain-C restatement of the qppocr-kernels
-AVX2 path, OpenMP over all host threads) on a bounded sample of the same
-workload, timed on this host.
+configs: the five BASELINE workloads, each with its GPU rate, the roofline
+fraction of its bound and the CPU oracle timed on this host (threads set
+explicitly, one warm-up round, then the median of the rounds):
+  cfg1 conv3x3 32->32 @160^2 + bias + ReLU and cfg2a-d depthwise + hardswish:
+    the op as a session node with resident weights, replicated over enough
+    input/output buffer sets that the sets together exceed 512 MB (twice the
+    256 MB Infinity Cache); a graph replay runs the copies back to back, each
+    on the next set, so every launch reads its operands cache-cold.  The
+    time per launch is the replay's HIP-event time over the copies.
+  cfg3 det 640^2 / cfg4 rec 32x320: the headline's stage rates, with the
+    per-kernel-class roofline fractions from per-node event times.
+  cfg5: det 1536^2 + 128 rec lines in width buckets (page wall time).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--cpu-rounds R] [--no-configs] [--node-report FILE]
 """
 import argparse
 import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -36,6 +52,7 @@ sys.path.insert(0, ROOT)
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 REC_BATCH = 32
+COLD_BYTES = 512 << 20      # buffer sets per op bench: twice the Infinity Cache
 
 
 def head_traffic_bytes():
@@ -55,25 +72,193 @@ OP_NAMES = {1: "conv", 2: "convt_pair_sigmoid", 3: "linear", 4: "layernorm", 5: 
             6: "softmax_argmax", 7: "convt", 8: "act"}
 
 
-def write_node_report(path, nets, graphs):
-    """Per node: average launch time (HIP events, eager launches) and the
-    fraction of its roofline (fp32 MFMA peak for products, HBM peak else)."""
+def node_rows(nets, name, g, node_ms):
     rows = []
-    for name, g, node_ms in graphs:
-        for i, d in enumerate(g.nodes):
-            fl, by, bound = nets.node_cost(g, d)
-            ms = node_ms[i]
-            row = {"graph": name, "node": i, "op": OP_NAMES.get(d["op"], str(d["op"])),
-                   "in": list(g.lshapes[d["inp"]]), "w": list(d["ws"]), "us": round(ms * 1e3, 2),
-                   "gflop": round(fl / 1e9, 4), "mb": round(by / 1e6, 3), "bound": bound}
-            if ms > 0:
-                tf, gbs = fl / (ms * 1e-3) / 1e12, by / (ms * 1e-3) / 1e9
-                row["tflops"], row["gbs"] = round(tf, 2), round(gbs, 1)
-                row["frac"] = round(tf / PEAK_FP32_MFMA_TFLOPS if bound == "mfma"
-                                    else gbs / PEAK_HBM_GBS, 4)
-            rows.append(row)
-    with open(path, "w") as f:
-        json.dump(rows, f, indent=0)
+    for i, d in enumerate(g.nodes):
+        fl, by, bound = nets.node_cost(g, d)
+        ms = node_ms[i]
+        row = {"graph": name, "node": i, "op": OP_NAMES.get(d["op"], str(d["op"])),
+               "in": list(g.lshapes[d["inp"]]), "w": list(d["ws"]), "us": round(ms * 1e3, 2),
+               "gflop": round(fl / 1e9, 4), "mb": round(by / 1e6, 3), "bound": bound}
+        if ms > 0:
+            tf, gbs = fl / (ms * 1e-3) / 1e12, by / (ms * 1e-3) / 1e9
+            row["tflops"], row["gbs"] = round(tf, 2), round(gbs, 1)
+            row["frac"] = round(tf / PEAK_FP32_MFMA_TFLOPS if bound == "mfma"
+                                else gbs / PEAK_HBM_GBS, 4)
+        rows.append(row)
+    return rows
+
+
+def class_fractions(nets, g, node_ms):
+    """Per roofline class: summed algorithmic work over summed node time
+    (eager launches, one event pair per node: an upper bound on the time,
+    so a lower bound on the fraction).  Fused launches book their time on
+    their first node and 0 on the others; the work of every node counts."""
+    agg = {"mfma": [0.0, 0.0], "hbm": [0.0, 0.0]}
+    for i, d in enumerate(g.nodes):
+        fl, by, bound = nets.node_cost(g, d)
+        a = agg[bound]
+        a[0] += fl if bound == "mfma" else by
+        a[1] += node_ms[i]
+    out = {}
+    for k, (work, ms) in agg.items():
+        if ms <= 0:
+            continue
+        if k == "mfma":
+            tf = work / (ms * 1e-3) / 1e12
+            out[k] = {"tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                      "us": round(ms * 1e3, 1)}
+        else:
+            gbs = work / (ms * 1e-3) / 1e9
+            out[k] = {"gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                      "us": round(ms * 1e3, 1)}
+    return out
+
+
+# ------------------------------------------------------------------ CPU side
+
+def cpu_threads():
+    """Threads for the CPU oracle: the host's cores available to this
+    process, capped by OMP_NUM_THREADS when the environment sets it (the
+    GPU box gives one GPU's job a share of the host)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_median(fn, rounds):
+    """One warm-up round, then the median wall time of `rounds` rounds (the
+    reference CLI bench discipline, qppocr-cli/src/main.rs:738-818)."""
+    fn()
+    ts = []
+    for _ in range(rounds):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+# ------------------------------------------------------------------ GPU side
+
+class ColdOpBench:
+    """One op as a session node with resident weights, copied over R input /
+    output buffer sets (R x set bytes > COLD_BYTES); a graph replay runs the
+    copies back to back.  add_node(g, x) appends the op reading tensor x."""
+
+    def __init__(self, nets, ops, ctx, x, add_node, set_bytes):
+        import numpy as np
+        self.R = max(2, -(-COLD_BYTES // set_bytes))
+        g = nets.Graph(x.shape)
+        ins = [0] + [g.tensor(x.shape) for _ in range(self.R - 1)]
+        outs = [add_node(g, t) for t in ins]
+        g.outputs = [outs[0]]
+        g.flags = nets.NET_SEPARATE_LAUNCHES     # one launch per copy
+        self.g = g
+        self.sess = nets.HipSession(g, ctx=ctx)
+        self.sess.run(x, outputs=False)
+        xc = np.ascontiguousarray(x, dtype=np.float32)
+        lib = ops._lib.load()
+        for t in ins[1:]:
+            ptr, n = self.sess.tensor_ptr(t)
+            ops.check(lib.qph_memcpy_h2d(ctx, ctypes.c_void_p(ptr),
+                                         xc.ctypes.data_as(ctypes.c_void_p), n * 4))
+        self.stream = lib.qph_ctx_stream(ctx)
+
+    def us_per_launch(self, replays, warmup=2):
+        import torch
+        st = torch.cuda.ExternalStream(self.stream)
+        for _ in range(warmup):
+            self.sess.run(None, outputs=False)
+        self.sess.sync()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(replays):
+            self.sess.run(None, outputs=False)
+        e1.record(st)
+        self.sess.sync()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (replays * self.R)
+
+    def close(self):
+        self.sess.close()
+
+
+def bench_cfg1(nets, ops, configs, ctx, replays, cpu_rounds, O):
+    from qppocr_amd._lib import ACT_RELU
+    x, w, b = configs.cfg1(0)
+    by, fl = configs.cfg1_bytes_flops()
+
+    def add_node(g, t):
+        if not g.weights:        # weight ids 0 (w) and 1 (bias), shared by the copies
+            g.weight(w)
+            g.weight(b)
+        return g.conv(t, 0, 1, pad=(1, 1, 1, 1), act=ACT_RELU)
+    ob = ColdOpBench(nets, ops, ctx, x, add_node, x.nbytes + 4 * 32 * 160 * 160)
+    us = ob.us_per_launch(replays)
+    ob.close()
+    tf = fl / (us * 1e-6) / 1e12
+    out = {"workload": "conv3x3 s1 p1 N=1 32->32 160x160 + bias + ReLU (seed 0)",
+           "us": round(us, 3), "tflops": round(tf, 2), "bound": "mfma",
+           "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4), "gflop": round(fl / 1e9, 4),
+           "kernel": "conv3x3_lds_kernel",
+           "method": f"HIP events over {replays} graph replays of {ob.R} copies on rotating "
+                     f"buffer sets ({ob.R * (x.nbytes + 4 * 32 * 160 * 160) >> 20} MB)"}
+    if O is not None:
+        params = O.conv_params(1, 1, 1, 1)
+        s = cpu_median(lambda: O.conv2d(x, w, b, params, O.ACT_RELU), cpu_rounds)
+        out["cpu_baseline"] = {"us": round(s * 1e6, 1),
+                               "tflops": round(fl / s / 1e12, 4), "rounds": cpu_rounds}
+    return out
+
+
+def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
+    from qppocr_amd._lib import ACT_HARDSWISH
+    res = {}
+    for tag, (x, w, b, k, s) in zip("abcd", configs.cfg2(1)):
+        c, hw = x.shape[1], x.shape[2]
+        by, fl = configs.cfg2_bytes_flops(c, hw, k, s)
+        oh = configs.conv_out_hw(hw, k, s, k // 2)
+
+        def add_node(g, t, w=w, b=b, k=k, s=s, c=c):
+            if not g.weights:
+                g.weight(w)
+                g.weight(b)
+            return g.conv(t, 0, 1, stride=(s, s), pad=(k // 2,) * 4, group=c, act=ACT_HARDSWISH)
+        set_bytes = x.nbytes + 4 * c * oh * oh
+        ob = ColdOpBench(nets, ops, ctx, x, add_node, set_bytes)
+        us = ob.us_per_launch(replays)
+        ob.close()
+        gbs = by / (us * 1e-6) / 1e9
+        out = {"workload": f"depthwise {k}x{k} s{s} pad {k // 2} C{c} {hw}x{hw} + hardswish",
+               "us": round(us, 3), "gbs": round(gbs, 1), "bound": "hbm",
+               "frac": round(gbs / PEAK_HBM_GBS, 4), "mb": round(by / 1e6, 3),
+               "kernel": f"depthwise_kernel<{k},{k}>",
+               "method": f"cache-cold: HIP events over {replays} graph replays of {ob.R} copies "
+                         f"on rotating buffer sets ({ob.R * set_bytes >> 20} MB)"}
+        if O is not None:
+            params = O.conv_params(s, s, k // 2, k // 2, group=c)
+
+            def run_cpu(x=x, w=w, b=b, params=params):
+                y = O.conv2d(x, w, b, params)
+                return O.binary_flat(y, O.hardsigmoid(y), 2)
+            sec = cpu_median(run_cpu, cpu_rounds)
+            out["cpu_baseline"] = {"us": round(sec * 1e6, 1), "gbs": round(by / sec / 1e9, 2),
+                                   "rounds": cpu_rounds}
+        res["cfg2" + tag] = out
+    return res
 
 
 def time_mixed_page(steps, warmup):
@@ -103,16 +288,34 @@ def time_mixed_page(steps, warmup):
     rec_ms = wall(page.run_rec)
     page_ms = wall(page.run)
     out = {"workload": "det 1x3x1536x1536 + 128 rec lines 3x48x{80..1280}, buckets of 160, "
-                       "<= 64 lines/batch, CTC masked past w/8",
+                       "<= 64 lines/batch, CTC masked past w/8 (seed 4)",
            "rec_batches": [[bw, len(idx)] for bw, idx in page.plan],
            "det_img_per_s": round(1e3 / det_ms, 2),
            "rec_lines_per_s": round(len(widths) * 1e3 / rec_ms, 1),
-           "page_ms": round(page_ms, 4), "det_ms": round(det_ms, 4),
-           "rec_ms": round(rec_ms, 4)}
+           "page_ms": round(page_ms, 4), "ms_per_image": round(page_ms, 4),
+           "det_ms": round(det_ms, 4), "rec_ms": round(rec_ms, 4)}
     page.close()
     for c in ctxs:
         ops.close_context(c)
-    return out
+    return out, (det_g, det_x, rw, lines, widths)
+
+
+def cpu_mixed_page(data, rounds):
+    """The mixed page on the CPU oracle: det at 1536^2 and every rec batch."""
+    from qppocr_amd import nets, pipeline
+    from oracle import nets as onets
+    det_g, det_x, rw, lines, widths = data
+    batches = [(nets.build_rec_graph(rw, len(idx), bw, pipeline.REC_H, probs=False),
+                pipeline.pack_lines(lines, idx, bw)) for bw, idx in pipeline.bucket_plan(widths)]
+    det_s = cpu_median(lambda: onets.run_graph(det_g, det_x), rounds)
+
+    def rec():
+        for g, x in batches:
+            onets.run_graph(g, x)
+    rec_s = cpu_median(rec, rounds)
+    return {"det_img_per_s": round(1.0 / det_s, 3),
+            "rec_lines_per_s": round(len(widths) / rec_s, 2),
+            "ms_per_image": round((det_s + rec_s) * 1e3, 1), "rounds": rounds}
 
 
 def main():
@@ -120,10 +323,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-steps", type=int, default=6, help="CPU baseline sample (steps)")
-    ap.add_argument("--mixed-page", action="store_true",
-                    help="also time the mixed-shape page (det 1536^2 + 128 bucketed rec lines)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--cpu-rounds", type=int, default=5,
+                    help="CPU baseline: timed rounds (median) after one warm-up round")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="headline step only (skip the per-config measurements)")
     ap.add_argument("--node-report", default="",
                     help="also write per-node times and roofline fractions (JSON) to this path")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -138,7 +342,7 @@ def main():
 
     import numpy as np
     import torch
-    from qppocr_amd import nets, ops
+    from qppocr_amd import configs, nets, ops
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -157,7 +361,7 @@ def main():
         del src, dst
 
     det_g, det_x = nets.build_det(2, 640, 640)
-    rec_g, rec_x = nets.build_rec(3, REC_BATCH, 320)
+    rec_g, rec_x = nets.build_rec(3, REC_BATCH, 320, probs=False)
     det = nets.HipSession(det_g, ctx=ctx)
     rec = nets.HipSession(rec_g, ctx=ctx_rec)
     # inputs resident in HBM: copied once, then every step reuses them
@@ -177,8 +381,9 @@ def main():
     both_sync()
 
     K = args.steps
-    # stage-isolated times: each session alone on its own stream
+
     def stage_ms(sess, st):
+        """Each session alone on its own stream: HIP events around K replays."""
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(st)
@@ -200,21 +405,30 @@ def main():
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / K
 
-    # the same step with host buffers at the boundary: det input up, det map
-    # down, rec input up, rec (val, idx) pairs down (pageable host memory)
-    pairs_id = rec_g.outputs[-1]
-    pairs_ptr, pairs_n = rec.tensor_ptr(pairs_id)
-    pairs_host = np.empty(pairs_n, np.float32)
+    # the same step with host buffers at the boundary, through the sessions'
+    # pinned staging buffers (deferred runs): det input up and det map down,
+    # rec input up and rec pairs down
+    det.staging(-1)[:] = det_x
+    det.staging(0)
+    rec.staging(-1)[:] = rec_x
+    rec.staging(0)
     torch.cuda.synchronize()
     h0 = time.perf_counter()
     for _ in range(K):
-        det.run(det_x, outputs=True)
-        rec.run(rec_x, outputs=False)
-        ops.check(lib.qph_memcpy_d2h(ctx_rec, pairs_host.ctypes.data_as(ctypes.c_void_p),
-                                     ctypes.c_void_p(pairs_ptr), pairs_n * 4))
-    both_sync()
+        det.run_async()
+        rec.run_async()
+        det.complete()
+        rec.complete()
     h1 = time.perf_counter()
     host_ms_step = (h1 - h0) * 1e3 / K
+
+    # the rec graph exporting the probability tensor as well
+    rec_p_g, _ = nets.build_rec(3, REC_BATCH, 320, probs=True)
+    rec_p = nets.HipSession(rec_p_g, ctx=ctx_rec)
+    rec_p.run(rec_x, outputs=False)
+    rec_p.sync()
+    rec_p_ms = stage_ms(rec_p, stream_rec)
+    rec_p.close()
 
     # dominant kernel: rec head GEMM, events around each node (eager launches)
     rec.set_profiling(True)
@@ -229,16 +443,16 @@ def main():
     rows = rec_g.numel(d["inp"]) // d["ws"][0]
     head_flops = 2 * rows * d["ws"][0] * d["ws"][1]
     achieved = head_flops / (head_ms * 1e-3) / 1e12
-
+    det.set_profiling(True)
+    for _ in range(K):
+        det.run(None, outputs=False)
+    det.sync()
+    det_node_ms = det.node_times()
+    det.set_profiling(False)
     if args.node_report:
-        det.set_profiling(True)
-        for _ in range(K):
-            det.run(None, outputs=False)
-        det.sync()
-        det_node_ms = det.node_times()
-        det.set_profiling(False)
-        write_node_report(args.node_report, nets, [("det", det_g, det_node_ms),
-                                                   ("rec", rec_g, node_ms)])
+        with open(args.node_report, "w") as f:
+            json.dump(node_rows(nets, "det", det_g, det_node_ms) +
+                      node_rows(nets, "rec", rec_g, node_ms), f, indent=0)
 
     det_flops = nets.flops(det_g)
     rec_flops = nets.flops(rec_g)
@@ -255,10 +469,12 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded inputs, random-init weights)",
-        "config": {"workload": "det 1x3x640x640 (config 3) + rec 32x3x48x320 (config 4) per step",
+        "config": {"workload": "det 1x3x640x640 (config 3) + rec 32x3x48x320 (config 4) per step, "
+                               "rec ending in the CTC (value, index) pairs",
                    "det_gflop": round(det_flops / 1e9, 3), "rec_gflop": round(rec_flops / 1e9, 3)},
         "det_img_per_s": round(1e3 / det_ms, 2),
         "rec_lines_per_s": round(REC_BATCH * 1e3 / rec_ms, 1),
+        "rec_lines_per_s_with_probs": round(REC_BATCH * 1e3 / rec_p_ms, 1),
         "det_ms": round(det_ms, 4),
         "rec_ms": round(rec_ms, 4),
         "serial_ms_per_step": round(det_ms + rec_ms, 4),
@@ -269,28 +485,51 @@ def main():
                      "traffic": head_traffic_bytes(), "avg_launch_ms": round(head_ms, 5)},
     }
 
-    if args.mixed_page:
-        result["mixed_page"] = time_mixed_page(K, args.warmup)
-
+    O = None
+    threads = None
     if not args.no_cpu:
         from oracle import nets as onets
         from oracle import oracle as O
         O.lib()
-        onets.run_graph(det_g, det_x)          # warm-up (page-in, thread pool)
-        c0 = time.perf_counter()
-        for _ in range(args.cpu_steps):
-            onets.run_graph(det_g, det_x)
-            onets.run_graph(rec_g, rec_x)
-        c1 = time.perf_counter()
-        cpu_step = (c1 - c0) / args.cpu_steps
+        threads = cpu_threads()
+        O.set_threads(threads)
+
+    cfgs = {}
+    if not args.no_configs:
+        reps = max(3, K // 5)
+        cfgs["cfg1"] = bench_cfg1(nets, ops, configs, ctx, reps, args.cpu_rounds, O)
+        cfgs.update(bench_cfg2(nets, ops, configs, ctx, reps, args.cpu_rounds, O))
+    cfgs["cfg3"] = {"workload": "det 1x3x640x640 (seed 2)", "img_per_s": result["det_img_per_s"],
+                    "ms": result["det_ms"], "gflop": round(det_flops / 1e9, 3),
+                    "classes": class_fractions(nets, det_g, det_node_ms)}
+    cfgs["cfg4"] = {"workload": "rec 32x3x48x320 (seed 3), pairs exit",
+                    "lines_per_s": result["rec_lines_per_s"], "ms": result["rec_ms"],
+                    "gflop": round(rec_flops / 1e9, 3),
+                    "classes": class_fractions(nets, rec_g, node_ms)}
+    mixed_data = None
+    if not args.no_configs:
+        cfgs["cfg5"], mixed_data = time_mixed_page(max(3, K // 5), 2)
+
+    if O is not None:
+        det_s = cpu_median(lambda: onets.run_graph(det_g, det_x), args.cpu_rounds)
+        rec_s = cpu_median(lambda: onets.run_graph(rec_g, rec_x), args.cpu_rounds)
+        cfgs["cfg3"]["cpu_baseline"] = {"img_per_s": round(1.0 / det_s, 3),
+                                        "rounds": args.cpu_rounds}
+        cfgs["cfg4"]["cpu_baseline"] = {"lines_per_s": round(REC_BATCH / rec_s, 2),
+                                        "rounds": args.cpu_rounds}
+        if mixed_data is not None:
+            cfgs["cfg5"]["cpu_baseline"] = cpu_mixed_page(mixed_data, args.cpu_rounds)
         result["cpu_baseline"] = {
-            "value": round(1.0 / cpu_step, 4),
+            "value": round(1.0 / (det_s + rec_s), 4),
             "unit": result["unit"],
-            "cores": O.threads(),
+            "cores": threads,
             "kind": "port",
-            "sample": f"{args.cpu_steps} steps of det 1x3x640x640 + rec 32x3x48x320, "
-                      f"{cpu_step:.3f} s/step, C oracle -O3 -mavx2 -mfma, OpenMP",
+            "sample": f"det 1x3x640x640 and rec 32x3x48x320 (pairs exit) on the CPU oracle, each "
+                      f"1 warm-up + median of {args.cpu_rounds} rounds ({det_s:.4f} + {rec_s:.4f} "
+                      f"s per step), OpenMP {threads} threads of {os.cpu_count()} logical CPUs "
+                      f"({cpu_model()}), -O3 -mavx2 -mfma, FTZ/DAZ",
         }
+    result["configs"] = cfgs
     print(json.dumps(result))
     det.close()
     rec.close()

@@ -242,7 +242,13 @@ typedef struct {
   const int64_t* weight_sizes;  /* floats per weight */
   int32_t n_outputs;
   const int32_t* outputs;       /* graph output tensor ids */
+  int32_t flags;                /* QPH_NET_* */
 } qph_net_spec;
+
+/* Every node its own launch: no shared launch of independent 3x3 convs, no
+ * depthwise + 1x1 (+ stem) fusion, no channel-last rec blocks (per-op
+ * measurement and debugging; the results are the same bits). */
+#define QPH_NET_SEPARATE_LAUNCHES 1
 
 typedef struct qph_net qph_net;
 
@@ -258,6 +264,24 @@ QPH_API int qph_net_destroy(qph_net* net);
  * captured into a HIP graph on the first run and replayed afterwards. */
 QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_device,
                         float* const* outputs_host);
+/* Deferred runs (DeviceSession::run_deferred + DeferredRun::complete,
+ * device.rs:105-110, 166-176): batch k+1 is packed and submitted while batch
+ * k runs.  qph_net_staging returns the net's pinned host buffer (allocated
+ * on first use with hipHostMalloc, owned by the net) for the input
+ * (slot -1) or output `slot`; a caller that writes its input there and
+ * reads its outputs from there needs no pageable copies.
+ * qph_net_run_async enqueues, on the context stream: the input upload from
+ * its staging buffer (flags & QPH_RUN_UPLOAD; otherwise the input tensor is
+ * used as it is), the graph, and the output downloads into their staging
+ * buffers (flags & QPH_RUN_DOWNLOAD), then returns.  qph_net_complete waits
+ * for all of it.  As in the reference, one net has one run in flight: a
+ * second qph_net_run_async before qph_net_complete is refused (the buffers
+ * are shared); qph_net_run completes a pending run first. */
+#define QPH_RUN_UPLOAD 1
+#define QPH_RUN_DOWNLOAD 2
+QPH_API int qph_net_staging(qph_net* net, int32_t slot, float** host, int64_t* numel);
+QPH_API int qph_net_run_async(qph_net* net, int32_t flags);
+QPH_API int qph_net_complete(qph_net* net);
 /* Device pointer of a tensor of the net (valid until destroy). */
 QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* numel);
 /* Average device time (ms) of each node over the runs since the last reset

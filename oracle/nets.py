@@ -116,7 +116,8 @@ def run_graph(g, x_in, keep=False):
             cols = d["ws"][0]
             p = x.reshape(-1, cols).copy()
             O.softmax_last_dim(p, cols)
-            T[d["out"]] = p.reshape(g.shapes[d["out"]])
+            if d["out"] >= 0:
+                T[d["out"]] = p.reshape(g.shapes[d["out"]])
             if d["out2"] >= 0:
                 T[d["out2"]] = O.ctc_argmax(p).reshape(g.shapes[d["out2"]])
         elif op == OP_CONVT:

@@ -45,6 +45,8 @@ def lib():
         sig = {
             "qpo_threads": ([], I),
             "qpo_set_threads": ([I], None),
+            "qpo_set_scalar": ([I], None),
+            "qpo_exp1x8": ([P, P], None),
             "qpo_exp1": ([F], F),
             "qpo_erf1": ([F], F),
             "qpo_relu_inplace": ([P, I64], None),
@@ -95,6 +97,20 @@ def threads():
 
 def set_threads(n):
     lib().qpo_set_threads(int(n))
+
+
+def exp1x8(x):
+    """exp1 on eight lanes at once (the AVX2 form)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(8)
+    y = np.empty(8, np.float32)
+    lib().qpo_exp1x8(_p(x), _p(y))
+    return y
+
+
+def set_scalar(on):
+    """Every GEMM and softmax in the scalar form (the AVX2 forms give the
+    same bits)."""
+    lib().qpo_set_scalar(int(bool(on)))
 
 
 def exp1(x):

@@ -18,13 +18,16 @@
  * output element's arithmetic is fixed, so results do not depend on the
  * thread count.  Loops are written so gcc -O3 -mavx2 -mfma vectorises them
  * without changing any element's operation sequence (-ffp-contract=off keeps
- * every non-fma a*b+c as two roundings, as Rust does).
+ * every non-fma a*b+c as two roundings, as Rust does).  The GEMMs run whole
+ * 6 x 16 tiles in the register form of the reference's AVX2 panel kernel
+ * (x86.rs:134-444) and the edges in a scalar form; qpo_set_scalar(1) makes
+ * every GEMM scalar, and the test suite checks the two give the same bits.
  */
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
-#include <xmmintrin.h>
+#include <immintrin.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -51,6 +54,12 @@ QPO_API void qpo_set_threads(int n) {
   (void)n;
 #endif
 }
+
+/* Forces the scalar form of the GEMMs and the softmax (for the
+ * scalar-vs-AVX2 self-check of the test suite; both forms give the same
+ * bits). */
+static int g_scalar = 0;
+QPO_API void qpo_set_scalar(int on) { g_scalar = on != 0; }
 
 static inline float bits_f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static inline uint32_t f_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -93,7 +102,29 @@ static inline float erf1(float x) {
   return bits_f(f_bits(r) | (f_bits(x) & 0x80000000u));
 }
 
+/* exp1 on eight lanes: the reference's exp256_ps (x86.rs:28-57) step for
+ * step -- min/max clamp, round-to-nearest-even, two fnmadd steps, the same
+ * Horner fmas, 2^k from exponent bits -- so each lane equals exp1. */
+static inline __m256 exp1x8(__m256 x) {
+  x = _mm256_min_ps(x, _mm256_set1_ps(88.0f));
+  x = _mm256_max_ps(x, _mm256_set1_ps(-88.0f));
+  const __m256 kf = _mm256_round_ps(_mm256_mul_ps(x, _mm256_set1_ps(1.442695f)),
+                                    _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+  __m256 r = _mm256_fnmadd_ps(kf, _mm256_set1_ps(0.6931472f), x);
+  r = _mm256_fnmadd_ps(kf, _mm256_set1_ps(-2.9802322e-8f), r);
+  __m256 p = _mm256_set1_ps(1.0f / 720.0f);
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f / 120.0f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f / 24.0f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f / 6.0f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(0.5f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f));
+  const __m256i ki = _mm256_add_epi32(_mm256_cvtps_epi32(kf), _mm256_set1_epi32(127));
+  return _mm256_mul_ps(_mm256_castsi256_ps(_mm256_slli_epi32(ki, 23)), p);
+}
+
 QPO_API float qpo_exp1(float x) { return exp1(x); }
+QPO_API void qpo_exp1x8(const float* x, float* y) { _mm256_storeu_ps(y, exp1x8(_mm256_loadu_ps(x))); }
 QPO_API float qpo_erf1(float x) { return erf1(x); }
 
 /* ------------------------------------------------------------- activations */
@@ -222,13 +253,26 @@ static void softmax_row(float* row, int64_t inner) {
   int64_t i2 = 0;
   if (inner >= 8) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    while (i2 + 8 <= inner) {
-      for (int j = 0; j < 8; j++) {
-        float ev = exp1(row[i2 + j] - mx);
-        row[i2 + j] = ev;
-        acc[j] += ev;
+    if (g_scalar) {
+      while (i2 + 8 <= inner) {
+        for (int j = 0; j < 8; j++) {
+          float ev = exp1(row[i2 + j] - mx);
+          row[i2 + j] = ev;
+          acc[j] += ev;
+        }
+        i2 += 8;
       }
-      i2 += 8;
+    } else {
+      /* the same eight lane chains as one vector (x86.rs:1091-1134) */
+      const __m256 vm = _mm256_set1_ps(mx);
+      __m256 va = _mm256_setzero_ps();
+      while (i2 + 8 <= inner) {
+        const __m256 ev = exp1x8(_mm256_sub_ps(_mm256_loadu_ps(row + i2), vm));
+        _mm256_storeu_ps(row + i2, ev);
+        va = _mm256_add_ps(va, ev);
+        i2 += 8;
+      }
+      _mm256_storeu_ps(acc, va);
     }
     sum = hsum8(acc);
   }
@@ -279,11 +323,12 @@ QPO_API int qpo_sgemm_path(int64_t m, int64_t n, int64_t k, int serial) {
 
 /* C[M,N] (row stride ldc) = A[M,K] * B where B's row kk starts at
  * brow[kk] (implicit GEMM, gemm.rs:75-128) or at b + kk*ldb; bias per row.
- * Blocking: 4 rows x 32 columns at a time, fma chains in registers. */
-static void gemm_block(const float* a, int64_t lda, const float* b, int64_t ldb,
-                       const float* const* brow, float* c, int64_t ldc, int64_t m, int64_t n,
-                       int64_t k, const float* bias, int path, int64_t i0, int64_t i1,
-                       int64_t j0, int64_t j1) {
+ * Scalar form over rows [i0, i1) x columns [j0, j1): 4 rows x 32 columns at
+ * a time, fma chains in registers. */
+static void gemm_block_scalar(const float* a, int64_t lda, const float* b, int64_t ldb,
+                              const float* const* brow, float* c, int64_t ldc, int64_t m,
+                              int64_t n, int64_t k, const float* bias, int path, int64_t i0,
+                              int64_t i1, int64_t j0, int64_t j1) {
   for (int64_t i = i0; i < i1; i += 4) {
     int64_t ni = i1 - i < 4 ? i1 - i : 4;
     for (int64_t jb = j0; jb < j1; jb += 32) {
@@ -314,6 +359,76 @@ static void gemm_block(const float* a, int64_t lda, const float* b, int64_t ldb,
   }
 }
 
+/* One full 6 x 16 tile at (i, j0) in the register form of the reference's
+ * AVX2 panel micro-kernel (x86.rs:134-444): twelve 8-wide accumulators,
+ * the row's A term broadcast, k ascending, one fma per term -- each
+ * element's chain is exactly the scalar form's. */
+static void tile6x16(const float* a, int64_t lda, const float* b, int64_t ldb,
+                     const float* const* brow, float* c, int64_t ldc, int64_t m, int64_t n,
+                     int64_t k, const float* bias, int path, int64_t i, int64_t j0) {
+  float init[6][16];
+  for (int r = 0; r < 6; r++)
+    for (int j = 0; j < 16; j++)
+      init[r][j] = (bias && bias_seeded(path, i + r, j0 + j, m, n)) ? bias[i + r] : 0.0f;
+  __m256 c0a = _mm256_loadu_ps(init[0]), c0b = _mm256_loadu_ps(init[0] + 8);
+  __m256 c1a = _mm256_loadu_ps(init[1]), c1b = _mm256_loadu_ps(init[1] + 8);
+  __m256 c2a = _mm256_loadu_ps(init[2]), c2b = _mm256_loadu_ps(init[2] + 8);
+  __m256 c3a = _mm256_loadu_ps(init[3]), c3b = _mm256_loadu_ps(init[3] + 8);
+  __m256 c4a = _mm256_loadu_ps(init[4]), c4b = _mm256_loadu_ps(init[4] + 8);
+  __m256 c5a = _mm256_loadu_ps(init[5]), c5b = _mm256_loadu_ps(init[5] + 8);
+  const float* a0 = a + i * lda;
+  for (int64_t kk = 0; kk < k; kk++) {
+    const float* bp = brow ? brow[kk] + j0 : b + kk * ldb + j0;
+    const __m256 b0 = _mm256_loadu_ps(bp), b1 = _mm256_loadu_ps(bp + 8);
+    __m256 av;
+    av = _mm256_broadcast_ss(a0 + kk);
+    c0a = _mm256_fmadd_ps(av, b0, c0a); c0b = _mm256_fmadd_ps(av, b1, c0b);
+    av = _mm256_broadcast_ss(a0 + lda + kk);
+    c1a = _mm256_fmadd_ps(av, b0, c1a); c1b = _mm256_fmadd_ps(av, b1, c1b);
+    av = _mm256_broadcast_ss(a0 + 2 * lda + kk);
+    c2a = _mm256_fmadd_ps(av, b0, c2a); c2b = _mm256_fmadd_ps(av, b1, c2b);
+    av = _mm256_broadcast_ss(a0 + 3 * lda + kk);
+    c3a = _mm256_fmadd_ps(av, b0, c3a); c3b = _mm256_fmadd_ps(av, b1, c3b);
+    av = _mm256_broadcast_ss(a0 + 4 * lda + kk);
+    c4a = _mm256_fmadd_ps(av, b0, c4a); c4b = _mm256_fmadd_ps(av, b1, c4b);
+    av = _mm256_broadcast_ss(a0 + 5 * lda + kk);
+    c5a = _mm256_fmadd_ps(av, b0, c5a); c5b = _mm256_fmadd_ps(av, b1, c5b);
+  }
+  float out[6][16];
+  _mm256_storeu_ps(out[0], c0a); _mm256_storeu_ps(out[0] + 8, c0b);
+  _mm256_storeu_ps(out[1], c1a); _mm256_storeu_ps(out[1] + 8, c1b);
+  _mm256_storeu_ps(out[2], c2a); _mm256_storeu_ps(out[2] + 8, c2b);
+  _mm256_storeu_ps(out[3], c3a); _mm256_storeu_ps(out[3] + 8, c3b);
+  _mm256_storeu_ps(out[4], c4a); _mm256_storeu_ps(out[4] + 8, c4b);
+  _mm256_storeu_ps(out[5], c5a); _mm256_storeu_ps(out[5] + 8, c5b);
+  for (int r = 0; r < 6; r++)
+    for (int j = 0; j < 16; j++) {
+      float v = out[r][j];
+      if (bias && !bias_seeded(path, i + r, j0 + j, m, n)) v = v + bias[i + r];
+      c[(i + r) * ldc + j0 + j] = v;
+    }
+}
+
+/* Rows [i0, i1) x columns [j0, j1) of the GEMM above: whole 6 x 16 tiles in
+ * the AVX2 form, the edges in the scalar form (same bits either way). */
+static void gemm_block(const float* a, int64_t lda, const float* b, int64_t ldb,
+                       const float* const* brow, float* c, int64_t ldc, int64_t m, int64_t n,
+                       int64_t k, const float* bias, int path, int64_t i0, int64_t i1,
+                       int64_t j0, int64_t j1) {
+  if (g_scalar) {
+    gemm_block_scalar(a, lda, b, ldb, brow, c, ldc, m, n, k, bias, path, i0, i1, j0, j1);
+    return;
+  }
+  const int64_t i6 = i0 + (i1 - i0) / 6 * 6, j16 = j0 + (j1 - j0) / 16 * 16;
+  for (int64_t i = i0; i < i6; i += 6)
+    for (int64_t j = j0; j < j16; j += 16)
+      tile6x16(a, lda, b, ldb, brow, c, ldc, m, n, k, bias, path, i, j);
+  if (j16 < j1 && i6 > i0)
+    gemm_block_scalar(a, lda, b, ldb, brow, c, ldc, m, n, k, bias, path, i0, i6, j16, j1);
+  if (i6 < i1)
+    gemm_block_scalar(a, lda, b, ldb, brow, c, ldc, m, n, k, bias, path, i6, i1, j0, j1);
+}
+
 /* sgemm / sgemm_res: gemm.rs:37-70, 223-507.  Result = chain (+bias by the
  * placement rule), then act, then += residual (residual has C's layout). */
 QPO_API void qpo_sgemm(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
@@ -321,15 +436,17 @@ QPO_API void qpo_sgemm(const float* a, const float* b, float* c, int64_t m, int6
                        const float* residual, int serial) {
   if (m == 0 || n == 0 || k == 0) return;
   int path = qpo_sgemm_path(m, n, k, serial);
-  int64_t mblocks = (m + 3) / 4;
+  /* blocks of 48 rows x 128 columns: the B block stays in L2 across the
+   * block's eight 6-row tiles */
+  int64_t mblocks = (m + 47) / 48;
   int64_t nblocks = (n + 127) / 128;
 #pragma omp parallel
   {
     qpo_ftz();
 #pragma omp for schedule(dynamic, 1) collapse(2)
-    for (int64_t mb = 0; mb < mblocks; mb++)
-      for (int64_t nb = 0; nb < nblocks; nb++) {
-        int64_t i0 = mb * 4, i1 = i0 + 4 < m ? i0 + 4 : m;
+    for (int64_t nb = 0; nb < nblocks; nb++)
+      for (int64_t mb = 0; mb < mblocks; mb++) {
+        int64_t i0 = mb * 48, i1 = i0 + 48 < m ? i0 + 48 : m;
         int64_t j0 = nb * 128, j1 = j0 + 128 < n ? j0 + 128 : n;
         gemm_block(a, k, b, n, NULL, c, ldc, m, n, k, bias, path, i0, i1, j0, j1);
       }
@@ -360,8 +477,11 @@ QPO_API int qpo_conv2d_out_shape(const int64_t* xs, const int64_t* ws, const int
  *   1x1 s1 g1 -> sgemm (conv.rs:264-460): per batch item W[M,C] x X[C,HW];
  *   depthwise (g > 1, C/g == 1) -> padded-plane direct conv (conv.rs:461-505,
  *     x86.rs:994-1060): acc = fma(w, x, acc) over ky then kx from 0, + bias;
- *   general -> implicit GEMM per output row (conv.rs:506-637): K order
- *     ch -> ky -> kx, N = ow, panel bias placement, act on each row GEMM.
+ *   general, x-stride 1 or 2 -> implicit GEMM per output row
+ *     (conv.rs:506-637): K order ch -> ky -> kx, N = ow, panel bias
+ *     placement, act on each row GEMM;
+ *   general, other x-strides -> im2col tiles (conv.rs:639-661): same K order,
+ *     N = rows * ow per tile.
  * act then residual (conv.rs:673-713, gemm.rs:478-507). */
 QPO_API int qpo_conv2d(const float* x, const int64_t* xs, const float* wt, const int64_t* ws,
                        const float* bias, const int64_t* p, int act, float c1, float c2, float c3,
@@ -377,7 +497,11 @@ QPO_API int qpo_conv2d(const float* x, const int64_t* xs, const float* wt, const
   const int depthwise = g > 1 && cg == 1;
   const float inv_c1 = 1.0f / c1;
 
-  if (g == 1 && kh == 1 && kw == 1 && sh == 1 && sw == 1) {
+  /* the reference's 1x1 test (conv.rs:264) does not look at the padding; its
+   * GEMM reads X as [C][oh*ow], which is the input only without padding, so a
+   * padded 1x1 conv is taken as the ordinary conv it is (general branch) */
+  if (g == 1 && kh == 1 && kw == 1 && sh == 1 && sw == 1 && ph == 0 && pw == 0 && peh == 0 &&
+      pew == 0) {
     /* 1x1: conv.rs:370-460.  N > 1 with threads > 1 runs sgemm_serial_res
      * per chunk (panel path); N == 1 runs sgemm_res (parallel rules). */
     int serial = n > 1;
@@ -387,7 +511,9 @@ QPO_API int qpo_conv2d(const float* x, const int64_t* xs, const float* wt, const
     return 0;
   }
 
-  if (depthwise) {
+  /* depthwise with one output per channel (conv.rs:461-505 indexes the
+   * weight by input channel); a channel multiplier goes the general way */
+  if (depthwise && m == c) {
     const int64_t pheight = ph + h + peh;
     const int64_t pwidth = pw + wd + pew;
 #pragma omp parallel
@@ -430,8 +556,65 @@ QPO_API int qpo_conv2d(const float* x, const int64_t* xs, const float* wt, const
     return 0;
   }
 
-  /* general grouped conv: implicit GEMM, one output row per sgemm call. */
   const int64_t mg = m / g, kk = cg * kh * kw;
+  if (sw != 1 && sw != 2) {
+    /* im2col branch (conv.rs:639-661, gemm.rs:771-867): tiles of `tile`
+     * output rows, each one sgemm_serial_res over the materialised patch
+     * matrix [kk][rows * ow] (N = rows * ow, so the panel bias rule runs over
+     * the tile's flattened columns).  The tile height is the reference's on
+     * one thread (conv.rs:508-524 with par::threads() == 1):
+     * min(oh, max(1, 2^19 / (kk * ow))). */
+    int64_t tile = ((int64_t)1 << 19) / (kk * ow > 1 ? kk * ow : 1);
+    if (tile < 1) tile = 1;
+    if (tile > oh) tile = oh;
+    const int64_t ntiles = (oh + tile - 1) / tile;
+#pragma omp parallel
+    {
+      qpo_ftz();
+      float* cols = (float*)malloc(sizeof(float) * (size_t)(kk * tile * ow));
+#pragma omp for schedule(dynamic, 1) collapse(3)
+      for (int64_t bn = 0; bn < n; bn++)
+        for (int64_t gi = 0; gi < g; gi++)
+          for (int64_t t = 0; t < ntiles; t++) {
+            const int64_t oy0 = t * tile, rows = oh - oy0 < tile ? oh - oy0 : tile;
+            const int64_t nn = rows * ow;
+            const float* xg = x + (bn * c + gi * cg) * h * wd;
+            /* im2col: row k = (ch, ky, kx), column (r, ox) */
+            for (int64_t ch = 0; ch < cg; ch++)
+              for (int64_t ky = 0; ky < kh; ky++)
+                for (int64_t kx = 0; kx < kw; kx++) {
+                  float* dst = cols + ((ch * kh + ky) * kw + kx) * nn;
+                  for (int64_t r = 0; r < rows; r++) {
+                    const int64_t iy = (oy0 + r) * sh - ph + ky;
+                    for (int64_t ox = 0; ox < ow; ox++) {
+                      const int64_t ix = ox * sw - pw + kx;
+                      dst[r * ow + ox] = (iy >= 0 && iy < h && ix >= 0 && ix < wd)
+                                             ? xg[(ch * h + iy) * wd + ix]
+                                             : 0.0f;
+                    }
+                  }
+                }
+            float* yt = y + (bn * m + gi * mg) * ohw + oy0 * ow;
+            const float* bg = bias ? bias + gi * mg : NULL;
+            gemm_block(wt + gi * mg * kk, kk, cols, nn, NULL, yt, ohw, mg, nn, kk, bg, 0, 0, mg, 0,
+                       nn);
+            if (act != 0)
+              for (int64_t r = 0; r < mg; r++)
+                for (int64_t i = 0; i < nn; i++)
+                  yt[r * ohw + i] = act1(yt[r * ohw + i], act, c1, c2, c3, inv_c1);
+          }
+      free(cols);
+    }
+    if (residual) {
+      int64_t total = n * m * ohw;
+#pragma omp parallel for schedule(static)
+      for (int64_t i = 0; i < total; i++) y[i] = y[i] + residual[i];
+    }
+    return 0;
+  }
+
+  /* general grouped conv, strides 1 and 2 along x: implicit GEMM, one output
+   * row per sgemm call. */
   const int64_t pwidth = (ow - 1) * sw + kw;
 #pragma omp parallel
   {
@@ -634,24 +817,22 @@ QPO_API void qpo_layernorm_chain(const float* x, const float* gamma, const float
  * a: [batch, m, k] (abatch 1 = shared), b: [batch, k, n] (bbatch 1 = shared). */
 QPO_API void qpo_matmul(const float* a, const float* b, float* out, int64_t batch, int64_t m,
                         int64_t k, int64_t n, int a_shared, int b_shared) {
+  /* every element: c = 0; c = fma(a_kk, b_kk_j, c) for kk ascending (no
+   * bias), in blocks of 48 rows x 128 columns per batch item */
+  const int64_t mblocks = (m + 47) / 48, nblocks = (n + 127) / 128;
 #pragma omp parallel
   {
     qpo_ftz();
-    float* crow = (float*)malloc(sizeof(float) * (size_t)n);
-#pragma omp for schedule(static)
-    for (int64_t t = 0; t < batch * m; t++) {
-      int64_t bi = t / m, mm = t % m;
-      const float* ar = a + (a_shared ? 0 : bi * m * k) + mm * k;
-      const float* bp = b + (b_shared ? 0 : bi * k * n);
-      for (int64_t j = 0; j < n; j++) crow[j] = 0.0f;
-      for (int64_t kk = 0; kk < k; kk++) {
-        float av = ar[kk];
-        const float* br = bp + kk * n;
-        for (int64_t j = 0; j < n; j++) crow[j] = fmaf(av, br[j], crow[j]);
-      }
-      memcpy(out + t * n, crow, sizeof(float) * (size_t)n);
-    }
-    free(crow);
+#pragma omp for schedule(dynamic, 1) collapse(3)
+    for (int64_t bi = 0; bi < batch; bi++)
+      for (int64_t nb = 0; nb < nblocks; nb++)
+        for (int64_t mb = 0; mb < mblocks; mb++) {
+          const float* ab = a + (a_shared ? 0 : bi * m * k);
+          const float* bb = b + (b_shared ? 0 : bi * k * n);
+          int64_t i0 = mb * 48, i1 = i0 + 48 < m ? i0 + 48 : m;
+          int64_t j0 = nb * 128, j1 = j0 + 128 < n ? j0 + 128 : n;
+          gemm_block(ab, k, bb, n, NULL, out + bi * m * n, n, m, n, k, NULL, 0, i0, i1, j0, j1);
+        }
   }
 }
 

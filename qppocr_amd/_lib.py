@@ -13,6 +13,8 @@ QPH_OK = 0
 ACT_NONE, ACT_GELU, ACT_RELU, ACT_HARDSWISH, ACT_SIGMOID = 0, 1, 2, 3, 4
 OP_CONV, OP_CONVT_PAIR_SIG, OP_LINEAR, OP_LAYERNORM, OP_ATTENTION = 1, 2, 3, 4, 5
 OP_SOFTMAX_ARGMAX, OP_CONVT, OP_ACT = 6, 7, 8
+RUN_UPLOAD, RUN_DOWNLOAD = 1, 2
+NET_SEPARATE_LAUNCHES = 1
 
 I64 = ctypes.c_int64
 I32 = ctypes.c_int32
@@ -47,7 +49,7 @@ class NetSpec(ctypes.Structure):
     _fields_ = [("n_tensors", I32), ("shapes", ctypes.POINTER(I64)),
                 ("alias", ctypes.POINTER(I32)), ("n_nodes", I32), ("nodes", ctypes.POINTER(Node)),
                 ("n_weights", I32), ("weight_sizes", ctypes.POINTER(I64)), ("n_outputs", I32),
-                ("outputs", ctypes.POINTER(I32))]
+                ("outputs", ctypes.POINTER(I32)), ("flags", I32)]
 
 
 # exported symbol -> (argtypes, restype); every symbol include/qppocr_hip.h declares
@@ -89,6 +91,9 @@ SIGNATURES = {
     "qph_net_destroy": ([P], ctypes.c_int),
     "qph_net_run": ([P, P, I32, ctypes.POINTER(P)], ctypes.c_int),
     "qph_net_tensor": ([P, I32, ctypes.POINTER(P), ctypes.POINTER(I64)], ctypes.c_int),
+    "qph_net_staging": ([P, I32, ctypes.POINTER(P), ctypes.POINTER(I64)], ctypes.c_int),
+    "qph_net_run_async": ([P, I32], ctypes.c_int),
+    "qph_net_complete": ([P], ctypes.c_int),
     "qph_net_set_profiling": ([P, I32], ctypes.c_int),
     "qph_net_node_times": ([P, ctypes.POINTER(ctypes.c_double), I32], ctypes.c_int),
 }

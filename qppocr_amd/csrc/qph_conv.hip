@@ -32,28 +32,33 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define CONV_LDS_FLOATS 16320  // 63.75 KB per workgroup: halo tile + weight slice
 
-// wk[k][mo] = w[mo][k] for k < kk, mo < m; zero elsewhere (Kpad x Mpad).
-__global__ void repack_conv_w_kernel(const float* __restrict__ w, int64_t m, int64_t kk,
+// Group g (blockIdx.y) of an ONNX [group * mg][kk] weight:
+// wk[g][k][mo] = w[g * mg + mo][k] for k < kk, mo < mg; zero elsewhere
+// (Kpad x Mpad per group).
+__global__ void repack_conv_w_kernel(const float* __restrict__ w, int64_t mg, int64_t kk,
                                      int64_t kpad, int64_t mpad, float* __restrict__ wk) {
   int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= kpad * mpad) return;
+  const int64_t g = blockIdx.y;
   int64_t k = idx / mpad, mo = idx - k * mpad;
-  wk[idx] = (k < kk && mo < m) ? w[mo * kk + k] : 0.0f;
+  wk[g * kpad * mpad + idx] = (k < kk && mo < mg) ? w[(g * mg + mo) * kk + k] : 0.0f;
 }
 
 static inline int64_t mpad_of(int64_t m) { return (m + 31) / 32 * 32; }
 static inline int64_t kpad_of(int64_t cg, int64_t khkw) { return (cg + 3) / 4 * 4 * khkw; }
 
-int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw) {
-  return kpad_of(cg, kh * kw) * mpad_of(m);
+int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw, int64_t group) {
+  return group * kpad_of(cg, kh * kw) * mpad_of(m / group);
 }
 
 int launch_repack_conv_w_taps(const float* wt, int64_t m, int64_t cg, int64_t khkw, float* wk,
-                              hipStream_t s) {
-  int64_t kpad = kpad_of(cg, khkw), mpad = mpad_of(m);
+                              hipStream_t s, int64_t group) {
+  if (group < 1 || group > 65535 || m % group) return fail(QPH_EINVAL, "repack: bad group");
+  const int64_t mg = m / group;
+  int64_t kpad = kpad_of(cg, khkw), mpad = mpad_of(mg);
   int64_t total = kpad * mpad;
-  hipLaunchKernelGGL(repack_conv_w_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, wt, m,
-                     cg * khkw, kpad, mpad, wk);
+  hipLaunchKernelGGL(repack_conv_w_kernel, dim3(ceil_div(total, 256), (unsigned)group), dim3(256),
+                     0, s, wt, mg, cg * khkw, kpad, mpad, wk);
   return launch_check("repack_conv_w_kernel");
 }
 
@@ -63,14 +68,38 @@ struct DenseConvK {
   const float* bias;
   const float* res;
   float* y;
+  // c, m: input / output channels of one group (C/g, M/g); ctot, mtot: of
+  // the tensors; group g reads channels [g c, g c + c), writes [g m, g m + m)
   int64_t c, h, w, m, mpad, kpad, kh, kw, sh, sw, ph, pw, oh, ow;
+  int64_t ctot, mtot, group;
   int64_t y_ctotal, y_coff, y_up;
+  int64_t seed_tile;   // 0: bias rule per output row (implicit GEMM, N = ow);
+                       // > 0: im2col tiles of this many rows (N = rows * ow)
   int tw, th;          // pixel block: th rows x tw cols
   int cchunk;          // input channels per LDS fill (multiple of 4)
   int rt, ct;          // halo rows / cols
   int tiles_x;         // pixel blocks along ow
   Act act;
 };
+
+// Where the reference seeds the chain with the bias (gemm.rs:7-16, panel
+// path): rows in the M % 4 tail of a 32-column panel narrower than 32.  The
+// implicit-GEMM branch (conv.rs:595-637) runs one GEMM per output row (N =
+// ow, column ox); the im2col branch (conv.rs:639-661, strides other than 1
+// and 2) one per tile of seed_tile output rows (N = rows * ow, column
+// (oy - tile start) * ow + ox).
+__device__ __forceinline__ bool dense_bias_seeded(const DenseConvK& p, int64_t co, int64_t oy,
+                                                  int64_t ox) {
+  if (co < p.m - p.m % 4) return false;
+  int64_t j = ox, n = p.ow;
+  if (p.seed_tile > 0) {
+    const int64_t t0 = oy / p.seed_tile * p.seed_tile;
+    const int64_t rows = p.oh - t0 < p.seed_tile ? p.oh - t0 : p.seed_tile;
+    j = (oy - t0) * p.ow + ox;
+    n = rows * p.ow;
+  }
+  return n - ((j >> 5) << 5) < 32;
+}
 
 // Writes v to the up x up block of output pixel (oy, ox) (nearest upsample
 // by an integer factor); rows as 16-byte stores when up is 4 or 8.
@@ -94,16 +123,20 @@ __device__ __forceinline__ void store_replicated(float* yb, int64_t yow, int64_t
 }
 
 // WM: waves along M (1: 16 channels, 4 waves along pixels; 2: 32 channels,
-// 2 waves along pixels).  NT: 16-pixel MFMA tiles per wave.  T: taps (kh*kw).
+// 2 waves along pixels).  NT: 16-pixel MFMA tiles per wave.  T: taps (kh*kw),
+// or 0 for any tap count (offsets computed per k-step instead of held in
+// registers).  blockIdx.z = batch item * group + group index.
 template <int WM, int NT, int T>
 __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
   constexpr int MB = 16 * WM;            // output channels per workgroup (4/WM waves along pixels)
+  constexpr int TR = T > 0 ? T : 1;      // register arrays of the fixed-tap form
   __shared__ float lds[CONV_LDS_FLOATS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wp = wave / WM;
   const int lg = lane >> 4, l16 = lane & 15;
-  const int64_t bn = blockIdx.z;
+  const int64_t bn = blockIdx.z / p.group, grp = blockIdx.z - bn * p.group;
+  const int taps = T > 0 ? T : (int)(p.kh * p.kw);
   const int64_t mblk0 = (int64_t)blockIdx.y * MB;
   const int64_t m0 = mblk0 + 16 * wm;
   const int tyb = blockIdx.x / p.tiles_x, txb = blockIdx.x - tyb * p.tiles_x;
@@ -128,15 +161,17 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
   }
   // per-lane offset of k-step s inside a group of four channels:
   // k_local = 4 s + lg -> channel k_local / T, tap k_local % T
-  int goff[T];
-#pragma unroll
-  for (int s = 0; s < T; s++) {
+  auto step_off = [&](int s) {
     int kl = 4 * s + lg;
-    int ci = kl / T, tap = kl - ci * T;
+    int ci = kl / taps, tap = kl - ci * taps;
     int ky = tap / kw, kx = tap - ky * kw;
-    goff[s] = ci * plane + ky * p.ct + kx;
-  }
+    return ci * plane + ky * p.ct + kx;
+  };
+  int goff[TR];
+#pragma unroll
+  for (int s = 0; s < TR; s++) goff[s] = T > 0 ? step_off(s) : 0;
 
+  const float* bias_g = p.bias ? p.bias + grp * p.m : nullptr;
   // accumulators (bias-seeded where the reference seeds)
   f32x4 acc[NT];
 #pragma unroll
@@ -145,27 +180,25 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
     for (int v = 0; v < 4; v++) {
       float s0 = 0.0f;
       int64_t co = m0 + 4 * lg + v;
-      if (p.bias && co < p.m && pval[t]) {
-        int64_t n0 = (pox[t] >> 5) << 5;
-        if ((p.ow - n0) < 32 && co >= p.m - p.m % 4) s0 = p.bias[co];
-      }
+      if (bias_g && co < p.m && pval[t] && dense_bias_seeded(p, co, poy[t], pox[t]))
+        s0 = bias_g[co];
       acc[t][v] = s0;
     }
 
-  // input image and repacked weights as buffer resources: offsets past the
-  // end read as 0
-  const float* xn = p.x + bn * p.c * p.h * p.w;
+  // input image (this group's channels) and repacked weights as buffer
+  // resources: offsets past the end read as 0
+  const float* xn = p.x + (bn * p.ctot + grp * p.c) * p.h * p.w;
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc((void*)xn, 0, (int)(p.c * p.h * p.w * 4), 0x00020000);
-  const __amdgpu_buffer_rsrc_t wr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)p.wk, 0, (int)(p.kpad * p.mpad * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.wk + grp * p.kpad * p.mpad), 0, (int)(p.kpad * p.mpad * 4), 0x00020000);
   const unsigned OOB = 0x80000000u;
 
   const int cpad = (int)((p.c + 3) / 4 * 4);
   for (int c0 = 0; c0 < cpad; c0 += p.cchunk) {
     const int cc = (cpad - c0) < p.cchunk ? (cpad - c0) : p.cchunk;  // multiple of 4
     float* tile = lds;
-    float* wsl = lds + ((cc * plane + 63) & ~63);     // [cc*T][MB]
+    float* wsl = lds + ((cc * plane + 63) & ~63);     // [cc*taps][MB]
     __syncthreads();
     // halo fill: cc channels x rt rows, one buffer->LDS load per 64 columns
     const int nrows = cc * p.rt;
@@ -189,8 +222,8 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
     // load moves 64/MB consecutive rows
     {
       constexpr int RPL = 64 / MB;   // rows per load
-      const int nkr = cc * T;
-      const int kr0 = c0 * T;
+      const int nkr = cc * taps;
+      const int kr0 = c0 * taps;
       const int lr = lane / MB, lc = lane - lr * MB;
       for (int r0 = wave * RPL; r0 < nkr; r0 += 4 * RPL) {
         const int kr = r0 + lr;
@@ -206,19 +239,32 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
     const float* wl = wsl + 16 * wm + l16;
     for (int q = 0; q < cc / 4; q++) {
       const float* tq = tile + q * 4 * plane;
-      const float* wq = wl + q * 4 * T * MB;
-      float a[T], b[T][NT];
+      const float* wq = wl + q * 4 * taps * MB;
+      if constexpr (T > 0) {
+        float a[T], b[T][NT];
 #pragma unroll
-      for (int s = 0; s < T; s++) {
-        a[s] = wq[(4 * s + lg) * MB];
+        for (int s = 0; s < T; s++) {
+          a[s] = wq[(4 * s + lg) * MB];
 #pragma unroll
-        for (int t = 0; t < NT; t++) b[s][t] = tq[goff[s] + poff[t]];
+          for (int t = 0; t < NT; t++) b[s][t] = tq[goff[s] + poff[t]];
+        }
+#pragma unroll
+        for (int s = 0; s < T; s++)
+#pragma unroll
+          for (int t = 0; t < NT; t++)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s][t], acc[t], 0, 0, 0);
+      } else {
+        for (int s = 0; s < taps; s++) {
+          const int go = step_off(s);
+          const float a = wq[(4 * s + lg) * MB];
+          float b[NT];
+#pragma unroll
+          for (int t = 0; t < NT; t++) b[t] = tq[go + poff[t]];
+#pragma unroll
+          for (int t = 0; t < NT; t++)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[t], acc[t], 0, 0, 0);
+        }
       }
-#pragma unroll
-      for (int s = 0; s < T; s++)
-#pragma unroll
-        for (int t = 0; t < NT; t++)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s][t], acc[t], 0, 0, 0);
     }
   }
 
@@ -237,15 +283,12 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
       badd[t][v] = 0.0f;
       rv[t][v] = 0.0f;
       if (!ok[t][v]) continue;
-      if (p.bias) {
-        int64_t n0 = (pox[t] >> 5) << 5;
-        bool seeded = (p.ow - n0) < 32 && co >= p.m - p.m % 4;
-        if (!seeded) {
-          badd[t][v] = p.bias[co];
-          hadd[t][v] = true;
-        }
+      if (bias_g && !dense_bias_seeded(p, co, poy[t], pox[t])) {
+        badd[t][v] = bias_g[co];
+        hadd[t][v] = true;
       }
-      if (p.res) rv[t][v] = p.res[((bn * p.m + co) * p.oh + poy[t]) * p.ow + pox[t]];
+      if (p.res)
+        rv[t][v] = p.res[((bn * p.mtot + grp * p.m + co) * p.oh + poy[t]) * p.ow + pox[t]];
     }
 #pragma unroll
   for (int t = 0; t < NT; t++)
@@ -257,7 +300,7 @@ __global__ __launch_bounds__(256) void dense_conv_kernel(DenseConvK p) {
       if (hadd[t][v]) xv = xv + badd[t][v];
       xv = act_apply(xv, p.act);
       if (p.res) xv = xv + rv[t][v];
-      float* yb = p.y + ((bn * p.y_ctotal + p.y_coff + co) * yoh) * yow;
+      float* yb = p.y + ((bn * p.y_ctotal + p.y_coff + grp * p.m + co) * yoh) * yow;
       store_replicated(yb, yow, poy[t], pox[t], (int)p.y_up, xv);
     }
 }
@@ -675,7 +718,9 @@ static void direct_params(const ConvArgs& a, const float* wk, DirectConvK& p) {
 }
 
 bool direct3x3_eligible(const ConvArgs& a) {
-  return a.kh == 3 && a.kw == 3 && a.group == 1 &&
+  // strides 1 and 2 along x: the implicit-GEMM branch and its per-row bias
+  // rule (other strides take the im2col branch's rule, dense_conv_kernel)
+  return a.kh == 3 && a.kw == 3 && a.group == 1 && (a.sw == 1 || a.sw == 2) &&
          a.c * a.h * a.w * 4 < (int64_t)0x80000000 && a.oh * a.ow < (1ll << 30) &&
          kpad_of(a.c, 9) * mpad_of(a.m) * 4 < (int64_t)0x80000000 &&
          (int64_t)ceil_div(a.m, 16) * ceil_div(a.oh * a.ow, 16) * a.n < (1ll << 29);
@@ -871,27 +916,32 @@ static int launch_smallc(const ConvArgs& a, hipStream_t s) {
   return launch_check("conv_smallc_kernel");
 }
 
-int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
-  if (smallc_eligible(a)) return launch_smallc(a, s);
+// Tile height of the reference's im2col branch (conv.rs:508-524) as it runs
+// on one thread: min(oh, max(1, 2^19 / (kk * ow))).  It sets N of each tile
+// GEMM and so where the bias is seeded.
+static int64_t im2col_tile_rows(const ConvArgs& a) {
+  const int64_t kk = a.c / a.group * a.kh * a.kw;
+  int64_t t = (int64_t(1) << 19) / std::max<int64_t>(1, kk * a.ow);
+  t = std::max<int64_t>(1, t);
+  return std::min(t, a.oh);
+}
+
+// Launch configuration of the implicit-GEMM kernel (also the validity check
+// a session runs at create time).
+static int dense_conv_config(const ConvArgs& a, DenseConvK& p, dim3& grid, bool& wide_m) {
   const int64_t khkw = a.kh * a.kw;
-  if (khkw != 9 && khkw != 25 && khkw != 1 && khkw != 4)
-    return fail(QPH_EUNSUPPORTED, "dense conv: kernel sizes with kh*kw in {1, 4, 9, 25} only");
-  const float* wk = a.wk;
-  if (!wk) {
-    if (!scratch_wk) return fail(QPH_EINVAL, "dense conv: no repacked weights");
-    QPH_TRY(launch_repack_conv_w_taps(a.wt, a.m, a.c, khkw, scratch_wk, s));
-    wk = scratch_wk;
-  }
-  // 3x3: direct kernel (input and weight buffers within 32-bit offsets)
-  if (direct3x3_eligible(a)) return launch_direct3x3(a, wk, s);
-  DenseConvK p{};
-  p.x = a.x; p.wk = wk; p.bias = a.bias; p.res = a.res; p.y = a.y;
-  p.c = a.c; p.h = a.h; p.w = a.w; p.m = a.m; p.mpad = mpad_of(a.m);
+  const int64_t g = a.group;
+  const int64_t cg = a.c / g, mg = a.m / g;
+  p = DenseConvK{};
+  p.x = a.x; p.wk = a.wk; p.bias = a.bias; p.res = a.res; p.y = a.y;
+  p.c = cg; p.h = a.h; p.w = a.w; p.m = mg; p.mpad = mpad_of(mg);
+  p.ctot = a.c; p.mtot = a.m; p.group = g;
   p.kh = a.kh; p.kw = a.kw; p.sh = a.sh; p.sw = a.sw; p.ph = a.ph; p.pw = a.pw;
   p.oh = a.oh; p.ow = a.ow;
   p.y_ctotal = a.y_ctotal; p.y_coff = a.y_coff; p.y_up = a.y_up;
+  p.seed_tile = (a.sw == 1 || a.sw == 2) ? 0 : im2col_tile_rows(a);
   p.act = a.act;
-  const bool wide_m = a.m > 16;
+  wide_m = mg > 16;
   const int mb = wide_m ? 32 : 16;
   // 2 MFMA tiles per wave; pixels per workgroup: 64 (WM=2) or 128 (WM=1)
   const int pix = wide_m ? 64 : 128;
@@ -901,28 +951,56 @@ int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
   p.ct = (int)((p.tw - 1) * a.sw + a.kw);
   const int plane = p.rt * p.ct;
   if (p.ct > 128) return fail(QPH_EUNSUPPORTED, "dense conv: halo row wider than 128");
-  if (a.c * a.h * a.w * 4 >= (int64_t)0x80000000)
+  if (cg * a.h * a.w * 4 >= (int64_t)0x80000000)
     return fail(QPH_EUNSUPPORTED, "dense conv: input image larger than 2 GB");
   // channel chunk (multiple of 4): halo + weight slice within the LDS budget
-  const int per4 = 4 * (plane + (int)khkw * mb);
-  int groups = (CONV_LDS_FLOATS - 64) / per4;
-  const int64_t cpad = (a.c + 3) / 4 * 4;
+  const int64_t per4 = 4 * ((int64_t)plane + khkw * mb);
+  int64_t groups = (CONV_LDS_FLOATS - 64) / per4;
+  const int64_t cpad = (cg + 3) / 4 * 4;
   if (groups <= 0) return fail(QPH_EUNSUPPORTED, "dense conv: kernel too large for the LDS tile");
-  if ((int64_t)groups * 4 > cpad) groups = (int)(cpad / 4);
-  p.cchunk = 4 * groups;
-  p.kpad = kpad_of(a.c, khkw);
+  if (groups * 4 > cpad) groups = cpad / 4;
+  p.cchunk = (int)(4 * groups);
+  p.kpad = kpad_of(cg, khkw);
   if (p.kpad * p.mpad * 4 >= (int64_t)0x80000000)
     return fail(QPH_EUNSUPPORTED, "dense conv: weights larger than 2 GB");
   p.tiles_x = (int)ceil_div(a.ow, p.tw);
-  const int tiles_y = (int)ceil_div(a.oh, p.th);
-  dim3 grid((unsigned)(p.tiles_x * tiles_y), ceil_div(a.m, mb), (unsigned)a.n);
-  if (a.n > 65535 || (int64_t)p.tiles_x * tiles_y > (1ll << 31))
+  const int64_t tiles_y = ceil_div(a.oh, p.th);
+  if (a.n * g > 65535 || (int64_t)p.tiles_x * tiles_y >= (1ll << 31))
     return fail(QPH_EUNSUPPORTED, "dense conv: grid too large");
+  grid = dim3((unsigned)(p.tiles_x * tiles_y), ceil_div(mg, mb), (unsigned)(a.n * g));
+  return QPH_OK;
+}
+
+int dense_conv_check(const ConvArgs& a) {
+  if (smallc_eligible(a)) return QPH_OK;
+  DenseConvK p;
+  dim3 grid;
+  bool wide_m;
+  return dense_conv_config(a, p, grid, wide_m);
+}
+
+int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk) {
+  if (smallc_eligible(a)) return launch_smallc(a, s);
+  const int64_t khkw = a.kh * a.kw;
+  const float* wk = a.wk;
+  if (!wk) {
+    if (!scratch_wk) return fail(QPH_EINVAL, "dense conv: no repacked weights");
+    QPH_TRY(launch_repack_conv_w_taps(a.wt, a.m, a.c / a.group, khkw, scratch_wk, s, a.group));
+    wk = scratch_wk;
+  }
+  // 3x3: direct kernel (input and weight buffers within 32-bit offsets)
+  if (direct3x3_eligible(a)) return launch_direct3x3(a, wk, s);
+  DenseConvK p;
+  dim3 grid;
+  bool wide_m;
+  QPH_TRY(dense_conv_config(a, p, grid, wide_m));
+  p.wk = wk;
   switch (khkw) {
     case 9: return launch_dense_t<9>(p, wide_m, grid, s);
     case 25: return launch_dense_t<25>(p, wide_m, grid, s);
     case 4: return launch_dense_t<4>(p, wide_m, grid, s);
-    default: return launch_dense_t<1>(p, wide_m, grid, s);
+    case 1: return launch_dense_t<1>(p, wide_m, grid, s);
+    default: return launch_dense_t<0>(p, wide_m, grid, s);
   }
 }
 

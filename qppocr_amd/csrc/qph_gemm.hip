@@ -749,24 +749,13 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
 }
 
 static int launch_wave(const GemmArgs& g, hipStream_t s) {
-  static int occ_dev[64], cus_dev[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-    return fail(QPH_EHIP, "gemm: no current device (or index past 63)");
-  if (occ_dev[dev] == 0) {
-    int occ = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)gemm_wave_kernel<true>, 64, 0) !=
-            hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        occ <= 0 || cus <= 0)
-      return fail(QPH_EHIP, "gemm: occupancy query failed");
-    cus_dev[dev] = cus;
-    occ_dev[dev] = occ;
-  }
+  int occ = 0, cus = 0;
+  QPH_TRY(device_cus(nullptr, &cus));
+  QPH_TRY(kernel_occupancy((const void*)gemm_wave_kernel<true>, 64, &occ));
   const int mb = (int)ceil_div(g.m, 64), nb = (int)ceil_div(g.n, 64);
   const int ntiles = mb * nb * (int)g.batch;
   const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
-  const int wg_xcd = std::max(1, std::min(per_xcd, occ_dev[dev] * cus_dev[dev] / NUM_XCD));
+  const int wg_xcd = std::max(1, std::min(per_xcd, occ * cus / NUM_XCD));
   // whole 64-row blocks: every tile issues its 16 row stores, which the
   // next tile's first wait counts on; 16-byte aligned output rows
   const bool rows = g.m % 64 == 0 && g.ldc % 4 == 0 && (uintptr_t)g.c % 16 == 0 &&
@@ -788,24 +777,13 @@ static bool wide_fits(const GemmArgs& g) {
 }
 
 static int launch_wide(const GemmArgs& g, hipStream_t s) {
-  static int occ_dev[64], cus_dev[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-    return fail(QPH_EHIP, "gemm: no current device (or index past 63)");
-  if (occ_dev[dev] == 0) {
-    int occ = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)gemm_wide_kernel, 256, 0) !=
-            hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        occ <= 0 || cus <= 0)
-      return fail(QPH_EHIP, "gemm: occupancy query failed");
-    cus_dev[dev] = cus;
-    occ_dev[dev] = occ;
-  }
+  int occ = 0, cus = 0;
+  QPH_TRY(device_cus(nullptr, &cus));
+  QPH_TRY(kernel_occupancy((const void*)gemm_wide_kernel, 256, &occ));
   const int mb = (int)ceil_div(g.m, 128), nb = (int)ceil_div(g.n, 128);
   const int ntiles = mb * nb * (int)g.batch;
   const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
-  const int wg_xcd = std::max(1, std::min(per_xcd, occ_dev[dev] * cus_dev[dev] / NUM_XCD));
+  const int wg_xcd = std::max(1, std::min(per_xcd, occ * cus / NUM_XCD));
   hipLaunchKernelGGL(gemm_wide_kernel, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(256), 0, s, g, mb,
                      nb, ntiles, per_xcd, wg_xcd);
   return launch_check("gemm_wide_kernel");
@@ -1089,19 +1067,10 @@ static void launch_lt(const LinArgs& g, hipStream_t s) {
 int launch_linear_nt(const LinArgs& g, hipStream_t s) {
   if (!linear_nt_eligible(g.m, g.n, g.k, g.lda))
     return fail(QPH_EUNSUPPORTED, "linear: shape outside the resident-weight kernel");
-  static int cus_dev[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-    return fail(QPH_EHIP, "linear: no current device (or index past 63)");
-  if (cus_dev[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      return fail(QPH_EHIP, "linear: device query failed");
-    cus_dev[dev] = cus;
-  }
+  int cus_i = 0;
+  QPH_TRY(device_cus(nullptr, &cus_i));
   const int64_t tiles = (int64_t)ceil_div(g.m, 32) * ceil_div(g.n, 32);
-  const int64_t cus = cus_dev[dev];
+  const int64_t cus = cus_i;
   if (g.k <= 128 || (tiles > 3 * cus && tiles <= 4 * cus))
     launch_lt<32, 32, 2>(g, s);
   else

@@ -143,6 +143,13 @@ inline Act make_act(const qph_act* a) {
 
 inline bool act_valid(const qph_act* a) { return !a || (a->kind >= 0 && a->kind <= 4); }
 
+// The conv the reference runs as a plain GEMM over X[C][H*W] (conv.rs:264):
+// 1x1, stride 1, one group; padding excluded (X is then not that matrix).
+inline bool conv_is_pointwise(const int64_t ws[4], const qph_conv_params& p) {
+  return p.group == 1 && ws[2] == 1 && ws[3] == 1 && p.sh == 1 && p.sw == 1 && p.ph == 0 &&
+         p.pw == 0 && p.peh == 0 && p.pew == 0;
+}
+
 // -------------------------------------------------------- launch helpers
 
 inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
@@ -246,6 +253,11 @@ struct DwPwArgs {
 // Lets kernel fn take up to the whole 160 KB of a CU's LDS as dynamic
 // shared memory; the attribute is set once per kernel and device.
 int allow_full_lds(const void* fn);
+// Compute units of the current device and the resident workgroups per CU of
+// kernel fn at `block` threads (no dynamic LDS), each queried once per
+// device (and kernel) and cached; safe to call from several host threads.
+int device_cus(int* dev_out, int* cus);
+int kernel_occupancy(const void* fn, int block, int* occ);
 bool dwpw_eligible(const DwPwArgs& a);
 // the stem conv that can run inside the dw + pw launch of a (3 -> a.c
 // channels, 3x3, stride 2, pad 1, into a 3x3 stride-2 pad-1 depthwise)
@@ -257,11 +269,14 @@ int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s);
 int launch_depthwise(const ConvArgs& a, hipStream_t s);
 // depthwise conv with x and y channel-last ([n][h][w][c]); 3x3 and 5x5
 int launch_depthwise_cl(const ConvArgs& a, hipStream_t s);
-int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw);
-// wk[Kpad][Mpad] k-major copy of an ONNX [M][cg][kh][kw] weight, Kpad =
-// ceil(cg/4)*4*khkw, Mpad = ceil(M/32)*32, zero-filled past the real extent.
+int64_t dense_conv_wk_floats(int64_t m, int64_t cg, int64_t kh, int64_t kw, int64_t group = 1);
+// Per group, wk[Kpad][Mpad] k-major copy of that group's rows of an ONNX
+// [M][cg][kh][kw] weight, Kpad = ceil(cg/4)*4*khkw, Mpad = ceil(M/g/32)*32,
+// zero-filled past the real extent; groups follow each other.
 int launch_repack_conv_w_taps(const float* wt, int64_t m, int64_t cg, int64_t khkw, float* wk,
-                              hipStream_t s);
+                              hipStream_t s, int64_t group = 1);
+// The implicit-GEMM launch checks of a dense (or grouped) conv, no launch.
+int dense_conv_check(const ConvArgs& a);
 
 int launch_convt2x2(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, const float* wt,
                     int64_t m, float* y, hipStream_t s);

@@ -38,6 +38,11 @@ struct qph_net {
   std::vector<hipEvent_t> ev;
   std::vector<double> node_ms;
   int64_t prof_runs;
+  // deferred runs: pinned host staging of the input and of each output
+  float* in_stage;
+  std::vector<float*> out_stage;
+  hipEvent_t done;
+  bool inflight;
 };
 
 static int64_t numel_of(const qph_net* net, int32_t id) {
@@ -81,7 +86,7 @@ static int run_node(qph_net* net, size_t i) {
   hipStream_t s = ctx->stream;
   const int64_t* xs = &net->shapes[4 * (size_t)n.in];
   float* x = net->tptr[n.in];
-  float* y = net->tptr[n.out];
+  float* y = n.out >= 0 ? net->tptr[n.out] : nullptr;
   const float* w = n.w >= 0 ? net->weights[n.w] : nullptr;
   const float* bias = n.bias >= 0 ? net->weights[n.bias] : nullptr;
   const float* w2 = n.w2 >= 0 ? net->weights[n.w2] : nullptr;
@@ -423,7 +428,9 @@ static int plan_dwpw(qph_net* net) {
 static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t nw) {
   const qph_node& n = net->nodes[i];
   QPH_TRY(check_tensor(net, n.in, false, i, n, "input"));
-  QPH_TRY(check_tensor(net, n.out, false, i, n, "output"));
+  // a softmax node may export pairs only (out = -1, the rec_argmax_pairs
+  // exit of device.rs:160-165)
+  QPH_TRY(check_tensor(net, n.out, n.op == QPH_OP_SOFTMAX_ARGMAX, i, n, "output"));
   QPH_TRY(check_tensor(net, n.in2, true, i, n, "second input"));
   QPH_TRY(check_tensor(net, n.out2, true, i, n, "second output"));
   for (int32_t wi : {n.w, n.bias, n.w2})
@@ -493,9 +500,12 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
       return QPH_OK;
     }
     case QPH_OP_LAYERNORM:
-      if (n.w < 0 || n.bias < 0 || wsize(n.w) != n.ws[0] || wsize(n.bias) != n.ws[0] ||
-          numel_of(net, n.in) % n.ws[0] || numel_of(net, n.out) != numel_of(net, n.in))
+      if (n.w < 0 || n.bias < 0 || n.ws[0] <= 0 || wsize(n.w) != n.ws[0] ||
+          wsize(n.bias) != n.ws[0] || numel_of(net, n.in) % n.ws[0] ||
+          numel_of(net, n.out) != numel_of(net, n.in))
         return fail(QPH_EINVAL, node_name(i, n) + ": layernorm shapes");
+      if (n.ws[0] > 4096)
+        return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": layernorm rows wider than 4096");
       return QPH_OK;
     case QPH_OP_ATTENTION:
       if (xs[2] * xs[3] != 3 * n.heads * n.dh || n.dh > 64 || xs[1] > 256 ||
@@ -505,8 +515,10 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
         return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": attention too large for LDS");
       return QPH_OK;
     case QPH_OP_SOFTMAX_ARGMAX:
-      if (n.ws[0] <= 0 || n.ws[0] > 32768 || numel_of(net, n.in) % n.ws[0] ||
-          numel_of(net, n.out) != numel_of(net, n.in))
+      if (n.out < 0 && n.out2 < 0)
+        return fail(QPH_EINVAL, node_name(i, n) + ": softmax without an output");
+      if (n.ws[0] <= 0 || n.ws[0] >= (1ll << 31) || numel_of(net, n.in) % n.ws[0] ||
+          (n.out >= 0 && numel_of(net, n.out) != numel_of(net, n.in)))
         return fail(QPH_EINVAL, node_name(i, n) + ": softmax row width / probs size");
       if (n.out2 >= 0 && numel_of(net, n.out2) != 2 * (numel_of(net, n.in) / n.ws[0]))
         return fail(QPH_EINVAL, node_name(i, n) + ": pairs size mismatch");
@@ -536,12 +548,37 @@ static int run_all(qph_net* net) {
       QPH_TRY(launch_dwpw(net->dwpw[i], s));
       step = net->dwpw[i].stem ? 3 : 2;
     } else {
-      QPH_TRY(run_node(net, i));
+      const int rc = run_node(net, i);
+      if (rc != QPH_OK) return fail(rc, node_name(i, net->nodes[i]) + ": " + qph_last_error());
     }
     if (net->profiling)
       for (size_t k = i + 1; k < i + step; k++) QPH_TRY_HIP(hipEventRecord(net->ev[k], s));
     i += step;
   }
+  return QPH_OK;
+}
+
+// Records the whole kernel sequence into a HIP graph (nothing executes).
+// Every launcher validates its arguments as it records, so a node that no
+// kernel takes fails here, at create time, naming the node.
+static int capture(qph_net* net) {
+  hipStream_t s = net->ctx->stream;
+  QPH_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = run_all(net);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(s, &g);
+  if (rc != QPH_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  QPH_TRY_HIP(e);
+  e = hipGraphInstantiate(&net->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_check(e, "hipGraphInstantiate");
+  }
+  net->graph = g;
+  net->graph_ready = true;
   return QPH_OK;
 }
 
@@ -553,6 +590,10 @@ static void release(qph_net* net) {
     (void)hipGraphDestroy(net->graph);
   }
   for (auto e : net->ev) (void)hipEventDestroy(e);
+  if (net->done) (void)hipEventDestroy(net->done);
+  if (net->in_stage) (void)hipHostFree(net->in_stage);
+  for (float* p : net->out_stage)
+    if (p) (void)hipHostFree(p);
   for (float* p : net->weights) (void)hipFree(p);
   for (float* p : net->wk)
     if (p) (void)hipFree(p);
@@ -566,12 +607,24 @@ extern "C" {
 
 QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
                            const float* const* weights_host, qph_net** out) {
-  if (!ctx || !spec || !out) return fail(QPH_EINVAL, "net_create: NULL argument");
+  if (!spec || !out) return fail(QPH_EINVAL, "net_create: NULL argument");
   *out = nullptr;
+  // the spec is checked before anything touches the device
   if (spec->n_tensors <= 0 || spec->n_nodes <= 0 || !spec->shapes || !spec->nodes)
     return fail(QPH_EINVAL, "net_create: empty graph");
   if (spec->n_weights > 0 && (!weights_host || !spec->weight_sizes))
     return fail(QPH_EINVAL, "net_create: missing weights");
+  if (spec->n_outputs < 0 || (spec->n_outputs > 0 && !spec->outputs))
+    return fail(QPH_EINVAL, "net_create: missing output list");
+  for (int32_t o = 0; o < spec->n_outputs; o++)
+    if (spec->outputs[o] < 0 || spec->outputs[o] >= spec->n_tensors)
+      return fail(QPH_EINVAL, "net_create: output " + std::to_string(o) + " names tensor " +
+                                  std::to_string(spec->outputs[o]) + " of " +
+                                  std::to_string(spec->n_tensors));
+  for (int32_t wi = 0; wi < spec->n_weights; wi++)
+    if (spec->weight_sizes[wi] < 0 || (spec->weight_sizes[wi] > 0 && !weights_host[wi]))
+      return fail(QPH_EINVAL, "net_create: weight " + std::to_string(wi) + " missing");
+  if (!ctx) return fail(QPH_EINVAL, "net_create: NULL context");
   qph_net* net = new qph_net();
   net->ctx = ctx;
   net->arena = nullptr;
@@ -579,12 +632,16 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
   net->graph_ready = false;
   net->profiling = false;
   net->prof_runs = 0;
+  net->in_stage = nullptr;
+  net->done = nullptr;
+  net->inflight = false;
   net->nodes.assign(spec->nodes, spec->nodes + spec->n_nodes);
   net->shapes.assign(spec->shapes, spec->shapes + 4 * (size_t)spec->n_tensors);
   net->alias.assign((size_t)spec->n_tensors, -1);
   if (spec->alias) net->alias.assign(spec->alias, spec->alias + spec->n_tensors);
   if (spec->n_outputs > 0 && spec->outputs)
     net->outputs.assign(spec->outputs, spec->outputs + spec->n_outputs);
+  net->out_stage.assign(net->outputs.size(), nullptr);
   net->tptr.assign((size_t)spec->n_tensors, nullptr);
   net->wk.assign(net->nodes.size(), nullptr);
   net->wt.assign(net->nodes.size(), nullptr);
@@ -644,18 +701,19 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     rc = validate_node(net, i, spec->weight_sizes, spec->n_weights);
     if (rc) return bail(rc);
     const qph_node& n = net->nodes[i];
-    const bool dense = n.op == QPH_OP_CONV &&
-                       !(n.cp.group == 1 && n.ws[2] == 1 && n.ws[3] == 1 && n.cp.sh == 1 &&
-                         n.cp.sw == 1) &&
-                       !(n.cp.group > 1 && n.ws[1] == 1);
+    // dense and grouped convs keep k-major repacked weights (the depthwise
+    // kernel reads the ONNX layout as it is)
+    const bool dense = n.op == QPH_OP_CONV && !conv_is_pointwise(n.ws, n.cp) &&
+                       !(n.cp.group > 1 && n.ws[1] == 1 && n.ws[0] == n.cp.group);
     if (dense) {
       float* d = nullptr;
-      rc = hip_check(hipMalloc((void**)&d, (size_t)dense_conv_wk_floats(n.ws[0], n.ws[1], n.ws[2], n.ws[3]) * 4),
-                     "hipMalloc(repacked weight)");
+      const size_t bytes =
+          (size_t)dense_conv_wk_floats(n.ws[0], n.ws[1], n.ws[2], n.ws[3], n.cp.group) * 4;
+      rc = hip_check(hipMalloc((void**)&d, bytes), "hipMalloc(repacked weight)");
       if (rc) return bail(rc);
       net->wk[i] = d;
       rc = launch_repack_conv_w_taps(net->weights[n.w], n.ws[0], n.ws[1], n.ws[2] * n.ws[3], d,
-                                     ctx->stream);
+                                     ctx->stream, n.cp.group);
       if (rc) return bail(rc);
     }
     if (n.op == QPH_OP_LINEAR) {
@@ -688,11 +746,24 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
       if (rc) return bail(rc);
     }
   }
-  plan_conv_groups(net);
-  plan_cl(net);
-  rc = plan_dwpw(net);
-  if (rc) return bail(rc);
+  const size_t nn = net->nodes.size();
+  if (spec->flags & QPH_NET_SEPARATE_LAUNCHES) {
+    net->plan.assign(nn, ConvArgs{});
+    net->group_len.assign(nn, 1);
+    net->cl_dw.assign(nn, false);
+    net->cl_pw.assign(nn, false);
+    net->cl_out.assign(nn, false);
+    net->dwpw.assign(nn, DwPwArgs{});
+    net->fused.assign(nn, false);
+  } else {
+    plan_conv_groups(net);
+    plan_cl(net);
+    rc = plan_dwpw(net);
+    if (rc) return bail(rc);
+  }
   rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (rc) return bail(rc);
+  rc = capture(net);
   if (rc) return bail(rc);
   *out = net;
   return QPH_OK;
@@ -730,9 +801,65 @@ QPH_API int qph_net_node_times(qph_net* net, double* ms, int32_t n) {
   return QPH_OK;
 }
 
+QPH_API int qph_net_staging(qph_net* net, int32_t slot, float** host, int64_t* numel) {
+  if (!net || !host) return fail(QPH_EINVAL, "net_staging: NULL argument");
+  if (slot < -1 || slot >= (int32_t)net->outputs.size())
+    return fail(QPH_EINVAL, "net_staging: slot " + std::to_string(slot) + " of " +
+                                std::to_string(net->outputs.size()) + " outputs");
+  const int32_t id = slot < 0 ? 0 : net->outputs[(size_t)slot];
+  float*& buf = slot < 0 ? net->in_stage : net->out_stage[(size_t)slot];
+  if (!buf) {
+    QPH_TRY_HIP(hipSetDevice(net->ctx->device));
+    void* p = nullptr;
+    QPH_TRY_HIP(hipHostMalloc(&p, (size_t)numel_of(net, id) * 4, hipHostMallocDefault));
+    buf = (float*)p;
+  }
+  *host = buf;
+  if (numel) *numel = numel_of(net, id);
+  return QPH_OK;
+}
+
+QPH_API int qph_net_run_async(qph_net* net, int32_t flags) {
+  if (!net) return fail(QPH_EINVAL, "net_run_async: NULL net");
+  if (net->inflight)
+    return fail(QPH_EINVAL, "net_run_async: the previous run of this net is not complete");
+  if (net->profiling) return fail(QPH_EINVAL, "net_run_async: profiling is on");
+  hipStream_t s = net->ctx->stream;
+  if ((flags & QPH_RUN_UPLOAD) && !net->in_stage)
+    return fail(QPH_EINVAL, "net_run_async: no input staging buffer (qph_net_staging -1)");
+  if (flags & QPH_RUN_DOWNLOAD)
+    for (size_t o = 0; o < net->outputs.size(); o++)
+      if (!net->out_stage[o])
+        return fail(QPH_EINVAL, "net_run_async: output " + std::to_string(o) +
+                                    " has no staging buffer");
+  if (!net->done) QPH_TRY_HIP(hipEventCreateWithFlags(&net->done, hipEventDisableTiming));
+  if (flags & QPH_RUN_UPLOAD)
+    QPH_TRY_HIP(hipMemcpyAsync(net->tptr[0], net->in_stage, (size_t)numel_of(net, 0) * 4,
+                               hipMemcpyHostToDevice, s));
+  if (!net->graph_ready) QPH_TRY(capture(net));
+  QPH_TRY_HIP(hipGraphLaunch(net->exec, s));
+  if (flags & QPH_RUN_DOWNLOAD)
+    for (size_t o = 0; o < net->outputs.size(); o++) {
+      const int32_t id = net->outputs[o];
+      QPH_TRY_HIP(hipMemcpyAsync(net->out_stage[o], net->tptr[id], (size_t)numel_of(net, id) * 4,
+                                 hipMemcpyDeviceToHost, s));
+    }
+  QPH_TRY_HIP(hipEventRecord(net->done, s));
+  net->inflight = true;
+  return QPH_OK;
+}
+
+QPH_API int qph_net_complete(qph_net* net) {
+  if (!net) return fail(QPH_EINVAL, "net_complete: NULL net");
+  if (!net->inflight) return QPH_OK;
+  net->inflight = false;
+  return hip_check(hipEventSynchronize(net->done), "hipEventSynchronize");
+}
+
 QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_device,
                         float* const* outputs_host) {
   if (!net) return fail(QPH_EINVAL, "net_run: NULL net");
+  if (net->inflight) QPH_TRY(qph_net_complete(net));
   hipStream_t s = net->ctx->stream;
   if (input) {
     size_t bytes = (size_t)numel_of(net, 0) * 4;
@@ -750,24 +877,7 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
     }
     net->prof_runs++;
   } else {
-    if (!net->graph_ready) {
-      QPH_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      int rc = run_all(net);
-      hipGraph_t g = nullptr;
-      hipError_t e = hipStreamEndCapture(s, &g);
-      if (rc != QPH_OK) {
-        if (g) (void)hipGraphDestroy(g);
-        return rc;
-      }
-      QPH_TRY_HIP(e);
-      e = hipGraphInstantiate(&net->exec, g, nullptr, nullptr, 0);
-      if (e != hipSuccess) {
-        (void)hipGraphDestroy(g);
-        return hip_check(e, "hipGraphInstantiate");
-      }
-      net->graph = g;
-      net->graph_ready = true;
-    }
+    if (!net->graph_ready) QPH_TRY(capture(net));
     QPH_TRY_HIP(hipGraphLaunch(net->exec, s));
   }
   if (outputs_host) {

@@ -22,9 +22,38 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 //   mu = (float)(sum_f64(x) / C); d = x - mu; sq = d*d (Pow 2);
 //   var = (float)(sum_f64(sq) / C); sd = sqrt(var + eps);
 //   y = ((d / sd) * gamma) + beta.
-// One wave per row; the f64 sums are exact for rows whose values span less
-// than 2^45 in magnitude ratio, which makes them independent of the order.
-// The row (cols <= 64*V) stays in registers across the three passes.
+// The reference sums each row sequentially in ascending order
+// (shape.rs:551-557).  One wave per row; the row (cols <= 64*V) stays in
+// registers across the three passes.  Each mean is taken from a shuffle-tree
+// f64 sum when that provably gives the sequential sum's f32 mean, else from
+// the sequential sum itself (lane 0 walks the row): see f64_mean_order_free.
+// Denormal terms count as zero (the CPU path converts with DAZ set,
+// par.rs:229-256).
+
+__device__ __forceinline__ double f64_daz(float v) {
+  return ((__float_as_uint(v) >> 23) & 0xff) == 0 ? 0.0 : (double)v;
+}
+
+// s, a: this lane's f64 partial sum of the row's terms and of their
+// magnitudes.  Any summation order of n terms is within
+// gamma_(n-1) * sum|x_i| of the exact sum (gamma_k = k u / (1 - k u),
+// u = 2^-53), so the tree sum and the sequential sum are within twice that
+// of each other.  Division by n and the conversion to f32 are monotone, so
+// when (tree - D) / n and (tree + D) / n round to the same f32 (bit for
+// bit), with D twice that bound (the extra covers the rounding of tree +- D),
+// the sequential sum rounds to it as well.  Wave-uniform result; false for
+// Inf / NaN and for rows whose mean sits that close to an f32 rounding
+// boundary (or rounds to a signed zero), which then take the sequential sum.
+__device__ __forceinline__ bool f64_mean_order_free(double s, double a, int64_t n, float* mean) {
+  s = wave_sum_f64(s);
+  a = wave_sum_f64(a);
+  const double k = (double)(n - 1) * 0x1p-53;
+  const double d = 4.0 * (k / (1.0 - k)) * a * (1.0 + 0x1p-30);
+  const float lo = (float)((s - d) / (double)n), hi = (float)((s + d) / (double)n);
+  *mean = lo;
+  return __float_as_uint(lo) == __float_as_uint(hi) && __builtin_isfinite(lo);
+}
+
 template <int V>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x,
                                                         const float* __restrict__ gamma,
@@ -45,22 +74,39 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     gv[u] = in ? gamma[j] : 0.0f;
     bv[u] = in ? beta[j] : 0.0f;
   }
-  double s = 0.0;
-#pragma unroll
-  for (int u = 0; u < V; u++)
-    if (lane + 64 * u < cols) s += (double)xv[u];
-  s = wave_sum_f64(s);
-  const float mu = (float)(s / (double)cols);
-  double s2 = 0.0;
+  double s = 0.0, sa = 0.0;
 #pragma unroll
   for (int u = 0; u < V; u++)
     if (lane + 64 * u < cols) {
-      float d = xv[u] - mu;
-      float sq = d * d;
-      s2 += (double)sq;
+      const double t = f64_daz(xv[u]);
+      s += t;
+      sa += __builtin_fabs(t);
     }
-  s2 = wave_sum_f64(s2);
-  const float var = (float)(s2 / (double)cols);
+  float mu;
+  if (!f64_mean_order_free(s, sa, cols, &mu)) {
+    s = 0.0;
+    if (lane == 0)
+      for (int64_t j = 0; j < cols; j++) s += f64_daz(xr[j]);
+    mu = (float)(__shfl(s, 0, 64) / (double)cols);
+  }
+  float sq[V];
+  double s2 = 0.0;
+#pragma unroll
+  for (int u = 0; u < V; u++) {
+    const float d = xv[u] - mu;
+    sq[u] = d * d;
+    if (lane + 64 * u < cols) s2 += f64_daz(sq[u]);
+  }
+  float var;
+  if (!f64_mean_order_free(s2, s2, cols, &var)) {   // squares: |x| = x
+    s2 = 0.0;
+    if (lane == 0)
+      for (int64_t j = 0; j < cols; j++) {
+        const float d = xr[j] - mu;
+        s2 += f64_daz(d * d);
+      }
+    var = (float)(__shfl(s2, 0, 64) / (double)cols);
+  }
   const float sd = __builtin_sqrtf(var + eps);
 #pragma unroll
   for (int u = 0; u < V; u++) {
@@ -111,7 +157,10 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
   return r;
 }
 
-// probs may alias logits (in-place softmax).  pairs may be NULL.
+// probs may alias logits (in-place softmax) or be NULL (pairs only: the
+// exponentials are then recomputed from the logits where the probabilities
+// would have been read back; exp1 is deterministic, so the values are the
+// same).  pairs may be NULL.
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, int64_t cols,
                                                            int64_t ld, float* probs, float* pairs) {
   __shared__ float buf[2][SM_CHUNK];
@@ -158,7 +207,7 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, 
         if (j < n) {
           float e = exp1(v[u] - mx);
           bb[j] = e;
-          pr[base + j] = e;
+          if (probs) pr[base + j] = e;
         }
       }
     }
@@ -200,7 +249,8 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, 
     } else {
       sum = 0.0f;
     }
-    for (int64_t i = full; i < cols; i++) sum = sum + pr[i];   // tail, in order
+    for (int64_t i = full; i < cols; i++)   // tail, in order
+      sum = sum + (probs ? pr[i] : exp1(xr[i] - mx));
     part[8] = sum;
   }
   __syncthreads();
@@ -214,14 +264,14 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, 
 #pragma unroll
     for (int u = 0; u < 8; u++) {
       int64_t i = i0 + 256 * u;
-      v[u] = i < cols ? pr[i] : 0.0f;
+      v[u] = i < cols ? (probs ? pr[i] : exp1(xr[i] - mx)) : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < 8; u++) {
       int64_t i = i0 + 256 * u;
       if (i < cols) {
         float p = v[u] * inv;
-        pr[i] = p;
+        if (probs) pr[i] = p;
         if (p > bv) {  // ascending i per thread: keeps the first strict max
           bv = p;
           bi = (int)i;
@@ -385,7 +435,7 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
     if (u < nu) {
       const int i = tid + 512 * u;
       const float p = e[u] * inv;
-      pr[i] = p;
+      if (probs) pr[i] = p;
       if (p > bv) {  // ascending i per thread: keeps the first strict max
         bv = p;
         bi = i;
@@ -512,7 +562,7 @@ __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, i
     if (u < nu) {
       const int i = tid + 512 * u;
       const float p = e[u] * inv;
-      pr[i] = p;
+      if (probs) pr[i] = p;
       if (p > bv) {  // ascending i per thread: keeps the first strict max
         bv = p;
         bi = i;
@@ -572,7 +622,7 @@ int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s) {
 
 int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
                           float* probs, float* pairs, hipStream_t s) {
-  if (!probs) return fail(QPH_EINVAL, "softmax_argmax: probs buffer required");
+  if (!probs && !pairs) return fail(QPH_EINVAL, "softmax_argmax: no output");
   return launch_softmax(logits, rows, cols, ld, probs, pairs, s);
 }
 
@@ -1031,10 +1081,23 @@ __global__ __launch_bounds__(256) void reduce_mean_kernel(const float* __restric
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  double s = 0.0;
-  for (int64_t j = lane; j < cols; j += 64) s += (double)x[row * cols + j];
-  s = wave_sum_f64(s);
-  if (lane == 0) out[row] = (float)(s / (double)cols);
+  const float* xr = x + row * cols;
+  double s = 0.0, sa = 0.0;
+  for (int64_t j = lane; j < cols; j += 64) {
+    const double t = f64_daz(xr[j]);
+    s += t;
+    sa += __builtin_fabs(t);
+  }
+  float mean;
+  // the reference's ascending sequential sum (shape.rs:551-557) wherever a
+  // tree sum could round to another f32 mean (f64_mean_order_free)
+  if (!f64_mean_order_free(s, sa, cols, &mean)) {
+    s = 0.0;
+    if (lane == 0)
+      for (int64_t j = 0; j < cols; j++) s += f64_daz(xr[j]);
+    mean = (float)(s / (double)cols);
+  }
+  if (lane == 0) out[row] = mean;
 }
 
 }  // namespace qph

@@ -5,8 +5,10 @@
 #include <cstring>
 #include <string>
 
+#include <map>
 #include <mutex>
 #include <set>
+#include <tuple>
 #include <utility>
 
 #include "qph_internal.h"
@@ -204,6 +206,46 @@ int allow_full_lds(const void* fn) {
   return QPH_OK;
 }
 
+int device_cus(int* dev_out, int* cus) {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  QPH_TRY_HIP(hipGetDevice(&dev));
+  if (dev_out) *dev_out = dev;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) {
+    *cus = it->second;
+    return QPH_OK;
+  }
+  int v = 0;
+  QPH_TRY_HIP(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+  if (v <= 0) return fail(QPH_EHIP, "device reports no compute units");
+  cache[dev] = v;
+  *cus = v;
+  return QPH_OK;
+}
+
+int kernel_occupancy(const void* fn, int block, int* occ) {
+  static std::mutex mu;
+  static std::map<std::tuple<const void*, int, int>, int> cache;
+  int dev = 0;
+  QPH_TRY_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(fn, block, dev);
+  auto it = cache.find(key);
+  if (it != cache.end()) {
+    *occ = it->second;
+    return QPH_OK;
+  }
+  int v = 0;
+  QPH_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, fn, block, 0));
+  if (v <= 0) return fail(QPH_EHIP, "kernel does not fit a compute unit");
+  cache[key] = v;
+  *occ = v;
+  return QPH_OK;
+}
+
 // Validates a conv node and launches its kernel.  wk: resident k-major
 // repacked weights of a dense conv (NULL: repacked into the context scratch).
 int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
@@ -219,7 +261,10 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
   const int64_t m = ws[0], cg = ws[1], kh = ws[2], kw = ws[3];
   const int64_t g = p->group;
   const int64_t oh = ys[2], ow = ys[3];
-  const bool pointwise = g == 1 && kh == 1 && kw == 1 && p->sh == 1 && p->sw == 1;
+  // the reference's 1x1 branch (conv.rs:264) reads X as a dense [C][oh*ow]
+  // matrix, which holds only without padding; a padded 1x1 conv is an
+  // ordinary conv and takes the implicit-GEMM branch here
+  const bool pointwise = conv_is_pointwise(ws, *p);
   const bool depthwise = g > 1 && cg == 1;
   const float* res = ep ? ep->residual : nullptr;
   int res_up = ep ? ep->res_up : 0;
@@ -275,11 +320,9 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
   ca.oh = oh; ca.ow = ow; ca.group = g;
   ca.act = a; ca.res = res; ca.y = y;
   ca.y_ctotal = y_ctotal; ca.y_coff = y_coff; ca.y_up = y_up;
-  if (depthwise) {
-    if (m != c) return fail(QPH_EUNSUPPORTED, "depthwise with channel multiplier != 1");
-    return launch_depthwise(ca, ctx->stream);
-  }
-  if (g != 1) return fail(QPH_EUNSUPPORTED, "grouped (non-depthwise) conv not implemented");
+  // depthwise (conv.rs:461-505) with one output per channel; a channel
+  // multiplier (M = k C) is a grouped conv with C/g = 1 and goes the general way
+  if (depthwise && m == c) return launch_depthwise(ca, ctx->stream);
   if (res && !plain_out) return fail(QPH_EUNSUPPORTED, "conv2d: residual with placed output");
   if (wk_resident) {
     ca.wk = wk_resident;
@@ -290,7 +333,7 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
     return launch_dense_conv(ca, ctx->stream, nullptr);
   }
   // standalone call: k-major repacked weights go to the context scratch
-  int64_t nwk = dense_conv_wk_floats(m, cg, kh, kw);
+  int64_t nwk = dense_conv_wk_floats(m, cg, kh, kw, g);
   void* wk = nullptr;
   QPH_TRY(ctx_workspace(ctx, (size_t)nwk * 4, &wk));
   return launch_dense_conv(ca, ctx->stream, (float*)wk);
@@ -419,7 +462,7 @@ QPH_API int qph_softmax_argmax(qph_ctx* ctx, const float* logits, int64_t rows, 
   CTX_CHECK(ctx);
   if (rows <= 0 || cols <= 0 || !logits || !pairs)
     return fail(QPH_EINVAL, "softmax_argmax: bad argument");
-  if (cols > 32768) return fail(QPH_EUNSUPPORTED, "softmax_argmax: cols > 32768");
+  if (cols >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax_argmax: cols >= 2^31");
   return launch_softmax_argmax(logits, rows, cols, cols, probs, pairs, ctx->stream);
 }
 

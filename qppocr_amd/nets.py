@@ -33,7 +33,8 @@ import math
 import numpy as np
 
 from . import _lib
-from ._lib import (ACT_GELU, ACT_HARDSWISH, ACT_NONE, ACT_RELU, Act, ConvParams, Node, NetSpec,
+from ._lib import (ACT_GELU, ACT_HARDSWISH, ACT_NONE, ACT_RELU, NET_SEPARATE_LAUNCHES, Act,
+                   ConvParams, Node, NetSpec,
                    OP_ACT, OP_ATTENTION, OP_CONV, OP_CONVT, OP_CONVT_PAIR_SIG, OP_LAYERNORM,
                    OP_LINEAR, OP_SOFTMAX_ARGMAX, check)
 
@@ -62,6 +63,7 @@ class Graph:
         self.nodes = []      # dicts (also read by the CPU oracle's executor)
         self.weights = []    # numpy float32 arrays
         self.outputs = []
+        self.flags = 0       # QPH_NET_* session flags
         self.tensor(input_shape)
 
     # -------------------------------------------------------------- tensors
@@ -137,9 +139,12 @@ class Graph:
                                heads=heads, dh=dh, eps=0.0, scale=scale))
         return out
 
-    def softmax_argmax(self, logits, cols):
+    def softmax_argmax(self, logits, cols, probs=True):
+        """Softmax over rows of `cols` then per-row argmax pairs; probs=False
+        exports the pairs only (rec_argmax_pairs, device.rs:160-165) and
+        returns (-1, pairs)."""
         s = self.shapes[logits]
-        probs = self.tensor(self.lshapes[logits])
+        probs = self.tensor(self.lshapes[logits]) if probs else -1
         rows = self.numel(logits) // cols
         pairs = self.tensor((s[0], rows // s[0], 2))
         self.nodes.append(dict(op=OP_SOFTMAX_ARGMAX, inp=logits, in2=-1, out=probs, out2=pairs,
@@ -169,7 +174,7 @@ class Graph:
         wsizes = (ctypes.c_int64 * max(1, len(self.weights)))(*[w.size for w in self.weights])
         outs = (ctypes.c_int32 * max(1, len(self.outputs)))(*self.outputs)
         spec = NetSpec(nt, shapes, alias, len(self.nodes), nodes, len(self.weights), wsizes,
-                       len(self.outputs), outs)
+                       len(self.outputs), outs, self.flags)
         keep = (shapes, alias, nodes, wsizes, outs)
         return spec, keep
 
@@ -287,8 +292,10 @@ def rec_weights(r):
     return ws
 
 
-def build_rec_graph(weights, batch, w, h=48):
-    """Rec graph for a [batch, 3, h, w] input over the weights of rec_weights()."""
+def build_rec_graph(weights, batch, w, h=48, probs=True):
+    """Rec graph for a [batch, 3, h, w] input over the weights of rec_weights().
+    probs=False: the head exports the (val, idx) pairs only, the GPU
+    sessions' CTC exit (rec_argmax_pairs, device.rs:160-165)."""
     it = iter(weights)
     g = Graph((batch, 3, h, w))
     nw = lambda: g.weight(next(it))  # noqa: E731
@@ -316,14 +323,14 @@ def build_rec_graph(weights, batch, w, h=48):
         x = g.linear(mm, w2, b2m, residual=x)
     wh, bh = nw(), nw()
     logits = g.linear(x, wh, bh)
-    probs, pairs = g.softmax_argmax(logits, REC_CLASSES)
-    g.outputs = [probs, pairs]
+    pr, pairs = g.softmax_argmax(logits, REC_CLASSES, probs)
+    g.outputs = [pr, pairs] if probs else [pairs]
     return g
 
 
-def build_rec(seed=3, batch=32, w=320, h=48):
+def build_rec(seed=3, batch=32, w=320, h=48, probs=True):
     x_in, r = rec_input(seed, batch, h, w)
-    g = build_rec_graph(rec_weights(r), batch, w, h)
+    g = build_rec_graph(rec_weights(r), batch, w, h, probs)
     return g, x_in
 
 
@@ -372,7 +379,8 @@ def node_cost(g, d):
     if op == OP_SOFTMAX_ARGMAX:
         cols = d["ws"][0]
         rows = g.numel(d["inp"]) // cols
-        return 0, (2 * rows * cols + 2 * rows) * f32, "hbm"
+        probs = rows * cols if d["out"] >= 0 else 0
+        return 0, (rows * cols + probs + 2 * rows) * f32, "hbm"
     if op == OP_LAYERNORM:
         cols = d["ws"][0]
         return 0, (2 * g.numel(d["inp"]) + 2 * cols) * f32, "hbm"
@@ -424,6 +432,26 @@ class HipSession:
             optr = (ctypes.c_void_p * len(outs))(*[o.ctypes.data_as(ctypes.c_void_p).value for o in outs])
         check(self.lib.qph_net_run(self.net, inp, is_dev, optr))
         return outs
+
+    def staging(self, slot):
+        """Pinned host buffer of the input (slot -1) or of output `slot`, as a
+        numpy view (owned by the session; valid until close)."""
+        p = ctypes.c_void_p()
+        n = ctypes.c_int64()
+        check(self.lib.qph_net_staging(self.net, slot, ctypes.byref(p), ctypes.byref(n)))
+        shape = self.graph.lshapes[0 if slot < 0 else self.graph.outputs[slot]]
+        buf = (ctypes.c_float * n.value).from_address(p.value)
+        return np.frombuffer(buf, dtype=np.float32).reshape(shape)
+
+    def run_async(self, upload=True, download=True):
+        """run_deferred (device.rs:172): enqueue input upload (from the input
+        staging buffer), the graph and the output downloads (into the output
+        staging buffers); complete() waits."""
+        flags = (_lib.RUN_UPLOAD if upload else 0) | (_lib.RUN_DOWNLOAD if download else 0)
+        check(self.lib.qph_net_run_async(self.net, flags))
+
+    def complete(self):
+        check(self.lib.qph_net_complete(self.net))
 
     def tensor_ptr(self, tid):
         p = ctypes.c_void_p()

@@ -197,15 +197,18 @@ def softmax_last_dim(t, inner):
     return t
 
 
-def softmax_argmax(logits):
+def softmax_argmax(logits, probs=True):
+    """Row softmax + argmax pairs; probs=False exports the pairs only (the
+    rec_argmax_pairs exit, qppocr-core/src/device.rs:160-165) and returns
+    (None, pairs)."""
     cols = logits.shape[-1]
     rows = logits.numel() // cols
-    probs = torch.empty_like(logits)
+    pr = torch.empty_like(logits) if probs else None
     pairs = torch.empty(tuple(logits.shape[:-1]) + (2,), device=logits.device)
     with _Call(_dev(logits)) as ctx:
-        check(_lib.load().qph_softmax_argmax(ctx, _ptr(logits), rows, cols, _ptr(probs),
-                                             _ptr(pairs)))
-    return probs, pairs
+        check(_lib.load().qph_softmax_argmax(ctx, _ptr(logits), rows, cols,
+                                             _ptr(pr) if probs else None, _ptr(pairs)))
+    return pr, pairs
 
 
 def ctc_argmax(probs, t_valid=None):

@@ -81,7 +81,7 @@ class PageRunner:
         self.plan = bucket_plan(self.widths)
         self.rec = []
         for k, (bw, idx) in enumerate(self.plan):
-            g = build_rec_graph(rec_w, len(idx), bw, REC_H)
+            g = build_rec_graph(rec_w, len(idx), bw, REC_H, probs=False)
             sess = HipSession(g, device, ctx=rec_ctxs[k % len(rec_ctxs)])
             self.rec.append((bw, idx, g, sess, pack_lines(lines, idx, bw)))
         self.lib = _lib.load()

@@ -96,3 +96,36 @@ def test_ops_refuse_host_tensors(lib):
 def test_version(lib):
     assert b"gfx950" in lib.qph_version()
 
+
+
+def _spec_with_outputs(outputs):
+    """A two-tensor ACT graph spec (no weights) with the given output ids."""
+    from qppocr_amd import nets
+    g = nets.Graph((1, 4, 2, 2))
+    t = g.tensor((1, 4, 2, 2))
+    g.nodes.append(dict(op=nets.OP_ACT, inp=0, in2=-1, out=t, out2=-1, w=-1, bias=-1, w2=-1,
+                        ws=(0, 0, 0, 0), w2s=(0, 0, 0, 0), cp=(1,) * 9, act=2, res_up=0,
+                        trans_out=0, y_ctotal=0, y_coff=0, y_up=1, heads=0, dh=0, eps=0.0,
+                        scale=0.0))
+    g.outputs = list(outputs)
+    return g.to_c()
+
+
+def test_net_create_checks_the_spec_before_the_device(lib):
+    """Output ids outside the tensor table are refused before any device
+    work (a bad id would otherwise index host tables out of range)."""
+    for bad in ([2], [-1], [0, 7]):
+        spec, keep = _spec_with_outputs(bad)
+        out = ctypes.c_void_p()
+        rc = lib.qph_net_create(None, ctypes.byref(spec), None, ctypes.byref(out))
+        assert rc == -1 and b"output" in lib.qph_last_error(), bad
+        assert out.value is None
+    spec, keep = _spec_with_outputs([1])
+    spec.n_outputs = 1
+    spec.outputs = None
+    assert lib.qph_net_create(None, ctypes.byref(spec), None, ctypes.byref(ctypes.c_void_p())) == -1
+    assert b"output list" in lib.qph_last_error()
+    # a valid spec gets as far as the context check
+    spec, keep = _spec_with_outputs([1])
+    assert lib.qph_net_create(None, ctypes.byref(spec), None, ctypes.byref(ctypes.c_void_p())) == -1
+    assert b"NULL context" in lib.qph_last_error()

@@ -81,6 +81,41 @@ def test_cfg4_rec_net(gpu, oracle):
     sess.close()
 
 
+def test_rec_pairs_only_and_deferred_runs(gpu, oracle):
+    """The rec graph with the pairs-only head (rec_argmax_pairs,
+    device.rs:160-165) gives the same pairs as the full graph and the
+    oracle; deferred runs (run_deferred / complete, device.rs:105-110,
+    166-176) through the pinned staging buffers give the same bits, and a
+    second deferred run before complete is refused."""
+    from qppocr_amd import nets
+    from qppocr_amd._lib import QphError
+    from oracle import nets as onets
+    g, x = nets.build_rec(3, 8, 240, probs=False)
+    assert len(g.outputs) == 1
+    print("rec 8x3x48x240 pairs only", flush=True)
+    sess = nets.HipSession(g)
+    (pairs,) = sess.run(x)
+    (pairs_ref,) = onets.run_graph(g, x)
+    assert (_ids(pairs) == _ids(pairs_ref)).all()
+    assert_bitexact(pairs[..., 0], pairs_ref[..., 0], "pairs-only values")
+    xin = sess.staging(-1)
+    out = sess.staging(0)
+    out[:] = np.nan
+    xin[:] = x
+    sess.run_async()
+    with pytest.raises(QphError):
+        sess.run_async()
+    sess.complete()
+    assert_bitexact(out, pairs, "deferred run pairs")
+    x2 = np.ascontiguousarray(x[::-1])
+    xin[:] = x2
+    sess.run_async()
+    sess.complete()
+    (pairs2_ref,) = onets.run_graph(g, x2)
+    assert (_ids(out) == _ids(pairs2_ref)).all()
+    sess.close()
+
+
 def test_cfg5_mixed_page(gpu, oracle):
     """det 1536^2 + 128 rec lines in width buckets, CTC masked past w/8:
     det map and every batch's pairs bit-exact with the oracle, and each
@@ -99,7 +134,7 @@ def test_cfg5_mixed_page(gpu, oracle):
     decoded = page.decode()
     for bw, idx, g, _, x in page.rec:
         print(f"cfg5 rec batch {len(idx)}x{bw}", flush=True)
-        _, pairs_ref = onets.run_graph(g, x)
+        pairs_ref = onets.run_graph(g, x)[-1]
         for b, i in enumerate(idx):
             assert (_ids(got[i]) == _ids(pairs_ref[b])).all(), f"line {i}"
             assert_bitexact(got[i][..., 0], pairs_ref[b][..., 0], f"line {i} values")

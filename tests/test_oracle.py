@@ -208,6 +208,72 @@ def test_conv_accumulation_order(oracle):
     assert (y.ravel() == big).all()
 
 
+def _im2col_seed_pattern(oh, ow, tile):
+    """Columns the reference's im2col branch seeds with the bias in an M%4
+    tail row: tiles of `tile` output rows, N = rows * ow per tile GEMM, the
+    panel rule over the tile's flattened columns (gemm.rs:7-16)."""
+    pat = np.zeros((oh, ow), bool)
+    for oy0 in range(0, oh, tile):
+        rows = min(tile, oh - oy0)
+        n = rows * ow
+        for j in range(n):
+            if n - (j // 32) * 32 < 32:
+                pat[oy0 + j // ow, j % ow] = True
+    return pat
+
+
+@pytest.mark.parametrize("shape", [(31, 31, 1, 2), (301, 301, 7, 16)],
+                         ids=["one tile", "tiles of 6 rows"])
+def test_conv_im2col_bias_placement(oracle, shape):
+    """x-stride 3 runs the im2col branch (conv.rs:639-661): one sgemm per
+    tile of rows with N = rows * ow, so the M%4-tail seeding follows the
+    tile's flattened columns, not each output row.  Chain 1, then 2^24,
+    bias 1: seeded gives 2^24 + 2, added after gives 2^24 -- the pattern of
+    2^24 + 2 in the tail row (row 4 of 5) shows where the bias went."""
+    h, w, k, cg = shape
+    big = np.float32(2.0 ** 24)
+    x = np.ones((1, cg, h, w), np.float32)
+    x[0, 1] = big
+    wt = np.zeros((5, cg, k, k), np.float32)
+    wt[:, 0, 0, 0] = 1            # k index 0
+    wt[:, 1, 0, 0] = 1            # k index k*k (channel 1, tap 0): after it
+    y = oracle.conv2d(x, wt, np.ones(5, np.float32), oracle.conv_params(3, 3, 0, 0))
+    oh, ow = y.shape[2:]
+    kk = cg * k * k
+    tile = min(oh, max(1, (1 << 19) // (kk * ow)))
+    if k == 7:
+        assert tile == 6 and oh == 99       # several tiles, last one partial
+    pat = _im2col_seed_pattern(oh, ow, tile)
+    assert (y[0, :4] == big).all()
+    assert (y[0, 4][pat] == big + 2).all() and (y[0, 4][~pat] == big).all()
+    # the per-row rule of the implicit-GEMM branch would differ here
+    per_row = np.ones((oh, ow), bool) if ow < 32 else None
+    if per_row is not None:
+        assert (pat != per_row).any()
+
+
+def test_conv_general_forms_vs_f64(oracle):
+    """Convs outside the reference test list that the dispatcher must still
+    run as convolutions: x-stride 3 (im2col branch), a padded 1x1 conv, a
+    depthwise conv with channel multiplier 2 (general branch), a 7x7 and a
+    2x3 dense kernel, and groups with several channels each."""
+    rng = XorShift(int(GOLD["rng"]["kernels_seed"], 16))
+    cases = [  # n, c, m, h, w, kh, kw, sh, sw, ph, pw, group
+        (1, 8, 12, 31, 29, 3, 3, 3, 3, 1, 1, 1),
+        (2, 6, 10, 20, 22, 5, 5, 1, 3, 2, 2, 2),
+        (1, 8, 13, 12, 14, 1, 1, 1, 1, 1, 2, 1),
+        (1, 8, 16, 17, 19, 3, 3, 1, 1, 1, 1, 8),
+        (1, 5, 7, 23, 21, 7, 7, 2, 2, 3, 3, 1),
+        (1, 6, 9, 15, 18, 2, 3, 1, 2, 0, 1, 3),
+    ]
+    for n, c, m, h, w, kh, kw, sh, sw, ph, pw, g in cases:
+        x = rng.fill((n, c, h, w))
+        wt = rng.fill((m, c // g, kh, kw))
+        b = rng.fill((m,))
+        y = oracle.conv2d(x, wt, b, oracle.conv_params(sh, sw, ph, pw, group=g))
+        rel_check(y, ref_conv_f64(x, wt, b, sh, sw, ph, pw, g))
+
+
 # -------------------------------------------------------------------- sgemm
 
 def test_sgemm_shapes_vs_f64(oracle):
@@ -271,6 +337,26 @@ def test_reduce_mean_exact(oracle):
     want = np.array([np.float32(x.reshape(6, 20)[i].astype(np.float64).sum() / 20.0)
                      for i in range(6)])
     assert (got == want).all()
+
+
+def test_reduce_mean_sequential_order(oracle):
+    """shape.rs:551-557 sums each row in ascending order in f64.  Row
+    [2^60, -2^60, 1 x 254]: in that order the ones survive (sum 254); a
+    pairwise or lane-strided order adds them to +-2^60 first, where they are
+    lost (|2^60| has an f64 ulp of 256)."""
+    row = np.ones(256, np.float32)
+    row[0], row[1] = 2.0 ** 60, -(2.0 ** 60)
+    x = np.stack([row, row[::-1].copy()])
+    got = oracle.reduce_mean_last(x)
+    for i in range(2):
+        s = 0.0
+        for v in x[i]:
+            s += float(v)
+        assert got[i] == np.float32(s / 256)
+    assert got[0] == np.float32(254 / 256)
+    # the strided (64-lane) order would give something else entirely
+    lanes = [sum(float(v) for v in row[l::64]) for l in range(64)]
+    assert np.float32(sum(lanes) / 256) != got[0]
 
 
 def test_layernorm_vs_f64_and_pow_square(oracle):
@@ -381,3 +467,51 @@ def test_rec_graph_invariants(oracle):
     ids = oracle.pairs_ids(pairs)
     assert (ids == probs.argmax(-1)).all()
     assert (pairs[..., 0] == probs.max(-1)).all()
+
+
+def test_gemm_tiles_match_scalar_form(oracle):
+    """The oracle's AVX2 6 x 16 GEMM tiles against its scalar form, bit for
+    bit (the reference's own AVX2-vs-scalar discipline, bitexact.rs):
+    sgemm on both bias paths with ragged edges, matmul, and convs on the
+    implicit-GEMM and im2col branches."""
+    rng = np.random.default_rng(31)
+
+    def both(fn):
+        oracle.set_scalar(False)
+        a = fn()
+        oracle.set_scalar(True)
+        try:
+            b = fn()
+        finally:
+            oracle.set_scalar(False)
+        return a, b
+
+    for m, n, k, serial in [(37, 150, 70, False), (64, 16, 4000, False), (13, 333, 9, True),
+                            (6, 16, 5, False), (100, 40, 256, True)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        bias = rng.standard_normal(m).astype(np.float32)
+        x, y = both(lambda: oracle.sgemm(a, b, m, n, k, bias, act=oracle.ACT_RELU, serial=serial))
+        assert (x == y).all(), (m, n, k)
+    a = rng.standard_normal((3, 50, 70)).astype(np.float32)
+    b = rng.standard_normal((70, 130)).astype(np.float32)
+    x, y = both(lambda: oracle.matmul(a, b))
+    assert (x == y).all()
+    b3 = rng.standard_normal((3, 70, 45)).astype(np.float32)
+    x, y = both(lambda: oracle.matmul(a, b3))
+    assert (x == y).all()
+    t = (rng.standard_normal((9, 1003)) * 30).astype(np.float32)
+    x, y = both(lambda: oracle.softmax_last_dim(t.copy(), 1003))
+    assert (x == y).all()
+    v = np.concatenate([(rng.standard_normal(8 * 4096) * 40).astype(np.float32),
+                        np.array([88.5, -88.5, 100, -100, 0, -0.0, 1e-30, 87.9], np.float32)])
+    got = np.concatenate([oracle.exp1x8(v[i:i + 8]) for i in range(0, v.size, 8)])
+    want = np.array([oracle.exp1(float(e)) for e in v], np.float32)
+    assert (got == want).all()
+    for (c, m, k, s, g) in [(16, 22, 3, 1, 1), (12, 18, 5, 2, 3), (8, 13, 3, 3, 1)]:
+        xin = rng.standard_normal((2, c, 29, 37)).astype(np.float32)
+        w = rng.standard_normal((m, c // g, k, k)).astype(np.float32)
+        bias = rng.standard_normal(m).astype(np.float32)
+        p = oracle.conv_params(s, s, k // 2, k // 2, group=g)
+        x, y = both(lambda: oracle.conv2d(xin, w, bias, p, oracle.ACT_RELU))
+        assert (x == y).all(), (c, m, k, s, g)
