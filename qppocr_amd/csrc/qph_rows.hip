@@ -34,19 +34,49 @@ __device__ __forceinline__ double f64_daz(float v) {
   return ((__float_as_uint(v) >> 23) & 0xff) == 0 ? 0.0 : (double)v;
 }
 
+// s + the f64 values of v over lanes 0..n-1 in lane order (every lane gets
+// the same sum): the terms come through v_readlane as wave-uniform values,
+// so the chain of adds runs without memory round trips.
+__device__ __forceinline__ double seq_sum_lanes(double s, float v, int n) {
+  n = __builtin_amdgcn_readfirstlane(n);
+  for (int l = 0; l < n; l++)
+    s += f64_daz(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)));
+  return s;
+}
+
+// Biased f32 exponent of a term as an exactness witness: nonzero finite
+// terms give their exponent, zeros (and DAZ-flushed denormals) 255.
+__device__ __forceinline__ int term_exp(float v) {
+  const int e = (int)((__float_as_uint(v) >> 23) & 0xff);
+  return e == 0 ? 255 : e;
+}
+
 // s, a: this lane's f64 partial sum of the row's terms and of their
-// magnitudes.  Any summation order of n terms is within
-// gamma_(n-1) * sum|x_i| of the exact sum (gamma_k = k u / (1 - k u),
-// u = 2^-53), so the tree sum and the sequential sum are within twice that
-// of each other.  Division by n and the conversion to f32 are monotone, so
-// when (tree - D) / n and (tree + D) / n round to the same f32 (bit for
-// bit), with D twice that bound (the extra covers the rounding of tree +- D),
-// the sequential sum rounds to it as well.  Wave-uniform result; false for
-// Inf / NaN and for rows whose mean sits that close to an f32 rounding
-// boundary (or rounds to a signed zero), which then take the sequential sum.
-__device__ __forceinline__ bool f64_mean_order_free(double s, double a, int64_t n, float* mean) {
+// magnitudes; emin: the smallest term_exp of its terms.  True (wave-uniform)
+// with *mean = (float)(sum / n) when the shuffle-tree sum gives the same f32
+// mean as the reference's sequential sum:
+//  - exact: every term is a multiple of 2^L, L = e_min - 127 - 23, and every
+//    partial sum of any order is at most sum|x_i| in magnitude; when that is
+//    below 2^(L + 53) every partial sum is exact in f64, so every order gives
+//    the exact sum;
+//  - else bounded: any order of n terms is within gamma_(n-1) * sum|x_i| of
+//    the exact sum (gamma_k = k u / (1 - k u), u = 2^-53), so the two sums
+//    are within twice that; division by n and the conversion to f32 are
+//    monotone, so when (tree - D) / n and (tree + D) / n round to the same
+//    f32 bits, with D twice that bound (the extra covers the rounding of
+//    tree +- D), the sequential sum rounds to it as well.
+// False for Inf / NaN and for the rare rows that meet neither test, which
+// then take the sequential sum.
+__device__ __forceinline__ bool f64_mean_order_free(double s, double a, int emin, int64_t n,
+                                                    float* mean) {
   s = wave_sum_f64(s);
   a = wave_sum_f64(a);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) emin = min(emin, __shfl_xor(emin, off, 64));
+  if (emin == 255 || a * (1.0 + 0x1p-40) < __builtin_ldexp(1.0, emin - 127 - 23 + 53)) {
+    *mean = (float)(s / (double)n);
+    return __builtin_isfinite(*mean);
+  }
   const double k = (double)(n - 1) * 0x1p-53;
   const double d = 4.0 * (k / (1.0 - k)) * a * (1.0 + 0x1p-30);
   const float lo = (float)((s - d) / (double)n), hi = (float)((s + d) / (double)n);
@@ -75,37 +105,41 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     bv[u] = in ? beta[j] : 0.0f;
   }
   double s = 0.0, sa = 0.0;
+  int emin = 255;
 #pragma unroll
   for (int u = 0; u < V; u++)
     if (lane + 64 * u < cols) {
       const double t = f64_daz(xv[u]);
       s += t;
       sa += __builtin_fabs(t);
+      emin = min(emin, term_exp(xv[u]));
     }
   float mu;
-  if (!f64_mean_order_free(s, sa, cols, &mu)) {
+  if (!f64_mean_order_free(s, sa, emin, cols, &mu)) {
+    // the reference's order: element 64 u + l sits in lane l, slot u
     s = 0.0;
-    if (lane == 0)
-      for (int64_t j = 0; j < cols; j++) s += f64_daz(xr[j]);
-    mu = (float)(__shfl(s, 0, 64) / (double)cols);
+    for (int u = 0; u < V; u++)
+      s = seq_sum_lanes(s, xv[u], (int)min<int64_t>(64, cols - 64 * u));
+    mu = (float)(s / (double)cols);
   }
   float sq[V];
   double s2 = 0.0;
+  int emin2 = 255;
 #pragma unroll
   for (int u = 0; u < V; u++) {
     const float d = xv[u] - mu;
     sq[u] = d * d;
-    if (lane + 64 * u < cols) s2 += f64_daz(sq[u]);
+    if (lane + 64 * u < cols) {
+      s2 += f64_daz(sq[u]);
+      emin2 = min(emin2, term_exp(sq[u]));
+    }
   }
   float var;
-  if (!f64_mean_order_free(s2, s2, cols, &var)) {   // squares: |x| = x
+  if (!f64_mean_order_free(s2, s2, emin2, cols, &var)) {   // squares: |x| = x
     s2 = 0.0;
-    if (lane == 0)
-      for (int64_t j = 0; j < cols; j++) {
-        const float d = xr[j] - mu;
-        s2 += f64_daz(d * d);
-      }
-    var = (float)(__shfl(s2, 0, 64) / (double)cols);
+    for (int u = 0; u < V; u++)
+      s2 = seq_sum_lanes(s2, sq[u], (int)min<int64_t>(64, cols - 64 * u));
+    var = (float)(s2 / (double)cols);
   }
   const float sd = __builtin_sqrtf(var + eps);
 #pragma unroll
@@ -1083,18 +1117,23 @@ __global__ __launch_bounds__(256) void reduce_mean_kernel(const float* __restric
   if (row >= rows) return;
   const float* xr = x + row * cols;
   double s = 0.0, sa = 0.0;
+  int emin = 255;
   for (int64_t j = lane; j < cols; j += 64) {
-    const double t = f64_daz(xr[j]);
+    const float v = xr[j];
+    const double t = f64_daz(v);
     s += t;
     sa += __builtin_fabs(t);
+    emin = min(emin, term_exp(v));
   }
   float mean;
   // the reference's ascending sequential sum (shape.rs:551-557) wherever a
   // tree sum could round to another f32 mean (f64_mean_order_free)
-  if (!f64_mean_order_free(s, sa, cols, &mean)) {
+  if (!f64_mean_order_free(s, sa, emin, cols, &mean)) {
     s = 0.0;
-    if (lane == 0)
-      for (int64_t j = 0; j < cols; j++) s += f64_daz(xr[j]);
+    for (int64_t j0 = 0; j0 < cols; j0 += 64) {
+      const float v = j0 + lane < cols ? xr[j0 + lane] : 0.0f;
+      s = seq_sum_lanes(s, v, (int)min<int64_t>(64, cols - j0));
+    }
     mean = (float)(s / (double)cols);
   }
   if (lane == 0) out[row] = mean;
