@@ -97,6 +97,23 @@ QPH_API int qph_conv2d(qph_ctx* ctx, const float* x, const int64_t xs[4], const 
                        const int64_t ws[4], const float* bias, const qph_conv_params* p,
                        const qph_act* act, const float* residual, float* y, int64_t ys_out[4]);
 
+/* Allocation-free qph_conv2d (same arguments, same results).  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  qph_conv2d repacks a dense conv's weights into the context's
+ * scratch, which it grows with hipMalloc; this form repacks them into a fixed
+ * device array of QPH_NOALLOC_WK_FLOATS floats (4 MiB per GPU, held until
+ * the process ends) and refuses (QPH_EUNSUPPORTED) a conv whose repacked
+ * weights need more: group * ceil(C/g/4)*4*kh*kw * ceil(M/g/32)*32 floats.
+ * Every call on one GPU uses that GPU's one array: calls that overlap on a
+ * GPU (from several streams or threads) race; calls on one stream are
+ * ordered.  1x1 and depthwise convs use no scratch either way. */
+#define QPH_NOALLOC_WK_FLOATS 1048576
+QPH_API int qph_conv2d_noalloc(qph_ctx* ctx, const float* x, const int64_t xs[4],
+                               const float* w, const int64_t ws[4], const float* bias,
+                               const qph_conv_params* p, const qph_act* act,
+                               const float* residual, float* y, int64_t ys_out[4]);
+
 /* Epilogue placement for the fused det neck (no reference counterpart as one
  * call; it is the reference's Conv -> Resize(nearest) -> Add / Concat node
  * sequence, qppocr-core/src/executor.rs:433-652, 885-951, 1889-1916, with

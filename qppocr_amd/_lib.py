@@ -15,6 +15,7 @@ OP_CONV, OP_CONVT_PAIR_SIG, OP_LINEAR, OP_LAYERNORM, OP_ATTENTION = 1, 2, 3, 4, 
 OP_SOFTMAX_ARGMAX, OP_CONVT, OP_ACT = 6, 7, 8
 RUN_UPLOAD, RUN_DOWNLOAD = 1, 2
 NET_SEPARATE_LAUNCHES = 1
+NOALLOC_WK_FLOATS = 1 << 20
 
 I64 = ctypes.c_int64
 I32 = ctypes.c_int32
@@ -69,6 +70,8 @@ SIGNATURES = {
     "qph_conv2d_out_shape": ([P, P, ctypes.POINTER(ConvParams), P], ctypes.c_int),
     "qph_conv2d": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act), P, P, P],
                    ctypes.c_int),
+    "qph_conv2d_noalloc": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act), P,
+                            P, P], ctypes.c_int),
     "qph_conv2d_ex": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act),
                        ctypes.POINTER(ConvEpilogue), P], ctypes.c_int),
     "qph_convtranspose2d": ([P, P, P, P, P, I64, I64, I64, I64, P, P], ctypes.c_int),

@@ -51,6 +51,7 @@ struct qph_ctx {
   bool own_stream;
   void* ws;         // scratch for standalone operator calls (repacked weights, masks)
   size_t ws_bytes;
+  float* noalloc_wk;  // device address of this device's fixed repack array (qph_conv2d_noalloc)
 };
 
 namespace qph {
@@ -224,10 +225,13 @@ struct ConvArgs {
 };
 // plan != NULL: a dense conv with resident weights is not launched; its
 // arguments are returned in *plan (other conv kinds fail with EUNSUPPORTED).
+// fixed_wk (fixed_floats long), when not NULL, takes the repacked weights of
+// a standalone dense conv instead of the context scratch (nothing allocated).
 int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
                   const float* wk_resident, const int64_t ws[4], const float* bias,
                   const qph_conv_params* p, const qph_act* act, const qph_conv_epilogue* ep,
-                  float* y, ConvArgs* plan = nullptr);
+                  float* y, ConvArgs* plan = nullptr, float* fixed_wk = nullptr,
+                  int64_t fixed_floats = 0);
 int launch_dense_conv(const ConvArgs& a, hipStream_t s, float* scratch_wk);
 // Depthwise conv (+ bias + act) feeding a 1x1 conv (+ bias + act) in one
 // kernel; wk = the 1x1 weights repacked k-major [ceil(C/4)*4][ceil(M/32)*32].

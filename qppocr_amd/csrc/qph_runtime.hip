@@ -57,6 +57,30 @@ int ctx_workspace(qph_ctx* ctx, size_t bytes, void** out) {
   return QPH_OK;
 }
 
+// The allocation-free conv entry point's device array: room for the k-major
+// repacked weights of one dense conv, one copy per GPU for the life of the
+// process.  Host code never uses this name as an address (on the host it is
+// only a stand-in): the device address comes from hipGetSymbolAddress,
+// looked up once per device with that device current, at context creation.
+static __device__ __align__(256) float scratch[QPH_NOALLOC_WK_FLOATS];
+
+static int scratch_address(int device, float** out) {
+  static std::mutex mu;
+  static std::map<int, float*> addr;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = addr.find(device);
+  if (it != addr.end()) {
+    *out = it->second;
+    return QPH_OK;
+  }
+  void* p = nullptr;
+  QPH_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  if (!p) return fail(QPH_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+  addr[device] = (float*)p;
+  *out = (float*)p;
+  return QPH_OK;
+}
+
 }  // namespace qph
 
 using namespace qph;
@@ -83,11 +107,14 @@ QPH_API int qph_ctx_create(int device, qph_ctx** out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(QPH_EUNSUPPORTED, std::string("qph_ctx_create: device is ") + prop.gcnArchName +
                                       ", this library is built for gfx950 only");
+  float* fixed_wk = nullptr;
+  QPH_TRY(scratch_address(device, &fixed_wk));   // device is current
   qph_ctx* c = new qph_ctx;
   c->device = device;
   c->own_stream = true;
   c->ws = nullptr;
   c->ws_bytes = 0;
+  c->noalloc_wk = fixed_wk;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;
@@ -251,7 +278,7 @@ int kernel_occupancy(const void* fn, int block, int* occ) {
 int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
                   const float* wk_resident, const int64_t ws[4], const float* bias,
                   const qph_conv_params* p, const qph_act* act, const qph_conv_epilogue* ep,
-                  float* y, ConvArgs* plan) {
+                  float* y, ConvArgs* plan, float* fixed_wk, int64_t fixed_floats) {
   CTX_CHECK(ctx);
   if (!x || !w || !y) return fail(QPH_EINVAL, "conv2d: NULL tensor");
   if (!act_valid(act)) return fail(QPH_EINVAL, "conv2d: bad activation kind");
@@ -332,8 +359,16 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
     }
     return launch_dense_conv(ca, ctx->stream, nullptr);
   }
-  // standalone call: k-major repacked weights go to the context scratch
+  // standalone call: k-major repacked weights go to the fixed array or the
+  // context scratch
   int64_t nwk = dense_conv_wk_floats(m, cg, kh, kw, g);
+  if (fixed_wk) {
+    if (nwk > fixed_floats)
+      return fail(QPH_EUNSUPPORTED,
+                  "conv2d_noalloc: the repacked weights need " + std::to_string(nwk) +
+                      " floats, the fixed device array holds " + std::to_string(fixed_floats));
+    return launch_dense_conv(ca, ctx->stream, fixed_wk);
+  }
   void* wk = nullptr;
   QPH_TRY(ctx_workspace(ctx, (size_t)nwk * 4, &wk));
   return launch_dense_conv(ca, ctx->stream, (float*)wk);
@@ -349,6 +384,18 @@ QPH_API int qph_conv2d(qph_ctx* ctx, const float* x, const int64_t xs[4], const 
   qph_conv_epilogue ep{};
   ep.residual = residual;
   return conv_dispatch(ctx, x, xs, w, nullptr, ws, bias, p, act, &ep, y);
+}
+
+QPH_API int qph_conv2d_noalloc(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
+                               const int64_t ws[4], const float* bias, const qph_conv_params* p,
+                               const qph_act* act, const float* residual, float* y,
+                               int64_t ys_out[4]) {
+  CTX_CHECK(ctx);
+  if (ys_out) QPH_TRY(qph_conv2d_out_shape(xs, ws, p, ys_out));
+  qph_conv_epilogue ep{};
+  ep.residual = residual;
+  return conv_dispatch(ctx, x, xs, w, nullptr, ws, bias, p, act, &ep, y, nullptr,
+                       ctx->noalloc_wk, QPH_NOALLOC_WK_FLOATS);
 }
 
 QPH_API int qph_conv2d_ex(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
