@@ -422,13 +422,26 @@ def main():
     h1 = time.perf_counter()
     host_ms_step = (h1 - h0) * 1e3 / K
 
-    # the rec graph exporting the probability tensor as well
+    # the rec graph exporting the probability tensor as well, and the rec
+    # graph with the fused head (GEMM + softmax argmax in one kernel)
     rec_p_g, _ = nets.build_rec(3, REC_BATCH, 320, probs=True)
     rec_p = nets.HipSession(rec_p_g, ctx=ctx_rec)
     rec_p.run(rec_x, outputs=False)
     rec_p.sync()
     rec_p_ms = stage_ms(rec_p, stream_rec)
     rec_p.close()
+    rec_f_g, _ = nets.build_rec(3, REC_BATCH, 320, fused_head=True)
+    rec_f = nets.HipSession(rec_f_g, ctx=ctx_rec)
+    rec_f.run(rec_x, outputs=False)
+    rec_f.sync()
+    rec_f_ms = stage_ms(rec_f, stream_rec)
+    rec_f.set_profiling(True)
+    for _ in range(K):
+        rec_f.run(None, outputs=False)
+    rec_f.sync()
+    fused_head_ms = rec_f.node_times()[len(rec_f_g.nodes) - 2]
+    rec_f.set_profiling(False)
+    rec_f.close()
 
     # dominant kernel: rec head GEMM, events around each node (eager launches)
     rec.set_profiling(True)
@@ -475,6 +488,8 @@ def main():
         "det_img_per_s": round(1e3 / det_ms, 2),
         "rec_lines_per_s": round(REC_BATCH * 1e3 / rec_ms, 1),
         "rec_lines_per_s_with_probs": round(REC_BATCH * 1e3 / rec_p_ms, 1),
+        "rec_lines_per_s_fused_head": round(REC_BATCH * 1e3 / rec_f_ms, 1),
+        "fused_head_ms": round(fused_head_ms, 5),
         "det_ms": round(det_ms, 4),
         "rec_ms": round(rec_ms, 4),
         "serial_ms_per_step": round(det_ms + rec_ms, 4),

@@ -80,6 +80,7 @@ typedef struct {
 #define QPH_ACT_RELU 2
 #define QPH_ACT_HARDSWISH 3
 #define QPH_ACT_SIGMOID 4
+#define QPH_ACT_HARDSIGMOID 5  /* HardSigmoid node alone (alpha = c1, beta = c2): the SE gate */
 typedef struct {
   int32_t kind;
   float c1, c2, c3;
@@ -183,6 +184,24 @@ QPH_API int qph_softmax_last_dim(qph_ctx* ctx, float* t, int64_t rows, int64_t i
 QPH_API int qph_softmax_argmax(qph_ctx* ctx, const float* logits, int64_t rows, int64_t cols,
                                float* probs, float* pairs);
 
+/* The rec head MatMul + Add(bias) + Softmax + CTC argmax in one GEMM whose
+ * epilogue keeps, per row and 64-column block, the logits' max, the first
+ * column holding it and the sum of exp1(v - max); a second kernel combines
+ * the blocks into pairs[2r] = 1 / sum (the max's probability) and
+ * pairs[2r+1] = index as u32 bits.  The logits never reach memory (the fused
+ * head of SURVEY's hot-path table; the reference's Metal n_head_argmax,
+ * qppocr-gpu/src/plan.rs:316-340, fuses only Softmax + argmax).  x [rows, k],
+ * w [k, n] (ONNX MatMul layout), bias [n] or NULL.  Not bit-identical to
+ * qph_linear + qph_softmax_argmax: the exponentials come from the hardware
+ * exp2 and the sum is taken per block and rescaled, so values agree to
+ * ~1e-6 relative (the target's bar is 1e-4); the index is
+ * the first maximum of the logits, which differs from the first maximum of
+ * the rounded probabilities only where two logits lie within a few ulps.
+ * Needs k % 16 == 0 and x 16-byte aligned with rows k floats apart. */
+QPH_API int qph_linear_softmax_argmax(qph_ctx* ctx, const float* x, const float* w,
+                                      const float* bias, int64_t rows, int64_t k, int64_t n,
+                                      float* pairs);
+
 /* CTC greedy argmax over probabilities (rec.rs:46-54): first strict max,
  * ties to the lowest index.  t_valid (may be NULL) masks steps t >= t_valid[b]
  * of batch item b (rows = batch * t_len) to (0, blank). */
@@ -214,6 +233,55 @@ QPH_API int qph_binary_inplace(qph_ctx* ctx, float* a, const float* b, int64_t r
 QPH_API int qph_reduce_mean_last(qph_ctx* ctx, const float* x, int64_t rows, int64_t cols,
                                  float* out);
 
+/* ------------------------------------ pooling, SE gate, resize, layout */
+
+/* global_avg_pool (qppocr-kernels/src/pool2d.rs:10-29): x [N, C, H, W] ->
+ * out [N, C] (f64 sum per plane in order, (sum / (H*W)) as f32). */
+QPH_API int qph_global_avg_pool(qph_ctx* ctx, const float* x, int64_t n, int64_t c,
+                                int64_t hw, float* out);
+/* mul_add_scale (elementwise.rs:134-179), the SE block's gated residual
+ * Add(Mul(feature, gate), residual) as fused by optimize.rs:429-497:
+ * out = feature * gate[channel] + residual, each op rounded; feature,
+ * residual and out [N, C, hw]. */
+QPH_API int qph_mul_add_scale(qph_ctx* ctx, const float* feature, const float* gate,
+                              const float* residual, int64_t n, int64_t c, int64_t hw,
+                              float* out);
+/* pool2d (pool2d.rs:51-236): max (max_pool = 1) or average (padding counted
+ * in the divisor) over kh x kw windows; pads ph/pw begin, peh/pew end.
+ * ys_out (may be NULL) receives [N, C, oh, ow], oh = (H + ph + peh - kh) /
+ * sh + 1. */
+QPH_API int qph_pool2d(qph_ctx* ctx, const float* x, const int64_t xs[4], int64_t kh,
+                       int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t peh,
+                       int64_t pew, int32_t max_pool, float* y, int64_t ys_out[4]);
+/* resize_bilinear (resize.rs:60-142) over the last two axes of [nc, h, w]. */
+QPH_API int qph_resize_bilinear(qph_ctx* ctx, const float* x, int64_t nc, int64_t h, int64_t w,
+                                int64_t oh, int64_t ow, int32_t align_corners, float* y);
+/* Rank-4 Transpose: y's dimension d is x's dimension perm[d]. */
+QPH_API int qph_transpose(qph_ctx* ctx, const float* x, const int64_t xs[4],
+                          const int32_t perm[4], float* y);
+
+/* ------------------------------------ steps either side of the networks */
+
+/* det input (qppocr-core/src/pipeline/engine.rs:959-982): u8 RGB
+ * [h, w, 3] -> f32 [1, 3, h, w], v = u8 * (1/255), (v - 0.5) * (1/0.5). */
+QPH_API int qph_det_normalize_u8(qph_ctx* ctx, const uint8_t* rgb, int64_t h, int64_t w,
+                                 float* out);
+/* resize_bilinear_rgb_u8 (resize.rs:153-209): u8 RGB [sh, sw, 3] ->
+ * [dh, dw, 3]. */
+QPH_API int qph_resize_bilinear_rgb_u8(qph_ctx* ctx, const uint8_t* src, int64_t sw, int64_t sh,
+                                       uint8_t* dst, int64_t dw, int64_t dh);
+/* pack_crop (qppocr-core/src/pipeline/crop.rs:153-190): a u8 RGB crop
+ * [ch, cw, 3] into one f32 [3, img_h, img_w] slot of a rec batch (resized
+ * to img_h x clamp(ceil(img_h * cw / ch), 1, img_w), or centred at its own
+ * size when pad_only), (u8 / 255 - 0.5) / 0.5; the rest of the slot is 0. */
+QPH_API int qph_pack_crop(qph_ctx* ctx, const uint8_t* crop, int64_t ch, int64_t cw,
+                          int64_t img_h, int64_t img_w, int32_t pad_only, float* dst);
+/* DB post front end (geometry.rs:287-301, resize.rs:219-247): mask =
+ * pred > thresh (u8 0/1), then (dilate != 0) the 2x2 dilation with anchor
+ * (1, 1), out-of-range samples ignored. */
+QPH_API int qph_db_mask(qph_ctx* ctx, const float* pred, int64_t h, int64_t w, float thresh,
+                        int32_t dilate, uint8_t* mask);
+
 /* ------------------------------------------------------------- session */
 
 /* A static det or rec graph (the optimised graph the DeviceContext receives,
@@ -227,6 +295,13 @@ QPH_API int qph_reduce_mean_last(qph_ctx* ctx, const float* x, int64_t rows, int
 #define QPH_OP_SOFTMAX_ARGMAX 6 /* logits -> probs (y, optional) and pairs (y2) */
 #define QPH_OP_CONVT 7         /* x -> y; w [Ci, Co, 2, 2] */
 #define QPH_OP_ACT 8           /* x -> y; act */
+#define QPH_OP_GAP 9           /* GlobalAveragePool: x [N,C,H,W] -> y [N,C,1,1] */
+#define QPH_OP_MUL_ADD_SCALE 10 /* y = in * in3 (gate [C] or [N,C]) + in2; y_ctotal/y_coff */
+#define QPH_OP_POOL 11         /* ws = {max?, 0, kh, kw}; cp strides and pads; y_ctotal/y_coff */
+#define QPH_OP_RESIZE 12       /* ws = {mode 0 nearest | 1 bilinear, align_corners, 0, 0};
+                                  output size from the tensor table; y_ctotal/y_coff (bilinear) */
+#define QPH_OP_TRANSPOSE 13    /* rank-4 permutation ws = {perm0..3} */
+#define QPH_OP_COPY_SLOT 14    /* x -> channels [y_coff, y_coff + C) of y (a Concat slot) */
 
 typedef struct {
   int32_t op;
@@ -244,6 +319,7 @@ typedef struct {
   int64_t y_ctotal, y_coff, y_up;
   int64_t heads, dh;
   float eps, scale;
+  int32_t in3;      /* third input tensor id (the MulAddScale gate), -1 if none */
 } qph_node;
 
 /* Tensor table: shape per tensor id (rank 4, unused trailing dims = 1).
@@ -266,6 +342,11 @@ typedef struct {
  * depthwise + 1x1 (+ stem) fusion, no channel-last rec blocks (per-op
  * measurement and debugging; the results are the same bits). */
 #define QPH_NET_SEPARATE_LAUNCHES 1
+/* A linear whose output only the pairs-only softmax argmax right after it
+ * reads (the rec head) runs as one GEMM with the softmax argmax in its
+ * epilogue; the logits are never stored (qph_linear_softmax_argmax).  Pairs
+ * within float rounding of the unfused path, not bit-identical. */
+#define QPH_NET_FUSED_HEAD 2
 
 typedef struct qph_net qph_net;
 

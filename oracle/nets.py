@@ -25,6 +25,22 @@ from . import oracle as O
 # op codes of include/qppocr_hip.h
 OP_CONV, OP_CONVT_PAIR_SIG, OP_LINEAR, OP_LAYERNORM, OP_ATTENTION = 1, 2, 3, 4, 5
 OP_SOFTMAX_ARGMAX, OP_CONVT, OP_ACT = 6, 7, 8
+OP_GAP, OP_MUL_ADD_SCALE, OP_POOL, OP_RESIZE, OP_TRANSPOSE, OP_COPY_SLOT = 9, 10, 11, 12, 13, 14
+ACT_HARDSIGMOID = 5
+
+
+def _store(T, g, d, y):
+    """Node output: the tensor itself, or its Concat slot [y_coff, y_coff + C)
+    (the reference's zero-copy Concat, executor.rs:1889-1916)."""
+    if d["y_ctotal"]:
+        out = T.get(d["out"])
+        if out is None:
+            out = np.zeros(g.shapes[d["out"]], dtype=np.float32)
+            T[d["out"]] = out
+        c0 = d["y_coff"]
+        out[:, c0:c0 + y.shape[1]] = y
+    else:
+        T[d["out"]] = y.reshape(g.shapes[d["out"]])
 
 
 def _act_nodes(y, act):
@@ -38,6 +54,8 @@ def _act_nodes(y, act):
         return O.gelu_inplace(y.copy())
     if act == O.ACT_SIGMOID:
         return O.sigmoid_tensor(y)
+    if act == ACT_HARDSIGMOID:
+        return O.hardsigmoid(y, O.HS_ALPHA, O.HS_BETA)
     return y
 
 
@@ -124,6 +142,36 @@ def run_graph(g, x_in, keep=False):
             T[d["out"]] = O.convtranspose2d(x.reshape(g.shapes[d["inp"]]), W[d["w"]].reshape(d["ws"]))
         elif op == OP_ACT:
             T[d["out"]] = _act_nodes(x.copy(), d["act"])
+        elif op == OP_GAP:
+            T[d["out"]] = O.global_avg_pool(x.reshape(g.shapes[d["inp"]]))
+        elif op == OP_MUL_ADD_SCALE:
+            n, c, h, w = g.shapes[d["inp"]]
+            gate = T[d["in3"]].reshape(-1)
+            f = x.reshape(n, c, h, w)
+            r = T[d["in2"]].reshape(n, c, h, w)
+            if gate.size == c:
+                y = O.mul_add_scale(f, gate, r)
+            else:                       # per-item gate: the Mul and Add nodes
+                y = O.binary_bcast(f.reshape(n * c, h * w), gate, n * c, h * w, 2, 0)
+                y = O.binary_flat(y, r.reshape(n * c, h * w), 0).reshape(n, c, h, w)
+            _store(T, g, d, y)
+        elif op == OP_POOL:
+            sh, sw, ph, pw, peh, pew = d["cp"][:6]
+            y = O.pool2d(x.reshape(g.shapes[d["inp"]]), d["ws"][2], d["ws"][3], sh, sw, ph, pw,
+                         peh, pew, bool(d["ws"][0]))
+            _store(T, g, d, y)
+        elif op == OP_RESIZE:
+            oh, ow = g.shapes[d["out"]][2:]
+            xi = x.reshape(g.shapes[d["inp"]])
+            if d["ws"][0]:
+                y = O.resize_bilinear(xi, oh, ow, bool(d["ws"][1]))
+            else:
+                y = O.resize_nearest(xi, oh, ow)
+            _store(T, g, d, y)
+        elif op == OP_TRANSPOSE:
+            T[d["out"]] = O.transpose4(x.reshape(g.shapes[d["inp"]]), d["ws"])
+        elif op == OP_COPY_SLOT:
+            _store(T, g, d, x.reshape(g.shapes[d["inp"]]).copy())
         else:
             raise ValueError(f"oracle executor: unknown op {op}")
     outs = [T[t].reshape(g.lshapes[t]) for t in g.outputs]

@@ -69,6 +69,16 @@ def lib():
             "qpo_layernorm_chain": ([P, P, P, F, I64, I64, P], None),
             "qpo_matmul": ([P, P, P, I64, I64, I64, I64, I, I], None),
             "qpo_ctc_argmax": ([P, I64, I64, P], None),
+            "qpo_global_avg_pool": ([P, I64, I64, P], None),
+            "qpo_mul_add_scale": ([P, P, P, P, I64, I64, I64], None),
+            "qpo_pool2d_out_hw": ([I64] * 10 + [P, P], None),
+            "qpo_pool2d": ([P] + [I64] * 12 + [I, P], None),
+            "qpo_resize_bilinear": ([P, I64, I64, I64, I64, I64, I, P], None),
+            "qpo_transpose4": ([P, P, P, P], None),
+            "qpo_det_normalize": ([P, I64, I64, P], None),
+            "qpo_resize_bilinear_rgb_u8": ([P, I64, I64, P, I64, I64], None),
+            "qpo_pack_crop": ([P, I64, I64, I64, I64, P, I], None),
+            "qpo_db_mask": ([P, I64, I64, F, I, P], None),
             "qpo_ctc_collapse": ([P, I64, P, P], I64),
         }
         for name, (args, res) in sig.items():
@@ -309,3 +319,91 @@ def ctc_collapse(pairs, t_len):
     conf = np.zeros(1, dtype=np.float32)
     cnt = lib().qpo_ctc_collapse(_p(pairs), t_len, _p(ids), _p(conf))
     return ids[:cnt].copy(), float(conf[0])
+
+
+# ------------------------------------------------------ pooling / SE / resize
+
+def global_avg_pool(x):
+    """[N, C, H, W] -> [N, C, 1, 1] (pool2d.rs:10-29, f64 sum in order)."""
+    x = _f32(x)
+    n, c = x.shape[:2]
+    out = np.empty((n, c, 1, 1), np.float32)
+    lib().qpo_global_avg_pool(_p(x), n * c, x.size // (n * c), _p(out))
+    return out
+
+
+def mul_add_scale(f, gate, r):
+    """f * gate[c] + r per channel plane (elementwise.rs:134-179)."""
+    f, gate, r = _f32(f), _f32(gate), _f32(r)
+    c = gate.size
+    hw = f.size // (f.shape[0] * f.shape[1])
+    out = np.empty_like(f)
+    lib().qpo_mul_add_scale(_p(f), _p(gate), _p(r), _p(out), c, hw, f.size)
+    return out
+
+
+def pool2d(x, kh, kw, sh, sw, ph, pw, peh, pew, max_pool):
+    """pool2d (pool2d.rs:51-236); returns [N, C, oh, ow]."""
+    x = _f32(x)
+    n, c, h, w = x.shape
+    oh, ow = ctypes.c_int64(), ctypes.c_int64()
+    lib().qpo_pool2d_out_hw(h, w, kh, kw, sh, sw, ph, pw, peh, pew, ctypes.byref(oh),
+                            ctypes.byref(ow))
+    y = np.empty((n, c, oh.value, ow.value), np.float32)
+    lib().qpo_pool2d(_p(x), n, c, h, w, kh, kw, sh, sw, ph, pw, peh, pew, int(max_pool), _p(y))
+    return y
+
+
+def resize_bilinear(x, oh, ow, align_corners=False):
+    """resize_bilinear (resize.rs:60-142) over the last two axes."""
+    x = _f32(x)
+    h, w = x.shape[-2:]
+    nc = x.size // (h * w)
+    y = np.empty(x.shape[:-2] + (oh, ow), np.float32)
+    lib().qpo_resize_bilinear(_p(x), nc, h, w, oh, ow, int(bool(align_corners)), _p(y))
+    return y
+
+
+def transpose4(x, perm):
+    x = _f32(x)
+    xs = _i64(x.shape)
+    pm = _i64(perm)
+    y = np.empty(tuple(x.shape[p] for p in perm), np.float32)
+    lib().qpo_transpose4(_p(x), _p(xs), _p(pm), _p(y))
+    return y
+
+
+def det_normalize(rgb):
+    """u8 [H, W, 3] -> f32 [1, 3, H, W] (engine.rs:959-982)."""
+    rgb = np.ascontiguousarray(rgb, np.uint8)
+    h, w = rgb.shape[:2]
+    out = np.empty((1, 3, h, w), np.float32)
+    lib().qpo_det_normalize(_p(rgb), h, w, _p(out))
+    return out
+
+
+def resize_bilinear_rgb_u8(src, dw, dh):
+    """u8 [sh, sw, 3] -> u8 [dh, dw, 3] (resize.rs:153-209)."""
+    src = np.ascontiguousarray(src, np.uint8)
+    sh, sw = src.shape[:2]
+    dst = np.empty((dh, dw, 3), np.uint8)
+    lib().qpo_resize_bilinear_rgb_u8(_p(src), sw, sh, _p(dst), dw, dh)
+    return dst
+
+
+def pack_crop(crop, img_h, img_w, pad_only=False):
+    """u8 crop [ch, cw, 3] -> f32 [3, img_h, img_w] slot (crop.rs:153-190)."""
+    crop = np.ascontiguousarray(crop, np.uint8)
+    ch, cw = crop.shape[:2]
+    dst = np.zeros((3, img_h, img_w), np.float32)
+    lib().qpo_pack_crop(_p(crop), ch, cw, img_h, img_w, _p(dst), int(bool(pad_only)))
+    return dst
+
+
+def db_mask(pred, thresh, dilate=True):
+    """DB threshold then 2x2 dilation (geometry.rs:287-301, resize.rs:219-247)."""
+    pred = _f32(pred)
+    h, w = pred.shape[-2:]
+    out = np.empty((h, w), np.uint8)
+    lib().qpo_db_mask(_p(pred), h, w, float(thresh), int(bool(dilate)), _p(out))
+    return out

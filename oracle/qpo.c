@@ -163,6 +163,7 @@ static inline float act1(float v, int kind, float c1, float c2, float c3, float 
     case 2: return relu1(v);
     case 3: return hswish1(v, c1, c2);
     case 4: return sigmoid1(v);
+    case 5: return hsig1(v, c1, c2);
     default: return v;
   }
 }
@@ -876,4 +877,285 @@ QPO_API int64_t qpo_ctc_collapse(const float* pairs, int64_t t_len, int32_t* ids
   }
   if (conf) *conf = cnt > 0 ? (float)(cs / (double)cnt) : 0.0f;
   return cnt;
+}
+
+/* ------------------------------------------- pooling, SE gate, bilinear */
+
+/* global_avg_pool: pool2d.rs:10-29 -- per (n, c) plane, f64 sum in
+ * ascending order, (sum / plane) as f32: reduce_mean over the plane. */
+QPO_API void qpo_global_avg_pool(const float* x, int64_t nc, int64_t plane, float* out) {
+  qpo_reduce_mean_last(x, nc, plane, out);
+}
+
+/* mul_add_scale: elementwise.rs:134-179 -- out = f * gate[plane % c] + r,
+ * the Mul and the Add each rounded (no fma). */
+QPO_API void qpo_mul_add_scale(const float* f, const float* gate, const float* r, float* out,
+                               int64_t c, int64_t hw, int64_t total) {
+  const int64_t planes = total / hw;
+#pragma omp parallel for schedule(static)
+  for (int64_t p = 0; p < planes; p++) {
+    const float g = gate[p % c];
+    for (int64_t i = 0; i < hw; i++) out[p * hw + i] = f[p * hw + i] * g + r[p * hw + i];
+  }
+}
+
+/* Rust's f32::max (IEEE maxNum: a NaN operand yields the other). */
+static inline float maxnum(float a, float b) { return fmaxf(a, b); }
+
+/* pool2d_out_hw: pool2d.rs:34-49. */
+QPO_API void qpo_pool2d_out_hw(int64_t h, int64_t w, int64_t kh, int64_t kw, int64_t sh,
+                               int64_t sw, int64_t ph, int64_t pw, int64_t peh, int64_t pew,
+                               int64_t* oh, int64_t* ow) {
+  const int64_t hh = h + ph + peh, ww = w + pw + pew;
+  *oh = (hh > kh ? hh - kh : 0) / sh + 1;
+  *ow = (ww > kw ? ww - kw : 0) / sw + 1;
+}
+
+/* pool2d_into: pool2d.rs:94-236.
+ *   2x2 s1 SAME_UPPER max (ph = pw = 0, peh = pew = 1, oh = h, ow = w):
+ *     vm[j] = max(r0[j], r1[j]) (r1 = next row, absent on the last row),
+ *     vm[w] = -f32::MAX, out[j] = max(vm[j], vm[j + 1])
+ *     (pool2x2_row_scalar, pool2d.rs:242-259);
+ *   otherwise per output: acc = -3.4e38 (max) or 0 (avg), taps ky outer, kx
+ *     inner, out-of-range taps skipped; max: v > acc ? v : acc; avg:
+ *     acc + v, then acc / (kh * kw) (the divisor counts padding). */
+QPO_API void qpo_pool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, int64_t kh,
+                        int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t peh,
+                        int64_t pew, int max_pool, float* y) {
+  int64_t oh, ow;
+  qpo_pool2d_out_hw(h, w, kh, kw, sh, sw, ph, pw, peh, pew, &oh, &ow);
+  const int special = max_pool && kh == 2 && kw == 2 && sh == 1 && sw == 1 && ph == 0 &&
+                      pw == 0 && peh == 1 && pew == 1 && oh == h && ow == w;
+#pragma omp parallel
+  {
+    float* vm = (float*)malloc(sizeof(float) * (size_t)(w + 1));
+#pragma omp for schedule(static)
+    for (int64_t p = 0; p < n * c; p++) {
+      const float* xp = x + p * h * w;
+      float* yp = y + p * oh * ow;
+      if (special) {
+        for (int64_t oy = 0; oy < oh; oy++) {
+          const float* r0 = xp + oy * w;
+          const float* r1 = oy + 1 < h ? r0 + w : NULL;
+          for (int64_t j = 0; j < w; j++) vm[j] = r1 ? maxnum(r0[j], r1[j]) : r0[j];
+          vm[w] = -3.40282347e38f;
+          for (int64_t j = 0; j < w; j++) yp[oy * ow + j] = maxnum(vm[j], vm[j + 1]);
+        }
+        continue;
+      }
+      for (int64_t oy = 0; oy < oh; oy++)
+        for (int64_t ox = 0; ox < ow; ox++) {
+          float acc = max_pool ? -3.4e38f : 0.0f;
+          for (int64_t ky = 0; ky < kh; ky++) {
+            const int64_t iy = oy * sh - ph + ky;
+            if (iy < 0 || iy >= h) continue;
+            for (int64_t kx = 0; kx < kw; kx++) {
+              const int64_t ix = ox * sw - pw + kx;
+              if (ix < 0 || ix >= w) continue;
+              const float v = xp[iy * w + ix];
+              acc = max_pool ? (v > acc ? v : acc) : acc + v;
+            }
+          }
+          yp[oy * ow + ox] = max_pool ? acc : acc / (float)(kh * kw);
+        }
+    }
+    free(vm);
+  }
+}
+
+/* resize_bilinear_into: resize.rs:60-142 with bilinear_row_scalar
+ * (resize.rs:252-273).  Source coordinate per output index i (f32):
+ * align_corners: i * (H - 1) / (oh - 1); else max(0, (i + 0.5) * H / oh - 0.5);
+ * base = clamp(floor(v), 0, H - 1), next = min(base + 1, H - 1),
+ * frac = v - base.  Value: t = r0[i0] * (1 - lx) * (1 - ly);
+ * t = fma(r0[i1] * lx, 1 - ly, t); t = fma(r1[i0] * (1 - lx), ly, t);
+ * out = fma(r1[i1] * lx, ly, t). */
+static void bilinear_map(int64_t n_out, int64_t n_in, int align, int64_t* i0, int64_t* i1,
+                         float* f) {
+  for (int64_t i = 0; i < n_out; i++) {
+    float v;
+    if (align && n_out > 1)
+      v = (float)i * (float)(n_in - 1) / (float)(n_out - 1);
+    else {
+      v = ((float)i + 0.5f) * (float)n_in / (float)n_out - 0.5f;
+      v = v > 0.0f ? v : 0.0f;
+    }
+    int64_t b = (int64_t)floorf(v);
+    if (b < 0) b = 0;
+    if (b > n_in - 1) b = n_in - 1;
+    i0[i] = b;
+    i1[i] = b + 1 < n_in - 1 ? b + 1 : n_in - 1;
+    f[i] = v - (float)b;
+  }
+}
+
+QPO_API void qpo_resize_bilinear(const float* x, int64_t nc, int64_t h, int64_t w, int64_t oh,
+                                 int64_t ow, int align, float* y) {
+  int64_t* iy0 = (int64_t*)malloc(sizeof(int64_t) * (size_t)oh);
+  int64_t* iy1 = (int64_t*)malloc(sizeof(int64_t) * (size_t)oh);
+  float* fy = (float*)malloc(sizeof(float) * (size_t)oh);
+  int64_t* ix0 = (int64_t*)malloc(sizeof(int64_t) * (size_t)ow);
+  int64_t* ix1 = (int64_t*)malloc(sizeof(int64_t) * (size_t)ow);
+  float* fx = (float*)malloc(sizeof(float) * (size_t)ow);
+  bilinear_map(oh, h, align, iy0, iy1, fy);
+  bilinear_map(ow, w, align, ix0, ix1, fx);
+#pragma omp parallel for schedule(static)
+  for (int64_t p = 0; p < nc; p++)
+    for (int64_t oy = 0; oy < oh; oy++) {
+      const float* r0 = x + (p * h + iy0[oy]) * w;
+      const float* r1 = x + (p * h + iy1[oy]) * w;
+      const float ly = fy[oy];
+      for (int64_t ox = 0; ox < ow; ox++) {
+        const float lx = fx[ox];
+        const int64_t a = ix0[ox], b = ix1[ox];
+        float t = r0[a] * (1.0f - lx) * (1.0f - ly);
+        t = fmaf(r0[b] * lx, 1.0f - ly, t);
+        t = fmaf(r1[a] * (1.0f - lx), ly, t);
+        y[(p * oh + oy) * ow + ox] = fmaf(r1[b] * lx, ly, t);
+      }
+    }
+  free(iy0); free(iy1); free(fy); free(ix0); free(ix1); free(fx);
+}
+
+/* Rank-4 transpose: y[i_perm] = x[i] with y's dim d = x's dim perm[d]. */
+QPO_API void qpo_transpose4(const float* x, const int64_t* xs, const int64_t* perm, float* y) {
+  int64_t ys[4], xst[4];
+  xst[3] = 1;
+  for (int d = 2; d >= 0; d--) xst[d] = xst[d + 1] * xs[d + 1];
+  for (int d = 0; d < 4; d++) ys[d] = xs[perm[d]];
+  const int64_t total = xs[0] * xs[1] * xs[2] * xs[3];
+#pragma omp parallel for schedule(static)
+  for (int64_t o = 0; o < total; o++) {
+    int64_t r = o, src = 0;
+    for (int d = 3; d >= 0; d--) {
+      const int64_t i = r % ys[d];
+      r /= ys[d];
+      src += i * xst[perm[d]];
+    }
+    y[o] = x[src];
+  }
+}
+
+/* -------------------------------------- steps either side of the path */
+
+/* det input: u8 RGB (h x w x 3, interleaved) -> NCHW f32,
+ * v = u8 * (1 / 255) then (v - 0.5) * (1 / 0.5) (engine.rs:959-982). */
+QPO_API void qpo_det_normalize(const uint8_t* rgb, int64_t h, int64_t w, float* out) {
+  const float scale = 1.0f / 255.0f, mean = 0.5f, istd = 1.0f / 0.5f;
+#pragma omp parallel for schedule(static)
+  for (int64_t y = 0; y < h; y++)
+    for (int64_t c = 0; c < 3; c++)
+      for (int64_t x = 0; x < w; x++) {
+        const float v = (float)rgb[(y * w + x) * 3 + c] * scale;
+        out[(c * h + y) * w + x] = (v - mean) * istd;
+      }
+}
+
+/* resize_bilinear_rgb_u8: resize.rs:153-209 (= pipeline/image.rs
+ * resize_bilinear_img for 3 channels): half-pixel map with (v as usize)
+ * truncation, the same two-multiply-then-fma weighting, then
+ * (val + 0.5).clamp(0, 255) as u8. */
+QPO_API void qpo_resize_bilinear_rgb_u8(const uint8_t* src, int64_t sw, int64_t sh, uint8_t* dst,
+                                        int64_t dw, int64_t dh) {
+  const float sx = (float)sw / (float)dw, sy = (float)sh / (float)dh;
+  int64_t* x0 = (int64_t*)malloc(sizeof(int64_t) * (size_t)dw);
+  int64_t* x1 = (int64_t*)malloc(sizeof(int64_t) * (size_t)dw);
+  float* fx = (float*)malloc(sizeof(float) * (size_t)dw);
+  for (int64_t x = 0; x < dw; x++) {
+    float v = ((float)x + 0.5f) * sx - 0.5f;
+    v = v > 0.0f ? v : 0.0f;
+    int64_t i0 = (int64_t)v;
+    if (i0 > sw - 1) i0 = sw - 1;
+    x0[x] = i0;
+    x1[x] = i0 + 1 < sw - 1 ? i0 + 1 : sw - 1;
+    fx[x] = v - (float)i0;
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t y = 0; y < dh; y++) {
+    float v = ((float)y + 0.5f) * sy - 0.5f;
+    v = v > 0.0f ? v : 0.0f;
+    int64_t j0 = (int64_t)v;
+    if (j0 > sh - 1) j0 = sh - 1;
+    const int64_t j1 = j0 + 1 < sh - 1 ? j0 + 1 : sh - 1;
+    const float fy = v - (float)j0;
+    const uint8_t* r0 = src + j0 * sw * 3;
+    const uint8_t* r1 = src + j1 * sw * 3;
+    for (int64_t x = 0; x < dw; x++) {
+      const int64_t a = x0[x] * 3, b = x1[x] * 3;
+      const float lx = fx[x];
+      for (int ch = 0; ch < 3; ch++) {
+        const float p00 = r0[a + ch], p01 = r0[b + ch], p10 = r1[a + ch], p11 = r1[b + ch];
+        float t = p00 * (1.0f - lx) * (1.0f - fy);
+        t = fmaf(p01 * lx, 1.0f - fy, t);
+        t = fmaf(p10 * (1.0f - lx), fy, t);
+        float val = fmaf(p11 * lx, fy, t);
+        val = val + 0.5f;
+        val = val < 0.0f ? 0.0f : (val > 255.0f ? 255.0f : val);
+        dst[(y * dw + x) * 3 + ch] = (uint8_t)val;
+      }
+    }
+  }
+  free(x0); free(x1); free(fx);
+}
+
+/* pack_crop: crop.rs:153-190 -- a text-line crop (u8 RGB, ch x cw) into one
+ * [3, img_h, img_w] slot of the zero-filled rec batch: pad_only: centred at
+ * original size (rows y0 = (img_h - ch) / 2 on, columns < min(cw, img_w));
+ * else resized (resize_bilinear_rgb_u8) to img_h x rw, rw =
+ * clamp(ceil(img_h * (cw / ch)), 1, img_w); value (u8 / 255 - 0.5) / 0.5
+ * (true divisions).  Positions not written stay 0. */
+QPO_API void qpo_pack_crop(const uint8_t* crop, int64_t ch, int64_t cw, int64_t img_h,
+                           int64_t img_w, float* dst, int pad_only) {
+  const int64_t plane = img_h * img_w;
+  if (pad_only) {
+    const int64_t y0 = (img_h - ch) / 2;
+    const int64_t cols = cw < img_w ? cw : img_w;
+    for (int64_t y = 0; y < ch; y++)
+      for (int64_t x = 0; x < cols; x++)
+        for (int c = 0; c < 3; c++) {
+          const float v = (float)crop[(y * cw + x) * 3 + c] / 255.0f;
+          dst[c * plane + (y + y0) * img_w + x] = (v - 0.5f) / 0.5f;
+        }
+    return;
+  }
+  const float ratio = (float)cw / (float)ch;
+  int64_t rw = (int64_t)ceilf((float)img_h * ratio);
+  if (rw > img_w) rw = img_w;
+  if (rw < 1) rw = 1;
+  uint8_t* r = (uint8_t*)malloc((size_t)(rw * img_h * 3));
+  qpo_resize_bilinear_rgb_u8(crop, cw, ch, r, rw, img_h);
+  for (int64_t y = 0; y < img_h; y++)
+    for (int64_t x = 0; x < rw; x++)
+      for (int c = 0; c < 3; c++) {
+        const float v = (float)r[(y * rw + x) * 3 + c] / 255.0f;
+        dst[(c * img_h + y) * img_w + x] = (v - 0.5f) / 0.5f;
+      }
+  free(r);
+}
+
+/* DB post front end (geometry.rs:287-301): mask = pred > thresh ? 1 : 0;
+ * with dilation, dilate2x2_max (resize.rs:219-247): out[y][x] = max over
+ * the in-range samples of rows y - 1 .. y and columns x - 1 .. x. */
+QPO_API void qpo_db_mask(const float* pred, int64_t h, int64_t w, float thresh, int dilate,
+                         uint8_t* out) {
+  uint8_t* m = (uint8_t*)malloc((size_t)(h * w));
+  for (int64_t i = 0; i < h * w; i++) m[i] = pred[i] > thresh ? 1 : 0;
+  if (!dilate) {
+    memcpy(out, m, (size_t)(h * w));
+    free(m);
+    return;
+  }
+  for (int64_t y = 0; y < h; y++)
+    for (int64_t x = 0; x < w; x++) {
+      uint8_t v = 0;
+      for (int64_t dy = -1; dy <= 0; dy++)
+        for (int64_t dx = -1; dx <= 0; dx++) {
+          const int64_t ny = y + dy, nx = x + dx;
+          if (ny < 0 || nx < 0) continue;
+          const uint8_t s = m[ny * w + nx];
+          v = s > v ? s : v;
+        }
+      out[y * w + x] = v;
+    }
+  free(m);
 }

@@ -13,8 +13,11 @@ QPH_OK = 0
 ACT_NONE, ACT_GELU, ACT_RELU, ACT_HARDSWISH, ACT_SIGMOID = 0, 1, 2, 3, 4
 OP_CONV, OP_CONVT_PAIR_SIG, OP_LINEAR, OP_LAYERNORM, OP_ATTENTION = 1, 2, 3, 4, 5
 OP_SOFTMAX_ARGMAX, OP_CONVT, OP_ACT = 6, 7, 8
+OP_GAP, OP_MUL_ADD_SCALE, OP_POOL, OP_RESIZE, OP_TRANSPOSE, OP_COPY_SLOT = 9, 10, 11, 12, 13, 14
+ACT_HARDSIGMOID = 5
 RUN_UPLOAD, RUN_DOWNLOAD = 1, 2
 NET_SEPARATE_LAUNCHES = 1
+NET_FUSED_HEAD = 2
 NOALLOC_WK_FLOATS = 1 << 20
 
 I64 = ctypes.c_int64
@@ -43,7 +46,7 @@ class Node(ctypes.Structure):
                 ("w", I32), ("bias", I32), ("w2", I32), ("ws", I64 * 4), ("w2s", I64 * 4),
                 ("cp", ConvParams), ("act", Act), ("res_up", I32), ("trans_out", I32),
                 ("y_ctotal", I64), ("y_coff", I64), ("y_up", I64), ("heads", I64),
-                ("dh", I64), ("eps", F32), ("scale", F32)]
+                ("dh", I64), ("eps", F32), ("scale", F32), ("in3", I32)]
 
 
 class NetSpec(ctypes.Structure):
@@ -70,6 +73,16 @@ SIGNATURES = {
     "qph_conv2d_out_shape": ([P, P, ctypes.POINTER(ConvParams), P], ctypes.c_int),
     "qph_conv2d": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act), P, P, P],
                    ctypes.c_int),
+    "qph_linear_softmax_argmax": ([P, P, P, P, I64, I64, I64, P], ctypes.c_int),
+    "qph_global_avg_pool": ([P, P, I64, I64, I64, P], ctypes.c_int),
+    "qph_mul_add_scale": ([P, P, P, P, I64, I64, I64, P], ctypes.c_int),
+    "qph_pool2d": ([P, P, P] + [I64] * 8 + [I32, P, P], ctypes.c_int),
+    "qph_resize_bilinear": ([P, P, I64, I64, I64, I64, I64, I32, P], ctypes.c_int),
+    "qph_transpose": ([P, P, P, P, P], ctypes.c_int),
+    "qph_det_normalize_u8": ([P, P, I64, I64, P], ctypes.c_int),
+    "qph_resize_bilinear_rgb_u8": ([P, P, I64, I64, P, I64, I64], ctypes.c_int),
+    "qph_pack_crop": ([P, P, I64, I64, I64, I64, I32, P], ctypes.c_int),
+    "qph_db_mask": ([P, P, I64, I64, F32, I32, P], ctypes.c_int),
     "qph_conv2d_noalloc": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act), P,
                             P, P], ctypes.c_int),
     "qph_conv2d_ex": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act),

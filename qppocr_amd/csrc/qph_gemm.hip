@@ -21,6 +21,7 @@ namespace qph {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u32_t __attribute__((ext_vector_type(4)));
 
 #define GEMM_BK 16
 
@@ -564,11 +565,19 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, float* dst,
 #define WV_AL (WV_A / 256)  // A-slab loads (16 bytes a lane)
 #define WV_BL (WV_B / 256)  // B-slab loads (16 bytes a lane: four 64-column rows each)
 
-// ROWS: the row-store epilogue (whole 64-row blocks, 16-byte aligned output
-// rows); otherwise each lane stores its own 64 values.
-template <bool ROWS>
+// Epilogue modes: WV_EPI_ELEM each lane stores its own 64 values;
+// WV_EPI_ROWS the row-store epilogue (whole 64-row blocks, 16-byte aligned
+// output rows); WV_EPI_ARGMAX no C at all: per row of the tile, the
+// (max, first index of the max, sum of exp1(v - max)) of its 64 columns goes
+// to g.part (one float4 per row and 64-column block), for head_pairs_kernel.
+#define WV_EPI_ELEM 0
+#define WV_EPI_ROWS 1
+#define WV_EPI_ARGMAX 2
+
+template <int EPI>
 __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int nb, int ntiles,
                                                        int per_xcd, int wg_xcd) {
+  constexpr bool ROWS = EPI == WV_EPI_ROWS;
   __shared__ __attribute__((aligned(16))) float lds[2 * WV_STAGE];
   const int lane = threadIdx.x;
   const int xcd = (int)(blockIdx.x % NUM_XCD), wl = (int)(blockIdx.x / NUM_XCD);
@@ -642,6 +651,8 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
       // kt - 1 are done too, so that stage takes slab kt + 1
       if (ROWS && kt == 0 && stored)
         wait_vmcnt<16>();
+      else if (EPI == WV_EPI_ARGMAX && kt == 0 && stored)
+        wait_vmcnt<2>();
       else
         wait_vmcnt<0>();
       __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -691,7 +702,70 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
       const int j = j0 + ni * 32 + lr;
       badd[ni] = g.bias_mode == 2 && j < N ? g.bias[j] : -0.0f;
     }
-    if constexpr (!ROWS) {
+    if constexpr (EPI == WV_EPI_ARGMAX) {
+      // each 32-row half through the stage of the last slab (pitch 72), then
+      // lane L takes row L % 32, columns 32 (L / 32) .. + 31 of the tile, in
+      // order: first strict max, then the exp1 sum against it; lanes L and
+      // L + 32 combine; exactly one 16-byte buffer store per half (rows past
+      // M and the upper lanes store out of range, which is dropped), so the
+      // next tile's first wait can count on two stores in flight
+      float* sc = lds + (st ^ 1) * WV_STAGE;
+      const int r = lane & 31, ch = lane >> 5;
+      const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)g.part, 0, (int)((int64_t)M * nb * 16), 0x00020000);
+      const int cb = j0 >> 6;
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+          for (int v = 0; v < 16; v++)
+            sc[(8 * (v >> 2) + 4 * lh + (v & 3)) * 72 + ni * 32 + lr] = acc[mi][ni][v] + badd[ni];
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        float vals[32];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const f32x4 t = *(const f32x4*)(sc + r * 72 + 32 * ch + 4 * q);
+          vals[4 * q] = t[0];
+          vals[4 * q + 1] = t[1];
+          vals[4 * q + 2] = t[2];
+          vals[4 * q + 3] = t[3];
+        }
+        const int jb = j0 + 32 * ch;
+        float m = -__builtin_inff();
+        int idx = 0x7fffffff;
+#pragma unroll
+        for (int q = 0; q < 32; q++)
+          if (jb + q < N && vals[q] > m) {
+            m = vals[q];
+            idx = jb + q;
+          }
+        // exp by the hardware exp2 (the sum only has to agree to float
+        // rounding; the polynomial exp1 costs ~7x the instructions here)
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 32; q++)
+          if (jb + q < N) sum += __builtin_amdgcn_exp2f((vals[q] - m) * 1.44269504f);
+        const float mo = __shfl_xor(m, 32, 64);
+        const int io = __shfl_xor(idx, 32, 64);
+        const float so = __shfl_xor(sum, 32, 64);
+        // lane r (< 32) holds columns 0..31, its partner 32..63
+        const float mm = fmaxf(m, mo);
+        const int ii = mo > m ? io : idx;
+        const float ss = sum * __builtin_amdgcn_exp2f((m - mm) * 1.44269504f) +
+                         (so > 0.0f ? so * __builtin_amdgcn_exp2f((mo - mm) * 1.44269504f) : 0.0f);
+        const int i = i0 + mi * 32 + r;
+        const unsigned off =
+            (ch == 0 && i < M) ? (unsigned)(((int64_t)i * nb + cb) * 16) : 0x80000000u;
+        f32x4 out;
+        out[0] = mm;
+        out[1] = __int_as_float(ii);
+        out[2] = ss;
+        out[3] = 0.0f;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, out), pr, off, 0, 0);
+      }
+    } else if constexpr (!ROWS) {
 #pragma unroll
       for (int mi = 0; mi < 2; mi++)
 #pragma unroll
@@ -748,10 +822,89 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
   }
 }
 
+// Per row: combines the (max, first index, exp1 sum) partials of its nb
+// column blocks into the (value, index) pair of the row's softmax argmax.
+// One wave per row; block t holds columns 64 t .. 64 t + 63, so among the
+// blocks whose max is the row max the lowest t has the lowest index.
+__global__ __launch_bounds__(256) void head_pairs_kernel(const float* __restrict__ part,
+                                                         int64_t rows, int nb,
+                                                         float* __restrict__ pairs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const f32x4* pr = (const f32x4*)part + row * nb;
+  float m = -__builtin_inff();
+  int idx = 0x7fffffff;
+  for (int t = lane; t < nb; t += 64) {
+    const f32x4 q = pr[t];
+    if (q[0] > m) {
+      m = q[0];
+      idx = __float_as_int(q[1]);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float mo = __shfl_xor(m, off, 64);
+    const int io = __shfl_xor(idx, off, 64);
+    if (mo > m || (mo == m && io < idx)) {
+      m = mo;
+      idx = io;
+    }
+  }
+  float sum = 0.0f;
+  for (int t = lane; t < nb; t += 64) {
+    const f32x4 q = pr[t];
+    sum += q[2] * __builtin_amdgcn_exp2f((q[0] - m) * 1.44269504f);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (lane == 0) {
+    pairs[2 * row] = 1.0f / sum;   // the max's exponential is exp1(0) = 1
+    pairs[2 * row + 1] = __int_as_float(idx);
+  }
+}
+
+bool head_argmax_eligible(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb) {
+  const int64_t tiles = (int64_t)ceil_div(m, 64) * ceil_div(n, 64);
+  return m > 0 && n > 0 && k > 0 && k % WB_BK == 0 && lda % 4 == 0 && tiles < (1ll << 30) &&
+         ((m - 1) * lda + k) * 4 < (1ll << 31) && ((k - 1) * ldb + n) * 4 < (1ll << 31) &&
+         (k * ldb + 128) * 4 < (1ll << 31) && (64 * lda + k) * 4 < (1ll << 31) &&
+         m * ceil_div(n, 64) * 16 < (1ll << 31);
+}
+
+int64_t head_argmax_part_floats(int64_t m, int64_t n) { return m * ceil_div(n, 64) * 4; }
+
+// Logits x[M][K] . w[K][N] + bias[N] never stored: the one-wave GEMM's
+// argmax epilogue writes per-block partials, head_pairs_kernel the pairs.
+int launch_head_argmax(const float* x, int64_t m, int64_t k, const float* w, int64_t ldb,
+                       int64_t n, const float* bias, float* part, float* pairs, hipStream_t s) {
+  if (!head_argmax_eligible(m, n, k, k, ldb))
+    return fail(QPH_EUNSUPPORTED, "fused head: shape outside the one-wave GEMM");
+  if ((uintptr_t)x % 16 != 0) return fail(QPH_EUNSUPPORTED, "fused head: A not 16-byte aligned");
+  GemmArgs g{};
+  g.a = x; g.lda = k; g.b = w; g.ldb = ldb;
+  g.m = m; g.n = n; g.k = k; g.batch = 1;
+  g.bias = bias; g.bias_mode = bias ? 2 : 0;
+  g.act = make_act(nullptr);
+  g.part = part;
+  int occ = 0, cus = 0;
+  QPH_TRY(device_cus(nullptr, &cus));
+  QPH_TRY(kernel_occupancy((const void*)gemm_wave_kernel<WV_EPI_ARGMAX>, 64, &occ));
+  const int mb = (int)ceil_div(m, 64), nb = (int)ceil_div(n, 64);
+  const int ntiles = mb * nb;
+  const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
+  const int wg_xcd = std::max(1, std::min(per_xcd, occ * cus / NUM_XCD));
+  hipLaunchKernelGGL(gemm_wave_kernel<WV_EPI_ARGMAX>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64),
+                     0, s, g, mb, nb, ntiles, per_xcd, wg_xcd);
+  QPH_TRY(launch_check("gemm_wave_kernel<argmax>"));
+  hipLaunchKernelGGL(head_pairs_kernel, dim3(ceil_div(m, 4)), dim3(256), 0, s, part, m, nb, pairs);
+  return launch_check("head_pairs_kernel");
+}
+
 static int launch_wave(const GemmArgs& g, hipStream_t s) {
   int occ = 0, cus = 0;
   QPH_TRY(device_cus(nullptr, &cus));
-  QPH_TRY(kernel_occupancy((const void*)gemm_wave_kernel<true>, 64, &occ));
+  QPH_TRY(kernel_occupancy((const void*)gemm_wave_kernel<WV_EPI_ROWS>, 64, &occ));
   const int mb = (int)ceil_div(g.m, 64), nb = (int)ceil_div(g.n, 64);
   const int ntiles = mb * nb * (int)g.batch;
   const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
@@ -761,10 +914,10 @@ static int launch_wave(const GemmArgs& g, hipStream_t s) {
   const bool rows = g.m % 64 == 0 && g.ldc % 4 == 0 && (uintptr_t)g.c % 16 == 0 &&
                     g.c_batch % 4 == 0;
   if (rows)
-    hipLaunchKernelGGL(gemm_wave_kernel<true>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s,
+    hipLaunchKernelGGL(gemm_wave_kernel<WV_EPI_ROWS>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s,
                        g, mb, nb, ntiles, per_xcd, wg_xcd);
   else
-    hipLaunchKernelGGL(gemm_wave_kernel<false>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s,
+    hipLaunchKernelGGL(gemm_wave_kernel<WV_EPI_ELEM>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64), 0, s,
                        g, mb, nb, ntiles, per_xcd, wg_xcd);
   return launch_check("gemm_wave_kernel");
 }

@@ -61,7 +61,7 @@ namespace qph {
 int ctx_workspace(qph_ctx* ctx, size_t bytes, void** out);
 
 // Activation kinds (qph_act.kind): 0 none, 1 gelu(c1,c2,c3), 2 relu,
-// 3 hardswish(alpha=c1, beta=c2), 4 sigmoid.
+// 3 hardswish(alpha=c1, beta=c2), 4 sigmoid, 5 hardsigmoid(alpha=c1, beta=c2).
 
 // exp1: qppocr-kernels/src/activation.rs:28-47 (x86.rs:28-57).
 __device__ __forceinline__ float exp1(float x) {
@@ -127,6 +127,7 @@ __device__ __forceinline__ float act_apply(float v, const Act& a) {
     case 2: return relu1(v);
     case 3: return v * hsig1(v, a.c1, a.c2);  // HardSigmoid node then Mul node
     case 4: return sigmoid1(v);
+    case 5: return hsig1(v, a.c1, a.c2);      // HardSigmoid node alone (the SE gate)
     default: return v;
   }
 }
@@ -142,7 +143,7 @@ inline Act make_act(const qph_act* a) {
   return r;
 }
 
-inline bool act_valid(const qph_act* a) { return !a || (a->kind >= 0 && a->kind <= 4); }
+inline bool act_valid(const qph_act* a) { return !a || (a->kind >= 0 && a->kind <= 5); }
 
 // The conv the reference runs as a plain GEMM over X[C][H*W] (conv.rs:264):
 // 1x1, stride 1, one group; padding excluded (X is then not that matrix).
@@ -171,8 +172,18 @@ struct GemmArgs {
   int res_up;                                      // 0 same shape; 2 = nearest 2x of a coarse map
   int64_t up_w, up_cw;                             // output / coarse image width (res_up)
   int trans_out;                                   // store C^T: c[j*ldc + i]
+  float* part;                                     // fused head: per-block argmax partials
 };
 int launch_gemm(const GemmArgs& g, hipStream_t s);
+// The rec head with the softmax-argmax fused into the GEMM (pairs only):
+// (max, first index, exp1 sum) per row and 64-column block into part
+// (head_argmax_part_floats floats), then the pairs.  Values within ~1e-6
+// of the unfused path's, not bit-identical (hardware exp2; the exp sum is
+// taken per block and rescaled); indices are the first maximum of the logits.
+bool head_argmax_eligible(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb);
+int64_t head_argmax_part_floats(int64_t m, int64_t n);
+int launch_head_argmax(const float* x, int64_t m, int64_t k, const float* w, int64_t ldb,
+                       int64_t n, const float* bias, float* part, float* pairs, hipStream_t s);
 
 // The session's linears: C[M][N] = act(A[M][K] * Wt[N][K]^T + bias) (+ res),
 // Wt the weight held transposed (k contiguous).
@@ -304,5 +315,32 @@ int launch_binary(float* a, const float* b, int64_t rows, int64_t cols, int op, 
                   hipStream_t s);
 int launch_mask_pairs(float* pairs, int64_t batch, int64_t t, const int32_t* t_valid,
                       hipStream_t s);
+// reduce_mean over the last axis (also GlobalAveragePool: rows = N*C planes)
+int launch_reduce_mean(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t s);
+
+// qph_aux.hip.  ctot / coff: the output is channels [coff, coff + c) of a
+// tensor with ctot channels (ctot = c, coff = 0 for a plain output).
+int launch_mul_add_scale(const float* f, const float* gate, const float* r, float* out, int64_t c,
+                         int64_t gmod, int64_t hw, int64_t planes, int64_t ctot, int64_t coff,
+                         hipStream_t s);
+void pool2d_out_hw(int64_t h, int64_t w, int64_t kh, int64_t kw, int64_t sh, int64_t sw,
+                   int64_t ph, int64_t pw, int64_t peh, int64_t pew, int64_t* oh, int64_t* ow);
+int launch_pool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, int64_t kh,
+                  int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t peh,
+                  int64_t pew, int max_pool, float* y, int64_t ctot, int64_t coff, hipStream_t s);
+int launch_resize_bilinear(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
+                           int64_t oh, int64_t ow, int align, float* y, int64_t ctot,
+                           int64_t coff, hipStream_t s);
+int launch_transpose4(const float* x, const int64_t xs[4], const int32_t perm[4], float* y,
+                      hipStream_t s);
+int launch_copy_slot(const float* x, float* y, int64_t c, int64_t hw, int64_t planes,
+                     int64_t ctot, int64_t coff, hipStream_t s);
+int launch_det_normalize(const uint8_t* rgb, int64_t h, int64_t w, float* out, hipStream_t s);
+int launch_resize_rgb_u8(const uint8_t* src, int64_t sw, int64_t sh, uint8_t* dst, int64_t dw,
+                         int64_t dh, hipStream_t s);
+int launch_pack_crop(const uint8_t* crop, int64_t ch, int64_t cw, int64_t img_h, int64_t img_w,
+                     float* dst, int pad_only, hipStream_t s);
+int launch_db_mask(const float* pred, int64_t h, int64_t w, float thresh, int dilate,
+                   uint8_t* out, hipStream_t s);
 
 }  // namespace qph

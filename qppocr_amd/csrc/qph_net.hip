@@ -27,6 +27,9 @@ struct qph_net {
   std::vector<bool> cl_dw;       // depthwise conv node run channel-last (in and out)
   std::vector<bool> cl_pw;       // 1x1 conv node run as a row-major GEMM, channel-last in and out
   std::vector<bool> cl_out;      // 1x1 conv node storing channel-last (trans_out) for a cl_dw reader
+  std::vector<bool> head;        // linear node i and the pairs-only softmax i + 1 run fused
+  std::vector<float*> head_part; // per fused head: its per-block argmax partials
+  std::vector<bool> nostore;     // per tensor: never materialised (a fused head's logits)
   std::vector<float*> tptr;      // per tensor device pointer
   std::vector<int64_t> pitch;    // per tensor: padded row pitch in floats (0: contiguous)
   char* arena;
@@ -155,6 +158,34 @@ static int run_node(qph_net* net, size_t i) {
     }
     case QPH_OP_ACT:
       return launch_elementwise_act(x, y, numel_of(net, n.in), make_act(&n.act), s);
+    case QPH_OP_GAP:
+      return launch_reduce_mean(x, xs[0] * xs[1], xs[2] * xs[3], y, s);
+    case QPH_OP_MUL_ADD_SCALE: {
+      // gate per channel ([C]) or per batch item and channel ([N, C])
+      const int64_t c = xs[1], planes = xs[0] * xs[1];
+      const float* gate = net->tptr[n.in3];
+      const int64_t gmod = numel_of(net, n.in3) == c ? c : planes;
+      return launch_mul_add_scale(x, gate, res, y, c, gmod, xs[2] * xs[3], planes,
+                                  n.y_ctotal ? n.y_ctotal : c, n.y_coff, s);
+    }
+    case QPH_OP_POOL:
+      return launch_pool2d(x, xs[0], xs[1], xs[2], xs[3], n.ws[2], n.ws[3], n.cp.sh, n.cp.sw,
+                           n.cp.ph, n.cp.pw, n.cp.peh, n.cp.pew, n.ws[0] != 0, y,
+                           n.y_ctotal ? n.y_ctotal : xs[1], n.y_coff, s);
+    case QPH_OP_RESIZE: {
+      const int64_t* ys = &net->shapes[4 * (size_t)n.out];
+      if (n.ws[0] == 0)
+        return launch_resize_nearest(x, xs[0] * xs[1], xs[2], xs[3], ys[2], ys[3], y, s);
+      return launch_resize_bilinear(x, xs[0], xs[1], xs[2], xs[3], ys[2], ys[3], n.ws[1] != 0, y,
+                                    n.y_ctotal ? n.y_ctotal : xs[1], n.y_coff, s);
+    }
+    case QPH_OP_TRANSPOSE: {
+      const int32_t perm[4] = {(int32_t)n.ws[0], (int32_t)n.ws[1], (int32_t)n.ws[2],
+                               (int32_t)n.ws[3]};
+      return launch_transpose4(x, xs, perm, y, s);
+    }
+    case QPH_OP_COPY_SLOT:
+      return launch_copy_slot(x, y, xs[1], xs[2] * xs[3], xs[0] * xs[1], n.y_ctotal, n.y_coff, s);
     default:
       return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unknown op");
   }
@@ -169,6 +200,43 @@ static int32_t storage_of(const qph_net* net, int32_t t) {
 // 32-column segment of the GEMM's stores is then one whole cache line instead
 // of parts of two.  Runs before the arena is laid out; ids are range-checked
 // here because the nodes are validated later.
+// With QPH_NET_FUSED_HEAD: a linear read only by the pairs-only softmax
+// argmax right after it (the rec head) runs as one GEMM whose epilogue keeps
+// per-block (max, index, exp sum) partials; its logits are never stored.
+// Runs before the arena is laid out (ids range-checked here: the nodes are
+// validated later).
+static void plan_fused_head(qph_net* net, int32_t flags) {
+  const size_t nn = net->nodes.size(), nt = net->tptr.size();
+  net->head.assign(nn, false);
+  net->head_part.assign(nn, nullptr);
+  net->nostore.assign(nt, false);
+  if (!(flags & QPH_NET_FUSED_HEAD)) return;
+  auto ok = [&](int32_t t) { return t >= 0 && (size_t)t < nt; };
+  for (size_t i = 0; i + 1 < nn; i++) {
+    const qph_node& q = net->nodes[i];
+    const qph_node& r = net->nodes[i + 1];
+    if (q.op != QPH_OP_LINEAR || r.op != QPH_OP_SOFTMAX_ARGMAX || !ok(q.out) || !ok(q.in) ||
+        !ok(r.out2) || r.out >= 0 || r.in != q.out || q.in2 >= 0 || q.act.kind != QPH_ACT_NONE ||
+        q.ws[0] <= 0 || q.ws[1] <= 0 || r.ws[0] != q.ws[1])
+      continue;
+    const int32_t t = q.out;
+    if (net->alias[(size_t)t] >= 0) continue;
+    bool single = true;
+    for (size_t t2 = 0; t2 < nt; t2++) single = single && net->alias[t2] != t;
+    for (size_t j = 0; j < nn; j++)
+      if (j != i + 1)
+        single = single && net->nodes[j].in != t && net->nodes[j].in2 != t &&
+                 net->nodes[j].in3 != t;
+    for (int32_t o : net->outputs) single = single && o != t;
+    const int64_t rows = numel_of(net, q.in) / q.ws[0];
+    if (!single || numel_of(net, q.in) % q.ws[0] ||
+        !head_argmax_eligible(rows, q.ws[1], q.ws[0], q.ws[0], (q.ws[1] + 3) / 4 * 4))
+      continue;
+    net->head[i] = true;
+    net->nostore[(size_t)t] = true;
+  }
+}
+
 static void plan_pitch(qph_net* net) {
   const size_t nt = net->tptr.size();
   net->pitch.assign(nt, 0);
@@ -180,6 +248,7 @@ static void plan_pitch(qph_net* net) {
   for (const qph_node& n : net->nodes) {
     if (ok(n.in)) readers[(size_t)storage_of(net, n.in)]++;
     if (ok(n.in2)) readers[(size_t)storage_of(net, n.in2)]++;
+    if (ok(n.in3)) readers[(size_t)storage_of(net, n.in3)]++;
   }
   for (int32_t o : net->outputs)
     if (ok(o)) readers[(size_t)storage_of(net, o)] += 1 << 20;   // outputs stay contiguous
@@ -269,6 +338,7 @@ static void plan_cl(qph_net* net) {
   for (const qph_node& n : net->nodes) {
     readers[(size_t)storage_of(net, n.in)]++;
     if (n.in2 >= 0) readers[(size_t)storage_of(net, n.in2)]++;
+    if (n.in3 >= 0) readers[(size_t)storage_of(net, n.in3)]++;
   }
   for (int32_t o : net->outputs) readers[(size_t)storage_of(net, o)] += 1 << 20;
   auto producer = [&](int32_t t) {
@@ -352,6 +422,7 @@ static int plan_dwpw(qph_net* net) {
   for (const qph_node& n : net->nodes) {
     readers[(size_t)storage_of(net, n.in)]++;
     if (n.in2 >= 0) readers[(size_t)storage_of(net, n.in2)]++;
+    if (n.in3 >= 0) readers[(size_t)storage_of(net, n.in3)]++;
   }
   for (int32_t o : net->outputs) readers[(size_t)storage_of(net, o)]++;
   for (size_t i = 0; i + 1 < nn; i++) {
@@ -425,6 +496,17 @@ static int plan_dwpw(qph_net* net) {
   return QPH_OK;
 }
 
+// The output of node i is [n, c, h, w], or channels [y_coff, y_coff + c) of a
+// [n, y_ctotal, h, w] tensor (a Concat slot).
+static int check_slot(const qph_net* net, size_t i, const qph_node& q, int64_t n, int64_t c,
+                      int64_t h, int64_t w) {
+  const int64_t* ys = &net->shapes[4 * (size_t)q.out];
+  const int64_t ct = q.y_ctotal ? q.y_ctotal : c;
+  if (q.y_coff < 0 || q.y_coff + c > ct || ys[0] != n || ys[1] != ct || ys[2] != h || ys[3] != w)
+    return fail(QPH_EINVAL, node_name(i, q) + ": output shape / Concat slot mismatch");
+  return QPH_OK;
+}
+
 static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t nw) {
   const qph_node& n = net->nodes[i];
   QPH_TRY(check_tensor(net, n.in, false, i, n, "input"));
@@ -432,6 +514,7 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
   // exit of device.rs:160-165)
   QPH_TRY(check_tensor(net, n.out, n.op == QPH_OP_SOFTMAX_ARGMAX, i, n, "output"));
   QPH_TRY(check_tensor(net, n.in2, true, i, n, "second input"));
+  QPH_TRY(check_tensor(net, n.in3, true, i, n, "third input"));
   QPH_TRY(check_tensor(net, n.out2, true, i, n, "second output"));
   for (int32_t wi : {n.w, n.bias, n.w2})
     if (wi >= nw) return fail(QPH_EINVAL, node_name(i, n) + ": bad weight index");
@@ -527,6 +610,51 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
       if (numel_of(net, n.out) != numel_of(net, n.in))
         return fail(QPH_EINVAL, node_name(i, n) + ": size mismatch");
       return QPH_OK;
+    case QPH_OP_GAP:
+      if (ys[0] != xs[0] || ys[1] != xs[1] || ys[2] != 1 || ys[3] != 1)
+        return fail(QPH_EINVAL, node_name(i, n) + ": GlobalAveragePool output must be [N,C,1,1]");
+      return QPH_OK;
+    case QPH_OP_MUL_ADD_SCALE: {
+      QPH_TRY(check_tensor(net, n.in3, false, i, n, "gate"));
+      if (n.in2 < 0) return fail(QPH_EINVAL, node_name(i, n) + ": MulAddScale without residual");
+      const int64_t g = numel_of(net, n.in3);
+      if (numel_of(net, n.in2) != numel_of(net, n.in) || (g != xs[1] && g != xs[0] * xs[1]))
+        return fail(QPH_EINVAL, node_name(i, n) + ": MulAddScale shapes");
+      QPH_TRY(check_slot(net, i, n, xs[0], xs[1], xs[2], xs[3]));
+      return QPH_OK;
+    }
+    case QPH_OP_POOL: {
+      if (n.ws[2] <= 0 || n.ws[3] <= 0 || n.cp.sh <= 0 || n.cp.sw <= 0 || n.cp.ph < 0 ||
+          n.cp.pw < 0 || n.cp.peh < 0 || n.cp.pew < 0)
+        return fail(QPH_EINVAL, node_name(i, n) + ": pool window");
+      int64_t oh, ow;
+      pool2d_out_hw(xs[2], xs[3], n.ws[2], n.ws[3], n.cp.sh, n.cp.sw, n.cp.ph, n.cp.pw, n.cp.peh,
+                    n.cp.pew, &oh, &ow);
+      QPH_TRY(check_slot(net, i, n, xs[0], xs[1], oh, ow));
+      return QPH_OK;
+    }
+    case QPH_OP_RESIZE:
+      if (n.ws[0] != 0 && n.ws[0] != 1)
+        return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": resize mode must be nearest or bilinear");
+      if (n.ws[0] == 0 && (n.y_ctotal || n.y_coff))
+        return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": nearest resize into a Concat slot");
+      QPH_TRY(check_slot(net, i, n, xs[0], xs[1], ys[2], ys[3]));
+      return QPH_OK;
+    case QPH_OP_TRANSPOSE: {
+      int seen = 0;
+      for (int d = 0; d < 4; d++) {
+        if (n.ws[d] < 0 || n.ws[d] > 3 || (seen >> n.ws[d]) & 1)
+          return fail(QPH_EINVAL, node_name(i, n) + ": perm is not a permutation of 0..3");
+        seen |= 1 << n.ws[d];
+        if (ys[d] != xs[n.ws[d]])
+          return fail(QPH_EINVAL, node_name(i, n) + ": transpose output shape");
+      }
+      return QPH_OK;
+    }
+    case QPH_OP_COPY_SLOT:
+      if (!n.y_ctotal) return fail(QPH_EINVAL, node_name(i, n) + ": copy slot needs y_ctotal");
+      QPH_TRY(check_slot(net, i, n, xs[0], xs[1], xs[2], xs[3]));
+      return QPH_OK;
     default:
       return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unsupported op");
   }
@@ -544,6 +672,17 @@ static int run_all(qph_net* net) {
     if (net->group_len[i] > 1) {
       QPH_TRY(launch_dense_conv_group(&net->plan[i], net->group_len[i], s));
       step = (size_t)net->group_len[i];
+    } else if (net->head[i]) {
+      const qph_node& q = net->nodes[i];
+      const qph_node& r = net->nodes[i + 1];
+      const int64_t k = q.ws[0], nn = q.ws[1];
+      const float* w = net->wk[i] ? net->wk[i] : net->weights[q.w];
+      const int64_t ldb = net->wk[i] ? (nn + 3) / 4 * 4 : nn;
+      const int rc = launch_head_argmax(net->tptr[q.in], numel_of(net, q.in) / k, k, w, ldb, nn,
+                                        q.bias >= 0 ? net->weights[q.bias] : nullptr,
+                                        net->head_part[i], net->tptr[r.out2], s);
+      if (rc != QPH_OK) return fail(rc, node_name(i, q) + ": " + qph_last_error());
+      step = 2;
     } else if (net->fused[i]) {
       QPH_TRY(launch_dwpw(net->dwpw[i], s));
       step = net->dwpw[i].stem ? 3 : 2;
@@ -596,6 +735,8 @@ static void release(qph_net* net) {
     if (p) (void)hipHostFree(p);
   for (float* p : net->weights) (void)hipFree(p);
   for (float* p : net->wk)
+    if (p) (void)hipFree(p);
+  for (float* p : net->head_part)
     if (p) (void)hipFree(p);
   for (float* p : net->wt)
     if (p) (void)hipFree(p);
@@ -665,11 +806,13 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
       return bail(QPH_EINVAL);
     }
   }
+  plan_fused_head(net, spec->flags);
   plan_pitch(net);
   std::vector<size_t> off((size_t)spec->n_tensors, 0);
   for (int32_t t = 0; t < spec->n_tensors; t++) {
     if (net->alias[t] >= 0) continue;
     off[t] = net->arena_bytes;
+    if (net->nostore[(size_t)t]) continue;
     int64_t words = numel_of(net, t);
     if (net->pitch[(size_t)t]) {
       const qph_node* q = nullptr;
@@ -747,6 +890,16 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     }
   }
   const size_t nn = net->nodes.size();
+  for (size_t i = 0; i < nn; i++) {
+    if (!net->head[i]) continue;
+    const qph_node& q = net->nodes[i];
+    const int64_t rows = numel_of(net, q.in) / q.ws[0];
+    float* d = nullptr;
+    rc = hip_check(hipMalloc((void**)&d, (size_t)head_argmax_part_floats(rows, q.ws[1]) * 4),
+                   "hipMalloc(head partials)");
+    if (rc) return bail(rc);
+    net->head_part[i] = d;
+  }
   if (spec->flags & QPH_NET_SEPARATE_LAUNCHES) {
     net->plan.assign(nn, ConvArgs{});
     net->group_len.assign(nn, 1);

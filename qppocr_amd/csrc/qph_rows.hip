@@ -1046,7 +1046,7 @@ __global__ void act_kernel(const float* __restrict__ x, float* __restrict__ y, i
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) {
     float v = x[i];
-    y[i] = a.kind == 5 ? hsig1(v, a.c1, a.c2) : act_apply(v, a);
+    y[i] = act_apply(v, a);
   }
 }
 
@@ -1139,6 +1139,13 @@ __global__ __launch_bounds__(256) void reduce_mean_kernel(const float* __restric
   if (lane == 0) out[row] = mean;
 }
 
+int launch_reduce_mean(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t s) {
+  if (rows >= (1ll << 33)) return fail(QPH_EUNSUPPORTED, "reduce_mean: too many rows");
+  hipLaunchKernelGGL(reduce_mean_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, x, rows, cols,
+                     out);
+  return launch_check("reduce_mean_kernel");
+}
+
 }  // namespace qph
 
 using namespace qph;
@@ -1147,7 +1154,5 @@ extern "C" QPH_API int qph_reduce_mean_last(qph_ctx* ctx, const float* x, int64_
                                             int64_t cols, float* out) {
   if (!ctx) return fail(QPH_EINVAL, "null context");
   if (rows <= 0 || cols <= 0 || !x || !out) return fail(QPH_EINVAL, "reduce_mean: bad argument");
-  hipLaunchKernelGGL(reduce_mean_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, ctx->stream, x,
-                     rows, cols, out);
-  return launch_check("reduce_mean_kernel");
+  return launch_reduce_mean(x, rows, cols, out, ctx->stream);
 }

@@ -513,6 +513,19 @@ QPH_API int qph_softmax_argmax(qph_ctx* ctx, const float* logits, int64_t rows, 
   return launch_softmax_argmax(logits, rows, cols, cols, probs, pairs, ctx->stream);
 }
 
+QPH_API int qph_linear_softmax_argmax(qph_ctx* ctx, const float* x, const float* w,
+                                      const float* bias, int64_t rows, int64_t k, int64_t n,
+                                      float* pairs) {
+  CTX_CHECK(ctx);
+  if (rows <= 0 || k <= 0 || n <= 0 || !x || !w || !pairs)
+    return fail(QPH_EINVAL, "linear_softmax_argmax: bad argument");
+  if (!head_argmax_eligible(rows, n, k, k, n))
+    return fail(QPH_EUNSUPPORTED, "linear_softmax_argmax: needs k % 16 == 0, operands < 2 GB");
+  void* part = nullptr;
+  QPH_TRY(ctx_workspace(ctx, (size_t)head_argmax_part_floats(rows, n) * 4, &part));
+  return launch_head_argmax(x, rows, k, w, n, n, bias, (float*)part, pairs, ctx->stream);
+}
+
 QPH_API int qph_ctc_argmax(qph_ctx* ctx, const float* probs, int64_t batch, int64_t t_len,
                            int64_t cols, const int32_t* t_valid_host, float* pairs) {
   CTX_CHECK(ctx);

@@ -33,10 +33,12 @@ import math
 import numpy as np
 
 from . import _lib
-from ._lib import (ACT_GELU, ACT_HARDSWISH, ACT_NONE, ACT_RELU, NET_SEPARATE_LAUNCHES, Act,
+from ._lib import (ACT_GELU, ACT_HARDSIGMOID, ACT_HARDSWISH, ACT_NONE, ACT_RELU, NET_FUSED_HEAD,
+                   NET_SEPARATE_LAUNCHES, Act,
                    ConvParams, Node, NetSpec,
-                   OP_ACT, OP_ATTENTION, OP_CONV, OP_CONVT, OP_CONVT_PAIR_SIG, OP_LAYERNORM,
-                   OP_LINEAR, OP_SOFTMAX_ARGMAX, check)
+                   OP_ACT, OP_ATTENTION, OP_CONV, OP_CONVT, OP_CONVT_PAIR_SIG, OP_COPY_SLOT,
+                   OP_GAP, OP_LAYERNORM, OP_LINEAR, OP_MUL_ADD_SCALE, OP_POOL, OP_RESIZE,
+                   OP_SOFTMAX_ARGMAX, OP_TRANSPOSE, check)
 
 HS = (1.0 / 6.0, 0.5, 0.0)
 GELU_C = (1.4142135, 1.0, 0.5)
@@ -46,7 +48,7 @@ LN_EPS = 1e-6
 
 
 def _act(kind):
-    if kind == ACT_HARDSWISH:
+    if kind in (ACT_HARDSWISH, ACT_HARDSIGMOID):
         return Act(kind, *HS)
     if kind == ACT_GELU:
         return Act(kind, *GELU_C)
@@ -153,6 +155,60 @@ class Graph:
                                y_coff=0, y_up=1, heads=0, dh=0, eps=0.0, scale=0.0))
         return probs, pairs
 
+    # ---------------------------------------------- pooling / SE / layout
+    def _node(self, op, x, out, **kw):
+        d = dict(op=op, inp=x, in2=-1, in3=-1, out=out, out2=-1, w=-1, bias=-1, w2=-1,
+                 ws=(0, 0, 0, 0), w2s=(0, 0, 0, 0), cp=(1, 1, 0, 0, 0, 0, 1, 1, 1), act=ACT_NONE,
+                 res_up=0, trans_out=0, y_ctotal=0, y_coff=0, y_up=1, heads=0, dh=0, eps=0.0,
+                 scale=0.0)
+        d.update(kw)
+        self.nodes.append(d)
+        return out
+
+    def global_avg_pool(self, x):
+        """GlobalAveragePool [N, C, H, W] -> [N, C, 1, 1] (pool2d.rs:10-29)."""
+        n, c = self.shapes[x][:2]
+        return self._node(OP_GAP, x, self.tensor((n, c, 1, 1)))
+
+    def mul_add_scale(self, feature, gate, residual, out=None, y_ctotal=0, y_coff=0):
+        """MulAddScale (optimize.rs:429-497): feature * gate + residual; out /
+        y_ctotal / y_coff place it in a Concat slot."""
+        n, c, h, w = self.shapes[feature]
+        out = self.tensor((n, c, h, w)) if out is None else out
+        return self._node(OP_MUL_ADD_SCALE, feature, out, in2=residual, in3=gate,
+                          y_ctotal=y_ctotal, y_coff=y_coff)
+
+    def pool(self, x, k, stride, pad=(0, 0, 0, 0), max_pool=True, out=None, y_ctotal=0,
+             y_coff=0):
+        """MaxPool / AveragePool (pool2d.rs:51-236); pad = (ph, pw, peh, pew)."""
+        n, c, h, w = self.shapes[x]
+        kh, kw = k
+        sh, sw = stride
+        ph, pw, peh, pew = pad
+        oh = max(h + ph + peh - kh, 0) // sh + 1
+        ow = max(w + pw + pew - kw, 0) // sw + 1
+        out = self.tensor((n, c, oh, ow)) if out is None else out
+        return self._node(OP_POOL, x, out, ws=(int(max_pool), 0, kh, kw),
+                          cp=(sh, sw, ph, pw, peh, pew, 1, 1, 1), y_ctotal=y_ctotal, y_coff=y_coff)
+
+    def resize(self, x, oh, ow, bilinear=True, align_corners=False, out=None, y_ctotal=0,
+               y_coff=0):
+        """Resize: nearest (resize.rs:8-57) or bilinear (resize.rs:60-142)."""
+        n, c = self.shapes[x][:2]
+        out = self.tensor((n, c, oh, ow)) if out is None else out
+        return self._node(OP_RESIZE, x, out, ws=(int(bilinear), int(align_corners), 0, 0),
+                          y_ctotal=y_ctotal, y_coff=y_coff)
+
+    def transpose(self, x, perm):
+        """Rank-4 Transpose: output dimension d is input dimension perm[d]."""
+        s = self.shapes[x]
+        return self._node(OP_TRANSPOSE, x, self.tensor(tuple(s[p] for p in perm)),
+                          ws=tuple(int(p) for p in perm))
+
+    def copy_slot(self, x, out, y_ctotal, y_coff):
+        """A Concat input no producer writes in place, copied into its slot."""
+        return self._node(OP_COPY_SLOT, x, out, y_ctotal=y_ctotal, y_coff=y_coff)
+
     # ------------------------------------------------------------ C struct
     def to_c(self):
         nt = len(self.shapes)
@@ -171,6 +227,7 @@ class Graph:
             nd.res_up, nd.trans_out = d["res_up"], d["trans_out"]
             nd.y_ctotal, nd.y_coff, nd.y_up = d["y_ctotal"], d["y_coff"], d["y_up"]
             nd.heads, nd.dh, nd.eps, nd.scale = d["heads"], d["dh"], d["eps"], d["scale"]
+            nd.in3 = d.get("in3", -1)
         wsizes = (ctypes.c_int64 * max(1, len(self.weights)))(*[w.size for w in self.weights])
         outs = (ctypes.c_int32 * max(1, len(self.outputs)))(*self.outputs)
         spec = NetSpec(nt, shapes, alias, len(self.nodes), nodes, len(self.weights), wsizes,
@@ -292,10 +349,14 @@ def rec_weights(r):
     return ws
 
 
-def build_rec_graph(weights, batch, w, h=48, probs=True):
+def build_rec_graph(weights, batch, w, h=48, probs=True, fused_head=False):
     """Rec graph for a [batch, 3, h, w] input over the weights of rec_weights().
     probs=False: the head exports the (val, idx) pairs only, the GPU
-    sessions' CTC exit (rec_argmax_pairs, device.rs:160-165)."""
+    sessions' CTC exit (rec_argmax_pairs, device.rs:160-165).  fused_head:
+    pairs only, and the session runs the head linear + softmax argmax as one
+    GEMM (QPH_NET_FUSED_HEAD; pairs to float rounding, not bit-exact)."""
+    if fused_head:
+        probs = False
     it = iter(weights)
     g = Graph((batch, 3, h, w))
     nw = lambda: g.weight(next(it))  # noqa: E731
@@ -325,12 +386,14 @@ def build_rec_graph(weights, batch, w, h=48, probs=True):
     logits = g.linear(x, wh, bh)
     pr, pairs = g.softmax_argmax(logits, REC_CLASSES, probs)
     g.outputs = [pr, pairs] if probs else [pairs]
+    if fused_head:
+        g.flags |= NET_FUSED_HEAD
     return g
 
 
-def build_rec(seed=3, batch=32, w=320, h=48, probs=True):
+def build_rec(seed=3, batch=32, w=320, h=48, probs=True, fused_head=False):
     x_in, r = rec_input(seed, batch, h, w)
-    g = build_rec_graph(rec_weights(r), batch, w, h, probs)
+    g = build_rec_graph(rec_weights(r), batch, w, h, probs, fused_head)
     return g, x_in
 
 
@@ -384,6 +447,16 @@ def node_cost(g, d):
     if op == OP_LAYERNORM:
         cols = d["ws"][0]
         return 0, (2 * g.numel(d["inp"]) + 2 * cols) * f32, "hbm"
+    if op == OP_GAP:
+        n, c = g.shapes[d["inp"]][:2]
+        return 0, (g.numel(d["inp"]) + n * c) * f32, "hbm"
+    if op == OP_MUL_ADD_SCALE:
+        return 0, (3 * g.numel(d["inp"]) + g.numel(d["in3"])) * f32, "hbm"
+    if op in (OP_POOL, OP_RESIZE, OP_COPY_SLOT):
+        n = g.shapes[d["inp"]][0]
+        c = g.shapes[d["inp"]][1]
+        oh, ow = g.shapes[d["out"]][2:]
+        return 0, (g.numel(d["inp"]) + n * c * oh * ow) * f32, "hbm"
     return 0, 2 * g.numel(d["inp"]) * f32, "hbm"
 
 

@@ -211,6 +211,19 @@ def softmax_argmax(logits, probs=True):
     return pr, pairs
 
 
+def linear_softmax_argmax(x, w, bias=None):
+    """The fused rec head: MatMul + Add(bias) + Softmax + argmax pairs in one
+    GEMM (logits never stored).  x [..., K], w [K, N]; returns pairs
+    [..., 2].  Values agree with the unfused path to float rounding."""
+    k, n = w.shape
+    rows = x.numel() // k
+    pairs = torch.empty(tuple(x.shape[:-1]) + (2,), device=x.device)
+    with _Call(_dev(x)) as ctx:
+        check(_lib.load().qph_linear_softmax_argmax(ctx, _ptr(x), _ptr(w), _ptr(bias), rows, k, n,
+                                                    _ptr(pairs)))
+    return pairs
+
+
 def ctc_argmax(probs, t_valid=None):
     """(value, index-bits) per step; probs [B, T, C] (rec.rs:34-90)."""
     b, t, c = probs.shape
@@ -293,3 +306,108 @@ def reduce_mean_last(x):
 def pairs_ids(pairs):
     """Index half of a pairs tensor as int64 (f32 bits -> u32)."""
     return pairs[..., 1].contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+
+
+# ------------------------------------------- pooling / SE gate / resize / layout
+
+def _ptr_any(t):
+    """Device pointer of a contiguous tensor of any dtype (u8 images)."""
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError("qppocr_amd ops take contiguous device tensors")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def global_avg_pool(x):
+    """global_avg_pool (qppocr-kernels/src/pool2d.rs:10-29): [N,C,H,W] -> [N,C,1,1]."""
+    n, c, h, w = x.shape
+    out = torch.empty((n, c, 1, 1), device=x.device)
+    with _Call(_dev(x)) as ctx:
+        check(_lib.load().qph_global_avg_pool(ctx, _ptr(x), n, c, h * w, _ptr(out)))
+    return out
+
+
+def mul_add_scale(feature, gate, residual):
+    """mul_add_scale (elementwise.rs:134-179): feature * gate[c] + residual."""
+    n, c, h, w = feature.shape
+    out = torch.empty_like(feature)
+    with _Call(_dev(feature)) as ctx:
+        check(_lib.load().qph_mul_add_scale(ctx, _ptr(feature), _ptr(gate), _ptr(residual), n, c,
+                                            h * w, _ptr(out)))
+    return out
+
+
+def pool2d(x, k, stride, pad=(0, 0, 0, 0), max_pool=True):
+    """pool2d (pool2d.rs:51-236); pad = (ph, pw, peh, pew)."""
+    n, c, h, w = x.shape
+    kh, kw = k
+    sh, sw = stride
+    ph, pw, peh, pew = pad
+    oh = max(h + ph + peh - kh, 0) // sh + 1
+    ow = max(w + pw + pew - kw, 0) // sw + 1
+    y = torch.empty((n, c, oh, ow), device=x.device)
+    ys = (_lib.I64 * 4)()
+    with _Call(_dev(x)) as ctx:
+        check(_lib.load().qph_pool2d(ctx, _ptr(x), i64arr(x.shape), kh, kw, sh, sw, ph, pw, peh,
+                                     pew, int(bool(max_pool)), _ptr(y), ys))
+    assert tuple(ys) == (n, c, oh, ow)
+    return y
+
+
+def resize_bilinear(x, oh, ow, align_corners=False):
+    """resize_bilinear (resize.rs:60-142) over the last two axes."""
+    h, w = x.shape[-2:]
+    nc = x.numel() // (h * w)
+    y = torch.empty(tuple(x.shape[:-2]) + (oh, ow), device=x.device)
+    with _Call(_dev(x)) as ctx:
+        check(_lib.load().qph_resize_bilinear(ctx, _ptr(x), nc, h, w, oh, ow,
+                                              int(bool(align_corners)), _ptr(y)))
+    return y
+
+
+def transpose(x, perm):
+    """Rank-4 Transpose."""
+    y = torch.empty(tuple(x.shape[p] for p in perm), device=x.device)
+    pm = (_lib.I32 * 4)(*perm)
+    with _Call(_dev(x)) as ctx:
+        check(_lib.load().qph_transpose(ctx, _ptr(x), i64arr(x.shape), pm, _ptr(y)))
+    return y
+
+
+def det_normalize_u8(rgb):
+    """det input (engine.rs:959-982): u8 [H, W, 3] -> f32 [1, 3, H, W]."""
+    h, w = rgb.shape[:2]
+    out = torch.empty((1, 3, h, w), device=rgb.device)
+    with _Call(_dev(rgb)) as ctx:
+        check(_lib.load().qph_det_normalize_u8(ctx, _ptr_any(rgb), h, w, _ptr(out)))
+    return out
+
+
+def resize_bilinear_rgb_u8(src, dw, dh):
+    """resize_bilinear_rgb_u8 (resize.rs:153-209): u8 [sh, sw, 3] -> [dh, dw, 3]."""
+    sh, sw = src.shape[:2]
+    dst = torch.empty((dh, dw, 3), dtype=torch.uint8, device=src.device)
+    with _Call(_dev(src)) as ctx:
+        check(_lib.load().qph_resize_bilinear_rgb_u8(ctx, _ptr_any(src), sw, sh, _ptr_any(dst),
+                                                     dw, dh))
+    return dst
+
+
+def pack_crop(crop, img_h, img_w, pad_only=False, out=None):
+    """pack_crop (crop.rs:153-190): u8 crop [ch, cw, 3] -> f32 [3, img_h, img_w]."""
+    ch, cw = crop.shape[:2]
+    if out is None:
+        out = torch.empty((3, img_h, img_w), device=crop.device)
+    with _Call(_dev(crop)) as ctx:
+        check(_lib.load().qph_pack_crop(ctx, _ptr_any(crop), ch, cw, img_h, img_w,
+                                        int(bool(pad_only)), _ptr(out)))
+    return out
+
+
+def db_mask(pred, thresh, dilate=True):
+    """DB threshold + 2x2 dilation (geometry.rs:287-301, resize.rs:219-247)."""
+    h, w = pred.shape[-2:]
+    out = torch.empty((h, w), dtype=torch.uint8, device=pred.device)
+    with _Call(_dev(pred)) as ctx:
+        check(_lib.load().qph_db_mask(ctx, _ptr(pred), h, w, float(thresh), int(bool(dilate)),
+                                      _ptr_any(out)))
+    return out

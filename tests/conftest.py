@@ -85,3 +85,22 @@ def assert_bitexact(got, ref, name=""):
         d = np.abs(got.astype(np.float64) - ref).max()
         pytest.fail(f"{name}: {neq.sum()} / {got.size} elements differ; first at {tuple(idx)}: "
                     f"{got[tuple(idx)]!r} vs {ref[tuple(idx)]!r}; max |diff| {d:.3e}")
+
+
+def pairs_tolerance_check(pairs, pairs_ref, logits_ref):
+    """The target's rule for the CTC argmax exit: values within 1e-4
+    relative (1e-5 absolute near zero) of the reference's, ids identical
+    except where the top-2 logit gap of the step is below 1e-4.  Returns the
+    number of steps whose ids differ (all of them near-ties)."""
+    pairs = np.asarray(pairs, np.float32).reshape(-1, 2)
+    pairs_ref = np.asarray(pairs_ref, np.float32).reshape(-1, 2)
+    logits = np.asarray(logits_ref, np.float32).reshape(pairs.shape[0], -1)
+    baseline_tol_check(pairs[:, 0], pairs_ref[:, 0])
+    ids = np.ascontiguousarray(pairs[:, 1]).view(np.uint32)
+    ids_ref = np.ascontiguousarray(pairs_ref[:, 1]).view(np.uint32)
+    diff = np.nonzero(ids != ids_ref)[0]
+    if diff.size:
+        top2 = -np.sort(-logits[diff], axis=1)[:, :2].astype(np.float64)
+        gap = top2[:, 0] - top2[:, 1]
+        assert (gap < 1e-4).all(), f"ids differ at steps {diff[gap >= 1e-4][:8]} (gaps {gap.max()})"
+    return int(diff.size)

@@ -1,0 +1,142 @@
+"""Parity of the operators around the hot path (pooling, the SE gate's
+MulAddScale, bilinear resize, transpose, Concat slots) and of the steps
+either side of the networks (det input normalisation, rec pack_crop, the DB
+threshold + dilation) with the CPU oracle, bit for bit, through the C ABI.
+Shapes follow the reference's own tests (qppocr-kernels/tests/kernels.rs:
+1143-1258, tests/rsz_par.rs)."""
+import numpy as np
+import pytest
+
+from conftest import XorShift, assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _n(t):
+    return t.detach().cpu().numpy()
+
+
+POOL_CASES = [  # (k, stride, pad (ph, pw, peh, pew), max)
+    ((2, 2), (1, 1), (0, 0, 1, 1), True),      # 2x2 s1 SAME_UPPER (the v6 det MaxPool)
+    ((3, 3), (2, 2), (1, 1, 1, 1), False),     # kernels.rs:1169
+    ((3, 3), (2, 2), (1, 1, 1, 1), True),
+    ((2, 2), (2, 2), (0, 0, 0, 0), False),
+    ((3, 2), (1, 2), (1, 0, 2, 1), True),
+]
+
+
+@pytest.mark.parametrize("case", POOL_CASES, ids=[str(c) for c in POOL_CASES])
+def test_pool2d(gpu, oracle, case):
+    torch = gpu
+    from qppocr_amd import ops
+    k, s, pad, mx = case
+    rng = XorShift(0x243F6A8885A308D3)
+    x = rng.fill((2, 3, 20, 30))
+    want = oracle.pool2d(x, k[0], k[1], s[0], s[1], *pad, mx)
+    assert_bitexact(_n(ops.pool2d(_t(torch, x), k, s, pad, mx)), want, f"pool {case}")
+
+
+def test_global_avg_pool_and_mul_add_scale(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(51)
+    x = rng.standard_normal((2, 40, 23, 37)).astype(np.float32)
+    x[0, 3, 0, 0] = 2.0 ** 40                 # a plane whose f64 sum order matters
+    x[0, 3, 0, 1] = -(2.0 ** 40)
+    assert_bitexact(_n(ops.global_avg_pool(_t(torch, x))), oracle.global_avg_pool(x), "GAP")
+    gate = rng.random(40).astype(np.float32)
+    r = rng.standard_normal(x.shape).astype(np.float32)
+    assert_bitexact(_n(ops.mul_add_scale(_t(torch, x), _t(torch, gate), _t(torch, r))),
+                    oracle.mul_add_scale(x, gate, r), "mul_add_scale")
+
+
+@pytest.mark.parametrize("align", [False, True])
+def test_resize_bilinear_and_transpose(gpu, oracle, align):
+    torch = gpu
+    from qppocr_amd import ops
+    rng = XorShift(0x243F6A8885A308D3)
+    x = rng.fill((2, 3, 20, 30))
+    for oh, ow in [(33, 47), (10, 15), (40, 60), (1, 1)]:
+        assert_bitexact(_n(ops.resize_bilinear(_t(torch, x), oh, ow, align)),
+                        oracle.resize_bilinear(x, oh, ow, align), f"bilinear {oh}x{ow}")
+    for perm in [(0, 2, 3, 1), (0, 3, 1, 2), (3, 2, 1, 0)]:
+        assert_bitexact(_n(ops.transpose(_t(torch, x), perm)), oracle.transpose4(x, perm),
+                        f"transpose {perm}")
+
+
+def test_det_normalize_resize_u8_pack_crop(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    sw, sh = 848, 816                              # the reference test's source (rsz_par.rs:42)
+    src = (np.arange(sw * sh * 3, dtype=np.int64) * 7919 % 256).astype(np.uint8).reshape(sh, sw, 3)
+    gsrc = _t(torch, src)
+    for dw, dh in [(832, 832), (400, 48), (960, 1216), (17, 33)]:
+        got = _n(ops.resize_bilinear_rgb_u8(gsrc, dw, dh))
+        assert (got == oracle.resize_bilinear_rgb_u8(src, dw, dh)).all(), (dw, dh)
+    rgb = src[:301, :417]
+    assert_bitexact(_n(ops.det_normalize_u8(_t(torch, rgb))), oracle.det_normalize(rgb), "det norm")
+    assert_bitexact(_n(ops.det_normalize_u8(_t(torch, src[:64, :128]))),
+                    oracle.det_normalize(src[:64, :128]), "det norm (vector stores)")
+    for (y0, y1, x0, x1, pad_only) in [(100, 154, 20, 330, False), (0, 40, 0, 500, True),
+                                        (10, 58, 5, 1900 // 4, False), (7, 20, 3, 900, False),
+                                        (0, 48, 0, 200, True)]:
+        crop = np.ascontiguousarray(src[y0:y1, x0:x1])
+        got = _n(ops.pack_crop(_t(torch, crop), 48, 320, pad_only))
+        assert_bitexact(got, oracle.pack_crop(crop, 48, 320, pad_only), f"pack_crop {y0, x1}")
+
+
+def test_db_mask(gpu, oracle):
+    torch = gpu
+    from qppocr_amd import ops
+    for h, w in [(832, 832), (37, 129), (1, 1), (5, 300), (300, 5)]:
+        i = np.arange(h * w, dtype=np.uint64)
+        m = (((i * np.uint64(2654435761)) >> np.uint64(24)) % np.uint64(256)).astype(np.uint8) % 3
+        pred = (m.reshape(h, w).astype(np.float32) * 0.4).astype(np.float32)   # 0, 0.4, 0.8
+        for dil in (True, False):
+            got = _n(ops.db_mask(_t(torch, pred), 0.3, dil))
+            assert (got == oracle.db_mask(pred, 0.3, dil)).all(), (h, w, dil)
+
+
+def test_session_se_block_concat_slots(gpu, oracle):
+    """A PP-OCRv6-style gated block through the session against the oracle's
+    node-by-node run: conv, depthwise, the SE path (GlobalAveragePool, 1x1 +
+    ReLU, 1x1 + HardSigmoid) into MulAddScale with a residual, written into a
+    Concat slot; a 2x2 s1 SAME_UPPER MaxPool and a bilinear Resize into the
+    other slots; the graph input copied into the last; then a Transpose."""
+    from qppocr_amd import nets
+    from qppocr_amd._lib import ACT_HARDSIGMOID, ACT_RELU, ACT_HARDSWISH
+    from oracle import nets as onets
+    r = nets.WeightRng(52)
+    g = nets.Graph((2, 16, 24, 28))
+    x = r.uniform((2, 16, 24, 28), -1, 1)
+    w1 = g.weight(r.kaiming((32, 16, 3, 3), 144))
+    b1 = g.weight(r.normal((32,), 0.1))
+    a = g.conv(0, w1, b1, pad=(1, 1, 1, 1), act=ACT_HARDSWISH)
+    wd = g.weight(r.kaiming((32, 1, 5, 5), 25))
+    bd = g.weight(r.normal((32,), 0.1))
+    d = g.conv(a, wd, bd, pad=(2, 2, 2, 2), group=32, act=ACT_HARDSWISH)
+    gp = g.global_avg_pool(d)
+    ws1 = g.weight(r.kaiming((8, 32, 1, 1), 32))
+    bs1 = g.weight(r.normal((8,), 0.1))
+    s1 = g.conv(gp, ws1, bs1, act=ACT_RELU)
+    ws2 = g.weight(r.kaiming((32, 8, 1, 1), 8))
+    bs2 = g.weight(r.normal((32,), 0.1))
+    gate = g.conv(s1, ws2, bs2, act=ACT_HARDSIGMOID)
+    cat = g.tensor((2, 32 + 32 + 32 + 16, 24, 28))
+    g.mul_add_scale(d, gate, a, out=cat, y_ctotal=112, y_coff=0)
+    g.pool(a, (2, 2), (1, 1), (0, 0, 1, 1), True, out=cat, y_ctotal=112, y_coff=32)
+    small = g.pool(a, (2, 2), (2, 2), (0, 0, 0, 0), False)
+    g.resize(small, 24, 28, bilinear=True, out=cat, y_ctotal=112, y_coff=64)
+    g.copy_slot(0, cat, 112, 96)
+    t = g.transpose(cat, (0, 2, 3, 1))
+    g.outputs = [cat, t]
+    sess = nets.HipSession(g)
+    outs = sess.run(x)
+    refs = onets.run_graph(g, x)
+    assert_bitexact(outs[0], refs[0], "concat tensor")
+    assert_bitexact(outs[1], refs[1], "transposed")
+    sess.close()

@@ -116,6 +116,26 @@ def test_rec_pairs_only_and_deferred_runs(gpu, oracle):
     sess.close()
 
 
+@pytest.mark.parametrize("batch,width", [(32, 320), (5, 160), (19, 480)])
+def test_rec_fused_head(gpu, oracle, batch, width):
+    """The rec graph with QPH_NET_FUSED_HEAD (head GEMM + softmax argmax in
+    one kernel, logits never stored) against the oracle's full graph under
+    the target's rule; every node before the head is bit-exact already."""
+    from conftest import pairs_tolerance_check
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    g, x = nets.build_rec(3, batch, width, fused_head=True)
+    print(f"rec {batch}x3x48x{width} fused head", flush=True)
+    sess = nets.HipSession(g)
+    (pairs,) = sess.run(x)
+    outs, T = onets.run_graph(g, x, keep=True)
+    logits = T[g.nodes[-2]["out"]]
+    pairs_tolerance_check(pairs, outs[0], logits)
+    (pairs2,) = sess.run(x)
+    assert_bitexact(pairs2, pairs, "fused head replay")
+    sess.close()
+
+
 def test_cfg5_mixed_page(gpu, oracle):
     """det 1536^2 + 128 rec lines in width buckets, CTC masked past w/8:
     det map and every batch's pairs bit-exact with the oracle, and each

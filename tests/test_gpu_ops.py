@@ -348,6 +348,38 @@ def test_softmax_argmax_and_ties(gpu, oracle):
     assert ids[3] == 50 and ids[5] == 0 and ids[7] == 18708
 
 
+@pytest.mark.parametrize("shape", [(1280, 256, 18709), (100, 256, 18709), (37, 64, 1001),
+                                   (130, 32, 70)], ids=lambda s: "x".join(map(str, s)))
+def test_linear_softmax_argmax_fused(gpu, oracle, shape):
+    """The fused head (GEMM + softmax + argmax, logits never stored) against
+    the oracle's MatMul, Add, Softmax, argmax under the target's rule:
+    values within 1e-4, ids equal except at top-2 logit gaps below 1e-4.
+    Planted exact ties and a maximum in the last, partial column block."""
+    torch = gpu
+    from conftest import pairs_tolerance_check
+    from qppocr_amd import ops
+    rows, k, n = shape
+    rng = np.random.default_rng(rows + n)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    w = (rng.standard_normal((k, n)) * math.sqrt(2 / k)).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    x[2] = 0.0                   # row 2: every logit is its bias, and
+    w[:, 3] = w[:, n // 2] = 0.0
+    b[3] = b[n // 2] = 60.0      # ... two equal maxima: the first wins
+    x[1] = 0.0                   # row 1: the max in the last, partial column block
+    x[1, 0] = 1.0
+    w[0, n - 1] = 100.0
+    logits = oracle.binary_bcast(oracle.matmul(x, w), b, rows, n, 0, 1)
+    ref = oracle.ctc_argmax(oracle.softmax_last_dim(logits.copy(), n))
+    pairs = _n(ops.linear_softmax_argmax(_t(torch, x), _t(torch, w), _t(torch, b)))
+    nd = pairs_tolerance_check(pairs, ref, logits)
+    ids = pairs[:, 1].copy().view(np.uint32)
+    assert ids[2] == 3 and ids[1] == n - 1
+    assert nd <= max(1, rows // 100)
+    rel = np.abs(pairs[:, 0].astype(np.float64) - ref[:, 0]) / np.abs(ref[:, 0])
+    assert rel.max() < 1e-5, rel.max()
+
+
 @pytest.mark.parametrize("cols", [18709, 19500, 40000, 7])
 def test_softmax_argmax_pairs_only(gpu, oracle, cols):
     """probs = NULL: pairs only (rec_argmax_pairs, device.rs:160-165), the

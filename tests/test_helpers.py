@@ -18,3 +18,21 @@ def test_bitexact_helper():
     assert_bitexact(np.array([0.0, np.nan, 1.0], np.float32), np.array([-0.0, np.nan, 1.0], np.float32))
     with pytest.raises(BaseException):
         assert_bitexact(np.array([1.0], np.float32), np.array([np.nextafter(np.float32(1), 2)]))
+
+
+def test_pairs_tolerance_helper():
+    """ids may differ only at near-ties of the logits; values within 1e-4."""
+    from conftest import pairs_tolerance_check
+
+    def pr(vals, ids):
+        p = np.zeros((len(vals), 2), np.float32)
+        p[:, 0] = vals
+        p[:, 1] = np.array(ids, np.uint32).view(np.float32)
+        return p
+    logits = np.array([[0.0, 5.0, 5.0 - 1e-6], [3.0, 1.0, 0.0]], np.float32)
+    ref = pr([0.5, 0.8], [1, 0])
+    assert pairs_tolerance_check(pr([0.50001, 0.8], [2, 0]), ref, logits) == 1
+    with pytest.raises(AssertionError):
+        pairs_tolerance_check(pr([0.5, 0.8], [1, 1]), ref, logits)    # gap 2: not a tie
+    with pytest.raises(AssertionError):
+        pairs_tolerance_check(pr([0.51, 0.8], [1, 0]), ref, logits)   # value off by 2%

@@ -515,3 +515,168 @@ def test_gemm_tiles_match_scalar_form(oracle):
         p = oracle.conv_params(s, s, k // 2, k // 2, group=g)
         x, y = both(lambda: oracle.conv2d(xin, w, bias, p, oracle.ACT_RELU))
         assert (x == y).all(), (c, m, k, s, g)
+
+
+# ---------------------------------------- pooling / SE / resize / pre-post
+
+def test_pool_and_resize_reference_cases(oracle):
+    """The reference's pool_and_resize_tests (kernels.rs:1143-1258) on its
+    own xorshift data: 2x2 s1 SAME_UPPER max pool against the clamped
+    brute force (exact), 3x3 s2 p1 avg pool against f64 / 9 (1e-5), global
+    average pool against the f64 sum in order (exact), bilinear 33 x 47 in
+    both coordinate modes against f64 (1e-4)."""
+    rng = XorShift(int(GOLD["rng"]["kernels_seed"], 16))
+    n, c, h, w = 2, 3, 20, 30
+    x = rng.fill((n, c, h, w))
+    y = oracle.pool2d(x, 2, 2, 1, 1, 0, 0, 1, 1, True)
+    assert y.shape == (n, c, h, w)
+    iy = np.minimum(np.arange(h)[:, None] + np.array([0, 1])[None], h - 1)
+    ix = np.minimum(np.arange(w)[:, None] + np.array([0, 1])[None], w - 1)
+    want = np.maximum.reduce([x[:, :, iy[:, a]][:, :, :, ix[:, b]] for a in (0, 1)
+                              for b in (0, 1)])
+    assert (y == want).all()
+    y = oracle.pool2d(x, 3, 3, 2, 2, 1, 1, 1, 1, False)
+    oh, ow = (20 + 2 - 3) // 2 + 1, (30 + 2 - 3) // 2 + 1
+    assert y.shape == (n, c, oh, ow)
+    xp = np.zeros((n, c, h + 2, w + 2))
+    xp[:, :, 1:1 + h, 1:1 + w] = x
+    s = sum(xp[:, :, ky:ky + 2 * oh:2, kx:kx + 2 * ow:2] for ky in range(3) for kx in range(3))
+    assert np.abs(y - (s / 9.0)).max() < 1e-5
+    g = oracle.global_avg_pool(x)
+    for i in range(n * c):
+        acc = 0.0
+        for v in x.reshape(n * c, -1)[i]:
+            acc += float(v)
+        assert g.ravel()[i] == np.float32(acc / (h * w))
+    for align in (False, True):
+        y = oracle.resize_bilinear(x, 33, 47, align)
+
+        def coords(no, ni):
+            i = np.arange(no, dtype=np.float64)
+            v = i * (ni - 1) / (no - 1) if align else np.maximum((i + 0.5) * ni / no - 0.5, 0)
+            i0 = np.clip(np.floor(v), 0, ni - 1).astype(int)
+            return i0, np.minimum(i0 + 1, ni - 1), v - i0
+        y0, y1, fy = coords(33, h)
+        x0, x1, fx = coords(47, w)
+        xd = x.astype(np.float64)
+        fy, fx = fy[:, None], fx[None, :]
+        want = (xd[:, :, y0][:, :, :, x0] * (1 - fx) * (1 - fy) +
+                xd[:, :, y0][:, :, :, x1] * fx * (1 - fy) +
+                xd[:, :, y1][:, :, :, x0] * (1 - fx) * fy + xd[:, :, y1][:, :, :, x1] * fx * fy)
+        assert np.abs(y - want).max() < 1e-4
+
+
+def test_pool_and_bilinear_vs_torch(oracle):
+    """Independent library cross-check: torch's max / avg pooling (padding
+    counted in the average's divisor) and half-pixel bilinear interpolation."""
+    torch = pytest.importorskip("torch")
+    F = torch.nn.functional
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((2, 5, 23, 31)).astype(np.float32)
+    t = torch.from_numpy(x).double()
+    y = oracle.pool2d(x, 3, 3, 2, 2, 1, 1, 1, 1, True)
+    assert (y == F.max_pool2d(t, 3, 2, 1).float().numpy()).all()
+    y = oracle.pool2d(x, 2, 2, 2, 2, 0, 0, 0, 0, False)
+    rel_check(y, F.avg_pool2d(t, 2, 2).numpy(), tol=1e-6)
+    y = oracle.pool2d(x, 3, 3, 1, 1, 1, 1, 1, 1, False)
+    rel_check(y, F.avg_pool2d(t, 3, 1, 1, count_include_pad=True).numpy(), tol=1e-6)
+    for oh, ow in [(46, 62), (11, 17), (23, 31)]:
+        y = oracle.resize_bilinear(x, oh, ow)
+        rel_check(y, F.interpolate(t, (oh, ow), mode="bilinear", align_corners=False).numpy(),
+                  tol=1e-5)
+    y = oracle.resize_bilinear(x, 40, 50, True)
+    rel_check(y, F.interpolate(t, (40, 50), mode="bilinear", align_corners=True).numpy(), tol=1e-5)
+
+
+def test_mul_add_scale_and_transpose(oracle):
+    """f * gate + r with the Mul and Add each rounded (elementwise.rs:134-179):
+    numpy float32 does exactly that; a fused multiply-add differs on this data."""
+    rng = np.random.default_rng(42)
+    f = rng.standard_normal((2, 6, 7, 9)).astype(np.float32)
+    gate = rng.random(6).astype(np.float32)
+    r = rng.standard_normal(f.shape).astype(np.float32)
+    out = oracle.mul_add_scale(f, gate, r)
+    want = f * gate[None, :, None, None] + r
+    assert (out == want).all()
+    fused = (f.astype(np.float64) * gate[None, :, None, None] + r).astype(np.float32)
+    assert (fused != want).any()
+    x = rng.standard_normal((2, 3, 4, 5)).astype(np.float32)
+    for perm in [(0, 2, 3, 1), (0, 3, 1, 2), (3, 2, 1, 0), (0, 1, 2, 3)]:
+        assert (oracle.transpose4(x, perm) == x.transpose(perm)).all()
+
+
+def _fma_f32(a, b, c):
+    """fma on float32 inputs via float64: exact here (u8 x weight products
+    and their sums fit 53 bits), then one rounding to float32."""
+    return (a.astype(np.float64) * b + c).astype(np.float32)
+
+
+def _resize_u8_restated(src, dw, dh):
+    """The scalar formula of the reference's resize test (rsz_par.rs:6-41)."""
+    sh, sw = src.shape[:2]
+    sx, sy = np.float32(sw) / np.float32(dw), np.float32(sh) / np.float32(dh)
+
+    def axis(n_out, n_in, s):
+        v = np.maximum((np.arange(n_out, dtype=np.float32) + np.float32(0.5)) * s - np.float32(0.5),
+                       np.float32(0))
+        i0 = np.minimum(v.astype(np.int64), n_in - 1)
+        return i0, np.minimum(i0 + 1, n_in - 1), (v - i0.astype(np.float32)).astype(np.float32)
+    x0, x1, fx = axis(dw, sw, sx)
+    y0, y1, fy = axis(dh, sh, sy)
+    s = src.astype(np.float32)
+    lx, ly = fx[None, :, None], fy[:, None, None]
+    one = np.float32(1)
+    p00, p01 = s[y0][:, x0], s[y0][:, x1]
+    p10, p11 = s[y1][:, x0], s[y1][:, x1]
+    t = (p00 * (one - lx)) * (one - ly)
+    t = _fma_f32(p01 * lx, one - ly, t)
+    t = _fma_f32(p10 * (one - lx), ly, t)
+    v = _fma_f32(p11 * lx, ly, t) + np.float32(0.5)
+    return np.clip(v, 0, 255).astype(np.uint8)
+
+
+def test_resize_rgb_u8_and_pack_crop(oracle):
+    """u8 bilinear resize against the reference test's scalar formula on its
+    source pattern (rsz_par.rs:42-52), then pack_crop (crop.rs:153-190):
+    width ceil(img_h * w / h) clamped to img_w, (u8 / 255 - 0.5) / 0.5 by
+    true divisions, zeros past the resized width; and the pad_only branch."""
+    sw, sh = 848, 816
+    src = (np.arange(sw * sh * 3, dtype=np.int64) * 7919 % 256).astype(np.uint8).reshape(sh, sw, 3)
+    for dw, dh in [(400, 48), (17, 33), (832, 832)]:
+        assert (oracle.resize_bilinear_rgb_u8(src, dw, dh) == _resize_u8_restated(src, dw, dh)).all()
+    crop = src[100:154, 20:330]                     # 54 x 310
+    dst = oracle.pack_crop(crop, 48, 320)
+    rw = min(int(np.ceil(np.float32(48) * (np.float32(310) / np.float32(54)))), 320)
+    assert rw == 276
+    r = _resize_u8_restated(crop, rw, 48).astype(np.float32)
+    want = (r / np.float32(255) - np.float32(0.5)) / np.float32(0.5)
+    assert (dst[:, :, :rw] == want.transpose(2, 0, 1)).all()
+    assert (dst[:, :, rw:] == 0).all()
+    crop = src[:40, :500]
+    dst = oracle.pack_crop(crop, 48, 320, pad_only=True)
+    v = (crop[:, :320].astype(np.float32) / np.float32(255) - np.float32(0.5)) / np.float32(0.5)
+    assert (dst[:, 4:44, :] == v.transpose(2, 0, 1)).all()
+    assert (dst[:, :4] == 0).all() and (dst[:, 44:] == 0).all()
+
+
+def test_det_normalize_and_db_mask(oracle):
+    """det input normalisation (engine.rs:959-982) in float32 steps; DB
+    threshold + 2x2 dilation against the reference test's brute force
+    (rsz_par.rs:55-84) on its mask pattern, thresholded at 0.5."""
+    rng = np.random.default_rng(43)
+    rgb = rng.integers(0, 256, (37, 53, 3)).astype(np.uint8)
+    got = oracle.det_normalize(rgb)
+    v = rgb.astype(np.float32) * (np.float32(1) / np.float32(255))
+    want = ((v - np.float32(0.5)) * (np.float32(1) / np.float32(0.5))).transpose(2, 0, 1)[None]
+    assert (got == want).all()
+    for h, w in [(37, 129), (1, 1), (5, 300), (300, 5), (832, 832)]:
+        i = np.arange(h * w, dtype=np.uint64)
+        mask = (((i * np.uint64(2654435761)) >> np.uint64(24)) % np.uint64(256)).astype(np.uint8) % 3
+        pred = mask.reshape(h, w).astype(np.float32)
+        binm = (pred > 0.5).astype(np.uint8)
+        want = binm.copy()
+        want[1:] = np.maximum(want[1:], binm[:-1])
+        want2 = want.copy()
+        want2[:, 1:] = np.maximum(want[:, 1:], want[:, :-1])
+        assert (oracle.db_mask(pred, 0.5) == want2).all(), (h, w)
+        assert (oracle.db_mask(pred, 0.5, dilate=False) == binm).all()
