@@ -245,7 +245,7 @@ def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
         out = {"workload": f"depthwise {k}x{k} s{s} pad {k // 2} C{c} {hw}x{hw} + hardswish",
                "us": round(us, 3), "gbs": round(gbs, 1), "bound": "hbm",
                "frac": round(gbs / PEAK_HBM_GBS, 4), "mb": round(by / 1e6, 3),
-               "kernel": f"depthwise_kernel<{k},{k}>",
+               "kernel": f"depthwise_wave_kernel<{k},{k}>",
                "method": f"cache-cold: HIP events over {replays} graph replays of {ob.R} copies "
                          f"on rotating buffer sets ({ob.R * set_bytes >> 20} MB)"}
         if O is not None:

@@ -1095,7 +1095,184 @@ __global__ __launch_bounds__(256) void depthwise_kernel(DwK p) {
   }
 }
 
+// Tiled depthwise (the HBM-bound NCHW form: cfg-style planes, no residual,
+// no upsampled store).  A workgroup is nw waves and one tile of TH x TW
+// outputs of a plane; thread t computes PX consecutive outputs of tile row
+// t / TPR (TPR = ceil(TW / PX) threads a row, TH = nw * (64 / TPR) rows).
+// The tile's input halo (rt x ct floats, zero where it falls outside the
+// image) arrives in LDS by buffer->LDS loads, all issued before one wait:
+// thread T of load round k brings halo element 64 nw k + T, out-of-image
+// elements carry an offset past the buffer and read 0.  Each output keeps the reference chain acc = fma(w, x, acc)
+// over ky then kx from 0, + bias, then the activation; its PX outputs share
+// the KH halo rows read once from LDS.  AK: 3 = HardSigmoid + Mul inline, 0
+// none, -1 any kind through act_apply.
+struct DwWaveK {
+  const float* x;
+  const float* w;
+  const float* bias;
+  float* y;
+  int c, h, w_, sh, ph, pw, oh, ow;
+  int th, tw, tpr, rt, ct, tiles_x;
+  int64_t y_ctotal, y_coff;
+  Act act;
+  int vec4;     // 16-byte aligned output rows (float4 stores when PX == 4)
+};
+
+template <int KH, int KW, int SW, int PX, int AK>
+__global__ __launch_bounds__(256) void depthwise_wave_kernel(DwWaveK p) {
+  extern __shared__ float halo[];
+  constexpr int NC = (PX - 1) * SW + KW;   // halo columns one thread reads per row
+  const int lane = threadIdx.x;            // thread of the workgroup
+  const int nthr = blockDim.x;
+  const int64_t plane = blockIdx.y;         // n * c + ch
+  const int ch = (int)(plane % p.c);
+  const int tyb = (int)blockIdx.x / p.tiles_x, txb = (int)blockIdx.x - tyb * p.tiles_x;
+  const int oy0 = tyb * p.th, ox0 = txb * p.tw;
+  const int iy0 = oy0 * p.sh - p.ph, ix0 = ox0 * SW - p.pw;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + plane * p.h * p.w_), 0, p.h * p.w_ * 4, 0x00020000);
+  const int nh = p.rt * p.ct;
+  const int wbase = lane & ~63;            // this wave's first thread
+  for (int e0 = wbase; e0 < nh; e0 += nthr) {
+    const int e = e0 + (lane & 63);
+    const int ry = e / p.ct, rx = e - ry * p.ct;
+    const int iy = iy0 + ry, ix = ix0 + rx;
+    const unsigned off = (e < nh && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w_)
+                             ? (unsigned)(iy * p.w_ + ix) * 4u
+                             : 0x80000000u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        xr, (__attribute__((address_space(3))) void*)(halo + e0), 4, off, 0, 0, 0);
+  }
+  float wr[KH * KW];
+#pragma unroll
+  for (int i = 0; i < KH * KW; i++) wr[i] = p.w[ch * KH * KW + i];
+  const float bv = p.bias ? p.bias[ch] : 0.0f;
+  __builtin_amdgcn_s_waitcnt(0);   // vmcnt(0), lgkmcnt(0): this wave's part is in LDS
+  __asm__ volatile("" ::: "memory");
+  if (nthr > 64) __syncthreads();   // and every other wave's
+  const int py = lane / p.tpr, g = lane - py * p.tpr;
+  const int oy = oy0 + py, oxs = ox0 + g * PX;
+  if (py >= p.th || oy >= p.oh || oxs >= p.ow) return;
+  float acc[PX];
+#pragma unroll
+  for (int i = 0; i < PX; i++) acc[i] = 0.0f;
+  const float* hb = halo + py * p.sh * p.ct + g * PX * SW;
+#pragma unroll
+  for (int ky = 0; ky < KH; ky++) {
+    float xv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) xv[j] = hb[ky * p.ct + j];
+#pragma unroll
+    for (int kx = 0; kx < KW; kx++)
+#pragma unroll
+      for (int i = 0; i < PX; i++) acc[i] = __builtin_fmaf(wr[ky * KW + kx], xv[i * SW + kx], acc[i]);
+  }
+  float out[PX];
+#pragma unroll
+  for (int i = 0; i < PX; i++) {
+    float v = acc[i] + bv;
+    if constexpr (AK == 3)
+      v = v * hsig1(v, p.act.c1, p.act.c2);
+    else if constexpr (AK < 0)
+      v = act_apply(v, p.act);
+    out[i] = v;
+  }
+  const int64_t bn = plane / p.c;
+  float* yr = p.y + ((bn * p.y_ctotal + p.y_coff + ch) * p.oh + oy) * (int64_t)p.ow;
+  if (PX == 4 && p.vec4 && oxs + 4 <= p.ow) {
+    *(float4*)(yr + oxs) = make_float4(out[0], out[1], out[2], out[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < PX; i++)
+      if (oxs + i < p.ow) yr[oxs + i] = out[i];
+  }
+}
+
+template <int KH, int KW, int SW, int PX>
+static void launch_dw_wave_ak(const DwWaveK& p, dim3 grid, int nthr, size_t lds, hipStream_t s) {
+  if (p.act.kind == 3)
+    hipLaunchKernelGGL((depthwise_wave_kernel<KH, KW, SW, PX, 3>), grid, dim3(nthr), lds, s, p);
+  else if (p.act.kind == 0)
+    hipLaunchKernelGGL((depthwise_wave_kernel<KH, KW, SW, PX, 0>), grid, dim3(nthr), lds, s, p);
+  else
+    hipLaunchKernelGGL((depthwise_wave_kernel<KH, KW, SW, PX, -1>), grid, dim3(nthr), lds, s, p);
+}
+
+template <int KH, int KW, int SW>
+static void launch_dw_wave_px(const DwWaveK& p, int px, dim3 grid, int nthr, size_t lds,
+                              hipStream_t s) {
+  if (px == 4)
+    launch_dw_wave_ak<KH, KW, SW, 4>(p, grid, nthr, lds, s);
+  else if (px == 2)
+    launch_dw_wave_ak<KH, KW, SW, 2>(p, grid, nthr, lds, s);
+  else
+    launch_dw_wave_ak<KH, KW, SW, 1>(p, grid, nthr, lds, s);
+}
+
+// The one-wave form takes 3x3 and 5x5 kernels, x-stride 1 or 2, plain or
+// channel-slice outputs without residual or upsampling, offsets in 32 bits.
+static bool dw_wave_eligible(const ConvArgs& a) {
+  return ((a.kh == 3 && a.kw == 3) || (a.kh == 5 && a.kw == 5)) && (a.sw == 1 || a.sw == 2) &&
+         !a.res && a.y_up == 1 && a.h * a.w * 4 < (1ll << 31) && a.oh < (1 << 20) &&
+         a.ow < (1 << 20) && a.n * a.c <= 65535;
+}
+
+static int launch_depthwise_wave(const ConvArgs& a, hipStream_t s) {
+  DwWaveK p{};
+  p.x = a.x; p.w = a.wt; p.bias = a.bias; p.y = a.y;
+  p.c = (int)a.c; p.h = (int)a.h; p.w_ = (int)a.w; p.sh = (int)a.sh; p.ph = (int)a.ph;
+  p.pw = (int)a.pw; p.oh = (int)a.oh; p.ow = (int)a.ow;
+  p.y_ctotal = a.y_ctotal; p.y_coff = a.y_coff;
+  p.act = a.act;
+  const int64_t planes = a.n * a.c;
+  // outputs per thread: the most that still leave >= 1024 waves (four per
+  // CU) to hide the load latency behind; then waves per workgroup, where
+  // >= 4096 waves remain (larger workgroups share their halo rows; on
+  // smaller grids the barrier costs more than the shared rows save)
+  int px = 1, nw = 1;
+  auto waves_of = [&](int cand, int w) {
+    const int tw = (int)std::min<int64_t>(a.ow, 16 * cand);
+    const int tpr = (tw + cand - 1) / cand;
+    const int th = w * (64 / tpr);
+    const int64_t tiles = planes * ceil_div(a.ow, tw) * ceil_div(a.oh, th);
+    return tiles * std::min<int64_t>(w, ceil_div((int64_t)std::min<int64_t>(th, a.oh) * tpr, 64));
+  };
+  for (int cand : {4, 2})
+    if (waves_of(cand, 1) >= 1024) {
+      px = cand;
+      break;
+    }
+  for (int w : {4, 2})
+    if (waves_of(px, w) >= 4096 && w * (64 / ((std::min<int64_t>(a.ow, 16 * px) + px - 1) / px)) <= a.oh) {
+      nw = w;
+      break;
+    }
+  p.tw = (int)std::min<int64_t>(a.ow, 16 * px);
+  p.tpr = (p.tw + px - 1) / px;
+  p.th = nw * (64 / p.tpr);
+  if (p.th > p.oh) p.th = p.oh;
+  p.rt = (p.th - 1) * p.sh + (int)a.kh;
+  p.ct = (p.tw - 1) * (int)a.sw + (int)a.kw;
+  p.tiles_x = (int)ceil_div(a.ow, p.tw);
+  p.vec4 = (a.ow % 4 == 0) && ((uintptr_t)a.y % 16 == 0);
+  const int64_t tiles = (int64_t)p.tiles_x * ceil_div(a.oh, p.th);
+  // (+64: the last lanes of a row group whose PX outputs run past a narrow
+  // tile read up to (PX - 1) * SW floats past the halo, for outputs they
+  // never store)
+  const size_t lds = (size_t)((p.rt * p.ct + 63) / 64 * 64 + 64) * 4;
+  if (tiles >= (1ll << 31) || lds > 64 * 1024)
+    return fail(QPH_EUNSUPPORTED, "depthwise: tile outside the one-wave kernel");
+  dim3 grid((unsigned)tiles, (unsigned)planes);
+  const int k = (int)a.kh, nthr = 64 * nw;
+  if (k == 3 && a.sw == 1) launch_dw_wave_px<3, 3, 1>(p, px, grid, nthr, lds, s);
+  else if (k == 3) launch_dw_wave_px<3, 3, 2>(p, px, grid, nthr, lds, s);
+  else if (a.sw == 1) launch_dw_wave_px<5, 5, 1>(p, px, grid, nthr, lds, s);
+  else launch_dw_wave_px<5, 5, 2>(p, px, grid, nthr, lds, s);
+  return launch_check("depthwise_wave_kernel");
+}
+
 int launch_depthwise(const ConvArgs& a, hipStream_t s) {
+  if (dw_wave_eligible(a)) return launch_depthwise_wave(a, s);
   DwK p{};
   p.x = a.x; p.w = a.wt; p.bias = a.bias; p.res = a.res; p.y = a.y;
   p.c = a.c; p.h = a.h; p.w_ = a.w; p.kh = a.kh; p.kw = a.kw; p.sh = a.sh; p.sw = a.sw;

@@ -135,6 +135,36 @@ def test_conv3x3_placed_output(gpu, oracle):
     assert_bitexact(_n(out), ref, "concat slots")
 
 
+# Depthwise convs at the shapes of the depthwise workloads (3x3 / 5x5, stride
+# 1 / 2, + hardswish) and two ragged planes large enough for the tiled kernel
+# to take four-wave workgroups (partial last tile in both directions).
+DW_CASES = [
+    ("dw3 s1 C64 160", 64, 160, 160, 3, 1),
+    ("dw3 s2 C128 80", 128, 80, 80, 3, 2),
+    ("dw5 s1 C256 40", 256, 40, 40, 5, 1),
+    ("dw5 s2 C256 40", 256, 40, 40, 5, 2),
+    ("dw3 s1 C64 130x150 (4 waves)", 64, 130, 150, 3, 1),
+    ("dw5 s2 C256 120 (4 waves)", 256, 120, 120, 5, 2),
+    ("dw3 s2 C8 9x300", 8, 9, 300, 3, 2),
+]
+
+
+@pytest.mark.parametrize("case", DW_CASES, ids=[c[0] for c in DW_CASES])
+def test_depthwise_shapes(gpu, oracle, case):
+    torch = gpu
+    from qppocr_amd import ops
+    name, c, h, w, k, s = case
+    rng = np.random.default_rng(_seed(name))
+    x = rng.uniform(-1, 1, (1, c, h, w)).astype(np.float32)
+    wt = rng.uniform(-1, 1, (c, 1, k, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (c,)).astype(np.float32)
+    y_ref = oracle.conv2d(x, wt, b, oracle.conv_params(s, s, k // 2, k // 2, group=c))
+    y_ref = oracle.binary_flat(y_ref, oracle.hardsigmoid(y_ref), 2)
+    y = ops.conv2d(_t(torch, x), _t(torch, wt), _t(torch, b),
+                   ops.conv_params(s, s, k // 2, k // 2, group=c), 3)
+    assert_bitexact(_n(y), y_ref, name)
+
+
 # 3x3 convs on the direct kernel: each per-wave tile shape (16/32 channels x
 # 16/32 pixels), a channel count that ends inside a group of four, M with a
 # partial last block and a bias-seeded M%4 tail (partial 32-column panel),
