@@ -519,37 +519,54 @@ __global__ __launch_bounds__(256) void conv3x3_direct_group_kernel(DirectConvGro
 // w / 2 from column 16 (w % 2), both 16-channel blocks of M.  K advances in
 // chunks of 8 input channels (72 k = 18 steps) through a ring of three LDS
 // stages, two chunks in flight while one is multiplied: the chunk's input
-// halo (8 x 4 rows x 34 columns, out-of-image words read 0 = the zero
-// padding) and its 72 weight rows of the k-major repack (32 floats each,
-// 16-float halves swapped on rows with k & 2 so that the four k rows of one
-// step hit distinct banks) arrive by buffer->LDS loads, 14 per wave per
-// chunk, so each wait counts exactly the chunks still loading.  Each direct3x3_unit step costs two vector-memory
-// loads per lane; here a step is three LDS reads and two MFMAs.
+// halo (8 x 4 rows x 40 columns from column ox0 - 4, out-of-image words read
+// 0 = the zero padding) and its 72 weight rows of the k-major repack (32
+// floats each, 16-float halves swapped on rows with k & 2 so that the four k
+// rows of one step hit distinct banks) arrive by 16-byte buffer->LDS loads:
+// 5 for the halo, 9 for the weights and 2 spare ones (out of range, into a
+// spare area) so that every wave issues exactly 4 a chunk and each wait
+// counts exactly the chunks still loading.  The image width is a multiple of
+// 4, so a 16-byte halo group lies wholly inside or wholly outside a row.
+// Each direct3x3_unit step costs two vector-memory loads per lane; here a
+// step is three LDS reads and two MFMAs.
 
 #define LC_CC 8                         // input channels per chunk
-#define LC_HP 34                        // halo row pitch (32 + 2 columns)
-#define LC_HALO 1280                    // 8 x 4 x 34 = 1088 floats, in 20 loads
+#define LC_HP 40                        // halo row pitch (4 + 32 + 4 columns)
+#define LC_HG 10                        // 16-byte groups per halo row
+#define LC_HALO (LC_CC * 4 * LC_HP)     // 1280 floats: 5 loads of 64 groups
 #define LC_NST 3                        // ring stages
 #define LC_WROWS (LC_CC * 9)            // 72 weight rows per chunk
-#define LC_W (LC_WROWS * 32)            // 2304 floats
-#define LC_STAGE (LC_HALO + LC_W)
-#define LC_HL (LC_HALO / 64)            // 20 halo loads per chunk (5 a wave)
-#define LC_WL (LC_W / 64)               // 36 weight loads per chunk
+#define LC_W (LC_WROWS * 32)            // 2304 floats: 9 loads
+#define LC_SPARE 512                    // 2 loads' worth of spare words
+#define LC_STAGE (LC_HALO + LC_W + LC_SPARE)
+#define LC_DMA (LC_STAGE / 256)         // 16 loads per chunk, 4 per wave
+#define LC_LEAD 6                       // steps the operand reads run ahead
 
 struct LdsConvGroup {
   DirectConvK k[DIRECT_GROUP_MAX];
   int tiles_x[DIRECT_GROUP_MAX];
-  int start[DIRECT_GROUP_MAX + 1];
+  int start[DIRECT_GROUP_MAX + 1];   // start[i] = total for i >= n
   int n;
 };
 
 // The ring stages are three __shared__ arrays of their own, picked at compile
 // time (the chunk loop is unrolled over the ring): that is what lets the
 // compiler tell the loads into one stage from the reads of another and place
-// no wait of its own before the operand reads.
+// no wait of its own before the operand reads.  The fixed costs around the
+// chunk loop are kept short: the first two chunks' loads go out before
+// anything else is read (bias terms included), a chunk's operands are all
+// read from LDS before its MFMAs (so the reads' latency is paid once a chunk,
+// not once a step), and AK (0 none, 2 ReLU, -1 any kind through act_apply)
+// keeps the epilogue free of the generic activation switch.
+template <int AK, bool ONE>
 __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x, int tile,
-                                              float* s0, float* s1, float* s2, int wave,
-                                              int lane) {
+                                              float* s0, float* s1, float* s2, float* s3,
+                                              int wave, int lane) {
+  // every parameter the loads depend on, fetched in one batch of scalar
+  // loads (left alone, the compiler fetches them in dependent rounds as the
+  // code first uses them, each round a full kernel-argument load latency)
+  __asm__ volatile("" ::"s"(p.x), "s"(p.wk), "s"(p.c), "s"(p.h), "s"(p.w), "s"(p.oh),
+                   "s"(p.ow), "s"(p.mpad), "s"(tiles_x), "s"(tile));
   const int l16 = lane & 15, lg = lane >> 4;
   const int per_img = tiles_x * ((p.oh + 1) / 2);
   const int img = tile / per_img, rem = tile - img * per_img;
@@ -560,74 +577,106 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
   const int poy = oy0 + r, pox = ox0 + c;
   const bool pval = poy < p.oh && pox < p.ow;
 
-  // chunk-invariant load offsets: halo word f = 64 q + lane of this wave's
-  // loads q = wave, wave + 4, ... (channel part in the scalar offset)
-  unsigned hoff[LC_HL / 4], woff[LC_WL / 4];
+  // chunk-invariant load offsets: load j = wave + 4 q of the chunk brings
+  // the 16-byte groups 64 j + lane of the stage (halo groups, then weight
+  // groups, then spare ones); the channel / weight-row part of the address
+  // is the scalar offset
+  unsigned doff[4];
 #pragma unroll
-  for (int j = 0; j < LC_HL / 4; j++) {
-    const int f = 64 * (wave + 4 * j) + lane;
-    const int cl = f / (4 * LC_HP), rr = (f / LC_HP) % 4, cc = f % LC_HP;
-    const int iy = oy0 - 1 + rr, ix = ox0 - 1 + cc;
-    const bool ok = f < LC_CC * 4 * LC_HP && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
-    hoff[j] = ok ? (unsigned)((cl * HW + iy * p.w + ix) * 4) : OOB;
-  }
-#pragma unroll
-  for (int j = 0; j < LC_WL / 4; j++) {
-    const int f = 64 * (wave + 4 * j) + lane;
-    const int kr = f >> 5, mc = (f & 31) ^ (((kr >> 1) & 1) << 4);
-    woff[j] = (unsigned)((kr * p.mpad + mc) * 4);
+  for (int q = 0; q < 4; q++) {
+    const int gi = 64 * (wave + 4 * q) + lane;
+    if (gi < LC_HALO / 4) {
+      const int cl = gi / (4 * LC_HG), rem = gi - cl * 4 * LC_HG;
+      const int rr = rem / LC_HG, gc = rem - rr * LC_HG;
+      const int iy = oy0 - 1 + rr, ix = ox0 - 4 + 4 * gc;
+      const bool ok = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+      doff[q] = ok ? (unsigned)((cl * HW + iy * p.w + ix) * 4) : OOB;
+    } else if (gi < (LC_HALO + LC_W) / 4) {
+      const int wg = gi - LC_HALO / 4, kr = wg >> 3;
+      const int mc = (4 * (wg & 7)) ^ (((kr >> 1) & 1) << 4);
+      doff[q] = (unsigned)((kr * p.mpad + mc) * 4);
+    } else {
+      doff[q] = OOB;
+    }
   }
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.x + (int64_t)img * p.c * HW), 0, p.c * HW * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.wk, 0, p.c * 9 * p.mpad * 4, 0x00020000);
+  // The loads are written as inline asm: through the builtin the compiler
+  // sees LDS writes in flight and, unable to tell the stage being refilled
+  // from the one being read, puts a full vmcnt(0) wait before some chunks'
+  // operand reads.  The explicit waits below cover every stage.
+  // per-chunk scalar offsets, as values (a field read inside the loop would
+  // be re-read from the kernel arguments after every compiler fence)
+  const unsigned hstep = __builtin_amdgcn_readfirstlane(LC_CC * HW * 4);
+  const unsigned wstep = __builtin_amdgcn_readfirstlane(LC_WROWS * p.mpad * 4);
   auto issue = [&](int ch, float* st) {
 #pragma unroll
-    for (int j = 0; j < LC_HL / 4; j++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xr, (__attribute__((address_space(3))) void*)(st + 64 * (wave + 4 * j)), 4, hoff[j],
-          ch * LC_CC * HW * 4, 0, 0);
-#pragma unroll
-    for (int j = 0; j < LC_WL / 4; j++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          wr, (__attribute__((address_space(3))) void*)(st + LC_HALO + 64 * (wave + 4 * j)), 4,
-          woff[j], ch * LC_WROWS * p.mpad * 4, 0, 0);
+    for (int q = 0; q < 4; q++) {
+      const int j = wave + 4 * q;   // wave-uniform
+      const bool halo = j < LC_HALO / 256;
+      const unsigned lds = __builtin_amdgcn_readfirstlane(
+          (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)(st + 256 * j));
+      const unsigned soff = ch * (halo ? hstep : wstep);
+      __asm__ volatile(
+          "s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds),
+          "v"(doff[q]), "s"(halo ? xr : wr), "s"(soff)
+          : "m0");
+    }
   };
+  // the bias terms, loaded before the chunks so that the chunk waits below
+  // (which count loads in issue order) never wait for them as well.
+  // The bias: seeded into the chain where the reference seeds (M%4 tail rows
+  // of a partial 32-column panel of the output row), else added after it;
+  // -0.0 (the exact additive identity) where nothing is added
+  float bld[2][4];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = mt * 16 + 4 * lg + v;
+      bld[mt][v] = (p.bias && co < p.m) ? p.bias[co] : 0.0f;
+    }
+
+  __asm__ volatile("" ::: "memory");
+  const int nch = p.c / LC_CC;   // ONE: exactly 4 (C = 32)
+  issue(0, s0);
+  if (ONE || nch > 1) issue(1, s1);
+  if constexpr (ONE) {
+    issue(2, s2);
+    issue(3, s3);
+  }
+  // the bias values are first used here, after every load is out (otherwise
+  // the accumulator set-up can be scheduled between the loads, with a wait
+  // for the bias loads in front of the later ones)
+  __asm__ volatile("" : "+v"(bld[0][0]), "+v"(bld[0][1]), "+v"(bld[0][2]), "+v"(bld[0][3]),
+                   "+v"(bld[1][0]), "+v"(bld[1][1]), "+v"(bld[1][2]), "+v"(bld[1][3])::"memory");
+  const int n0 = (pox >> 5) << 5;
+  const bool tail_panel = (p.ow - n0) < 32;
+  const int mtail = p.m - p.m % 4;
+  float bterm[2][4];
+  f32x4 acc[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = mt * 16 + 4 * lg + v;
+      const bool seeded = p.bias && tail_panel && co >= mtail;
+      acc[mt][v] = seeded ? bld[mt][v] : 0.0f;
+      bterm[mt][v] = (p.bias && !seeded) ? bld[mt][v] : -0.0f;
+    }
+
   // per-step operand offsets inside a stage: k = 4 s + g of the chunk
   int boff[LC_WROWS / 4];
 #pragma unroll
   for (int s = 0; s < LC_WROWS / 4; s++) {
     const int k = 4 * s + lg, cl = k / 9, tap = k - 9 * cl;
     const int ky = tap / 3, kx = tap - 3 * ky;
-    boff[s] = cl * 4 * LC_HP + (r + ky) * LC_HP + c + kx;
+    boff[s] = cl * 4 * LC_HP + (r + ky) * LC_HP + c + kx + 3;
   }
 
-  // accumulators, bias-seeded where the reference seeds
-  f32x4 acc[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      float s0 = 0.0f;
-      const int co = mt * 16 + 4 * lg + v;
-      if (p.bias && co < p.m && pval) {
-        const int n0 = (pox >> 5) << 5;
-        if ((p.ow - n0) < 32 && co >= p.m - p.m % 4) s0 = p.bias[co];
-      }
-      acc[mt][v] = s0;
-    }
-
-  // the epilogue's bias terms, loaded now (latency under the chunk loop)
-  float bterm[2][4];
-#pragma unroll
-  for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const int co = mt * 16 + 4 * lg + v;
-      bterm[mt][v] = (p.bias && co < p.m) ? p.bias[co] : 0.0f;
-    }
-  constexpr int PER = (LC_HL + LC_WL) / 4;   // loads per wave per chunk
-  const int nch = p.c / LC_CC;
+  constexpr int PER = LC_DMA / 4;   // loads per wave per chunk
   auto stage = [&](auto st) -> float* {
     constexpr int S = decltype(st)::value;
     if constexpr (S == 0) return s0;
@@ -637,8 +686,35 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, 2>;
-  issue(0, s0);
-  if (nch > 1) issue(1, s1);
+  // one chunk's 36 MFMAs from stage st
+  auto mma = [&](const float* st) {
+    const float* wst = st + LC_HALO;
+    float av[LC_WROWS / 4][2], bv[LC_WROWS / 4];
+#pragma unroll
+    for (int s = 0; s < LC_WROWS / 4; s++) {
+      const int k = 4 * s + lg;
+      bv[s] = st[boff[s]];
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++)
+        av[s][mt] = wst[k * 32 + ((mt * 16 + l16) ^ (((k >> 1) & 1) << 4))];
+    }
+#pragma unroll
+    for (int s = 0; s < LC_WROWS / 4; s++)
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++)
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s][mt], bv[s], acc[mt], 0, 0, 0);
+    // schedule: the operand reads of the first LC_LEAD steps, then each step's
+    // two MFMAs followed by the reads of the step LC_LEAD ahead, so that
+    // reads run LC_LEAD steps ahead of their use (left to itself the
+    // scheduler reads each step's operands just before its MFMAs)
+    __builtin_amdgcn_sched_group_barrier(0x100, 3 * LC_LEAD, 0);
+#pragma unroll
+    for (int s = LC_LEAD; s < LC_WROWS / 4; s++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * LC_LEAD, 0);
+  };
   auto body = [&](auto sti, int ch) {
     constexpr int S = decltype(sti)::value;
     // this chunk in (the next one may still load); then a barrier with no
@@ -653,58 +729,95 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
     if (ch + 2 < nch) issue(ch + 2, stage(std::integral_constant<int, (S + 2) % LC_NST>{}));
-    const float* st = stage(sti);
-    const float* wst = st + LC_HALO;
-#pragma unroll
-    for (int s = 0; s < LC_WROWS / 4; s++) {
-      const int k = 4 * s + lg;
-      const float b = st[boff[s]];
-#pragma unroll
-      for (int mt = 0; mt < 2; mt++) {
-        const float a = wst[k * 32 + ((mt * 16 + l16) ^ (((k >> 1) & 1) << 4))];
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[mt], 0, 0, 0);
-      }
-    }
+    mma(stage(sti));
   };
-  for (int ch = 0; ch < nch; ch += LC_NST) {
-    body(S0{}, ch);
-    if (ch + 1 < nch) body(S1{}, ch + 1);
-    if (ch + 2 < nch) body(S2{}, ch + 2);
+  if constexpr (ONE) {
+    // all four chunks loading from the start, each multiplied as soon as
+    // every wave's part of it is in (no stage is refilled, so a barrier only
+    // publishes the chunk)
+    auto arrive = [&](auto left) {
+      wait_vmcnt<decltype(left)::value * PER>();
+      __asm__ volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+      __asm__ volatile("" ::: "memory");
+    };
+    arrive(std::integral_constant<int, 3>{});
+    mma(s0);
+    arrive(std::integral_constant<int, 2>{});
+    mma(s1);
+    arrive(std::integral_constant<int, 1>{});
+    mma(s2);
+    arrive(std::integral_constant<int, 0>{});
+    mma(s3);
+  } else {
+    for (int ch = 0; ch < nch; ch += LC_NST) {
+      body(S0{}, ch);
+      if (ch + 1 < nch) body(S1{}, ch + 1);
+      if (ch + 2 < nch) body(S2{}, ch + 2);
+    }
   }
 
   // epilogue as in direct3x3_unit
+  if (!pval) return;
   const int64_t yoh = (int64_t)p.oh * p.y_up, yow = (int64_t)p.ow * p.y_up;
+  float* ybase = p.y + ((int64_t)img * p.y_ctotal + p.y_coff) * yoh * yow;
+  const float* rbase = p.res ? p.res + ((int64_t)img * p.m * p.oh + poy) * p.ow + pox : nullptr;
 #pragma unroll
   for (int mt = 0; mt < 2; mt++)
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       const int co = mt * 16 + 4 * lg + v;
-      if (!pval || co >= p.m) continue;
-      float xv = acc[mt][v];
-      if (p.bias) {
-        const int n0 = (pox >> 5) << 5;
-        const bool seeded = (p.ow - n0) < 32 && co >= p.m - p.m % 4;
-        if (!seeded) xv = xv + bterm[mt][v];
-      }
-      xv = act_apply(xv, p.act);
-      if (p.res) xv = xv + p.res[(((int64_t)img * p.m + co) * p.oh + poy) * p.ow + pox];
-      float* yb = p.y + (((int64_t)img * p.y_ctotal + p.y_coff + co) * yoh) * yow;
-      store_replicated(yb, yow, poy, pox, (int)p.y_up, xv);
+      if (co >= p.m) continue;
+      float xv = acc[mt][v] + bterm[mt][v];
+      if constexpr (AK == 2)
+        xv = relu1(xv);
+      else if constexpr (AK < 0)
+        xv = act_apply(xv, p.act);
+      if (rbase) xv = xv + rbase[(int64_t)co * p.oh * p.ow];
+      store_replicated(ybase + (int64_t)co * yoh * yow, yow, poy, pox, (int)p.y_up, xv);
     }
 }
 
+template <int AK, int NG>
 __global__ __launch_bounds__(256) void conv3x3_lds_kernel(LdsConvGroup g) {
   __shared__ __attribute__((aligned(16))) float s0[LC_STAGE], s1[LC_STAGE], s2[LC_STAGE];
   const int lane = threadIdx.x & 63;
   // "& 3" bounds the wave index, so that the LDS offsets of the loads and
   // reads have known ranges
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
-  const int t = blockIdx.x;
-  if (t >= g.start[g.n]) return;
-  if (t < g.start[1]) lds_conv_tile(g.k[0], g.tiles_x[0], t, s0, s1, s2, wave, lane);
-  else if (t < g.start[2]) lds_conv_tile(g.k[1], g.tiles_x[1], t - g.start[1], s0, s1, s2, wave, lane);
-  else if (t < g.start[3]) lds_conv_tile(g.k[2], g.tiles_x[2], t - g.start[2], s0, s1, s2, wave, lane);
-  else lds_conv_tile(g.k[3], g.tiles_x[3], t - g.start[3], s0, s1, s2, wave, lane);
+  const int t = blockIdx.x;   // < start[DIRECT_GROUP_MAX]: the grid is the total
+  if constexpr (NG == 1) {
+    lds_conv_tile<AK, false>(g.k[0], g.tiles_x[0], t, s0, s1, s2, nullptr, wave, lane);
+  } else {
+    // the member conv, without branches: start[] is non-decreasing
+    const int i = (t >= g.start[1]) + (t >= g.start[2]) + (t >= g.start[3]);
+    lds_conv_tile<AK, false>(g.k[i], g.tiles_x[i], t - g.start[i], s0, s1, s2, nullptr, wave,
+                             lane);
+  }
+}
+
+// One plain 32-channel conv (no residual, no upsampled store, no activation
+// other than ReLU): the whole input halo and all 288 weight rows of a tile
+// (four chunks, 64 KB with the spare words) are loaded at once, so the waves
+// wait once and meet at one barrier instead of four.  The arguments are
+// scalars, 14 dwords, which the dispatch can preload into SGPRs.
+template <int AK>
+__global__ __launch_bounds__(256) void conv3x3_lds32_kernel(const float* x, const float* wk,
+                                                            const float* bias, float* y, int h,
+                                                            int w, int m, int tiles_x,
+                                                            int y_ctotal, int y_coff) {
+  __shared__ __attribute__((aligned(16))) float st[4 * LC_STAGE];
+  DirectConvK p{};
+  p.x = x; p.wk = wk; p.bias = bias; p.res = nullptr; p.y = y;
+  p.c = 32; p.h = h; p.w = w; p.m = m; p.mpad = 32;
+  p.sh = 1; p.sw = 1; p.ph = 1; p.pw = 1; p.oh = h; p.ow = w;
+  p.y_ctotal = y_ctotal; p.y_coff = y_coff; p.y_up = 1;
+  p.act.kind = AK;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+  lds_conv_tile<AK, true>(p, tiles_x, blockIdx.x, st, st + LC_STAGE, st + 2 * LC_STAGE,
+                          st + 3 * LC_STAGE, wave, lane);
 }
 
 static void direct_params(const ConvArgs& a, const float* wk, DirectConvK& p) {
@@ -729,7 +842,8 @@ bool direct3x3_eligible(const ConvArgs& a) {
 static bool lds3x3_eligible(const ConvArgs& a) {
   return direct3x3_eligible(a) && a.sh == 1 && a.sw == 1 && a.ph == 1 && a.pw == 1 &&
          a.m <= 32 && a.c % LC_CC == 0 && a.c > 0 && mpad_of(a.m) == 32 &&
-         a.c * a.h * a.w * 4 < (int64_t)0x80000000;
+         a.c * a.h * a.w * 4 < (int64_t)0x80000000 && a.w % 4 == 0 &&
+         (uintptr_t)a.x % 16 == 0;
 }
 
 static int launch_lds3x3(const ConvArgs* a, int n, hipStream_t s) {
@@ -744,7 +858,36 @@ static int launch_lds3x3(const ConvArgs* a, int n, hipStream_t s) {
   }
   for (int i = n; i <= DIRECT_GROUP_MAX; i++) g.start[i] = (int)total;
   if (total >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "conv: grid too large");
-  hipLaunchKernelGGL(conv3x3_lds_kernel, dim3((unsigned)total), dim3(256), 0, s, g);
+  int kind = a[0].act.kind;
+  for (int i = 1; i < n; i++)
+    if (a[i].act.kind != kind) kind = -1;
+  const dim3 grid((unsigned)total);
+  if (n == 1 && a[0].c == 32 && (kind == 0 || kind == 2) && !a[0].res && a[0].y_up == 1 &&
+      a[0].y_ctotal < (1ll << 31) && a[0].y_coff < (1ll << 31)) {
+    const DirectConvK& k = g.k[0];
+    if (kind == 0)
+      hipLaunchKernelGGL(conv3x3_lds32_kernel<0>, grid, dim3(256), 0, s, k.x, k.wk, k.bias, k.y,
+                         k.h, k.w, k.m, g.tiles_x[0], (int)k.y_ctotal, (int)k.y_coff);
+    else
+      hipLaunchKernelGGL(conv3x3_lds32_kernel<2>, grid, dim3(256), 0, s, k.x, k.wk, k.bias, k.y,
+                         k.h, k.w, k.m, g.tiles_x[0], (int)k.y_ctotal, (int)k.y_coff);
+    return launch_check("conv3x3_lds32_kernel");
+  }
+  if (n == 1) {
+    if (kind == 0)
+      hipLaunchKernelGGL((conv3x3_lds_kernel<0, 1>), grid, dim3(256), 0, s, g);
+    else if (kind == 2)
+      hipLaunchKernelGGL((conv3x3_lds_kernel<2, 1>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((conv3x3_lds_kernel<-1, 1>), grid, dim3(256), 0, s, g);
+  } else {
+    if (kind == 0)
+      hipLaunchKernelGGL((conv3x3_lds_kernel<0, 4>), grid, dim3(256), 0, s, g);
+    else if (kind == 2)
+      hipLaunchKernelGGL((conv3x3_lds_kernel<2, 4>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((conv3x3_lds_kernel<-1, 4>), grid, dim3(256), 0, s, g);
+  }
   return launch_check("conv3x3_lds_kernel");
 }
 
