@@ -5,9 +5,14 @@ Headline step: one det forward on 1x3x640x640 plus one rec forward on a
 batch of 32 lines of 3x48x320 (the det image and the 32 text lines of one
 page), both as replayed HIP graphs with their inputs already resident in
 HBM.  The rec session ends in the CTC exit of the reference's GPU sessions
-(rec_argmax_pairs, qppocr-core/src/device.rs:160-165): softmax + argmax
-emit the (value, index) pairs the decoder reads; the probability tensor is
-not stored (rec_lines_per_s_with_probs is the same graph exporting it too).
+(rec_argmax_pairs, qppocr-core/src/device.rs:160-165): the (value, index)
+pairs the decoder reads.  In the headline graph the head linear carries the
+softmax + argmax in its epilogue (the fused head: logits never reach HBM;
+values within 1e-4 relative of the reference, ids equal except where a
+step's top-2 logit gap is below 1e-4).  Beside it: rec_lines_per_s_bitexact_
+pairs, the graph with the separate head softmax whose pairs are bit-exact,
+and rec_lines_per_s_with_probs, that graph exporting the probability tensor
+too.
 The det and rec sessions run on two contexts (two streams), as a page
 pipeline runs the det of one page next to the rec of another: value = steps
 per second = det images per second with 32 recognised lines each, over the
@@ -15,12 +20,14 @@ wall time of K steps with both streams busy.  det_img_per_s and
 rec_lines_per_s are the stage-isolated rates (HIP events around each
 session alone, on its own stream).
 
-roofline: the dominant kernel, the rec head GEMM (1280 x 18709 x 256,
-12.26 GFLOP of the step's 20.86).  Its average launch time comes from HIP
-events around each node of the rec graph (eager launches on the session
-stream) over the same number of steps.  traffic (HBM bytes per launch) is
-the calibrated FETCH_SIZE + WRITE_SIZE figure in
-profiles/rec_head_gemm_traffic.md.
+roofline: the dominant kernel, the fused rec head (GEMM 1280 x 18709 x
+256, 12.26 GFLOP of the step's 20.86, with the softmax / argmax epilogue),
+bound by the MFMA pipe.  Its average launch time comes from HIP events
+around each node of the rec graph (eager launches on the session stream)
+over the same number of steps.  traffic (HBM bytes per launch) is the
+calibrated FETCH_SIZE + WRITE_SIZE figure in
+profiles/rec_fused_head_traffic.md.  head_gemm_unfused gives the same
+figures for the plain head GEMM of the bit-exact graph.
 
 configs: the five BASELINE workloads, each with its GPU rate, the roofline
 fraction of its bound and the CPU oracle timed on this host (threads set
@@ -55,10 +62,10 @@ REC_BATCH = 32
 COLD_BYTES = 512 << 20      # buffer sets per op bench: twice the Infinity Cache
 
 
-def head_traffic_bytes():
-    """HBM bytes per launch of the rec head GEMM from the committed counter
+def head_traffic_bytes(name="rec_fused_head_traffic.md"):
+    """HBM bytes per launch of a rec head kernel from its committed counter
     summary, or None when it is absent."""
-    path = os.path.join(ROOT, "profiles", "rec_head_gemm_traffic.md")
+    path = os.path.join(ROOT, "profiles", name)
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch"):
@@ -272,14 +279,14 @@ def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
 
 def time_mixed_page(steps, warmup):
     """det 1x3x1536x1536 + 128 rec lines (widths {80..1280}, buckets of 160,
-    <= 64 lines per batch), inputs resident.  det and the rec batches run on
+    <= 64 lines per batch, fused rec heads), inputs resident.  det and the rec batches run on
     three streams (det; rec batches alternating over two): page_ms is the
     wall time per page over the steps; det_ms / rec_ms are each stage alone."""
     import torch
     from qppocr_amd import ops, pipeline
     det_g, det_x, rw, lines, widths = pipeline.mixed_page(4, 1536, 128)
     ctxs = [ops.new_context(0) for _ in range(3)]
-    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths, contexts=ctxs)
+    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths, contexts=ctxs, fused_head=True)
     page.upload()
     for _ in range(warmup):
         page.run()
@@ -370,7 +377,7 @@ def main():
         del src, dst
 
     det_g, det_x = nets.build_det(2, 640, 640)
-    rec_g, rec_x = nets.build_rec(3, REC_BATCH, 320, probs=False)
+    rec_g, rec_x = nets.build_rec(3, REC_BATCH, 320, fused_head=True)
     det = nets.HipSession(det_g, ctx=ctx)
     rec = nets.HipSession(rec_g, ctx=ctx_rec)
     # inputs resident in HBM: copied once, then every step reuses them
@@ -431,26 +438,30 @@ def main():
     h1 = time.perf_counter()
     host_ms_step = (h1 - h0) * 1e3 / K
 
-    # the rec graph exporting the probability tensor as well, and the rec
-    # graph with the fused head (GEMM + softmax argmax in one kernel)
+    # the rec graph with the separate head softmax (bit-exact pairs), and
+    # that graph exporting the probability tensor as well
     rec_p_g, _ = nets.build_rec(3, REC_BATCH, 320, probs=True)
     rec_p = nets.HipSession(rec_p_g, ctx=ctx_rec)
     rec_p.run(rec_x, outputs=False)
     rec_p.sync()
     rec_p_ms = stage_ms(rec_p, stream_rec)
     rec_p.close()
-    rec_f_g, _ = nets.build_rec(3, REC_BATCH, 320, fused_head=True)
-    rec_f = nets.HipSession(rec_f_g, ctx=ctx_rec)
-    rec_f.run(rec_x, outputs=False)
-    rec_f.sync()
-    rec_f_ms = stage_ms(rec_f, stream_rec)
-    rec_f.set_profiling(True)
+    rec_e_g, _ = nets.build_rec(3, REC_BATCH, 320, probs=False)
+    rec_e = nets.HipSession(rec_e_g, ctx=ctx_rec)
+    rec_e.run(rec_x, outputs=False)
+    rec_e.sync()
+    rec_e_ms = stage_ms(rec_e, stream_rec)
+    rec_e.set_profiling(True)
     for _ in range(K):
-        rec_f.run(None, outputs=False)
-    rec_f.sync()
-    fused_head_ms = rec_f.node_times()[len(rec_f_g.nodes) - 2]
-    rec_f.set_profiling(False)
-    rec_f.close()
+        rec_e.run(None, outputs=False)
+    rec_e.sync()
+    e_node_ms = rec_e.node_times()
+    rec_e.set_profiling(False)
+    rec_e.close()
+    e_head = len(rec_e_g.nodes) - 2
+    unfused = {"kernel": "rec head GEMM 1280x18709x256 (gemm_wave_kernel<1>)",
+               "avg_launch_ms": round(e_node_ms[e_head], 5),
+               "softmax_argmax_ms": round(e_node_ms[e_head + 1], 5)}
 
     # dominant kernel: rec head GEMM, events around each node (eager launches)
     rec.set_profiling(True)
@@ -459,7 +470,7 @@ def main():
     rec.sync()
     node_ms = rec.node_times()
     rec.set_profiling(False)
-    head = len(rec_g.nodes) - 2        # linear 256 -> 18709
+    head = len(rec_g.nodes) - 2        # linear 256 -> 18709 + softmax / argmax
     head_ms = node_ms[head]
     d = rec_g.nodes[head]
     rows = rec_g.numel(d["inp"]) // d["ws"][0]
@@ -496,17 +507,22 @@ def main():
                    "det_gflop": round(det_flops / 1e9, 3), "rec_gflop": round(rec_flops / 1e9, 3)},
         "det_img_per_s": round(1e3 / det_ms, 2),
         "rec_lines_per_s": round(REC_BATCH * 1e3 / rec_ms, 1),
+        "rec_lines_per_s_bitexact_pairs": round(REC_BATCH * 1e3 / rec_e_ms, 1),
         "rec_lines_per_s_with_probs": round(REC_BATCH * 1e3 / rec_p_ms, 1),
-        "rec_lines_per_s_fused_head": round(REC_BATCH * 1e3 / rec_f_ms, 1),
-        "fused_head_ms": round(fused_head_ms, 5),
         "det_ms": round(det_ms, 4),
         "rec_ms": round(rec_ms, 4),
         "serial_ms_per_step": round(det_ms + rec_ms, 4),
         "pcie_inclusive_img_per_s": round(1e3 / host_ms_step, 3),
-        "roofline": {"bound": "mfma", "kernel": "rec head GEMM 1280x18709x256 (gemm_wave_kernel)",
+        "roofline": {"bound": "mfma",
+                     "kernel": "fused rec head: GEMM 1280x18709x256 + softmax/argmax epilogue "
+                               "(gemm_wave_kernel<2> + head_pairs_kernel)",
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": head_traffic_bytes(), "avg_launch_ms": round(head_ms, 5)},
+        "head_gemm_unfused": dict(unfused, **{
+            "frac": round(head_flops / (unfused["avg_launch_ms"] * 1e-3) / 1e12
+                          / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": head_traffic_bytes("rec_head_gemm_traffic.md")}),
     }
 
     O = None
@@ -526,7 +542,7 @@ def main():
     cfgs["cfg3"] = {"workload": "det 1x3x640x640 (seed 2)", "img_per_s": result["det_img_per_s"],
                     "ms": result["det_ms"], "gflop": round(det_flops / 1e9, 3),
                     "classes": class_fractions(nets, det_g, det_node_ms)}
-    cfgs["cfg4"] = {"workload": "rec 32x3x48x320 (seed 3), pairs exit",
+    cfgs["cfg4"] = {"workload": "rec 32x3x48x320 (seed 3), pairs exit (fused head)",
                     "lines_per_s": result["rec_lines_per_s"], "ms": result["rec_ms"],
                     "gflop": round(rec_flops / 1e9, 3),
                     "classes": class_fractions(nets, rec_g, node_ms)}

@@ -619,10 +619,13 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
       const unsigned lds = __builtin_amdgcn_readfirstlane(
           (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)(st + 256 * j));
       const unsigned soff = ch * (halo ? hstep : wstep);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // m0 is reserved; nothing else uses it here
       __asm__ volatile(
           "s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds),
           "v"(doff[q]), "s"(halo ? xr : wr), "s"(soff)
           : "m0");
+#pragma clang diagnostic pop
     }
   };
   // the bias terms, loaded before the chunks so that the chunk waits below

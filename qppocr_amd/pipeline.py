@@ -70,9 +70,12 @@ class PageRunner:
     det graph and every rec batch graph.  contexts (optional): the det runs
     on contexts[0] and the rec batches round-robin on the others (each
     context is one stream, so they run concurrently); by default everything
-    runs on the device's shared context."""
+    runs on the device's shared context.  fused_head: the rec sessions run
+    the head linear with the softmax / argmax in its epilogue (pairs within
+    the 1e-4 tolerance, not bit-exact)."""
 
-    def __init__(self, det_graph, det_input, rec_w, lines, widths, device=0, contexts=None):
+    def __init__(self, det_graph, det_input, rec_w, lines, widths, device=0, contexts=None,
+                 fused_head=False):
         ctxs = list(contexts) if contexts else [None]
         rec_ctxs = ctxs[1:] or ctxs[:1]
         self.det = HipSession(det_graph, device, ctx=ctxs[0])
@@ -81,7 +84,7 @@ class PageRunner:
         self.plan = bucket_plan(self.widths)
         self.rec = []
         for k, (bw, idx) in enumerate(self.plan):
-            g = build_rec_graph(rec_w, len(idx), bw, REC_H, probs=False)
+            g = build_rec_graph(rec_w, len(idx), bw, REC_H, probs=False, fused_head=fused_head)
             sess = HipSession(g, device, ctx=rec_ctxs[k % len(rec_ctxs)])
             self.rec.append((bw, idx, g, sess, pack_lines(lines, idx, bw)))
         self.lib = _lib.load()

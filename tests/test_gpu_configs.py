@@ -165,6 +165,36 @@ def test_cfg5_mixed_page(gpu, oracle):
     page.close()
 
 
+def test_cfg5_mixed_page_fused_head(gpu, oracle):
+    """The mixed page with fused rec heads (the benchmarked form): every
+    batch's pairs under the target's rule against the oracle's full graph,
+    and the decoded lines equal to the oracle's wherever no id changed."""
+    from conftest import pairs_tolerance_check
+    from qppocr_amd import pipeline
+    from oracle import nets as onets
+    det_g, det_x, rw, lines, widths = pipeline.mixed_page(4, 1536, 128)
+    print("cfg5 fused heads: det 1536^2 + 128 lines", flush=True)
+    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths, fused_head=True)
+    page.upload()
+    page.run()
+    page.sync()
+    got = page.rec_pairs()
+    decoded = page.decode()
+    for bw, idx, g, _, x in page.rec:
+        print(f"cfg5 fused rec batch {len(idx)}x{bw}", flush=True)
+        outs, T = onets.run_graph(g, x, keep=True)
+        pairs_ref, logits = outs[-1], T[g.nodes[-2]["out"]]
+        mine = np.stack([got[i] for i in idx])
+        changed = pairs_tolerance_check(mine, pairs_ref, logits)
+        for b, i in enumerate(idx):
+            if (_ids(got[i]) == _ids(pairs_ref[b])).all():
+                t_valid = int(widths[i]) // pipeline.REC_STRIDE
+                ref_ids, _ = oracle.ctc_collapse(pairs_ref[b][:t_valid], t_valid)
+                assert decoded[i][0] == [int(v) for v in ref_ids], f"line {i} ids"
+        print(f"  steps with a near-tie id change: {changed}", flush=True)
+    page.close()
+
+
 def test_session_fusion_rules(gpu, oracle):
     """The session fuses a depthwise conv into the following 1x1 conv only
     when nothing else reads the intermediate: here one block's intermediate
