@@ -126,8 +126,8 @@ def class_fractions(nets, g, node_ms):
 
 def cpu_threads():
     """Threads for the CPU oracle: the host's cores available to this
-    process, capped by OMP_NUM_THREADS when the environment sets it (the
-    GPU box gives one GPU's job a share of the host)."""
+    process, capped by OMP_NUM_THREADS when the environment sets it (a
+    host shared by several GPUs' jobs gives each a share of its cores)."""
     n = len(os.sched_getaffinity(0))
     env = os.environ.get("OMP_NUM_THREADS", "")
     if env.isdigit() and int(env) > 0:
@@ -226,7 +226,7 @@ def bench_cfg1(nets, ops, configs, ctx, replays, cpu_rounds, O):
     out = {"workload": "conv3x3 s1 p1 N=1 32->32 160x160 + bias + ReLU (seed 0)",
            "us": round(us, 3), "tflops": round(tf, 2), "bound": "mfma",
            "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4), "gflop": round(fl / 1e9, 4),
-           "kernel": "conv3x3_lds_kernel<2, 1>",
+           "kernel": "conv3x3_lds32_kernel<2>",
            "method": f"HIP events over {replays} graph replays of {ob.R} back-to-back "
                      f"launches on the same input (device time per launch)",
            "us_cache_cold": round(us_cold, 3),

@@ -188,13 +188,13 @@ QPH_API int qph_softmax_argmax(qph_ctx* ctx, const float* logits, int64_t rows, 
  * epilogue keeps, per row and 64-column block, the logits' max, the first
  * column holding it and the sum of exp1(v - max); a second kernel combines
  * the blocks into pairs[2r] = 1 / sum (the max's probability) and
- * pairs[2r+1] = index as u32 bits.  The logits never reach memory (the fused
- * head of SURVEY's hot-path table; the reference's Metal n_head_argmax,
+ * pairs[2r+1] = index as u32 bits.  The logits never reach memory (no single
+ * reference kernel does this; the reference's Metal n_head_argmax,
  * qppocr-gpu/src/plan.rs:316-340, fuses only Softmax + argmax).  x [rows, k],
  * w [k, n] (ONNX MatMul layout), bias [n] or NULL.  Not bit-identical to
  * qph_linear + qph_softmax_argmax: the exponentials come from the hardware
  * exp2 and the sum is taken per block and rescaled, so values agree to
- * ~1e-6 relative (the target's bar is 1e-4); the index is
+ * ~1e-6 relative (the tolerance of the pairs is 1e-4); the index is
  * the first maximum of the logits, which differs from the first maximum of
  * the rounded probabilities only where two logits lie within a few ulps.
  * Needs k % 16 == 0 and x 16-byte aligned with rows k floats apart. */
@@ -352,14 +352,16 @@ typedef struct qph_net qph_net;
 
 /* create_session (device.rs:88-101): validates every node (unsupported ->
  * QPH_EUNSUPPORTED naming the node), copies the weights to device memory
- * owned by the net and plans the activation arena. */
+ * owned by the net, plans the fusions and the activation arena, and
+ * captures the kernel sequence into a HIP graph, so that a graph the
+ * kernels cannot run fails here rather than at the first run. */
 QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
                            const float* const* weights_host, qph_net** out);
 QPH_API int qph_net_destroy(qph_net* net);
 /* DeviceSession::run (device.rs:130): input from the host (or device when
- * input_is_device), outputs copied to the host buffers (sizes from the
- * tensor table) unless outputs_host is NULL.  The kernel sequence is
- * captured into a HIP graph on the first run and replayed afterwards. */
+ * input_is_device; NULL keeps the input tensor as it is), the net's HIP
+ * graph replayed, outputs copied to the host buffers (sizes from the
+ * tensor table) unless outputs_host is NULL. */
 QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_device,
                         float* const* outputs_host);
 /* Deferred runs (DeviceSession::run_deferred + DeferredRun::complete,

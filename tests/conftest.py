@@ -65,7 +65,7 @@ def rel_check(got, ref, tol=1e-5):
 
 
 def baseline_tol_check(got, ref):
-    """Elementwise |g - r| <= max(1e-4 |r|, 1e-5) (the fp32 tolerance of the target)."""
+    """Elementwise |g - r| <= max(1e-4 |r|, 1e-5) (the fp32 tolerance of the path)."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     bad = np.abs(got - ref) > np.maximum(1e-4 * np.abs(ref), 1e-5)
@@ -88,7 +88,7 @@ def assert_bitexact(got, ref, name=""):
 
 
 def pairs_tolerance_check(pairs, pairs_ref, logits_ref):
-    """The target's rule for the CTC argmax exit: values within 1e-4
+    """The tolerance rule for the CTC argmax exit: values within 1e-4
     relative (1e-5 absolute near zero) of the reference's, ids identical
     except where the top-2 logit gap of the step is below 1e-4.  Returns the
     number of steps whose ids differ (all of them near-ties)."""

@@ -1,7 +1,7 @@
 """End-to-end parity of the five workloads on the GPU against the CPU oracle.
 
 Bar: bit-exact fp32 outputs (every element equal) and identical CTC argmax
-ids; the target's tolerance (1e-4 relative / 1e-5 absolute, argmax ids equal
+ids; the fp32 tolerance (1e-4 relative / 1e-5 absolute, argmax ids equal
 except where the top-2 logit gap is below 1e-4) is checked as well, so a
 future kernel that trades exactness for speed still has a stated bar.
 """
@@ -120,7 +120,7 @@ def test_rec_pairs_only_and_deferred_runs(gpu, oracle):
 def test_rec_fused_head(gpu, oracle, batch, width):
     """The rec graph with QPH_NET_FUSED_HEAD (head GEMM + softmax argmax in
     one kernel, logits never stored) against the oracle's full graph under
-    the target's rule; every node before the head is bit-exact already."""
+    the pairs tolerance rule; every node before the head is bit-exact already."""
     from conftest import pairs_tolerance_check
     from qppocr_amd import nets
     from oracle import nets as onets
@@ -167,7 +167,7 @@ def test_cfg5_mixed_page(gpu, oracle):
 
 def test_cfg5_mixed_page_fused_head(gpu, oracle):
     """The mixed page with fused rec heads (the benchmarked form): every
-    batch's pairs under the target's rule against the oracle's full graph,
+    batch's pairs under the pairs tolerance rule against the oracle's full graph,
     and the decoded lines equal to the oracle's wherever no id changed."""
     from conftest import pairs_tolerance_check
     from qppocr_amd import pipeline

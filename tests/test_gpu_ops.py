@@ -40,6 +40,12 @@ CONV_CASES = [tuple(c) for c in GOLD["conv_cases"]["cases"]] + [
     ("dense 32->40 3x3 wide M", 2, 32, 40, 19, 37, 3, 3, 1, 1, 1, 1, 1, True),
     ("M=3 3x3 (all tail)", 1, 4, 3, 16, 16, 3, 3, 1, 1, 1, 1, 1, True),
     ("1x1 batch=3 M%4", 3, 20, 13, 7, 9, 1, 1, 1, 1, 0, 0, 1, True),
+    # the LDS-staged 3x3 kernels: one-shot 32 channels with seeded tail rows
+    # in a partial panel, a ring of 5 chunks, and a width that is not a
+    # multiple of 4 (direct kernel)
+    ("lds 32->30 3x3 tail panel", 2, 32, 30, 20, 36, 3, 3, 1, 1, 1, 1, 1, True),
+    ("lds ring 40->20 3x3", 1, 40, 20, 12, 44, 3, 3, 1, 1, 1, 1, 1, True),
+    ("3x3 32->32 w%4 != 0", 1, 32, 32, 10, 30, 3, 3, 1, 1, 1, 1, 1, True),
 ]
 
 
@@ -382,7 +388,7 @@ def test_softmax_argmax_and_ties(gpu, oracle):
                                    (130, 32, 70)], ids=lambda s: "x".join(map(str, s)))
 def test_linear_softmax_argmax_fused(gpu, oracle, shape):
     """The fused head (GEMM + softmax + argmax, logits never stored) against
-    the oracle's MatMul, Add, Softmax, argmax under the target's rule:
+    the oracle's MatMul, Add, Softmax, argmax under the pairs tolerance rule:
     values within 1e-4, ids equal except at top-2 logit gaps below 1e-4.
     Planted exact ties and a maximum in the last, partial column block."""
     torch = gpu
