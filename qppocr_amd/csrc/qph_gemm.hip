@@ -321,6 +321,206 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
   for (int v = 0; v < 4; v++) epilogue_put(g, C, R != nullptr, e[v], ii + 4 * lg + v, jj + l16, acc[v]);
 }
 
+// ------------------------------------------------------- pointwise tiles
+//
+// 1x1 convs with few output channels over many pixels (the det FPN
+// laterals, M = 96, K = 32..256, N = 400..25600): C[M][N] = W[M][K] X[K][N],
+// then bias, act and residual (or the nearest-2x upsampled coarse map) as in
+// epilogue_gather / epilogue_put.  A workgroup is one wave owning 16 columns
+// and MBW 16-row blocks, each a v_mfma_f32_16x16x4f32 chain over k in order
+// (from 0, or from the bias where the reference seeds it).  K advances in
+// slabs of 16 through an NST-stage LDS ring filled by 16-byte buffer->LDS
+// loads: one for the X slab (16 rows x 16 columns) and MBW for the W slab
+// (16 k of each row, its four 16-byte chunks rotated by row % 4 so that the
+// A reads of one step spread over the banks).  The wave waits only on its own
+// loads: no workgroup barrier.  Bias and residual terms are loaded before
+// the first slab, so the slab waits, which count loads in issue order, never
+// wait for them.  The loads are inline asm, so the compiler adds no waits
+// of its own for the stages.
+template <int MBW, int NST>
+__global__ __launch_bounds__(64) void gemm_pw_kernel(GemmArgs g, int mgroups) {
+  extern __shared__ float pw_lds[];
+  constexpr int STAGE = 256 * (1 + MBW);   // floats: X slab, then W slab
+  constexpr int PER = 1 + MBW;             // loads per slab
+  const int lane = threadIdx.x;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int blk = blockIdx.x;
+  const int mg = blk % mgroups, pg = blk / mgroups;
+  const int64_t bt = blockIdx.z;
+  const int64_t n0 = (int64_t)pg * 16, m0 = (int64_t)mg * (16 * MBW);
+  const int64_t M = g.m, N = g.n;
+  const unsigned OOB = 0x80000000u;
+  const float* Ab = g.a + bt * g.a_batch;
+  const float* Bb = g.b + bt * g.b_batch;
+
+  // bias and residual terms first
+  const float* R = g.res ? g.res + bt * g.r_batch : nullptr;
+  const int64_t j = n0 + l16;
+  const int64_t rcol = (R && j < N) ? res_col(g, j) : 0;
+  float bld[MBW][4], rld[MBW][4];
+#pragma unroll
+  for (int mb = 0; mb < MBW; mb++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int64_t i = m0 + 16 * mb + 4 * lg + v;
+      const bool ok = i < M && j < N;
+      bld[mb][v] = (g.bias_mode == 1 && ok) ? g.bias[i] : 0.0f;
+      rld[mb][v] = (R && ok) ? R[i * g.ldr + rcol] : 0.0f;
+    }
+  __asm__ volatile("" ::: "memory");
+
+  // per-lane slab offsets (the k0 part is the scalar offset)
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)Bb, 0, (int)(g.k * g.ldb * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)Ab, 0, (int)(M * g.lda * 4), 0x00020000);
+  const int xrow = lane >> 2, xc = lane & 3;
+  const unsigned xoff = (n0 + 4 * xc < N) ? (unsigned)((xrow * g.ldb + n0 + 4 * xc) * 4) : OOB;
+  unsigned woff[MBW];
+#pragma unroll
+  for (int q = 0; q < MBW; q++) {
+    const int idx = 64 * q + lane, r = idx >> 2, c = (idx & 3) ^ (r & 3);
+    woff[q] = (m0 + r < M) ? (unsigned)(((m0 + r) * g.lda + 4 * c) * 4) : OOB;
+  }
+  const unsigned xstep = __builtin_amdgcn_readfirstlane((unsigned)(16 * g.ldb * 4));
+  const int nslab = (int)(g.k / 16);
+  auto issue = [&](int q) {
+    float* st = pw_lds + (q % NST) * STAGE;
+    const unsigned lx = __builtin_amdgcn_readfirstlane(
+        (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)st);
+    const unsigned sx = (unsigned)q * xstep, sw = (unsigned)q * 64u;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // m0 is reserved; nothing else uses it here
+    __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lx),
+                     "v"(xoff), "s"(xr), "s"(sx)
+                     : "m0");
+#pragma unroll
+    for (int w = 0; w < MBW; w++)
+      __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(
+                           lx + 1024u * (1 + w)),
+                       "v"(woff[w]), "s"(wr), "s"(sw)
+                       : "m0");
+#pragma clang diagnostic pop
+  };
+#pragma unroll
+  for (int q = 0; q < NST - 1; q++)
+    if (q < nslab) issue(q);
+  // the bias and residual values are first used after the first loads are out
+#pragma unroll
+  for (int mb = 0; mb < MBW; mb++)
+    __asm__ volatile("" : "+v"(bld[mb][0]), "+v"(bld[mb][1]), "+v"(bld[mb][2]),
+                     "+v"(bld[mb][3]), "+v"(rld[mb][0]), "+v"(rld[mb][1]), "+v"(rld[mb][2]),
+                     "+v"(rld[mb][3])::"memory");
+  f32x4 acc[MBW];
+  float bterm[MBW][4];
+#pragma unroll
+  for (int mb = 0; mb < MBW; mb++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int64_t i = m0 + 16 * mb + 4 * lg + v;
+      const bool seeded = g.bias_mode == 1 && i < M && j < N && bias_seeded(g.seed_rule, i, j, M, N);
+      acc[mb][v] = seeded ? bld[mb][v] : 0.0f;
+      bterm[mb][v] = (g.bias_mode == 1 && !seeded) ? bld[mb][v] : -0.0f;
+    }
+  // operand offsets inside a stage
+  const int boff = lg * 16 + l16;   // + 64 s
+  int aoff[MBW];
+#pragma unroll
+  for (int mb = 0; mb < MBW; mb++) {
+    const int r = 16 * mb + l16;
+    aoff[mb] = 256 + r * 16 + lg;   // + 4 (s ^ (r & 3))
+  }
+  for (int q = 0; q < nslab; q++) {
+    __asm__ volatile("" ::: "memory");
+    if (q + NST - 1 < nslab) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): slab q - 1's reads are done
+      issue(q + NST - 1);
+    }
+    // slab q in: the loads of the slabs after it may still be in flight
+    const int after = min(NST - 1, nslab - 1 - q);
+    if (NST >= 4 && after >= 3) wait_vmcnt<3 * PER>();
+    else if (NST >= 3 && after == 2) wait_vmcnt<2 * PER>();
+    else if (after == 1) wait_vmcnt<PER>();
+    else wait_vmcnt<0>();
+    __asm__ volatile("" ::: "memory");
+    const float* st = pw_lds + (q % NST) * STAGE;
+    float bv[4], av[4][MBW];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) {
+      bv[s4] = st[boff + 64 * s4];
+#pragma unroll
+      for (int mb = 0; mb < MBW; mb++) {
+        const int r = 16 * mb + l16;
+        av[s4][mb] = st[aoff[mb] + 4 * (s4 ^ (r & 3))];
+      }
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+      for (int mb = 0; mb < MBW; mb++)
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s4][mb], bv[s4], acc[mb], 0, 0, 0);
+  }
+  float* Cb = g.c + bt * g.c_batch;
+#pragma unroll
+  for (int mb = 0; mb < MBW; mb++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int64_t i = m0 + 16 * mb + 4 * lg + v;
+      if (i >= M || j >= N) continue;
+      float x = acc[mb][v] + bterm[mb][v];
+      x = act_apply(x, g.act);
+      if (R) x = x + rld[mb][v];
+      Cb[i * g.ldc + j] = x;
+    }
+}
+
+// The pointwise kernel takes K a multiple of 16, M <= 128, 16-byte aligned
+// rows of both operands, N a multiple of 4 and offsets within 31 bits.
+static bool pw_eligible(const GemmArgs& g) {
+  return !g.trans_out && g.part == nullptr && g.bias_mode != 2 && g.k % 16 == 0 &&
+         g.k >= 16 && g.m <= 128 && g.n % 4 == 0 && g.ldb % 4 == 0 && g.lda % 4 == 0 &&
+         g.a_batch % 4 == 0 && g.b_batch % 4 == 0 && (uintptr_t)g.a % 16 == 0 &&
+         (uintptr_t)g.b % 16 == 0 && g.k * g.ldb * 4 < (1ll << 31) &&
+         g.m * g.lda * 4 < (1ll << 31) && g.ldb >= g.n && g.lda >= g.k;
+}
+
+template <int MBW>
+static void launch_pw_m(const GemmArgs& g, int mgroups, dim3 grid, bool deep, hipStream_t s) {
+  const size_t lds = (size_t)(deep ? 4 : 2) * 256 * (1 + MBW) * 4;
+  if (deep)
+    hipLaunchKernelGGL((gemm_pw_kernel<MBW, 4>), grid, dim3(64), lds, s, g, mgroups);
+  else
+    hipLaunchKernelGGL((gemm_pw_kernel<MBW, 2>), grid, dim3(64), lds, s, g, mgroups);
+}
+
+static int launch_pw(const GemmArgs& g, hipStream_t s) {
+  const int mb = (int)ceil_div(g.m, 16);
+  const int64_t pgroups = ceil_div(g.n, 16);
+  // blocks per wave: the largest divisor of mb that still leaves >= 2048
+  // waves (else 1): more blocks share one X slab, fewer spread the chains
+  int mbw = 1;
+  for (int c = mb; c >= 1; c--)
+    if (mb % c == 0 && pgroups * (mb / c) * g.batch >= 2048) {
+      mbw = c;
+      break;
+    }
+  const int mgroups = mb / mbw;
+  if (pgroups * mgroups >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "gemm: grid too large");
+  dim3 grid((unsigned)(pgroups * mgroups), 1, (unsigned)g.batch);
+  const bool deep = g.k > 32;
+  switch (mbw) {
+    case 1: launch_pw_m<1>(g, mgroups, grid, deep, s); break;
+    case 2: launch_pw_m<2>(g, mgroups, grid, deep, s); break;
+    case 3: launch_pw_m<3>(g, mgroups, grid, deep, s); break;
+    case 4: launch_pw_m<4>(g, mgroups, grid, deep, s); break;
+    case 5: launch_pw_m<5>(g, mgroups, grid, deep, s); break;
+    case 6: launch_pw_m<6>(g, mgroups, grid, deep, s); break;
+    case 7: launch_pw_m<7>(g, mgroups, grid, deep, s); break;
+    default: launch_pw_m<8>(g, mgroups, grid, deep, s); break;
+  }
+  return launch_check("gemm_pw_kernel");
+}
+
 static int launch_skinny(const GemmArgs& g, hipStream_t s) {
   dim3 grid(ceil_div(g.n, 32), ceil_div(g.m, 32), (unsigned)g.batch);
   const bool vec = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (g.a_batch % 4 == 0) &&
@@ -963,6 +1163,7 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
     if (wide_fits(g) && tiles < (double)(1u << 30)) return launch_wide(g, s);
     return launch_cfg<2, 2>(g, s);
   }
+  if (pw_eligible(g)) return launch_pw(g, s);
   return launch_skinny(g, s);
 }
 
