@@ -71,18 +71,39 @@ struct DwPwK {
   const float* bst;
   int hin, win;
   Act act_s;
+  int xvec;          // stem input in 16-byte chunks (region column 0 one left)
 };
 
 // stem input region of a tile: 3 channels x 7 rows x 67 columns, rows 68
 // floats apart (a row arrives as a 64-lane load and a 3-lane load: only
-// active lanes write LDS); the stem tile is 3 rows x 33 columns of stem
-// outputs
+// active lanes write LDS; or, when the input width is a multiple of 4, as
+// 17 aligned 16-byte chunks starting one column further left); the stem
+// tile is 3 rows x 33 columns of stem outputs
 #define ST_RR 7
 #define ST_RP 68
 #define ST_IN (3 * ST_RR * ST_RP)
 #define ST_K 28            // 27 taps after one leading zero term
 #define ST_PX 99           // 3 x 33 stem outputs
 #define ST_PB 7            // 16-pixel blocks covering them
+#define ST_CT 36           // halo row pitch of the stem launch (3x3 stride 2)
+#define ST_PCP 132         // its channel pitch (3 rows of 36, rounded to 64, + 4)
+
+// Halo geometry of the 16-byte load path (VEC: left padding KW / 2, image
+// width a multiple of 4, 16-byte aligned tensors).  A halo row starts at the
+// 4-aligned column SHIFT columns left of the tile's first tap, so every
+// 16-byte chunk of it is wholly inside or wholly outside the image; CT
+// columns a row (a multiple of 4), CPR chunks a row, CH chunks a channel
+// (odd: a channel pitch of 4 mod 8 words puts the 16-byte reads of 16
+// consecutive channels on 16 disjoint groups of 4 banks).  Channels are
+// contiguous, so one 64-lane load fills 64 consecutive chunks.
+template <int KH, int KW, int SW>
+struct VecGeom {
+  static constexpr int SHIFT = (4 - (KW / 2) % 4) % 4;
+  static constexpr int CT = (SHIFT + 15 * SW + KW + 3) / 4 * 4;
+  static constexpr int CPR = CT / 4;
+  static constexpr int CH = KH * CPR + ((KH * CPR) % 2 == 0 ? 1 : 0);
+  static constexpr int PITCH = 4 * CH;
+};
 
 // AK = 3: every activation of the launch is the HardSigmoid + Mul pair
 // (both nets' blocks), applied inline; AK = 0: any, through act_apply
@@ -92,8 +113,9 @@ __device__ __forceinline__ float act_k(float v, const Act& a) {
   else return act_apply(v, a);
 }
 
-template <int KH, int KW, int SW, int PX, bool STEM, int AK>
+template <int KH, int KW, int SW, int PX, bool STEM, int AK, bool VEC>
 __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
+  static_assert(!(STEM && VEC), "the stem computes its halo");
   extern __shared__ float lds[];
   float* halo = lds;                 // [c][KH][ct]
   float* wsl = lds + p.halo;         // [cpad][64]
@@ -149,33 +171,70 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
       const __amdgpu_buffer_rsrc_t ir = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(p.xin + (int64_t)img * 3 * iplane), 0, (int)(3 * iplane * 4), 0x00020000);
       const int jy0 = 2 * iy0 - 1, jx0 = 2 * ix0 - 1;
-      for (int cr = wave; cr < 3 * ST_RR; cr += 4) {
-        const int c = cr / ST_RR, rr = cr - c * ST_RR;
-        const int iy = jy0 + rr;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          const int col = 64 * j + lane, ix = jx0 + col;
-          const bool ok = iy >= 0 && iy < p.hin && ix >= 0 && ix < p.win;
-          if (j == 0 || lane < 3)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ir, (__attribute__((address_space(3))) void*)(xin + cr * ST_RP + 64 * j), 4,
-                ok ? (unsigned)(((c * p.hin + iy) * p.win + ix) * 4) : OOB, 0, 0, 0);
-        }
-      }
-      // stem weights in their ONNX layout [c][27] (27 c <= 28 c floats in
-      // whole 64-word loads), the bias in one load (64 floats of room)
+      // stem weights in their ONNX layout [c][27] and the bias (27 c and c
+      // floats: whole 16-byte chunks, c being 16 or 32)
       const int nws = 27 * p.c;
       const __amdgpu_buffer_rsrc_t swr =
           __builtin_amdgcn_make_buffer_rsrc((void*)p.wst, 0, nws * 4, 0x00020000);
-      for (int base = wave * 64; base < nws; base += 256)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            swr, (__attribute__((address_space(3))) void*)(wsm + base), 4,
-            (unsigned)(base + lane) * 4u, 0, 0, 0);
-      if (p.bst && wave == 0) {
-        const __amdgpu_buffer_rsrc_t sbr =
-            __builtin_amdgcn_make_buffer_rsrc((void*)p.bst, 0, p.c * 4, 0x00020000);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(sbr, (__attribute__((address_space(3))) void*)bsm,
-                                                 4, (unsigned)lane * 4u, 0, 0, 0);
+      if (p.xvec) {
+        // chunk q: region row q / 17 (channel, row), columns jx0 - 1 + 4 (q % 17)
+        // .. + 3, wholly inside or outside the image (width % 4 == 0)
+        for (int q0 = wave * 64; q0 < 3 * ST_RR * 17; q0 += 256) {
+          const int q = q0 + lane, cr = q / 17, j = q - 17 * cr;
+          const int c = cr / ST_RR, iy = jy0 + cr - c * ST_RR, ix = jx0 - 1 + 4 * j;
+          const bool ok = iy >= 0 && iy < p.hin && ix >= 0 && ix < p.win;
+          if (q < 3 * ST_RR * 17)
+            lds_load16(ir, xin + 4 * q0, ok ? (unsigned)(((c * p.hin + iy) * p.win + ix) * 4) : OOB, 0);
+        }
+        for (int base = wave * 256; base < nws; base += 1024)
+          if (base + 4 * lane < nws) lds_load16(swr, wsm + base, (unsigned)(base + 4 * lane) * 4u, 0);
+        if (p.bst && wave == 0 && 4 * lane < p.c) {
+          const __amdgpu_buffer_rsrc_t sbr =
+              __builtin_amdgcn_make_buffer_rsrc((void*)p.bst, 0, p.c * 4, 0x00020000);
+          lds_load16(sbr, bsm, (unsigned)lane * 16u, 0);
+        }
+      } else {
+        for (int cr = wave; cr < 3 * ST_RR; cr += 4) {
+          const int c = cr / ST_RR, rr = cr - c * ST_RR;
+          const int iy = jy0 + rr;
+#pragma unroll
+          for (int j = 0; j < 2; j++) {
+            const int col = 64 * j + lane, ix = jx0 + col;
+            const bool ok = iy >= 0 && iy < p.hin && ix >= 0 && ix < p.win;
+            if (j == 0 || lane < 3)
+              __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                  ir, (__attribute__((address_space(3))) void*)(xin + cr * ST_RP + 64 * j), 4,
+                  ok ? (unsigned)(((c * p.hin + iy) * p.win + ix) * 4) : OOB, 0, 0, 0);
+          }
+        }
+        for (int base = wave * 64; base < nws; base += 256)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              swr, (__attribute__((address_space(3))) void*)(wsm + base), 4,
+              (unsigned)(base + lane) * 4u, 0, 0, 0);
+        if (p.bst && wave == 0) {
+          const __amdgpu_buffer_rsrc_t sbr =
+              __builtin_amdgcn_make_buffer_rsrc((void*)p.bst, 0, p.c * 4, 0x00020000);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(sbr, (__attribute__((address_space(3))) void*)bsm,
+                                                   4, (unsigned)lane * 4u, 0, 0, 0);
+        }
+      }
+    } else if constexpr (VEC) {
+      // chunk q of the [c][CH] halo: channel q / CH, row (q % CH) / CPR,
+      // columns ix0 - SHIFT + 4 ((q % CH) % CPR) .. + 3; chunks outside the
+      // image (and the odd channel's spare chunk) carry an out-of-range
+      // offset and read 0; lanes past the last chunk stay inactive
+      using G = VecGeom<KH, KW, SW>;
+      const int ix0a = ix0 - G::SHIFT;
+      const int nch = p.c * G::CH;
+      for (int q0 = wave * 64; q0 < nch; q0 += 256) {
+        const int q = q0 + lane;
+        const int ci = q / G::CH, rem = q - ci * G::CH;
+        const int r = rem / G::CPR, j = rem - r * G::CPR;
+        const int iy = iy0 + r, ix = ix0a + 4 * j;
+        const bool ok = r < KH && iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+        if (q < nch)
+          lds_load16(xr, halo + 4 * q0, ok ? (unsigned)((ci * (int)plane + iy * p.w + ix) * 4) : OOB,
+                     0);
       }
     } else {
       const int per_c = KH * p.ct;
@@ -201,75 +260,137 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)p.wk, 0, p.cpad * p.mpad * 4, 0x00020000);
     const int m0 = slice * DWPW_MSLICE;
-    const unsigned woff = m0 + lane < p.mpad ? (unsigned)((m0 + lane) * 4) : OOB;
-    // (STEM: the pointwise weights go to registers below, not to LDS)
-    for (int k = wave; k < (STEM ? 0 : p.cpad); k += 4)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          wr, (__attribute__((address_space(3))) void*)(wsl + k * 64), 4, woff,
-          k * p.mpad * 4, 0, 0);
-    // depthwise weights and bias (contiguous [c][KH*KW] and [c])
+    // weight row k holds column j of the slice at j ^ (16 (k % 4)), so that
+    // phase 3's four row groups read four disjoint groups of 16 banks
+    // (a wave's rows k = wave + 4 i all have k % 4 == wave)
+    const int wcol = m0 + (lane ^ (16 * wave));
+    const unsigned woff = wcol < p.mpad ? (unsigned)(wcol * 4) : OOB;
     const int nwd = p.c * KH * KW;
     const __amdgpu_buffer_rsrc_t dwr =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.wd, 0, nwd * 4, 0x00020000);
-    for (int base = wave * 64; base < nwd; base += 256)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          dwr, (__attribute__((address_space(3))) void*)(wdl + base), 4,
-          (unsigned)(base + lane) * 4u, 0, 0, 0);
-    if (p.bd) {
-      const __amdgpu_buffer_rsrc_t br =
-          __builtin_amdgcn_make_buffer_rsrc((void*)p.bd, 0, p.c * 4, 0x00020000);
-      for (int base = wave * 64; base < p.c; base += 256)
+    if constexpr (VEC) {
+      // 16-byte chunks: the weight rows k (16 chunks of the slice each;
+      // mpad is a multiple of 32, so a chunk is wholly inside or outside
+      // it; chunk j of row k lands at j ^ (4 (k % 4))), the depthwise
+      // weights and bias (c % 4 == 0: whole chunks)
+      for (int q0 = wave * 64; q0 < p.cpad * 16; q0 += 256) {
+        const int q = q0 + lane, col = m0 + 4 * ((q & 15) ^ (4 * ((q >> 4) & 3)));
+        lds_load16(wr, wsl + 4 * q0, col < p.mpad ? (unsigned)(((q >> 4) * p.mpad + col) * 4) : OOB, 0);
+      }
+      for (int base = wave * 256; base < nwd; base += 1024)
+        if (base + 4 * lane < nwd) lds_load16(dwr, wdl + base, (unsigned)(base + 4 * lane) * 4u, 0);
+      if (p.bd) {
+        const __amdgpu_buffer_rsrc_t br =
+            __builtin_amdgcn_make_buffer_rsrc((void*)p.bd, 0, p.c * 4, 0x00020000);
+        for (int base = wave * 256; base < p.c; base += 1024)
+          if (base + 4 * lane < p.c)
+            lds_load16(br, wdl + p.wdl_pad + base, (unsigned)(base + 4 * lane) * 4u, 0);
+      }
+    } else {
+      // (STEM: the pointwise weights go to registers below, not to LDS)
+      for (int k = wave; k < (STEM ? 0 : p.cpad); k += 4)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            br, (__attribute__((address_space(3))) void*)(wdl + p.wdl_pad + base), 4,
+            wr, (__attribute__((address_space(3))) void*)(wsl + k * 64), 4, woff,
+            k * p.mpad * 4, 0, 0);
+      // depthwise weights and bias (contiguous [c][KH*KW] and [c])
+      for (int base = wave * 64; base < nwd; base += 256)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            dwr, (__attribute__((address_space(3))) void*)(wdl + base), 4,
             (unsigned)(base + lane) * 4u, 0, 0, 0);
+      if (p.bd) {
+        const __amdgpu_buffer_rsrc_t br =
+            __builtin_amdgcn_make_buffer_rsrc((void*)p.bd, 0, p.c * 4, 0x00020000);
+        for (int base = wave * 64; base < p.c; base += 256)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              br, (__attribute__((address_space(3))) void*)(wdl + p.wdl_pad + base), 4,
+              (unsigned)(base + lane) * 4u, 0, 0, 0);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 
-  // phase S: the stem outputs of the halo, block (pixel block pb, channel
-  // block cb) per wave task; lane (g, l) feeds stem pixel 16 pb + l's tap
-  // k' = 4 s + g and takes outputs (pixel 16 pb + 4 g + v, channel 16 cb + l)
+  // phase S: the stem outputs of the halo, pixel block pb (16 stem pixels)
+  // per wave task, all channel blocks cb (16 channels each) of that block in
+  // the task; lane (g, l) feeds stem pixel 16 pb + l's tap k' = 4 s + g and
+  // takes outputs (pixel 16 pb + 4 g + v, channel 16 cb + l)
   if constexpr (STEM) {
     const int l16 = lane & 15, lg = lane >> 4;
     const int sy0 = oy * p.sh - p.ph, sx0 = ox0 * p.sw - p.pw;
+    constexpr int NCB = 2;          // channel blocks: c is 16 or 32
+    const int ncb = p.c >> 4;
     // tap offsets in the input region, k = k' - 1 = c * 9 + ky * 3 + kx
+    // (-1: the leading zero term)
     int koff[ST_K / 4];
 #pragma unroll
     for (int s = 0; s < ST_K / 4; s++) {
       const int k = 4 * s + lg - 1;
       const int c = k / 9, ky = (k - 9 * c) / 3, kx = k - 9 * c - 3 * ky;
-      koff[s] = k < 0 ? -1 : (c * ST_RR + ky) * ST_RP + kx;
+      koff[s] = k < 0 ? -1 : (c * ST_RR + ky) * ST_RP + kx + p.xvec;
     }
-    const int ntask = ST_PB * (p.c / 16);
-    for (int task = wave; task < ntask; task += 4) {
-      const int pb = task % ST_PB, cb = task / ST_PB;
-      const int q = pb * 16 + l16;
-      const int qr = q / 33, qc = q - 33 * qr;
-      const int poff = 2 * qr * ST_RP + 2 * qc;
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // this lane's weights and bias of every channel block, read once:
+    // weight (k', channel) = w[ch][k' - 1], 0 for the leading term (27
+    // words apart over the 16 channels: no bank conflict); the words read
+    // for absent blocks or the leading term are in bounds and unused
+    float bw[NCB][ST_K / 4], bb[NCB];
 #pragma unroll
-      for (int s = 0; s < ST_K / 4; s++) {
-        const float a = (koff[s] >= 0 && q < ST_PX) ? xin[koff[s] + poff] : 0.0f;
-        // weight (k', channel): 0 for the leading term, else w[ch][k' - 1]
-        // (27 words apart over the 16 channels: no bank conflict)
-        const float b = koff[s] >= 0 ? wsm[(cb * 16 + l16) * 27 + 4 * s + lg - 1] : 0.0f;
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
-      }
-      const int ch = cb * 16 + l16;
-      const float bias = bsm[ch];
+    for (int cb = 0; cb < NCB; cb++) {
+#pragma unroll
+      for (int s = 0; s < ST_K / 4; s++)
+        bw[cb][s] = wsm[cb < ncb && koff[s] >= 0 ? (cb * 16 + l16) * 27 + 4 * s + lg - 1 : 0];
+      bb[cb] = bsm[cb * 16 + l16];
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+      for (int s = 0; s < ST_K / 4; s++) bw[cb][s] = koff[s] >= 0 ? bw[cb][s] : 0.0f;
+    for (int pb = wave; pb < ST_PB; pb += 4) {
+      const int q = pb * 16 + l16;
+      const bool qok = q < ST_PX;
+      const int qr = (q >= 33) + (q >= 66), qc = q - 33 * qr;
+      const int poff = 2 * qr * ST_RP + 2 * qc;
+      // the input operands, one LDS round trip (the leading term and pixels
+      // past the tile read word 0 and select 0)
+      float a[ST_K / 4];
+#pragma unroll
+      for (int s = 0; s < ST_K / 4; s++) a[s] = xin[koff[s] >= 0 && qok ? koff[s] + poff : 0];
+      // this lane's four output pixels: halo offset, inside the stem map
+      // (outside: the depthwise's zero padding).  Pixels past the tile
+      // (block 6, row 3) land in the channel pitch's spare words
+      // (3 ST_CT + 12 < ST_PCP), which the depthwise never reads.
+      int hoff[4];
+      bool inmap[4];
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int qo = pb * 16 + 4 * lg + v;
-        if (qo >= ST_PX) continue;
-        const int ro = qo / 33, co = qo - 33 * ro;
+        const int ro = (qo >= 33) + (qo >= 66) + (qo >= 99), co = qo - 33 * ro;
         const int sy = sy0 + ro, sx = sx0 + co;
-        float val = 0.0f;   // the depthwise's zero padding
-        if (sy >= 0 && sy < p.h && sx >= 0 && sx < p.w) {
-          val = p.bst ? acc[v] + bias : acc[v];
-          val = act_k<AK>(val, p.act_s);
+        hoff[v] = ro * ST_CT + co;
+        inmap[v] = sy >= 0 && sy < p.h && sx >= 0 && sx < p.w;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < ST_K / 4; s++) a[s] = koff[s] >= 0 && qok ? a[s] : 0.0f;
+      f32x4 acc[NCB];
+#pragma unroll
+      for (int cb = 0; cb < NCB; cb++) {
+        acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (cb < ncb) {
+#pragma unroll
+          for (int s = 0; s < ST_K / 4; s++)
+            acc[cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bw[cb][s], acc[cb], 0, 0, 0);
         }
-        halo[ch * p.pcp + ro * p.ct + co] = val;
+      }
+#pragma unroll
+      for (int cb = 0; cb < NCB; cb++) {
+        if (cb < ncb) {
+          float* hc = halo + (cb * 16 + l16) * ST_PCP;
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const float y = act_k<AK>(p.bst ? acc[cb][v] + bb[cb] : acc[cb][v], p.act_s);
+            hc[hoff[v]] = inmap[v] ? y : 0.0f;
+          }
+        }
       }
     }
     __syncthreads();
@@ -279,7 +400,10 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   // (part, channel): pixels part * PX .. part * PX + PX - 1 of channel ci
   const int npx = p.oh * p.ow;
   {
-    constexpr int NC = (PX - 1) * SW + KW;   // halo columns of a task's row
+    // halo columns of a task's row, from its 16-byte aligned start (the
+    // first tap SH columns in)
+    constexpr int SH = VEC ? VecGeom<KH, KW, SW>::SHIFT : 0;
+    constexpr int NC = SH + (PX - 1) * SW + KW;
     constexpr bool V4 = (PX * SW) % 4 == 0;  // row start 16-byte aligned
     constexpr int NV = (NC + 3) / 4;
     constexpr int NR = V4 ? 4 * NV : NC;
@@ -296,40 +420,53 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         const float* wp = wdl + ci * KH * KW;
 #pragma unroll
         for (int j = 0; j < KH * KW; j++) wv[j] = wp[j];
-        const float* hp = halo + ci * p.pcp + px0 * SW;
+        const float* hp = halo + ci * (VEC ? VecGeom<KH, KW, SW>::PITCH : p.pcp) + px0 * SW;
+        // every row read before the first FMA (one LDS round trip)
+        float r[KH][NR];
 #pragma unroll
         for (int ky = 0; ky < KH; ky++) {
-          float r[NR];
-          const float* rp = hp + ky * p.ct;
+          const float* rp = hp + ky * (VEC ? VecGeom<KH, KW, SW>::CT : p.ct);
           if constexpr (V4) {
+            // only the words the taps use (SH .. NC - 1): 16-byte reads of
+            // whole aligned chunks, single words at either end (a partly
+            // dead 16-byte destination would let its registers be reused
+            // under the pending read, and the compiler then waits)
 #pragma unroll
             for (int v = 0; v < NV; v++) {
-              const f32x4 t4 = *(const f32x4*)(rp + 4 * v);
-              r[4 * v] = t4[0];
-              r[4 * v + 1] = t4[1];
-              r[4 * v + 2] = t4[2];
-              r[4 * v + 3] = t4[3];
+              if (4 * v >= SH && 4 * v + 4 <= NC) {
+                const f32x4 t4 = *(const f32x4*)(rp + 4 * v);
+                r[ky][4 * v] = t4[0];
+                r[ky][4 * v + 1] = t4[1];
+                r[ky][4 * v + 2] = t4[2];
+                r[ky][4 * v + 3] = t4[3];
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                  if (4 * v + e >= SH && 4 * v + e < NC) r[ky][4 * v + e] = rp[4 * v + e];
+              }
             }
           } else {
 #pragma unroll
-            for (int j = 0; j < NC; j++) r[j] = rp[j];
+            for (int j = SH; j < NC; j++) r[ky][j] = rp[j];
           }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the FMAs
+#pragma unroll
+        for (int ky = 0; ky < KH; ky++)
 #pragma unroll
           for (int kx = 0; kx < KW; kx++)
 #pragma unroll
             for (int q = 0; q < PX; q++)
-              acc[q] = __builtin_fmaf(wv[ky * KW + kx], r[q * SW + kx], acc[q]);
-        }
+              acc[q] = __builtin_fmaf(wv[ky * KW + kx], r[ky][SH + q * SW + kx], acc[q]);
       }
+      // the bias read once (in bounds for every ci < cpad), the outputs
+      // past the image or the channels select 0
+      const float bdv = p.bd ? wdl[p.wdl_pad + ci] : 0.0f;
       float o[PX];
 #pragma unroll
       for (int q = 0; q < PX; q++) {
-        float v = 0.0f;
-        if (ci < p.c && ox0 + px0 + q < p.ow) {
-          v = acc[q] + (p.bd ? wdl[p.wdl_pad + ci] : 0.0f);
-          v = act_k<AK>(v, p.act_d);
-        }
-        o[q] = v;
+        const float v = act_k<AK>(acc[q] + bdv, p.act_d);
+        o[q] = (ci < p.c && ox0 + px0 + q < p.ow) ? v : 0.0f;
       }
       float* tp = t + ci * 16 + px0;
       if constexpr (PX % 4 == 0) {
@@ -357,7 +494,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     if (p.bp && mo < p.m && pok && bias_seeded(p.seed_rule, mo, px, p.m, npx)) s0 = bpre[v];
     acc[v] = s0;
   }
-  const float* al = wsl + lg * 64 + wave * 16 + l16;
+  const float* al = wsl + lg * 64 + ((wave * 16 + l16) ^ (16 * lg));   // swizzled rows
   const float* bl = t + lg * 16 + l16;
   const int nsteps = p.cpad >> 2;
   int s = 0;
@@ -367,15 +504,43 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
       acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wreg[u], bl[u * 64], acc, 0, 0, 0);
     s = nsteps;
   }
-  for (; s + 4 <= nsteps; s += 4) {
-    float av[4], bv[4];
+  if (s + 4 <= nsteps) {
+    // groups of 4 steps in two register sets: the next group's operands
+    // are read before this group's MFMAs (a group past the end re-reads
+    // the current one: in bounds, unused)
+    float a0[4], b0[4], a1[4], b1[4];
+    auto ld = [&](float* a, float* b, const float* ap, const float* bp) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      av[u] = al[(s + u) * 256];
-      bv[u] = bl[(s + u) * 64];
+      for (int u = 0; u < 4; u++) {
+        a[u] = ap[u * 256];
+        b[u] = bp[u * 64];
+      }
+    };
+    auto mm = [&](const float* a, const float* b) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+    };
+    const float* ap = al;
+    const float* bp = bl;
+    ld(a0, b0, ap, bp);
+    for (; s + 8 <= nsteps; s += 8) {
+      ld(a1, b1, ap + 1024, bp + 256);
+      mm(a0, b0);
+      const int nx = s + 12 <= nsteps ? 2 : 1;
+      ld(a0, b0, ap + nx * 1024, bp + nx * 256);
+      mm(a1, b1);
+      // reads of the next group ahead of each group's MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      ap += 2048;
+      bp += 512;
     }
-#pragma unroll
-    for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u], acc, 0, 0, 0);
+    if (s + 4 <= nsteps) {
+      mm(a0, b0);
+      s += 4;
+    }
   }
   for (; s < nsteps; s++)
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(al[s * 256], bl[s * 64], acc, 0, 0, 0);
@@ -434,32 +599,53 @@ bool dwpw_eligible(const DwPwArgs& a) {
          (a.m + 31) / 32 * 32 * ((a.c + 3) / 4 * 4) * 4 < (1ll << 31);
 }
 
-template <int KH, int KW, int SW, int PX, bool STEM, int AK>
+template <int KH, int KW, int SW, int PX, bool STEM, int AK, bool VEC>
 static int launch_dwpw_a(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
-  // the widest halo row read of a task stays inside its channel's pitch
-  static_assert((16 - PX) * SW + 4 * (((PX - 1) * SW + KW + 3) / 4) <= (15 * SW + KW + 3) / 4 * 4 + 4,
+  // the widest halo row read of a task stays inside its row
+  static_assert(VEC || (16 - PX) * SW + 4 * (((PX - 1) * SW + KW + 3) / 4) <=
+                           (15 * SW + KW + 3) / 4 * 4 + 4,
                 "depthwise row reads past the halo row");
-  QPH_TRY(allow_full_lds((const void*)dwpw_kernel<KH, KW, SW, PX, STEM, AK>));
-  hipLaunchKernelGGL((dwpw_kernel<KH, KW, SW, PX, STEM, AK>), grid, dim3(256), lds, s, p);
+  static_assert(!VEC || (16 - PX) * SW +
+                            ((PX * SW) % 4 == 0
+                                 ? 4 * ((VecGeom<KH, KW, SW>::SHIFT + (PX - 1) * SW + KW + 3) / 4)
+                                 : VecGeom<KH, KW, SW>::SHIFT + (PX - 1) * SW + KW) <=
+                            VecGeom<KH, KW, SW>::CT,
+                "depthwise row reads past the halo row");
+  QPH_TRY(allow_full_lds((const void*)dwpw_kernel<KH, KW, SW, PX, STEM, AK, VEC>));
+  hipLaunchKernelGGL((dwpw_kernel<KH, KW, SW, PX, STEM, AK, VEC>), grid, dim3(256), lds, s, p);
   return launch_check("dwpw_kernel");
 }
 
-template <int KH, int KW, int SW, int PX, bool STEM = false>
+template <int KH, int KW, int SW, int PX, bool STEM = false, bool VEC = false>
 static int launch_dwpw_t(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
   const bool hs = p.act_d.kind == 3 && p.act_p.kind == 3 && (!STEM || p.act_s.kind == 3);
-  return hs ? launch_dwpw_a<KH, KW, SW, PX, STEM, 3>(grid, lds, p, s)
-            : launch_dwpw_a<KH, KW, SW, PX, STEM, 0>(grid, lds, p, s);
+  return hs ? launch_dwpw_a<KH, KW, SW, PX, STEM, 3, VEC>(grid, lds, p, s)
+            : launch_dwpw_a<KH, KW, SW, PX, STEM, 0, VEC>(grid, lds, p, s);
 }
 
-
-template <int KH, int KW, int SW>
+template <int KH, int KW, int SW, bool VEC>
 static int launch_dwpw_px(int px, dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
   switch (px) {
-    case 8: return launch_dwpw_t<KH, KW, SW, 8>(grid, lds, p, s);
-    case 4: return launch_dwpw_t<KH, KW, SW, 4>(grid, lds, p, s);
-    case 2: return launch_dwpw_t<KH, KW, SW, 2>(grid, lds, p, s);
-    default: return launch_dwpw_t<KH, KW, SW, 1>(grid, lds, p, s);
+    case 8: return launch_dwpw_t<KH, KW, SW, 8, false, VEC>(grid, lds, p, s);
+    case 4: return launch_dwpw_t<KH, KW, SW, 4, false, VEC>(grid, lds, p, s);
+    case 2: return launch_dwpw_t<KH, KW, SW, 2, false, VEC>(grid, lds, p, s);
+    default: return launch_dwpw_t<KH, KW, SW, 1, false, VEC>(grid, lds, p, s);
   }
+}
+
+template <int KH, int KW, int SW>
+static int launch_dwpw_v(bool vec, int px, dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
+  return vec ? launch_dwpw_px<KH, KW, SW, true>(px, grid, lds, p, s)
+             : launch_dwpw_px<KH, KW, SW, false>(px, grid, lds, p, s);
+}
+
+// the 16-byte load path: left padding KW / 2 (the halo geometry assumes
+// it), whole 16-byte chunks of image rows and of the weight arrays, 16-byte
+// aligned tensors
+static bool dwpw_vec(const DwPwArgs& a) {
+  auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  return !a.stem && a.pw == a.kw / 2 && a.w % 4 == 0 && a.c % 4 == 0 && al(a.x) && al(a.wd) &&
+         (!a.bd || al(a.bd)) && al(a.wk);
 }
 
 bool dwpw_stem_eligible(const DwPwArgs& a) {
@@ -497,18 +683,33 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
     if (!dwpw_stem_eligible(a)) return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: unsupported shape");
     p.xin = a.xin; p.wst = a.wst; p.bst = a.bst; p.act_s = a.act_s;
     p.hin = (int)a.hin; p.win = (int)a.win;
+    auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    p.xvec = a.win % 4 == 0 && al16(a.xin) && al16(a.wst) && (!a.bst || al16(a.bst));
+    // the stem phase writes the halo with these pitches as constants (and
+    // parks the pixels past its tile in the spare words of each channel)
+    if (p.ct != ST_CT || p.pcp != ST_PCP || 3 * ST_CT + 13 > ST_PCP)
+      return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: halo pitch");
     if (p.cpad != 16 * px || p.slices != 1)
       return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: unsupported shape");
     lds -= (size_t)p.wrows * 4;   // pointwise weights in registers
     p.wrows = 0;
     lds += (size_t)(ST_IN + ST_K * a.c + 64) * 4;
     // cpad 16 -> 1 pixel per depthwise task, 32 -> 2
-    if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true>(grid, lds, p, s);
-    return launch_dwpw_t<3, 3, 2, 1, true>(grid, lds, p, s);
+    if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true, false>(grid, lds, p, s);
+    return launch_dwpw_t<3, 3, 2, 1, true, false>(grid, lds, p, s);
   }
-  if (a.kh == 5) return launch_dwpw_px<5, 5, 1>(px, grid, lds, p, s);
-  if (a.sw == 1) return launch_dwpw_px<3, 3, 1>(px, grid, lds, p, s);
-  return launch_dwpw_px<3, 3, 2>(px, grid, lds, p, s);
+  // the 16-byte path's halo: whole chunks, channels contiguous
+  const int vch = a.kh == 5 ? VecGeom<5, 5, 1>::CH : a.sw == 1 ? VecGeom<3, 3, 1>::CH
+                                                              : VecGeom<3, 3, 2>::CH;
+  const bool vec = dwpw_vec(a) && a.c * 4 * vch <= DWPW_MAX_HALO;
+  if (vec) {
+    lds -= (size_t)p.halo * 4;
+    p.halo = (int)a.c * 4 * vch;
+    lds += (size_t)p.halo * 4;
+  }
+  if (a.kh == 5) return launch_dwpw_v<5, 5, 1>(vec, px, grid, lds, p, s);
+  if (a.sw == 1) return launch_dwpw_v<3, 3, 1>(vec, px, grid, lds, p, s);
+  return launch_dwpw_v<3, 3, 2>(vec, px, grid, lds, p, s);
 }
 
 }  // namespace qph

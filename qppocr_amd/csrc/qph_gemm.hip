@@ -734,14 +734,6 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs g, int mb, int 
   }
 }
 
-// 16-byte buffer->LDS load: lane L's four words land at dst + 4L.  (A plain
-// function, so that only the device compile checks the builtin's size.)
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, float* dst, unsigned voff,
-                                           int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
-                                           voff, soff, 0, 0);
-}
-
 // ------------------------------------------------ one-wave 64x64 tiles
 //
 // The rec head (PLAIN: column bias, no activation / residual / transposed

@@ -203,6 +203,14 @@ bool gemm_takes_wide(int64_t m, int64_t n, int64_t batch);
 // wt[j][i] = w[i][j] for a [k][n] row-major w
 int launch_transpose(const float* w, int64_t k, int64_t n, float* wt, hipStream_t s);
 
+// 16-byte buffer->LDS load: lane L's four words land at dst + 4L.  (A plain
+// function, so that only the device compile checks the builtin's size.)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, float* dst, unsigned voff,
+                                           int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, soff, 0, 0);
+}
+
 // s_waitcnt that waits until at most N vector-memory operations of this
 // wave are outstanding (N < 64); the export and LDS/scalar counters are left
 // at their maxima (no wait).  Encoding: vmcnt bits [3:0] and [15:14].

@@ -323,6 +323,50 @@ def test_session_stem_fusion(gpu, oracle, case):
     sess.close()
 
 
+BLOCK_CASES = [
+    # n, c, h, w, depthwise kernel, stride, pad, pointwise channels, activation
+    (1, 128, 40, 40, 3, 1, 1, 128, "hs"),   # det block 7: 16-byte loads, 8 px a task
+    (1, 128, 40, 40, 5, 1, 2, 128, "hs"),   # det block 9: 5x5
+    (1, 128, 40, 40, 3, 2, 1, 256, "hs"),   # det block 12: stride 2, four 64-channel slices
+    (2, 64, 23, 44, 3, 1, 1, 96, "hs"),     # partial tiles and slice, odd height
+    (1, 32, 30, 36, 3, 2, 1, 64, "hs"),     # stride 2, 2 px a task, partial tile
+    (1, 16, 17, 20, 3, 1, 1, 32, "relu"),   # 1 px a task, generic activations
+    (1, 64, 24, 48, 5, 1, 2, 64, "hs"),     # 5x5, 4 px a task
+    (1, 64, 20, 42, 3, 1, 1, 64, "hs"),     # width % 4 != 0: one-word loads
+    (1, 30, 20, 40, 3, 1, 1, 40, "hs"),     # channels % 4 != 0: one-word loads
+    (1, 32, 20, 40, 3, 1, 0, 32, "hs"),     # no padding: one-word loads
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_session_block_paths(gpu, oracle, case):
+    """Depthwise + 1x1 blocks fused into one launch, over both halo load
+    paths (16-byte chunks when the width and channel count are multiples
+    of 4 and the padding is k // 2; one-word loads otherwise), 1 to 8
+    pixels a depthwise task, 3x3 and 5x5, strides 1 and 2, partial tiles
+    and channel slices; bit-exact against the oracle."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    n, c, h, w, k, st, pad, m, act = case
+    kind = nets.ACT_RELU if act == "relu" else nets.ACT_HARDSWISH
+    r = nets.WeightRng(n * 17 + c * 5 + h + w + k + m)
+    g = nets.Graph((n, c, h, w))
+    wd = g.weight(r.kaiming((c, 1, k, k), k * k))
+    bd = g.weight(r.normal((c,), 0.1))
+    t = g.conv(0, wd, bd, stride=(st, st), pad=(pad,) * 4, group=c, act=kind)
+    wp = g.weight(r.kaiming((m, c, 1, 1), c))
+    bp = g.weight(r.normal((m,), 0.1))
+    y = g.conv(t, wp, bp, act=kind)
+    g.outputs = [y]
+    x = r.uniform((n, c, h, w), -1.0, 1.0)
+    print(f"block {case}", flush=True)
+    sess = nets.HipSession(g)
+    got = sess.run(x)
+    ref = onets.run_graph(g, x)
+    assert_bitexact(got[0], ref[0], "block output")
+    sess.close()
+
+
 def test_session_channel_last_chain_px(gpu, oracle):
     """Channel-last depthwise with four outputs per thread: x-stride 2 and 1
     at odd output widths (19), and a ReLU depthwise (the generic activation
