@@ -345,7 +345,8 @@ def main():
     ap.add_argument("--no-configs", action="store_true",
                     help="headline step only (skip the per-config measurements)")
     ap.add_argument("--node-report", default="",
-                    help="also write per-node times and roofline fractions (JSON) to this path")
+                    help="also write per-node work, eager per-node times and the launch plans "
+                         "of the headline graphs (JSON) to this path")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a kernel of "
                          "known traffic for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -483,9 +484,13 @@ def main():
     det_node_ms = det.node_times()
     det.set_profiling(False)
     if args.node_report:
+        # per-node work and eager event times, and each graph's launch plan
+        # (for matching a kernel trace of the replays: qppocr_amd.trace_report)
         with open(args.node_report, "w") as f:
-            json.dump(node_rows(nets, "det", det_g, det_node_ms) +
-                      node_rows(nets, "rec", rec_g, node_ms), f, indent=0)
+            json.dump({"det": {"nodes": node_rows(nets, "det", det_g, det_node_ms),
+                               "plan": det.plan()},
+                       "rec": {"nodes": node_rows(nets, "rec", rec_g, node_ms),
+                               "plan": rec.plan()}}, f, indent=0)
 
     det_flops = nets.flops(det_g)
     rec_flops = nets.flops(rec_g)

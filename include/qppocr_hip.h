@@ -392,6 +392,15 @@ QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* n
 QPH_API int qph_net_set_profiling(qph_net* net, int32_t on);
 QPH_API int qph_net_node_times(qph_net* net, double* ms_per_node, int32_t n);
 
+/* The launch sequence of a run, for profilers matching kernel traces to
+ * nodes: launch j covers nodes first[j] .. first[j] + nodes[j] - 1 and
+ * issues kernels[j] kernels (the fused rec head: 2; every other launch: 1).
+ * Fills at most cap entries of each non-NULL array and stores the number of
+ * launches in *n_launches.  No counterpart in the reference (whose executor
+ * runs node by node); for profiling tools. */
+QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* kernels,
+                         int32_t cap, int32_t* n_launches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,6 +112,7 @@ SIGNATURES = {
     "qph_net_complete": ([P], ctypes.c_int),
     "qph_net_set_profiling": ([P, I32], ctypes.c_int),
     "qph_net_node_times": ([P, ctypes.POINTER(ctypes.c_double), I32], ctypes.c_int),
+    "qph_net_plan": ([P, P, P, P, I32, P], ctypes.c_int),
 }
 
 _lib = None

@@ -954,6 +954,30 @@ QPH_API int qph_net_node_times(qph_net* net, double* ms, int32_t n) {
   return QPH_OK;
 }
 
+QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* kernels,
+                         int32_t cap, int32_t* n_launches) {
+  if (!net || !n_launches) return fail(QPH_EINVAL, "net_plan: NULL argument");
+  // the stepping of run_all: one launch per plain node, one per fused
+  // block / dense group / fused head (the head is two kernels)
+  int32_t n = 0;
+  const size_t nn = net->nodes.size();
+  for (size_t i = 0; i < nn; n++) {
+    size_t step = 1;
+    int32_t nk = 1;
+    if (net->group_len[i] > 1) step = (size_t)net->group_len[i];
+    else if (net->head[i]) step = 2, nk = 2;
+    else if (net->fused[i]) step = net->dwpw[i].stem ? 3 : 2;
+    if (n < cap) {
+      if (first) first[n] = (int32_t)i;
+      if (nodes) nodes[n] = (int32_t)step;
+      if (kernels) kernels[n] = nk;
+    }
+    i += step;
+  }
+  *n_launches = n;
+  return QPH_OK;
+}
+
 QPH_API int qph_net_staging(qph_net* net, int32_t slot, float** host, int64_t* numel) {
   if (!net || !host) return fail(QPH_EINVAL, "net_staging: NULL argument");
   if (slot < -1 || slot >= (int32_t)net->outputs.size())

@@ -544,6 +544,15 @@ class HipSession:
         check(self.lib.qph_net_node_times(self.net, arr, n))
         return list(arr)
 
+    def plan(self):
+        """The launch sequence of a run: (first node, nodes covered, kernels
+        issued) per launch."""
+        n = len(self.graph.nodes)
+        first, nodes, kern = ((ctypes.c_int32 * n)() for _ in range(3))
+        cnt = ctypes.c_int32()
+        check(self.lib.qph_net_plan(self.net, first, nodes, kern, n, ctypes.byref(cnt)))
+        return [(first[j], nodes[j], kern[j]) for j in range(cnt.value)]
+
     def close(self):
         if self.net:
             self.lib.qph_net_destroy(self.net)

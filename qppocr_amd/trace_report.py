@@ -1,0 +1,145 @@
+"""Per-launch and per-kernel-class roofline summary of the headline graphs
+from a rocprofv3 kernel trace of bench.py.
+
+    rocprofv3 --kernel-trace --output-format csv -d OUT -o run -- \\
+        python3 bench.py --no-cpu --no-configs --node-report OUT/nodes.json
+    python3 -m qppocr_amd.trace_report OUT/run_kernel_trace.csv OUT/nodes.json
+
+The node report carries each graph's nodes (algorithmic flops and bytes per
+node) and its launch plan (the nodes each launch covers, the kernels it
+issues).  A graph's kernels are taken per stream, cut where the stream was
+idle for more than 20 us (bench.py synchronises before each stage), and
+each stretch is read as consecutive replays of the graph's kernel count.
+Only replays that ran alone (no kernel of another stream inside their span)
+and back to back (no gap above 2 us between their kernels: graph replays,
+not the eager profiling runs) are used, and their first kernel must carry
+the signature most replays start with.  A launch's time is the median over
+those replays of its kernels' summed durations; its work is the sum over
+the nodes it covers.  Each launch and kernel class is priced against both
+rooflines (fp32 MFMA 157.3 TFLOP/s, HBM 8 TB/s) and its fraction is given
+at the one it comes closer to."""
+import collections
+import csv
+import json
+import statistics
+import sys
+
+PEAK_TFLOPS = 157.3
+PEAK_GBS = 8000.0
+IDLE_NS = 20000
+GAP_NS = 2000
+
+
+def _name(r):
+    return r["Kernel_Name"].split("(")[0].replace("void ", "").replace("qph::", "")
+
+
+def _sig(r):
+    return (_name(r), r["Grid_Size_X"], r["Grid_Size_Y"], r["Grid_Size_Z"])
+
+
+def _t(r, k):
+    return int(r[k + "_Timestamp"])
+
+
+def candidate_replays(rows, nk):
+    """(stream, kernels) chunks of nk kernels at the starts of busy stretches."""
+    by_stream = collections.defaultdict(list)
+    for r in rows:
+        by_stream[r["Stream_Id"]].append(r)
+    out = []
+    for sid, seq in by_stream.items():
+        seq.sort(key=lambda r: _t(r, "Start"))
+        start = 0
+        for i in range(1, len(seq) + 1):
+            if i == len(seq) or _t(seq[i], "Start") - _t(seq[i - 1], "End") > IDLE_NS:
+                for j in range(start, i - nk + 1, nk):
+                    out.append((sid, seq[j:j + nk]))
+                start = i
+    return out
+
+
+def alone_replays(rows, nk):
+    spans = [(_t(r, "Start"), _t(r, "End"), r["Stream_Id"]) for r in rows]
+    cands = candidate_replays(rows, nk)
+    good = []
+    for sid, rep in cands:
+        t0, t1 = _t(rep[0], "Start"), _t(rep[-1], "End")
+        gaps = [_t(rep[j + 1], "Start") - _t(rep[j], "End") for j in range(nk - 1)]
+        if max(gaps, default=0) >= GAP_NS:
+            continue
+        if any(s < t1 and e > t0 and st != sid for s, e, st in spans):
+            continue
+        good.append(rep)
+    if not good:
+        return []
+    first = collections.Counter(_sig(rep[0]) for rep in good).most_common(1)[0][0]
+    return [rep for rep in good if _sig(rep[0]) == first]
+
+
+def summarize(name, graph, rows):
+    plan, nodes = graph["plan"], graph["nodes"]
+    nk = sum(k for _, _, k in plan)
+    reps = alone_replays(rows, nk)
+    if not reps:
+        raise SystemExit(f"{name}: no alone back-to-back replay of {nk} kernels in the trace")
+    launches = []
+    k = 0
+    for first, cnt, nker in plan:
+        durs = [sum(_t(r, "End") - _t(r, "Start") for r in rep[k:k + nker]) for rep in reps]
+        kn = " + ".join(_name(r) for r in reps[0][k:k + nker])
+        fl = sum(n["gflop"] for n in nodes[first:first + cnt]) * 1e9
+        by = sum(n["mb"] for n in nodes[first:first + cnt]) * 1e6
+        ops = ",".join(n["op"] for n in nodes[first:first + cnt])
+        launches.append((kn, first, cnt, ops, statistics.median(durs) / 1e3, fl, by))
+        k += nker
+    total = sum(l[4] for l in launches)
+    fl_all = sum(l[5] for l in launches)
+    lines = [f"### {name}: {len(launches)} launches ({nk} kernels), {len(reps)} replays; "
+             f"summed median launch time {total:.1f} us, {fl_all / 1e9:.3f} GFLOP "
+             f"({fl_all / (total * 1e-6) / 1e12:.1f} TFLOP/s over the graph)", ""]
+    lines.append("| # | kernel | nodes | ops | us | GFLOP | MB | TFLOP/s | GB/s | frac | bound |")
+    lines.append("|---:|---|---|---|---:|---:|---:|---:|---:|---:|---|")
+    for j, (kn, first, cnt, ops, us, fl, by) in enumerate(launches):
+        tf, gb = fl / (us * 1e-6) / 1e12, by / (us * 1e-6) / 1e9
+        fm, fh = tf / PEAK_TFLOPS, gb / PEAK_GBS
+        lines.append(f"| {j} | `{kn}` | {first}-{first + cnt - 1} | {ops} | {us:.2f} | "
+                     f"{fl / 1e9:.4f} | {by / 1e6:.2f} | {tf:.2f} | {gb:.0f} | {max(fm, fh):.3f} | "
+                     f"{'mfma' if fm >= fh else 'hbm'} |")
+    lines.append("")
+    fam = collections.OrderedDict()
+    for kn, first, cnt, ops, us, fl, by in launches:
+        f = " + ".join(x.strip().split("<")[0] for x in kn.split("+"))
+        a = fam.setdefault(f, [0, 0.0, 0.0, 0.0])
+        a[0] += 1
+        a[1] += us
+        a[2] += fl
+        a[3] += by
+    lines.append("| kernel class | launches | us | share | TFLOP/s | frac MFMA | GB/s | frac HBM |")
+    lines.append("|---|---:|---:|---:|---:|---:|---:|---:|")
+    for f, (n, us, fl, by) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
+        tf, gb = fl / (us * 1e-6) / 1e12, by / (us * 1e-6) / 1e9
+        lines.append(f"| `{f}` | {n} | {us:.1f} | {us / total:.2f} | {tf:.2f} | "
+                     f"{tf / PEAK_TFLOPS:.3f} | {gb:.0f} | {gb / PEAK_GBS:.3f} |")
+    lines.append("")
+    return lines
+
+
+def main(argv):
+    if len(argv) != 3:
+        raise SystemExit("usage: python -m qppocr_amd.trace_report KERNEL_TRACE_CSV NODE_REPORT_JSON")
+    rows = list(csv.DictReader(open(argv[1])))
+    rep = json.load(open(argv[2]))
+    out = ["# Launch and kernel-class rooflines of the headline graphs", "",
+           f"From `{argv[1]}` and `{argv[2]}`: medians over the graph replays that ran alone "
+           "(durations of back-to-back kernels in a replayed graph, so each includes its share "
+           "of the launch overhead).  Work per launch: the algorithmic flops and bytes of the "
+           "nodes it covers (each input, weight and output counted once); frac: against the "
+           "roofline the launch comes closer to (fp32 MFMA 157.3 TFLOP/s, HBM 8 TB/s).", ""]
+    for name in ("det", "rec"):
+        out += summarize(name, rep[name], rows)
+    print("\n".join(out))
+
+
+if __name__ == "__main__":
+    main(sys.argv)
