@@ -234,13 +234,16 @@ def test_conv_im2col_bias_placement(gpu, oracle, shape):
     assert (y[0, 4] == big + 2).any() and (y[0, 4] == big).any()
 
 
-# the last nine take the pointwise kernel (M <= 128, K % 16 == 0, N % 4 ==
+# the last eleven take the pointwise kernel (M <= 128, K % 16 == 0, N % 4 ==
 # 0): the det lateral shapes, an M % 4 tail with partial panels, 7 and 8
-# row blocks, one block, and wide ones where a wave takes 8, 6 or 2 blocks
+# row blocks, one block, wide ones where a wave takes 8, 6 or 2 blocks, and
+# small grids with every slab in flight (a 16-stage ring wrapping over 32
+# slabs; 8 stages for 5 slabs)
 SGEMM_SHAPES = [(1, 1, 1), (64, 64, 64), (1, 500, 300), (17, 33, 129), (256, 96, 384),
                 (1, 368, 368 * 9), (17, 713, 77), (5, 37, 13),
                 (96, 400, 256), (96, 25600, 32), (100, 1600, 128), (128, 6400, 64),
-                (13, 100, 48), (7, 36, 16), (128, 32768, 16), (96, 33024, 32), (32, 32768, 48)]
+                (13, 100, 48), (7, 36, 16), (128, 32768, 16), (96, 33024, 32), (32, 32768, 48),
+                (64, 256, 512), (48, 96, 80)]
 
 
 @pytest.mark.parametrize("mnk", SGEMM_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in SGEMM_SHAPES])
