@@ -761,24 +761,34 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
     }
   }
 
-  // epilogue as in direct3x3_unit
+  // epilogue as in direct3x3_unit; every residual term is read before the
+  // first store (a load after a store that may alias the output makes the
+  // compiler wait for that store to complete, once per output)
   if (!pval) return;
   const int64_t yoh = (int64_t)p.oh * p.y_up, yow = (int64_t)p.ow * p.y_up;
   float* ybase = p.y + ((int64_t)img * p.y_ctotal + p.y_coff) * yoh * yow;
   const float* rbase = p.res ? p.res + ((int64_t)img * p.m * p.oh + poy) * p.ow + pox : nullptr;
+  float outv[2][4];
 #pragma unroll
   for (int mt = 0; mt < 2; mt++)
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       const int co = mt * 16 + 4 * lg + v;
-      if (co >= p.m) continue;
       float xv = acc[mt][v] + bterm[mt][v];
       if constexpr (AK == 2)
         xv = relu1(xv);
       else if constexpr (AK < 0)
         xv = act_apply(xv, p.act);
-      if (rbase) xv = xv + rbase[(int64_t)co * p.oh * p.ow];
-      store_replicated(ybase + (int64_t)co * yoh * yow, yow, poy, pox, (int)p.y_up, xv);
+      if (rbase && co < p.m) xv = xv + rbase[(int64_t)co * p.oh * p.ow];
+      outv[mt][v] = xv;
+    }
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = mt * 16 + 4 * lg + v;
+      if (co < p.m) store_replicated(ybase + (int64_t)co * yoh * yow, yow, poy, pox, (int)p.y_up,
+                                     outv[mt][v]);
     }
 }
 
