@@ -339,8 +339,9 @@ typedef struct {
 } qph_net_spec;
 
 /* Every node its own launch: no shared launch of independent 3x3 convs, no
- * depthwise + 1x1 (+ stem) fusion, no channel-last rec blocks (per-op
- * measurement and debugging; the results are the same bits). */
+ * depthwise + 1x1 (+ stem) fusion, no QKV linear + attention launch, no
+ * channel-last rec blocks (per-op measurement and debugging; the results
+ * are the same bits). */
 #define QPH_NET_SEPARATE_LAUNCHES 1
 /* A linear whose output only the pairs-only softmax argmax right after it
  * reads (the rec head) runs as one GEMM with the softmax argmax in its
@@ -382,13 +383,18 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
 QPH_API int qph_net_staging(qph_net* net, int32_t slot, float** host, int64_t* numel);
 QPH_API int qph_net_run_async(qph_net* net, int32_t flags);
 QPH_API int qph_net_complete(qph_net* net);
-/* Device pointer of a tensor of the net (valid until destroy). */
+/* Device pointer of a tensor of the net (valid until destroy).  Tensors that
+ * a fused launch consumes inside itself are never written: a depthwise
+ * output inside a depthwise + 1x1 block, a stem output inside the first
+ * block, the QKV output of a linear + attention launch, a fused head's
+ * logits. */
 QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* numel);
 /* Average device time (ms) of each node over the runs since the last reset
  * when profiling is on (events around each node; graph replay disabled).
  * A launch that covers several nodes (a depthwise + 1x1 block, a stem conv
- * run inside the first block, a group of independent 3x3 convs) is booked
- * on its first node; the nodes it covers read only the event overhead. */
+ * run inside the first block, a group of independent 3x3 convs, a QKV
+ * linear + attention) is booked on its first node; the nodes it covers
+ * read only the event overhead. */
 QPH_API int qph_net_set_profiling(qph_net* net, int32_t on);
 QPH_API int qph_net_node_times(qph_net* net, double* ms_per_node, int32_t n);
 

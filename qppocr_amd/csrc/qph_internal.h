@@ -197,6 +197,13 @@ struct LinArgs {
   const float* res;           // [M][N], or NULL
 };
 bool linear_nt_eligible(int64_t m, int64_t n, int64_t k, int64_t lda);
+// the rec QKV linear (x [batch * t][k] . Wt[3 heads dh][k]^T + bias) and
+// the attention after it in one launch; wt is the linear's resident
+// transposed weight
+bool qkv_attention_eligible(int64_t batch, int64_t t, int64_t heads, int64_t dh, int64_t k);
+int launch_qkv_attention(const float* x, const float* wt, const float* bias, int64_t batch,
+                         int64_t t, int64_t heads, int64_t dh, int64_t k, float scale, float* out,
+                         hipStream_t s);
 int launch_linear_nt(const LinArgs& g, hipStream_t s);
 // true when launch_gemm takes the 128x128 persistent kernel for this shape
 bool gemm_takes_wide(int64_t m, int64_t n, int64_t batch);

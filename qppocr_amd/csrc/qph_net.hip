@@ -28,6 +28,7 @@ struct qph_net {
   std::vector<bool> cl_pw;       // 1x1 conv node run as a row-major GEMM, channel-last in and out
   std::vector<bool> cl_out;      // 1x1 conv node storing channel-last (trans_out) for a cl_dw reader
   std::vector<bool> head;        // linear node i and the pairs-only softmax i + 1 run fused
+  std::vector<bool> qa_fused;    // linear node i (QKV) and attention node i + 1, one launch
   std::vector<float*> head_part; // per fused head: its per-block argmax partials
   std::vector<bool> nostore;     // per tensor: never materialised (a fused head's logits)
   std::vector<float*> tptr;      // per tensor device pointer
@@ -233,6 +234,48 @@ static void plan_fused_head(qph_net* net, int32_t flags) {
         !head_argmax_eligible(rows, q.ws[1], q.ws[0], q.ws[0], (q.ws[1] + 3) / 4 * 4))
       continue;
     net->head[i] = true;
+    net->nostore[(size_t)t] = true;
+  }
+}
+
+// A linear read only by the attention right after it (the rec QKV
+// projection), with no activation or residual, whose output is the
+// attention's q, k, v of head dimension 32 over T <= 64 rows (T % 4 == 0)
+// and whose K is a multiple of 64 up to 256: both run as one launch
+// (qkv_attention_kernel), the QKV tensor never stored.  The linear keeps
+// its resident transposed weight (same rule as the resident-weight
+// linears).  Runs after plan_pitch (both tensors contiguous) and before
+// the arena is laid out.
+static void plan_qkv_attention(qph_net* net, int32_t flags) {
+  const size_t nn = net->nodes.size(), nt = net->tptr.size();
+  net->qa_fused.assign(nn, false);
+  if (flags & QPH_NET_SEPARATE_LAUNCHES) return;
+  auto ok = [&](int32_t t) { return t >= 0 && (size_t)t < nt; };
+  for (size_t i = 0; i + 1 < nn; i++) {
+    const qph_node& q = net->nodes[i];
+    const qph_node& r = net->nodes[i + 1];
+    if (q.op != QPH_OP_LINEAR || r.op != QPH_OP_ATTENTION || !ok(q.in) || !ok(q.out) ||
+        !ok(r.out) || r.in != q.out || q.in2 >= 0 || q.act.kind != QPH_ACT_NONE ||
+        q.ws[0] <= 0 || q.ws[1] != 3 * (int64_t)r.heads * r.dh || net->head[i])
+      continue;
+    const int32_t t = q.out;
+    const int64_t* xs = &net->shapes[4 * (size_t)t];
+    const int64_t k = q.ws[0], rows = numel_of(net, q.in) / k;
+    if (net->alias[(size_t)t] >= 0 || net->alias[(size_t)q.in] >= 0 || net->pitch[(size_t)t] ||
+        net->pitch[(size_t)q.in] || numel_of(net, q.in) % k || xs[2] * xs[3] != q.ws[1] ||
+        rows != xs[0] * xs[1])
+      continue;
+    bool single = true;
+    for (size_t t2 = 0; t2 < nt; t2++) single = single && net->alias[t2] != t;
+    for (size_t j = 0; j < nn; j++)
+      if (j != i + 1)
+        single = single && net->nodes[j].in != t && net->nodes[j].in2 != t &&
+                 net->nodes[j].in3 != t;
+    for (int32_t o : net->outputs) single = single && o != t;
+    if (!single || gemm_takes_wide(rows, q.ws[1], 1) || !linear_nt_eligible(rows, q.ws[1], k, k) ||
+        !qkv_attention_eligible(xs[0], xs[1], r.heads, r.dh, k))
+      continue;
+    net->qa_fused[i] = true;
     net->nostore[(size_t)t] = true;
   }
 }
@@ -686,6 +729,16 @@ static int run_all(qph_net* net) {
     } else if (net->fused[i]) {
       QPH_TRY(launch_dwpw(net->dwpw[i], s));
       step = net->dwpw[i].stem ? 3 : 2;
+    } else if (net->qa_fused[i]) {
+      const qph_node& q = net->nodes[i];
+      const qph_node& r = net->nodes[i + 1];
+      const int64_t* xs = &net->shapes[4 * (size_t)q.out];
+      const int rc = launch_qkv_attention(net->tptr[q.in], net->wt[i],
+                                          q.bias >= 0 ? net->weights[q.bias] : nullptr, xs[0],
+                                          xs[1], r.heads, r.dh, q.ws[0], r.scale,
+                                          net->tptr[r.out], s);
+      if (rc != QPH_OK) return fail(rc, node_name(i, q) + ": " + qph_last_error());
+      step = 2;
     } else {
       const int rc = run_node(net, i);
       if (rc != QPH_OK) return fail(rc, node_name(i, net->nodes[i]) + ": " + qph_last_error());
@@ -808,6 +861,7 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
   }
   plan_fused_head(net, spec->flags);
   plan_pitch(net);
+  plan_qkv_attention(net, spec->flags);
   std::vector<size_t> off((size_t)spec->n_tensors, 0);
   for (int32_t t = 0; t < spec->n_tensors; t++) {
     if (net->alias[t] >= 0) continue;
@@ -958,7 +1012,8 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
                          int32_t cap, int32_t* n_launches) {
   if (!net || !n_launches) return fail(QPH_EINVAL, "net_plan: NULL argument");
   // the stepping of run_all: one launch per plain node, one per fused
-  // block / dense group / fused head (the head is two kernels)
+  // block / dense group / fused head (the head is two kernels) / QKV linear
+  // + attention
   int32_t n = 0;
   const size_t nn = net->nodes.size();
   for (size_t i = 0; i < nn; n++) {
@@ -967,6 +1022,7 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
     if (net->group_len[i] > 1) step = (size_t)net->group_len[i];
     else if (net->head[i]) step = 2, nk = 2;
     else if (net->fused[i]) step = net->dwpw[i].stem ? 3 : 2;
+    else if (net->qa_fused[i]) step = 2;
     if (n < cap) {
       if (first) first[n] = (int32_t)i;
       if (nodes) nodes[n] = (int32_t)step;

@@ -836,6 +836,128 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
 // probability block to 16-row, 16-column tiles, whose extra outputs are
 // never used.
 
+// The attention of one (batch, head) once q (times scale), k and v of its
+// rows are in LDS (rows t .. tp - 1 zero): scores, the softmax with the
+// reference's lane chains, P.V, written to out[r * D + d] (out at the
+// head's first column of the batch's first row).  NT threads.
+template <int DH, bool MF, int NT>
+__device__ __forceinline__ void attention_rows(const float* sq, const float* sk, const float* sv,
+                                               float* sp, int t, int tp, int ldp, int blk,
+                                               int64_t D, float* __restrict__ out) {
+  constexpr int LD = DH + 1;
+  const int full = t >= 8 ? (t / 8) * 8 : 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lg = lane >> 4, l16 = lane & 15;
+  for (int r0 = 0; r0 < t; r0 += blk) {
+    const int rb = (t - r0) < blk ? (t - r0) : blk;
+    if (MF) {
+      // S block (rb x t) in 16x16 tiles over the waves
+      const int nr = (rb + 15) / 16, nc = tp / 16;
+      for (int tl = wave; tl < nr * nc; tl += NT / 64) {
+        const int br = tl / nc, bc = tl - br * nc;
+        const float* a = sq + (r0 + 16 * br + l16) * LD + lg;
+        const float* bk = sk + (16 * bc + l16) * LD + lg;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s4 = 0; s4 < DH / 4; s4++)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4], bk[4 * s4], acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) sp[(16 * br + 4 * lg + v) * ldp + 16 * bc + l16] = acc[v];
+      }
+    } else {
+      // scores S[r][j] = chain over d of fma(q[r][d], k[j][d], acc)
+      for (int i = tid; i < rb * t; i += NT) {
+        const int r = i / t, j = i - r * t;
+        const float* qr = sq + (r0 + r) * LD;
+        const float* kj = sk + j * LD;
+        float acc = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DH; d++) acc = __builtin_fmaf(qr[d], kj[d], acc);
+        sp[r * ldp + j] = acc;
+      }
+    }
+    __syncthreads();
+    // softmax, eight threads per row (groups never straddle a wave)
+    for (int g0 = 0; g0 < rb; g0 += NT / 8) {
+      const int r = g0 + (tid >> 3), lj = tid & 7;
+      const bool rowok = r < rb;
+      float* pr = sp + (rowok ? r : 0) * ldp;
+      float mx = -__builtin_inff();
+      if (rowok)
+        for (int j = lj; j < t; j += 8) mx = fmaxf(mx, pr[j]);
+      for (int off = 4; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 8));
+      if (t < 8 && rowok) {   // narrow rows: sequential max from the first element
+        mx = pr[0];
+        for (int j = 1; j < t; j++)
+          if (pr[j] > mx) mx = pr[j];
+      }
+      float s = 0.0f;
+      if (rowok)
+        for (int j = lj; j < t; j += 8) {
+          const float e = exp1(pr[j] - mx);
+          pr[j] = e;
+          if (j < full) s = s + e;   // lane lj's chain, ascending j
+        }
+      // tree of the eight lane chains, then the tail in order (lane 0)
+      const int gb = (threadIdx.x & 63) & ~7;
+      const float l0 = __shfl(s, gb + 0, 64), l1 = __shfl(s, gb + 1, 64);
+      const float l2 = __shfl(s, gb + 2, 64), l3 = __shfl(s, gb + 3, 64);
+      const float l4 = __shfl(s, gb + 4, 64), l5 = __shfl(s, gb + 5, 64);
+      const float l6 = __shfl(s, gb + 6, 64), l7 = __shfl(s, gb + 7, 64);
+      float sum = 0.0f;
+      if (rowok && lj == 0) {
+        if (t >= 8) sum = ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7));
+        for (int j = full; j < t; j++) sum = sum + pr[j];
+      }
+      sum = __shfl(sum, gb, 64);
+      const float inv = 1.0f / sum;
+      if (rowok)
+        for (int j = lj; j < t; j += 8) pr[j] = pr[j] * inv;
+    }
+    __syncthreads();
+    if (MF) {
+      // O block (rb x DH) = P . v in 16x16 tiles, k = j over exactly t terms
+      const int nr = (rb + 15) / 16;
+      for (int tl = wave; tl < nr * (DH / 16); tl += NT / 64) {
+        const int br = tl / (DH / 16), bc = tl - br * (DH / 16);
+        const float* a = sp + (16 * br + l16) * ldp + lg;
+        const float* bv = sv + lg * LD + 16 * bc + l16;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s4 = 0; s4 < t / 4; s4++)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4], bv[4 * s4 * LD], acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          const int r = 16 * br + 4 * lg + v;
+          if (r < rb) out[(int64_t)(r0 + r) * D + 16 * bc + l16] = acc[v];
+        }
+      }
+    } else {
+      // O[r][d] = chain over j of fma(P[r][j], v[j][d], acc); operands read
+      // eight j at a time so their LDS reads are in flight together
+      for (int i = tid; i < rb * DH; i += NT) {
+        const int r = i / DH, d = i - r * DH;
+        const float* p = sp + r * ldp;
+        const float* vd = sv + d;
+        float acc = 0.0f;
+        int j = 0;
+        for (; j + 8 <= t; j += 8) {
+          float pv[8], vv[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            pv[u] = p[j + u];
+            vv[u] = vd[(j + u) * LD];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; u++) acc = __builtin_fmaf(pv[u], vv[u], acc);
+        }
+        for (; j < t; j++) acc = __builtin_fmaf(p[j], vd[j * LD], acc);
+        out[(int64_t)(r0 + r) * D + d] = acc;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <int DH, bool MF>
 __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restrict__ qkv,
                                                            int64_t T, int64_t H, float scale,
@@ -878,117 +1000,199 @@ __global__ __launch_bounds__(256) void attention_dh_kernel(const float* __restri
     }
   }
   __syncthreads();
-  const int full = t >= 8 ? (t / 8) * 8 : 0;
-  const int lane = tid & 63, wave = tid >> 6;
+  attention_rows<DH, MF, 256>(sq, sk, sv, sp, t, tp, ldp, blk, D, out + b * T * D + h * DH);
+}
+
+// The rec QKV linear and the attention that reads it, one launch: one
+// workgroup of 512 threads per (batch, head) computes its head's q, k and v
+// columns of the linear for the batch's T rows (T <= 64, T % 4 == 0, head
+// dimension 32, K = 64 NK <= 256), then the attention of those rows; the
+// QKV tensor never reaches HBM.  The product is linear_nt_kernel's: 16x16
+// output blocks on v_mfma_f32_16x16x4f32, each a chain over k ascending
+// from 0 (x rows as A, the resident transposed weight rows as B, the same
+// 64-k slabs with 16-byte chunks swizzled by row), then + bias (or -0.0,
+// the exact identity), so q, k and v are bit-identical to the stored
+// linear output; q is then multiplied by scale and rows T .. tp - 1 are 0,
+// as attention_dh_kernel loads them.  K slabs go through two LDS stages
+// (x: 64 rows, rows past T read 0; weights: the head's 96 rows), 5 loads
+// per wave per slab.  Reference: the MatMul (+ Add) of the QKV projection
+// (gemm.rs) and the attention nodes after it (qppocr-core/src/executor.rs).
+#define QA_ROWS 64                      // x rows of a slab (T <= 64)
+#define QA_STAGE ((QA_ROWS + 96) * 64)  // floats: x slab, then weight slab
+template <int NK>
+__global__ __launch_bounds__(512) void qkv_attention_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ wt,
+                                                            const float* __restrict__ bias,
+                                                            int T, int H, float scale, int blk,
+                                                            float* __restrict__ out) {
+  constexpr int DH = 32, LD = DH + 1, K = NK * 64;
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lg = lane >> 4, l16 = lane & 15;
-  for (int r0 = 0; r0 < t; r0 += blk) {
-    const int rb = (t - r0) < blk ? (t - r0) : blk;
-    if (MF) {
-      // S block (rb x t) in 16x16 tiles over the four waves
-      const int nr = (rb + 15) / 16, nc = tp / 16;
-      for (int tl = wave; tl < nr * nc; tl += 4) {
-        const int br = tl / nc, bc = tl - br * nc;
-        const float* a = sq + (r0 + 16 * br + l16) * LD + lg;
-        const float* bk = sk + (16 * bc + l16) * LD + lg;
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int b = blockIdx.x / H, h = blockIdx.x - b * H;
+  const int64_t D = (int64_t)H * DH;
+  const int tp = (T + 15) / 16 * 16;
+  const int nrb = tp / 16, nblk = nrb * 6;   // 16x16 blocks: row blocks x (q, k, v) x 2
+  // this wave's blocks j = wave + 8 i (at most 3: tp <= 64 gives 24 blocks)
+  float badd[3];
 #pragma unroll
-        for (int s4 = 0; s4 < DH / 4; s4++)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4], bk[4 * s4], acc, 0, 0, 0);
-#pragma unroll
-        for (int v = 0; v < 4; v++) sp[(16 * br + 4 * lg + v) * ldp + 16 * bc + l16] = acc[v];
-      }
-    } else {
-      // scores S[r][j] = chain over d of fma(q[r][d], k[j][d], acc)
-      for (int i = tid; i < rb * t; i += 256) {
-        const int r = i / t, j = i - r * t;
-        const float* qr = sq + (r0 + r) * LD;
-        const float* kj = sk + j * LD;
-        float acc = 0.0f;
-#pragma unroll
-        for (int d = 0; d < DH; d++) acc = __builtin_fmaf(qr[d], kj[d], acc);
-        sp[r * ldp + j] = acc;
-      }
-    }
-    __syncthreads();
-    // softmax, eight threads per row (groups never straddle a wave)
-    for (int g0 = 0; g0 < rb; g0 += 32) {
-      const int r = g0 + (tid >> 3), lj = tid & 7;
-      const bool rowok = r < rb;
-      float* pr = sp + (rowok ? r : 0) * ldp;
-      float mx = -__builtin_inff();
-      if (rowok)
-        for (int j = lj; j < t; j += 8) mx = fmaxf(mx, pr[j]);
-      for (int off = 4; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 8));
-      if (t < 8 && rowok) {   // narrow rows: sequential max from the first element
-        mx = pr[0];
-        for (int j = 1; j < t; j++)
-          if (pr[j] > mx) mx = pr[j];
-      }
-      float s = 0.0f;
-      if (rowok)
-        for (int j = lj; j < t; j += 8) {
-          const float e = exp1(pr[j] - mx);
-          pr[j] = e;
-          if (j < full) s = s + e;   // lane lj's chain, ascending j
-        }
-      // tree of the eight lane chains, then the tail in order (lane 0)
-      const int gb = (threadIdx.x & 63) & ~7;
-      const float l0 = __shfl(s, gb + 0, 64), l1 = __shfl(s, gb + 1, 64);
-      const float l2 = __shfl(s, gb + 2, 64), l3 = __shfl(s, gb + 3, 64);
-      const float l4 = __shfl(s, gb + 4, 64), l5 = __shfl(s, gb + 5, 64);
-      const float l6 = __shfl(s, gb + 6, 64), l7 = __shfl(s, gb + 7, 64);
-      float sum = 0.0f;
-      if (rowok && lj == 0) {
-        if (t >= 8) sum = ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7));
-        for (int j = full; j < t; j++) sum = sum + pr[j];
-      }
-      sum = __shfl(sum, gb, 64);
-      const float inv = 1.0f / sum;
-      if (rowok)
-        for (int j = lj; j < t; j += 8) pr[j] = pr[j] * inv;
-    }
-    __syncthreads();
-    if (MF) {
-      // O block (rb x DH) = P . v in 16x16 tiles, k = j over exactly t terms
-      const int nr = (rb + 15) / 16;
-      for (int tl = wave; tl < nr * (DH / 16); tl += 4) {
-        const int br = tl / (DH / 16), bc = tl - br * (DH / 16);
-        const float* a = sp + (16 * br + l16) * ldp + lg;
-        const float* bv = sv + lg * LD + 16 * bc + l16;
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s4 = 0; s4 < t / 4; s4++)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s4], bv[4 * s4 * LD], acc, 0, 0, 0);
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-          const int r = 16 * br + 4 * lg + v;
-          if (r < rb) out[(b * T + r0 + r) * D + h * DH + 16 * bc + l16] = acc[v];
-        }
-      }
-    } else {
-      // O[r][d] = chain over j of fma(P[r][j], v[j][d], acc); operands read
-      // eight j at a time so their LDS reads are in flight together
-      for (int i = tid; i < rb * DH; i += 256) {
-        const int r = i / DH, d = i - r * DH;
-        const float* p = sp + r * ldp;
-        const float* vd = sv + d;
-        float acc = 0.0f;
-        int j = 0;
-        for (; j + 8 <= t; j += 8) {
-          float pv[8], vv[8];
-#pragma unroll
-          for (int u = 0; u < 8; u++) {
-            pv[u] = p[j + u];
-            vv[u] = vd[(j + u) * LD];
-          }
-#pragma unroll
-          for (int u = 0; u < 8; u++) acc = __builtin_fmaf(pv[u], vv[u], acc);
-        }
-        for (; j < t; j++) acc = __builtin_fmaf(p[j], vd[j * LD], acc);
-        out[(b * T + r0 + r) * D + h * DH + d] = acc;
-      }
-    }
-    __syncthreads();
+  for (int i = 0; i < 3; i++) {
+    const int j = wave + 8 * i, cb = j % 6, n = 16 * cb + l16;
+    const int64_t col = (int64_t)(n / 32) * D + h * DH + (n & 31);
+    badd[i] = (bias && j < nblk) ? bias[col] : -0.0f;
   }
+  const unsigned OOB = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(x + (int64_t)b * T * K), 0, T * K * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)wt, 0, (int)(3 * D * K * 4), 0x00020000);
+  // load u of a slab (0..4 per wave): 16-byte chunk q = 64 (5 wave + u) +
+  // lane of the stage; x rows 0..63 (chunks 0..1023), then weight rows
+  // 0..95; chunk position p of row r holds source chunk p ^ (r % 16)
+  unsigned off[5];
+#pragma unroll
+  for (int u = 0; u < 5; u++) {
+    const int q = 64 * (5 * wave + u) + lane;
+    if (q < QA_ROWS * 16) {
+      const int r = q >> 4, c = (q & 15) ^ (r & 15);
+      off[u] = r < T ? (unsigned)((r * K + 4 * c) * 4) : OOB;
+    } else {
+      const int n = (q >> 4) - QA_ROWS, c = (q & 15) ^ (n & 15);
+      const int64_t col = (int64_t)(n / 32) * D + h * DH + (n & 31);
+      off[u] = (unsigned)((col * K + 4 * c) * 4);
+    }
+  }
+  // the loads as inline asm: the compiler then leaves the waits to the
+  // explicit vmcnt counts below (it cannot tell the two stages apart and
+  // would wait for both before every slab's reads)
+  auto issue = [&](int kt, float* st) {
+    const unsigned so = __builtin_amdgcn_readfirstlane((unsigned)(kt * 64 * 4));
+#pragma unroll
+    for (int u = 0; u < 5; u++) {
+      const bool isx = 5 * wave + u < QA_ROWS / 4;   // wave-uniform
+      const unsigned m = __builtin_amdgcn_readfirstlane(
+          (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)(st + 256 * (5 * wave + u)));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // m0 is reserved; nothing else uses it here
+      __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m),
+                       "v"(off[u]), "s"(isx ? xr : wr), "s"(so)
+                       : "m0");
+#pragma clang diagnostic pop
+    }
+  };
+  float* st0 = sm;
+  float* st1 = sm + QA_STAGE;
+  issue(0, st0);
+  if (NK > 1) issue(1, st1);
+  f32x4 acc[3];
+#pragma unroll
+  for (int i = 0; i < 3; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // a wave's blocks j = wave + 8 i; past nblk it multiplies block 0 again
+  // (no branches in the chain; those results are never used)
+  int arow[3], wrow[3];
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    const int j = wave + 8 * i < nblk ? wave + 8 * i : 0, rb = j / 6, cb = j - 6 * rb;
+    arow[i] = (16 * rb + l16) * 64 + lg;
+    wrow[i] = (QA_ROWS + 16 * cb + l16) * 64 + lg;
+  }
+#pragma unroll
+  for (int kt = 0; kt < NK; kt++) {
+    __asm__ volatile("" ::: "memory");
+    if (kt + 1 < NK)
+      wait_vmcnt<5>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    const float* st = (kt & 1) ? st1 : st0;
+    float av[3][16], bv[3][16];
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+      for (int s4 = 0; s4 < 16; s4++) {
+        av[i][s4] = st[arow[i] + 4 * (s4 ^ l16)];
+        bv[i][s4] = st[wrow[i] + 4 * (s4 ^ l16)];
+      }
+#pragma unroll
+    for (int s4 = 0; s4 < 16; s4++)
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][s4], bv[i][s4], acc[i], 0, 0, 0);
+    if (kt + 2 < NK) {
+      // every wave's reads of this stage done, then its refill
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+      __asm__ volatile("" ::: "memory");
+      issue(kt + 2, (kt & 1) ? st1 : st0);
+    }
+  }
+  __syncthreads();   // the stages are free: q, k, v go where they were
+  float* sq = sm;                       // tp x LD (scaled q)
+  float* sk = sq + QA_ROWS * LD;        // tp x LD
+  float* sv = sk + QA_ROWS * LD;        // tp x LD
+  float* sp = sv + QA_ROWS * LD;        // blk (rounded to 16) x (tp + 1)
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    const int j = wave + 8 * i, rb = j / 6, cb = j - 6 * rb;
+    if (j < nblk) {
+      const int n = 16 * cb + l16, which = n / 32, d = n & 31;
+      float* dst = which == 0 ? sq : which == 1 ? sk : sv;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int r = 16 * rb + 4 * lg + v;
+        const float y = acc[i][v] + badd[i];
+        dst[r * LD + d] = r < T ? (which == 0 ? y * scale : y) : 0.0f;   // Mul node on q
+      }
+    }
+  }
+  __syncthreads();
+  attention_rows<DH, true, 512>(sq, sk, sv, sp, T, tp, tp + 1, blk, D,
+                                out + (int64_t)b * T * D + h * DH);
+}
+
+bool qkv_attention_eligible(int64_t batch, int64_t t, int64_t heads, int64_t dh, int64_t k) {
+  return dh == 32 && t > 0 && t <= QA_ROWS && t % 4 == 0 && k % 64 == 0 && k >= 64 &&
+         k <= 256 && batch * heads < (1ll << 31) && 3 * heads * dh * k * 4 < (1ll << 31) &&
+         t * k * 4 < (1ll << 31);
+}
+
+int launch_qkv_attention(const float* x, const float* wt, const float* bias, int64_t batch,
+                         int64_t t, int64_t heads, int64_t dh, int64_t k, float scale, float* out,
+                         hipStream_t s) {
+  if (!qkv_attention_eligible(batch, t, heads, dh, k))
+    return fail(QPH_EUNSUPPORTED, "qkv + attention: shape outside the fused kernel");
+  if ((uintptr_t)x % 16 || (uintptr_t)wt % 16)
+    return fail(QPH_EUNSUPPORTED, "qkv + attention: operands not 16-byte aligned");
+  // the two stages (the attention's q, k, v and scores fit in them after)
+  const size_t lds = (size_t)2 * QA_STAGE * 4;
+  const int blk = (int)t;   // all query rows in one block
+  const dim3 grid((unsigned)(batch * heads));
+  switch (k / 64) {
+    case 1:
+      QPH_TRY(allow_full_lds((const void*)qkv_attention_kernel<1>));
+      hipLaunchKernelGGL(qkv_attention_kernel<1>, grid, dim3(512), lds, s, x, wt, bias, (int)t,
+                         (int)heads, scale, blk, out);
+      break;
+    case 2:
+      QPH_TRY(allow_full_lds((const void*)qkv_attention_kernel<2>));
+      hipLaunchKernelGGL(qkv_attention_kernel<2>, grid, dim3(512), lds, s, x, wt, bias, (int)t,
+                         (int)heads, scale, blk, out);
+      break;
+    case 3:
+      QPH_TRY(allow_full_lds((const void*)qkv_attention_kernel<3>));
+      hipLaunchKernelGGL(qkv_attention_kernel<3>, grid, dim3(512), lds, s, x, wt, bias, (int)t,
+                         (int)heads, scale, blk, out);
+      break;
+    default:
+      QPH_TRY(allow_full_lds((const void*)qkv_attention_kernel<4>));
+      hipLaunchKernelGGL(qkv_attention_kernel<4>, grid, dim3(512), lds, s, x, wt, bias, (int)t,
+                         (int)heads, scale, blk, out);
+      break;
+  }
+  return launch_check("qkv_attention_kernel");
 }
 
 static size_t attention_dh_lds(int64_t t, int64_t dh, int64_t blk, bool mf) {

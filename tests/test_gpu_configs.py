@@ -5,6 +5,8 @@ ids; the fp32 tolerance (1e-4 relative / 1e-5 absolute, argmax ids equal
 except where the top-2 logit gap is below 1e-4) is checked as well, so a
 future kernel that trades exactness for speed still has a stated bar.
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -241,6 +243,8 @@ LINEAR_CASES = [
     (64, 128, 200, True, "none", False, True),       # 2 slabs
     (50, 320, 64, True, "gelu", False, False),       # 5 slabs
     (96, 448, 37, False, "none", True, False),       # 7 slabs, odd N
+    (70, 64, 40, True, "none", False, False),        # 1 slab, ragged rows
+    (40, 128, 96, True, "gelu", True, False),        # 2 slabs
 ]
 
 
@@ -279,6 +283,72 @@ def test_session_linear_shapes(gpu, oracle, case):
     ref = onets.run_graph(g, xin)
     for i, (a, bb) in enumerate(zip(got, ref)):
         assert_bitexact(a, bb, f"output {i}")
+    sess.close()
+
+
+QKV_ATTN_CASES = [
+    # batch, T, K, heads, bias
+    (2, 40, 256, 8, True),    # the rec encoder's shape (one launch for both nodes)
+    (3, 64, 128, 4, True),    # 64 rows: four 16-row blocks, three output blocks a wave
+    (1, 12, 64, 2, False),    # one K slab, one row block, no bias
+    (2, 36, 192, 8, True),    # three slabs, partial last row block
+    (2, 30, 256, 8, True),    # T % 4 != 0: the linear and the attention apart
+    (1, 40, 320, 8, True),    # K = 320: the linear and the attention apart
+]
+
+
+@pytest.mark.parametrize("case", QKV_ATTN_CASES, ids=lambda c: "x".join(map(str, c[:4])) + ("b" if c[4] else ""))
+def test_session_qkv_attention(gpu, oracle, case):
+    """A linear read only by the attention after it (head dimension 32,
+    T <= 64, T % 4 == 0, K a multiple of 64 up to 256) runs with it as one
+    launch, the QKV tensor never stored; other shapes run the two nodes
+    apart.  Bit-exact against the oracle either way."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    b, t, k, heads, has_b = case
+    dh = 32
+    r = nets.WeightRng(b * 1000 + t * 10 + k + heads)
+    g = nets.Graph((b, t, k))
+    w = g.weight(r.kaiming((k, 3 * heads * dh), k))
+    bias = g.weight(r.normal((3 * heads * dh,), 0.1)) if has_b else -1
+    qkv = g.linear(0, w, bias)
+    o = g.attention(qkv, heads, dh, 1.0 / math.sqrt(dh))
+    g.outputs = [o]
+    x = r.normal((b, t, k), 1.0)
+    print(f"qkv + attention {case}", flush=True)
+    sess = nets.HipSession(g)
+    got = sess.run(x)
+    ref = onets.run_graph(g, x)
+    assert_bitexact(got[0], ref[0], "attention output")
+    sess.close()
+
+
+def test_session_layernorm_linear_sequential_rows(gpu, oracle):
+    """LayerNorm (K = 256) then a linear: rows with a huge cancelling pair
+    (+-1e15, +-1e18) make the shuffle-tree f64 sums of the mean unprovable,
+    so those rows take the sequential sum; a constant row and a
+    large-offset row beside ordinary ones; bit-exact against the oracle."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    r = nets.WeightRng(41)
+    rows, k, n = 96, 256, 64
+    g = nets.Graph((1, rows, k))
+    gam = g.weight((1.0 + r.normal((k,), 0.1)).astype(np.float32))
+    bet = g.weight(r.normal((k,), 0.1))
+    x = g.layernorm(0, gam, bet, nets.LN_EPS)
+    w = g.weight(r.kaiming((k, n), k))
+    b = g.weight(r.normal((n,), 0.1))
+    y = g.linear(x, w, b)
+    g.outputs = [y]
+    xin = r.normal((1, rows, k), 1.0)
+    xin[0, 3, 7], xin[0, 3, 200] = 1e15, -1e15
+    xin[0, 17, 0], xin[0, 17, 255] = -1e18, 1e18
+    xin[0, 40, :] = 1e7 + r.normal((k,), 1e-3)
+    xin[0, 41, :] = 3.0
+    sess = nets.HipSession(g)
+    got = sess.run(xin)
+    ref = onets.run_graph(g, xin)
+    assert_bitexact(got[0], ref[0], "layernorm + linear")
     sess.close()
 
 
