@@ -31,7 +31,8 @@ figures for the plain head GEMM of the bit-exact graph.
 
 configs: the five BASELINE workloads, each with its GPU rate, the roofline
 fraction of its bound and the CPU oracle timed on this host (threads set
-explicitly, one warm-up round, then the median of the rounds):
+explicitly, one warm-up round, then the median of at least --cpu-rounds
+rounds, run until each leg has taken 2 s, 5 s for the headline's det and rec):
   cfg1 conv3x3 32->32 @160^2 + bias + ReLU and cfg2a-d depthwise + hardswish:
     the op as a session node with resident weights, replicated over enough
     input/output buffer sets that the sets together exceed 512 MB (twice the
@@ -60,6 +61,8 @@ PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 REC_BATCH = 32
 COLD_BYTES = 512 << 20      # buffer sets per op bench: twice the Infinity Cache
+CPU_HEADLINE_MIN_S = 5.0    # CPU oracle: seconds of timed rounds for det and for rec
+CPU_CONFIG_MIN_S = 2.0      # ... and for each single-op / page config
 
 
 def head_traffic_bytes(name="rec_fused_head_traffic.md"):
@@ -86,7 +89,13 @@ def node_rows(nets, name, g, node_ms):
         ms = node_ms[i]
         row = {"graph": name, "node": i, "op": OP_NAMES.get(d["op"], str(d["op"])),
                "in": list(g.lshapes[d["inp"]]), "w": list(d["ws"]), "us": round(ms * 1e3, 2),
-               "gflop": round(fl / 1e9, 4), "mb": round(by / 1e6, 3), "bound": bound}
+               "gflop": round(fl / 1e9, 4), "mb": round(by / 1e6, 3), "bound": bound,
+               # tensor ids and the bytes "mb" books for them (the input read
+               # once, the output written y_up^2 times), so a launch covering
+               # several nodes can drop a tensor that never leaves it
+               "t_in": d["inp"], "t_out": d["out"],
+               "in_mb": round(g.numel(d["inp"]) * 4 / 1e6, 3),
+               "out_mb": round(g.numel(d["out"]) * d["y_up"] ** 2 * 4 / 1e6, 3)}
         if ms > 0:
             tf, gbs = fl / (ms * 1e-3) / 1e12, by / (ms * 1e-3) / 1e9
             row["tflops"], row["gbs"] = round(tf, 2), round(gbs, 1)
@@ -145,16 +154,18 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_median(fn, rounds):
-    """One warm-up round, then the median wall time of `rounds` rounds (the
-    reference CLI bench discipline, qppocr-cli/src/main.rs:738-818)."""
+def cpu_sample(fn, rounds, min_s=0.0):
+    """One warm-up round, then timed rounds until at least `rounds` have run
+    and together they took `min_s` seconds (the reference CLI bench
+    discipline, qppocr-cli/src/main.rs:738-818, with a time floor so the
+    sample is some seconds of CPU work).  Returns (median seconds, rounds)."""
     fn()
     ts = []
-    for _ in range(rounds):
+    while len(ts) < rounds or (sum(ts) < min_s and len(ts) < 1000000):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
-    return statistics.median(ts)
+    return statistics.median(ts), len(ts)
 
 
 # ------------------------------------------------------------------ GPU side
@@ -234,9 +245,10 @@ def bench_cfg1(nets, ops, configs, ctx, replays, cpu_rounds, O):
                           f"({ob.R * set_bytes >> 20} MB, past the 256 MB Infinity Cache)"}
     if O is not None:
         params = O.conv_params(1, 1, 1, 1)
-        s = cpu_median(lambda: O.conv2d(x, w, b, params, O.ACT_RELU), cpu_rounds)
+        s, n = cpu_sample(lambda: O.conv2d(x, w, b, params, O.ACT_RELU), cpu_rounds,
+                          CPU_CONFIG_MIN_S)
         out["cpu_baseline"] = {"us": round(s * 1e6, 1),
-                               "tflops": round(fl / s / 1e12, 4), "rounds": cpu_rounds}
+                               "tflops": round(fl / s / 1e12, 4), "rounds": n}
     return out
 
 
@@ -270,9 +282,9 @@ def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
             def run_cpu(x=x, w=w, b=b, params=params):
                 y = O.conv2d(x, w, b, params)
                 return O.binary_flat(y, O.hardsigmoid(y), 2)
-            sec = cpu_median(run_cpu, cpu_rounds)
+            sec, n = cpu_sample(run_cpu, cpu_rounds, CPU_CONFIG_MIN_S)
             out["cpu_baseline"] = {"us": round(sec * 1e6, 1), "gbs": round(by / sec / 1e9, 2),
-                                   "rounds": cpu_rounds}
+                                   "rounds": n}
         res["cfg2" + tag] = out
     return res
 
@@ -323,15 +335,15 @@ def cpu_mixed_page(data, rounds):
     det_g, det_x, rw, lines, widths = data
     batches = [(nets.build_rec_graph(rw, len(idx), bw, pipeline.REC_H, probs=False),
                 pipeline.pack_lines(lines, idx, bw)) for bw, idx in pipeline.bucket_plan(widths)]
-    det_s = cpu_median(lambda: onets.run_graph(det_g, det_x), rounds)
+    det_s, det_n = cpu_sample(lambda: onets.run_graph(det_g, det_x), rounds, CPU_CONFIG_MIN_S)
 
     def rec():
         for g, x in batches:
             onets.run_graph(g, x)
-    rec_s = cpu_median(rec, rounds)
+    rec_s, rec_n = cpu_sample(rec, rounds, CPU_CONFIG_MIN_S)
     return {"det_img_per_s": round(1.0 / det_s, 3),
             "rec_lines_per_s": round(len(widths) / rec_s, 2),
-            "ms_per_image": round((det_s + rec_s) * 1e3, 1), "rounds": rounds}
+            "ms_per_image": round((det_s + rec_s) * 1e3, 1), "rounds": [det_n, rec_n]}
 
 
 def main():
@@ -341,7 +353,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-rounds", type=int, default=5,
-                    help="CPU baseline: timed rounds (median) after one warm-up round")
+                    help="CPU baseline: least timed rounds (median) after one warm-up round; "
+                         "more run until the leg's time floor is reached")
     ap.add_argument("--no-configs", action="store_true",
                     help="headline step only (skip the per-config measurements)")
     ap.add_argument("--node-report", default="",
@@ -556,12 +569,13 @@ def main():
         cfgs["cfg5"], mixed_data = time_mixed_page(max(3, K // 5), 2)
 
     if O is not None:
-        det_s = cpu_median(lambda: onets.run_graph(det_g, det_x), args.cpu_rounds)
-        rec_s = cpu_median(lambda: onets.run_graph(rec_g, rec_x), args.cpu_rounds)
-        cfgs["cfg3"]["cpu_baseline"] = {"img_per_s": round(1.0 / det_s, 3),
-                                        "rounds": args.cpu_rounds}
+        det_s, det_n = cpu_sample(lambda: onets.run_graph(det_g, det_x), args.cpu_rounds,
+                                  CPU_HEADLINE_MIN_S)
+        rec_s, rec_n = cpu_sample(lambda: onets.run_graph(rec_g, rec_x), args.cpu_rounds,
+                                  CPU_HEADLINE_MIN_S)
+        cfgs["cfg3"]["cpu_baseline"] = {"img_per_s": round(1.0 / det_s, 3), "rounds": det_n}
         cfgs["cfg4"]["cpu_baseline"] = {"lines_per_s": round(REC_BATCH / rec_s, 2),
-                                        "rounds": args.cpu_rounds}
+                                        "rounds": rec_n}
         if mixed_data is not None:
             cfgs["cfg5"]["cpu_baseline"] = cpu_mixed_page(mixed_data, args.cpu_rounds)
         result["cpu_baseline"] = {
@@ -570,7 +584,8 @@ def main():
             "cores": threads,
             "kind": "port",
             "sample": f"det 1x3x640x640 and rec 32x3x48x320 (pairs exit) on the CPU oracle, each "
-                      f"1 warm-up + median of {args.cpu_rounds} rounds ({det_s:.4f} + {rec_s:.4f} "
+                      f"1 warm-up + median of the rounds in >= {CPU_HEADLINE_MIN_S:.0f} s "
+                      f"({det_n} det, {rec_n} rec rounds; {det_s:.4f} + {rec_s:.4f} "
                       f"s per step), OpenMP {threads} threads of {os.cpu_count()} logical CPUs "
                       f"({cpu_model()}), -O3 -mavx2 -mfma, FTZ/DAZ",
         }

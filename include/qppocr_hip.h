@@ -385,9 +385,10 @@ QPH_API int qph_net_run_async(qph_net* net, int32_t flags);
 QPH_API int qph_net_complete(qph_net* net);
 /* Device pointer of a tensor of the net (valid until destroy).  Tensors that
  * a fused launch consumes inside itself are never written: a depthwise
- * output inside a depthwise + 1x1 block, a stem output inside the first
- * block, the QKV output of a linear + attention launch, a fused head's
- * logits. */
+ * output inside a depthwise + 1x1 block and a stem output inside the first
+ * block keep stale arena storage; the QKV output of a linear + attention
+ * launch and a fused head's logits have none, and asking for them returns
+ * QPH_EINVAL. */
 QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* numel);
 /* Average device time (ms) of each node over the runs since the last reset
  * when profiling is on (events around each node; graph replay disabled).

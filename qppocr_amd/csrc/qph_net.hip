@@ -30,7 +30,7 @@ struct qph_net {
   std::vector<bool> head;        // linear node i and the pairs-only softmax i + 1 run fused
   std::vector<bool> qa_fused;    // linear node i (QKV) and attention node i + 1, one launch
   std::vector<float*> head_part; // per fused head: its per-block argmax partials
-  std::vector<bool> nostore;     // per tensor: never materialised (a fused head's logits)
+  std::vector<bool> nostore;     // per tensor: never materialised (inside one fused launch)
   std::vector<float*> tptr;      // per tensor device pointer
   std::vector<int64_t> pitch;    // per tensor: padded row pitch in floats (0: contiguous)
   char* arena;
@@ -984,6 +984,11 @@ QPH_API int qph_net_destroy(qph_net* net) {
 QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* numel) {
   if (!net || id < 0 || id >= (int32_t)net->tptr.size())
     return fail(QPH_EINVAL, "net_tensor: bad tensor id");
+  // a tensor consumed inside one fused launch (a fused head's logits, the
+  // QKV output of a linear + attention launch) owns no arena bytes: its
+  // pointer would name the next tensor's storage
+  if (net->nostore[(size_t)id])
+    return fail(QPH_EINVAL, "net_tensor: tensor is internal to a fused launch and never stored");
   if (dev_ptr) *dev_ptr = net->tptr[id];
   if (numel) *numel = numel_of(net, id);
   return QPH_OK;

@@ -303,7 +303,7 @@ def test_session_qkv_attention(gpu, oracle, case):
     T <= 64, T % 4 == 0, K a multiple of 64 up to 256) runs with it as one
     launch, the QKV tensor never stored; other shapes run the two nodes
     apart.  Bit-exact against the oracle either way."""
-    from qppocr_amd import nets
+    from qppocr_amd import _lib, nets
     from oracle import nets as onets
     b, t, k, heads, has_b = case
     dh = 32
@@ -320,6 +320,13 @@ def test_session_qkv_attention(gpu, oracle, case):
     got = sess.run(x)
     ref = onets.run_graph(g, x)
     assert_bitexact(got[0], ref[0], "attention output")
+    fused = t % 4 == 0 and k <= 256
+    assert (sess.plan()[0][1] == 2) == fused
+    if fused:   # the QKV tensor has no storage to hand out
+        with pytest.raises(_lib.QphError, match="never stored"):
+            sess.tensor_ptr(qkv)
+    else:
+        assert sess.tensor_ptr(qkv)[1] == b * t * 3 * heads * dh
     sess.close()
 
 
