@@ -408,6 +408,74 @@ QPH_API int qph_net_node_times(qph_net* net, double* ms_per_node, int32_t n);
 QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* kernels,
                          int32_t cap, int32_t* n_launches);
 
+/* ------------------------------------------------------------------------
+ * Sessions over the reference's plan model (qppocr-gpu/src/plan.rs): the
+ * GraphPlan a PlanBuilder produces for one input shape (plan.rs:100-156) is
+ * handed over as plain arrays and run by the HIP kernel set of the Vulkan
+ * backend's dispatch contracts (vulkan/pipeline.rs:84-136, the shaders
+ * qppocr-gpu/shaders/n_*.comp).  The arena holds u32 words: activations NHWC
+ * with channels padded to a multiple of 4, parameter blocks, weights
+ * repacked by nhwc.rs; word 0 is the real batch count (plan.rs:587-593).
+ * Each dispatch computes the CPU operation it stands for in the CPU's
+ * operation order, so outputs are bit-identical to the CPU executor running
+ * the same node sequence (the conv bias rule assumes channel counts that
+ * are multiples of 4; a parameter block carries only the padded ones).
+ * ---------------------------------------------------------------------- */
+
+/* One static segment (GraphPlan.uploads and .upload_init entries). */
+typedef struct qph_plan_upload {
+  uint32_t off;           /* word offset in the arena */
+  uint32_t n_words;
+  const uint32_t* words;  /* host; read during qph_plan_create only */
+} qph_plan_upload;
+
+/* One Dispatch (plan.rs:84-107): kernel = qph_plan_kernel_id(Dispatch.kernel). */
+typedef struct qph_plan_dispatch {
+  int32_t kernel;
+  uint32_t p_off;         /* word offset of the parameter block */
+  uint32_t groups[3];     /* the dispatch grid; groups[1] carries the batch of the
+                             conv / pool / resize family, groups[0] that of n_reduce_fin */
+} qph_plan_dispatch;
+
+typedef struct qph_plan_spec {
+  uint32_t total_words;                 /* GraphPlan.total_words */
+  int32_t n_uploads;
+  const qph_plan_upload* uploads;
+  int32_t n_dispatches;
+  const qph_plan_dispatch* dispatches;  /* in execution order */
+  uint32_t in_f32_off;                  /* GraphPlan.in_f32_off: the NCHW f32 input */
+  int64_t in_numel;
+  int32_t n_outputs;                    /* GraphPlan.out_offs */
+  const uint32_t* out_offs;
+  const int64_t* out_numel;             /* words per output ((value, index) pairs: rows * 2) */
+} qph_plan_spec;
+
+typedef struct qph_plan qph_plan;
+
+/* KernelSet lookup by Dispatch.kernel name (vulkan/pipeline.rs:84-136):
+ * the id, or QPH_EUNSUPPORTED for a kernel outside the set (the Metal-only
+ * n_conv8_mma*, n_conv8h, n_conv_dw_tile, n_convt4w, n_head_argmax). */
+QPH_API int qph_plan_kernel_id(const char* name);
+/* The session's load step (vulkan/session.rs): allocates the arena,
+ * writes the uploads, decodes every parameter block (refusing regions
+ * outside the arena, unknown kernels and malformed blocks with the
+ * dispatch's index) and captures the launches into a HIP graph. */
+QPH_API int qph_plan_create(qph_ctx* ctx, const qph_plan_spec* spec, qph_plan** out);
+QPH_API int qph_plan_destroy(qph_plan* plan);
+/* real_n for the following runs (0 = every batch row): the reference's run
+ * writes it to word 0 before each submit. */
+QPH_API int qph_plan_set_real_n(qph_plan* plan, uint32_t real_n);
+/* One run: input (numel = in_numel) to in_f32_off, the dispatches, then
+ * the outputs to the host buffers (NULL entries skipped) and a sync.
+ * input NULL: the arena's input region is used as it is. */
+QPH_API int qph_plan_run(qph_plan* plan, const float* input, int32_t input_is_device,
+                         float* const* outputs_host);
+/* The device arena (valid until destroy), for reading any region. */
+QPH_API int qph_plan_arena(qph_plan* plan, float** dev, int64_t* words);
+/* Number of launches the decoded plan issues per run (an n_reduce_hw and
+ * its n_reduce_fin are one).  No counterpart in the reference. */
+QPH_API int qph_plan_launches(qph_plan* plan, int32_t* n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,22 @@ class NetSpec(ctypes.Structure):
                 ("outputs", ctypes.POINTER(I32)), ("flags", I32)]
 
 
+class PlanUpload(ctypes.Structure):
+    _fields_ = [("off", ctypes.c_uint32), ("n_words", ctypes.c_uint32), ("words", P)]
+
+
+class PlanDispatch(ctypes.Structure):
+    _fields_ = [("kernel", I32), ("p_off", ctypes.c_uint32), ("groups", ctypes.c_uint32 * 3)]
+
+
+class PlanSpec(ctypes.Structure):
+    _fields_ = [("total_words", ctypes.c_uint32), ("n_uploads", I32),
+                ("uploads", ctypes.POINTER(PlanUpload)), ("n_dispatches", I32),
+                ("dispatches", ctypes.POINTER(PlanDispatch)), ("in_f32_off", ctypes.c_uint32),
+                ("in_numel", I64), ("n_outputs", I32), ("out_offs", ctypes.POINTER(ctypes.c_uint32)),
+                ("out_numel", ctypes.POINTER(I64))]
+
+
 # exported symbol -> (argtypes, restype); every symbol include/qppocr_hip.h declares
 SIGNATURES = {
     "qph_ctx_create": ([ctypes.c_int, ctypes.POINTER(P)], ctypes.c_int),
@@ -113,6 +129,13 @@ SIGNATURES = {
     "qph_net_set_profiling": ([P, I32], ctypes.c_int),
     "qph_net_node_times": ([P, ctypes.POINTER(ctypes.c_double), I32], ctypes.c_int),
     "qph_net_plan": ([P, P, P, P, I32, P], ctypes.c_int),
+    "qph_plan_kernel_id": ([ctypes.c_char_p], ctypes.c_int),
+    "qph_plan_create": ([P, ctypes.POINTER(PlanSpec), ctypes.POINTER(P)], ctypes.c_int),
+    "qph_plan_destroy": ([P], ctypes.c_int),
+    "qph_plan_set_real_n": ([P, ctypes.c_uint32], ctypes.c_int),
+    "qph_plan_run": ([P, P, I32, P], ctypes.c_int),
+    "qph_plan_arena": ([P, ctypes.POINTER(P), ctypes.POINTER(I64)], ctypes.c_int),
+    "qph_plan_launches": ([P, ctypes.POINTER(I32)], ctypes.c_int),
 }
 
 _lib = None

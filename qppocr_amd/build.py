@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "libqppocr_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["qph_runtime.hip", "qph_gemm.hip", "qph_conv.hip", "qph_block.hip", "qph_rows.hip",
-           "qph_net.hip", "qph_aux.hip"]
+           "qph_net.hip", "qph_aux.hip", "qph_plan.hip"]
 
 CFLAGS = [
     "--offload-arch=gfx950",

@@ -319,6 +319,11 @@ int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s);
 int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
                           float* probs, float* pairs, hipStream_t s);
 int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, hipStream_t s);
+int launch_argmax_pitched(const float* probs, int64_t rows, int64_t cols, int64_t ld,
+                          float* pairs, hipStream_t s);
+// logits rows ld floats apart, probabilities rows ldo floats apart (either may be NULL)
+int launch_softmax_pitched(const float* logits, int64_t rows, int64_t cols, int64_t ld,
+                           float* probs, int64_t ldo, float* pairs, hipStream_t s);
 int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
                      float scale, float* out, hipStream_t s);
 int launch_attention_generic(const float* qkv, int64_t batch, int64_t t, int64_t heads,
@@ -332,6 +337,11 @@ int launch_mask_pairs(float* pairs, int64_t batch, int64_t t, const int32_t* t_v
                       hipStream_t s);
 // reduce_mean over the last axis (also GlobalAveragePool: rows = N*C planes)
 int launch_reduce_mean(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t s);
+// row r's element j at x[(r / rpg) * gstride + (r % rpg) * rstride + j * estride],
+// its mean to out[r * ostride] (ostride 4: the row's other three words set to 0)
+int launch_reduce_mean_rows(const float* x, int64_t rows, int64_t cols, int64_t rpg,
+                            int64_t gstride, int64_t rstride, int64_t estride, float* out,
+                            int64_t ostride, hipStream_t s);
 
 // qph_aux.hip.  ctot / coff: the output is channels [coff, coff + c) of a
 // tensor with ctot channels (ctot = c, coff = 0 for a plain output).

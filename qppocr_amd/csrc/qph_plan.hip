@@ -1,0 +1,1180 @@
+// The reference's whole-graph plan model (qppocr-gpu/src/plan.rs) on HIP.
+//
+// The reference's Vulkan and Metal sessions consume a GraphPlan
+// (plan.rs:100-156): one arena of u32 words that holds the activations
+// NHWC with channels padded to a multiple of 4 (plan.rs:10-17), the
+// parameter blocks and the repacked weights (nhwc.rs:28-204), plus a
+// dispatch list naming a kernel of the backend's set
+// (vulkan/pipeline.rs:84-136) and the word offset of its parameter block.
+// This file is the HIP backend's kernel set for those dispatches.
+// qph_plan_create copies the static words into a device arena, decodes
+// every parameter block once on the host, checks every region a dispatch
+// names against the arena, and captures the launches into a HIP graph;
+// qph_plan_run replays it.
+//
+// Numerics: each dispatch computes the CPU operation it stands for with the
+// CPU's operation order, so a plan's outputs are bit-identical to the CPU
+// executor running the same node sequence:
+//  - n_conv / n_conv8: the conv chain in the CPU's k order (channel, ky,
+//    kx) with its bias placement (conv.rs:264-661, gemm.rs:7-16), then the
+//    activation, then the residual.  The rule needs the real output channel
+//    count and the real input channel count, which a parameter block does
+//    not carry (only their padded values); they are exact when both are
+//    multiples of 4, as in every det and rec conv.
+//  - n_conv_dw: acc = fma(w, x, acc) over ky then kx, + bias (conv.rs:461-505).
+//  - n_convt: the chain over input channels from 0, + bias, activation.
+//  - n_elem / n_channel: the separately rounded IEEE ops of the CPU nodes,
+//    exp1-based sigmoid, fma-based HardSigmoid (activation.rs:168-201).
+//  - n_reduce_last, n_reduce_hw + n_reduce_fin: f64 means (shape.rs:510-560,
+//    pool2d.rs:10-29); the pair is run as one launch.
+//  - n_softmax: the reference softmax (activation.rs:321-403);
+//    n_exit3_argmax the first strict maximum (rec.rs:46-54).
+//  - n_attn_mm: the batched MatMul's k-ascending fma chains (shape.rs:568-698).
+// Real-batch early exit: word 0 of the arena holds real_n (plan.rs:587-593);
+// the entry, exit3, pool, depthwise, conv and channel kernels skip batch
+// rows past it as the reference's kernels do; the GEMM-based dispatches
+// compute the padded rows too (never read).
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "qph_internal.h"
+
+namespace qph {
+
+namespace {
+
+constexpr uint32_t OFF_NONE = 0xFFFFFFFFu;
+
+const char* const kPlanKernels[] = {
+    "n_entry",   "n_exit",      "n_exit3",     "n_exit3_argmax", "n_elem",
+    "n_channel", "n_conv",      "n_conv8",     "n_conv_dw",      "n_convt",
+    "n_pool",    "n_reduce_hw", "n_reduce_fin", "n_reduce_last", "n_resize",
+    "n_transpose", "n_transpose_nd", "n_concat_c", "n_softmax",  "n_attn_mm"};
+constexpr int kNumPlanKernels = (int)(sizeof(kPlanKernels) / sizeof(kPlanKernels[0]));
+enum {
+  PK_ENTRY, PK_EXIT, PK_EXIT3, PK_EXIT3_ARGMAX, PK_ELEM, PK_CHANNEL, PK_CONV, PK_CONV8,
+  PK_CONV_DW, PK_CONVT, PK_POOL, PK_REDUCE_HW, PK_REDUCE_FIN, PK_REDUCE_LAST, PK_RESIZE,
+  PK_TRANSPOSE, PK_TRANSPOSE_ND, PK_CONCAT_C, PK_SOFTMAX, PK_ATTN_MM
+};
+
+__device__ __forceinline__ unsigned real_n(const float* arena) {
+  return *(const unsigned*)arena;
+}
+
+__device__ __forceinline__ float4 act4(float4 v, const Act& a) {
+  return make_float4(act_apply(v.x, a), act_apply(v.y, a), act_apply(v.z, a), act_apply(v.w, a));
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// ------------------------------------------------------------ entry / exit
+
+// f32 NCHW [nb][c][h][w] -> NHWC [nb][h][w][cpad], pad channels 0 (n_entry.comp).
+struct EntryK { const float* arena; const float* x; float* y; int64_t nb, c, hw, cp4; };
+__global__ __launch_bounds__(256) void plan_entry_kernel(EntryK p) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.nb * p.hw) return;
+  const int64_t n = gid / p.hw, pos = gid - n * p.hw;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && n >= rn) return;
+  const float* xn = p.x + n * p.c * p.hw + pos;
+  float4* yo = (float4*)p.y + gid * p.cp4;
+  for (int64_t c4 = 0; c4 < p.cp4; c4++) {
+    const int64_t b = c4 * 4;
+    float4 v;
+    v.x = b + 0 < p.c ? xn[(b + 0) * p.hw] : 0.0f;
+    v.y = b + 1 < p.c ? xn[(b + 1) * p.hw] : 0.0f;
+    v.z = b + 2 < p.c ? xn[(b + 2) * p.hw] : 0.0f;
+    v.w = b + 3 < p.c ? xn[(b + 3) * p.hw] : 0.0f;
+    yo[c4] = v;
+  }
+}
+
+// NHWC -> NCHW, pad channels dropped, optional sigmoid (n_exit.comp).
+struct ExitK { const float* x; float* y; int64_t nb, c, hw, cpad; int sigmoid; };
+__global__ __launch_bounds__(256) void plan_exit_kernel(ExitK p) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.nb * p.hw) return;
+  const int64_t n = gid / p.hw, pos = gid - n * p.hw;
+  const float* xr = p.x + gid * p.cpad;
+  float* yn = p.y + n * p.c * p.hw + pos;
+  for (int64_t c = 0; c < p.c; c++) {
+    const float v = xr[c];
+    yn[c * p.hw] = p.sigmoid ? sigmoid1(v) : v;
+  }
+}
+
+// rows x cpad -> rows x cols (n_exit3.comp).
+struct Exit3K { const float* arena; const float* x; float* y; int64_t rows, cols, cpad, rpb; };
+__global__ __launch_bounds__(256) void plan_exit3_kernel(Exit3K p) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.rows * p.cols) return;
+  const int64_t row = gid / p.cols, col = gid - row * p.cols;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && row >= (int64_t)rn * p.rpb) return;
+  p.y[gid] = p.x[row * p.cpad + col];
+}
+
+// ------------------------------------------------------- elementwise ops
+
+// n_elem.comp op codes: 0 relu, 1 sigmoid, 2 hardsigmoid(p1, p2), 3 clip(p1, p2),
+// 4 add, 5 mul, 6 + scalar, 7 * scalar, 8 - row value, 9 square, 10 sqrt,
+// 11 / row value, 12 sub, 13 div.  One IEEE operation per element, as the
+// CPU nodes (elementwise.rs:40-62, activation.rs:168-239).
+struct ElemK { const float* a; const float* b; float* y; int64_t nv; int op; float p1, p2; int64_t c4; };
+
+__device__ __forceinline__ float elem1(int op, float a, float b, float p1, float p2) {
+  switch (op) {
+    case 0: return relu1(a);
+    case 1: return sigmoid1(a);
+    case 2: return hsig1(a, p1, p2);
+    case 3: {  // clip_seg_scalar (activation.rs:223-229)
+      const float m = a < p1 ? p1 : a;
+      return p2 < m ? p2 : m;
+    }
+    case 4: case 6: return a + b;
+    case 5: case 7: return a * b;
+    case 8: case 12: return a - b;
+    case 9: return a * a;  // Pow with the constant exponent 2: powf(a, 2) is a * a rounded
+    case 10: return __builtin_sqrtf(a);
+    default: return a / b;  // 11, 13
+  }
+}
+
+__global__ __launch_bounds__(256) void plan_elem_kernel(ElemK p) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.nv) return;
+  const float4 a = ((const float4*)p.a)[i];
+  float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (p.op == 4 || p.op == 5 || p.op == 12 || p.op == 13) {
+    b = ((const float4*)p.b)[i];
+  } else if (p.op == 6 || p.op == 7) {
+    const float s = p.b[0];
+    b = make_float4(s, s, s, s);
+  } else if (p.op == 8 || p.op == 11) {
+    const float s = p.b[(i / p.c4) * 4];
+    b = make_float4(s, s, s, s);
+  }
+  float4 o;
+  o.x = elem1(p.op, a.x, b.x, p.p1, p.p2);
+  o.y = elem1(p.op, a.y, b.y, p.p1, p.p2);
+  o.z = elem1(p.op, a.z, b.z, p.p1, p.p2);
+  o.w = elem1(p.op, a.w, b.w, p.p1, p.p2);
+  ((float4*)p.y)[i] = o;
+}
+
+// n_channel.comp: per-channel gate broadcast over the feature rows; gate row
+// = feature row / hw.  0 a*g, 1 a+g, 2 a*g + r (MulAddScale, two roundings,
+// elementwise.rs:134-179), 3 a * hardsigmoid(g), 4 a * sigmoid(g), 5 a*g + r[gate row].
+struct ChannelK {
+  const float* arena; const float* a; const float* g; const float* r; float* y;
+  int64_t nv, c4, hw; int op; float p1, p2;
+};
+__global__ __launch_bounds__(256) void plan_channel_kernel(ChannelK p) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.nv) return;
+  const int64_t c4 = i % p.c4, frow = i / p.c4, grow = frow / p.hw;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && frow >= (int64_t)rn * p.hw) return;
+  const float4 a = ((const float4*)p.a)[i];
+  const float4 g = ((const float4*)p.g)[grow * p.c4 + c4];
+  float4 o;
+  switch (p.op) {
+    case 0: o = make_float4(a.x * g.x, a.y * g.y, a.z * g.z, a.w * g.w); break;
+    case 1: o = add4(a, g); break;
+    case 2: case 5: {
+      const float4 r = ((const float4*)p.r)[p.op == 2 ? i : grow * p.c4 + c4];
+      o = add4(make_float4(a.x * g.x, a.y * g.y, a.z * g.z, a.w * g.w), r);
+      break;
+    }
+    case 3:
+      o = make_float4(a.x * hsig1(g.x, p.p1, p.p2), a.y * hsig1(g.y, p.p1, p.p2),
+                      a.z * hsig1(g.z, p.p1, p.p2), a.w * hsig1(g.w, p.p1, p.p2));
+      break;
+    default:
+      o = make_float4(a.x * sigmoid1(g.x), a.y * sigmoid1(g.y), a.z * sigmoid1(g.z),
+                      a.w * sigmoid1(g.w));
+      break;
+  }
+  ((float4*)p.y)[i] = o;
+}
+
+// ------------------------------------------------------------ dense conv
+//
+// NHWC conv on v_mfma_f32_16x16x4f32: a wave owns 16 output channels x 64
+// output pixels (four 16x16 blocks sharing the weight operand).  K runs in
+// the CPU's order k = c * taps + t (t = ky * kw + kx); the weights are the
+// plan's repack w[(t * cin + c) * N + co] (nhwc.rs:28-57).  Out-of-image taps
+// and pad channels contribute 0 (the padded channels come last in k, so
+// their +0 terms leave the chain as it was).  The bias enters the chain first
+// where the CPU seeds it (rule below), else it is added after; then the
+// activation; then the residual.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct ConvK {
+  const float* arena; const float* x; const float* w; const float* bias; const float* res;
+  float* y;
+  int64_t P, N, ow, oh, iw, ih, cin, taps, kw, sh, sw, pt, pl;
+  int rule_kind;   // 0 pointwise sgemm (M = N, N = P), 1 implicit GEMM per row, 2 im2col tiles
+  int rule_path;   // 0 panel, 1 m-rows (pointwise only)
+  int64_t tile;    // im2col tile height
+  Act act;
+};
+
+__device__ __forceinline__ bool conv_seeded(const ConvK& p, int64_t co, int64_t px) {
+  if (p.rule_kind == 0) return bias_seeded(p.rule_path, co, px, p.N, p.P);
+  const int64_t oy = px / p.ow, ox = px - oy * p.ow;
+  if (p.rule_kind == 1) return bias_seeded(0, co, ox, p.N, p.ow);
+  const int64_t t0 = (oy / p.tile) * p.tile;
+  const int64_t rows = min(p.tile, p.oh - t0);
+  return bias_seeded(0, co, (oy - t0) * p.ow + ox, p.N, rows * p.ow);
+}
+
+__global__ __launch_bounds__(256) void plan_conv_kernel(ConvK p) {
+  const int64_t b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && b >= rn) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t ncob = (p.N + 15) / 16;
+  const int64_t co0 = (wave % ncob) * 16, px0 = (wave / ncob) * 64;
+  if (px0 >= p.P) return;
+  const int li = lane & 15, kq = lane >> 4;
+  // operand A: row co = co0 + li; operand B of block j: pixel px0 + 16 j + li
+  const int64_t co_a = co0 + li;
+  const bool co_ok = co_a < p.N;
+  int64_t oyb[4], oxb[4];
+  bool pok[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int64_t px = px0 + 16 * j + li;
+    pok[j] = px < p.P;
+    oyb[j] = pok[j] ? (px / p.ow) * p.sh - p.pt : 0;
+    oxb[j] = pok[j] ? (px % p.ow) * p.sw - p.pl : 0;
+  }
+  const float* xb = p.x + b * p.ih * p.iw * p.cin;
+  // accumulators: lane holds rows co0 + 4 kq + v, column px0 + 16 j + li
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int64_t px = px0 + 16 * j + li;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int64_t co = co0 + 4 * kq + v;
+      acc[j][v] = (p.bias && co < p.N && px < p.P && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
+    }
+  }
+  const int64_t K = p.cin * p.taps;
+  for (int64_t k0 = 0; k0 < K; k0 += 4) {
+    const int64_t k = k0 + kq;
+    const int64_t c = k / p.taps, t = k - c * p.taps;
+    const int64_t ky = t / p.kw, kx = t - ky * p.kw;
+    const float a = co_ok ? p.w[(t * p.cin + c) * p.N + co_a] : 0.0f;
+    float bv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int64_t iy = oyb[j] + ky, ix = oxb[j] + kx;
+      const bool in = pok[j] && iy >= 0 && iy < p.ih && ix >= 0 && ix < p.iw;
+      bv[j] = in ? xb[(iy * p.iw + ix) * p.cin + c] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[j], acc[j], 0, 0, 0);
+  }
+  const int64_t cob = co0 + 4 * kq;  // multiple of 4, N % 4 == 0: the four rows are all in or out
+  if (cob >= p.N) return;
+  const float* yres = p.res ? p.res + b * p.P * p.N : nullptr;
+  float* yb = p.y + b * p.P * p.N;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int64_t px = px0 + 16 * j + li;
+    if (px >= p.P) continue;
+    float o[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float x = acc[j][v];
+      if (p.bias && !conv_seeded(p, cob + v, px)) x = x + p.bias[cob + v];
+      x = act_apply(x, p.act);
+      if (yres) x = x + yres[px * p.N + cob + v];
+      o[v] = x;
+    }
+    *(float4*)(yb + px * p.N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// ------------------------------------------------------------- depthwise
+struct DwK {
+  const float* arena; const float* x; const float* w; const float* bias; const float* res;
+  float* y;
+  int64_t P, c4, ow, iw, ih, taps, kw, sh, sw, pt, pl;
+  Act act;
+};
+__global__ __launch_bounds__(256) void plan_dw_kernel(DwK p) {
+  const int64_t b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && b >= rn) return;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.P * p.c4) return;
+  const int64_t c4 = gid % p.c4, m = gid / p.c4;
+  const int64_t oy = m / p.ow, ox = m - oy * p.ow;
+  const float4* xb = (const float4*)p.x + b * p.ih * p.iw * p.c4;
+  const float4* w4 = (const float4*)p.w;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int64_t t = 0; t < p.taps; t++) {
+    const int64_t ky = t / p.kw, kx = t - ky * p.kw;
+    const int64_t iy = oy * p.sh - p.pt + ky, ix = ox * p.sw - p.pl + kx;
+    float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (iy >= 0 && iy < p.ih && ix >= 0 && ix < p.iw) xv = xb[(iy * p.iw + ix) * p.c4 + c4];
+    const float4 wv = w4[t * p.c4 + c4];
+    acc.x = __builtin_fmaf(wv.x, xv.x, acc.x);
+    acc.y = __builtin_fmaf(wv.y, xv.y, acc.y);
+    acc.z = __builtin_fmaf(wv.z, xv.z, acc.z);
+    acc.w = __builtin_fmaf(wv.w, xv.w, acc.w);
+  }
+  // yc = acc + bv with bv = 0 when there is no bias (conv.rs:461-505)
+  const float4 bv = p.bias ? ((const float4*)p.bias)[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float4 o = act4(add4(acc, bv), p.act);
+  if (p.res) o = add4(o, ((const float4*)p.res)[b * p.P * p.c4 + gid]);
+  ((float4*)p.y)[b * p.P * p.c4 + gid] = o;
+}
+
+// ------------------------------------------------------- conv transpose
+// every output pixel from one tap (kh <= sh, kw <= sw): the chain over the
+// (padded) input channels from 0, + bias, activation (n_convt.comp layout)
+struct ConvtK {
+  const float* x; const float* w; const float* bias; float* y;
+  int64_t P, nv, ow, iw, ih, cin, sh, sw, kw;
+  Act act;
+};
+__global__ __launch_bounds__(256) void plan_convt_kernel(ConvtK p) {
+  const int64_t b = blockIdx.y;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.P * p.nv) return;
+  const int64_t n4 = gid % p.nv, m = gid / p.nv;
+  const int64_t oy = m / p.ow, ox = m - oy * p.ow;
+  const int64_t iy = oy / p.sh, ky = oy - iy * p.sh, ix = ox / p.sw, kx = ox - ix * p.sw;
+  const int64_t tap = ky * p.kw + kx;
+  const float* xr = p.x + (b * p.ih * p.iw + iy * p.iw + ix) * p.cin;
+  const float4* w4 = (const float4*)p.w + tap * p.cin * p.nv + n4;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int64_t ci = 0; ci < p.cin; ci++) {
+    const float xv = xr[ci];
+    const float4 wv = w4[ci * p.nv];
+    acc.x = __builtin_fmaf(xv, wv.x, acc.x);
+    acc.y = __builtin_fmaf(xv, wv.y, acc.y);
+    acc.z = __builtin_fmaf(xv, wv.z, acc.z);
+    acc.w = __builtin_fmaf(xv, wv.w, acc.w);
+  }
+  if (p.bias) acc = add4(acc, ((const float4*)p.bias)[n4]);
+  ((float4*)p.y)[b * p.P * p.nv + gid] = act4(acc, p.act);
+}
+
+// ------------------------------------------------------------------ pool
+// pool2d.rs:94-259 on NHWC (see pool2d_kernel for the arithmetic)
+struct PoolNK {
+  const float* arena; const float* x; float* y;
+  int64_t P, c4, ow, iw, ih, kh, kw, sh, sw, pt, pl;
+  int max_pool, special;
+};
+__device__ __forceinline__ float pool_acc(bool mx, float acc, float t) {
+  return mx ? (t > acc ? t : acc) : acc + t;
+}
+__global__ __launch_bounds__(256) void plan_pool_kernel(PoolNK p) {
+  const int64_t b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && b >= rn) return;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.P * p.c4) return;
+  const int64_t c4 = gid % p.c4, m = gid / p.c4;
+  const int64_t oy = m / p.ow, ox = m - oy * p.ow;
+  const float4* xb = (const float4*)p.x + b * p.ih * p.iw * p.c4;
+  float4 o;
+  if (p.special) {  // 2x2 stride 1 SAME_UPPER max (pool2x2_row_scalar, pool2d.rs:242-259)
+    const bool r1 = oy + 1 < p.ih;
+    const float4 a0 = xb[(oy * p.iw + ox) * p.c4 + c4];
+    float4 va = a0;
+    if (r1) {
+      const float4 a1 = xb[((oy + 1) * p.iw + ox) * p.c4 + c4];
+      va = make_float4(fmaxf(a0.x, a1.x), fmaxf(a0.y, a1.y), fmaxf(a0.z, a1.z), fmaxf(a0.w, a1.w));
+    }
+    float4 vb = make_float4(-3.40282347e38f, -3.40282347e38f, -3.40282347e38f, -3.40282347e38f);
+    if (ox + 1 < p.iw) {
+      const float4 b0 = xb[(oy * p.iw + ox + 1) * p.c4 + c4];
+      vb = b0;
+      if (r1) {
+        const float4 b1 = xb[((oy + 1) * p.iw + ox + 1) * p.c4 + c4];
+        vb = make_float4(fmaxf(b0.x, b1.x), fmaxf(b0.y, b1.y), fmaxf(b0.z, b1.z), fmaxf(b0.w, b1.w));
+      }
+    }
+    o = make_float4(fmaxf(va.x, vb.x), fmaxf(va.y, vb.y), fmaxf(va.z, vb.z), fmaxf(va.w, vb.w));
+  } else {
+    const bool mx = p.max_pool;
+    const float init = mx ? -3.4e38f : 0.0f;
+    float4 acc = make_float4(init, init, init, init);
+    for (int64_t ky = 0; ky < p.kh; ky++) {
+      const int64_t iy = oy * p.sh - p.pt + ky;
+      if (iy < 0 || iy >= p.ih) continue;
+      for (int64_t kx = 0; kx < p.kw; kx++) {
+        const int64_t ix = ox * p.sw - p.pl + kx;
+        if (ix < 0 || ix >= p.iw) continue;
+        const float4 t = xb[(iy * p.iw + ix) * p.c4 + c4];
+        acc = make_float4(pool_acc(mx, acc.x, t.x), pool_acc(mx, acc.y, t.y),
+                          pool_acc(mx, acc.z, t.z), pool_acc(mx, acc.w, t.w));
+      }
+    }
+    if (!mx) {
+      const float area = (float)(p.kh * p.kw);
+      acc = make_float4(acc.x / area, acc.y / area, acc.z / area, acc.w / area);
+    }
+    o = acc;
+  }
+  ((float4*)p.y)[b * p.P * p.c4 + gid] = o;
+}
+
+// ------------------------------------------------------ nearest resize
+// resize.rs:26-57: iy = min((int)((float)oy * (float)H / (float)oh), H - 1)
+struct ResizeNK { const float* x; float* y; int64_t P, c4, ow, oh, iw, ih; };
+__global__ __launch_bounds__(256) void plan_resize_kernel(ResizeNK p) {
+  const int64_t b = blockIdx.y;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.P * p.c4) return;
+  const int64_t c4 = gid % p.c4, m = gid / p.c4;
+  const int64_t oy = m / p.ow, ox = m - oy * p.ow;
+  int64_t iy = (int64_t)((float)oy * (float)p.ih / (float)p.oh);
+  int64_t ix = (int64_t)((float)ox * (float)p.iw / (float)p.ow);
+  if (iy > p.ih - 1) iy = p.ih - 1;
+  if (ix > p.iw - 1) ix = p.iw - 1;
+  const float4* xb = (const float4*)p.x + b * p.ih * p.iw * p.c4;
+  ((float4*)p.y)[b * p.P * p.c4 + gid] = xb[(iy * p.iw + ix) * p.c4 + c4];
+}
+
+// ------------------------------------------------------ data movement
+struct Transpose2K { const float* x; float* y; int64_t r, c; };
+__global__ __launch_bounds__(256) void plan_transpose2_kernel(Transpose2K p) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.r * p.c) return;
+  const int64_t x = i / p.r, y = i - x * p.r;  // out[x][y] = in[y][x]
+  p.y[i] = p.x[y * p.c + x];
+}
+
+struct TransposeNK { const float* x; float* y; int64_t total; int rank; int64_t dims[5]; int perm[5]; };
+__global__ __launch_bounds__(256) void plan_transpose_nd_kernel(TransposeNK p) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.total) return;
+  int64_t oc[5] = {0, 0, 0, 0, 0}, ic[5] = {0, 0, 0, 0, 0};
+  int64_t rem = i;
+  for (int d = p.rank - 1; d >= 0; d--) {
+    const int64_t od = p.dims[p.perm[d]];
+    oc[d] = rem % od;
+    rem /= od;
+  }
+  for (int d = 0; d < p.rank; d++) ic[p.perm[d]] = oc[d];
+  int64_t src = 0;
+  for (int d = 0; d < p.rank; d++) src = src * p.dims[d] + ic[d];
+  p.y[i] = p.x[src];
+}
+
+struct ConcatK { const float* arena; float* y; int64_t hw, outc4; int n; uint32_t src[8]; int64_t c4len[8]; };
+__global__ __launch_bounds__(256) void plan_concat_kernel(ConcatK p) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.hw * p.outc4) return;
+  const int64_t c4 = gid % p.outc4, pos = gid / p.outc4;
+  int64_t acc = 0;
+  for (int i = 0; i < p.n; i++) {
+    if (c4 < acc + p.c4len[i]) {
+      const float4* s = (const float4*)(p.arena + p.src[i]);
+      ((float4*)p.y)[gid] = s[pos * p.c4len[i] + (c4 - acc)];
+      return;
+    }
+    acc += p.c4len[i];
+  }
+}
+
+// pad columns [cols, cpad) of rows x cpad set to 0 (n_softmax.comp's tail)
+struct PadColsK { float* y; int64_t rows, cols, cpad; };
+__global__ __launch_bounds__(256) void plan_pad_cols_kernel(PadColsK p) {
+  const int64_t w = p.cpad - p.cols;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.rows * w) return;
+  const int64_t r = i / w;
+  p.y[r * p.cpad + p.cols + (i - r * w)] = 0.0f;
+}
+
+inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+// ------------------------------------------------------------ the plan
+
+struct PlanUpload {
+  uint32_t off, n;
+  const uint32_t* words;
+};
+
+}  // namespace qph
+
+struct qph_plan {
+  qph_ctx* ctx;
+  uint32_t total_words;
+  float* arena;
+  std::vector<std::function<int(hipStream_t)>> launches;
+  std::vector<int32_t> launch_dispatch;  // first dispatch of each launch
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+  bool graph_ready;
+  uint32_t in_off;
+  int64_t in_numel;
+  std::vector<uint32_t> out_off;
+  std::vector<int64_t> out_numel;
+  uint32_t real_n;
+};
+
+namespace qph {
+namespace {
+
+struct Decoder {
+  qph_plan* pl;
+  std::vector<PlanUpload> ups;  // sorted by offset
+  int idx = 0;
+  const char* kname = "";
+  uint32_t p_off = 0;
+
+  std::string where() const {
+    return "plan dispatch " + std::to_string(idx) + " (" + kname + ", params at word " +
+           std::to_string(p_off) + ")";
+  }
+  // the parameter block [p_off, p_off + n) from the uploaded static words
+  int params(uint32_t n, const uint32_t** out) {
+    auto it = std::upper_bound(ups.begin(), ups.end(), p_off,
+                               [](uint32_t v, const PlanUpload& u) { return v < u.off; });
+    if (it == ups.begin()) return fail(QPH_EINVAL, where() + ": parameter block not uploaded");
+    --it;
+    if ((uint64_t)p_off + n > (uint64_t)it->off + it->n)
+      return fail(QPH_EINVAL, where() + ": parameter block shorter than " + std::to_string(n) +
+                                  " words");
+    *out = it->words + (p_off - it->off);
+    return QPH_OK;
+  }
+  // a region of n words at off inside the arena (16-byte aligned for vec4 access)
+  int region(uint32_t off, uint64_t n, bool vec4, const char* what) {
+    if (off == OFF_NONE || (uint64_t)off + n > pl->total_words)
+      return fail(QPH_EINVAL, where() + ": " + what + " [" + std::to_string(off) + ", +" +
+                                  std::to_string(n) + ") outside the arena of " +
+                                  std::to_string(pl->total_words) + " words");
+    if (vec4 && off % 4)
+      return fail(QPH_EINVAL, where() + ": " + what + " not 16-byte aligned");
+    return QPH_OK;
+  }
+  float* at(uint32_t off) const { return pl->arena + off; }
+};
+
+inline float f32_of(uint32_t u) {
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// the conv family's act word (plan.rs:1346): 0 none, 1 gelu(c1, c2, c3), 2 relu
+int conv_act(Decoder& d, uint32_t act, float c1, float c2, float c3, Act* out) {
+  qph_act a{};
+  if (act == 0) {
+    a.kind = QPH_ACT_NONE;
+  } else if (act == 1) {
+    a.kind = QPH_ACT_GELU; a.c1 = c1; a.c2 = c2; a.c3 = c3;
+  } else if (act == 2) {
+    a.kind = QPH_ACT_RELU;
+  } else {
+    return fail(QPH_EUNSUPPORTED, d.where() + ": activation " + std::to_string(act));
+  }
+  if (act == 1 && !(c1 != 0.0f)) return fail(QPH_EINVAL, d.where() + ": gelu with c1 = 0");
+  if (act != 1) a.c1 = 1.0f;
+  *out = make_act(&a);
+  return QPH_OK;
+}
+
+int add_launch(qph_plan* pl, int dispatch, std::function<int(hipStream_t)> f) {
+  pl->launches.push_back(std::move(f));
+  pl->launch_dispatch.push_back(dispatch);
+  return QPH_OK;
+}
+
+struct PendingHw { uint32_t in, scratch; int64_t m, c, nb; };
+
+int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
+  const uint32_t* w;
+  QPH_TRY(d.params(21, &w));
+  const uint32_t in = w[0], wo = w[1], bo = w[2], out = w[3];
+  const int64_t P = w[4], N = w[5], ow = w[6], iw = w[7], ih = w[8], cin = 4 * (int64_t)w[9];
+  const int64_t taps = w[10], kw = w[11], sh = w[12], sw = w[13], pt = w[14], pl = w[15];
+  const uint32_t ro = w[20];
+  const int64_t nb = q.groups[1];
+  if (nb < 1 || P < 1 || N < 4 || N % 4 || ow < 1 || P % ow || iw < 1 || ih < 1 || cin < 4 ||
+      taps < 1 || kw < 1 || taps % kw || sh < 1 || sw < 1)
+    return fail(QPH_EINVAL, d.where() + ": bad conv geometry");
+  const int64_t oh = P / ow, kh = taps / kw;
+  Act act;
+  QPH_TRY(conv_act(d, w[16], f32_of(w[17]), f32_of(w[18]), f32_of(w[19]), &act));
+  QPH_TRY(d.region(in, (uint64_t)nb * ih * iw * cin, true, "input"));
+  QPH_TRY(d.region(wo, (uint64_t)taps * cin * N, false, "weights"));
+  QPH_TRY(d.region(out, (uint64_t)nb * P * N, true, "output"));
+  if (bo != OFF_NONE) QPH_TRY(d.region(bo, (uint64_t)N, true, "bias"));
+  if (ro != OFF_NONE) QPH_TRY(d.region(ro, (uint64_t)nb * P * N, true, "residual"));
+  const float* x = d.at(in);
+  const float* wt = d.at(wo);
+  const float* bias = bo == OFF_NONE ? nullptr : d.at(bo);
+  const float* res = ro == OFF_NONE ? nullptr : d.at(ro);
+  float* y = d.at(out);
+  // the CPU branch (conv.rs:264, 506-661) and its bias rule
+  const bool pointwise = taps == 1 && sh == 1 && sw == 1 && pt == 0 && pl == 0 && oh == ih &&
+                         ow == iw;
+  ConvK k{};
+  k.arena = d.pl->arena; k.x = x; k.w = wt; k.bias = bias; k.res = res; k.y = y;
+  k.P = P; k.N = N; k.ow = ow; k.oh = oh; k.iw = iw; k.ih = ih; k.cin = cin; k.taps = taps;
+  k.kw = kw; k.sh = sh; k.sw = sw; k.pt = pt; k.pl = pl; k.act = act; k.tile = 1;
+  if (pointwise) {
+    // 1x1: one sgemm per image, M = N channels, N = P pixels (conv.rs:370-460)
+    const double fl = (double)N * (double)P * (double)cin;
+    k.rule_kind = 0;
+    k.rule_path = (nb > 1 || fl < 2e5 || (P + 31) / 32 >= 2) ? 0 : 1;
+    // nothing seeded (panel rule with N % 4 == 0): pixels x channels as one
+    // GEMM over the NHWC rows, bias per column after the chain
+    const bool seeded_any = bias && k.rule_path == 1 && P % 32 != 0;
+    if (!seeded_any) {
+      GemmArgs g{};
+      g.a = x; g.lda = cin; g.a_batch = 0;
+      g.b = wt; g.ldb = N; g.b_batch = 0;
+      g.c = y; g.ldc = N; g.c_batch = 0;
+      g.m = nb * P; g.n = N; g.k = cin; g.batch = 1;
+      g.bias = bias; g.bias_mode = bias ? 2 : 0; g.seed_rule = 0;
+      g.act = act;
+      g.res = res; g.ldr = N; g.r_batch = 0;
+      return add_launch(d.pl, d.idx, [g](hipStream_t s) { return launch_gemm(g, s); });
+    }
+  } else if (sw == 1 || sw == 2) {
+    k.rule_kind = 1;  // implicit GEMM, one sgemm per output row (N = ow)
+  } else {
+    k.rule_kind = 2;  // im2col tiles (conv.rs:639-661), tile height on one thread
+    const int64_t kk = cin * kh * kw;
+    int64_t tile = ((int64_t)1 << 19) / (kk * ow > 1 ? kk * ow : 1);
+    if (tile < 1) tile = 1;
+    if (tile > oh) tile = oh;
+    k.tile = tile;
+  }
+  const int64_t waves = ((N + 15) / 16) * ((P + 63) / 64);
+  if (waves / 4 + 1 >= (1ll << 31) || nb > 65535)
+    return fail(QPH_EUNSUPPORTED, d.where() + ": conv grid too large");
+  return add_launch(d.pl, d.idx, [k, waves, nb](hipStream_t s) {
+    hipLaunchKernelGGL(plan_conv_kernel, dim3((unsigned)((waves + 3) / 4), (unsigned)nb),
+                       dim3(256), 0, s, k);
+    return launch_check("plan_conv_kernel");
+  });
+}
+
+int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pending) {
+  qph_plan* pl = d.pl;
+  const uint32_t* w = nullptr;
+  switch (q.kernel) {
+    case PK_ENTRY: {
+      QPH_TRY(d.params(7, &w));
+      const int64_t nb = w[2], c = w[3], h = w[4], wd = w[5], cp = w[6];
+      if (nb < 1 || c < 1 || h < 1 || wd < 1 || cp < c || cp % 4)
+        return fail(QPH_EINVAL, d.where() + ": bad entry shape");
+      QPH_TRY(d.region(w[0], (uint64_t)nb * c * h * wd, false, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)nb * h * wd * cp, true, "output"));
+      EntryK k{pl->arena, d.at(w[0]), d.at(w[1]), nb, c, h * wd, cp / 4};
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_entry_kernel, dim3(blocks_for(k.nb * k.hw)), dim3(256), 0, s, k);
+        return launch_check("plan_entry_kernel");
+      });
+    }
+    case PK_EXIT: {
+      QPH_TRY(d.params(8, &w));
+      const int64_t nb = w[2], c = w[3], h = w[4], wd = w[5], cp = w[6];
+      if (nb < 1 || c < 1 || h < 1 || wd < 1 || cp < c || cp % 4 || (w[7] != 0 && w[7] != 4))
+        return fail(QPH_EINVAL, d.where() + ": bad exit shape or activation");
+      QPH_TRY(d.region(w[0], (uint64_t)nb * h * wd * cp, true, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)nb * c * h * wd, false, "output"));
+      ExitK k{d.at(w[0]), d.at(w[1]), nb, c, h * wd, cp, w[7] == 4};
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_exit_kernel, dim3(blocks_for(k.nb * k.hw)), dim3(256), 0, s, k);
+        return launch_check("plan_exit_kernel");
+      });
+    }
+    case PK_EXIT3:
+    case PK_EXIT3_ARGMAX: {
+      QPH_TRY(d.params(6, &w));
+      const int64_t rows = w[2], cols = w[3], cp = w[4], rpb = w[5];
+      if (rows < 1 || cols < 1 || cp < cols || rpb < 1)
+        return fail(QPH_EINVAL, d.where() + ": bad rows / cols");
+      QPH_TRY(d.region(w[0], (uint64_t)rows * cp, false, "input"));
+      const float* x = d.at(w[0]);
+      float* y = d.at(w[1]);
+      if (q.kernel == PK_EXIT3_ARGMAX) {
+        QPH_TRY(d.region(w[1], (uint64_t)rows * 2, false, "pairs"));
+        if (cols >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, d.where() + ": row too wide");
+        return add_launch(pl, d.idx, [=](hipStream_t s) {
+          return launch_argmax_pitched(x, rows, cols, cp, y, s);
+        });
+      }
+      QPH_TRY(d.region(w[1], (uint64_t)rows * cols, false, "output"));
+      Exit3K k{pl->arena, x, y, rows, cols, cp, rpb};
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_exit3_kernel, dim3(blocks_for(k.rows * k.cols)), dim3(256), 0, s, k);
+        return launch_check("plan_exit3_kernel");
+      });
+    }
+    case PK_ELEM: {
+      QPH_TRY(d.params(7, &w));
+      const int op = (int)w[0];
+      const int64_t n = w[4];
+      if (op < 0 || op > 13) return fail(QPH_EUNSUPPORTED, d.where() + ": op " + std::to_string(op));
+      if (n < 4 || n % 4) return fail(QPH_EINVAL, d.where() + ": element count not a multiple of 4");
+      QPH_TRY(d.region(w[1], (uint64_t)n, true, "input"));
+      QPH_TRY(d.region(w[3], (uint64_t)n, true, "output"));
+      ElemK k{d.at(w[1]), nullptr, d.at(w[3]), n / 4, op, f32_of(w[5]), f32_of(w[6]), 1};
+      if (op == 4 || op == 5 || op == 12 || op == 13) {
+        QPH_TRY(d.region(w[2], (uint64_t)n, true, "second input"));
+        k.b = d.at(w[2]);
+      } else if (op == 6 || op == 7) {
+        QPH_TRY(d.region(w[2], 1, false, "scalar"));
+        k.b = d.at(w[2]);
+      } else if (op == 8 || op == 11) {
+        k.c4 = w[5];  // the row's vec4 count, as the bits of p1
+        if (k.c4 < 1 || (n / 4) % k.c4)
+          return fail(QPH_EINVAL, d.where() + ": row vector width does not divide the tensor");
+        QPH_TRY(d.region(w[2], (uint64_t)(n / 4 / k.c4) * 4, true, "row values"));
+        k.b = d.at(w[2]);
+      }
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_elem_kernel, dim3(blocks_for(k.nv)), dim3(256), 0, s, k);
+        return launch_check("plan_elem_kernel");
+      });
+    }
+    case PK_CHANNEL: {
+      QPH_TRY(d.params(10, &w));
+      const int op = (int)w[0];
+      const int64_t n = w[5], cp = w[6], hw = w[9];
+      if (op < 0 || op > 5) return fail(QPH_EUNSUPPORTED, d.where() + ": op " + std::to_string(op));
+      if (n < 4 || n % 4 || cp < 4 || cp % 4 || (n / 4) % (cp / 4) || hw < 1)
+        return fail(QPH_EINVAL, d.where() + ": bad channel broadcast shape");
+      const int64_t frows = n / cp, grows = (frows - 1) / hw + 1;
+      QPH_TRY(d.region(w[1], (uint64_t)n, true, "input"));
+      QPH_TRY(d.region(w[2], (uint64_t)grows * cp, true, "gate"));
+      QPH_TRY(d.region(w[4], (uint64_t)n, true, "output"));
+      ChannelK k{pl->arena, d.at(w[1]), d.at(w[2]), nullptr, d.at(w[4]), n / 4, cp / 4, hw, op,
+                 f32_of(w[7]), f32_of(w[8])};
+      if (op == 2) {
+        QPH_TRY(d.region(w[3], (uint64_t)n, true, "residual"));
+        k.r = d.at(w[3]);
+      } else if (op == 5) {
+        QPH_TRY(d.region(w[3], (uint64_t)grows * cp, true, "shift"));
+        k.r = d.at(w[3]);
+      }
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_channel_kernel, dim3(blocks_for(k.nv)), dim3(256), 0, s, k);
+        return launch_check("plan_channel_kernel");
+      });
+    }
+    case PK_CONV:
+    case PK_CONV8:
+      return decode_conv(d, q);
+    case PK_CONV_DW: {
+      QPH_TRY(d.params(20, &w));
+      const int64_t P = w[4], C = w[5], ow = w[6], iw = w[7], ih = w[8], taps = w[9], kw = w[10];
+      const int64_t sh = w[11], sw = w[12], pt = w[13], pl_ = w[14];
+      const int64_t nb = q.groups[1];
+      if (nb < 1 || nb > 65535 || P < 1 || C < 4 || C % 4 || ow < 1 || P % ow || iw < 1 ||
+          ih < 1 || taps < 1 || kw < 1 || taps % kw || sh < 1 || sw < 1)
+        return fail(QPH_EINVAL, d.where() + ": bad depthwise geometry");
+      Act act;
+      QPH_TRY(conv_act(d, w[15], f32_of(w[16]), f32_of(w[17]), f32_of(w[18]), &act));
+      QPH_TRY(d.region(w[0], (uint64_t)nb * ih * iw * C, true, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)taps * C, true, "weights"));
+      QPH_TRY(d.region(w[3], (uint64_t)nb * P * C, true, "output"));
+      if (w[2] != OFF_NONE) QPH_TRY(d.region(w[2], (uint64_t)C, true, "bias"));
+      if (w[19] != OFF_NONE) QPH_TRY(d.region(w[19], (uint64_t)nb * P * C, true, "residual"));
+      DwK k{pl->arena, d.at(w[0]), d.at(w[1]), w[2] == OFF_NONE ? nullptr : d.at(w[2]),
+            w[19] == OFF_NONE ? nullptr : d.at(w[19]), d.at(w[3]),
+            P, C / 4, ow, iw, ih, taps, kw, sh, sw, pt, pl_, act};
+      return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
+        hipLaunchKernelGGL(plan_dw_kernel, dim3(blocks_for(k.P * k.c4), (unsigned)nb), dim3(256), 0,
+                           s, k);
+        return launch_check("plan_dw_kernel");
+      });
+    }
+    case PK_CONVT: {
+      QPH_TRY(d.params(18, &w));
+      const int64_t P = w[4], N = w[5], ow = w[6], iw = w[7], ih = w[8], cin = w[9];
+      const int64_t sh = w[11], sw = w[12], kw = w[13];
+      const int64_t nb = q.groups[1];
+      if (nb < 1 || nb > 65535 || P < 1 || N < 4 || N % 4 || ow < 1 || P % ow || iw < 1 ||
+          ih < 1 || cin < 4 || cin % 4 || (int64_t)w[10] * 4 != cin || sh < 1 || sw < 1 ||
+          kw < 1 || kw > sw || P / ow > ih * sh || ow > iw * sw)
+        return fail(QPH_EINVAL, d.where() + ": bad conv-transpose geometry");
+      Act act;
+      QPH_TRY(conv_act(d, w[14], f32_of(w[15]), f32_of(w[16]), f32_of(w[17]), &act));
+      const int64_t max_tap = (sh - 1) * kw + (sw - 1);
+      QPH_TRY(d.region(w[0], (uint64_t)nb * ih * iw * cin, false, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)(max_tap + 1) * cin * N, true, "weights"));
+      QPH_TRY(d.region(w[3], (uint64_t)nb * P * N, true, "output"));
+      if (w[2] != OFF_NONE) QPH_TRY(d.region(w[2], (uint64_t)N, true, "bias"));
+      ConvtK k{d.at(w[0]), d.at(w[1]), w[2] == OFF_NONE ? nullptr : d.at(w[2]), d.at(w[3]),
+               P, N / 4, ow, iw, ih, cin, sh, sw, kw, act};
+      return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
+        hipLaunchKernelGGL(plan_convt_kernel, dim3(blocks_for(k.P * k.nv), (unsigned)nb), dim3(256),
+                           0, s, k);
+        return launch_check("plan_convt_kernel");
+      });
+    }
+    case PK_POOL: {
+      QPH_TRY(d.params(14, &w));
+      const int64_t P = w[2], C = w[3], ow = w[4], iw = w[5], ih = w[6], kh = w[7], kw = w[8];
+      const int64_t sh = w[9], sw = w[10], pt = w[11], pl_ = w[12];
+      const int64_t nb = q.groups[1];
+      if (nb < 1 || nb > 65535 || P < 1 || C < 4 || C % 4 || ow < 1 || P % ow || iw < 1 ||
+          ih < 1 || kh < 1 || kw < 1 || sh < 1 || sw < 1)
+        return fail(QPH_EINVAL, d.where() + ": bad pool geometry");
+      QPH_TRY(d.region(w[0], (uint64_t)nb * ih * iw * C, true, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)nb * P * C, true, "output"));
+      PoolNK k{pl->arena, d.at(w[0]), d.at(w[1]), P, C / 4, ow, iw, ih, kh, kw, sh, sw, pt, pl_,
+               w[13] != 0, 0};
+      k.special = k.max_pool && kh == 2 && kw == 2 && sh == 1 && sw == 1 && pt == 0 && pl_ == 0 &&
+                  P / ow == ih && ow == iw;
+      return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
+        hipLaunchKernelGGL(plan_pool_kernel, dim3(blocks_for(k.P * k.c4), (unsigned)nb), dim3(256),
+                           0, s, k);
+        return launch_check("plan_pool_kernel");
+      });
+    }
+    case PK_REDUCE_HW: {
+      QPH_TRY(d.params(4, &w));
+      const int64_t m = w[2], c = w[3], nb = q.groups[1];
+      if (nb < 1 || m < 1 || c < 4 || c % 4) return fail(QPH_EINVAL, d.where() + ": bad reduce shape");
+      QPH_TRY(d.region(w[0], (uint64_t)nb * m * c, true, "input"));
+      pending.push_back({w[0], w[1], m, c, nb});
+      return QPH_OK;  // runs with its n_reduce_fin
+    }
+    case PK_REDUCE_FIN: {
+      QPH_TRY(d.params(5, &w));
+      const uint32_t scratch = w[0], out = w[1];
+      const int64_t c = w[3], m = w[4], nb = q.groups[0];
+      auto it = std::find_if(pending.begin(), pending.end(),
+                             [&](const PendingHw& h) { return h.scratch == scratch; });
+      if (it == pending.end() || it->c != c || it->m != m || it->nb != nb)
+        return fail(QPH_EUNSUPPORTED, d.where() + ": no matching n_reduce_hw before it");
+      QPH_TRY(d.region(out, (uint64_t)nb * c, true, "output"));
+      const float* x = d.at(it->in);
+      float* y = d.at(out);
+      pending.erase(it);
+      // GlobalAveragePool: channel c of image b is the mean over the P
+      // pixels x[(b * P + p) * C + c]
+      return add_launch(pl, d.idx, [=](hipStream_t s) {
+        return launch_reduce_mean_rows(x, nb * c, m, c, m * c, 1, c, y, 1, s);
+      });
+    }
+    case PK_REDUCE_LAST: {
+      QPH_TRY(d.params(6, &w));
+      const int64_t rows = w[2], cols = w[3], cp = w[4];
+      if (rows < 1 || cols < 1 || cp < cols) return fail(QPH_EINVAL, d.where() + ": bad rows / cols");
+      QPH_TRY(d.region(w[0], (uint64_t)rows * cp, false, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)rows * 4, false, "output"));
+      const float* x = d.at(w[0]);
+      float* y = d.at(w[1]);
+      return add_launch(pl, d.idx, [=](hipStream_t s) {
+        return launch_reduce_mean_rows(x, rows, cols, rows, 0, cp, 1, y, 4, s);
+      });
+    }
+    case PK_RESIZE: {
+      QPH_TRY(d.params(9, &w));
+      const int64_t P = w[2], C = w[3], ow = w[4], iw = w[5], ih = w[6], nb = q.groups[1];
+      if (nb < 1 || nb > 65535 || P < 1 || C < 4 || C % 4 || ow < 1 || P % ow || iw < 1 || ih < 1)
+        return fail(QPH_EINVAL, d.where() + ": bad resize geometry");
+      QPH_TRY(d.region(w[0], (uint64_t)nb * ih * iw * C, true, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)nb * P * C, true, "output"));
+      ResizeNK k{d.at(w[0]), d.at(w[1]), P, C / 4, ow, P / ow, iw, ih};
+      return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
+        hipLaunchKernelGGL(plan_resize_kernel, dim3(blocks_for(k.P * k.c4), (unsigned)nb),
+                           dim3(256), 0, s, k);
+        return launch_check("plan_resize_kernel");
+      });
+    }
+    case PK_TRANSPOSE: {
+      QPH_TRY(d.params(4, &w));
+      const int64_t r = w[2], c = w[3];
+      if (r < 1 || c < 1) return fail(QPH_EINVAL, d.where() + ": empty transpose");
+      QPH_TRY(d.region(w[0], (uint64_t)r * c, false, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)r * c, false, "output"));
+      Transpose2K k{d.at(w[0]), d.at(w[1]), r, c};
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_transpose2_kernel, dim3(blocks_for(k.r * k.c)), dim3(256), 0, s, k);
+        return launch_check("plan_transpose2_kernel");
+      });
+    }
+    case PK_TRANSPOSE_ND: {
+      QPH_TRY(d.params(14, &w));
+      TransposeNK k{};
+      k.total = w[2];
+      k.rank = (int)w[3];
+      if (k.rank < 1 || k.rank > 5) return fail(QPH_EINVAL, d.where() + ": rank outside 1..5");
+      int64_t prod = 1;
+      bool seen[5] = {false, false, false, false, false};
+      for (int i = 0; i < k.rank; i++) {
+        k.dims[i] = w[4 + i];
+        k.perm[i] = (int)w[9 + i];
+        if (k.dims[i] < 1 || k.perm[i] < 0 || k.perm[i] >= k.rank || seen[k.perm[i]])
+          return fail(QPH_EINVAL, d.where() + ": bad dims / permutation");
+        seen[k.perm[i]] = true;
+        prod *= k.dims[i];
+      }
+      if (prod != k.total || k.total < 1) return fail(QPH_EINVAL, d.where() + ": total != product");
+      QPH_TRY(d.region(w[0], (uint64_t)k.total, false, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)k.total, false, "output"));
+      k.x = d.at(w[0]);
+      k.y = d.at(w[1]);
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_transpose_nd_kernel, dim3(blocks_for(k.total)), dim3(256), 0, s, k);
+        return launch_check("plan_transpose_nd_kernel");
+      });
+    }
+    case PK_CONCAT_C: {
+      QPH_TRY(d.params(4, &w));
+      const int64_t hw = w[1], n = w[2], outc4 = w[3];
+      if (hw < 1 || n < 1 || n > 8 || outc4 < 1)
+        return fail(QPH_EINVAL, d.where() + ": bad concat (1 to 8 inputs)");
+      QPH_TRY(d.params(4 + 2 * (uint32_t)n, &w));
+      ConcatK k{};
+      k.arena = pl->arena; k.hw = hw; k.outc4 = outc4; k.n = (int)n;
+      int64_t sum = 0;
+      for (int i = 0; i < n; i++) {
+        k.src[i] = w[4 + 2 * i];
+        k.c4len[i] = w[5 + 2 * i];
+        if (k.c4len[i] < 1) return fail(QPH_EINVAL, d.where() + ": empty concat input");
+        QPH_TRY(d.region(k.src[i], (uint64_t)hw * k.c4len[i] * 4, true, "concat input"));
+        sum += k.c4len[i];
+      }
+      if (sum != outc4) return fail(QPH_EINVAL, d.where() + ": input channels do not sum to the output's");
+      QPH_TRY(d.region(w[0], (uint64_t)hw * outc4 * 4, true, "output"));
+      k.y = d.at(w[0]);
+      return add_launch(pl, d.idx, [k](hipStream_t s) {
+        hipLaunchKernelGGL(plan_concat_kernel, dim3(blocks_for(k.hw * k.outc4)), dim3(256), 0, s, k);
+        return launch_check("plan_concat_kernel");
+      });
+    }
+    case PK_SOFTMAX: {
+      QPH_TRY(d.params(6, &w));
+      const int64_t rows = w[2], cols = w[3], cp = w[4];
+      if (rows < 1 || cols < 1 || cp < cols) return fail(QPH_EINVAL, d.where() + ": bad rows / cols");
+      QPH_TRY(d.region(w[0], (uint64_t)rows * cp, false, "input"));
+      QPH_TRY(d.region(w[1], (uint64_t)rows * cp, false, "output"));
+      const float* x = d.at(w[0]);
+      float* y = d.at(w[1]);
+      if (x != y && (uint64_t)w[1] < (uint64_t)w[0] + rows * cp &&
+          (uint64_t)w[0] < (uint64_t)w[1] + rows * cp)
+        return fail(QPH_EUNSUPPORTED, d.where() + ": input and output overlap");
+      PadColsK pk{y, rows, cols, cp};
+      return add_launch(pl, d.idx, [=](hipStream_t s) {
+        QPH_TRY(launch_softmax_pitched(x, rows, cols, cp, y, cp, nullptr, s));
+        if (cp == cols) return QPH_OK;
+        hipLaunchKernelGGL(plan_pad_cols_kernel, dim3(blocks_for(rows * (cp - cols))), dim3(256),
+                           0, s, pk);
+        return launch_check("plan_pad_cols_kernel");
+      });
+    }
+    case PK_ATTN_MM: {
+      QPH_TRY(d.params(8, &w));
+      const int64_t m = w[3], kk = w[4], n = w[5], batch = w[6];
+      if (m < 1 || kk < 1 || n < 1 || batch < 1 || batch > 65535)
+        return fail(QPH_EINVAL, d.where() + ": bad batched matmul shape");
+      QPH_TRY(d.region(w[0], (uint64_t)batch * m * kk, false, "A"));
+      QPH_TRY(d.region(w[1], (uint64_t)batch * kk * n, false, "B"));
+      QPH_TRY(d.region(w[2], (uint64_t)batch * m * n, false, "output"));
+      GemmArgs g{};
+      g.a = d.at(w[0]); g.lda = kk; g.a_batch = m * kk;
+      g.b = d.at(w[1]); g.ldb = n; g.b_batch = kk * n;
+      g.c = d.at(w[2]); g.ldc = n; g.c_batch = m * n;
+      g.m = m; g.n = n; g.k = kk; g.batch = batch;
+      g.bias = nullptr; g.bias_mode = 0; g.seed_rule = 0;
+      g.act = make_act(nullptr);
+      return add_launch(pl, d.idx, [g](hipStream_t s) { return launch_gemm(g, s); });
+    }
+    default:
+      return fail(QPH_EUNSUPPORTED, d.where() + ": kernel id " + std::to_string(q.kernel) +
+                                        " is not in the HIP kernel set");
+  }
+}
+
+int capture_plan(qph_plan* pl) {
+  hipStream_t s = pl->ctx->stream;
+  QPH_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = QPH_OK;
+  for (size_t i = 0; i < pl->launches.size() && rc == QPH_OK; i++) {
+    rc = pl->launches[i](s);
+    if (rc != QPH_OK)
+      rc = fail(rc, "plan dispatch " + std::to_string(pl->launch_dispatch[i]) + ": " +
+                        qph_last_error());
+  }
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(s, &g);
+  if (rc != QPH_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  QPH_TRY_HIP(e);
+  e = hipGraphInstantiate(&pl->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_check(e, "hipGraphInstantiate");
+  }
+  pl->graph = g;
+  pl->graph_ready = true;
+  return QPH_OK;
+}
+
+void release_plan(qph_plan* pl) {
+  if (!pl) return;
+  (void)hipStreamSynchronize(pl->ctx->stream);
+  if (pl->graph_ready) {
+    (void)hipGraphExecDestroy(pl->exec);
+    (void)hipGraphDestroy(pl->graph);
+  }
+  if (pl->arena) (void)hipFree(pl->arena);
+  delete pl;
+}
+
+}  // namespace
+}  // namespace qph
+
+using namespace qph;
+
+extern "C" {
+
+QPH_API int qph_plan_kernel_id(const char* name) {
+  if (!name) return fail(QPH_EINVAL, "plan_kernel_id: NULL name");
+  for (int i = 0; i < kNumPlanKernels; i++)
+    if (std::strcmp(name, kPlanKernels[i]) == 0) return i;
+  return fail(QPH_EUNSUPPORTED, std::string("plan kernel ") + name + " is not in the HIP kernel set");
+}
+
+QPH_API int qph_plan_create(qph_ctx* ctx, const qph_plan_spec* spec, qph_plan** out) {
+  if (!ctx || !spec || !out) return fail(QPH_EINVAL, "plan_create: NULL argument");
+  *out = nullptr;
+  if (spec->total_words < 1 || spec->n_dispatches < 1 || spec->n_uploads < 0 ||
+      (spec->n_uploads && !spec->uploads) || !spec->dispatches || spec->n_outputs < 1 ||
+      !spec->out_offs || !spec->out_numel || spec->in_numel < 1)
+    return fail(QPH_EINVAL, "plan_create: empty plan");
+  if ((uint64_t)spec->in_f32_off + (uint64_t)spec->in_numel > spec->total_words)
+    return fail(QPH_EINVAL, "plan_create: the input region is outside the arena");
+  for (int32_t o = 0; o < spec->n_outputs; o++)
+    if (spec->out_numel[o] < 1 ||
+        (uint64_t)spec->out_offs[o] + (uint64_t)spec->out_numel[o] > spec->total_words)
+      return fail(QPH_EINVAL, "plan_create: output " + std::to_string(o) + " is outside the arena");
+  Decoder d;
+  for (int32_t u = 0; u < spec->n_uploads; u++) {
+    const qph_plan_upload& up = spec->uploads[u];
+    if (up.n_words == 0) continue;
+    if (!up.words || (uint64_t)up.off + up.n_words > spec->total_words)
+      return fail(QPH_EINVAL, "plan_create: upload " + std::to_string(u) + " is outside the arena");
+    d.ups.push_back({up.off, up.n_words, up.words});
+  }
+  std::sort(d.ups.begin(), d.ups.end(),
+            [](const PlanUpload& a, const PlanUpload& b) { return a.off < b.off; });
+  for (size_t u = 1; u < d.ups.size(); u++)
+    if ((uint64_t)d.ups[u - 1].off + d.ups[u - 1].n > d.ups[u].off)
+      return fail(QPH_EINVAL, "plan_create: uploads overlap");
+
+  qph_plan* pl = new qph_plan();
+  pl->ctx = ctx;
+  pl->total_words = spec->total_words;
+  pl->arena = nullptr;
+  pl->graph_ready = false;
+  pl->in_off = spec->in_f32_off;
+  pl->in_numel = spec->in_numel;
+  pl->out_off.assign(spec->out_offs, spec->out_offs + spec->n_outputs);
+  pl->out_numel.assign(spec->out_numel, spec->out_numel + spec->n_outputs);
+  pl->real_n = 0;
+  d.pl = pl;
+  auto bail = [&](int rc) {
+    release_plan(pl);
+    return rc;
+  };
+  int rc = hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+  if (rc) return bail(rc);
+  rc = hip_check(hipMalloc((void**)&pl->arena, (size_t)spec->total_words * 4), "hipMalloc(plan arena)");
+  if (rc) return bail(rc);
+  rc = hip_check(hipMemset(pl->arena, 0, (size_t)spec->total_words * 4), "hipMemset(plan arena)");
+  if (rc) return bail(rc);
+  for (const PlanUpload& up : d.ups) {
+    rc = hip_check(hipMemcpy(pl->arena + up.off, up.words, (size_t)up.n * 4, hipMemcpyHostToDevice),
+                   "hipMemcpy(plan upload)");
+    if (rc) return bail(rc);
+  }
+  std::vector<PendingHw> pending;
+  for (int32_t i = 0; i < spec->n_dispatches; i++) {
+    const qph_plan_dispatch& q = spec->dispatches[i];
+    d.idx = i;
+    d.kname = (q.kernel >= 0 && q.kernel < kNumPlanKernels) ? kPlanKernels[q.kernel] : "?";
+    d.p_off = q.p_off;
+    rc = decode(d, q, pending);
+    if (rc) return bail(rc);
+  }
+  if (!pending.empty())
+    return bail(fail(QPH_EUNSUPPORTED, "plan_create: an n_reduce_hw without its n_reduce_fin"));
+  rc = capture_plan(pl);
+  if (rc) return bail(rc);
+  *out = pl;
+  return QPH_OK;
+}
+
+QPH_API int qph_plan_destroy(qph_plan* pl) {
+  release_plan(pl);
+  return QPH_OK;
+}
+
+QPH_API int qph_plan_set_real_n(qph_plan* pl, uint32_t real_n) {
+  if (!pl) return fail(QPH_EINVAL, "plan_set_real_n: NULL plan");
+  pl->real_n = real_n;
+  return QPH_OK;
+}
+
+QPH_API int qph_plan_run(qph_plan* pl, const float* input, int32_t input_is_device,
+                         float* const* outputs_host) {
+  if (!pl) return fail(QPH_EINVAL, "plan_run: NULL plan");
+  hipStream_t s = pl->ctx->stream;
+  // word 0: the real batch rows of this run (0 = all), written before the graph
+  QPH_TRY_HIP(hipMemcpyAsync(pl->arena, &pl->real_n, 4, hipMemcpyHostToDevice, s));
+  if (input)
+    QPH_TRY_HIP(hipMemcpyAsync(pl->arena + pl->in_off, input, (size_t)pl->in_numel * 4,
+                               input_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
+  QPH_TRY_HIP(hipGraphLaunch(pl->exec, s));
+  if (outputs_host) {
+    for (size_t o = 0; o < pl->out_off.size(); o++) {
+      if (!outputs_host[o]) continue;
+      QPH_TRY_HIP(hipMemcpyAsync(outputs_host[o], pl->arena + pl->out_off[o],
+                                 (size_t)pl->out_numel[o] * 4, hipMemcpyDeviceToHost, s));
+    }
+    QPH_TRY_HIP(hipStreamSynchronize(s));
+  }
+  return QPH_OK;
+}
+
+QPH_API int qph_plan_arena(qph_plan* pl, float** dev, int64_t* words) {
+  if (!pl) return fail(QPH_EINVAL, "plan_arena: NULL plan");
+  if (dev) *dev = pl->arena;
+  if (words) *words = pl->total_words;
+  return QPH_OK;
+}
+
+QPH_API int qph_plan_launches(qph_plan* pl, int32_t* n) {
+  if (!pl || !n) return fail(QPH_EINVAL, "plan_launches: NULL argument");
+  *n = (int32_t)pl->launches.size();
+  return QPH_OK;
+}
+
+}  // extern "C"

@@ -196,7 +196,8 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
 // would have been read back; exp1 is deterministic, so the values are the
 // same).  pairs may be NULL.
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, int64_t cols,
-                                                           int64_t ld, float* probs, float* pairs) {
+                                                           int64_t ld, float* probs, int64_t ldo,
+                                                           float* pairs) {
   __shared__ float buf[2][SM_CHUNK];
   __shared__ float part[16];
   __shared__ float red[8];
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
   const float* xr = logits + row * ld;
-  float* pr = probs + row * cols;
+  float* pr = probs + row * ldo;
 
   // max over the row, eight loads in flight per thread
   float mx = -__builtin_inff();
@@ -368,7 +369,7 @@ __device__ __forceinline__ float block_max_512(float v, float* red) {
 }
 
 __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, int cols, int ld,
-                                                          float* probs, float* pairs) {
+                                                          float* probs, int ldo, float* pairs) {
   __shared__ __attribute__((aligned(16))) float win[2][8 * SM_WIN_PITCH];
   __shared__ float part[16];
   __shared__ float red[8];
@@ -461,7 +462,7 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
   }
   __syncthreads();
   const float inv = 1.0f / part[8];
-  float* pr = probs + row * cols;
+  float* pr = probs + row * ldo;
   float bv = -__builtin_inff();
   int bi = 0x7fffffff;
 #pragma unroll
@@ -516,7 +517,7 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
 #define SM_LDS_PER_THREAD 38            // ceil(SM_LDS_MAX_COLS / 512)
 
 __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, int cols, int ld,
-                                                          float* probs, float* pairs) {
+                                                          float* probs, int ldo, float* pairs) {
   __shared__ __attribute__((aligned(16))) float tr[8 * SM_TP];
   __shared__ float tail[8];
   __shared__ float red[8];
@@ -588,7 +589,7 @@ __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, i
   }
   __syncthreads();
   const float inv = 1.0f / total;
-  float* pr = probs + row * cols;
+  float* pr = probs + row * ldo;
   float bv = -__builtin_inff();
   int bi = 0x7fffffff;
 #pragma unroll
@@ -630,24 +631,30 @@ __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, i
   }
 }
 
-// logits rows ld floats apart (ld >= cols); probs contiguous.
-static int launch_softmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
-                          float* probs, float* pairs, hipStream_t s) {
+// logits rows ld floats apart (ld >= cols); probs rows ldo floats apart.
+int launch_softmax_pitched(const float* logits, int64_t rows, int64_t cols, int64_t ld,
+                           float* probs, int64_t ldo, float* pairs, hipStream_t s) {
   if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
-  if (ld < cols) return fail(QPH_EINVAL, "softmax: row pitch below the row width");
-  if (cols <= SM_LDS_MAX_COLS && ld < (1ll << 31)) {
+  if (ld < cols || ldo < cols) return fail(QPH_EINVAL, "softmax: row pitch below the row width");
+  if (probs == logits && ldo != ld) return fail(QPH_EINVAL, "softmax: in place with two pitches");
+  if (cols <= SM_LDS_MAX_COLS && ld < (1ll << 31) && ldo < (1ll << 31)) {
     hipLaunchKernelGGL(softmax_lds_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
-                       (int)cols, (int)ld, probs, pairs);
+                       (int)cols, (int)ld, probs, (int)ldo, pairs);
     return launch_check("softmax_lds_kernel");
   }
-  if (cols <= SM_REG_MAX_COLS && ld < (1ll << 31)) {
+  if (cols <= SM_REG_MAX_COLS && ld < (1ll << 31) && ldo < (1ll << 31)) {
     hipLaunchKernelGGL(softmax_reg_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
-                       (int)cols, (int)ld, probs, pairs);
+                       (int)cols, (int)ld, probs, (int)ldo, pairs);
     return launch_check("softmax_reg_kernel");
   }
   hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols,
-                     ld, probs, pairs);
+                     ld, probs, ldo, pairs);
   return launch_check("softmax_rows_kernel");
+}
+
+static int launch_softmax(const float* logits, int64_t rows, int64_t cols, int64_t ld,
+                          float* probs, float* pairs, hipStream_t s) {
+  return launch_softmax_pitched(logits, rows, cols, ld, probs, cols, pairs, s);
 }
 
 int launch_softmax_rows(float* t, int64_t rows, int64_t cols, hipStream_t s) {
@@ -662,12 +669,12 @@ int launch_softmax_argmax(const float* logits, int64_t rows, int64_t cols, int64
 
 // argmax over probabilities: first strict max (rec.rs:46-54).
 __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ probs,
-                                                     int64_t rows, int64_t cols,
+                                                     int64_t rows, int64_t cols, int64_t ld,
                                                      float* __restrict__ pairs) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float* pr = probs + row * cols;
+  const float* pr = probs + row * ld;
   float bv = pr[0];
   int bi = 0;
   bool have = false;
@@ -697,10 +704,15 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ p
   }
 }
 
-int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, hipStream_t s) {
+int launch_argmax_pitched(const float* probs, int64_t rows, int64_t cols, int64_t ld,
+                          float* pairs, hipStream_t s) {
   hipLaunchKernelGGL(argmax_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, probs, rows, cols,
-                     pairs);
+                     ld, pairs);
   return launch_check("argmax_kernel");
+}
+
+int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, hipStream_t s) {
+  return launch_argmax_pitched(probs, rows, cols, cols, pairs, s);
 }
 
 // Steps t >= t_valid[b] become (0, blank): the padded tail of a bucketed
@@ -1314,16 +1326,27 @@ int launch_binary(float* a, const float* b, int64_t rows, int64_t cols, int op, 
 }
 
 // reduce_mean over the last axis (shape.rs:510-560): f64 sum, / cols, to f32.
-__global__ __launch_bounds__(256) void reduce_mean_kernel(const float* __restrict__ x, int64_t rows,
-                                                          int64_t cols, float* __restrict__ out) {
+// Row r's element j is x[(r / rpg) * gstride + (r % rpg) * rstride + j * estride]
+// (contiguous rows: rpg = rows, rstride = cols, estride = 1); its mean goes
+// to out[r * ostride], and with ostride == 4 the other three words of the
+// row's group of four are set to 0.
+struct MeanRows {
+  const float* x;
+  int64_t rows, cols, rpg, gstride, rstride, estride;
+  float* out;
+  int64_t ostride;
+};
+
+__global__ __launch_bounds__(256) void reduce_mean_kernel(MeanRows p) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const float* xr = x + row * cols;
+  if (row >= p.rows) return;
+  const int64_t cols = p.cols, es = p.estride;
+  const float* xr = p.x + (row / p.rpg) * p.gstride + (row % p.rpg) * p.rstride;
   double s = 0.0, sa = 0.0;
   int emin = 255;
   for (int64_t j = lane; j < cols; j += 64) {
-    const float v = xr[j];
+    const float v = xr[j * es];
     const double t = f64_daz(v);
     s += t;
     sa += __builtin_fabs(t);
@@ -1335,19 +1358,27 @@ __global__ __launch_bounds__(256) void reduce_mean_kernel(const float* __restric
   if (!f64_mean_order_free(s, sa, emin, cols, &mean)) {
     s = 0.0;
     for (int64_t j0 = 0; j0 < cols; j0 += 64) {
-      const float v = j0 + lane < cols ? xr[j0 + lane] : 0.0f;
+      const float v = j0 + lane < cols ? xr[(j0 + lane) * es] : 0.0f;
       s = seq_sum_lanes(s, v, (int)min<int64_t>(64, cols - j0));
     }
     mean = (float)(s / (double)cols);
   }
-  if (lane == 0) out[row] = mean;
+  if (lane == 0) p.out[row * p.ostride] = mean;
+  if (p.ostride == 4 && lane >= 1 && lane <= 3) p.out[row * 4 + lane] = 0.0f;
+}
+
+int launch_reduce_mean_rows(const float* x, int64_t rows, int64_t cols, int64_t rpg,
+                            int64_t gstride, int64_t rstride, int64_t estride, float* out,
+                            int64_t ostride, hipStream_t s) {
+  if (rows >= (1ll << 33)) return fail(QPH_EUNSUPPORTED, "reduce_mean: too many rows");
+  if (rows <= 0 || cols <= 0 || rpg <= 0) return fail(QPH_EINVAL, "reduce_mean: empty rows");
+  MeanRows p{x, rows, cols, rpg, gstride, rstride, estride, out, ostride};
+  hipLaunchKernelGGL(reduce_mean_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, p);
+  return launch_check("reduce_mean_kernel");
 }
 
 int launch_reduce_mean(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t s) {
-  if (rows >= (1ll << 33)) return fail(QPH_EUNSUPPORTED, "reduce_mean: too many rows");
-  hipLaunchKernelGGL(reduce_mean_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, x, rows, cols,
-                     out);
-  return launch_check("reduce_mean_kernel");
+  return launch_reduce_mean_rows(x, rows, cols, rows, 0, cols, 1, out, 1, s);
 }
 
 }  // namespace qph
