@@ -29,7 +29,11 @@ calibrated FETCH_SIZE + WRITE_SIZE figure in
 profiles/rec_fused_head_traffic.md.  head_gemm_unfused gives the same
 figures for the plain head GEMM of the bit-exact graph.
 
-configs: the five BASELINE workloads, each with its GPU rate, the roofline
+plan_model: the same det and rec graphs lowered to the reference's plan
+model (GraphPlan dispatch lists over an NHWC arena) and run by the HIP
+kernel set of its n_* dispatch contracts (qph_plan_*), each plan alone.
+
+configs: the five benchmark workloads, each with its GPU rate, the roofline
 fraction of its bound and the CPU oracle timed on this host (threads set
 explicitly, one warm-up round, then the median of at least --cpu-rounds
 rounds, run until each leg has taken 2 s, 5 s for the headline's det and rec):
@@ -152,6 +156,41 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def time_plan_model(det_g, det_x, rec_x, stage_ms, ctx, ctx_rec, stream, stream_rec, both_sync,
+                    report_path):
+    """The headline graphs as the reference's plan model runs them: each
+    graph lowered to a GraphPlan (qppocr_amd.plan, PlanBuilder's Vulkan
+    configuration: rec with the pairs exit, no fused head) and replayed
+    alone on its stream, HIP events around the replays (inputs resident)."""
+    from qppocr_amd import nets, plan
+    rec_g, _ = nets.build_rec(3, REC_BATCH, 320, probs=False)
+    out = {"workload": "det 1x3x640x640 and rec 32x3x48x320 (pairs exit) as GraphPlans on the "
+                       "n_* kernel set",
+           "method": "HIP events over the timed replays of each plan alone (word 0 and the "
+                     "graph launch per replay)"}
+    plans = {}
+    for name, g, x, c, st in (("det", det_g, det_x, ctx, stream),
+                              ("rec", rec_g, rec_x, ctx_rec, stream_rec)):
+        pl = plan.build_plan(g)
+        sess = plan.HipPlanSession(pl, ctx=c)
+        sess.run(x, outputs=False)
+        sess.run(None, outputs=False)
+        both_sync()
+        ms = stage_ms(sess, st)
+        out[name + "_ms"] = round(ms, 4)
+        out[name + "_dispatches"] = len(pl.dispatches)
+        out[name + "_launches"] = sess.launches()
+        out[name + "_arena_mib"] = round(pl.total_words * 4 / 2 ** 20, 1)
+        plans[name] = [[d[0], d[3]] for d in pl.dispatches]
+        sess.close()
+    out["det_img_per_s"] = round(1e3 / out["det_ms"], 2)
+    out["rec_lines_per_s"] = round(REC_BATCH * 1e3 / out["rec_ms"], 1)
+    if report_path:
+        with open(report_path, "w") as f:
+            json.dump(plans, f)
+    return out
 
 
 def cpu_sample(fn, rounds, min_s=0.0):
@@ -360,6 +399,12 @@ def main():
     ap.add_argument("--node-report", default="",
                     help="also write per-node work, eager per-node times and the launch plans "
                          "of the headline graphs (JSON) to this path")
+    ap.add_argument("--no-plan", action="store_true",
+                    help="skip the plan-model leg (the headline graphs as GraphPlans)")
+    ap.add_argument("--plan-only", action="store_true",
+                    help="run only the plan-model leg and print its figures (profiling)")
+    ap.add_argument("--plan-report", default="",
+                    help="write the plan-model graphs' dispatch lists (JSON) to this path")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a kernel of "
                          "known traffic for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -392,6 +437,29 @@ def main():
 
     det_g, det_x = nets.build_det(2, 640, 640)
     rec_g, rec_x = nets.build_rec(3, REC_BATCH, 320, fused_head=True)
+    if args.plan_only:
+        # the plan-model leg alone (for kernel traces of the plan path)
+        def sync_all():
+            ops.check(lib.qph_sync(ctx))
+            ops.check(lib.qph_sync(ctx_rec))
+            torch.cuda.synchronize()
+
+        def stage(sess, st):
+            for _ in range(args.warmup):
+                sess.run(None, outputs=False)
+            sync_all()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(args.steps):
+                sess.run(None, outputs=False)
+            e1.record(st)
+            sync_all()
+            return e0.elapsed_time(e1) / args.steps
+        leg = time_plan_model(det_g, det_x, rec_x, stage, ctx, ctx_rec, stream, stream_rec,
+                              sync_all, args.plan_report)
+        print(json.dumps({"plan_model": leg, "steps": args.steps, "warmup": args.warmup}))
+        return
     det = nets.HipSession(det_g, ctx=ctx)
     rec = nets.HipSession(rec_g, ctx=ctx_rec)
     # inputs resident in HBM: copied once, then every step reuses them
@@ -496,6 +564,10 @@ def main():
     det.sync()
     det_node_ms = det.node_times()
     det.set_profiling(False)
+    plan_leg = None
+    if not args.no_plan:
+        plan_leg = time_plan_model(det_g, det_x, rec_x, stage_ms, ctx, ctx_rec, stream, stream_rec,
+                                   both_sync, args.plan_report)
     if args.node_report:
         # per-node work and eager event times, and each graph's launch plan
         # (for matching a kernel trace of the replays: qppocr_amd.trace_report)
@@ -520,7 +592,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded inputs, random-init weights)",
-        "config": {"workload": "det 1x3x640x640 (config 3) + rec 32x3x48x320 (config 4) per step, "
+        "config": {"workload": "det 1x3x640x640 + rec 32x3x48x320 per step, "
                                "rec ending in the CTC (value, index) pairs",
                    "det_gflop": round(det_flops / 1e9, 3), "rec_gflop": round(rec_flops / 1e9, 3)},
         "det_img_per_s": round(1e3 / det_ms, 2),
@@ -542,6 +614,8 @@ def main():
                           / PEAK_FP32_MFMA_TFLOPS, 4),
             "traffic": head_traffic_bytes("rec_head_gemm_traffic.md")}),
     }
+    if plan_leg is not None:
+        result["plan_model"] = plan_leg
 
     O = None
     threads = None

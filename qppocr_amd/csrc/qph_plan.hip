@@ -209,8 +209,8 @@ __global__ __launch_bounds__(256) void plan_channel_kernel(ChannelK p) {
 
 // ------------------------------------------------------------ dense conv
 //
-// NHWC conv on v_mfma_f32_16x16x4f32: a wave owns 16 output channels x 64
-// output pixels (four 16x16 blocks sharing the weight operand).  K runs in
+// NHWC conv on v_mfma_f32_16x16x4f32 (16 output channels x 16 pixels per
+// block, the weight operand shared by a wave's blocks).  K runs in
 // the CPU's order k = c * taps + t (t = ky * kw + kx); the weights are the
 // plan's repack w[(t * cin + c) * N + co] (nhwc.rs:28-57).  Out-of-image taps
 // and pad channels contribute 0 (the padded channels come last in k, so
@@ -238,74 +238,225 @@ __device__ __forceinline__ bool conv_seeded(const ConvK& p, int64_t co, int64_t 
   return bias_seeded(0, co, (oy - t0) * p.ow + ox, p.N, rows * p.ow);
 }
 
+constexpr int CONV_NB = 2;  // 16-pixel blocks per wave
+constexpr int CONV_CS = 8;  // k-steps (4 k each) loaded per batch
+
+// A wave owns 16 output channels x 32 output pixels.  Lane (li = lane % 16,
+// kq = lane / 16) supplies k = 4 s + kq of step s; it walks its (channel,
+// ky, kx) by +4 in k without divisions.  Operands move in batches of 8
+// steps (three words a step per lane), the next batch's loads in flight
+// while this batch's MFMAs run.  Index arithmetic is 32-bit (the launcher
+// keeps every region below 2^31 words).
 __global__ __launch_bounds__(256) void plan_conv_kernel(ConvK p) {
-  const int64_t b = blockIdx.y;
+  const int b = blockIdx.y;
   const unsigned rn = real_n(p.arena);
-  if (rn != 0 && b >= rn) return;
+  if (rn != 0 && (unsigned)b >= rn) return;
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t ncob = (p.N + 15) / 16;
-  const int64_t co0 = (wave % ncob) * 16, px0 = (wave / ncob) * 64;
-  if (px0 >= p.P) return;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int N = (int)p.N, P = (int)p.P, ow = (int)p.ow;
+  const int ncob = (N + 15) >> 4;
+  const int co0 = (wave % ncob) * 16, px0 = (wave / ncob) * (16 * CONV_NB);
+  if (px0 >= P) return;
   const int li = lane & 15, kq = lane >> 4;
-  // operand A: row co = co0 + li; operand B of block j: pixel px0 + 16 j + li
-  const int64_t co_a = co0 + li;
-  const bool co_ok = co_a < p.N;
-  int64_t oyb[4], oxb[4];
-  bool pok[4];
+  const int co_a = co0 + li;
+  const bool co_ok = co_a < N;
+  const int cin = (int)p.cin, taps = (int)p.taps, kw = (int)p.kw, kh = taps / kw;
+  const int iw = (int)p.iw, ih = (int)p.ih;
+  int iy0[CONV_NB], ix0[CONV_NB];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int64_t px = px0 + 16 * j + li;
-    pok[j] = px < p.P;
-    oyb[j] = pok[j] ? (px / p.ow) * p.sh - p.pt : 0;
-    oxb[j] = pok[j] ? (px % p.ow) * p.sw - p.pl : 0;
+  for (int j = 0; j < CONV_NB; j++) {
+    const int px = px0 + 16 * j + li;
+    const int oy = px / ow, ox = px - oy * ow;
+    iy0[j] = px < P ? oy * (int)p.sh - (int)p.pt : -(1 << 30);
+    ix0[j] = ox * (int)p.sw - (int)p.pl;
   }
-  const float* xb = p.x + b * p.ih * p.iw * p.cin;
-  // accumulators: lane holds rows co0 + 4 kq + v, column px0 + 16 j + li
-  f32x4 acc[4];
+  const float* xb = p.x + (size_t)b * ih * iw * cin;
+  f32x4 acc[CONV_NB];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int64_t px = px0 + 16 * j + li;
+  for (int j = 0; j < CONV_NB; j++) {
+    const int px = px0 + 16 * j + li;
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      const int64_t co = co0 + 4 * kq + v;
-      acc[j][v] = (p.bias && co < p.N && px < p.P && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
+      const int co = co0 + 4 * kq + v;
+      acc[j][v] = (p.bias && co < N && px < P && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
     }
   }
-  const int64_t K = p.cin * p.taps;
-  for (int64_t k0 = 0; k0 < K; k0 += 4) {
-    const int64_t k = k0 + kq;
-    const int64_t c = k / p.taps, t = k - c * p.taps;
-    const int64_t ky = t / p.kw, kx = t - ky * p.kw;
-    const float a = co_ok ? p.w[(t * p.cin + c) * p.N + co_a] : 0.0f;
-    float bv[4];
+  // the lane's first k = kq: k = c * taps + ky * kw + kx
+  int c = kq / taps, ky = (kq % taps) / kw, kx = (kq % taps) % kw;
+  const int steps = cin * taps / 4;
+  // operands of CONV_CS steps per batch: a[u] (weight), b[u][j] (pixels)
+  auto load_batch = [&](int s0, float (&a)[CONV_CS], float (&bv)[CONV_CS][CONV_NB]) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int64_t iy = oyb[j] + ky, ix = oxb[j] + kx;
-      const bool in = pok[j] && iy >= 0 && iy < p.ih && ix >= 0 && ix < p.iw;
-      bv[j] = in ? xb[(iy * p.iw + ix) * p.cin + c] : 0.0f;
+    for (int u = 0; u < CONV_CS; u++) {
+      if (s0 + u >= steps) break;  // wave-uniform
+      a[u] = co_ok ? p.w[((ky * kw + kx) * cin + c) * N + co_a] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < CONV_NB; j++) {
+        const int iy = iy0[j] + ky, ix = ix0[j] + kx;
+        const bool in = (unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw;
+        bv[u][j] = in ? xb[(iy * iw + ix) * cin + c] : 0.0f;
+      }
+      kx += 4;
+      while (kx >= kw) {
+        kx -= kw;
+        if (++ky == kh) {
+          ky = 0;
+          c++;
+        }
+      }
     }
+  };
+  auto mma_batch = [&](int s0, const float (&a)[CONV_CS], const float (&bv)[CONV_CS][CONV_NB]) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[j], acc[j], 0, 0, 0);
+    for (int u = 0; u < CONV_CS; u++) {
+      if (s0 + u >= steps) break;  // wave-uniform: the chain has exactly K terms
+#pragma unroll
+      for (int j = 0; j < CONV_NB; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], bv[u][j], acc[j], 0, 0, 0);
+    }
+  };
+  // two batch buffers: the next batch's loads are in flight during this
+  // batch's MFMAs
+  float a0[CONV_CS], a1[CONV_CS], b0[CONV_CS][CONV_NB], b1[CONV_CS][CONV_NB];
+  load_batch(0, a0, b0);
+  for (int s0 = 0; s0 < steps; s0 += 2 * CONV_CS) {
+    if (s0 + CONV_CS < steps) load_batch(s0 + CONV_CS, a1, b1);
+    mma_batch(s0, a0, b0);
+    if (s0 + CONV_CS >= steps) break;
+    if (s0 + 2 * CONV_CS < steps) load_batch(s0 + 2 * CONV_CS, a0, b0);
+    mma_batch(s0 + CONV_CS, a1, b1);
   }
-  const int64_t cob = co0 + 4 * kq;  // multiple of 4, N % 4 == 0: the four rows are all in or out
-  if (cob >= p.N) return;
-  const float* yres = p.res ? p.res + b * p.P * p.N : nullptr;
-  float* yb = p.y + b * p.P * p.N;
+  const int cob = co0 + 4 * kq;  // multiple of 4, N % 4 == 0: the four rows are all in or out
+  if (cob >= N) return;
+  const float* yres = p.res ? p.res + (size_t)b * P * N : nullptr;
+  float* yb = p.y + (size_t)b * P * N;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int64_t px = px0 + 16 * j + li;
-    if (px >= p.P) continue;
+  for (int j = 0; j < CONV_NB; j++) {
+    const int px = px0 + 16 * j + li;
+    if (px >= P) continue;
     float o[4];
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       float x = acc[j][v];
       if (p.bias && !conv_seeded(p, cob + v, px)) x = x + p.bias[cob + v];
       x = act_apply(x, p.act);
-      if (yres) x = x + yres[px * p.N + cob + v];
+      if (yres) x = x + yres[px * N + cob + v];
       o[v] = x;
     }
-    *(float4*)(yb + px * p.N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+    *(float4*)(yb + px * N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// The same conv for up to CONV_LDS_TAPS taps with the patch matrix staged in
+// LDS: a one-wave workgroup owns 16 output channels x 32 pixels; per group
+// of 4 input channels it stores, for each tap t and pixel j, the 16-byte
+// channel quad x[pixel(j, t)][4g .. 4g + 3] (0 outside the image) at
+// slot t * 32 + j, then runs that group's taps steps (k = c * taps + t within
+// the group, the CPU's order) with B read from LDS.  The next group's quads
+// and weights are loaded into registers while this group's MFMAs run.
+constexpr int CONV_LDS_TAPS = 16;
+constexpr int CONV_LDS_SLOTS = (CONV_LDS_TAPS * 32 + 63) / 64;  // quads per lane and group
+
+__global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
+  extern __shared__ float4 patch[];  // [taps][32]
+  const int b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && (unsigned)b >= rn) return;
+  const int lane = threadIdx.x;
+  const int wave = blockIdx.x;
+  const int N = (int)p.N, P = (int)p.P, ow = (int)p.ow;
+  const int ncob = (N + 15) >> 4;
+  const int co0 = (wave % ncob) * 16, px0 = (wave / ncob) * 32;
+  const int li = lane & 15, kq = lane >> 4;
+  const int co_a = co0 + li;
+  const bool co_ok = co_a < N;
+  const int cin = (int)p.cin, taps = (int)p.taps, kw = (int)p.kw;
+  const int iw = (int)p.iw, ih = (int)p.ih;
+  const float* xb = p.x + (size_t)b * ih * iw * cin;
+  // the slots this lane fills: q = lane + 64 i -> (t = q / 32, j = q % 32);
+  // their input word offsets (channel 0), -1 outside the image
+  int soff[CONV_LDS_SLOTS];
+#pragma unroll
+  for (int i = 0; i < CONV_LDS_SLOTS; i++) {
+    const int q = lane + 64 * i;
+    const int t = q >> 5, px = px0 + (q & 31);
+    soff[i] = -1;
+    if (t < taps && px < P) {
+      const int oy = px / ow, ox = px - oy * ow;
+      const int iy = oy * (int)p.sh - (int)p.pt + t / kw, ix = ox * (int)p.sw - (int)p.pl + t % kw;
+      if ((unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw) soff[i] = (iy * iw + ix) * cin;
+    }
+  }
+  f32x4 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int px = px0 + 16 * j + li;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = co0 + 4 * kq + v;
+      acc[j][v] = (p.bias && co < N && px < P && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
+    }
+  }
+  // step u of a group: k = 4 u + kq -> channel c_u = k / taps, tap t_u = k % taps
+  const int groups = cin / 4;
+  float4 quad[CONV_LDS_SLOTS];
+  float wa[CONV_LDS_TAPS] = {};
+  auto load_group = [&](int g) {
+#pragma unroll
+    for (int i = 0; i < CONV_LDS_SLOTS; i++)
+      quad[i] = soff[i] >= 0 ? *(const float4*)(xb + soff[i] + 4 * g)
+                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int u = 0; u < CONV_LDS_TAPS; u++) {
+      if (u < taps) {  // wave-uniform
+        const int k = 4 * u + kq, c = k / taps, t = k - c * taps;
+        wa[u] = co_ok ? p.w[(t * cin + 4 * g + c) * N + co_a] : 0.0f;
+      }
+    }
+  };
+  load_group(0);
+  for (int g = 0; g < groups; g++) {
+#pragma unroll
+    for (int i = 0; i < CONV_LDS_SLOTS; i++) {
+      const int q = lane + 64 * i;
+      if (q < taps * 32) patch[q] = quad[i];
+    }
+    float wc[CONV_LDS_TAPS];
+#pragma unroll
+    for (int u = 0; u < CONV_LDS_TAPS; u++) wc[u] = wa[u];
+    __syncthreads();
+    if (g + 1 < groups) load_group(g + 1);
+#pragma unroll
+    for (int u = 0; u < CONV_LDS_TAPS; u++) {
+      if (u < taps) {  // wave-uniform: the chain has exactly the group's terms
+        const int k = 4 * u + kq, c = k / taps, t = k - c * taps;
+        const float* row = (const float*)(patch + t * 32);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(wc[u], row[(16 * j + li) * 4 + c], acc[j],
+                                                        0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  const int cob = co0 + 4 * kq;
+  if (cob >= N) return;
+  const float* yres = p.res ? p.res + (size_t)b * P * N : nullptr;
+  float* yb = p.y + (size_t)b * P * N;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int px = px0 + 16 * j + li;
+    if (px >= P) continue;
+    float o[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float x = acc[j][v];
+      if (p.bias && !conv_seeded(p, cob + v, px)) x = x + p.bias[cob + v];
+      x = act_apply(x, p.act);
+      if (yres) x = x + yres[px * N + cob + v];
+      o[v] = x;
+    }
+    *(float4*)(yb + px * N + cob) = make_float4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -545,22 +696,56 @@ struct Decoder {
   int idx = 0;
   const char* kname = "";
   uint32_t p_off = 0;
+  // the dispatch list, what each dispatch reads and writes (word offsets of
+  // its regions), the graph outputs, and the dispatches a fused launch took
+  const qph_plan_dispatch* disp = nullptr;
+  int n_disp = 0;
+  std::vector<uint32_t> wr;
+  std::vector<std::vector<uint32_t>> rd;
+  std::vector<uint32_t> outs;
+  std::vector<char> skip;
 
   std::string where() const {
     return "plan dispatch " + std::to_string(idx) + " (" + kname + ", params at word " +
            std::to_string(p_off) + ")";
   }
-  // the parameter block [p_off, p_off + n) from the uploaded static words
-  int params(uint32_t n, const uint32_t** out) {
-    auto it = std::upper_bound(ups.begin(), ups.end(), p_off,
+  // the n words at off from the uploaded static words, or nullptr
+  const uint32_t* find(uint32_t off, uint32_t n) const {
+    auto it = std::upper_bound(ups.begin(), ups.end(), off,
                                [](uint32_t v, const PlanUpload& u) { return v < u.off; });
-    if (it == ups.begin()) return fail(QPH_EINVAL, where() + ": parameter block not uploaded");
+    if (it == ups.begin()) return nullptr;
     --it;
-    if ((uint64_t)p_off + n > (uint64_t)it->off + it->n)
-      return fail(QPH_EINVAL, where() + ": parameter block shorter than " + std::to_string(n) +
-                                  " words");
-    *out = it->words + (p_off - it->off);
+    if ((uint64_t)off + n > (uint64_t)it->off + it->n) return nullptr;
+    return it->words + (off - it->off);
+  }
+  // the parameter block [p_off, p_off + n) of the dispatch being decoded
+  int params(uint32_t n, const uint32_t** out) {
+    *out = find(p_off, n);
+    if (!*out)
+      return fail(QPH_EINVAL, where() + ": parameter block of " + std::to_string(n) +
+                                  " words not uploaded");
     return QPH_OK;
+  }
+  // dispatch j's parameter block (lookahead), nullptr when j is past the end,
+  // is another kernel or has a short block
+  const uint32_t* peek(int j, int kernel, uint32_t n) const {
+    if (j >= n_disp || disp[j].kernel != kernel || skip[j]) return nullptr;
+    return find(disp[j].p_off, n);
+  }
+  // true when no dispatch after `after` other than those in ok reads a word
+  // of [o, o + len) before a later dispatch writes into it, and no graph
+  // output lies in it
+  bool only_readers(int after, uint32_t o, uint64_t len, std::initializer_list<int> ok) const {
+    const uint64_t e = (uint64_t)o + len;
+    for (uint32_t g : outs)
+      if (g >= o && g < e) return false;
+    for (int j = after + 1; j < n_disp; j++) {
+      bool reads = false;
+      for (uint32_t r : rd[j]) reads = reads || (r >= o && r < e);
+      if (reads && std::find(ok.begin(), ok.end(), j) == ok.end()) return false;
+      if (wr[j] >= o && wr[j] < e) return true;
+    }
+    return true;
   }
   // a region of n words at off inside the arena (16-byte aligned for vec4 access)
   int region(uint32_t off, uint64_t n, bool vec4, const char* what) {
@@ -574,6 +759,101 @@ struct Decoder {
   }
   float* at(uint32_t off) const { return pl->arena + off; }
 };
+
+// Word counts of the parameter blocks (the n_*.comp layouts; n_concat_c has
+// 4 + 2 per input).
+const uint32_t kParamWords[kNumPlanKernels] = {7, 8, 6, 6, 7, 10, 21, 21, 20, 18,
+                                               14, 4, 5, 6, 9, 4, 14, 4, 6, 8};
+
+// What dispatch q reads (region start offsets) and writes.
+void dispatch_io(const Decoder& d, const qph_plan_dispatch& q, uint32_t* wr,
+                 std::vector<uint32_t>* rd) {
+  *wr = OFF_NONE;
+  rd->clear();
+  if (q.kernel < 0 || q.kernel >= kNumPlanKernels) return;
+  const uint32_t* w = d.find(q.p_off, kParamWords[q.kernel]);
+  if (!w) return;
+  auto r = [&](std::initializer_list<int> idx) {
+    for (int i : idx)
+      if (w[i] != OFF_NONE) rd->push_back(w[i]);
+  };
+  switch (q.kernel) {
+    case PK_ELEM: r({1, 2}); *wr = w[3]; break;
+    case PK_CHANNEL: r({1, 2, 3}); *wr = w[4]; break;
+    case PK_CONV: case PK_CONV8: r({0, 1, 2, 20}); *wr = w[3]; break;
+    case PK_CONV_DW: r({0, 1, 2, 19}); *wr = w[3]; break;
+    case PK_CONVT: r({0, 1, 2}); *wr = w[3]; break;
+    case PK_ATTN_MM: r({0, 1}); *wr = w[2]; break;
+    case PK_CONCAT_C: {
+      const uint32_t n = w[2];
+      if (n > 8 || !(w = d.find(q.p_off, 4 + 2 * n))) return;
+      for (uint32_t i = 0; i < n; i++) rd->push_back(w[4 + 2 * i]);
+      *wr = w[0];
+      break;
+    }
+    default: r({0}); *wr = w[1]; break;  // entry, exits, pool, reductions, resize, transposes, softmax
+  }
+}
+
+// The epilogue of a conv-family launch after absorbing the dispatches that
+// only consume its output: act (hardswish from n_elem 2 + n_elem 5 on it),
+// a per-column bias (the [V] broadcast n_channel 1 after a MatMul), a
+// residual (n_elem 4), and the region the fused launch writes.  Each step is
+// the operation the absorbed dispatch performs, in the same order (bias,
+// activation, residual), so the values are those of the separate dispatches.
+struct Epi {
+  uint32_t y;
+  Act act;
+  uint32_t bias, res;
+};
+
+int absorb(Decoder& d, uint64_t len, int64_t cols, bool gemm, Epi* e) {
+  int last = d.idx;   // the dispatch whose output e->y is
+  for (int j = d.idx + 1; j < d.n_disp; j = last + 1) {
+    const uint32_t* w;
+    const uint32_t* w2;
+    if (e->act.kind == 0 && e->res == OFF_NONE && (w = d.peek(j, PK_ELEM, 7)) && w[0] == 2 &&
+        w[1] == e->y && w[4] == len && (w2 = d.peek(j + 1, PK_ELEM, 7)) && w2[0] == 5 &&
+        w2[4] == len &&
+        ((w2[1] == e->y && w2[2] == w[3]) || (w2[1] == w[3] && w2[2] == e->y)) &&
+        d.only_readers(last, e->y, len, {j, j + 1}) && d.only_readers(j, w[3], len, {j + 1})) {
+      QPH_TRY(d.region(w2[3], len, true, "fused output"));
+      qph_act a{};
+      a.kind = QPH_ACT_HARDSWISH;
+      std::memcpy(&a.c1, &w[5], 4);
+      std::memcpy(&a.c2, &w[6], 4);
+      e->act = make_act(&a);
+      e->y = w2[3];
+      d.skip[j] = d.skip[j + 1] = 1;
+      last = j + 1;
+      continue;
+    }
+    if (gemm && e->bias == OFF_NONE && e->act.kind == 0 && e->res == OFF_NONE &&
+        (w = d.peek(j, PK_CHANNEL, 10)) && w[0] == 1 && w[1] == e->y && w[5] == len &&
+        (int64_t)w[6] == cols && (uint64_t)w[9] * cols == len &&
+        d.only_readers(last, e->y, len, {j})) {
+      QPH_TRY(d.region(w[2], (uint64_t)cols, true, "fused bias"));
+      QPH_TRY(d.region(w[4], len, true, "fused output"));
+      e->bias = w[2];
+      e->y = w[4];
+      d.skip[j] = 1;
+      last = j;
+      continue;
+    }
+    if (e->res == OFF_NONE && (w = d.peek(j, PK_ELEM, 7)) && w[0] == 4 && w[4] == len &&
+        (w[1] == e->y || w[2] == e->y) && w[1] != w[2] && d.only_readers(last, e->y, len, {j})) {
+      const uint32_t other = w[1] == e->y ? w[2] : w[1];
+      QPH_TRY(d.region(other, len, true, "fused residual"));
+      QPH_TRY(d.region(w[3], len, true, "fused output"));
+      e->res = other;
+      e->y = w[3];
+      d.skip[j] = 1;
+      last = j;
+    }
+    break;  // nothing follows a residual
+  }
+  return QPH_OK;
+}
 
 inline float f32_of(uint32_t u) {
   float f;
@@ -647,14 +927,17 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
     // GEMM over the NHWC rows, bias per column after the chain
     const bool seeded_any = bias && k.rule_path == 1 && P % 32 != 0;
     if (!seeded_any) {
+      Epi e{out, act, bo, ro};
+      QPH_TRY(absorb(d, (uint64_t)nb * P * N, N, true, &e));
       GemmArgs g{};
       g.a = x; g.lda = cin; g.a_batch = 0;
       g.b = wt; g.ldb = N; g.b_batch = 0;
-      g.c = y; g.ldc = N; g.c_batch = 0;
+      g.c = d.at(e.y); g.ldc = N; g.c_batch = 0;
       g.m = nb * P; g.n = N; g.k = cin; g.batch = 1;
-      g.bias = bias; g.bias_mode = bias ? 2 : 0; g.seed_rule = 0;
-      g.act = act;
-      g.res = res; g.ldr = N; g.r_batch = 0;
+      g.bias = e.bias == OFF_NONE ? nullptr : d.at(e.bias);
+      g.bias_mode = g.bias ? 2 : 0; g.seed_rule = 0;
+      g.act = e.act;
+      g.res = e.res == OFF_NONE ? nullptr : d.at(e.res); g.ldr = N; g.r_batch = 0;
       return add_launch(d.pl, d.idx, [g](hipStream_t s) { return launch_gemm(g, s); });
     }
   } else if (sw == 1 || sw == 2) {
@@ -667,9 +950,24 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
     if (tile > oh) tile = oh;
     k.tile = tile;
   }
-  const int64_t waves = ((N + 15) / 16) * ((P + 63) / 64);
-  if (waves / 4 + 1 >= (1ll << 31) || nb > 65535)
-    return fail(QPH_EUNSUPPORTED, d.where() + ": conv grid too large");
+  const int64_t waves = ((N + 15) / 16) * ((P + 16 * CONV_NB - 1) / (16 * CONV_NB));
+  if (waves / 4 + 1 >= (1ll << 31) || nb > 65535 || ih * iw * cin >= (1ll << 31) ||
+      taps * cin * N >= (1ll << 31) || P * N >= (1ll << 31))
+    return fail(QPH_EUNSUPPORTED, d.where() + ": conv grid or regions too large");
+  Epi e{out, act, bo, ro};
+  QPH_TRY(absorb(d, (uint64_t)nb * P * N, N, false, &e));
+  k.act = e.act;
+  k.res = e.res == OFF_NONE ? nullptr : d.at(e.res);
+  k.y = d.at(e.y);
+  if (taps <= CONV_LDS_TAPS) {
+    const int64_t lwaves = ((N + 15) / 16) * ((P + 31) / 32);
+    const size_t lds = (size_t)taps * 32 * 16;
+    return add_launch(d.pl, d.idx, [k, lwaves, nb, lds](hipStream_t s) {
+      hipLaunchKernelGGL(plan_conv_lds_kernel, dim3((unsigned)lwaves, (unsigned)nb), dim3(64), lds,
+                         s, k);
+      return launch_check("plan_conv_lds_kernel");
+    });
+  }
   return add_launch(d.pl, d.idx, [k, waves, nb](hipStream_t s) {
     hipLaunchKernelGGL(plan_conv_kernel, dim3((unsigned)((waves + 3) / 4), (unsigned)nb),
                        dim3(256), 0, s, k);
@@ -800,9 +1098,11 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       QPH_TRY(d.region(w[3], (uint64_t)nb * P * C, true, "output"));
       if (w[2] != OFF_NONE) QPH_TRY(d.region(w[2], (uint64_t)C, true, "bias"));
       if (w[19] != OFF_NONE) QPH_TRY(d.region(w[19], (uint64_t)nb * P * C, true, "residual"));
+      Epi e{w[3], act, OFF_NONE, w[19]};
+      QPH_TRY(absorb(d, (uint64_t)nb * P * C, C, false, &e));
       DwK k{pl->arena, d.at(w[0]), d.at(w[1]), w[2] == OFF_NONE ? nullptr : d.at(w[2]),
-            w[19] == OFF_NONE ? nullptr : d.at(w[19]), d.at(w[3]),
-            P, C / 4, ow, iw, ih, taps, kw, sh, sw, pt, pl_, act};
+            e.res == OFF_NONE ? nullptr : d.at(e.res), d.at(e.y),
+            P, C / 4, ow, iw, ih, taps, kw, sh, sw, pt, pl_, e.act};
       return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
         hipLaunchKernelGGL(plan_dw_kernel, dim3(blocks_for(k.P * k.c4), (unsigned)nb), dim3(256), 0,
                            s, k);
@@ -978,9 +1278,26 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       if (x != y && (uint64_t)w[1] < (uint64_t)w[0] + rows * cp &&
           (uint64_t)w[0] < (uint64_t)w[1] + rows * cp)
         return fail(QPH_EUNSUPPORTED, d.where() + ": input and output overlap");
+      // the first maximum of each row in the same pass when an
+      // n_exit3_argmax of this output follows (after n_exit3 reads of it):
+      // the softmax kernels take it from the probabilities they store
+      float* pairs = nullptr;
+      for (int j = d.idx + 1; j < d.n_disp; j++) {
+        const uint32_t* e3 = d.peek(j, PK_EXIT3, 6);
+        const uint32_t* am = d.peek(j, PK_EXIT3_ARGMAX, 6);
+        if (e3 && e3[0] == w[1] && ((uint64_t)e3[1] >= (uint64_t)w[1] + rows * cp ||
+                                    (uint64_t)e3[1] + (uint64_t)e3[2] * e3[3] <= w[1]))
+          continue;
+        if (am && am[0] == w[1] && am[2] == rows && am[3] == cols && am[4] == cp) {
+          QPH_TRY(d.region(am[1], (uint64_t)rows * 2, false, "pairs"));
+          pairs = d.at(am[1]);
+          d.skip[j] = 1;
+        }
+        break;
+      }
       PadColsK pk{y, rows, cols, cp};
       return add_launch(pl, d.idx, [=](hipStream_t s) {
-        QPH_TRY(launch_softmax_pitched(x, rows, cols, cp, y, cp, nullptr, s));
+        QPH_TRY(launch_softmax_pitched(x, rows, cols, cp, y, cp, pairs, s));
         if (cp == cols) return QPH_OK;
         hipLaunchKernelGGL(plan_pad_cols_kernel, dim3(blocks_for(rows * (cp - cols))), dim3(256),
                            0, s, pk);
@@ -1115,9 +1432,17 @@ QPH_API int qph_plan_create(qph_ctx* ctx, const qph_plan_spec* spec, qph_plan** 
                    "hipMemcpy(plan upload)");
     if (rc) return bail(rc);
   }
+  d.disp = spec->dispatches;
+  d.n_disp = spec->n_dispatches;
+  d.wr.assign((size_t)d.n_disp, OFF_NONE);
+  d.rd.assign((size_t)d.n_disp, {});
+  d.skip.assign((size_t)d.n_disp, 0);
+  d.outs.assign(spec->out_offs, spec->out_offs + spec->n_outputs);
+  for (int32_t i = 0; i < d.n_disp; i++) dispatch_io(d, d.disp[i], &d.wr[i], &d.rd[i]);
   std::vector<PendingHw> pending;
   for (int32_t i = 0; i < spec->n_dispatches; i++) {
     const qph_plan_dispatch& q = spec->dispatches[i];
+    if (d.skip[i]) continue;  // taken into an earlier dispatch's launch
     d.idx = i;
     d.kname = (q.kernel >= 0 && q.kernel < kNumPlanKernels) ? kPlanKernels[q.kernel] : "?";
     d.p_off = q.p_off;

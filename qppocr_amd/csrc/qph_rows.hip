@@ -631,12 +631,84 @@ __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, i
   }
 }
 
+// Narrow rows (cols <= SM_SMALL_MAX_COLS, e.g. the attention's T-wide
+// rows): one thread per row runs softmax_row as written
+// (activation.rs:346-403 / x86.rs:1091-1134): the max over eight lane
+// maxima then the tail, exp1 stored with the eight lane sums, their hadd
+// tree ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7)), the tail added in
+// order, then the multiply by 1 / sum; pairs: the first strict maximum of
+// the probabilities.  In place when probs == logits (each element is read
+// before it is written).
+#define SM_SMALL_MAX_COLS 128
+__global__ __launch_bounds__(256) void softmax_small_kernel(const float* logits, int64_t rows,
+                                                            int cols, int64_t ld, float* probs,
+                                                            int64_t ldo, float* pairs) {
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const float* xr = logits + row * ld;
+  float* pr = probs + row * ldo;
+  int i = 0;
+  float mx;
+  if (cols >= 8) {
+    float vmax[8];
+    for (int j = 0; j < 8; j++) vmax[j] = xr[j];
+    for (; i + 8 <= cols; i += 8)
+      for (int j = 0; j < 8; j++)
+        if (xr[i + j] > vmax[j]) vmax[j] = xr[i + j];
+    mx = vmax[0];
+    for (int j = 1; j < 8; j++)
+      if (vmax[j] > mx) mx = vmax[j];
+  } else {
+    i = 1;
+    mx = xr[0];
+  }
+  for (; i < cols; i++)
+    if (xr[i] > mx) mx = xr[i];
+  float sum = 0.0f;
+  int i2 = 0;
+  if (cols >= 8) {
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (; i2 + 8 <= cols; i2 += 8)
+      for (int j = 0; j < 8; j++) {
+        const float e = exp1(xr[i2 + j] - mx);
+        pr[i2 + j] = e;
+        acc[j] = acc[j] + e;
+      }
+    sum = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+  }
+  for (; i2 < cols; i2++) {
+    const float e = exp1(xr[i2] - mx);
+    pr[i2] = e;
+    sum = sum + e;
+  }
+  const float inv = 1.0f / sum;
+  float bv = 0.0f;
+  int bi = 0;
+  for (int k = 0; k < cols; k++) {
+    const float p = pr[k] * inv;
+    pr[k] = p;
+    if (k == 0 || p > bv) {
+      bv = p;
+      bi = k;
+    }
+  }
+  if (pairs) {
+    pairs[2 * row] = bv;
+    pairs[2 * row + 1] = __uint_as_float((unsigned)bi);
+  }
+}
+
 // logits rows ld floats apart (ld >= cols); probs rows ldo floats apart.
 int launch_softmax_pitched(const float* logits, int64_t rows, int64_t cols, int64_t ld,
                            float* probs, int64_t ldo, float* pairs, hipStream_t s) {
   if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
   if (ld < cols || ldo < cols) return fail(QPH_EINVAL, "softmax: row pitch below the row width");
   if (probs == logits && ldo != ld) return fail(QPH_EINVAL, "softmax: in place with two pitches");
+  if (cols <= SM_SMALL_MAX_COLS && probs) {
+    hipLaunchKernelGGL(softmax_small_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, logits,
+                       rows, (int)cols, ld, probs, ldo, pairs);
+    return launch_check("softmax_small_kernel");
+  }
   if (cols <= SM_LDS_MAX_COLS && ld < (1ll << 31) && ldo < (1ll << 31)) {
     hipLaunchKernelGGL(softmax_lds_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
                        (int)cols, (int)ld, probs, (int)ldo, pairs);
