@@ -460,6 +460,138 @@ __global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
   }
 }
 
+// The conv for 1, 4 or 9 taps with every operand moved by buffer->LDS
+// loads (no staging registers) and CONV_DMA_D groups of 4 input channels in
+// flight.  Per group a lane issues XQ loads of channel quads (slot
+// q = lane + 64 i: tap q / 32, pixel q % 32; outside the image or past the
+// slots an offset past the buffer, which reads 0) and WQ loads of weight
+// chunks (chunk r = lane + 64 i: row r / 4 = 4 t + c, output channels
+// co0 + 4 (r % 4) .. + 3).  Loads are inline asm, so the compiler adds no
+// waits of its own; the wait before group g's steps leaves the loads of
+// the groups after it outstanding (vmcnt counts in issue order).  A group's
+// buffer is refilled only after the MFMAs that read it were issued.
+constexpr int CONV_DMA_D = 4;
+
+template <int TAPS>
+struct DmaGeom {
+  static constexpr int XQ = (TAPS * 32 + 63) / 64;   // quad loads per lane and group
+  static constexpr int WQ = (TAPS * 16 + 63) / 64;   // weight-chunk loads per lane and group
+  static constexpr int L = XQ + WQ;
+  static constexpr int BUF = (XQ + WQ) * 64;         // float4 per group buffer
+};
+
+template <int TAPS>
+__global__ __launch_bounds__(64) void plan_conv_dma_kernel(ConvK p) {
+  using G = DmaGeom<TAPS>;
+  extern __shared__ float4 ring[];  // CONV_DMA_D buffers of G::BUF float4
+  const int b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && (unsigned)b >= rn) return;
+  const int lane = threadIdx.x;
+  const int N = (int)p.N, P = (int)p.P, ow = (int)p.ow;
+  const int ncob = (N + 15) >> 4;
+  const int co0 = (blockIdx.x % ncob) * 16, px0 = (blockIdx.x / ncob) * 32;
+  const int li = lane & 15, kq = lane >> 4;
+  const int cin = (int)p.cin, kw = (int)p.kw;
+  const int iw = (int)p.iw, ih = (int)p.ih;
+  const unsigned OOB = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + (size_t)b * ih * iw * cin), 0, ih * iw * cin * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.w, 0, TAPS * cin * N * 4, 0x00020000);
+  int xo[G::XQ], wo[G::WQ];   // word offsets at group 0, -1: reads 0
+#pragma unroll
+  for (int i = 0; i < G::XQ; i++) {
+    const int q = lane + 64 * i, t = q >> 5, px = px0 + (q & 31);
+    xo[i] = -1;
+    if (t < TAPS && px < P) {
+      const int oy = px / ow, ox = px - oy * ow;
+      const int iy = oy * (int)p.sh - (int)p.pt + t / kw, ix = ox * (int)p.sw - (int)p.pl + t % kw;
+      if ((unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw) xo[i] = (iy * iw + ix) * cin;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < G::WQ; i++) {
+    const int r = lane + 64 * i, row = r >> 2, t = row >> 2, c = row & 3, co = co0 + 4 * (r & 3);
+    wo[i] = (row < 4 * TAPS && co < N) ? (t * cin + c) * N + co : -1;
+  }
+  auto issue = [&](int g) {
+    float4* buf = ring + (g % CONV_DMA_D) * G::BUF;
+#pragma unroll
+    for (int i = 0; i < G::L; i++) {
+      const bool isx = i < G::XQ;
+      const unsigned off = isx ? (xo[i] >= 0 ? (unsigned)((xo[i] + 4 * g) * 4) : OOB)
+                               : (wo[i - G::XQ] >= 0 ? (unsigned)((wo[i - G::XQ] + 4 * g * N) * 4) : OOB);
+      const unsigned m = __builtin_amdgcn_readfirstlane(
+          (unsigned)(uintptr_t)(__attribute__((address_space(3))) float4*)(buf + 64 * i));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // m0 is reserved; nothing else uses it here
+      __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m),
+                       "v"(off), "s"(isx ? xr : wr)
+                       : "m0");
+#pragma clang diagnostic pop
+    }
+  };
+  f32x4 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int px = px0 + 16 * j + li;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = co0 + 4 * kq + v;
+      acc[j][v] = (p.bias && co < N && px < P && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
+    }
+  }
+  const int groups = cin / 4;
+#pragma unroll
+  for (int g = 0; g < CONV_DMA_D - 1; g++)
+    if (g < groups) issue(g);
+  for (int g = 0; g < groups; g++) {
+    __asm__ volatile("" ::: "memory");
+    if (g + CONV_DMA_D - 1 < groups) issue(g + CONV_DMA_D - 1);
+    const int ahead = min(CONV_DMA_D - 1, groups - 1 - g);   // groups issued after g
+    switch (ahead) {
+      case 3: wait_vmcnt<3 * G::L>(); break;
+      case 2: wait_vmcnt<2 * G::L>(); break;
+      case 1: wait_vmcnt<G::L>(); break;
+      default: wait_vmcnt<0>(); break;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    const float* xq = (const float*)(ring + (g % CONV_DMA_D) * G::BUF);
+    const float* wq = xq + 4 * 64 * G::XQ;
+#pragma unroll
+    for (int u = 0; u < TAPS; u++) {
+      const int k = 4 * u + kq, c = k / TAPS, t = k - c * TAPS;
+      const float a = wq[(4 * t + c) * 16 + li];
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xq[(t * 32 + 16 * j + li) * 4 + c], acc[j],
+                                                      0, 0, 0);
+    }
+  }
+  const int cob = co0 + 4 * kq;
+  if (cob >= N) return;
+  const float* yres = p.res ? p.res + (size_t)b * P * N : nullptr;
+  float* yb = p.y + (size_t)b * P * N;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int px = px0 + 16 * j + li;
+    if (px >= P) continue;
+    float o[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float x = acc[j][v];
+      if (p.bias && !conv_seeded(p, cob + v, px)) x = x + p.bias[cob + v];
+      x = act_apply(x, p.act);
+      if (yres) x = x + yres[px * N + cob + v];
+      o[v] = x;
+    }
+    *(float4*)(yb + px * N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // ------------------------------------------------------------- depthwise
 struct DwK {
   const float* arena; const float* x; const float* w; const float* bias; const float* res;
@@ -959,8 +1091,27 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
   k.act = e.act;
   k.res = e.res == OFF_NONE ? nullptr : d.at(e.res);
   k.y = d.at(e.y);
+  const int64_t lwaves = ((N + 15) / 16) * ((P + 31) / 32);
+  // the ring pays off from two channel groups on (a 3-channel stem has one)
+  if ((taps == 1 || taps == 4 || taps == 9) && cin >= 8 && taps * cin * N * 4 < (1ll << 31) &&
+      ih * iw * cin * 4 < (1ll << 31) && lwaves < (1ll << 31)) {
+    auto go = [k, lwaves, nb](auto fn, size_t lds, hipStream_t s) {
+      hipLaunchKernelGGL(fn, dim3((unsigned)lwaves, (unsigned)nb), dim3(64), lds, s, k);
+      return launch_check("plan_conv_dma_kernel");
+    };
+    if (taps == 1)
+      return add_launch(d.pl, d.idx, [go](hipStream_t s) {
+        return go(plan_conv_dma_kernel<1>, CONV_DMA_D * DmaGeom<1>::BUF * 16, s);
+      });
+    if (taps == 4)
+      return add_launch(d.pl, d.idx, [go](hipStream_t s) {
+        return go(plan_conv_dma_kernel<4>, CONV_DMA_D * DmaGeom<4>::BUF * 16, s);
+      });
+    return add_launch(d.pl, d.idx, [go](hipStream_t s) {
+      return go(plan_conv_dma_kernel<9>, CONV_DMA_D * DmaGeom<9>::BUF * 16, s);
+    });
+  }
   if (taps <= CONV_LDS_TAPS) {
-    const int64_t lwaves = ((N + 15) / 16) * ((P + 31) / 32);
     const size_t lds = (size_t)taps * 32 * 16;
     return add_launch(d.pl, d.idx, [k, lwaves, nb, lds](hipStream_t s) {
       hipLaunchKernelGGL(plan_conv_lds_kernel, dim3((unsigned)lwaves, (unsigned)nb), dim3(64), lds,

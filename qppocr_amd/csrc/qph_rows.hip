@@ -632,69 +632,103 @@ __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, i
 }
 
 // Narrow rows (cols <= SM_SMALL_MAX_COLS, e.g. the attention's T-wide
-// rows): one thread per row runs softmax_row as written
-// (activation.rs:346-403 / x86.rs:1091-1134): the max over eight lane
-// maxima then the tail, exp1 stored with the eight lane sums, their hadd
-// tree ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7)), the tail added in
-// order, then the multiply by 1 / sum; pairs: the first strict maximum of
-// the probabilities.  In place when probs == logits (each element is read
-// before it is written).
+// rows): eight threads per row, thread j running the reference's lane j
+// (activation.rs:346-403 / x86.rs:1091-1134): its max over elements
+// 8 g + j of the full groups, its chain of exp1 terms; lane 0 then combines
+// the eight maxima in order and takes the tail elements one by one, forms
+// the hadd tree ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7)) and adds
+// the tail exponentials in order; every element is multiplied by 1 / sum.
+// pairs: the first strict maximum of the probabilities (lane maxima
+// combined by value, then lowest index).  In place when probs == logits
+// (each element is read before it is written, by the thread that writes it).
 #define SM_SMALL_MAX_COLS 128
 __global__ __launch_bounds__(256) void softmax_small_kernel(const float* logits, int64_t rows,
                                                             int cols, int64_t ld, float* probs,
                                                             int64_t ldo, float* pairs) {
-  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= rows) return;
-  const float* xr = logits + row * ld;
-  float* pr = probs + row * ldo;
-  int i = 0;
-  float mx;
-  if (cols >= 8) {
-    float vmax[8];
-    for (int j = 0; j < 8; j++) vmax[j] = xr[j];
-    for (; i + 8 <= cols; i += 8)
-      for (int j = 0; j < 8; j++)
-        if (xr[i + j] > vmax[j]) vmax[j] = xr[i + j];
-    mx = vmax[0];
-    for (int j = 1; j < 8; j++)
-      if (vmax[j] > mx) mx = vmax[j];
-  } else {
-    i = 1;
-    mx = xr[0];
-  }
-  for (; i < cols; i++)
-    if (xr[i] > mx) mx = xr[i];
-  float sum = 0.0f;
-  int i2 = 0;
-  if (cols >= 8) {
-    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (; i2 + 8 <= cols; i2 += 8)
-      for (int j = 0; j < 8; j++) {
-        const float e = exp1(xr[i2 + j] - mx);
-        pr[i2 + j] = e;
-        acc[j] = acc[j] + e;
-      }
-    sum = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
-  }
-  for (; i2 < cols; i2++) {
-    const float e = exp1(xr[i2] - mx);
-    pr[i2] = e;
-    sum = sum + e;
-  }
-  const float inv = 1.0f / sum;
-  float bv = 0.0f;
-  int bi = 0;
-  for (int k = 0; k < cols; k++) {
-    const float p = pr[k] * inv;
-    pr[k] = p;
-    if (k == 0 || p > bv) {
-      bv = p;
-      bi = k;
+  const int j = threadIdx.x & 7;
+  const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const bool live = row < rows;
+  const float* xr = logits + (live ? row : 0) * ld;
+  float* pr = probs + (live ? row : 0) * ldo;
+  const int q = cols >= 8 ? cols / 8 : 0;  // full groups of eight
+  float vm = -__builtin_inff();
+  if (live && q > 0) {
+    vm = xr[j];
+    for (int g = 1; g < q; g++) {
+      const float v = xr[8 * g + j];
+      if (v > vm) vm = v;
     }
   }
+  // lane 0 of the row: the reference's combination order
+  float mx = 0.0f;
+  {
+    float lm[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) lm[t] = __shfl(vm, t, 8);
+    if (j == 0 && live) {
+      int i;
+      if (q > 0) {
+        mx = lm[0];
+        for (int t = 1; t < 8; t++)
+          if (lm[t] > mx) mx = lm[t];
+        i = 8 * q;
+      } else {
+        mx = xr[0];
+        i = 1;
+      }
+      for (; i < cols; i++)
+        if (xr[i] > mx) mx = xr[i];
+    }
+    mx = __shfl(mx, 0, 8);
+  }
+  float acc = 0.0f;
+  if (live)
+    for (int g = 0; g < q; g++) {
+      const float e = exp1(xr[8 * g + j] - mx);
+      pr[8 * g + j] = e;
+      acc = acc + e;
+    }
+  float inv;
+  {
+    float la[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) la[t] = __shfl(acc, t, 8);
+    float sum = 0.0f;
+    if (j == 0 && live) {
+      if (q > 0) sum = ((la[0] + la[4]) + (la[1] + la[5])) + ((la[2] + la[6]) + (la[3] + la[7]));
+      for (int i = 8 * q; i < cols; i++) {
+        const float e = exp1(xr[i] - mx);
+        pr[i] = e;
+        sum = sum + e;
+      }
+    }
+    inv = __shfl(1.0f / sum, 0, 8);
+  }
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  if (live)
+    for (int k = j; k < cols; k += 8) {
+      const float p = pr[k] * inv;
+      pr[k] = p;
+      if (bi == 0x7fffffff || p > bv) {
+        bv = p;
+        bi = k;
+      }
+    }
   if (pairs) {
-    pairs[2 * row] = bv;
-    pairs[2 * row + 1] = __uint_as_float((unsigned)bi);
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 8);
+      const int oi = __shfl_xor(bi, off, 8);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (j == 0 && live) {
+      pairs[2 * row] = bv;
+      pairs[2 * row + 1] = __uint_as_float((unsigned)bi);
+    }
   }
 }
 
@@ -705,7 +739,7 @@ int launch_softmax_pitched(const float* logits, int64_t rows, int64_t cols, int6
   if (ld < cols || ldo < cols) return fail(QPH_EINVAL, "softmax: row pitch below the row width");
   if (probs == logits && ldo != ld) return fail(QPH_EINVAL, "softmax: in place with two pitches");
   if (cols <= SM_SMALL_MAX_COLS && probs) {
-    hipLaunchKernelGGL(softmax_small_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, logits,
+    hipLaunchKernelGGL(softmax_small_kernel, dim3(ceil_div(rows, 32)), dim3(256), 0, s, logits,
                        rows, (int)cols, ld, probs, ldo, pairs);
     return launch_check("softmax_small_kernel");
   }
