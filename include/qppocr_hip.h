@@ -465,9 +465,11 @@ QPH_API int qph_plan_destroy(qph_plan* plan);
 /* real_n for the following runs (0 = every batch row): the reference's run
  * writes it to word 0 before each submit. */
 QPH_API int qph_plan_set_real_n(qph_plan* plan, uint32_t real_n);
-/* One run: input (numel = in_numel) to in_f32_off, the dispatches, then
- * the outputs to the host buffers (NULL entries skipped) and a sync.
- * input NULL: the arena's input region is used as it is. */
+/* One run: real_n to word 0, input (numel = in_numel) to in_f32_off, the
+ * dispatches, then the outputs to the host buffers (NULL entries skipped)
+ * and a sync; without outputs the run is only enqueued on the context's
+ * stream.  input NULL: the arena's input region is used as it is.  Runs of
+ * one plan share its arena: calls on one plan must not overlap. */
 QPH_API int qph_plan_run(qph_plan* plan, const float* input, int32_t input_is_device,
                          float* const* outputs_host);
 /* The device arena (valid until destroy), for reading any region. */

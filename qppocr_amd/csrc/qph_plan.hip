@@ -790,6 +790,11 @@ __global__ __launch_bounds__(256) void plan_pad_cols_kernel(PadColsK p) {
   p.y[r * p.cpad + p.cols + (i - r * w)] = 0.0f;
 }
 
+// word 0 of the arena: the run's real batch count, passed by value
+__global__ void plan_set_real_n_kernel(unsigned* arena, unsigned real_n) {
+  if (threadIdx.x == 0) arena[0] = real_n;
+}
+
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -1623,8 +1628,12 @@ QPH_API int qph_plan_run(qph_plan* pl, const float* input, int32_t input_is_devi
                          float* const* outputs_host) {
   if (!pl) return fail(QPH_EINVAL, "plan_run: NULL plan");
   hipStream_t s = pl->ctx->stream;
-  // word 0: the real batch rows of this run (0 = all), written before the graph
-  QPH_TRY_HIP(hipMemcpyAsync(pl->arena, &pl->real_n, 4, hipMemcpyHostToDevice, s));
+  // word 0: the real batch rows of this run (0 = all), written before the
+  // graph by a kernel that takes the value as an argument (stream-ordered,
+  // no host buffer for a later qph_plan_set_real_n to race with)
+  hipLaunchKernelGGL(plan_set_real_n_kernel, dim3(1), dim3(64), 0, s, (unsigned*)pl->arena,
+                     pl->real_n);
+  QPH_TRY(launch_check("plan_set_real_n_kernel"));
   if (input)
     QPH_TRY_HIP(hipMemcpyAsync(pl->arena + pl->in_off, input, (size_t)pl->in_numel * 4,
                                input_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));

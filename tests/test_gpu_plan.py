@@ -573,3 +573,22 @@ def test_plan_rec_graph(gpu, oracle, probs):
     ref = onets.run_graph(g, x)
     for i, (a, b) in enumerate(zip(got, ref)):
         assert_bitexact(a, b, f"output {i}")
+
+
+def test_plan_rec_padded_batch_real_n(gpu, oracle):
+    """A rec plan built for a padded batch of 3 run with real_n = 2 (the
+    reference session's batch grain, vulkan/session.rs:283-296): the two
+    real items' pairs equal the oracle's run of the 2-item graph; the padded
+    item holds garbage and is never read."""
+    from oracle import nets as onets
+    from qppocr_amd import nets, plan
+    x2, r = nets.rec_input(3, 2, 48, 160)
+    ws = nets.rec_weights(r)
+    g2 = nets.build_rec_graph(ws, 2, 160, probs=False)
+    g3 = nets.build_rec_graph(ws, 3, 160, probs=False)
+    x3 = np.concatenate([x2, np.full((1, 3, 48, 160), 1e30, np.float32)], 0)
+    s = plan.HipPlanSession(plan.build_plan(g3))
+    got = s.run(x3, real_n=2)[0]
+    s.close()
+    ref = onets.run_graph(g2, x2)[0]
+    assert_bitexact(got[:2], ref, "pairs of the real items")
