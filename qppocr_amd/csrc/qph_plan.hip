@@ -822,6 +822,7 @@ struct qph_plan {
   std::vector<uint32_t> out_off;
   std::vector<int64_t> out_numel;
   uint32_t real_n;
+  std::vector<float*> owned;  // transposed weight copies for the resident-weight GEMM
 };
 
 namespace qph {
@@ -1066,6 +1067,22 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
     if (!seeded_any) {
       Epi e{out, act, bo, ro};
       QPH_TRY(absorb(d, (uint64_t)nb * P * N, N, true, &e));
+      if (!gemm_takes_wide(nb * P, N, 1) && linear_nt_eligible(nb * P, N, cin, cin) &&
+          in % 4 == 0) {
+        // the session's linear kernel: the weight held transposed ([N][K],
+        // k contiguous), made once here on the plan's stream
+        float* wt_t = nullptr;
+        QPH_TRY_HIP(hipMalloc((void**)&wt_t, (size_t)N * cin * 4));
+        d.pl->owned.push_back(wt_t);
+        QPH_TRY(launch_transpose(wt, cin, N, wt_t, d.pl->ctx->stream));
+        LinArgs la{};
+        la.a = x; la.lda = cin; la.wt = wt_t; la.c = d.at(e.y);
+        la.m = nb * P; la.n = N; la.k = cin;
+        la.bias = e.bias == OFF_NONE ? nullptr : d.at(e.bias);
+        la.act = e.act;
+        la.res = e.res == OFF_NONE ? nullptr : d.at(e.res);
+        return add_launch(d.pl, d.idx, [la](hipStream_t s) { return launch_linear_nt(la, s); });
+      }
       GemmArgs g{};
       g.a = x; g.lda = cin; g.a_batch = 0;
       g.b = wt; g.ldb = N; g.b_batch = 0;
@@ -1518,6 +1535,7 @@ void release_plan(qph_plan* pl) {
     (void)hipGraphDestroy(pl->graph);
   }
   if (pl->arena) (void)hipFree(pl->arena);
+  for (float* p : pl->owned) (void)hipFree(p);
   delete pl;
 }
 
