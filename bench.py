@@ -47,8 +47,15 @@ rounds, run until each leg has taken 2 s, 5 s for the headline's det and rec):
     per-kernel-class roofline fractions from per-node event times.
   cfg5: det 1536^2 + 128 rec lines in width buckets (page wall time).
 
+aux: the operators around the nets -- page resize, det input normalisation,
+rec line packing, the DB mask, the SE block's pool and gate, MaxPool,
+bilinear Resize, Transpose -- each at a page-scale shape: device time per
+launch, cache-cold (a captured graph over rotating buffer sets past 512 MB),
+against the HBM roofline.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--cpu-rounds R] [--no-configs] [--node-report FILE]
+                       [--no-plan] [--plan-only] [--aux-only]
 """
 import argparse
 import ctypes
@@ -328,6 +335,139 @@ def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
     return res
 
 
+def aux_specs(torch, lib, ctx):
+    """The operators around the nets, each at a page-scale shape (the mixed
+    page's det size 1536^2 and a 32-line rec batch): (name, workload, kernel,
+    make_set, call, launches per set, algorithmic bytes per set).  make_set()
+    allocates one input / output buffer set, call(s) issues its launches on
+    ctx's stream."""
+    P = ctypes.c_void_p
+    I64 = ctypes.c_int64
+
+    def u8(*shape):
+        return torch.randint(0, 256, shape, dtype=torch.uint8, device="cuda")
+
+    def f32(*shape):
+        return torch.rand(shape, device="cuda")
+
+    def ptr(t):
+        return P(t.data_ptr())
+
+    def nb(*ts):
+        return sum(t.numel() * t.element_size() for t in ts)
+    specs = []
+    # page image -> det input size (resize.rs:153-209)
+    specs.append(("resize_rgb_u8", "u8 RGB 2048x2048 -> 1536x1536 bilinear",
+                  "resize_rgb_u8_kernel", lambda: (u8(2048, 2048, 3), u8(1536, 1536, 3)),
+                  lambda s: lib.qph_resize_bilinear_rgb_u8(ctx, ptr(s[0]), 2048, 2048, ptr(s[1]),
+                                                           1536, 1536), 1, nb))
+    # det input normalisation (engine.rs:959-982)
+    specs.append(("det_normalize_u8", "u8 RGB 1536x1536 -> f32 1x3x1536x1536 ((v/255-0.5)/0.5)",
+                  "det_normalize_kernel", lambda: (u8(1536, 1536, 3), f32(1, 3, 1536, 1536)),
+                  lambda s: lib.qph_det_normalize_u8(ctx, ptr(s[0]), 1536, 1536, ptr(s[1])), 1,
+                  nb))
+
+    # rec line packing (crop.rs:153-190): 32 crops of 40x240 into 3x48x320 slots
+    def crops():
+        return tuple(u8(40, 240, 3) for _ in range(32)) + (f32(32, 3, 48, 320),)
+
+    def pack(s):
+        for i in range(32):
+            r = lib.qph_pack_crop(ctx, ptr(s[i]), 40, 240, 48, 320, 0,
+                                  P(s[32].data_ptr() + i * 3 * 48 * 320 * 4))
+            if r != 0:
+                return r
+        return 0
+    specs.append(("pack_crop", "32 u8 RGB crops 40x240 -> f32 32x3x48x320 (resized to 48x288, "
+                  "zero tail), one launch per line", "pack_crop_kernel", crops, pack, 32, nb))
+    # DB threshold + 2x2 dilation (geometry.rs:287-301, resize.rs:219-247)
+    specs.append(("db_mask", "f32 probability map 1536x1536 -> u8 mask, thresh 0.3, dilated",
+                  "db_mask_kernel", lambda: (f32(1536, 1536), u8(1536, 1536)),
+                  lambda s: lib.qph_db_mask(ctx, ptr(s[0]), 1536, 1536, ctypes.c_float(0.3), 1,
+                                            ptr(s[1])), 1, nb))
+    # SE squeeze and excite (pool2d.rs:10-29, elementwise.rs:134-179)
+    specs.append(("global_avg_pool", "f32 1x256x96x96 -> 1x256 (f64 mean per plane)",
+                  "reduce_mean_kernel", lambda: (f32(1, 256, 96, 96), f32(256)),
+                  lambda s: lib.qph_global_avg_pool(ctx, ptr(s[0]), 1, 256, 96 * 96, ptr(s[1])),
+                  1, nb))
+    specs.append(("mul_add_scale", "f32 1x256x96x96 * gate[256] + residual",
+                  "mul_add_scale_kernel",
+                  lambda: (f32(1, 256, 96, 96), f32(256), f32(1, 256, 96, 96),
+                           f32(1, 256, 96, 96)),
+                  lambda s: lib.qph_mul_add_scale(ctx, ptr(s[0]), ptr(s[1]), ptr(s[2]), 1, 256,
+                                                  96 * 96, ptr(s[3])), 1, nb))
+    # MaxPool (pool2d.rs:94-236)
+    xs_pool = (I64 * 4)(32, 64, 48, 160)
+    ys_pool = (I64 * 4)()
+    specs.append(("pool2d_max", "f32 32x64x48x160 -> 32x64x24x80, max 2x2 stride 2",
+                  "pool2d_kernel", lambda: (f32(32, 64, 48, 160), f32(32, 64, 24, 80)),
+                  lambda s: lib.qph_pool2d(ctx, ptr(s[0]), xs_pool, 2, 2, 2, 2, 0, 0, 0, 0, 1,
+                                           ptr(s[1]), ys_pool), 1, nb))
+    # bilinear Resize (resize.rs:60-142): a det map back to page size
+    specs.append(("resize_bilinear", "f32 1x1x384x384 -> 1536x1536 (half-pixel)",
+                  "resize_bilinear_kernel", lambda: (f32(384, 384), f32(1536, 1536)),
+                  lambda s: lib.qph_resize_bilinear(ctx, ptr(s[0]), 1, 384, 384, 1536, 1536, 0,
+                                                    ptr(s[1])), 1, nb))
+    xs_tr = (I64 * 4)(1, 96, 384, 384)
+    perm = (ctypes.c_int32 * 4)(0, 2, 3, 1)
+    specs.append(("transpose", "f32 1x96x384x384 -> 1x384x384x96 (NCHW -> NHWC)",
+                  "transpose4_kernel", lambda: (f32(1, 96, 384, 384), f32(1, 384, 384, 96)),
+                  lambda s: lib.qph_transpose(ctx, ptr(s[0]), xs_tr, perm, ptr(s[1])), 1, nb))
+    return specs
+
+
+def bench_aux(ops, replays):
+    """Device time per launch of the operators around the nets (aux_specs),
+    cache-cold: R buffer sets (R x set bytes > COLD_BYTES) whose launches are
+    captured once into a graph, replayed `replays` times between HIP events."""
+    import torch
+    lib = ops._lib.load()
+    ctx = ops.new_context(0)
+    st = torch.cuda.Stream()
+    ops.check(lib.qph_ctx_set_stream(ctx, ctypes.c_void_p(st.cuda_stream)))
+    torch.manual_seed(5)
+    out = {}
+    try:
+        for name, workload, kernel, make, call, nl, nbytes in aux_specs(torch, lib, ctx):
+            first = make()
+            set_bytes = nbytes(*first)
+            R = max(2, -(-COLD_BYTES // set_bytes))
+            sets = [first] + [make() for _ in range(R - 1)]
+            torch.cuda.synchronize()
+            with torch.cuda.stream(st):
+                for s in sets:
+                    ops.check(call(s))
+            st.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=st):
+                for s in sets:
+                    ops.check(call(s))
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(st):
+                graph.replay()
+                e0.record(st)
+                for _ in range(replays):
+                    graph.replay()
+                e1.record(st)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (replays * R * nl)
+            by = set_bytes / nl
+            gbs = by / (us * 1e-6) / 1e9
+            out[name] = {"workload": workload, "kernel": kernel, "us": round(us, 3),
+                         "mb": round(by / 1e6, 4), "gbs": round(gbs, 1), "bound": "hbm",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4),
+                         "method": f"cache-cold: HIP events over {replays} replays of a graph "
+                                   f"of {R * nl} launches on {R} rotating buffer sets "
+                                   f"({R * set_bytes >> 20} MB)"}
+            del graph, sets, first
+            torch.cuda.synchronize()
+    finally:
+        ops.check(lib.qph_ctx_set_stream(ctx, None))
+        ops.close_context(ctx)
+    return out
+
+
 def time_mixed_page(steps, warmup):
     """det 1x3x1536x1536 + 128 rec lines (widths {80..1280}, buckets of 160,
     <= 64 lines per batch, fused rec heads), inputs resident.  det and the rec batches run on
@@ -405,6 +545,8 @@ def main():
                     help="run only the plan-model leg and print its figures (profiling)")
     ap.add_argument("--plan-report", default="",
                     help="write the plan-model graphs' dispatch lists (JSON) to this path")
+    ap.add_argument("--aux-only", action="store_true",
+                    help="run only the leg of the operators around the nets (profiling)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a kernel of "
                          "known traffic for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -422,6 +564,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.aux_only:
+        print(json.dumps({"aux": bench_aux(ops, max(3, args.steps // 5))}))
+        return
     ctx = ops.context(0)           # det stream
     ctx_rec = ops.new_context(0)   # rec stream
     lib = ops._lib.load()
@@ -664,6 +809,8 @@ def main():
                       f"({cpu_model()}), -O3 -mavx2 -mfma, FTZ/DAZ",
         }
     result["configs"] = cfgs
+    if not args.no_configs:
+        result["aux"] = bench_aux(ops, max(3, K // 5))
     print(json.dumps(result))
     det.close()
     rec.close()

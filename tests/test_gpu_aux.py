@@ -140,3 +140,42 @@ def test_session_se_block_concat_slots(gpu, oracle):
     assert_bitexact(outs[0], refs[0], "concat tensor")
     assert_bitexact(outs[1], refs[1], "transposed")
     sess.close()
+
+
+def test_aux_ops_graph_replays_match_eager(gpu):
+    """The benchmark's aux leg (bench.aux_specs) captures these C-ABI calls
+    into a graph on a caller's stream: each replay, with eager work and a
+    synchronisation between replays, reproduces the eager output exactly."""
+    torch = gpu
+    import ctypes
+
+    import bench
+    from qppocr_amd import ops
+    lib = ops._lib.load()
+    ctx = ops.new_context(0)
+    st = torch.cuda.Stream()
+    ops.check(lib.qph_ctx_set_stream(ctx, ctypes.c_void_p(st.cuda_stream)))
+    try:
+        torch.manual_seed(7)
+        for name, _, _, make, call, _, _ in bench.aux_specs(torch, lib, ctx):
+            print("aux graph case", name, flush=True)
+            s = make()                       # the last tensor of a set is the output
+            torch.cuda.synchronize()
+            with torch.cuda.stream(st):
+                ops.check(call(s))
+            st.synchronize()
+            want = s[-1].clone()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=st):
+                ops.check(call(s))
+            for rep in range(3):
+                s[-1].fill_(77 if s[-1].dtype == torch.uint8 else float("nan"))
+                torch.cuda.synchronize()
+                with torch.cuda.stream(st):
+                    g.replay()
+                st.synchronize()
+                assert torch.equal(s[-1], want), (name, rep)
+            del g, s, want
+    finally:
+        ops.check(lib.qph_ctx_set_stream(ctx, None))
+        ops.close_context(ctx)
