@@ -4,6 +4,8 @@
 // networks (det input normalisation, rec line packing, the DB threshold and
 // dilation).  All are bandwidth-bound: one thread per output element (or per
 // four), coalesced along the fastest output axis, each output written once.
+#include <algorithm>
+
 #include "qph_internal.h"
 
 namespace qph {
@@ -29,25 +31,53 @@ __global__ __launch_bounds__(256) void mul_add_scale_kernel(const float* __restr
                                                             int64_t gmod, int64_t hw,
                                                             int64_t planes, int64_t ctot,
                                                             int64_t coff) {
-  const int64_t total = planes * hw;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t p = i / hw, e = i - p * hw;
-    const float v = f[i] * gate[p % gmod];
-    out[out_plane(p, c, ctot, coff) * hw + e] = v + r[i];
+  // a workgroup: 1024 elements of a plane (four coalesced passes); planes
+  // by blockIdx.y, so no thread divides its index
+  const int64_t e0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  for (int64_t p = blockIdx.y; p < planes; p += gridDim.y) {
+    const float g = gate[p % gmod];
+    const float* fp = f + p * hw;
+    const float* rp = r + p * hw;
+    float* op = out + out_plane(p, c, ctot, coff) * hw;
+    float fv[4], rv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int64_t e = e0 + u * 256;
+      fv[u] = e < hw ? fp[e] : 0.0f;
+      rv[u] = e < hw ? rp[e] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int64_t e = e0 + u * 256;
+      const float v = fv[u] * g;
+      if (e < hw) op[e] = v + rv[u];
+    }
   }
 }
 
 int launch_mul_add_scale(const float* f, const float* gate, const float* r, float* out, int64_t c,
                          int64_t gmod, int64_t hw, int64_t planes, int64_t ctot, int64_t coff,
                          hipStream_t s) {
-  const int64_t total = planes * hw;
-  if (total <= 0) return QPH_OK;
-  int64_t blocks = (total + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(mul_add_scale_kernel, dim3((unsigned)blocks), dim3(256), 0, s, f, gate, r,
-                     out, c, gmod, hw, planes, ctot, coff);
+  if (planes <= 0 || hw <= 0) return QPH_OK;
+  if (ceil_div(hw, 1024) >= (1ll << 31))
+    return fail(QPH_EUNSUPPORTED, "mul_add_scale: plane too large");
+  hipLaunchKernelGGL(mul_add_scale_kernel,
+                     dim3((unsigned)ceil_div(hw, 1024), (unsigned)std::min<int64_t>(planes, 65535)),
+                     dim3(256), 0, s, f, gate, r, out, c, gmod, hw, planes, ctot, coff);
   return launch_check("mul_add_scale_kernel");
+}
+
+// Division of n < 2^31 by a divisor d >= 1 fixed per launch: with l =
+// ceil(log2 d) and M = ceil(2^(32 + l) / d) (at most 33 bits), floor(n / d)
+// = (n * M) >> (32 + l), since M d - 2^(32 + l) < d keeps the product's
+// excess over n / d below n / 2^(32 + l) < 1 / (2d) (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994).
+static void invariant_divisor(int64_t d, uint64_t* m, int* sh) {
+  int l = 0;
+  while ((1ll << l) < d) l++;
+  const unsigned __int128 num = (unsigned __int128)1 << (32 + l);
+  *m = (uint64_t)((num + (unsigned __int128)(d - 1)) / (unsigned __int128)d);
+  *sh = 32 + l;
 }
 
 // ---------------------------------------------------------------- pool2d
@@ -67,13 +97,19 @@ struct PoolK {
   int64_t c, h, w, oh, ow, kh, kw, sh, sw, ph, pw;
   int64_t ctot, coff;
   int special, max_pool;
+  uint64_t mag;   // oy = (idx * mag) >> shift: idx / ow for idx < oh * ow < 2^31
+  int shift;
 };
 
+// One thread per output of a plane (planes by blockIdx.y); K = the window's
+// side when it is K x K (taps unrolled), 0 for any window.
+template <int K>
 __global__ __launch_bounds__(256) void pool2d_kernel(PoolK p) {
   const int64_t plane = blockIdx.y;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= p.oh * p.ow) return;
-  const int64_t oy = idx / p.ow, ox = idx - oy * p.ow;
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  if (idx >= (uint32_t)(p.oh * p.ow)) return;
+  const uint32_t oyu = (uint32_t)(((uint64_t)idx * p.mag) >> p.shift);
+  const int64_t oy = oyu, ox = idx - oyu * (uint32_t)p.ow;
   const float* xp = p.x + plane * p.h * p.w;
   float v;
   if (p.special) {
@@ -84,18 +120,21 @@ __global__ __launch_bounds__(256) void pool2d_kernel(PoolK p) {
     if (ox + 1 < p.w) b = has_r1 ? fmaxf(r0[ox + 1], r0[ox + 1 + p.w]) : r0[ox + 1];
     v = fmaxf(a, b);
   } else {
+    const int64_t kh = K ? K : p.kh, kw = K ? K : p.kw;
     float acc = p.max_pool ? -3.4e38f : 0.0f;
-    for (int64_t ky = 0; ky < p.kh; ky++) {
+#pragma unroll(K > 0 ? K : 1)
+    for (int64_t ky = 0; ky < kh; ky++) {
       const int64_t iy = oy * p.sh - p.ph + ky;
       if (iy < 0 || iy >= p.h) continue;
-      for (int64_t kx = 0; kx < p.kw; kx++) {
+#pragma unroll(K > 0 ? K : 1)
+      for (int64_t kx = 0; kx < kw; kx++) {
         const int64_t ix = ox * p.sw - p.pw + kx;
         if (ix < 0 || ix >= p.w) continue;
         const float t = xp[iy * p.w + ix];
         acc = p.max_pool ? (t > acc ? t : acc) : acc + t;
       }
     }
-    v = p.max_pool ? acc : acc / (float)(p.kh * p.kw);
+    v = p.max_pool ? acc : acc / (float)(kh * kw);
   }
   p.y[out_plane(plane, p.c, p.ctot, p.coff) * p.oh * p.ow + idx] = v;
 }
@@ -121,8 +160,14 @@ int launch_pool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, in
               peh == 1 && pew == 1 && p.oh == h && p.ow == w;
   if (n * c > 65535 || p.oh * p.ow >= (1ll << 31))
     return fail(QPH_EUNSUPPORTED, "pool2d: grid too large");
-  hipLaunchKernelGGL(pool2d_kernel, dim3(ceil_div(p.oh * p.ow, 256), (unsigned)(n * c)),
-                     dim3(256), 0, s, p);
+  invariant_divisor(p.ow, &p.mag, &p.shift);
+  const dim3 grid((unsigned)ceil_div(p.oh * p.ow, 256), (unsigned)(n * c));
+  if (!p.special && kh == 2 && kw == 2)
+    hipLaunchKernelGGL(pool2d_kernel<2>, grid, dim3(256), 0, s, p);
+  else if (!p.special && kh == 3 && kw == 3)
+    hipLaunchKernelGGL(pool2d_kernel<3>, grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(pool2d_kernel<0>, grid, dim3(256), 0, s, p);
   return launch_check("pool2d_kernel");
 }
 
@@ -158,31 +203,59 @@ struct BilinearK {
   int align;
 };
 
+#define AUX_RY 8   // output rows per thread of the 2-D resize and mask kernels
+
+// A workgroup: 256 output columns x AUX_RY output rows of one plane.  The
+// rows' source coordinates are computed once (into LDS), each thread's
+// column coordinate once for its AUX_RY outputs; row groups by blockIdx.y
+// (strided past 65535 groups), planes by blockIdx.z.
 __global__ __launch_bounds__(256) void resize_bilinear_kernel(BilinearK p) {
-  const int64_t plane = blockIdx.y;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= p.oh * p.ow) return;
-  const int64_t oy = idx / p.ow, ox = idx - oy * p.ow;
-  int64_t y0, y1, x0, x1;
-  float ly, lx;
-  bilinear_coord(oy, p.oh, p.h, p.align, y0, y1, ly);
+  __shared__ int64_t ry0[AUX_RY], ry1[AUX_RY];
+  __shared__ float rly[AUX_RY];
+  const int64_t plane = blockIdx.z;
+  const int64_t ox = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  int64_t x0, x1;
+  float lx;
   bilinear_coord(ox, p.ow, p.w, p.align, x0, x1, lx);
-  const float* r0 = p.x + (plane * p.h + y0) * p.w;
-  const float* r1 = p.x + (plane * p.h + y1) * p.w;
-  float t = r0[x0] * (1.0f - lx) * (1.0f - ly);
-  t = __builtin_fmaf(r0[x1] * lx, 1.0f - ly, t);
-  t = __builtin_fmaf(r1[x0] * (1.0f - lx), ly, t);
-  p.y[out_plane(plane, p.c, p.ctot, p.coff) * p.oh * p.ow + idx] =
-      __builtin_fmaf(r1[x1] * lx, ly, t);
+  const float* xp = p.x + plane * p.h * p.w;
+  float* yp = p.y + out_plane(plane, p.c, p.ctot, p.coff) * p.oh * p.ow;
+  for (int64_t oy0 = (int64_t)blockIdx.y * AUX_RY; oy0 < p.oh;
+       oy0 += (int64_t)gridDim.y * AUX_RY) {
+    __syncthreads();   // the previous group's reads of the row table are done
+    if (threadIdx.x < AUX_RY) {
+      int64_t a, b;
+      float f;
+      bilinear_coord(oy0 + threadIdx.x, p.oh, p.h, p.align, a, b, f);
+      ry0[threadIdx.x] = a;
+      ry1[threadIdx.x] = b;
+      rly[threadIdx.x] = f;
+    }
+    __syncthreads();
+    if (ox < p.ow) {
+      const int nr = (int)std::min<int64_t>(p.oh - oy0, AUX_RY);
+      for (int r = 0; r < nr; r++) {
+        const float ly = rly[r];
+        const float* r0 = xp + ry0[r] * p.w;
+        const float* r1 = xp + ry1[r] * p.w;
+        float t = r0[x0] * (1.0f - lx) * (1.0f - ly);
+        t = __builtin_fmaf(r0[x1] * lx, 1.0f - ly, t);
+        t = __builtin_fmaf(r1[x0] * (1.0f - lx), ly, t);
+        yp[(oy0 + r) * p.ow + ox] = __builtin_fmaf(r1[x1] * lx, ly, t);
+      }
+    }
+  }
 }
 
 int launch_resize_bilinear(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
                            int64_t oh, int64_t ow, int align, float* y, int64_t ctot,
                            int64_t coff, hipStream_t s) {
-  if (n * c > 65535 || oh * ow >= (1ll << 31))
+  if (n * c > 65535 || ceil_div(ow, 256) >= (1ll << 31))
     return fail(QPH_EUNSUPPORTED, "resize_bilinear: grid too large");
   BilinearK p{x, y, c, h, w, oh, ow, ctot, coff, align};
-  hipLaunchKernelGGL(resize_bilinear_kernel, dim3(ceil_div(oh * ow, 256), (unsigned)(n * c)),
+  hipLaunchKernelGGL(resize_bilinear_kernel,
+                     dim3((unsigned)ceil_div(ow, 256),
+                          (unsigned)std::min<int64_t>(ceil_div(oh, AUX_RY), 65535),
+                          (unsigned)(n * c)),
                      dim3(256), 0, s, p);
   return launch_check("resize_bilinear_kernel");
 }
@@ -198,24 +271,111 @@ struct TransposeK {
   int64_t ys[4];
   int64_t xst[4];   // input stride of output dimension d's source dimension
   int64_t total;
+  uint64_t mag[4];  // n / ys[d] = (n * mag[d]) >> sh[d] for n < 2^31 (32-bit form)
+  int sh[4];
 };
 
+template <bool I32>
 __global__ __launch_bounds__(256) void transpose4_kernel(TransposeK p) {
   for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < p.total;
        o += (int64_t)gridDim.x * blockDim.x) {
-    int64_t r = o, src = 0;
+    int64_t src = 0;
+    if constexpr (I32) {
+      uint32_t r = (uint32_t)o;
 #pragma unroll
-    for (int d = 3; d >= 0; d--) {
-      const int64_t i = r % p.ys[d];
-      r /= p.ys[d];
-      src += i * p.xst[d];
+      for (int d = 3; d >= 0; d--) {
+        const uint32_t q = (uint32_t)(((uint64_t)r * p.mag[d]) >> p.sh[d]);
+        src += (int64_t)(r - q * (uint32_t)p.ys[d]) * p.xst[d];
+        r = q;
+      }
+    } else {
+      int64_t r = o;
+#pragma unroll
+      for (int d = 3; d >= 0; d--) {
+        const int64_t i = r % p.ys[d];
+        r /= p.ys[d];
+        src += i * p.xst[d];
+      }
     }
     p.y[o] = p.x[src];
   }
 }
 
+// Tiled form, for a permutation that moves the input's contiguous axis:
+// output axis 3 reads input axis A = perm[3] != 3.  A workgroup copies a
+// 64 (axis A) x 64 (input axis 3) tile at one index of the two other input
+// axes through LDS: its loads run along input axis 3, its stores along
+// output axis 3 (input axis A), both contiguous.  The tile's rows are 65
+// floats apart, so the column reads of the store phase fall on distinct
+// banks.
+struct TransposeTileK {
+  const float* x;
+  float* y;
+  int64_t na, n3;         // sizes of input axes A and 3
+  int64_t ia;             // input stride of axis A
+  int64_t o3;             // output stride of the output axis input axis 3 lands on
+  int64_t nc;             // size of the inner batch axis C
+  int64_t ib, ic, ob, oc; // input / output strides of the batch axes B (outer), C
+  int64_t tiles_a;        // tiles along axis A
+};
+
+__global__ __launch_bounds__(256) void transpose4_tile_kernel(TransposeTileK p) {
+  __shared__ float t[64 * 65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t a0 = (int64_t)(blockIdx.x % p.tiles_a) * 64;
+  const int64_t c0 = (int64_t)(blockIdx.x / p.tiles_a) * 64;
+  const int64_t bb = blockIdx.y / p.nc, bc = blockIdx.y - bb * p.nc;
+  const float* xb = p.x + bb * p.ib + bc * p.ic;
+  float* yb = p.y + bb * p.ob + bc * p.oc;
+#pragma unroll 4
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t a = a0 + r, c = c0 + tx;
+    if (a < p.na && c < p.n3) t[r * 65 + tx] = xb[a * p.ia + c];
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t c = c0 + r, a = a0 + tx;
+    if (a < p.na && c < p.n3) yb[c * p.o3 + a] = t[tx * 65 + r];
+  }
+}
+
 int launch_transpose4(const float* x, const int64_t xs[4], const int32_t perm[4], float* y,
                       hipStream_t s) {
+  if (perm[3] != 3) {
+    // output strides, and the output stride of each input axis
+    int64_t ost[4], o_in[4];
+    ost[3] = 1;
+    for (int d = 2; d >= 0; d--) ost[d] = ost[d + 1] * xs[perm[d + 1]];
+    for (int d = 0; d < 4; d++) o_in[perm[d]] = ost[d];
+    int64_t ist[4];
+    ist[3] = 1;
+    for (int d = 2; d >= 0; d--) ist[d] = ist[d + 1] * xs[d + 1];
+    const int A = perm[3];
+    int bax[2], nb = 0;
+    for (int k = 0; k < 3; k++)
+      if (k != A) bax[nb++] = k;
+    TransposeTileK p{};
+    p.x = x;
+    p.y = y;
+    p.na = xs[A];
+    p.n3 = xs[3];
+    p.ia = ist[A];
+    p.o3 = o_in[3];
+    p.nc = xs[bax[1]];
+    p.ib = ist[bax[0]];
+    p.ic = ist[bax[1]];
+    p.ob = o_in[bax[0]];
+    p.oc = o_in[bax[1]];
+    p.tiles_a = ceil_div(p.na, 64);
+    const int64_t tiles = p.tiles_a * ceil_div(p.n3, 64);
+    const int64_t batch = xs[bax[0]] * xs[bax[1]];
+    if (p.na * p.n3 >= 256 && batch <= 65535 && tiles < (1ll << 31)) {
+      hipLaunchKernelGGL(transpose4_tile_kernel, dim3((unsigned)tiles, (unsigned)batch), dim3(256),
+                         0, s, p);
+      return launch_check("transpose4_tile_kernel");
+    }
+  }
   TransposeK p{};
   p.x = x;
   p.y = y;
@@ -225,12 +385,17 @@ int launch_transpose4(const float* x, const int64_t xs[4], const int32_t perm[4]
   for (int d = 0; d < 4; d++) {
     p.ys[d] = xs[perm[d]];
     p.xst[d] = st[perm[d]];
+    invariant_divisor(p.ys[d], &p.mag[d], &p.sh[d]);
   }
   p.total = xs[0] * xs[1] * xs[2] * xs[3];
   if (p.total <= 0) return QPH_OK;
   int64_t blocks = (p.total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(transpose4_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+  // the 32-bit form: every index and grid-stride step stays below 2^31 + 2^24
+  if (p.total < (1ll << 31))
+    hipLaunchKernelGGL(transpose4_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(transpose4_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, p);
   return launch_check("transpose4_kernel");
 }
 
@@ -267,43 +432,61 @@ int launch_copy_slot(const float* x, float* y, int64_t c, int64_t hw, int64_t pl
 // qppocr-core/src/pipeline/engine.rs:959-982: the det input from u8 RGB
 // (interleaved, h x w x 3) to NCHW f32: v = u8 * (1 / 255) then
 // (v - 0.5) * (1 / 0.5).  A thread takes four consecutive pixels of one row:
-// twelve bytes in (three dwords), four floats out per channel plane.
+// twelve bytes in (three dwords when the rows allow), four floats out per
+// channel plane.  Quads by blockIdx.x, rows by blockIdx.y (strided).
 __global__ __launch_bounds__(256) void det_normalize_kernel(const uint8_t* __restrict__ rgb,
                                                             int64_t h, int64_t w,
-                                                            float* __restrict__ out, int vec4) {
-  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // pixel quad
+                                                            float* __restrict__ out, int vec) {
+  const int64_t qx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t wq = (w + 3) / 4;
-  const int64_t y = q / wq;
-  if (y >= h) return;
-  const int64_t x0 = (q - y * wq) * 4;
+  if (qx >= wq) return;
+  const int64_t x0 = qx * 4;
   const float scale = 1.0f / 255.0f, mean = 0.5f, istd = 1.0f / 0.5f;
-  const uint8_t* src = rgb + (y * w + x0) * 3;
   const int n = (int)(w - x0 < 4 ? w - x0 : 4);
-  float v[3][4];
+  for (int64_t y = blockIdx.y; y < h; y += gridDim.y) {
+    const uint8_t* src = rgb + (y * w + x0) * 3;
+    uint8_t b[12];
+    if (vec) {   // w % 4 == 0: the quad's twelve bytes start 4-byte aligned
+      const uint32_t* s32 = (const uint32_t*)src;
 #pragma unroll
-  for (int k = 0; k < 4; k++)
+      for (int q = 0; q < 3; q++) {
+        const uint32_t t = s32[q];
+#pragma unroll
+        for (int k = 0; k < 4; k++) b[4 * q + k] = (uint8_t)(t >> (8 * k));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 12; i++) b[i] = i < 3 * n ? src[i] : 0;
+    }
+    float v[3][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int c = 0; c < 3; c++) {
+        const float u = k < n ? (float)b[k * 3 + c] : 0.0f;
+        v[c][k] = (u * scale - mean) * istd;
+      }
 #pragma unroll
     for (int c = 0; c < 3; c++) {
-      const float u = k < n ? (float)src[k * 3 + c] : 0.0f;
-      v[c][k] = (u * scale - mean) * istd;
-    }
-#pragma unroll
-  for (int c = 0; c < 3; c++) {
-    float* d = out + (c * h + y) * w + x0;
-    if (n == 4 && vec4) {
-      *(float4*)d = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
-    } else {
-      for (int k = 0; k < n; k++) d[k] = v[c][k];
+      float* d = out + (c * h + y) * w + x0;
+      if (vec) {
+        *(float4*)d = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+      } else {
+        for (int k = 0; k < n; k++) d[k] = v[c][k];
+      }
     }
   }
 }
 
 int launch_det_normalize(const uint8_t* rgb, int64_t h, int64_t w, float* out, hipStream_t s) {
-  const int64_t quads = h * ((w + 3) / 4);
-  if (quads >= (1ll << 40)) return fail(QPH_EUNSUPPORTED, "det_normalize: image too large");
-  const int vec4 = (w & 3) == 0 && (uintptr_t)out % 16 == 0;   // 16-byte aligned rows
-  hipLaunchKernelGGL(det_normalize_kernel, dim3(ceil_div(quads, 256)), dim3(256), 0, s, rgb, h, w,
-                     out, vec4);
+  const int64_t wq = (w + 3) / 4;
+  if (ceil_div(wq, 256) >= (1ll << 31))
+    return fail(QPH_EUNSUPPORTED, "det_normalize: image too wide");
+  // whole quads, 16-byte aligned output rows, 4-byte aligned input quads
+  const int vec = (w & 3) == 0 && (uintptr_t)out % 16 == 0 && (uintptr_t)rgb % 4 == 0;
+  hipLaunchKernelGGL(det_normalize_kernel,
+                     dim3((unsigned)ceil_div(wq, 256), (unsigned)std::min<int64_t>(h, 65535)),
+                     dim3(256), 0, s, rgb, h, w, out, vec);
   return launch_check("det_normalize_kernel");
 }
 
@@ -341,24 +524,35 @@ struct RgbResizeK {
   float sx, sy;
 };
 
+// One thread per output pixel: columns by blockIdx.x, rows by blockIdx.y
+// (strided past 65535 rows), so no thread divides its index.  (With one
+// column of several rows a thread, its 12 byte gathers a pixel leave too few
+// waves in flight.)
 __global__ __launch_bounds__(256) void resize_rgb_u8_kernel(RgbResizeK p, uint8_t* __restrict__ dst) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= p.dw * p.dh) return;
-  const int64_t y = idx / p.dw, x = idx - y * p.dw;
-  int64_t j0, j1, x0, x1;
-  float fy, lx;
-  u8_axis(y, p.sy, p.sh, j0, j1, fy);
+  const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (x >= p.dw) return;
+  int64_t x0, x1;
+  float lx;
   u8_axis(x, p.sx, p.sw, x0, x1, lx);
-  const uint8_t* r0 = p.src + j0 * p.sw * 3;
-  const uint8_t* r1 = p.src + j1 * p.sw * 3;
+  for (int64_t y = blockIdx.y; y < p.dh; y += gridDim.y) {
+    int64_t j0, j1;
+    float fy;
+    u8_axis(y, p.sy, p.sh, j0, j1, fy);
+    const uint8_t* r0 = p.src + j0 * p.sw * 3;
+    const uint8_t* r1 = p.src + j1 * p.sw * 3;
+    uint8_t* d = dst + (y * p.dw + x) * 3;
 #pragma unroll
-  for (int ch = 0; ch < 3; ch++) dst[idx * 3 + ch] = u8_sample(r0, r1, x0 * 3, x1 * 3, lx, fy, ch);
+    for (int ch = 0; ch < 3; ch++) d[ch] = u8_sample(r0, r1, x0 * 3, x1 * 3, lx, fy, ch);
+  }
 }
 
 int launch_resize_rgb_u8(const uint8_t* src, int64_t sw, int64_t sh, uint8_t* dst, int64_t dw,
                          int64_t dh, hipStream_t s) {
+  if (ceil_div(dw, 256) >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "resize_rgb_u8: too wide");
   RgbResizeK p{src, sw, sh, dw, dh, (float)sw / (float)dw, (float)sh / (float)dh};
-  hipLaunchKernelGGL(resize_rgb_u8_kernel, dim3(ceil_div(dw * dh, 256)), dim3(256), 0, s, p, dst);
+  hipLaunchKernelGGL(resize_rgb_u8_kernel,
+                     dim3((unsigned)ceil_div(dw, 256), (unsigned)std::min<int64_t>(dh, 65535)),
+                     dim3(256), 0, s, p, dst);
   return launch_check("resize_rgb_u8_kernel");
 }
 
@@ -438,27 +632,39 @@ int launch_pack_crop(const uint8_t* crop, int64_t ch, int64_t cw, int64_t img_h,
 // (qppocr-kernels/src/resize.rs:219-247): mask = pred > thresh; with
 // dilation out[y][x] = max of the in-range masks of rows y - 1, y and
 // columns x - 1, x.  One pass: each thread thresholds its own window.
+// A thread: one column of AUX_RY rows (row groups by blockIdx.y, strided),
+// carrying the masks of the row above (columns x - 1 and x) down the column.
 __global__ __launch_bounds__(256) void db_mask_kernel(const float* __restrict__ pred, int64_t h,
                                                       int64_t w, float thresh, int dilate,
                                                       uint8_t* __restrict__ out) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= h * w) return;
-  const int64_t y = idx / w, x = idx - y * w;
-  uint8_t v = pred[idx] > thresh ? 1 : 0;
-  if (dilate) {
-    if (x > 0 && pred[idx - 1] > thresh) v = 1;
-    if (y > 0) {
-      if (pred[idx - w] > thresh) v = 1;
-      if (x > 0 && pred[idx - w - 1] > thresh) v = 1;
+  const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (x >= w) return;
+  for (int64_t y0 = (int64_t)blockIdx.y * AUX_RY; y0 < h; y0 += (int64_t)gridDim.y * AUX_RY) {
+    bool up = false, upl = false;   // masks at (y - 1, x) and (y - 1, x - 1)
+    if (dilate && y0 > 0) {
+      const float* pr = pred + (y0 - 1) * w;
+      up = pr[x] > thresh;
+      upl = x > 0 && pr[x - 1] > thresh;
+    }
+    const int nr = (int)std::min<int64_t>(h - y0, AUX_RY);
+    for (int r = 0; r < nr; r++) {
+      const float* pr = pred + (y0 + r) * w;
+      const bool m = pr[x] > thresh;
+      const bool ml = dilate && x > 0 && pr[x - 1] > thresh;
+      out[(y0 + r) * w + x] = (m || (dilate && (ml || up || upl))) ? 1 : 0;
+      up = m;
+      upl = ml;
     }
   }
-  out[idx] = v;
 }
 
 int launch_db_mask(const float* pred, int64_t h, int64_t w, float thresh, int dilate,
                    uint8_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(db_mask_kernel, dim3(ceil_div(h * w, 256)), dim3(256), 0, s, pred, h, w,
-                     thresh, dilate, out);
+  if (ceil_div(w, 256) >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "db_mask: map too wide");
+  hipLaunchKernelGGL(db_mask_kernel,
+                     dim3((unsigned)ceil_div(w, 256),
+                          (unsigned)std::min<int64_t>(ceil_div(h, AUX_RY), 65535)),
+                     dim3(256), 0, s, pred, h, w, thresh, dilate, out);
   return launch_check("db_mask_kernel");
 }
 

@@ -67,12 +67,10 @@ __device__ __forceinline__ int term_exp(float v) {
 //    tree +- D), the sequential sum rounds to it as well.
 // False for Inf / NaN and for the rare rows that meet neither test, which
 // then take the sequential sum.
-__device__ __forceinline__ bool f64_mean_order_free(double s, double a, int emin, int64_t n,
-                                                    float* mean) {
-  s = wave_sum_f64(s);
-  a = wave_sum_f64(a);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) emin = min(emin, __shfl_xor(emin, off, 64));
+// f64_mean_check is the test on a row's totals (however they were summed);
+// f64_mean_order_free first sums the wave's lane partials.
+__device__ __forceinline__ bool f64_mean_check(double s, double a, int emin, int64_t n,
+                                               float* mean) {
   if (emin == 255 || a * (1.0 + 0x1p-40) < __builtin_ldexp(1.0, emin - 127 - 23 + 53)) {
     *mean = (float)(s / (double)n);
     return __builtin_isfinite(*mean);
@@ -82,6 +80,15 @@ __device__ __forceinline__ bool f64_mean_order_free(double s, double a, int emin
   const float lo = (float)((s - d) / (double)n), hi = (float)((s + d) / (double)n);
   *mean = lo;
   return __float_as_uint(lo) == __float_as_uint(hi) && __builtin_isfinite(lo);
+}
+
+__device__ __forceinline__ bool f64_mean_order_free(double s, double a, int emin, int64_t n,
+                                                    float* mean) {
+  s = wave_sum_f64(s);
+  a = wave_sum_f64(a);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) emin = min(emin, __shfl_xor(emin, off, 64));
+  return f64_mean_check(s, a, emin, n, mean);
 }
 
 template <int V>
@@ -1473,12 +1480,99 @@ __global__ __launch_bounds__(256) void reduce_mean_kernel(MeanRows p) {
   if (p.ostride == 4 && lane >= 1 && lane <= 3) p.out[row * 4 + lane] = 0.0f;
 }
 
+// Long rows (a global average pool's planes): one 256-thread workgroup per
+// row, every load of a pass issued before its terms are summed (16-byte
+// loads when the row is contiguous and aligned).  The lane partials meet
+// through LDS and f64_mean_check runs on the row's totals: it holds for any
+// summation order, and a row that fails it takes the same sequential sum as
+// above, on wave 0.
+template <bool VEC>
+__global__ __launch_bounds__(256) void reduce_mean_wg_kernel(MeanRows p) {
+  __shared__ double ls[4], la[4];
+  __shared__ int le[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t cols = p.cols, es = p.estride;
+  const float* xr = p.x + (row / p.rpg) * p.gstride + (row % p.rpg) * p.rstride;
+  double s = 0.0, sa = 0.0;
+  int emin = 255;
+  // padding terms are 0.0f: they add 0 and their term_exp (255) is no minimum
+  auto term = [&](float v) {
+    const double t = f64_daz(v);
+    s += t;
+    sa += __builtin_fabs(t);
+    emin = min(emin, term_exp(v));
+  };
+  if constexpr (VEC) {
+    const int64_t nq = cols >> 2;
+    const f32x4* xq = (const f32x4*)xr;
+    for (int64_t q0 = 0; q0 < nq; q0 += 256 * 8) {
+      f32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int64_t q = q0 + u * 256 + tid;
+        v[u] = q < nq ? xq[q] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) term(v[u][c]);
+    }
+    for (int64_t j = (nq << 2) + tid; j < cols; j += 256) term(xr[j]);
+  } else {
+    for (int64_t j0 = 0; j0 < cols; j0 += 256 * 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int64_t j = j0 + u * 256 + tid;
+        v[u] = j < cols ? xr[j * es] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) term(v[u]);
+    }
+  }
+  s = wave_sum_f64(s);
+  sa = wave_sum_f64(sa);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) emin = min(emin, __shfl_xor(emin, off, 64));
+  if (lane == 0) {
+    ls[wave] = s;
+    la[wave] = sa;
+    le[wave] = emin;
+  }
+  __syncthreads();
+  s = ((ls[0] + ls[1]) + ls[2]) + ls[3];
+  sa = ((la[0] + la[1]) + la[2]) + la[3];
+  emin = min(min(le[0], le[1]), min(le[2], le[3]));
+  float mean;
+  if (!f64_mean_check(s, sa, emin, cols, &mean)) {   // the same outcome in every thread
+    if (wave != 0) return;
+    s = 0.0;
+    for (int64_t j0 = 0; j0 < cols; j0 += 64) {
+      const float v = j0 + lane < cols ? xr[(j0 + lane) * es] : 0.0f;
+      s = seq_sum_lanes(s, v, (int)min<int64_t>(64, cols - j0));
+    }
+    mean = (float)(s / (double)cols);
+  }
+  if (tid == 0) p.out[row * p.ostride] = mean;
+  if (p.ostride == 4 && tid >= 1 && tid <= 3) p.out[row * 4 + tid] = 0.0f;
+}
+
 int launch_reduce_mean_rows(const float* x, int64_t rows, int64_t cols, int64_t rpg,
                             int64_t gstride, int64_t rstride, int64_t estride, float* out,
                             int64_t ostride, hipStream_t s) {
   if (rows >= (1ll << 33)) return fail(QPH_EUNSUPPORTED, "reduce_mean: too many rows");
   if (rows <= 0 || cols <= 0 || rpg <= 0) return fail(QPH_EINVAL, "reduce_mean: empty rows");
   MeanRows p{x, rows, cols, rpg, gstride, rstride, estride, out, ostride};
+  if (cols >= 1024 && rows < (1ll << 31)) {
+    const bool vec = estride == 1 && (uintptr_t)x % 16 == 0 && gstride % 4 == 0 &&
+                     rstride % 4 == 0;
+    if (vec)
+      hipLaunchKernelGGL(reduce_mean_wg_kernel<true>, dim3((unsigned)rows), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(reduce_mean_wg_kernel<false>, dim3((unsigned)rows), dim3(256), 0, s, p);
+    return launch_check("reduce_mean_wg_kernel");
+  }
   hipLaunchKernelGGL(reduce_mean_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, p);
   return launch_check("reduce_mean_kernel");
 }

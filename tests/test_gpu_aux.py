@@ -68,6 +68,22 @@ def test_resize_bilinear_and_transpose(gpu, oracle, align):
                         f"transpose {perm}")
 
 
+def test_transpose_every_permutation(gpu):
+    """All 24 rank-4 permutations on shapes with ragged 64-tiles: the tiled
+    path (input axis 3 moved) and the element path, against numpy's
+    transpose (a copy, so equality is exact)."""
+    import itertools
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(53)
+    for shape in [(3, 70, 5, 130), (1, 96, 40, 72), (2, 1, 65, 1)]:
+        x = rng.standard_normal(shape).astype(np.float32)
+        gx = _t(torch, x)
+        for perm in itertools.permutations(range(4)):
+            got = _n(ops.transpose(gx, perm))
+            assert np.array_equal(got, np.transpose(x, perm)), (shape, perm)
+
+
 def test_det_normalize_resize_u8_pack_crop(gpu, oracle):
     torch = gpu
     from qppocr_amd import ops
@@ -140,6 +156,29 @@ def test_session_se_block_concat_slots(gpu, oracle):
     assert_bitexact(outs[0], refs[0], "concat tensor")
     assert_bitexact(outs[1], refs[1], "transposed")
     sess.close()
+
+
+def test_mean_of_long_rows(gpu, oracle):
+    """Rows of 1024 terms and more take one workgroup per row: 16-byte loads
+    (GAP planes of 96x96, rows of 4096) or scalar ones (rows of 1027, not
+    16-byte aligned), with rows whose tree sum could round differently
+    (2^60 cancellations, a 2^30 magnitude span, a 3e38 term, denormals) and
+    so take the sequential sum."""
+    torch = gpu
+    from qppocr_amd import ops
+    rng = np.random.default_rng(52)
+    x = rng.standard_normal((2, 6, 96, 96)).astype(np.float32)
+    x[0, 1, 0, :2] = 2.0 ** 60, -(2.0 ** 60)
+    x[0, 2] *= np.exp2(rng.integers(-15, 15, (96, 96))).astype(np.float32)
+    x[1, 3, 5, 7] = 3.0e38
+    x[1, 4, :3, :5] = np.float32(1e-40)
+    assert_bitexact(_n(ops.global_avg_pool(_t(torch, x))), oracle.global_avg_pool(x), "GAP 96^2")
+    for rows, cols in [(5, 1027), (3, 4096), (2, 1024)]:
+        y = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+        y[0, 0], y[0, 1] = 2.0 ** 60, -(2.0 ** 60)    # sequential: cancel, the rest survive
+        got = _n(ops.reduce_mean_last(_t(torch, y)))
+        assert_bitexact(got, oracle.reduce_mean_last(y), f"mean {rows}x{cols}")
+        assert got[0] != 0.0
 
 
 def test_aux_ops_graph_replays_match_eager(gpu):
