@@ -387,7 +387,7 @@ def aux_specs(torch, lib, ctx):
                                             ptr(s[1])), 1, nb))
     # SE squeeze and excite (pool2d.rs:10-29, elementwise.rs:134-179)
     specs.append(("global_avg_pool", "f32 1x256x96x96 -> 1x256 (f64 mean per plane)",
-                  "reduce_mean_kernel", lambda: (f32(1, 256, 96, 96), f32(256)),
+                  "reduce_mean_wg_kernel<true>", lambda: (f32(1, 256, 96, 96), f32(256)),
                   lambda s: lib.qph_global_avg_pool(ctx, ptr(s[0]), 1, 256, 96 * 96, ptr(s[1])),
                   1, nb))
     specs.append(("mul_add_scale", "f32 1x256x96x96 * gate[256] + residual",
@@ -400,7 +400,7 @@ def aux_specs(torch, lib, ctx):
     xs_pool = (I64 * 4)(32, 64, 48, 160)
     ys_pool = (I64 * 4)()
     specs.append(("pool2d_max", "f32 32x64x48x160 -> 32x64x24x80, max 2x2 stride 2",
-                  "pool2d_kernel", lambda: (f32(32, 64, 48, 160), f32(32, 64, 24, 80)),
+                  "pool2d_kernel<2>", lambda: (f32(32, 64, 48, 160), f32(32, 64, 24, 80)),
                   lambda s: lib.qph_pool2d(ctx, ptr(s[0]), xs_pool, 2, 2, 2, 2, 0, 0, 0, 0, 1,
                                            ptr(s[1]), ys_pool), 1, nb))
     # bilinear Resize (resize.rs:60-142): a det map back to page size
@@ -411,7 +411,7 @@ def aux_specs(torch, lib, ctx):
     xs_tr = (I64 * 4)(1, 96, 384, 384)
     perm = (ctypes.c_int32 * 4)(0, 2, 3, 1)
     specs.append(("transpose", "f32 1x96x384x384 -> 1x384x384x96 (NCHW -> NHWC)",
-                  "transpose4_kernel", lambda: (f32(1, 96, 384, 384), f32(1, 384, 384, 96)),
+                  "transpose4_tile_kernel", lambda: (f32(1, 96, 384, 384), f32(1, 384, 384, 96)),
                   lambda s: lib.qph_transpose(ctx, ptr(s[0]), xs_tr, perm, ptr(s[1])), 1, nb))
     return specs
 
