@@ -380,6 +380,19 @@ def aux_specs(torch, lib, ctx):
         return 0
     specs.append(("pack_crop", "32 u8 RGB crops 40x240 -> f32 32x3x48x320 (resized to 48x288, "
                   "zero tail), one launch per line", "pack_crop_kernel", crops, pack, 32, nb))
+    ptrs = {}
+
+    def pack_batch(s):
+        # the descriptor arrays of a set, built once (host memory, read at launch)
+        key = s[32].data_ptr()
+        if key not in ptrs:
+            ptrs[key] = ((ctypes.c_void_p * 32)(*[t.data_ptr() for t in s[:32]]),
+                         (I64 * 32)(*([40] * 32)), (I64 * 32)(*([240] * 32)),
+                         (ctypes.c_int32 * 32)())
+        cp, ch, cw, po = ptrs[key]
+        return lib.qph_pack_crops(ctx, 32, cp, ch, cw, po, 48, 320, ptr(s[32]))
+    specs.append(("pack_crops", "the same 32 lines in one launch (the batch entry point)",
+                  "pack_crops_kernel", crops, pack_batch, 1, nb))
     # DB threshold + 2x2 dilation (geometry.rs:287-301, resize.rs:219-247)
     specs.append(("db_mask", "f32 probability map 1536x1536 -> u8 mask, thresh 0.3, dilated",
                   "db_mask_kernel", lambda: (f32(1536, 1536), u8(1536, 1536)),

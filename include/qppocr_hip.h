@@ -276,6 +276,15 @@ QPH_API int qph_resize_bilinear_rgb_u8(qph_ctx* ctx, const uint8_t* src, int64_t
  * size when pad_only), (u8 / 255 - 0.5) / 0.5; the rest of the slot is 0. */
 QPH_API int qph_pack_crop(qph_ctx* ctx, const uint8_t* crop, int64_t ch, int64_t cw,
                           int64_t img_h, int64_t img_w, int32_t pad_only, float* dst);
+/* A whole rec batch: crops[i] (device u8 RGB [ch[i], cw[i], 3]) into slot i
+ * of dst [n, 3, img_h, img_w] exactly as qph_pack_crop with pad_only[i]; one
+ * launch per 64 lines, the line descriptors in the kernel arguments.  The
+ * arrays are host memory, the crops and dst device memory.  Replaces the
+ * per-line pack loop that fills a rec batch
+ * (qppocr-core/src/pipeline/engine.rs:1413-1431). */
+QPH_API int qph_pack_crops(qph_ctx* ctx, int32_t n, const uint8_t* const* crops,
+                           const int64_t* ch, const int64_t* cw, const int32_t* pad_only,
+                           int64_t img_h, int64_t img_w, float* dst);
 /* DB post front end (geometry.rs:287-301, resize.rs:219-247): mask =
  * pred > thresh (u8 0/1), then (dilate != 0) the 2x2 dilation with anchor
  * (1, 1), out-of-range samples ignored. */

@@ -98,6 +98,7 @@ SIGNATURES = {
     "qph_det_normalize_u8": ([P, P, I64, I64, P], ctypes.c_int),
     "qph_resize_bilinear_rgb_u8": ([P, P, I64, I64, P, I64, I64], ctypes.c_int),
     "qph_pack_crop": ([P, P, I64, I64, I64, I64, I32, P], ctypes.c_int),
+    "qph_pack_crops": ([P, I32, P, P, P, P, I64, I64, P], ctypes.c_int),
     "qph_db_mask": ([P, P, I64, I64, F32, I32, P], ctypes.c_int),
     "qph_conv2d_noalloc": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act), P,
                             P, P], ctypes.c_int),

@@ -574,29 +574,29 @@ struct PackCropK {
   int pad_only;
 };
 
-__global__ __launch_bounds__(256) void pack_crop_kernel(PackCropK p) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= p.img_h * p.img_w) return;
-  const int64_t y = idx / p.img_w, x = idx - y * p.img_w;
-  const int64_t plane = p.img_h * p.img_w;
-  float v[3] = {0.0f, 0.0f, 0.0f};
+// The value of slot pixel (y, x) for one crop, channels in v (0 outside the
+// crop's placed / resized area).
+__device__ __forceinline__ void pack_pixel(const uint8_t* crop, int64_t ch, int64_t cw, int64_t rw,
+                                           int64_t y0, float sx, float sy, int pad_only,
+                                           int64_t y, int64_t x, float v[3]) {
+  v[0] = v[1] = v[2] = 0.0f;
   bool in = false;
   uint8_t u[3];
-  if (p.pad_only) {
-    const int64_t cy = y - p.y0;
-    if (cy >= 0 && cy < p.ch && x < p.cw) {
+  if (pad_only) {
+    const int64_t cy = y - y0;
+    if (cy >= 0 && cy < ch && x < cw) {
       in = true;
 #pragma unroll
-      for (int c = 0; c < 3; c++) u[c] = p.crop[(cy * p.cw + x) * 3 + c];
+      for (int c = 0; c < 3; c++) u[c] = crop[(cy * cw + x) * 3 + c];
     }
-  } else if (x < p.rw) {
+  } else if (x < rw) {
     in = true;
     int64_t j0, j1, x0, x1;
     float fy, lx;
-    u8_axis(y, p.sy, p.ch, j0, j1, fy);
-    u8_axis(x, p.sx, p.cw, x0, x1, lx);
-    const uint8_t* r0 = p.crop + j0 * p.cw * 3;
-    const uint8_t* r1 = p.crop + j1 * p.cw * 3;
+    u8_axis(y, sy, ch, j0, j1, fy);
+    u8_axis(x, sx, cw, x0, x1, lx);
+    const uint8_t* r0 = crop + j0 * cw * 3;
+    const uint8_t* r1 = crop + j1 * cw * 3;
 #pragma unroll
     for (int c = 0; c < 3; c++) u[c] = u8_sample(r0, r1, x0 * 3, x1 * 3, lx, fy, c);
   }
@@ -604,8 +604,95 @@ __global__ __launch_bounds__(256) void pack_crop_kernel(PackCropK p) {
 #pragma unroll
     for (int c = 0; c < 3; c++) v[c] = ((float)u[c] / 255.0f - 0.5f) / 0.5f;
   }
+}
+
+__global__ __launch_bounds__(256) void pack_crop_kernel(PackCropK p) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= p.img_h * p.img_w) return;
+  const int64_t y = idx / p.img_w, x = idx - y * p.img_w;
+  const int64_t plane = p.img_h * p.img_w;
+  float v[3];
+  pack_pixel(p.crop, p.ch, p.cw, p.rw, p.y0, p.sx, p.sy, p.pad_only, y, x, v);
 #pragma unroll
   for (int c = 0; c < 3; c++) p.dst[c * plane + idx] = v[c];
+}
+
+// A whole rec batch in one launch: up to PACK_LINES crops, their descriptors
+// in the kernel arguments; line blockIdx.y fills slot blockIdx.y.
+#define PACK_LINES 64
+struct PackLine {
+  const uint8_t* crop;
+  int32_t ch, cw, rw, y0;
+  float sx, sy;
+  int32_t pad_only, pad;
+};
+struct PackCropsK {
+  float* dst;
+  int64_t img_h, img_w;
+  uint64_t mag;   // idx / img_w = (idx * mag) >> shift (slot size < 2^31)
+  int32_t shift;
+  PackLine line[PACK_LINES];
+};
+
+__global__ __launch_bounds__(256) void pack_crops_kernel(PackCropsK p) {
+  const PackLine& L = p.line[blockIdx.y];
+  const int64_t plane = p.img_h * p.img_w;
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  if (idx >= (uint32_t)plane) return;
+  const int64_t y = (int64_t)(((uint64_t)idx * p.mag) >> p.shift), x = idx - y * p.img_w;
+  float v[3];
+  pack_pixel(L.crop, L.ch, L.cw, L.rw, L.y0, L.sx, L.sy, L.pad_only, y, x, v);
+  float* d = p.dst + (int64_t)blockIdx.y * 3 * plane;
+#pragma unroll
+  for (int c = 0; c < 3; c++) d[c * plane + idx] = v[c];
+}
+
+// The resized width and the axis scales of one crop (crop.rs:153-190).
+static void pack_geometry(int64_t ch, int64_t cw, int64_t img_h, int64_t img_w, int pad_only,
+                          int64_t* rw, int64_t* y0, float* sx, float* sy) {
+  *y0 = (img_h - ch) / 2;
+  *rw = 0;
+  *sx = *sy = 0.0f;
+  if (!pad_only) {
+    const float ratio = (float)cw / (float)ch;
+    int64_t r = (int64_t)__builtin_ceilf((float)img_h * ratio);
+    r = r > img_w ? img_w : r;
+    *rw = r < 1 ? 1 : r;
+    *sx = (float)cw / (float)*rw;
+    *sy = (float)ch / (float)img_h;
+  }
+}
+
+int launch_pack_crops(int n, const uint8_t* const* crops, const int64_t* ch, const int64_t* cw,
+                      const int32_t* pad_only, int64_t img_h, int64_t img_w, float* dst,
+                      hipStream_t s) {
+  if (img_h * img_w >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "pack_crops: slot too large");
+  for (int i = 0; i < n; i++)
+    if (ch[i] >= (1ll << 31) || cw[i] >= (1ll << 31))
+      return fail(QPH_EUNSUPPORTED, "pack_crops: crop too large");
+  PackCropsK p{};
+  p.img_h = img_h;
+  p.img_w = img_w;
+  invariant_divisor(img_w, &p.mag, &p.shift);
+  for (int b = 0; b < n; b += PACK_LINES) {
+    const int m = std::min(PACK_LINES, n - b);
+    p.dst = dst + (int64_t)b * 3 * img_h * img_w;
+    for (int i = 0; i < m; i++) {
+      PackLine& L = p.line[i];
+      int64_t rw, y0;
+      pack_geometry(ch[b + i], cw[b + i], img_h, img_w, pad_only[b + i], &rw, &y0, &L.sx, &L.sy);
+      L.crop = crops[b + i];
+      L.ch = (int32_t)ch[b + i];
+      L.cw = (int32_t)cw[b + i];
+      L.rw = (int32_t)rw;
+      L.y0 = (int32_t)y0;
+      L.pad_only = pad_only[b + i] != 0;
+    }
+    hipLaunchKernelGGL(pack_crops_kernel, dim3((unsigned)ceil_div(img_h * img_w, 256), (unsigned)m),
+                       dim3(256), 0, s, p);
+    QPH_TRY(launch_check("pack_crops_kernel"));
+  }
+  return QPH_OK;
 }
 
 int launch_pack_crop(const uint8_t* crop, int64_t ch, int64_t cw, int64_t img_h, int64_t img_w,
@@ -613,15 +700,7 @@ int launch_pack_crop(const uint8_t* crop, int64_t ch, int64_t cw, int64_t img_h,
   PackCropK p{};
   p.crop = crop; p.dst = dst; p.ch = ch; p.cw = cw; p.img_h = img_h; p.img_w = img_w;
   p.pad_only = pad_only;
-  p.y0 = (img_h - ch) / 2;
-  if (!pad_only) {
-    const float ratio = (float)cw / (float)ch;
-    int64_t rw = (int64_t)__builtin_ceilf((float)img_h * ratio);
-    rw = rw > img_w ? img_w : rw;
-    p.rw = rw < 1 ? 1 : rw;
-    p.sx = (float)cw / (float)p.rw;
-    p.sy = (float)ch / (float)img_h;
-  }
+  pack_geometry(ch, cw, img_h, img_w, pad_only, &p.rw, &p.y0, &p.sx, &p.sy);
   hipLaunchKernelGGL(pack_crop_kernel, dim3(ceil_div(img_h * img_w, 256)), dim3(256), 0, s, p);
   return launch_check("pack_crop_kernel");
 }
@@ -757,6 +836,22 @@ QPH_API int qph_pack_crop(qph_ctx* ctx, const uint8_t* crop, int64_t ch, int64_t
     return fail(QPH_EINVAL, "pack_crop: bad argument");
   if (pad_only && ch > img_h) return fail(QPH_EINVAL, "pack_crop: pad_only crop taller than img_h");
   return launch_pack_crop(crop, ch, cw, img_h, img_w, dst, pad_only != 0, ctx->stream);
+}
+
+QPH_API int qph_pack_crops(qph_ctx* ctx, int32_t n, const uint8_t* const* crops,
+                           const int64_t* ch, const int64_t* cw, const int32_t* pad_only,
+                           int64_t img_h, int64_t img_w, float* dst) {
+  CTX_CHECK(ctx);
+  if (n <= 0 || !crops || !ch || !cw || !pad_only || img_h <= 0 || img_w <= 0 || !dst)
+    return fail(QPH_EINVAL, "pack_crops: bad argument");
+  for (int32_t i = 0; i < n; i++) {
+    if (!crops[i] || ch[i] <= 0 || cw[i] <= 0)
+      return fail(QPH_EINVAL, "pack_crops: bad crop " + std::to_string(i));
+    if (pad_only[i] && ch[i] > img_h)
+      return fail(QPH_EINVAL, "pack_crops: pad_only crop " + std::to_string(i) +
+                                  " taller than img_h");
+  }
+  return launch_pack_crops(n, crops, ch, cw, pad_only, img_h, img_w, dst, ctx->stream);
 }
 
 QPH_API int qph_db_mask(qph_ctx* ctx, const float* pred, int64_t h, int64_t w, float thresh,

@@ -403,6 +403,27 @@ def pack_crop(crop, img_h, img_w, pad_only=False, out=None):
     return out
 
 
+def pack_crops(crops, img_h, img_w, pad_only=None, out=None):
+    """A rec batch in one launch per 64 lines (engine.rs:1413-1431 packs it
+    line by line): u8 crops [ch, cw, 3] -> f32 [n, 3, img_h, img_w], line i
+    as pack_crop(crops[i], img_h, img_w, pad_only[i])."""
+    n = len(crops)
+    for c in crops:
+        if c.dtype != torch.uint8 or c.dim() != 3 or c.shape[2] != 3:
+            raise ValueError("pack_crops takes u8 [ch, cw, 3] crops")
+    if pad_only is None:
+        pad_only = [False] * n
+    if out is None:
+        out = torch.empty((n, 3, img_h, img_w), device=crops[0].device)
+    ptrs = (ctypes.c_void_p * n)(*[_ptr_any(c).value for c in crops])
+    ch = (_lib.I64 * n)(*[c.shape[0] for c in crops])
+    cw = (_lib.I64 * n)(*[c.shape[1] for c in crops])
+    po = (_lib.I32 * n)(*[int(bool(p)) for p in pad_only])
+    with _Call(_dev(crops[0])) as ctx:
+        check(_lib.load().qph_pack_crops(ctx, n, ptrs, ch, cw, po, img_h, img_w, _ptr(out)))
+    return out
+
+
 def db_mask(pred, thresh, dilate=True):
     """DB threshold + 2x2 dilation (geometry.rs:287-301, resize.rs:219-247)."""
     h, w = pred.shape[-2:]

@@ -105,6 +105,31 @@ def test_det_normalize_resize_u8_pack_crop(gpu, oracle):
         assert_bitexact(got, oracle.pack_crop(crop, 48, 320, pad_only), f"pack_crop {y0, x1}")
 
 
+def test_pack_crops_batch(gpu, oracle):
+    """A 70-line rec batch (two launches: 64 + 6 lines) of crops that are
+    resized (tall, wide and clamped at img_w, 1x1) or centred (pad_only),
+    bit-exact per line against the oracle's pack_crop and against the
+    one-line entry point; a pad_only crop taller than img_h is refused."""
+    torch = gpu
+    from qppocr_amd import _lib, ops
+    rng = np.random.default_rng(54)
+    shapes = [(54, 310), (40, 500), (1, 1), (48, 200), (30, 40), (7, 900), (20, 64)]
+    crops, pads = [], []
+    for i in range(70):
+        ch, cw = shapes[i % len(shapes)]
+        pad = ch <= 48 and i % 3 == 0
+        crops.append(rng.integers(0, 256, (ch, cw, 3), dtype=np.uint8))
+        pads.append(pad)
+    gcrops = [_t(torch, c) for c in crops]
+    got = _n(ops.pack_crops(gcrops, 48, 320, pads))
+    assert got.shape == (70, 3, 48, 320)
+    for i, (c, pad) in enumerate(zip(crops, pads)):
+        assert_bitexact(got[i], oracle.pack_crop(c, 48, 320, pad), f"line {i} pad {pad}")
+        assert np.array_equal(got[i], _n(ops.pack_crop(gcrops[i], 48, 320, pad)))
+    with pytest.raises(_lib.QphError, match="taller"):
+        ops.pack_crops([gcrops[0]], 48, 320, [True])
+
+
 def test_db_mask(gpu, oracle):
     torch = gpu
     from qppocr_amd import ops
