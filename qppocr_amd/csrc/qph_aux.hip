@@ -99,6 +99,7 @@ struct PoolK {
   int special, max_pool;
   uint64_t mag;   // oy = (idx * mag) >> shift: idx / ow for idx < oh * ow < 2^31
   int shift;
+  int pair;       // 2x2 window, sw 2, pw 0, even w, 8-byte aligned x: float2 rows
 };
 
 // One thread per output of a plane (planes by blockIdx.y); K = the window's
@@ -119,6 +120,19 @@ __global__ __launch_bounds__(256) void pool2d_kernel(PoolK p) {
     float b = -3.40282347e38f;
     if (ox + 1 < p.w) b = has_r1 ? fmaxf(r0[ox + 1], r0[ox + 1 + p.w]) : r0[ox + 1];
     v = fmaxf(a, b);
+  } else if (K == 2 && p.pair) {
+    // 2x2, column stride 2, no column padding, even width: each window row is
+    // one 8-byte load; taps still in the order (0,0), (0,1), (1,0), (1,1)
+    float acc = p.max_pool ? -3.4e38f : 0.0f;
+#pragma unroll
+    for (int ky = 0; ky < 2; ky++) {
+      const int64_t iy = oy * p.sh - p.ph + ky;
+      if (iy < 0 || iy >= p.h) continue;
+      const float2 t = *(const float2*)(xp + iy * p.w + 2 * ox);
+      acc = p.max_pool ? (t.x > acc ? t.x : acc) : acc + t.x;
+      acc = p.max_pool ? (t.y > acc ? t.y : acc) : acc + t.y;
+    }
+    v = p.max_pool ? acc : acc / 4.0f;
   } else {
     const int64_t kh = K ? K : p.kh, kw = K ? K : p.kw;
     float acc = p.max_pool ? -3.4e38f : 0.0f;
@@ -161,6 +175,10 @@ int launch_pool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, in
   if (n * c > 65535 || p.oh * p.ow >= (1ll << 31))
     return fail(QPH_EUNSUPPORTED, "pool2d: grid too large");
   invariant_divisor(p.ow, &p.mag, &p.shift);
+  // every window's two columns 2 ox, 2 ox + 1 lie inside the row (2 (ow - 1) + 1
+  // <= w - 1 with pw = 0) and start 8-byte aligned when w is even
+  p.pair = kh == 2 && kw == 2 && sw == 2 && pw == 0 && w % 2 == 0 &&
+           (uintptr_t)x % 8 == 0 && 2 * (p.ow - 1) + 1 <= w - 1;
   const dim3 grid((unsigned)ceil_div(p.oh * p.ow, 256), (unsigned)(n * c));
   if (!p.special && kh == 2 && kw == 2)
     hipLaunchKernelGGL(pool2d_kernel<2>, grid, dim3(256), 0, s, p);

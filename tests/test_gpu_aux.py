@@ -26,6 +26,9 @@ POOL_CASES = [  # (k, stride, pad (ph, pw, peh, pew), max)
     ((3, 3), (2, 2), (1, 1, 1, 1), True),
     ((2, 2), (2, 2), (0, 0, 0, 0), False),
     ((3, 2), (1, 2), (1, 0, 2, 1), True),
+    ((2, 2), (2, 2), (0, 0, 0, 0), True),      # 2x2 s2: paired column loads on even widths
+    ((2, 2), (2, 2), (1, 0, 1, 0), True),      # ... with padded rows
+    ((2, 2), (2, 2), (1, 0, 0, 0), False),
 ]
 
 
@@ -35,9 +38,10 @@ def test_pool2d(gpu, oracle, case):
     from qppocr_amd import ops
     k, s, pad, mx = case
     rng = XorShift(0x243F6A8885A308D3)
-    x = rng.fill((2, 3, 20, 30))
-    want = oracle.pool2d(x, k[0], k[1], s[0], s[1], *pad, mx)
-    assert_bitexact(_n(ops.pool2d(_t(torch, x), k, s, pad, mx)), want, f"pool {case}")
+    for shape in [(2, 3, 20, 30), (1, 2, 9, 31)]:   # even and odd widths
+        x = rng.fill(shape)
+        want = oracle.pool2d(x, k[0], k[1], s[0], s[1], *pad, mx)
+        assert_bitexact(_n(ops.pool2d(_t(torch, x), k, s, pad, mx)), want, f"pool {case} {shape}")
 
 
 def test_global_avg_pool_and_mul_add_scale(gpu, oracle):
