@@ -337,6 +337,9 @@ struct TransposeTileK {
   int64_t tiles_a;        // tiles along axis A
 };
 
+// V4: n3 and every row start a multiple of 4 floats (16-byte aligned), so a
+// thread loads 4 consecutive elements of a tile row at once.
+template <bool V4>
 __global__ __launch_bounds__(256) void transpose4_tile_kernel(TransposeTileK p) {
   __shared__ float t[64 * 65];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -345,10 +348,26 @@ __global__ __launch_bounds__(256) void transpose4_tile_kernel(TransposeTileK p) 
   const int64_t bb = blockIdx.y / p.nc, bc = blockIdx.y - bb * p.nc;
   const float* xb = p.x + bb * p.ib + bc * p.ic;
   float* yb = p.y + bb * p.ob + bc * p.oc;
+  if constexpr (V4) {
+    // 16 threads a tile row (4 columns each), 16 rows a pass
+    const int cq = (threadIdx.x & 15) * 4, rq = threadIdx.x >> 4;
+#pragma unroll
+    for (int r = rq; r < 64; r += 16) {
+      const int64_t a = a0 + r, c = c0 + cq;
+      if (a < p.na && c < p.n3) {   // n3 % 4 == 0: the quad is whole
+        const float4 v = *(const float4*)(xb + a * p.ia + c);
+        t[r * 65 + cq] = v.x;
+        t[r * 65 + cq + 1] = v.y;
+        t[r * 65 + cq + 2] = v.z;
+        t[r * 65 + cq + 3] = v.w;
+      }
+    }
+  } else {
 #pragma unroll 4
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t a = a0 + r, c = c0 + tx;
-    if (a < p.na && c < p.n3) t[r * 65 + tx] = xb[a * p.ia + c];
+    for (int r = ty; r < 64; r += 4) {
+      const int64_t a = a0 + r, c = c0 + tx;
+      if (a < p.na && c < p.n3) t[r * 65 + tx] = xb[a * p.ia + c];
+    }
   }
   __syncthreads();
 #pragma unroll 4
@@ -389,8 +408,13 @@ int launch_transpose4(const float* x, const int64_t xs[4], const int32_t perm[4]
     const int64_t tiles = p.tiles_a * ceil_div(p.n3, 64);
     const int64_t batch = xs[bax[0]] * xs[bax[1]];
     if (p.na * p.n3 >= 256 && batch <= 65535 && tiles < (1ll << 31)) {
-      hipLaunchKernelGGL(transpose4_tile_kernel, dim3((unsigned)tiles, (unsigned)batch), dim3(256),
-                         0, s, p);
+      const dim3 grid((unsigned)tiles, (unsigned)batch);
+      // row starts b * ib + c * ic + a * ia: 16-byte aligned when x is and
+      // every input stride of axes 0..2 is a multiple of 4 (n3 % 4 == 0)
+      if (p.n3 % 4 == 0 && (uintptr_t)x % 16 == 0)
+        hipLaunchKernelGGL(transpose4_tile_kernel<true>, grid, dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL(transpose4_tile_kernel<false>, grid, dim3(256), 0, s, p);
       return launch_check("transpose4_tile_kernel");
     }
   }
