@@ -549,6 +549,16 @@ __device__ __forceinline__ void u8_axis(int64_t i, float scale, int64_t n_in, in
   f = v - (float)b;
 }
 
+__device__ __forceinline__ uint8_t u8_mix(float p00, float p01, float p10, float p11, float lx,
+                                          float fy) {
+  float t = p00 * (1.0f - lx) * (1.0f - fy);
+  t = __builtin_fmaf(p01 * lx, 1.0f - fy, t);
+  t = __builtin_fmaf(p10 * (1.0f - lx), fy, t);
+  float val = __builtin_fmaf(p11 * lx, fy, t) + 0.5f;
+  val = val < 0.0f ? 0.0f : (val > 255.0f ? 255.0f : val);
+  return (uint8_t)val;
+}
+
 __device__ __forceinline__ uint8_t u8_sample(const uint8_t* r0, const uint8_t* r1, int64_t a,
                                              int64_t b, float lx, float fy, int ch) {
   const float p00 = r0[a + ch], p01 = r0[b + ch], p10 = r1[a + ch], p11 = r1[b + ch];
@@ -564,6 +574,8 @@ struct RgbResizeK {
   const uint8_t* src;
   int64_t sw, sh, dw, dh;
   float sx, sy;
+  int64_t total;   // source bytes
+  int words;       // src 4-byte aligned: tap pairs by dword loads
 };
 
 // One thread per output pixel: columns by blockIdx.x, rows by blockIdx.y
@@ -583,15 +595,41 @@ __global__ __launch_bounds__(256) void resize_rgb_u8_kernel(RgbResizeK p, uint8_
     const uint8_t* r0 = p.src + j0 * p.sw * 3;
     const uint8_t* r1 = p.src + j1 * p.sw * 3;
     uint8_t* d = dst + (y * p.dw + x) * 3;
+    const int64_t o0 = (j0 * p.sw + x0) * 3, o1 = (j1 * p.sw + x0) * 3;
+    const int64_t b0 = o0 & ~(int64_t)3, b1 = o1 & ~(int64_t)3;
+    if (p.words && x1 == x0 + 1 && b0 + 12 <= p.total && b1 + 12 <= p.total) {
+      // both taps of a row are the 6 bytes from o: three aligned dwords hold
+      // them (o - base <= 3, so bytes up to base + 8)
+      uint8_t q0[6], q1[6];
+      const uint32_t* w0 = (const uint32_t*)(p.src + b0);
+      const uint32_t* w1 = (const uint32_t*)(p.src + b1);
+      const uint32_t a0 = w0[0], a1 = w0[1], a2 = w0[2];
+      const uint32_t c0 = w1[0], c1 = w1[1], c2 = w1[2];
+      const int s0 = (int)(o0 - b0) * 8, s1 = (int)(o1 - b1) * 8;
+      const uint64_t lo0 = (uint64_t)a0 | ((uint64_t)a1 << 32);
+      const uint64_t lo1 = (uint64_t)c0 | ((uint64_t)c1 << 32);
+      const uint64_t v0 = s0 ? (lo0 >> s0) | ((uint64_t)a2 << (64 - s0)) : lo0;
+      const uint64_t v1 = s1 ? (lo1 >> s1) | ((uint64_t)c2 << (64 - s1)) : lo1;
 #pragma unroll
-    for (int ch = 0; ch < 3; ch++) d[ch] = u8_sample(r0, r1, x0 * 3, x1 * 3, lx, fy, ch);
+      for (int k = 0; k < 6; k++) {
+        q0[k] = (uint8_t)(v0 >> (8 * k));
+        q1[k] = (uint8_t)(v1 >> (8 * k));
+      }
+#pragma unroll
+      for (int ch = 0; ch < 3; ch++)
+        d[ch] = u8_mix(q0[ch], q0[3 + ch], q1[ch], q1[3 + ch], lx, fy);
+    } else {
+#pragma unroll
+      for (int ch = 0; ch < 3; ch++) d[ch] = u8_sample(r0, r1, x0 * 3, x1 * 3, lx, fy, ch);
+    }
   }
 }
 
 int launch_resize_rgb_u8(const uint8_t* src, int64_t sw, int64_t sh, uint8_t* dst, int64_t dw,
                          int64_t dh, hipStream_t s) {
   if (ceil_div(dw, 256) >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "resize_rgb_u8: too wide");
-  RgbResizeK p{src, sw, sh, dw, dh, (float)sw / (float)dw, (float)sh / (float)dh};
+  RgbResizeK p{src, sw, sh, dw, dh, (float)sw / (float)dw, (float)sh / (float)dh,
+               sw * sh * 3, (uintptr_t)src % 4 == 0};
   hipLaunchKernelGGL(resize_rgb_u8_kernel,
                      dim3((unsigned)ceil_div(dw, 256), (unsigned)std::min<int64_t>(dh, 65535)),
                      dim3(256), 0, s, p, dst);
