@@ -1016,40 +1016,42 @@ __global__ __launch_bounds__(64) void gemm_wave_kernel(GemmArgs g, int mb, int n
 
 // Per row: combines the (max, first index, exp1 sum) partials of its nb
 // column blocks into the (value, index) pair of the row's softmax argmax.
-// One wave per row; block t holds columns 64 t .. 64 t + 63, so among the
-// blocks whose max is the row max the lowest t has the lowest index.
+// One wave per row, one pass over the partials: each lane keeps a running
+// (max, index, sum against that max), rescaling the sum when the max rises;
+// block t holds columns 64 t .. 64 t + 63, so a lane's first strict max and,
+// across lanes, the lower index among equal maxima give the first maximum.
 __global__ __launch_bounds__(256) void head_pairs_kernel(const float* __restrict__ part,
                                                          int64_t rows, int nb,
                                                          float* __restrict__ pairs) {
+  const float L2E = 1.44269504f;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const f32x4* pr = (const f32x4*)part + row * nb;
-  float m = -__builtin_inff();
+  float m = -__builtin_inff(), sum = 0.0f;
   int idx = 0x7fffffff;
   for (int t = lane; t < nb; t += 64) {
     const f32x4 q = pr[t];
     if (q[0] > m) {
+      sum = (sum > 0.0f ? sum * __builtin_amdgcn_exp2f((m - q[0]) * L2E) : 0.0f) + q[2];
       m = q[0];
       idx = __float_as_int(q[1]);
+    } else {
+      sum += q[2] * __builtin_amdgcn_exp2f((q[0] - m) * L2E);
     }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float mo = __shfl_xor(m, off, 64);
     const int io = __shfl_xor(idx, off, 64);
-    if (mo > m || (mo == m && io < idx)) {
-      m = mo;
-      idx = io;
-    }
+    const float so = __shfl_xor(sum, off, 64);
+    const float mm = fmaxf(m, mo);
+    // a lane without partials has sum 0 and max -inf: its term is 0
+    sum = (sum > 0.0f ? sum * __builtin_amdgcn_exp2f((m - mm) * L2E) : 0.0f) +
+          (so > 0.0f ? so * __builtin_amdgcn_exp2f((mo - mm) * L2E) : 0.0f);
+    if (mo > m || (mo == m && io < idx)) idx = io;
+    m = mm;
   }
-  float sum = 0.0f;
-  for (int t = lane; t < nb; t += 64) {
-    const f32x4 q = pr[t];
-    sum += q[2] * __builtin_amdgcn_exp2f((q[0] - m) * 1.44269504f);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
   if (lane == 0) {
     pairs[2 * row] = 1.0f / sum;   // the max's exponential is exp1(0) = 1
     pairs[2 * row + 1] = __int_as_float(idx);
