@@ -69,6 +69,8 @@ def test_null_context_is_an_error_not_a_crash(lib):
     act = None
     assert lib.qph_conv2d(None, None, None, None, None, None, None, act, None, None, None) == -1
     assert lib.qph_softmax_last_dim(None, None, 1, 1) == -1
+    assert lib.qph_pack_crops(None, 1, None, None, None, None, 48, 320, None) == -1
+    assert lib.qph_plan_run(None, None, 1, None) == -1
     assert lib.qph_net_run(None, None, 0, None) == -1
     assert lib.qph_net_destroy(None) == 0
     assert lib.qph_ctx_destroy(None) == 0
