@@ -51,7 +51,8 @@ aux: the operators around the nets -- page resize, det input normalisation,
 rec line packing, the DB mask, the SE block's pool and gate, MaxPool,
 bilinear Resize, Transpose -- each at a page-scale shape: device time per
 launch, cache-cold (a captured graph over rotating buffer sets past 512 MB),
-against the HBM roofline.
+against the HBM roofline, with the CPU oracle on the same inputs beside each
+(1 s floor per operator).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--cpu-rounds R] [--no-configs] [--node-report FILE]
@@ -74,6 +75,7 @@ REC_BATCH = 32
 COLD_BYTES = 512 << 20      # buffer sets per op bench: twice the Infinity Cache
 CPU_HEADLINE_MIN_S = 5.0    # CPU oracle: seconds of timed rounds for det and for rec
 CPU_CONFIG_MIN_S = 2.0      # ... and for each single-op / page config
+CPU_AUX_MIN_S = 1.0         # ... and for each operator of the aux leg
 
 
 def head_traffic_bytes(name="rec_fused_head_traffic.md"):
@@ -338,9 +340,10 @@ def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
 def aux_specs(torch, lib, ctx):
     """The operators around the nets, each at a page-scale shape (the mixed
     page's det size 1536^2 and a 32-line rec batch): (name, workload, kernel,
-    make_set, call, launches per set, algorithmic bytes per set).  make_set()
-    allocates one input / output buffer set, call(s) issues its launches on
-    ctx's stream."""
+    make_set, call, launches per set, algorithmic bytes per set, cpu).
+    make_set() allocates one input / output buffer set, call(s) issues its
+    launches on ctx's stream, cpu(O, h) runs the oracle's work for the same
+    set (host arrays h)."""
     P = ctypes.c_void_p
     I64 = ctypes.c_int64
 
@@ -360,12 +363,13 @@ def aux_specs(torch, lib, ctx):
     specs.append(("resize_rgb_u8", "u8 RGB 2048x2048 -> 1536x1536 bilinear",
                   "resize_rgb_u8_kernel", lambda: (u8(2048, 2048, 3), u8(1536, 1536, 3)),
                   lambda s: lib.qph_resize_bilinear_rgb_u8(ctx, ptr(s[0]), 2048, 2048, ptr(s[1]),
-                                                           1536, 1536), 1, nb))
+                                                           1536, 1536), 1, nb,
+                  lambda O, h: O.resize_bilinear_rgb_u8(h[0], 1536, 1536)))
     # det input normalisation (engine.rs:959-982)
     specs.append(("det_normalize_u8", "u8 RGB 1536x1536 -> f32 1x3x1536x1536 ((v/255-0.5)/0.5)",
                   "det_normalize_kernel", lambda: (u8(1536, 1536, 3), f32(1, 3, 1536, 1536)),
                   lambda s: lib.qph_det_normalize_u8(ctx, ptr(s[0]), 1536, 1536, ptr(s[1])), 1,
-                  nb))
+                  nb, lambda O, h: O.det_normalize(h[0])))
 
     # rec line packing (crop.rs:153-190): 32 crops of 40x240 into 3x48x320 slots
     def crops():
@@ -378,8 +382,11 @@ def aux_specs(torch, lib, ctx):
             if r != 0:
                 return r
         return 0
+    def pack_cpu(O, h):
+        for i in range(32):
+            O.pack_crop(h[i], 48, 320, False)
     specs.append(("pack_crop", "32 u8 RGB crops 40x240 -> f32 32x3x48x320 (resized to 48x288, "
-                  "zero tail), one launch per line", "pack_crop_kernel", crops, pack, 32, nb))
+                  "zero tail), one launch per line", "pack_crop_kernel", crops, pack, 32, nb, pack_cpu))
     ptrs = {}
 
     def pack_batch(s):
@@ -392,47 +399,54 @@ def aux_specs(torch, lib, ctx):
         cp, ch, cw, po = ptrs[key]
         return lib.qph_pack_crops(ctx, 32, cp, ch, cw, po, 48, 320, ptr(s[32]))
     specs.append(("pack_crops", "the same 32 lines in one launch (the batch entry point)",
-                  "pack_crops_kernel", crops, pack_batch, 1, nb))
+                  "pack_crops_kernel", crops, pack_batch, 1, nb, pack_cpu))
     # DB threshold + 2x2 dilation (geometry.rs:287-301, resize.rs:219-247)
     specs.append(("db_mask", "f32 probability map 1536x1536 -> u8 mask, thresh 0.3, dilated",
                   "db_mask_kernel", lambda: (f32(1536, 1536), u8(1536, 1536)),
                   lambda s: lib.qph_db_mask(ctx, ptr(s[0]), 1536, 1536, ctypes.c_float(0.3), 1,
-                                            ptr(s[1])), 1, nb))
+                                            ptr(s[1])), 1, nb,
+                  lambda O, h: O.db_mask(h[0], 0.3, True)))
     # SE squeeze and excite (pool2d.rs:10-29, elementwise.rs:134-179)
     specs.append(("global_avg_pool", "f32 1x256x96x96 -> 1x256 (f64 mean per plane)",
                   "reduce_mean_wg_kernel<true>", lambda: (f32(1, 256, 96, 96), f32(256)),
                   lambda s: lib.qph_global_avg_pool(ctx, ptr(s[0]), 1, 256, 96 * 96, ptr(s[1])),
-                  1, nb))
+                  1, nb, lambda O, h: O.global_avg_pool(h[0])))
     specs.append(("mul_add_scale", "f32 1x256x96x96 * gate[256] + residual",
                   "mul_add_scale_kernel",
                   lambda: (f32(1, 256, 96, 96), f32(256), f32(1, 256, 96, 96),
                            f32(1, 256, 96, 96)),
                   lambda s: lib.qph_mul_add_scale(ctx, ptr(s[0]), ptr(s[1]), ptr(s[2]), 1, 256,
-                                                  96 * 96, ptr(s[3])), 1, nb))
+                                                  96 * 96, ptr(s[3])), 1, nb,
+                  lambda O, h: O.mul_add_scale(h[0], h[1], h[2])))
     # MaxPool (pool2d.rs:94-236)
     xs_pool = (I64 * 4)(32, 64, 48, 160)
     ys_pool = (I64 * 4)()
     specs.append(("pool2d_max", "f32 32x64x48x160 -> 32x64x24x80, max 2x2 stride 2",
                   "pool2d_kernel<2>", lambda: (f32(32, 64, 48, 160), f32(32, 64, 24, 80)),
                   lambda s: lib.qph_pool2d(ctx, ptr(s[0]), xs_pool, 2, 2, 2, 2, 0, 0, 0, 0, 1,
-                                           ptr(s[1]), ys_pool), 1, nb))
+                                           ptr(s[1]), ys_pool), 1, nb,
+                  lambda O, h: O.pool2d(h[0], 2, 2, 2, 2, 0, 0, 0, 0, True)))
     # bilinear Resize (resize.rs:60-142): a det map back to page size
     specs.append(("resize_bilinear", "f32 1x1x384x384 -> 1536x1536 (half-pixel)",
                   "resize_bilinear_kernel", lambda: (f32(384, 384), f32(1536, 1536)),
                   lambda s: lib.qph_resize_bilinear(ctx, ptr(s[0]), 1, 384, 384, 1536, 1536, 0,
-                                                    ptr(s[1])), 1, nb))
+                                                    ptr(s[1])), 1, nb,
+                  lambda O, h: O.resize_bilinear(h[0], 1536, 1536, False)))
     xs_tr = (I64 * 4)(1, 96, 384, 384)
     perm = (ctypes.c_int32 * 4)(0, 2, 3, 1)
     specs.append(("transpose", "f32 1x96x384x384 -> 1x384x384x96 (NCHW -> NHWC)",
                   "transpose4_tile_kernel", lambda: (f32(1, 96, 384, 384), f32(1, 384, 384, 96)),
-                  lambda s: lib.qph_transpose(ctx, ptr(s[0]), xs_tr, perm, ptr(s[1])), 1, nb))
+                  lambda s: lib.qph_transpose(ctx, ptr(s[0]), xs_tr, perm, ptr(s[1])), 1, nb,
+                  lambda O, h: O.transpose4(h[0], (0, 2, 3, 1))))
     return specs
 
 
-def bench_aux(ops, replays):
+def bench_aux(ops, replays, O=None, cpu_rounds=5):
     """Device time per launch of the operators around the nets (aux_specs),
     cache-cold: R buffer sets (R x set bytes > COLD_BYTES) whose launches are
-    captured once into a graph, replayed `replays` times between HIP events."""
+    captured once into a graph, replayed `replays` times between HIP events.
+    With the oracle O: its time on the same set beside each (median of the
+    rounds in >= CPU_AUX_MIN_S, per launch)."""
     import torch
     lib = ops._lib.load()
     ctx = ops.new_context(0)
@@ -441,7 +455,7 @@ def bench_aux(ops, replays):
     torch.manual_seed(5)
     out = {}
     try:
-        for name, workload, kernel, make, call, nl, nbytes in aux_specs(torch, lib, ctx):
+        for name, workload, kernel, make, call, nl, nbytes, cpu in aux_specs(torch, lib, ctx):
             first = make()
             set_bytes = nbytes(*first)
             R = max(2, -(-COLD_BYTES // set_bytes))
@@ -473,6 +487,11 @@ def bench_aux(ops, replays):
                          "method": f"cache-cold: HIP events over {replays} replays of a graph "
                                    f"of {R * nl} launches on {R} rotating buffer sets "
                                    f"({R * set_bytes >> 20} MB)"}
+            if O is not None:
+                h = [t.cpu().numpy() for t in first]
+                sec, n = cpu_sample(lambda: cpu(O, h), cpu_rounds, CPU_AUX_MIN_S)
+                out[name]["cpu_baseline"] = {"us": round(sec * 1e6 / nl, 1),
+                                             "gbs": round(by / (sec / nl) / 1e9, 2), "rounds": n}
             del graph, sets, first
             torch.cuda.synchronize()
     finally:
@@ -823,7 +842,7 @@ def main():
         }
     result["configs"] = cfgs
     if not args.no_configs:
-        result["aux"] = bench_aux(ops, max(3, K // 5))
+        result["aux"] = bench_aux(ops, max(3, K // 5), O, args.cpu_rounds)
     print(json.dumps(result))
     det.close()
     rec.close()

@@ -225,7 +225,7 @@ def test_aux_ops_graph_replays_match_eager(gpu):
     ops.check(lib.qph_ctx_set_stream(ctx, ctypes.c_void_p(st.cuda_stream)))
     try:
         torch.manual_seed(7)
-        for name, _, _, make, call, _, _ in bench.aux_specs(torch, lib, ctx):
+        for name, _, _, make, call, _, _, _ in bench.aux_specs(torch, lib, ctx):
             print("aux graph case", name, flush=True)
             s = make()                       # the last tensor of a set is the output
             torch.cuda.synchronize()
