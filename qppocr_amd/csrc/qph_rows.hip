@@ -1482,10 +1482,10 @@ __global__ __launch_bounds__(256) void reduce_mean_kernel(MeanRows p) {
 
 // Long rows (a global average pool's planes): one 256-thread workgroup per
 // row, every load of a pass issued before its terms are summed (16-byte
-// loads when the row is contiguous and aligned).  The lane partials meet
-// through LDS and f64_mean_check runs on the row's totals: it holds for any
-// summation order, and a row that fails it takes the same sequential sum as
-// above, on wave 0.
+// loads when the row is contiguous and aligned: 16 a thread, so a pass covers
+// 16384 terms).  The lane partials meet through LDS and f64_mean_check runs
+// on the row's totals: it holds for any summation order, and a row that
+// fails it takes the same sequential sum as above, on wave 0.
 template <bool VEC>
 __global__ __launch_bounds__(256) void reduce_mean_wg_kernel(MeanRows p) {
   __shared__ double ls[4], la[4];
@@ -1506,15 +1506,15 @@ __global__ __launch_bounds__(256) void reduce_mean_wg_kernel(MeanRows p) {
   if constexpr (VEC) {
     const int64_t nq = cols >> 2;
     const f32x4* xq = (const f32x4*)xr;
-    for (int64_t q0 = 0; q0 < nq; q0 += 256 * 8) {
-      f32x4 v[8];
+    for (int64_t q0 = 0; q0 < nq; q0 += 256 * 16) {
+      f32x4 v[16];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
+      for (int u = 0; u < 16; u++) {
         const int64_t q = q0 + u * 256 + tid;
         v[u] = q < nq ? xq[q] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       }
 #pragma unroll
-      for (int u = 0; u < 8; u++)
+      for (int u = 0; u < 16; u++)
 #pragma unroll
         for (int c = 0; c < 4; c++) term(v[u][c]);
     }
