@@ -500,16 +500,21 @@ def bench_aux(ops, replays, O=None, cpu_rounds=5):
     return out
 
 
-def time_mixed_page(steps, warmup):
+def time_mixed_page(steps, warmup, engine=False, data=None):
     """det 1x3x1536x1536 + 128 rec lines (widths {80..1280}, buckets of 160,
     <= 64 lines per batch, fused rec heads), inputs resident.  det and the rec batches run on
     three streams (det; rec batches alternating over two): page_ms is the
-    wall time per page over the steps; det_ms / rec_ms are each stage alone."""
+    wall time per page over the steps; det_ms / rec_ms are each stage alone.
+    engine: the lines batched as the reference engine batches them for a GPU
+    session (spans of 64 px, 64 lines a forward, widths rounded to 64), each
+    batch on a 64-row net run with real_n = its line count."""
+    import numpy as np
     import torch
     from qppocr_amd import ops, pipeline
-    det_g, det_x, rw, lines, widths = pipeline.mixed_page(4, 1536, 128)
+    det_g, det_x, rw, lines, widths = data if data else pipeline.mixed_page(4, 1536, 128)
     ctxs = [ops.new_context(0) for _ in range(3)]
-    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths, contexts=ctxs, fused_head=True)
+    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths, contexts=ctxs, fused_head=True,
+                               engine=engine)
     page.upload()
     for _ in range(warmup):
         page.run()
@@ -526,9 +531,16 @@ def time_mixed_page(steps, warmup):
     det_ms = wall(page.run_det)
     rec_ms = wall(page.run_rec)
     page_ms = wall(page.run)
-    out = {"workload": "det 1x3x1536x1536 + 128 rec lines 3x48x{80..1280}, buckets of 160, "
-                       "<= 64 lines/batch, CTC masked past w/8 (seed 4)",
+    creates = page.net_create_ms
+    out = {"workload": ("det 1x3x1536x1536 + 128 rec lines 3x48x{80..1280}, engine batching "
+                        "(spans of 64 px, <= 64 lines a forward, widths to 64, batch padded to "
+                        "64 with real_n), CTC masked past w/8 (seed 4)") if engine else
+                       ("det 1x3x1536x1536 + 128 rec lines 3x48x{80..1280}, buckets of 160, "
+                        "<= 64 lines/batch, CTC masked past w/8 (seed 4)"),
            "rec_batches": [[bw, len(idx)] for bw, idx in page.plan],
+           "rec_net_create_ms": {"n": len(creates),
+                                 "mean": round(float(np.mean(creates)), 2),
+                                 "max": round(float(np.max(creates)), 2)},
            "det_img_per_s": round(1e3 / det_ms, 2),
            "rec_lines_per_s": round(len(widths) * 1e3 / rec_ms, 1),
            "page_ms": round(page_ms, 4), "ms_per_image": round(page_ms, 4),
@@ -818,6 +830,8 @@ def main():
     mixed_data = None
     if not args.no_configs:
         cfgs["cfg5"], mixed_data = time_mixed_page(max(3, K // 5), 2)
+        cfgs["cfg5"]["engine_batching"], _ = time_mixed_page(max(3, K // 5), 2, engine=True,
+                                                             data=mixed_data)
 
     if O is not None:
         det_s, det_n = cpu_sample(lambda: onets.run_graph(det_g, det_x), args.cpu_rounds,

@@ -48,6 +48,11 @@ QPH_API int qph_ctx_destroy(qph_ctx* ctx);
  * the context's own; NULL restores the context's stream. */
 QPH_API int qph_ctx_set_stream(qph_ctx* ctx, void* hip_stream);
 QPH_API void* qph_ctx_stream(qph_ctx* ctx);
+/* Bytes of device scratch the context has allocated for standalone operator
+ * calls (it grows on demand with hipMalloc; 0 until a call needs it).  No
+ * counterpart in the reference; for tests of the allocation-free entry
+ * point and for memory accounting. */
+QPH_API int qph_ctx_scratch_bytes(qph_ctx* ctx, size_t* bytes);
 QPH_API int qph_sync(qph_ctx* ctx);
 /* Thread-local message of the last failed call (empty string if none). */
 QPH_API const char* qph_last_error(void);
@@ -58,6 +63,9 @@ QPH_API int qph_malloc(qph_ctx* ctx, void** ptr, size_t bytes);
 QPH_API int qph_free(qph_ctx* ctx, void* ptr);
 QPH_API int qph_memcpy_h2d(qph_ctx* ctx, void* dst, const void* src_host, size_t bytes);
 QPH_API int qph_memcpy_d2h(qph_ctx* ctx, void* dst_host, const void* src, size_t bytes);
+/* Fills bytes with (value & 0xff), asynchronously on the context stream, by a
+ * kernel (never hipMemsetAsync), so it may be recorded into a captured
+ * graph. */
 QPH_API int qph_memset(qph_ctx* ctx, void* dst, int value, size_t bytes);
 
 /* ------------------------------------------------------------ operators */
@@ -389,6 +397,20 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
  * are shared); qph_net_run completes a pending run first. */
 #define QPH_RUN_UPLOAD 1
 #define QPH_RUN_DOWNLOAD 2
+/* Real batch count (the plan model's params[0] slot, qppocr-gpu/src/plan.rs:
+ * 587-593, which the GPU sessions write before a run padded to
+ * DeviceSession::batch_grain, qppocr-core/src/device.rs:139-157): the runs
+ * that follow compute batch items 0 .. real_n - 1 only, 1 <= real_n <= the
+ * input's batch dimension.  Every kernel of such a run is launched over the
+ * real items alone (a HIP graph per distinct count, captured by this call
+ * the first time the count is set), the input upload and the output
+ * downloads of qph_net_run / qph_net_run_async move real_n items, and
+ * batch items past real_n keep stale contents.  Requires every tensor
+ * derived from the input to keep the batch as its first dimension
+ * (QPH_EUNSUPPORTED otherwise); refused while a deferred run is in flight.
+ * qph_net_real_n reads the current count and the batch dimension. */
+QPH_API int qph_net_set_real_n(qph_net* net, int32_t real_n);
+QPH_API int qph_net_real_n(qph_net* net, int32_t* real_n, int32_t* batch);
 QPH_API int qph_net_staging(qph_net* net, int32_t slot, float** host, int64_t* numel);
 QPH_API int qph_net_run_async(qph_net* net, int32_t flags);
 QPH_API int qph_net_complete(qph_net* net);

@@ -86,6 +86,7 @@ SIGNATURES = {
     "qph_memcpy_h2d": ([P, P, P, ctypes.c_size_t], ctypes.c_int),
     "qph_memcpy_d2h": ([P, P, P, ctypes.c_size_t], ctypes.c_int),
     "qph_memset": ([P, P, ctypes.c_int, ctypes.c_size_t], ctypes.c_int),
+    "qph_ctx_scratch_bytes": ([P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "qph_conv2d_out_shape": ([P, P, ctypes.POINTER(ConvParams), P], ctypes.c_int),
     "qph_conv2d": ([P, P, P, P, P, P, ctypes.POINTER(ConvParams), ctypes.POINTER(Act), P, P, P],
                    ctypes.c_int),
@@ -124,6 +125,8 @@ SIGNATURES = {
     "qph_net_destroy": ([P], ctypes.c_int),
     "qph_net_run": ([P, P, I32, ctypes.POINTER(P)], ctypes.c_int),
     "qph_net_tensor": ([P, I32, ctypes.POINTER(P), ctypes.POINTER(I64)], ctypes.c_int),
+    "qph_net_set_real_n": ([P, I32], ctypes.c_int),
+    "qph_net_real_n": ([P, ctypes.POINTER(I32), ctypes.POINTER(I32)], ctypes.c_int),
     "qph_net_staging": ([P, I32, ctypes.POINTER(P), ctypes.POINTER(I64)], ctypes.c_int),
     "qph_net_run_async": ([P, I32], ctypes.c_int),
     "qph_net_complete": ([P], ctypes.c_int),

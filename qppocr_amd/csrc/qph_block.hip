@@ -591,10 +591,20 @@ static int halo_floats(const DwPwArgs& a) { return (int)(a.c * halo_pcp(a)); }
 // pixels per depthwise task: about one task per thread
 static int dw_px(int64_t cpad) { return cpad >= 128 ? 8 : cpad >= 64 ? 4 : cpad >= 32 ? 2 : 1; }
 
+// LDS of a (non-stem) launch with `halo` floats of input halo: halo,
+// k-major pointwise weight slice, depthwise outputs, depthwise weights and
+// bias (the layout launch_dwpw sizes)
+static int64_t dwpw_lds_bytes(const DwPwArgs& a, int64_t halo) {
+  const int64_t cpad = (a.c + 3) / 4 * 4;
+  return (halo + cpad * 64 + cpad * 16 + (a.c * a.kh * a.kw + 63) / 64 * 64 + (a.c + 63) / 64 * 64) *
+         4;
+}
+
 bool dwpw_eligible(const DwPwArgs& a) {
   return ((a.kh == 3 && a.kw == 3) || (a.kh == 5 && a.kw == 5)) && a.c > 0 &&
          a.c <= DWPW_MAX_C && a.m > 0 && a.n <= 65535 && (a.sw == 1 || a.sw == 2) &&
          halo_per_c(a) <= 128 && halo_floats(a) <= DWPW_MAX_HALO &&
+         dwpw_lds_bytes(a, halo_floats(a)) <= 160 * 1024 &&
          a.c * a.h * a.w * 4 < (int64_t)0x80000000 && a.oh * a.ow < (1ll << 30) &&
          (a.m + 31) / 32 * 32 * ((a.c + 3) / 4 * 4) * 4 < (1ll << 31);
 }
@@ -674,7 +684,7 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
   p.halo = halo_floats(a);
   p.wrows = p.cpad * 64;
   p.wdl_pad = (int)((a.c * a.kh * a.kw + 63) / 64 * 64);
-  size_t lds = (size_t)(p.halo + p.wrows + p.cpad * 16 + p.wdl_pad + (a.c + 63) / 64 * 64) * 4;
+  size_t lds = (size_t)dwpw_lds_bytes(a, p.halo);
   const int64_t tiles = (int64_t)p.tiles_x * a.oh;
   if (tiles >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "dw+pw block: grid too large");
   dim3 grid((unsigned)tiles, (unsigned)p.slices, (unsigned)a.n);
@@ -701,7 +711,8 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
   // the 16-byte path's halo: whole chunks, channels contiguous
   const int vch = a.kh == 5 ? VecGeom<5, 5, 1>::CH : a.sw == 1 ? VecGeom<3, 3, 1>::CH
                                                               : VecGeom<3, 3, 2>::CH;
-  const bool vec = dwpw_vec(a) && a.c * 4 * vch <= DWPW_MAX_HALO;
+  const bool vec = dwpw_vec(a) && a.c * 4 * vch <= DWPW_MAX_HALO &&
+                   dwpw_lds_bytes(a, a.c * 4 * vch) <= 160 * 1024;
   if (vec) {
     lds -= (size_t)p.halo * 4;
     p.halo = (int)a.c * 4 * vch;

@@ -1270,11 +1270,16 @@ __global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, i
 #pragma unroll
     for (int u = 0; u < LB; u++) lds_load16(br, b + 4 * u * LT_BK, boff[u], so);
   };
+  // each chain starts at 0, or at its column's bias when the bias seeds it
+  // (a lane's four accumulator rows share the column j)
   f32x4 acc[BM][BN];
 #pragma unroll
-  for (int bm = 0; bm < BM; bm++)
+  for (int bn = 0; bn < BN; bn++) {
+    const int j = j0 + wn * (TN / 2) + bn * 16 + l16;
+    const float b0 = (g.bias_seed && g.bias && j < N) ? g.bias[j] : 0.0f;
 #pragma unroll
-    for (int bn = 0; bn < BN; bn++) acc[bm][bn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int bm = 0; bm < BM; bm++) acc[bm][bn] = f32x4{b0, b0, b0, b0};
+  }
   float av[BM][16], bv[BN][16];
   // operands of a slab: lane (g, l16) takes k = 4s + g of its rows, s = 0..15
   auto fetch = [&](auto st) {
@@ -1320,7 +1325,7 @@ __global__ __launch_bounds__(256) void linear_nt_kernel(LinArgs g, int ntiles, i
 #pragma unroll
   for (int bn = 0; bn < BN; bn++) {
     const int j = j0 + wn * (TN / 2) + bn * 16 + l16;
-    badd[bn] = (g.bias && j < N) ? g.bias[j] : -0.0f;
+    badd[bn] = (g.bias && !g.bias_seed && j < N) ? g.bias[j] : -0.0f;
 #pragma unroll
     for (int bm = 0; bm < BM; bm++) {
       const int ib = i0 + wm * (TM / 2) + bm * 16 + 4 * lg;

@@ -195,6 +195,7 @@ struct LinArgs {
   const float* bias;          // per column, or NULL
   Act act;
   const float* res;           // [M][N], or NULL
+  int bias_seed;              // 1: the bias starts each chain instead of following it
 };
 bool linear_nt_eligible(int64_t m, int64_t n, int64_t k, int64_t lda);
 // the rec QKV linear (x [batch * t][k] . Wt[3 heads dh][k]^T + bias) and

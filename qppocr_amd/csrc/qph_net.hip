@@ -14,7 +14,11 @@ using namespace qph;
 struct qph_net {
   qph_ctx* ctx;
   std::vector<qph_node> nodes;
-  std::vector<int64_t> shapes;   // 4 per tensor
+  std::vector<int64_t> shapes_full;  // 4 per tensor, as created
+  std::vector<int64_t> shapes;   // 4 per tensor, batch dimension cut to real_n
+  std::vector<bool> batch_major; // per tensor: derived from the input, batch outermost
+  int64_t batch;                 // the input's batch dimension (the net's capacity)
+  int64_t real_n;                // batch items the next run computes (1..batch)
   std::vector<int32_t> alias;
   std::vector<int32_t> outputs;
   std::vector<float*> weights;   // device copies
@@ -35,9 +39,8 @@ struct qph_net {
   std::vector<int64_t> pitch;    // per tensor: padded row pitch in floats (0: contiguous)
   char* arena;
   size_t arena_bytes;
-  hipGraph_t graph;
-  hipGraphExec_t exec;
-  bool graph_ready;
+  std::vector<hipGraph_t> graphs;     // per real_n (index 1..batch): captured on first use
+  std::vector<hipGraphExec_t> execs;
   bool profiling;
   std::vector<hipEvent_t> ev;
   std::vector<double> node_ms;
@@ -49,8 +52,15 @@ struct qph_net {
   bool inflight;
 };
 
+// Elements of a tensor in the current run (batch-major tensors hold
+// real_n batch items) and of its storage.
 static int64_t numel_of(const qph_net* net, int32_t id) {
   const int64_t* s = &net->shapes[4 * (size_t)id];
+  return s[0] * s[1] * s[2] * s[3];
+}
+
+static int64_t numel_full(const qph_net* net, int32_t id) {
+  const int64_t* s = &net->shapes_full[4 * (size_t)id];
   return s[0] * s[1] * s[2] * s[3];
 }
 
@@ -64,6 +74,14 @@ static int check_tensor(const qph_net* net, int32_t id, bool optional, size_t i,
   if (id < 0 || id >= (int32_t)net->tptr.size())
     return fail(QPH_EINVAL, node_name(i, n) + ": bad " + what + " tensor id");
   return QPH_OK;
+}
+
+// The 1x1 path's bias-placement rule for n batch items of px pixels
+// (qppocr-kernels/src/conv.rs:264-460, as conv_dispatch picks it): 0 = the
+// bias after the chain everywhere, 1 = the N == 1 panel / m-rows rule.
+static int pw_seed_rule(int64_t n, int64_t m, int64_t px, int64_t c) {
+  const double fl = (double)m * (double)px * (double)c;
+  return (n > 1 || fl < 2e5 || (px + 31) / 32 >= 2) ? 0 : 1;
 }
 
 // Linear node i over its resident transposed weight.
@@ -115,6 +133,11 @@ static int run_node(qph_net* net, size_t i) {
         g.a = x; g.lda = n.ws[1]; g.wt = w; g.c = y;
         g.m = xs[0] * xs[2] * xs[3]; g.n = n.ws[0]; g.k = n.ws[1];
         g.bias = bias; g.act = make_act(&n.act); g.res = nullptr;
+        // the m-rows rule (one batch item of at most 32 pixels, as a run at
+        // real_n = 1 can be) seeds the chain with the bias for the pixels
+        // past the last full 32-pixel block: all of them below 32 pixels
+        const int64_t px = xs[2] * xs[3];
+        g.bias_seed = bias && pw_seed_rule(xs[0], g.n, px, g.k) == 1 && px < 32;
         return launch_linear_nt(g, s);
       }
       qph_conv_epilogue ep{};
@@ -410,9 +433,10 @@ static void plan_cl(qph_net* net) {
   auto pw_ok = [&](const qph_node& q) {
     const int64_t* xs = &net->shapes[4 * (size_t)q.in];
     const int64_t m = q.ws[0], c = q.ws[1], px = xs[2] * xs[3];
-    const double fl = (double)m * (double)px * (double)c;
-    const int rule = (xs[0] > 1 || fl < 2e5 || (px + 31) / 32 >= 2) ? 0 : 1;
-    return rule == 0 && m % 4 == 0 && linear_nt_eligible(xs[0] * px, m, c, c);
+    // (a run over one batch item, real_n = 1, may need the m-rows rule:
+    // run_node seeds the chains then, see below)
+    return pw_seed_rule(xs[0], m, px, c) == 0 && m % 4 == 0 &&
+           linear_nt_eligible(xs[0] * px, m, c, c);
   };
   for (size_t e = 0; e < nn; e++) {
     const qph_node& last = net->nodes[e];
@@ -495,8 +519,7 @@ static int plan_dwpw(qph_net* net) {
     f.bp = q.bias >= 0 ? net->weights[q.bias] : nullptr;
     f.m = q.ws[0];
     // the 1x1 path's bias-placement rule (as conv_dispatch picks it)
-    const double fl = (double)f.m * (double)(f.oh * f.ow) * (double)f.c;
-    f.seed_rule = (f.n > 1 || fl < 2e5 || (f.oh * f.ow + 31) / 32 >= 2) ? 0 : 1;
+    f.seed_rule = pw_seed_rule(f.n, f.m, f.oh * f.ow, f.c);
     f.act_p = make_act(&q.act);
     f.trans_out = q.trans_out || net->cl_out[i + 1];
     f.y = net->tptr[q.out];
@@ -713,7 +736,12 @@ static int run_all(qph_net* net) {
     if (net->profiling) QPH_TRY_HIP(hipEventRecord(net->ev[i], s));
     size_t step = 1;
     if (net->group_len[i] > 1) {
-      QPH_TRY(launch_dense_conv_group(&net->plan[i], net->group_len[i], s));
+      ConvArgs grp[4];
+      for (int k = 0; k < net->group_len[i] && k < 4; k++) {
+        grp[k] = net->plan[i + (size_t)k];
+        grp[k].n = net->real_n;
+      }
+      QPH_TRY(launch_dense_conv_group(grp, net->group_len[i], s));
       step = (size_t)net->group_len[i];
     } else if (net->head[i]) {
       const qph_node& q = net->nodes[i];
@@ -727,7 +755,10 @@ static int run_all(qph_net* net) {
       if (rc != QPH_OK) return fail(rc, node_name(i, q) + ": " + qph_last_error());
       step = 2;
     } else if (net->fused[i]) {
-      QPH_TRY(launch_dwpw(net->dwpw[i], s));
+      DwPwArgs f = net->dwpw[i];
+      f.n = net->real_n;
+      f.seed_rule = pw_seed_rule(f.n, f.m, f.oh * f.ow, f.c);
+      QPH_TRY(launch_dwpw(f, s));
       step = net->dwpw[i].stem ? 3 : 2;
     } else if (net->qa_fused[i]) {
       const qph_node& q = net->nodes[i];
@@ -750,11 +781,13 @@ static int run_all(qph_net* net) {
   return QPH_OK;
 }
 
-// Records the whole kernel sequence into a HIP graph (nothing executes).
-// Every launcher validates its arguments as it records, so a node that no
-// kernel takes fails here, at create time, naming the node.
+// Records the whole kernel sequence for the current real_n into a HIP
+// graph (nothing executes).  Every launcher validates its arguments as it
+// records, so a node that no kernel takes fails here, at create time (or
+// at the first run with a new real_n), naming the node.
 static int capture(qph_net* net) {
   hipStream_t s = net->ctx->stream;
+  const size_t r = (size_t)net->real_n;
   QPH_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
   int rc = run_all(net);
   hipGraph_t g = nullptr;
@@ -764,22 +797,57 @@ static int capture(qph_net* net) {
     return rc;
   }
   QPH_TRY_HIP(e);
-  e = hipGraphInstantiate(&net->exec, g, nullptr, nullptr, 0);
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
   if (e != hipSuccess) {
     (void)hipGraphDestroy(g);
     return hip_check(e, "hipGraphInstantiate");
   }
-  net->graph = g;
-  net->graph_ready = true;
+  net->graphs[r] = g;
+  net->execs[r] = x;
   return QPH_OK;
+}
+
+// The graph of the current real_n, captured on first use.
+static int launch_graph(qph_net* net) {
+  const size_t r = (size_t)net->real_n;
+  if (!net->execs[r]) QPH_TRY(capture(net));
+  QPH_TRY_HIP(hipGraphLaunch(net->execs[r], net->ctx->stream));
+  return QPH_OK;
+}
+
+// Batch-major tensors: the input, and every output of a node that reads a
+// batch-major tensor (each op maps batch item b of its inputs to batch
+// item b of its outputs).  A run over real_n items cuts their first
+// dimension to real_n; that is a batch cut only when the first dimension
+// is the batch, which real_n requires of every batch-major tensor.
+static void mark_batch_major(qph_net* net) {
+  const size_t nt = net->shapes_full.size() / 4;
+  net->batch_major.assign(nt, false);
+  net->batch_major[0] = true;
+  auto bm = [&](int32_t t) { return t >= 0 && (size_t)t < nt && net->batch_major[(size_t)t]; };
+  for (const qph_node& n : net->nodes) {
+    if (!(bm(n.in) || bm(n.in2) || bm(n.in3))) continue;
+    if (n.out >= 0 && (size_t)n.out < nt) net->batch_major[(size_t)n.out] = true;
+    if (n.out2 >= 0 && (size_t)n.out2 < nt) net->batch_major[(size_t)n.out2] = true;
+  }
+  for (size_t t = 0; t < nt; t++)
+    if (net->alias[t] >= 0 && (size_t)net->alias[t] < nt && net->batch_major[t])
+      net->batch_major[(size_t)net->alias[t]] = true;
+}
+
+static void set_eff_shapes(qph_net* net) {
+  net->shapes = net->shapes_full;
+  for (size_t t = 0; t < net->batch_major.size(); t++)
+    if (net->batch_major[t]) net->shapes[4 * t] = net->real_n;
 }
 
 static void release(qph_net* net) {
   if (!net) return;
   (void)hipStreamSynchronize(net->ctx->stream);
-  if (net->graph_ready) {
-    (void)hipGraphExecDestroy(net->exec);
-    (void)hipGraphDestroy(net->graph);
+  for (size_t r = 0; r < net->execs.size(); r++) {
+    if (net->execs[r]) (void)hipGraphExecDestroy(net->execs[r]);
+    if (net->graphs[r]) (void)hipGraphDestroy(net->graphs[r]);
   }
   for (auto e : net->ev) (void)hipEventDestroy(e);
   if (net->done) (void)hipEventDestroy(net->done);
@@ -823,14 +891,16 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
   net->ctx = ctx;
   net->arena = nullptr;
   net->arena_bytes = 0;
-  net->graph_ready = false;
   net->profiling = false;
   net->prof_runs = 0;
   net->in_stage = nullptr;
   net->done = nullptr;
   net->inflight = false;
   net->nodes.assign(spec->nodes, spec->nodes + spec->n_nodes);
-  net->shapes.assign(spec->shapes, spec->shapes + 4 * (size_t)spec->n_tensors);
+  net->shapes_full.assign(spec->shapes, spec->shapes + 4 * (size_t)spec->n_tensors);
+  net->shapes = net->shapes_full;
+  net->batch = net->shapes_full[0];
+  net->real_n = net->batch;
   net->alias.assign((size_t)spec->n_tensors, -1);
   if (spec->alias) net->alias.assign(spec->alias, spec->alias + spec->n_tensors);
   if (spec->n_outputs > 0 && spec->outputs)
@@ -859,6 +929,13 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
       return bail(QPH_EINVAL);
     }
   }
+  if (net->batch <= 0 || net->batch > (1 << 20)) {
+    fail(QPH_EINVAL, "net_create: input batch dimension out of range");
+    return bail(QPH_EINVAL);
+  }
+  mark_batch_major(net);
+  net->graphs.assign((size_t)net->batch + 1, nullptr);
+  net->execs.assign((size_t)net->batch + 1, nullptr);
   plan_fused_head(net, spec->flags);
   plan_pitch(net);
   plan_qkv_attention(net, spec->flags);
@@ -990,7 +1067,7 @@ QPH_API int qph_net_tensor(qph_net* net, int32_t id, float** dev_ptr, int64_t* n
   if (net->nostore[(size_t)id])
     return fail(QPH_EINVAL, "net_tensor: tensor is internal to a fused launch and never stored");
   if (dev_ptr) *dev_ptr = net->tptr[id];
-  if (numel) *numel = numel_of(net, id);
+  if (numel) *numel = numel_full(net, id);
   return QPH_OK;
 }
 
@@ -1039,6 +1116,40 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
   return QPH_OK;
 }
 
+QPH_API int qph_net_set_real_n(qph_net* net, int32_t real_n) {
+  if (!net) return fail(QPH_EINVAL, "net_set_real_n: NULL net");
+  if (real_n < 1 || real_n > net->batch)
+    return fail(QPH_EINVAL, "net_set_real_n: " + std::to_string(real_n) + " outside 1.." +
+                                std::to_string(net->batch));
+  if (net->inflight)
+    return fail(QPH_EINVAL, "net_set_real_n: the previous run of this net is not complete");
+  if (real_n == net->real_n) return QPH_OK;
+  for (size_t t = 0; t < net->batch_major.size(); t++)
+    if (net->batch_major[t] && net->shapes_full[4 * t] != net->batch)
+      return fail(QPH_EUNSUPPORTED, "net_set_real_n: tensor " + std::to_string(t) +
+                                        " does not keep the batch as its first dimension");
+  const int64_t prev = net->real_n;
+  net->real_n = real_n;
+  set_eff_shapes(net);
+  // capture now, so a failure names its node here and the first run with
+  // this count pays no capture time
+  const int rc = net->execs[(size_t)real_n] ? QPH_OK : capture(net);
+  if (rc != QPH_OK) {
+    const std::string msg = qph_last_error();
+    net->real_n = prev;
+    set_eff_shapes(net);
+    return fail(rc, msg);
+  }
+  return QPH_OK;
+}
+
+QPH_API int qph_net_real_n(qph_net* net, int32_t* real_n, int32_t* batch) {
+  if (!net) return fail(QPH_EINVAL, "net_real_n: NULL net");
+  if (real_n) *real_n = (int32_t)net->real_n;
+  if (batch) *batch = (int32_t)net->batch;
+  return QPH_OK;
+}
+
 QPH_API int qph_net_staging(qph_net* net, int32_t slot, float** host, int64_t* numel) {
   if (!net || !host) return fail(QPH_EINVAL, "net_staging: NULL argument");
   if (slot < -1 || slot >= (int32_t)net->outputs.size())
@@ -1049,11 +1160,11 @@ QPH_API int qph_net_staging(qph_net* net, int32_t slot, float** host, int64_t* n
   if (!buf) {
     QPH_TRY_HIP(hipSetDevice(net->ctx->device));
     void* p = nullptr;
-    QPH_TRY_HIP(hipHostMalloc(&p, (size_t)numel_of(net, id) * 4, hipHostMallocDefault));
+    QPH_TRY_HIP(hipHostMalloc(&p, (size_t)numel_full(net, id) * 4, hipHostMallocDefault));
     buf = (float*)p;
   }
   *host = buf;
-  if (numel) *numel = numel_of(net, id);
+  if (numel) *numel = numel_full(net, id);
   return QPH_OK;
 }
 
@@ -1074,8 +1185,7 @@ QPH_API int qph_net_run_async(qph_net* net, int32_t flags) {
   if (flags & QPH_RUN_UPLOAD)
     QPH_TRY_HIP(hipMemcpyAsync(net->tptr[0], net->in_stage, (size_t)numel_of(net, 0) * 4,
                                hipMemcpyHostToDevice, s));
-  if (!net->graph_ready) QPH_TRY(capture(net));
-  QPH_TRY_HIP(hipGraphLaunch(net->exec, s));
+  QPH_TRY(launch_graph(net));
   if (flags & QPH_RUN_DOWNLOAD)
     for (size_t o = 0; o < net->outputs.size(); o++) {
       const int32_t id = net->outputs[o];
@@ -1115,8 +1225,7 @@ QPH_API int qph_net_run(qph_net* net, const float* input, int32_t input_is_devic
     }
     net->prof_runs++;
   } else {
-    if (!net->graph_ready) QPH_TRY(capture(net));
-    QPH_TRY_HIP(hipGraphLaunch(net->exec, s));
+    QPH_TRY(launch_graph(net));
   }
   if (outputs_host) {
     for (size_t o = 0; o < net->outputs.size(); o++) {

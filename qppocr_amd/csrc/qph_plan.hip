@@ -469,7 +469,8 @@ __global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
 // co0 + 4 (r % 4) .. + 3).  Loads are inline asm, so the compiler adds no
 // waits of its own; the wait before group g's steps leaves the loads of
 // the groups after it outstanding (vmcnt counts in issue order).  A group's
-// buffer is refilled only after the MFMAs that read it were issued.
+// buffer is refilled only after every LDS read of it has returned (an
+// explicit lgkmcnt(0) ahead of the refill).
 constexpr int CONV_DMA_D = 4;
 
 template <int TAPS>
@@ -547,6 +548,10 @@ __global__ __launch_bounds__(64) void plan_conv_dma_kernel(ConvK p) {
   for (int g = 0; g < CONV_DMA_D - 1; g++)
     if (g < groups) issue(g);
   for (int g = 0; g < groups; g++) {
+    // the refill below lands in the buffer group g - 1 read: every LDS
+    // read of it must have returned first (lgkmcnt(0); one-wave workgroup,
+    // so no other wave reads it)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
     __asm__ volatile("" ::: "memory");
     if (g + CONV_DMA_D - 1 < groups) issue(g + CONV_DMA_D - 1);
     const int ahead = min(CONV_DMA_D - 1, groups - 1 - g);   // groups issued after g

@@ -88,6 +88,19 @@ using namespace qph;
 #define CTX_CHECK(ctx) \
   if (!(ctx)) return fail(QPH_EINVAL, "null context")
 
+// Fills `head` (< 16) bytes, `body16` 16-byte words and `tail` (< 16) bytes
+// with the byte of v4 (replicated four times).
+__global__ __launch_bounds__(256) void fill_bytes_kernel(unsigned char* head, size_t nhead,
+                                                         uint4* body, size_t body16,
+                                                         unsigned char* tail, size_t ntail,
+                                                         unsigned v4) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t k = i; k < body16; k += stride) body[k] = make_uint4(v4, v4, v4, v4);
+  if (i < nhead) head[i] = (unsigned char)v4;
+  if (i < ntail) tail[i] = (unsigned char)v4;
+}
+
 extern "C" {
 
 QPH_API const char* qph_last_error(void) { return g_last_error.c_str(); }
@@ -154,6 +167,13 @@ QPH_API int qph_ctx_set_stream(qph_ctx* ctx, void* stream) {
 
 QPH_API void* qph_ctx_stream(qph_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
 
+QPH_API int qph_ctx_scratch_bytes(qph_ctx* ctx, size_t* bytes) {
+  CTX_CHECK(ctx);
+  if (!bytes) return fail(QPH_EINVAL, "ctx_scratch_bytes: NULL argument");
+  *bytes = ctx->ws_bytes;
+  return QPH_OK;
+}
+
 QPH_API int qph_sync(qph_ctx* ctx) {
   CTX_CHECK(ctx);
   QPH_TRY_HIP(hipStreamSynchronize(ctx->stream));
@@ -190,7 +210,20 @@ QPH_API int qph_memcpy_d2h(qph_ctx* ctx, void* dst, const void* src, size_t byte
 
 QPH_API int qph_memset(qph_ctx* ctx, void* dst, int value, size_t bytes) {
   CTX_CHECK(ctx);
-  return hip_check(hipMemsetAsync(dst, value, bytes, ctx->stream), "hipMemsetAsync");
+  if (!bytes) return QPH_OK;
+  if (!dst) return fail(QPH_EINVAL, "memset: NULL destination");
+  // a fill kernel, not hipMemsetAsync: a caller may capture the context
+  // stream into a graph, and memset nodes are kept out of graphs
+  unsigned char* p = (unsigned char*)dst;
+  const size_t head = std::min(bytes, (size_t)((16 - (uintptr_t)p % 16) % 16));
+  const size_t body16 = (bytes - head) / 16;
+  const size_t tail = bytes - head - body16 * 16;
+  const unsigned b = (unsigned)value & 0xffu;
+  const size_t blocks = std::max<size_t>(1, std::min<size_t>((body16 + 255) / 256, 8192));
+  hipLaunchKernelGGL(fill_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, p, head,
+                     (uint4*)(p + head), body16, p + head + body16 * 16, tail,
+                     b | (b << 8) | (b << 16) | (b << 24));
+  return launch_check("fill_bytes_kernel");
 }
 
 // ------------------------------------------------------------------ conv

@@ -488,11 +488,36 @@ class HipSession:
         check(self.lib.qph_net_create(self.ctx, ctypes.byref(spec), warr, ctypes.byref(p)))
         self.net = p
 
+    @property
+    def batch(self):
+        """The input's batch dimension: the most batch items a run computes."""
+        return self.graph.lshapes[0][0]
+
+    @property
+    def real_n(self):
+        r, b = ctypes.c_int32(), ctypes.c_int32()
+        check(self.lib.qph_net_real_n(self.net, ctypes.byref(r), ctypes.byref(b)))
+        return r.value
+
+    def set_real_n(self, n):
+        """Real batch count of the runs that follow (the plan model's
+        params[0], qppocr-gpu/src/plan.rs:587-593): batch items past it are
+        neither uploaded, computed nor downloaded."""
+        check(self.lib.qph_net_set_real_n(self.net, int(n)))
+
     def run(self, x, outputs=True):
-        """x: numpy input (host) or a device pointer int; returns numpy outputs."""
+        """x: numpy input (host) or a device pointer int; returns numpy outputs.
+        A host input with fewer batch items than the net holds (a batch
+        padded to the session's grain) sets the real count to its length
+        first; outputs then hold the real items only."""
         if isinstance(x, np.ndarray):
             x = np.ascontiguousarray(x, dtype=np.float32)
-            assert x.size == self.graph.numel(0)
+            full = self.graph.lshapes[0]
+            if x.shape[1:] == tuple(full[1:]) and 1 <= x.shape[0] <= full[0]:
+                if x.shape[0] != self.real_n:
+                    self.set_real_n(x.shape[0])
+            else:
+                assert x.size == self.graph.numel(0)
             inp, is_dev = x.ctypes.data_as(ctypes.c_void_p), 0
         elif x is None:
             inp, is_dev = None, 1
@@ -501,7 +526,9 @@ class HipSession:
         outs = None
         optr = None
         if outputs:
-            outs = [np.empty(self.graph.lshapes[t], dtype=np.float32) for t in self.graph.outputs]
+            rn = self.real_n
+            outs = [np.empty((rn,) + tuple(self.graph.lshapes[t][1:]), dtype=np.float32)
+                    for t in self.graph.outputs]
             optr = (ctypes.c_void_p * len(outs))(*[o.ctypes.data_as(ctypes.c_void_p).value for o in outs])
         check(self.lib.qph_net_run(self.net, inp, is_dev, optr))
         return outs

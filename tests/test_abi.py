@@ -72,6 +72,8 @@ def test_null_context_is_an_error_not_a_crash(lib):
     assert lib.qph_pack_crops(None, 1, None, None, None, None, 48, 320, None) == -1
     assert lib.qph_plan_run(None, None, 1, None) == -1
     assert lib.qph_net_run(None, None, 0, None) == -1
+    assert lib.qph_net_set_real_n(None, 1) == -1
+    assert lib.qph_net_real_n(None, None, None) == -1
     assert lib.qph_net_destroy(None) == 0
     assert lib.qph_ctx_destroy(None) == 0
     out = P()

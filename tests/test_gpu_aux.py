@@ -247,3 +247,46 @@ def test_aux_ops_graph_replays_match_eager(gpu):
     finally:
         ops.check(lib.qph_ctx_set_stream(ctx, None))
         ops.close_context(ctx)
+
+
+def test_memset_fill_kernel_eager_and_captured(gpu):
+    """qph_memset fills exactly the bytes asked for (unaligned start and
+    length, the 16-byte body and both ends) with value & 0xff, eagerly and
+    when recorded into a captured graph (replayed three times with eager
+    work in between)."""
+    torch = gpu
+    import ctypes
+
+    from qppocr_amd import ops
+    lib = ops._lib.load()
+    ctx = ops.new_context(0)
+    st = torch.cuda.Stream()
+    ops.check(lib.qph_ctx_set_stream(ctx, ctypes.c_void_p(st.cuda_stream)))
+    try:
+        buf = torch.zeros(70000, dtype=torch.uint8, device="cuda")
+        base = buf.data_ptr()
+        for off, n, v in [(3, 1000, 0x1A5), (0, 64, 7), (5, 9, 255), (16, 65536, 0), (1, 1, 3)]:
+            print(f"memset off {off} bytes {n} value {v}", flush=True)
+            buf.fill_(0xEE)
+            torch.cuda.synchronize()
+            ops.check(lib.qph_memset(ctx, ctypes.c_void_p(base + off), v, n))
+            st.synchronize()
+            h = buf.cpu().numpy()
+            assert (h[off:off + n] == (v & 0xff)).all()
+            assert (h[:off] == 0xEE).all() and (h[off + n:] == 0xEE).all()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            ops.check(lib.qph_memset(ctx, ctypes.c_void_p(base + 7), 0x42, 33333))
+        for rep in range(3):
+            buf.fill_(0x11)
+            torch.cuda.synchronize()
+            with torch.cuda.stream(st):
+                g.replay()
+            st.synchronize()
+            h = buf.cpu().numpy()
+            assert (h[7:7 + 33333] == 0x42).all() and (h[:7] == 0x11).all(), rep
+            assert (h[7 + 33333:] == 0x11).all(), rep
+        del g
+    finally:
+        ops.check(lib.qph_ctx_set_stream(ctx, None))
+        ops.close_context(ctx)

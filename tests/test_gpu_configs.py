@@ -138,6 +138,126 @@ def test_rec_fused_head(gpu, oracle, batch, width):
     sess.close()
 
 
+def _d2h(sess, tid):
+    import ctypes
+    ptr, n = sess.tensor_ptr(tid)
+    host = np.empty(n, dtype=np.float32)
+    sess.sync()
+    assert sess.lib.qph_memcpy_d2h(sess.ctx, host.ctypes.data_as(ctypes.c_void_p),
+                                   ctypes.c_void_p(ptr), n * 4) == 0
+    return host
+
+
+def test_rec_real_n_padded_batch(gpu, oracle):
+    """A 64-row rec net run with real_n (the plan model's params[0],
+    qppocr-gpu/src/plan.rs:587-593; DeviceSession::batch_grain,
+    qppocr-core/src/device.rs:139-157): 37 real lines give the oracle's bits
+    for a 37-line batch, the 27 padded items are neither uploaded nor
+    computed (their input and output rows keep the previous full run's
+    contents), real_n = 1 gives the oracle's 1-line batch, and the 64-item
+    graph still gives its earlier bits afterwards."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    r = nets.WeightRng(3)
+    rw = nets.rec_weights(r)
+    x64 = r.uniform((64, 3, 48, 160), -1.0, 1.0)
+    x37 = r.uniform((37, 3, 48, 160), -1.0, 1.0)
+    g = nets.build_rec_graph(rw, 64, 160)
+    print("rec 64x3x48x160 net, full run then real_n 37 / 1 / 64", flush=True)
+    sess = nets.HipSession(g)
+    assert sess.batch == 64 and sess.real_n == 64
+    probs64, pairs64 = sess.run(x64)
+    probs, pairs = sess.run(x37)
+    assert sess.real_n == 37 and probs.shape[0] == 37 and pairs.shape[0] == 37
+    g37 = nets.build_rec_graph(rw, 37, 160)
+    probs_ref, pairs_ref = onets.run_graph(g37, x37)
+    assert_bitexact(probs, probs_ref, "real_n 37 probs")
+    assert (_ids(pairs) == _ids(pairs_ref)).all()
+    assert_bitexact(pairs[..., 0], pairs_ref[..., 0], "real_n 37 pair values")
+    # padded items untouched: input rows 37.. hold x64's, outputs the full run's
+    dev_in = _d2h(sess, 0).reshape(x64.shape)
+    assert_bitexact(dev_in[:37], x37, "uploaded real rows")
+    assert_bitexact(dev_in[37:], x64[37:], "padded input rows not uploaded")
+    dev_pairs = _d2h(sess, g.outputs[1]).reshape(pairs64.shape)
+    assert_bitexact(dev_pairs[37:], pairs64[37:], "padded pair rows not computed")
+    dev_probs = _d2h(sess, g.outputs[0]).reshape(probs64.shape)
+    assert_bitexact(dev_probs[37:], probs64[37:], "padded prob rows not computed")
+    probs1, pairs1 = sess.run(x37[:1])
+    g1 = nets.build_rec_graph(rw, 1, 160)
+    probs1_ref, pairs1_ref = onets.run_graph(g1, x37[:1])
+    assert_bitexact(probs1, probs1_ref, "real_n 1 probs")
+    assert (_ids(pairs1) == _ids(pairs1_ref)).all()
+    again64, _ = sess.run(x64)
+    assert_bitexact(again64, probs64, "64-item graph after real_n runs")
+    ref64 = onets.run_graph(g, x64)[0]
+    assert_bitexact(probs64, ref64, "full 64-item run")
+    sess.close()
+
+
+def test_rec_real_n_fused_head_and_refusals(gpu, oracle):
+    """The fused-head 64-row net at real_n 37 under the pairs tolerance rule
+    against the oracle's 37-line graph; out-of-range counts and a count
+    change while a deferred run is in flight are refused."""
+    from conftest import pairs_tolerance_check
+    from qppocr_amd import nets
+    from qppocr_amd._lib import QphError
+    from oracle import nets as onets
+    r = nets.WeightRng(5)
+    rw = nets.rec_weights(r)
+    x37 = r.uniform((37, 3, 48, 160), -1.0, 1.0)
+    g = nets.build_rec_graph(rw, 64, 160, fused_head=True)
+    print("rec 64x3x48x160 fused head, real_n 37", flush=True)
+    sess = nets.HipSession(g)
+    (pairs,) = sess.run(x37)
+    g37 = nets.build_rec_graph(rw, 37, 160, probs=False)
+    outs, T = onets.run_graph(g37, x37, keep=True)
+    pairs_tolerance_check(pairs, outs[0], T[g37.nodes[-2]["out"]])
+    for bad in (0, 65, -1):
+        with pytest.raises(QphError):
+            sess.set_real_n(bad)
+    assert sess.real_n == 37
+    xin = sess.staging(-1)
+    out = sess.staging(0)
+    xin[:37] = x37
+    sess.run_async()
+    with pytest.raises(QphError):
+        sess.set_real_n(12)
+    sess.complete()
+    assert_bitexact(out[:37], pairs, "deferred run at real_n 37")
+    sess.close()
+
+
+def test_cfg5_engine_batching(gpu, oracle):
+    """The mixed page's lines batched as the reference engine batches them
+    for a GPU session (width spans of 64, 64 lines a forward, widths rounded
+    to 64; engine.rs:1211-1290, 1413-1422) and run on 64-row nets with
+    real_n: every batch's pairs bit-exact with the oracle's graph of exactly
+    that batch, and the decoded lines equal to the oracle's collapse."""
+    from qppocr_amd import pipeline
+    from oracle import nets as onets
+    det_g, det_x, rw, lines, widths = pipeline.mixed_page(4, 1536, 128)
+    print("cfg5 engine batching: 128 lines on 64-row nets", flush=True)
+    page = pipeline.PageRunner(det_g, det_x, rw, lines, widths, engine=True)
+    assert all(len(idx) <= 64 and bw % 64 == 0 for bw, idx in page.plan)
+    page.upload()
+    page.run()
+    page.sync()
+    got = page.rec_pairs()
+    decoded = page.decode()
+    for bw, idx, g, sess, x in page.rec:
+        assert sess.batch == 64 and sess.real_n == len(idx)
+        print(f"engine rec batch {len(idx)}x{bw}", flush=True)
+        gb = pipeline.build_rec_graph(rw, len(idx), bw, pipeline.REC_H, probs=False)
+        pairs_ref = onets.run_graph(gb, x)[-1]
+        for b, i in enumerate(idx):
+            assert (_ids(got[i]) == _ids(pairs_ref[b])).all(), f"line {i}"
+            assert_bitexact(got[i][..., 0], pairs_ref[b][..., 0], f"line {i} values")
+            t_valid = int(widths[i]) // pipeline.REC_STRIDE
+            ref_ids, _ = oracle.ctc_collapse(pairs_ref[b][:t_valid], t_valid)
+            assert decoded[i][0] == [int(v) for v in ref_ids], f"line {i} ids"
+    page.close()
+
+
 def test_cfg5_mixed_page(gpu, oracle):
     """det 1536^2 + 128 rec lines in width buckets, CTC masked past w/8:
     det map and every batch's pairs bit-exact with the oracle, and each

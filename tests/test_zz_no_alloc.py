@@ -67,3 +67,35 @@ def test_conv2d_noalloc_refuses_oversize_weights(gpu):
                   ops.act(0), None)
     assert rc == -3 and b"fixed device array" in lib.qph_last_error()
     assert 512 * 9 * 512 > _lib.NOALLOC_WK_FLOATS
+
+
+def test_conv2d_noalloc_allocates_nothing(gpu):
+    """On a fresh context, qph_conv2d_noalloc called before any qph_conv2d
+    leaves the context's hipMalloc-grown scratch at 0 bytes (so it cannot
+    have fallen back to it), and still matches qph_conv2d bit for bit; the
+    qph_conv2d call that follows does grow the scratch (the query sees it)."""
+    torch = gpu
+    from qppocr_amd import _lib, ops
+    lib = _lib.load()
+    ctx = ops.new_context(0)
+    try:
+        def scratch():
+            v = ctypes.c_size_t()
+            assert lib.qph_ctx_scratch_bytes(ctx, ctypes.byref(v)) == 0
+            return v.value
+        rng = np.random.default_rng(72)
+        x = torch.from_numpy(rng.standard_normal((1, 48, 36, 40)).astype(np.float32)).cuda()
+        wt = torch.from_numpy(rng.standard_normal((64, 48, 3, 3)).astype(np.float32)).cuda()
+        b = torch.from_numpy(rng.standard_normal(64).astype(np.float32)).cuda()
+        params = ops.conv_params(1, 1, 1, 1)
+        print("noalloc on a fresh context: dense 3x3 48->64 36x40", flush=True)
+        assert scratch() == 0
+        rc2, y2 = _call(lib, "qph_conv2d_noalloc", ctx, torch, x, wt, b, params, ops.act(2), None)
+        assert rc2 == 0, lib.qph_last_error()
+        assert scratch() == 0
+        rc1, y1 = _call(lib, "qph_conv2d", ctx, torch, x, wt, b, params, ops.act(2), None)
+        assert rc1 == 0, lib.qph_last_error()
+        assert scratch() > 0
+        assert_bitexact(y2.cpu().numpy(), y1.cpu().numpy(), "noalloc on a fresh context")
+    finally:
+        ops.close_context(ctx)
