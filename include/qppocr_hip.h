@@ -487,11 +487,17 @@ typedef struct qph_plan qph_plan;
  * the id, or QPH_EUNSUPPORTED for a kernel outside the set (the Metal-only
  * n_conv8_mma*, n_conv8h, n_conv_dw_tile, n_convt4w, n_head_argmax). */
 QPH_API int qph_plan_kernel_id(const char* name);
-/* The session's load step (vulkan/session.rs): allocates the arena,
- * writes the uploads, decodes every parameter block (refusing regions
- * outside the arena, unknown kernels and malformed blocks with the
- * dispatch's index) and captures the launches into a HIP graph. */
+/* The session's load step (vulkan/session.rs): decodes every parameter
+ * block on the host first (refusing regions outside the arena, unknown
+ * kernels and malformed blocks with the dispatch's index, before any device
+ * call), then allocates the arena, writes the uploads and captures the
+ * launches into a HIP graph. */
 QPH_API int qph_plan_create(qph_ctx* ctx, const qph_plan_spec* spec, qph_plan** out);
+/* The checks of qph_plan_create alone, on the host: no context and no
+ * device are needed (QPH_OK, or the error qph_plan_create would return for
+ * a malformed plan).  No counterpart in the reference, whose load step
+ * builds the device objects as it goes; for loaders that vet a plan first. */
+QPH_API int qph_plan_validate(const qph_plan_spec* spec);
 QPH_API int qph_plan_destroy(qph_plan* plan);
 /* real_n for the following runs (0 = every batch row): the reference's run
  * writes it to word 0 before each submit. */

@@ -7,7 +7,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libqppocr_hip.so")
+# QPPOCR_HIP_LIB names another build of the same library (the host-code
+# sanitizer build, for CPU runs of the host-side checks)
+LIB_PATH = os.environ.get("QPPOCR_HIP_LIB") or os.path.join(HERE, "libqppocr_hip.so")
 
 QPH_OK = 0
 ACT_NONE, ACT_GELU, ACT_RELU, ACT_HARDSWISH, ACT_SIGMOID = 0, 1, 2, 3, 4
@@ -135,6 +137,7 @@ SIGNATURES = {
     "qph_net_plan": ([P, P, P, P, I32, P], ctypes.c_int),
     "qph_plan_kernel_id": ([ctypes.c_char_p], ctypes.c_int),
     "qph_plan_create": ([P, ctypes.POINTER(PlanSpec), ctypes.POINTER(P)], ctypes.c_int),
+    "qph_plan_validate": ([ctypes.POINTER(PlanSpec)], ctypes.c_int),
     "qph_plan_destroy": ([P], ctypes.c_int),
     "qph_plan_set_real_n": ([P, ctypes.c_uint32], ctypes.c_int),
     "qph_plan_run": ([P, P, I32, P], ctypes.c_int),

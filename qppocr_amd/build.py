@@ -34,9 +34,16 @@ CFLAGS = [
 ]
 
 
-def _compile(src):
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC] + CFLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+# host-code sanitizers only (the device code is built as usual): each
+# -fsanitize= goes to the host compilation alone
+SANITIZE = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host",
+            "-fno-omit-frame-pointer"]
+
+
+def _compile(src, build_dir=None, extra=()):
+    obj = os.path.join(build_dir or BUILD, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC] + CFLAGS + list(extra) + ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
@@ -46,27 +53,37 @@ def _compile(src):
     return obj
 
 
-def build(verbose=False):
-    os.makedirs(BUILD, exist_ok=True)
+def build(verbose=False, sanitize=False):
+    """sanitize: a host-code ASan + UBSan build into _build/sanitize/ (for CPU
+    runs of the host-side checks under LD_PRELOAD of the ASan runtime, with
+    QPPOCR_HIP_LIB pointing at it); the product library is not touched."""
+    bdir = os.path.join(BUILD, "sanitize") if sanitize else BUILD
+    lib = os.path.join(bdir, "libqppocr_hip.so") if sanitize else LIB
+    extra = SANITIZE if sanitize else []
+    os.makedirs(bdir, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda src: _compile(src, bdir, extra), SOURCES))
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
+    if sanitize:   # host code only: no GPU sanitizer on the link either
+        cmd[1:1] = ["-fno-gpu-sanitize", "-fsanitize=address", "-fsanitize=undefined", "-shared-libsan"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
     # every symbol must resolve (a kernel whose host stub was dropped shows
-    # up here, not at the first launch)
-    try:
-        ctypes.CDLL(os.path.abspath(tmp), mode=os.RTLD_NOW)
-    except OSError as e:
-        os.remove(tmp)
-        raise RuntimeError(f"built library does not load: {e}")
-    os.replace(tmp, LIB)
+    # up here, not at the first launch); a sanitizer build needs its runtime
+    # preloaded to load, so it is not loaded here
+    if not sanitize:
+        try:
+            ctypes.CDLL(os.path.abspath(tmp), mode=os.RTLD_NOW)
+        except OSError as e:
+            os.remove(tmp)
+            raise RuntimeError(f"built library does not load: {e}")
+    os.replace(tmp, lib)
     if verbose:
-        print("built", LIB)
-    return LIB
+        print("built", lib)
+    return lib
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, sanitize="--sanitize" in sys.argv[1:])

@@ -835,6 +835,10 @@ namespace {
 
 struct Decoder {
   qph_plan* pl;
+  // dry: validation only (qph_plan_validate, and qph_plan_create before it
+  // touches the device): no device memory, nothing copied or launched; the
+  // launches recorded into pl are discarded
+  bool dry = false;
   std::vector<PlanUpload> ups;  // sorted by offset
   int idx = 0;
   const char* kname = "";
@@ -900,7 +904,12 @@ struct Decoder {
       return fail(QPH_EINVAL, where() + ": " + what + " not 16-byte aligned");
     return QPH_OK;
   }
-  float* at(uint32_t off) const { return pl->arena + off; }
+  // device address of word off (in a dry pass: of an arena based at 256,
+  // so alignment tests see what the real 256-byte aligned arena gives)
+  float* at(uint32_t off) const {
+    const uintptr_t base = dry ? (uintptr_t)256 : (uintptr_t)pl->arena;
+    return (float*)(base + (uintptr_t)off * 4);
+  }
 };
 
 // Word counts of the parameter blocks (the n_*.comp layouts; n_concat_c has
@@ -1077,9 +1086,11 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
         // the session's linear kernel: the weight held transposed ([N][K],
         // k contiguous), made once here on the plan's stream
         float* wt_t = nullptr;
-        QPH_TRY_HIP(hipMalloc((void**)&wt_t, (size_t)N * cin * 4));
-        d.pl->owned.push_back(wt_t);
-        QPH_TRY(launch_transpose(wt, cin, N, wt_t, d.pl->ctx->stream));
+        if (!d.dry) {
+          QPH_TRY_HIP(hipMalloc((void**)&wt_t, (size_t)N * cin * 4));
+          d.pl->owned.push_back(wt_t);
+          QPH_TRY(launch_transpose(wt, cin, N, wt_t, d.pl->ctx->stream));
+        }
         LinArgs la{};
         la.a = x; la.lda = cin; la.wt = wt_t; la.c = d.at(e.y);
         la.m = nb * P; la.n = N; la.k = cin;
@@ -1532,9 +1543,73 @@ int capture_plan(qph_plan* pl) {
   return QPH_OK;
 }
 
+// The spec's checks that need no device, its uploads sorted into d.ups.
+int check_spec(const qph_plan_spec* spec, Decoder& d) {
+  if (spec->total_words < 1 || spec->n_dispatches < 1 || spec->n_uploads < 0 ||
+      (spec->n_uploads && !spec->uploads) || !spec->dispatches || spec->n_outputs < 1 ||
+      !spec->out_offs || !spec->out_numel || spec->in_numel < 1)
+    return fail(QPH_EINVAL, "plan_create: empty plan");
+  if ((uint64_t)spec->in_f32_off + (uint64_t)spec->in_numel > spec->total_words)
+    return fail(QPH_EINVAL, "plan_create: the input region is outside the arena");
+  for (int32_t o = 0; o < spec->n_outputs; o++)
+    if (spec->out_numel[o] < 1 ||
+        (uint64_t)spec->out_offs[o] + (uint64_t)spec->out_numel[o] > spec->total_words)
+      return fail(QPH_EINVAL, "plan_create: output " + std::to_string(o) + " is outside the arena");
+  for (int32_t u = 0; u < spec->n_uploads; u++) {
+    const qph_plan_upload& up = spec->uploads[u];
+    if (up.n_words == 0) continue;
+    if (!up.words || (uint64_t)up.off + up.n_words > spec->total_words)
+      return fail(QPH_EINVAL, "plan_create: upload " + std::to_string(u) + " is outside the arena");
+    d.ups.push_back({up.off, up.n_words, up.words});
+  }
+  std::sort(d.ups.begin(), d.ups.end(),
+            [](const PlanUpload& a, const PlanUpload& b) { return a.off < b.off; });
+  for (size_t u = 1; u < d.ups.size(); u++)
+    if ((uint64_t)d.ups[u - 1].off + d.ups[u - 1].n > d.ups[u].off)
+      return fail(QPH_EINVAL, "plan_create: uploads overlap");
+  return QPH_OK;
+}
+
+// Decodes every dispatch of the spec into launches on d.pl (consumer
+// folding included); every parameter block and region is checked here.
+int decode_all(Decoder& d, const qph_plan_spec* spec) {
+  d.disp = spec->dispatches;
+  d.n_disp = spec->n_dispatches;
+  d.wr.assign((size_t)d.n_disp, OFF_NONE);
+  d.rd.assign((size_t)d.n_disp, {});
+  d.skip.assign((size_t)d.n_disp, 0);
+  d.outs.assign(spec->out_offs, spec->out_offs + spec->n_outputs);
+  for (int32_t i = 0; i < d.n_disp; i++) dispatch_io(d, d.disp[i], &d.wr[i], &d.rd[i]);
+  std::vector<PendingHw> pending;
+  for (int32_t i = 0; i < spec->n_dispatches; i++) {
+    const qph_plan_dispatch& q = spec->dispatches[i];
+    if (d.skip[i]) continue;  // taken into an earlier dispatch's launch
+    d.idx = i;
+    d.kname = (q.kernel >= 0 && q.kernel < kNumPlanKernels) ? kPlanKernels[q.kernel] : "?";
+    d.p_off = q.p_off;
+    QPH_TRY(decode(d, q, pending));
+  }
+  if (!pending.empty())
+    return fail(QPH_EUNSUPPORTED, "plan_create: an n_reduce_hw without its n_reduce_fin");
+  return QPH_OK;
+}
+
+// A dry decode: no context, no device.
+int validate_plan(const qph_plan_spec* spec) {
+  Decoder d;
+  QPH_TRY(check_spec(spec, d));
+  qph_plan tmp{};
+  tmp.ctx = nullptr;
+  tmp.arena = nullptr;
+  tmp.total_words = spec->total_words;
+  d.pl = &tmp;
+  d.dry = true;
+  return decode_all(d, spec);
+}
+
 void release_plan(qph_plan* pl) {
   if (!pl) return;
-  (void)hipStreamSynchronize(pl->ctx->stream);
+  if (pl->ctx) (void)hipStreamSynchronize(pl->ctx->stream);
   if (pl->graph_ready) {
     (void)hipGraphExecDestroy(pl->exec);
     (void)hipGraphDestroy(pl->graph);
@@ -1558,32 +1633,18 @@ QPH_API int qph_plan_kernel_id(const char* name) {
   return fail(QPH_EUNSUPPORTED, std::string("plan kernel ") + name + " is not in the HIP kernel set");
 }
 
+QPH_API int qph_plan_validate(const qph_plan_spec* spec) {
+  if (!spec) return fail(QPH_EINVAL, "plan_validate: NULL argument");
+  return validate_plan(spec);
+}
+
 QPH_API int qph_plan_create(qph_ctx* ctx, const qph_plan_spec* spec, qph_plan** out) {
   if (!ctx || !spec || !out) return fail(QPH_EINVAL, "plan_create: NULL argument");
   *out = nullptr;
-  if (spec->total_words < 1 || spec->n_dispatches < 1 || spec->n_uploads < 0 ||
-      (spec->n_uploads && !spec->uploads) || !spec->dispatches || spec->n_outputs < 1 ||
-      !spec->out_offs || !spec->out_numel || spec->in_numel < 1)
-    return fail(QPH_EINVAL, "plan_create: empty plan");
-  if ((uint64_t)spec->in_f32_off + (uint64_t)spec->in_numel > spec->total_words)
-    return fail(QPH_EINVAL, "plan_create: the input region is outside the arena");
-  for (int32_t o = 0; o < spec->n_outputs; o++)
-    if (spec->out_numel[o] < 1 ||
-        (uint64_t)spec->out_offs[o] + (uint64_t)spec->out_numel[o] > spec->total_words)
-      return fail(QPH_EINVAL, "plan_create: output " + std::to_string(o) + " is outside the arena");
+  // every block and region is checked before anything touches the device
+  QPH_TRY(validate_plan(spec));
   Decoder d;
-  for (int32_t u = 0; u < spec->n_uploads; u++) {
-    const qph_plan_upload& up = spec->uploads[u];
-    if (up.n_words == 0) continue;
-    if (!up.words || (uint64_t)up.off + up.n_words > spec->total_words)
-      return fail(QPH_EINVAL, "plan_create: upload " + std::to_string(u) + " is outside the arena");
-    d.ups.push_back({up.off, up.n_words, up.words});
-  }
-  std::sort(d.ups.begin(), d.ups.end(),
-            [](const PlanUpload& a, const PlanUpload& b) { return a.off < b.off; });
-  for (size_t u = 1; u < d.ups.size(); u++)
-    if ((uint64_t)d.ups[u - 1].off + d.ups[u - 1].n > d.ups[u].off)
-      return fail(QPH_EINVAL, "plan_create: uploads overlap");
+  QPH_TRY(check_spec(spec, d));
 
   qph_plan* pl = new qph_plan();
   pl->ctx = ctx;
@@ -1611,25 +1672,8 @@ QPH_API int qph_plan_create(qph_ctx* ctx, const qph_plan_spec* spec, qph_plan** 
                    "hipMemcpy(plan upload)");
     if (rc) return bail(rc);
   }
-  d.disp = spec->dispatches;
-  d.n_disp = spec->n_dispatches;
-  d.wr.assign((size_t)d.n_disp, OFF_NONE);
-  d.rd.assign((size_t)d.n_disp, {});
-  d.skip.assign((size_t)d.n_disp, 0);
-  d.outs.assign(spec->out_offs, spec->out_offs + spec->n_outputs);
-  for (int32_t i = 0; i < d.n_disp; i++) dispatch_io(d, d.disp[i], &d.wr[i], &d.rd[i]);
-  std::vector<PendingHw> pending;
-  for (int32_t i = 0; i < spec->n_dispatches; i++) {
-    const qph_plan_dispatch& q = spec->dispatches[i];
-    if (d.skip[i]) continue;  // taken into an earlier dispatch's launch
-    d.idx = i;
-    d.kname = (q.kernel >= 0 && q.kernel < kNumPlanKernels) ? kPlanKernels[q.kernel] : "?";
-    d.p_off = q.p_off;
-    rc = decode(d, q, pending);
-    if (rc) return bail(rc);
-  }
-  if (!pending.empty())
-    return bail(fail(QPH_EUNSUPPORTED, "plan_create: an n_reduce_hw without its n_reduce_fin"));
+  rc = decode_all(d, spec);
+  if (rc) return bail(rc);
   rc = capture_plan(pl);
   if (rc) return bail(rc);
   *out = pl;

@@ -416,6 +416,42 @@ def build_plan(graph):
     return PlanWriter(graph).build()
 
 
+def plan_spec(plan, lib=None):
+    """The qph_plan_spec of a GraphPlan and the buffers it points into (keep
+    both alive while the spec is used)."""
+    lib = lib or _lib.load()
+    ups = [(off, np.ascontiguousarray(w, dtype=np.uint32)) for off, w in plan.uploads]
+    uarr = (_lib.PlanUpload * len(ups))()
+    for i, (off, w) in enumerate(ups):
+        uarr[i].off = off
+        uarr[i].n_words = w.size
+        uarr[i].words = w.ctypes.data_as(ctypes.c_void_p)
+    darr = (_lib.PlanDispatch * len(plan.dispatches))()
+    for i, (name, p_off, groups, _) in enumerate(plan.dispatches):
+        kid = lib.qph_plan_kernel_id(name.encode())
+        if kid < 0:
+            check(kid)
+        darr[i].kernel = kid
+        darr[i].p_off = p_off
+        for j in range(3):
+            darr[i].groups[j] = groups[j]
+    offs = (ctypes.c_uint32 * len(plan.outputs))(*[o[0] for o in plan.outputs])
+    nums = (ctypes.c_int64 * len(plan.outputs))(*[o[1] for o in plan.outputs])
+    spec = _lib.PlanSpec(plan.total_words, len(ups), uarr, len(plan.dispatches), darr,
+                         plan.in_f32_off, int(np.prod(plan.in_shape)), len(plan.outputs), offs,
+                         nums)
+    return spec, (ups, uarr, darr, offs, nums)
+
+
+def validate_plan(plan):
+    """qph_plan_validate: every check of the load step, on the host (raises
+    QphError naming the dispatch for a malformed plan)."""
+    lib = _lib.load()
+    spec, keep = plan_spec(plan, lib)
+    check(lib.qph_plan_validate(ctypes.byref(spec)))
+    del keep
+
+
 class HipPlanSession:
     """A session over a GraphPlan: the reference's Vulkan / Metal session load
     and run steps (vulkan/session.rs) on the HIP kernel set (qph_plan_*)."""
@@ -425,27 +461,7 @@ class HipPlanSession:
         self.lib = _lib.load()
         self.ctx = ctx if ctx is not None else ops.context(device)
         self.plan = plan
-        ups = [(off, np.ascontiguousarray(w, dtype=np.uint32)) for off, w in plan.uploads]
-        self._keep = ups
-        uarr = (_lib.PlanUpload * len(ups))()
-        for i, (off, w) in enumerate(ups):
-            uarr[i].off = off
-            uarr[i].n_words = w.size
-            uarr[i].words = w.ctypes.data_as(ctypes.c_void_p)
-        darr = (_lib.PlanDispatch * len(plan.dispatches))()
-        for i, (name, p_off, groups, _) in enumerate(plan.dispatches):
-            kid = self.lib.qph_plan_kernel_id(name.encode())
-            if kid < 0:
-                check(kid)
-            darr[i].kernel = kid
-            darr[i].p_off = p_off
-            for j in range(3):
-                darr[i].groups[j] = groups[j]
-        offs = (ctypes.c_uint32 * len(plan.outputs))(*[o[0] for o in plan.outputs])
-        nums = (ctypes.c_int64 * len(plan.outputs))(*[o[1] for o in plan.outputs])
-        spec = _lib.PlanSpec(plan.total_words, len(ups), uarr, len(plan.dispatches), darr,
-                             plan.in_f32_off, int(np.prod(plan.in_shape)), len(plan.outputs), offs,
-                             nums)
+        spec, self._keep = plan_spec(plan, self.lib)
         p = ctypes.c_void_p()
         check(self.lib.qph_plan_create(self.ctx, ctypes.byref(spec), ctypes.byref(p)))
         self.handle = p

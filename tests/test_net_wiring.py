@@ -1,0 +1,180 @@
+"""The det and rec graphs' wiring, pinned independently of qppocr_amd/nets.py.
+
+The GPU sessions and the CPU oracle both consume the node list nets.py
+builds, so a wiring mistake there (FPN order, a residual source, pre-LN
+placement, the QKV head split) would pass every parity test.  Here a plain
+torch float64 forward of each architecture, written from the workload
+description alone (det: stem, 11 dw+pw blocks, FPN with 1x1 laterals, nearest
+2x top-down adds, 3x3 smoothing, upsample + concat, DB head; rec: stem, 4
+dw+pw blocks, two pre-LN encoder blocks, head + softmax), consumes the weight
+list in its documented creation order and must agree with the oracle running
+nets.py's graph.  Variants of the f64 forward with one plausible wiring
+mistake each must disagree, so the comparison can see such mistakes.
+CPU only."""
+import math
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+F = torch.nn.functional
+
+HS_ALPHA, HS_BETA = 1.0 / 6.0, 0.5
+
+
+def _t(a):
+    return torch.from_numpy(np.asarray(a, dtype=np.float64))
+
+
+def _hswish(x):
+    return x * torch.clamp(x * HS_ALPHA + HS_BETA, 0.0, 1.0)
+
+
+def _conv(x, w, b, stride=1, pad=(0, 0, 0, 0), groups=1):
+    """pad = (top, left, bottom, right)."""
+    x = F.pad(x, (pad[1], pad[3], pad[0], pad[2]))
+    return F.conv2d(x, _t(w), _t(b), stride=stride, groups=groups)
+
+
+DET_BLOCKS = [(3, 2, 16, 32), (3, 1, 32, 32), (3, 2, 32, 64), (3, 1, 64, 64), (3, 2, 64, 128),
+              (3, 1, 128, 128), (3, 1, 128, 128), (5, 1, 128, 128), (5, 1, 128, 128),
+              (5, 1, 128, 128), (3, 2, 128, 256)]
+
+
+def det_f64(weights, x, mistake=None):
+    """Det forward: stem conv3x3 s2 3->16 + hardswish; blocks 2..12 = dw(k, s,
+    pad k/2) + hardswish -> 1x1 + hardswish; C2..C5 = outputs of blocks 3, 5,
+    11, 12; laterals 1x1 -> 96 (made in the order C5, C4, C3, C2), in_k =
+    lateral_k + nearest-2x(in_{k+1}); smoothing 3x3 96->24 of in5, in4, in3,
+    in2, each upsampled to the C2 size and concatenated in that order; head
+    conv3x3 96->24 + ReLU, ConvT 2x2 s2 24->24, ConvT 2x2 s2 24->1 (no bias),
+    sigmoid."""
+    it = iter(weights)
+    w = lambda: next(it)  # noqa: E731
+    h = _hswish(_conv(_t(x), w(), w(), 2, (1, 1, 1, 1)))
+    feats = {}
+    for bi, (k, s, cin, cout) in enumerate(DET_BLOCKS, start=2):
+        h = _hswish(_conv(h, w(), w(), s, (k // 2,) * 4, groups=cin))
+        h = _hswish(_conv(h, w(), w()))
+        feats[bi] = h
+    c2, c3, c4, c5 = feats[3], feats[5], feats[11], feats[12]
+    up = lambda t, f: t.repeat_interleave(f, 2).repeat_interleave(f, 3)  # noqa: E731
+    in5 = _conv(c5, w(), w())
+    in4 = _conv(c4, w(), w()) + up(in5, 2)
+    in3 = _conv(c3, w(), w()) + up(in4, 2)
+    if mistake == "lateral_residual":
+        in2 = _conv(c2, w(), w()) + up(in4, 4)     # adds the wrong coarse map
+    else:
+        in2 = _conv(c2, w(), w()) + up(in3, 2)
+    p = []
+    for src, f in [(in5, 8), (in4, 4), (in3, 2), (in2, 1)]:
+        p.append(up(_conv(src, w(), w(), 1, (1, 1, 1, 1)), f))
+    if mistake == "concat_order":
+        p = p[::-1]
+    fuse = torch.cat(p, 1)
+    hh = torch.relu(_conv(fuse, w(), w(), 1, (1, 1, 1, 1)))
+    t1 = F.conv_transpose2d(hh, _t(w()), stride=2)
+    t2 = F.conv_transpose2d(t1, _t(w()), stride=2)
+    return torch.sigmoid(t2)
+
+
+REC_BLOCKS = [((2, 2), (1, 1, 1, 1), 32), ((2, 2), (1, 1, 1, 1), 64), ((2, 1), (1, 1, 1, 1), 128),
+              ((3, 1), (0, 1, 0, 1), 256)]
+
+
+def _ln(x, g, b, eps=1e-6):
+    mu = x.mean(-1, keepdim=True)
+    var = ((x - mu) ** 2).mean(-1, keepdim=True)
+    return (x - mu) / torch.sqrt(var + eps) * _t(g) + _t(b)
+
+
+def rec_f64(weights, x, heads=8, dh=32, mistake=None):
+    """Rec forward: stem conv3x3 s2 3->32 + hardswish; dw+pw blocks (dw
+    strides (2,2), (2,2), (2,1), (3,1), the last padded (0,1)) with
+    hardswish after each conv; [B, 256, 1, T] -> [B, T, 256]; two pre-LN
+    encoder blocks: x += proj(attention(LN1(x))), x += W2 gelu(W1 LN2(x))
+    (8 heads of 32, q scaled by 1/sqrt(32), QKV columns ordered (3, heads,
+    dh), erf GELU); head linear 256 -> 18709, softmax.  Returns (logits,
+    probs)."""
+    it = iter(weights)
+    w = lambda: next(it)  # noqa: E731
+    h = _hswish(_conv(_t(x), w(), w(), 2, (1, 1, 1, 1)))
+    for st, pad, cin in REC_BLOCKS:
+        h = _hswish(_conv(h, w(), w(), st, pad, groups=cin))
+        h = _hswish(_conv(h, w(), w()))
+    bsz, c, one, t = h.shape
+    assert one == 1
+    x = h.reshape(bsz, c, t).transpose(1, 2)
+    for _ in range(2):
+        g1, b1, wq, bq, wo, bo, g2, b2, w1, bm1, w2, bm2 = (w() for _ in range(12))
+        a_in = x if mistake == "post_ln" else _ln(x, g1, b1)
+        qkv = a_in @ _t(wq) + _t(bq)
+        if mistake == "head_split":
+            qkv = qkv.reshape(bsz, t, heads, 3, dh).permute(3, 0, 2, 1, 4)
+        else:
+            qkv = qkv.reshape(bsz, t, 3, heads, dh).permute(2, 0, 3, 1, 4)
+        q, k, v = qkv[0] * (1.0 / math.sqrt(dh)), qkv[1], qkv[2]
+        att = torch.softmax(q @ k.transpose(-1, -2), -1) @ v
+        att = att.transpose(1, 2).reshape(bsz, t, heads * dh)
+        x = x + att @ _t(wo) + _t(bo)
+        if mistake == "post_ln":
+            x = _ln(x, g1, b1)
+        m_in = _ln(x, g2, b2)
+        mm = m_in @ _t(w1) + _t(bm1)
+        mm = 0.5 * mm * (1.0 + torch.erf(mm / math.sqrt(2.0)))
+        x = (m_in if mistake == "mlp_residual" else x) + mm @ _t(w2) + _t(bm2)
+    logits = x @ _t(w()) + _t(w())
+    return logits, torch.softmax(logits, -1)
+
+
+def _close(got, ref, rel):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max()) <= rel * max(1.0, float(np.abs(ref).max()))
+
+
+@pytest.fixture(scope="module")
+def det_case(oracle):
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    g, x = nets.build_det(2, 96, 64)
+    return g, x, onets.run_graph(g, x)[0]
+
+
+@pytest.fixture(scope="module")
+def rec_case(oracle):
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    g, x = nets.build_rec(3, 2, 96)
+    outs, T = onets.run_graph(g, x, keep=True)
+    return g, x, T[g.nodes[-2]["out"]], outs[0]
+
+
+def test_det_graph_matches_independent_f64_forward(det_case):
+    g, x, got = det_case
+    ref = det_f64(g.weights, x).numpy()
+    assert got.shape == ref.shape == (1, 1, 96, 64)
+    assert _close(got, ref, 1e-5), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("mistake", ["lateral_residual", "concat_order"])
+def test_det_f64_forward_sees_wiring_mistakes(det_case, mistake):
+    g, x, got = det_case
+    wrong = det_f64(g.weights, x, mistake).numpy()
+    assert not _close(got, wrong, 1e-3)
+
+
+def test_rec_graph_matches_independent_f64_forward(rec_case):
+    g, x, logits, probs = rec_case
+    ref_logits, ref_probs = rec_f64(g.weights, x)
+    assert logits.reshape(ref_logits.shape).shape == (2, 12, 18709)
+    assert _close(logits.reshape(ref_logits.shape), ref_logits.numpy(), 1e-5)
+    # f32 exp1 (relative error < 1e-5) against f64 exp
+    assert np.abs(probs.reshape(ref_probs.shape) - ref_probs.numpy()).max() < 1e-5
+
+
+@pytest.mark.parametrize("mistake", ["post_ln", "head_split", "mlp_residual"])
+def test_rec_f64_forward_sees_wiring_mistakes(rec_case, mistake):
+    g, x, logits, _ = rec_case
+    wrong, _ = rec_f64(g.weights, x, mistake=mistake)
+    assert not _close(logits.reshape(wrong.shape), wrong.numpy(), 1e-3)

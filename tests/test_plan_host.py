@@ -130,3 +130,98 @@ def test_kernel_set_names(lib):
     assert all(i >= 0 for i in ids) and len(set(ids)) == len(ids) == 20
     for n in (b"n_conv8_mma", b"n_conv8h", b"n_head_argmax", b"n_convt4w", b"n_conv_dw_tile"):
         assert lib.qph_plan_kernel_id(n) < 0
+
+
+# ------------------------------------------------------ host-side validation
+
+class _Plan:
+    """A small hand-built GraphPlan (word 0 = real_n, a 4-word input)."""
+
+    def __init__(self):
+        self.p = plan.GraphPlan()
+        self.words = 0
+        self.static(np.array([0], np.uint32))
+        self.p.in_f32_off = self.alloc(4)
+        self.p.in_shape = (4,)
+
+    def alloc(self, n):
+        off = self.words
+        self.words += max(4, (int(n) + 3) // 4 * 4)
+        return off
+
+    def static(self, w):
+        w = np.ascontiguousarray(w, np.uint32).reshape(-1)
+        off = self.alloc(w.size)
+        self.p.uploads.append((off, w))
+        return off
+
+    def dispatch(self, kernel, params, groups=(1, 1, 1)):
+        pw = np.array([v if isinstance(v, (int, np.integer)) else plan.f32_bits(v) for v in params],
+                      np.uint32)
+        self.p.dispatches.append((kernel, self.static(pw), tuple(groups), -1))
+
+    def done(self, out_off, numel):
+        self.p.outputs.append((out_off, int(numel), (int(numel),)))
+        self.p.total_words = self.words
+        return self.p
+
+
+OFF_NONE = 0xFFFFFFFF
+
+
+def test_validate_accepts_the_written_plans(lib):
+    """qph_plan_validate (no context, no device) passes the det and rec plans
+    the writer produces, the checks qph_plan_create runs first."""
+    plan.validate_plan(plan.build_plan(nets.build_det(2, 96, 64)[0]))
+    plan.validate_plan(plan.build_plan(nets.build_rec(3, 2, 160, probs=False)[0]))
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.dispatch("n_elem", [0, x, OFF_NONE, x, 16, 0.0, 0.0])
+    plan.validate_plan(mp.done(x, 16))
+
+
+def test_validate_refuses_malformed_plans(lib):
+    """Malformed plans are refused on the host, naming what is wrong: a
+    region past the arena, a misaligned vec4 region, a parameter block that
+    was never uploaded, an n_reduce_fin with no n_reduce_hw before it, an
+    output or input outside the arena, overlapping uploads."""
+    from qppocr_amd import _lib
+
+    def refused(p, match):
+        with pytest.raises(_lib.QphError, match=match):
+            plan.validate_plan(p)
+
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.dispatch("n_elem", [0, x, OFF_NONE, x + 1000, 16, 0.0, 0.0])
+    refused(mp.done(x, 16), "outside the arena")
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.dispatch("n_elem", [0, x + 1, OFF_NONE, x, 12, 0.0, 0.0])
+    refused(mp.done(x, 16), "16-byte aligned")
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.p.dispatches.append(("n_elem", mp.alloc(8), (1, 1, 1), -1))   # block never uploaded
+    refused(mp.done(x, 16), "not uploaded")
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.dispatch("n_reduce_fin", [x, x, 1, 4, 4])
+    refused(mp.done(x, 4), "n_reduce_hw")
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.dispatch("n_elem", [0, x, OFF_NONE, x, 16, 0.0, 0.0])
+    p = mp.done(x, 16)
+    p.outputs[0] = (p.total_words - 4, 16, (16,))
+    refused(p, "output 0 is outside")
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.dispatch("n_elem", [0, x, OFF_NONE, x, 16, 0.0, 0.0])
+    p = mp.done(x, 16)
+    p.in_f32_off = p.total_words - 2
+    refused(p, "input region")
+    mp = _Plan()
+    x = mp.alloc(16)
+    mp.dispatch("n_elem", [0, x, OFF_NONE, x, 16, 0.0, 0.0])
+    p = mp.done(x, 16)
+    p.uploads.append((p.uploads[-1][0] + 2, np.zeros(4, np.uint32)))
+    refused(p, "overlap")
