@@ -300,6 +300,48 @@ def bench_cfg1(nets, ops, configs, ctx, replays, cpu_rounds, O):
     return out
 
 
+def stream_floor_us(n_in, n_out, replays):
+    """Per-launch time of torch's own device copy streaming the same bytes
+    cache-cold (n_in floats read, n_out written: a plain copy when the sizes
+    are equal, else a copy of every (n_in / n_out)-th input, which reads
+    every cache line of the input), R rotating buffer sets past COLD_BYTES,
+    R launches per graph replay: the floor for moving an op's compulsory
+    bytes in one launch in this harness."""
+    import torch
+    set_bytes = 4 * (n_in + n_out)
+    R = max(2, -(-COLD_BYTES // set_bytes))
+    xs = [torch.rand(n_in, device="cuda") for _ in range(R)]
+    ys = [torch.empty(n_out, device="cuda") for _ in range(R)]
+    ratio = n_in // n_out
+
+    def body():
+        for x, y in zip(xs, ys):
+            if ratio == 1:
+                y.copy_(x)
+            else:
+                y.copy_(x.view(n_out, ratio)[:, 0])
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        body()
+    st.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=st):
+        body()
+    with torch.cuda.stream(st):
+        for _ in range(2):
+            gr.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(replays):
+            gr.replay()
+        e1.record(st)
+    st.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * R)
+    del gr, xs, ys
+    return us
+
+
 def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
     from qppocr_amd._lib import ACT_HARDSWISH
     res = {}
@@ -318,12 +360,19 @@ def bench_cfg2(nets, ops, configs, ctx, replays, cpu_rounds, O):
         us = ob.us_per_launch(replays)
         ob.close()
         gbs = by / (us * 1e-6) / 1e9
+        floor = stream_floor_us(x.size, c * oh * oh, replays)
         out = {"workload": f"depthwise {k}x{k} s{s} pad {k // 2} C{c} {hw}x{hw} + hardswish",
                "us": round(us, 3), "gbs": round(gbs, 1), "bound": "hbm",
                "frac": round(gbs / PEAK_HBM_GBS, 4), "mb": round(by / 1e6, 3),
-               "kernel": f"depthwise_wave_kernel<{k},{k}>",
+               "kernel": f"depthwise_rows_kernel<{k},{s}>",
                "method": f"cache-cold: HIP events over {replays} graph replays of {ob.R} copies "
-                         f"on rotating buffer sets ({ob.R * set_bytes >> 20} MB)"}
+                         f"on rotating buffer sets ({ob.R * set_bytes >> 20} MB)",
+               "stream_floor_us": round(floor, 3),
+               "floor_method": "torch's device copy reading the input bytes and writing the "
+                               "output bytes (for the stride-2 cases every 4th input, which "
+                               "touches every line of the input), timed the same way: one "
+                               "launch's floor for these bytes",
+               "frac_of_floor": round(floor / us, 3)}
         if O is not None:
             params = O.conv_params(s, s, k // 2, k // 2, group=c)
 

@@ -1427,7 +1427,183 @@ static int launch_depthwise_wave(const ConvArgs& a, hipStream_t s) {
   return launch_check("depthwise_wave_kernel");
 }
 
+// Depthwise over whole image rows (the HBM-bound NCHW form: cfg-style
+// planes whose width is a multiple of 4).  A thread owns 4V adjacent
+// outputs of one output row (V 16-byte stores): group gg of a row covers
+// outputs [4V gg, 4V gg + 4V), whose own input columns are [4VS gg, 4VS gg +
+// 4VS) -- VS 16-byte loads per input row, straight into registers.  A wave
+// holds whole output rows, 64 / g of them (g = groups per row), lanes in row
+// order, so the K/2 input columns left of a group are the last ones of the
+// lane before it and the K/2 + 1 - S right of it the first ones of the lane
+// after it: cross-lane shuffles inside the wave, 0 at the image border (the
+// zero padding); rows above or below the image read 0 through the buffer
+// range check.  A plane takes whole waves, so its channel is the same across
+// a wave and the weights and bias come through scalar loads.  Every load is
+// issued before the first fma; no LDS, no barrier.  Each output keeps the
+// reference chain acc = fma(w, x, acc) over ky then kx from 0 (out-of-image
+// taps are fma(w, 0, acc) there, which leave acc unchanged), + bias, then
+// the activation.
+struct DwRowsK {
+  const float* x;
+  const float* w;
+  const float* bias;
+  float* y;
+  int c, h, w_, oh, ow;
+  int g, rw;         // groups per output row, output rows per wave (rw * g <= 64)
+  int wpp;           // waves per plane: ceil(oh / rw)
+  int planes;
+  int y_ctotal, y_coff;
+  Act act;
+};
+
+template <int K, int S, int V, int AK>
+__global__ __launch_bounds__(256) void depthwise_rows_kernel(DwRowsK p) {
+  constexpr int RIN = K;                     // input rows of one output row
+  constexpr int NL = K / 2, NR = K / 2 + 1 - S;
+  constexpr int OWN = 4 * V * S;             // own input columns of a row
+  constexpr int NW = NL + OWN + NR;          // input columns of a row one thread uses
+  const int lane = threadIdx.x & 63;
+  const unsigned wv = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned plane = wv / (unsigned)p.wpp;
+  if (plane >= (unsigned)p.planes) return;   // whole waves past the last plane
+  const int row_in_wave = lane / p.g, gg = lane - row_in_wave * p.g;
+  const int oy = (int)(wv - plane * (unsigned)p.wpp) * p.rw + row_in_wave;
+  const bool valid = row_in_wave < p.rw && oy < p.oh;
+  const int ch = (int)(plane % (unsigned)p.c);
+  const int iw = p.w_;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + (int64_t)plane * p.h * iw), 0, p.h * iw * 4, 0x00020000);
+  const int iy0 = oy * S - NL, ix0 = OWN * gg;
+  // the own columns of each input row, every load issued first (lanes past
+  // the wave's rows read nothing: an out-of-range offset)
+  float xin[RIN][NW];
+#pragma unroll
+  for (int r = 0; r < RIN; r++) {
+    const int iy = iy0 + r;
+    const unsigned off =
+        (valid && iy >= 0 && iy < p.h) ? (unsigned)(iy * iw + ix0) * 4u : 0x80000000u;
+#pragma unroll
+    for (int v = 0; v < V * S; v++) {
+      const f32x4 q =
+          __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 16 * v, 0));
+#pragma unroll
+      for (int e = 0; e < 4; e++) xin[r][NL + 4 * v + e] = q[e];
+    }
+  }
+  float wr[K * K];
+#pragma unroll
+  for (int i = 0; i < K * K; i++) wr[i] = p.w[ch * K * K + i];
+  const float bv = p.bias ? p.bias[ch] : 0.0f;
+  // the neighbours' columns, from the lanes beside this one in the same
+  // row, or 0 at the image border
+  const bool left_in = gg > 0, right_in = gg + 1 < p.g;
+#pragma unroll
+  for (int r = 0; r < RIN; r++) {
+#pragma unroll
+    for (int j = 0; j < NL; j++) {
+      const float v = __shfl_up(xin[r][NL + OWN - NL + j], 1, 64);
+      xin[r][j] = left_in ? v : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NR; j++) {
+      const float v = __shfl_down(xin[r][NL + j], 1, 64);
+      xin[r][NL + OWN + j] = right_in ? v : 0.0f;
+    }
+  }
+  if (!valid) return;
+  const int64_t bn = plane / (unsigned)p.c;
+  float* yp = p.y + ((bn * p.y_ctotal + p.y_coff + ch) * (int64_t)p.oh + oy) * p.ow + 4 * V * gg;
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    float out[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int i = 4 * v + e;
+      float acc = 0.0f;
+#pragma unroll
+      for (int ky = 0; ky < K; ky++)
+#pragma unroll
+        for (int kx = 0; kx < K; kx++) acc = __builtin_fmaf(wr[ky * K + kx], xin[ky][S * i + kx], acc);
+      float o = acc + bv;
+      if constexpr (AK == 3)
+        o = o * hsig1(o, p.act.c1, p.act.c2);
+      else if constexpr (AK < 0)
+        o = act_apply(o, p.act);
+      out[e] = o;
+    }
+    *(f32x4*)(yp + 4 * v) = f32x4{out[0], out[1], out[2], out[3]};
+  }
+}
+
+// Outputs per thread (4 or 8) for the whole-row form: 0 when a row of
+// groups does not fit a wave.  Eight when four would leave a quarter or more
+// of a wave's lanes idle and eight fit rows with fewer idle (the 160-wide
+// planes: 40 groups of 4 fill 40 lanes, 20 groups of 8 fill 60).
+static int dw_rows_v(int64_t ow) {
+  if (ow % 4) return 0;
+  const int64_t g1 = ow / 4;
+  const int64_t idle1 = g1 <= 64 ? 64 - (64 / g1) * g1 : 64;
+  if (ow % 8 == 0 && ow / 8 <= 64) {
+    const int64_t g2 = ow / 8, idle2 = 64 - (64 / g2) * g2;
+    if (idle1 >= 16 && idle2 < idle1) return 2;
+  }
+  return g1 <= 64 ? 1 : 0;
+}
+
+// Whole-row form: k x k kernel (3 or 5) with padding k / 2 on the left and
+// top, equal strides 1 or 2, input width = stride * output width, output
+// rows of at most 64 groups, 16-byte aligned tensors, plain or channel-slice
+// output.
+static bool dw_rows_eligible(const ConvArgs& a) {
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  return ((a.kh == 3 && a.kw == 3) || (a.kh == 5 && a.kw == 5)) && a.sh == a.sw &&
+         (a.sw == 1 || a.sw == 2) && a.ph == a.kh / 2 && a.pw == a.kw / 2 && !a.res &&
+         a.y_up == 1 && dw_rows_v(a.ow) > 0 && a.w == a.sw * a.ow && al16(a.x) && al16(a.y) &&
+         a.h * a.w * 4 < (1ll << 31) && a.n * a.c < (1ll << 31) &&
+         a.n * a.y_ctotal * a.oh * a.ow < (1ll << 40);
+}
+
+template <int K, int S, int V>
+static void launch_dw_rows_ak(const DwRowsK& p, dim3 grid, hipStream_t s) {
+  if (p.act.kind == 3)
+    hipLaunchKernelGGL((depthwise_rows_kernel<K, S, V, 3>), grid, dim3(256), 0, s, p);
+  else if (p.act.kind == 0)
+    hipLaunchKernelGGL((depthwise_rows_kernel<K, S, V, 0>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((depthwise_rows_kernel<K, S, V, -1>), grid, dim3(256), 0, s, p);
+}
+
+template <int K, int S>
+static void launch_dw_rows_v(const DwRowsK& p, int v, dim3 grid, hipStream_t s) {
+  if (v == 2) launch_dw_rows_ak<K, S, 2>(p, grid, s);
+  else launch_dw_rows_ak<K, S, 1>(p, grid, s);
+}
+
+static int launch_depthwise_rows(const ConvArgs& a, hipStream_t s) {
+  DwRowsK p{};
+  p.x = a.x; p.w = a.wt; p.bias = a.bias; p.y = a.y;
+  p.c = (int)a.c; p.h = (int)a.h; p.w_ = (int)a.w; p.oh = (int)a.oh; p.ow = (int)a.ow;
+  const int v = dw_rows_v(a.ow);
+  p.g = (int)(a.ow / (4 * v));
+  p.rw = 64 / p.g;
+  p.y_ctotal = (int)a.y_ctotal; p.y_coff = (int)a.y_coff;
+  p.act = a.act;
+  const int64_t planes = a.n * a.c;
+  p.wpp = (int)ceil_div(a.oh, p.rw);
+  p.planes = (int)planes;
+  const int64_t blocks = ceil_div(planes * p.wpp, 4);
+  if (blocks >= (1ll << 30)) return fail(QPH_EUNSUPPORTED, "depthwise: grid too large");
+  const dim3 grid((unsigned)blocks);
+  const int k = (int)a.kh;
+  if (k == 3 && a.sw == 1) launch_dw_rows_v<3, 1>(p, v, grid, s);
+  else if (k == 3) launch_dw_rows_v<3, 2>(p, v, grid, s);
+  else if (a.sw == 1) launch_dw_rows_v<5, 1>(p, v, grid, s);
+  else launch_dw_rows_v<5, 2>(p, v, grid, s);
+  return launch_check("depthwise_rows_kernel");
+}
+
 int launch_depthwise(const ConvArgs& a, hipStream_t s) {
+  if (dw_rows_eligible(a)) return launch_depthwise_rows(a, s);
   if (dw_wave_eligible(a)) return launch_depthwise_wave(a, s);
   DwK p{};
   p.x = a.x; p.w = a.wt; p.bias = a.bias; p.res = a.res; p.y = a.y;
