@@ -40,6 +40,7 @@
 #include <algorithm>
 #include <cstring>
 #include <functional>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -597,6 +598,168 @@ __global__ __launch_bounds__(64) void plan_conv_dma_kernel(ConvK p) {
   }
 }
 
+// 3x3 convs with x-stride SW (the det neck and head over the NHWC arena):
+// a workgroup of NCB waves, one 16-channel output block each, owns 32
+// consecutive output pixels of one output row.  Per group of 4 input
+// channels it loads, once for all its waves, the 3 x (31 SW + 3) halo quads
+// those pixels read (slot r * HC + col: input row iy0 + r, column ix0 + col,
+// 0 outside the image) and the group's 36 weight rows (t * 4 + c) for all
+// its output blocks (past N: 0), by buffer->LDS loads; the B operand of tap
+// (ky, kx) and pixel j is then halo quad (ky, j * SW + kx).  Groups move
+// through a CONV_DMA_D-deep ring: before a group's steps each wave waits for
+// its own loads of that group, then a barrier (every wave's loads of it in,
+// every wave's reads of the previous buffer done) frees the previous buffer
+// for the refill.  Chain order (k = c * 9 + t within a group), bias rule and
+// epilogue are plan_conv_dma_kernel's, so the outputs are the same bits with
+// the halo loaded once instead of once per tap and per output block.
+template <int SW>
+struct HaloGeom {
+  static constexpr int HC = 31 * SW + 3;               // halo columns
+  static constexpr int HQ = 3 * HC;                    // halo quads per group
+  static constexpr int HQP = (HQ + 63) / 64 * 64;      // their slots (whole loads)
+};
+
+// Up to four independent such convs of one batch count, one launch: conv m
+// takes workgroups [start[m], start[m + 1]) (the det neck's four smoothing
+// convs, whose sizes differ 64-fold, so the small ones run beside the large
+// one instead of after it).
+#define HALO_GROUP_MAX 4
+struct HaloGroup {
+  ConvK k[HALO_GROUP_MAX];
+  int tiles_x[HALO_GROUP_MAX];
+  int start[HALO_GROUP_MAX + 1];
+};
+
+template <int SW, int NCB>
+__device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x, int tile,
+                                                    float4* ring) {
+  using G = HaloGeom<SW>;
+  constexpr int WC = 36 * 4 * NCB;                     // weight chunks per group
+  constexpr int L = (G::HQP + WC + 64 * NCB - 1) / (64 * NCB);   // loads per wave per group
+  constexpr int BUF = L * 64 * NCB;                    // float4 per group buffer
+  const int b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && (unsigned)b >= rn) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = (int)p.N, ow = (int)p.ow, P = (int)p.P;
+  const int oy = tile / tiles_x, ox0 = (tile - oy * tiles_x) * 32;
+  const int li = lane & 15, kq = lane >> 4;
+  const int co0 = wave * 16;
+  const int cin = (int)p.cin, iw = (int)p.iw, ih = (int)p.ih;
+  const int iy0 = oy * (int)p.sh - (int)p.pt, ix0 = ox0 * SW - (int)p.pl;
+  const unsigned OOB = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + (size_t)b * ih * iw * cin), 0, ih * iw * cin * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.w, 0, 9 * cin * N * 4, 0x00020000);
+  // this wave's loads: slots 64 (L wave + i) + lane; halo slots [0, HQP),
+  // weight slots [HQP, HQP + WC): every load is wholly one or the other
+  int off[L];
+#pragma unroll
+  for (int i = 0; i < L; i++) {
+    const int s = 64 * (L * wave + i) + lane;
+    off[i] = -1;
+    if (s < G::HQ) {
+      const int r = s / G::HC, col = s - r * G::HC, iy = iy0 + r, ix = ix0 + col;
+      if ((unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw) off[i] = (iy * iw + ix) * cin;
+    } else if (s >= G::HQP && s < G::HQP + WC) {
+      const int w = s - G::HQP, row = w / (4 * NCB), j = w - row * (4 * NCB);
+      const int t = row >> 2, c = row & 3;
+      if (4 * j < N) off[i] = (t * cin + c) * N + 4 * j;
+    }
+  }
+  auto issue = [&](int g) {
+    float4* buf = ring + (g % CONV_DMA_D) * BUF;
+#pragma unroll
+    for (int i = 0; i < L; i++) {
+      const bool isx = 64 * (L * wave + i) < G::HQP;   // wave-uniform
+      const unsigned o = off[i] < 0 ? OOB : (unsigned)((off[i] + (isx ? 4 * g : 4 * g * N)) * 4);
+      const unsigned m = __builtin_amdgcn_readfirstlane(
+          (unsigned)(uintptr_t)(__attribute__((address_space(3))) float4*)(buf + 64 * (L * wave + i)));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // m0 is reserved; nothing else uses it here
+      __asm__ volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m),
+                       "v"(o), "s"(isx ? xr : wr)
+                       : "m0");
+#pragma clang diagnostic pop
+    }
+  };
+  f32x4 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int ox = ox0 + 16 * j + li, px = oy * ow + ox;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int co = co0 + 4 * kq + v;
+      acc[j][v] = (p.bias && co < N && ox < ow && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
+    }
+  }
+  const int groups = cin / 4;
+#pragma unroll
+  for (int g = 0; g < CONV_DMA_D - 1; g++)
+    if (g < groups) issue(g);
+  for (int g = 0; g < groups; g++) {
+    const int ahead = min(CONV_DMA_D - 2, groups - 1 - g);   // groups issued after g
+    switch (ahead) {
+      case 2: wait_vmcnt<2 * L>(); break;
+      case 1: wait_vmcnt<L>(); break;
+      default: wait_vmcnt<0>(); break;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the previous buffer are back
+    __builtin_amdgcn_s_barrier();         // and every wave's; group g is in for all
+    __asm__ volatile("" ::: "memory");
+    if (g + CONV_DMA_D - 1 < groups) issue(g + CONV_DMA_D - 1);   // into the buffer of g - 1
+    const float* hq = (const float*)(ring + (g % CONV_DMA_D) * BUF);
+    const float* wq = hq + 4 * G::HQP;
+#pragma unroll
+    for (int u = 0; u < 9; u++) {
+      const int k = 4 * u + kq, c = k / 9, t = k - c * 9, ky = t / 3, kx = t - ky * 3;
+      const float a = wq[(4 * t + c) * (16 * NCB) + co0 + li];
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+            a, hq[(ky * G::HC + (16 * j + li) * SW + kx) * 4 + c], acc[j], 0, 0, 0);
+    }
+  }
+  const int cob = co0 + 4 * kq;
+  if (cob >= N) return;
+  const float* yres = p.res ? p.res + (size_t)b * P * N : nullptr;
+  float* yb = p.y + (size_t)b * P * N;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int ox = ox0 + 16 * j + li;
+    if (ox >= ow) continue;
+    const int px = oy * ow + ox;
+    float o[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float x = acc[j][v];
+      if (p.bias && !conv_seeded(p, cob + v, px)) x = x + p.bias[cob + v];
+      x = act_apply(x, p.act);
+      if (yres) x = x + yres[px * N + cob + v];
+      o[v] = x;
+    }
+    *(float4*)(yb + px * N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+template <int SW, int NCB>
+__global__ __launch_bounds__(64 * NCB) void plan_conv_halo_kernel(ConvK p, int tiles_x) {
+  extern __shared__ float4 ring[];
+  plan_conv_halo_tile<SW, NCB>(p, tiles_x, (int)blockIdx.x, ring);
+}
+
+template <int SW, int NCB>
+__global__ __launch_bounds__(64 * NCB) void plan_conv_halo_group_kernel(HaloGroup g) {
+  extern __shared__ float4 ring[];
+  const int t = (int)blockIdx.x;   // < start[HALO_GROUP_MAX]: the grid is the total
+  int m = 0;
+#pragma unroll
+  for (int i = 1; i < HALO_GROUP_MAX; i++) m += t >= g.start[i] ? 1 : 0;
+  plan_conv_halo_tile<SW, NCB>(g.k[m], g.tiles_x[m], t - g.start[m], ring);
+}
+
 // ------------------------------------------------------------- depthwise
 struct DwK {
   const float* arena; const float* x; const float* w; const float* bias; const float* res;
@@ -851,6 +1014,17 @@ struct Decoder {
   std::vector<std::vector<uint32_t>> rd;
   std::vector<uint32_t> outs;
   std::vector<char> skip;
+  // an open group of 3x3 halo convs launched together (first member's
+  // position); see join_halo_group
+  struct Span { uint64_t lo, hi; };
+  struct HaloOpen {
+    std::shared_ptr<HaloGroup> g;
+    int n = 0, sw = 0, ncb = 0;
+    int64_t nb = 0;
+    int last = -1;                    // dispatch index of the last member
+    std::vector<Span> reads, writes;  // the members' and the dispatches' between them
+  };
+  HaloOpen halo;
 
   std::string where() const {
     return "plan dispatch " + std::to_string(idx) + " (" + kname + ", params at word " +
@@ -1039,6 +1213,55 @@ int add_launch(qph_plan* pl, int dispatch, std::function<int(hipStream_t)> f) {
 
 struct PendingHw { uint32_t in, scratch; int64_t m, c, nb; };
 
+size_t halo_lds(int sw, int ncb) {
+  const int hqp = sw == 1 ? HaloGeom<1>::HQP : HaloGeom<2>::HQP;
+  const int l = (hqp + 144 * ncb + 64 * ncb - 1) / (64 * ncb);
+  return (size_t)CONV_DMA_D * l * 64 * ncb * 16;
+}
+
+// A 3x3 halo conv joins the open group (and launches with its first member,
+// earlier in the launch order) when: the group has room and the same
+// stride, output-block count and batch count; every dispatch since the
+// group's last member is an n_resize (the det neck's pattern: smoothing conv,
+// upsample, smoothing conv, ...); and none of the regions this conv's launch
+// reads (input, weights, bias, residual) overlaps a region written by a
+// member or by those n_resize dispatches, nor does the region it writes
+// overlap one they read or write.  Its absorbed epilogue moves with it.
+bool join_halo_group(Decoder& d, const ConvK& k, int tiles_x, int64_t oh, int sw, int ncb,
+                     int64_t nb, const std::vector<Decoder::Span>& rd, const Decoder::Span& wr) {
+  Decoder::HaloOpen& h = d.halo;
+  if (!h.g || h.n >= HALO_GROUP_MAX || h.sw != sw || h.ncb != ncb || h.nb != nb) return false;
+  auto over = [](const Decoder::Span& a, const Decoder::Span& b) { return a.lo < b.hi && b.lo < a.hi; };
+  std::vector<Decoder::Span> reads = h.reads, writes = h.writes;
+  for (int m = h.last + 1; m < d.idx; m++) {
+    const qph_plan_dispatch& q = d.disp[m];
+    const uint32_t* w = q.kernel == PK_RESIZE ? d.find(q.p_off, 9) : nullptr;
+    if (!w || d.skip[(size_t)m]) return false;
+    const uint64_t nbm = q.groups[1];
+    reads.push_back({w[0], w[0] + nbm * w[5] * w[6] * w[3]});
+    writes.push_back({w[1], w[1] + nbm * w[2] * w[3]});
+  }
+  for (const auto& r : rd)
+    for (const auto& w : writes)
+      if (over(r, w)) return false;
+  for (const auto& w : writes)
+    if (over(wr, w)) return false;
+  for (const auto& r : reads)
+    if (over(wr, r)) return false;
+  HaloGroup& g = *h.g;
+  const int i = h.n++;
+  g.k[i] = k;
+  g.tiles_x[i] = tiles_x;
+  g.start[i + 1] = g.start[i] + (int)(oh * tiles_x);
+  for (int j = i + 2; j <= HALO_GROUP_MAX; j++) g.start[j] = g.start[i + 1];
+  h.reads = reads;
+  for (const auto& r : rd) h.reads.push_back(r);
+  h.writes = writes;
+  h.writes.push_back(wr);
+  h.last = d.idx;
+  return true;
+}
+
 int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
   const uint32_t* w;
   QPH_TRY(d.params(21, &w));
@@ -1130,6 +1353,50 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
   k.res = e.res == OFF_NONE ? nullptr : d.at(e.res);
   k.y = d.at(e.y);
   const int64_t lwaves = ((N + 15) / 16) * ((P + 31) / 32);
+  // 3x3 convs with up to four 16-channel output blocks: the halo kernel
+  if (kh == 3 && kw == 3 && (sw == 1 || sw == 2) && N <= 64 && cin >= 8 &&
+      9 * cin * N * 4 < (1ll << 31) && ih * iw * cin * 4 < (1ll << 31) &&
+      oh * ((ow + 31) / 32) < (1ll << 31)) {
+    const int tiles_x = (int)((ow + 31) / 32), ncb = (int)((N + 15) / 16);
+    // what this conv (with its absorbed epilogue) reads and writes
+    using Span = Decoder::Span;
+    std::vector<Span> rd{{in, in + (uint64_t)nb * ih * iw * cin}, {wo, wo + (uint64_t)taps * cin * N}};
+    if (e.bias != OFF_NONE) rd.push_back({e.bias, e.bias + (uint64_t)N});
+    if (e.res != OFF_NONE) rd.push_back({e.res, e.res + (uint64_t)nb * P * N});
+    const Span wr{e.y, e.y + (uint64_t)nb * P * N};
+    if (join_halo_group(d, k, tiles_x, oh, (int)sw, ncb, nb, rd, wr)) return QPH_OK;
+    auto g = std::make_shared<HaloGroup>();
+    g->k[0] = k;
+    g->tiles_x[0] = tiles_x;
+    d.halo = Decoder::HaloOpen{};
+    d.halo.g = g;
+    d.halo.n = 1;
+    d.halo.sw = (int)sw;
+    d.halo.ncb = ncb;
+    d.halo.nb = nb;
+    d.halo.last = d.idx;
+    d.halo.reads = rd;
+    d.halo.writes = {wr};
+    g->start[0] = 0;
+    for (int i = 1; i <= HALO_GROUP_MAX; i++) g->start[i] = (int)(oh * tiles_x);
+    const size_t lds = halo_lds((int)sw, ncb);
+    const unsigned nbu = (unsigned)nb;
+#define QPH_HALO(S, C)                                                                      \
+  if (sw == S && ncb == C)                                                                  \
+    return add_launch(d.pl, d.idx, [g, lds, nbu](hipStream_t s) {                           \
+      const dim3 grid((unsigned)g->start[HALO_GROUP_MAX], nbu);                             \
+      if (g->start[1] == g->start[HALO_GROUP_MAX])                                          \
+        hipLaunchKernelGGL((plan_conv_halo_kernel<S, C>), grid, dim3(64 * C), lds, s,       \
+                           g->k[0], g->tiles_x[0]);                                         \
+      else                                                                                  \
+        hipLaunchKernelGGL((plan_conv_halo_group_kernel<S, C>), grid, dim3(64 * C), lds, s, \
+                           *g);                                                             \
+      return launch_check("plan_conv_halo_kernel");                                         \
+    });
+    QPH_HALO(1, 1) QPH_HALO(1, 2) QPH_HALO(1, 3) QPH_HALO(1, 4)
+    QPH_HALO(2, 1) QPH_HALO(2, 2) QPH_HALO(2, 3) QPH_HALO(2, 4)
+#undef QPH_HALO
+  }
   // the ring pays off from two channel groups on (a 3-channel stem has one)
   if ((taps == 1 || taps == 4 || taps == 9) && cin >= 8 && taps * cin * N * 4 < (1ll << 31) &&
       ih * iw * cin * 4 < (1ll << 31) && lwaves < (1ll << 31)) {
@@ -1161,6 +1428,68 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
     hipLaunchKernelGGL(plan_conv_kernel, dim3((unsigned)((waves + 3) / 4), (unsigned)nb),
                        dim3(256), 0, s, k);
     return launch_check("plan_conv_kernel");
+  });
+}
+
+// The nine dispatches PlanBuilder writes for a LayerNorm over contiguous
+// rows, starting at an n_reduce_last (w: its block): mean M = mean(X);
+// D = X - M (n_elem 8); SQ = D * D (n_elem 9); V = mean(SQ); VE = V + eps
+// (n_elem 6, eps a static word); S = sqrt(VE) (n_elem 10); Y0 = D / S
+// (n_elem 11); Y1 = Y0 * gamma (n_channel 0); Y = Y1 + beta (n_channel 1).
+// That is layernorm_kernel's operation sequence (the f64 means the
+// reference's, each step rounded to f32 in the same order), so when every
+// intermediate is read only inside the run and is no graph output, the run
+// is one layernorm launch: *folded, the eight dispatches after it skipped.
+int fold_layernorm(Decoder& d, const uint32_t* w, bool* folded) {
+  *folded = false;
+  const uint32_t X = w[0], M = w[1];
+  const uint32_t R = w[2], C = w[3];
+  if (w[4] != C || C < 4 || C % 4 || C > 4096 || R < 1) return QPH_OK;
+  const uint64_t n = (uint64_t)R * C;
+  const int i = d.idx;
+  const uint32_t* e8 = d.peek(i + 1, PK_ELEM, 7);
+  const uint32_t* e9 = d.peek(i + 2, PK_ELEM, 7);
+  const uint32_t* r2 = d.peek(i + 3, PK_REDUCE_LAST, 6);
+  const uint32_t* e6 = d.peek(i + 4, PK_ELEM, 7);
+  const uint32_t* e10 = d.peek(i + 5, PK_ELEM, 7);
+  const uint32_t* e11 = d.peek(i + 6, PK_ELEM, 7);
+  const uint32_t* c0 = d.peek(i + 7, PK_CHANNEL, 10);
+  const uint32_t* c1 = d.peek(i + 8, PK_CHANNEL, 10);
+  if (!e8 || !e9 || !r2 || !e6 || !e10 || !e11 || !c0 || !c1) return QPH_OK;
+  const uint32_t D = e8[3], SQ = e9[3], V = r2[1], VE = e6[3], S = e10[3], Y0 = e11[3];
+  const uint32_t Y1 = c0[4], Y = c1[4], G = c0[2], B = c1[2];
+  const bool shape =
+      e8[0] == 8 && e8[1] == X && e8[2] == M && e8[4] == n && e8[5] == C / 4 &&
+      e9[0] == 9 && e9[1] == D && e9[4] == n &&
+      r2[0] == SQ && r2[2] == R && r2[3] == C && r2[4] == C &&
+      e6[0] == 6 && e6[1] == V && e6[4] == 4 * R &&
+      e10[0] == 10 && e10[1] == VE && e10[4] == 4 * R &&
+      e11[0] == 11 && e11[1] == D && e11[2] == S && e11[4] == n && e11[5] == C / 4 &&
+      c0[0] == 0 && c0[1] == Y0 && c0[3] == OFF_NONE && c0[5] == n && c0[6] == C && c0[9] == R &&
+      c1[0] == 1 && c1[1] == Y1 && c1[3] == OFF_NONE && c1[5] == n && c1[6] == C && c1[9] == R;
+  if (!shape) return QPH_OK;
+  const uint32_t* eps_w = d.find(e6[2], 1);
+  if (!eps_w) return QPH_OK;   // eps not a static word: the dispatches one by one
+  // intermediates read only inside the run (and no graph output)
+  if (!d.only_readers(i, M, 4ull * R, {i + 1}) || !d.only_readers(i + 1, D, n, {i + 2, i + 6}) ||
+      !d.only_readers(i + 2, SQ, n, {i + 3}) || !d.only_readers(i + 3, V, 4ull * R, {i + 4}) ||
+      !d.only_readers(i + 4, VE, 4ull * R, {i + 5}) || !d.only_readers(i + 5, S, 4ull * R, {i + 6}) ||
+      !d.only_readers(i + 6, Y0, n, {i + 7}) || !d.only_readers(i + 7, Y1, n, {i + 8}))
+    return QPH_OK;
+  QPH_TRY(d.region(X, n, true, "LayerNorm input"));
+  QPH_TRY(d.region(Y, n, true, "LayerNorm output"));
+  QPH_TRY(d.region(G, C, true, "LayerNorm gamma"));
+  QPH_TRY(d.region(B, C, true, "LayerNorm beta"));
+  float eps;
+  std::memcpy(&eps, eps_w, 4);
+  const float* x = d.at(X);
+  const float* g = d.at(G);
+  const float* b = d.at(B);
+  float* y = d.at(Y);
+  for (int j = i + 1; j <= i + 8; j++) d.skip[(size_t)j] = 1;
+  *folded = true;
+  return add_launch(d.pl, d.idx, [=](hipStream_t s) {
+    return launch_layernorm(x, g, b, eps, R, C, y, s);
   });
 }
 
@@ -1372,6 +1701,9 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       QPH_TRY(d.params(6, &w));
       const int64_t rows = w[2], cols = w[3], cp = w[4];
       if (rows < 1 || cols < 1 || cp < cols) return fail(QPH_EINVAL, d.where() + ": bad rows / cols");
+      bool folded = false;
+      QPH_TRY(fold_layernorm(d, w, &folded));
+      if (folded) return QPH_OK;
       QPH_TRY(d.region(w[0], (uint64_t)rows * cp, false, "input"));
       QPH_TRY(d.region(w[1], (uint64_t)rows * 4, false, "output"));
       const float* x = d.at(w[0]);

@@ -122,6 +122,54 @@ def test_plan_conv(gpu, oracle, case):
     assert_bitexact(got, nhwc(ref), "conv")
 
 
+@pytest.mark.parametrize("dependent", [False, True])
+def test_plan_halo_convs_share_a_launch(gpu, oracle, dependent):
+    """Two 9-tap convs with 24 outputs (the det neck's smoothing shape) with an
+    n_resize between them run as one launch when the second reads nothing
+    the resize or the first writes; when the second reads the first's output
+    it keeps its own launch.  Bit-exact against the oracle either way."""
+    from qppocr_amd import plan as P
+    O = oracle
+    r = rng(91 + int(dependent))
+    c, m, h1, h2 = 32, 24, 20, 40
+    x1 = rnd(r, (1, c, h1, h1))
+    x2 = rnd(r, (1, c, h2, h2))
+    w1 = rnd(r, (m, c, 3, 3), 1.0 / math.sqrt(c * 9))
+    w2 = rnd(r, (m, m if dependent else c, 3, 3), 1.0 / math.sqrt(c * 9))
+    b1, b2 = rnd(r, (m,), 0.1), rnd(r, (m,), 0.1)
+    p = O.conv_params(1, 1, 1, 1, 1, 1)
+    ref1 = O.conv2d(x1, w1, b1, p, O.ACT_RELU)
+    ref2 = O.conv2d(ref1 if dependent else x2, w2, b2, p, O.ACT_NONE)
+    up = O.resize_nearest(ref1, 2 * h1, 2 * h1)
+    mp = MiniPlan()
+    x1o, x2o = mp.static(nhwc(x1)), mp.static(nhwc(x2))
+    w1o = mp.static(np.concatenate([P.repack_conv_w(w1, m, c, 3, 3), np.zeros(32, np.uint32)]))
+    c2 = m if dependent else c
+    w2o = mp.static(np.concatenate([P.repack_conv_w(w2, m, c2, 3, 3), np.zeros(32, np.uint32)]))
+    b1o, b2o = mp.static(P.conv_bias(b1, m)), mp.static(P.conv_bias(b2, m))
+    y1o = mp.alloc(h1 * h1 * m)
+    upo = mp.alloc(4 * h1 * h1 * m)
+    hi = h1 if dependent else h2
+    y2o = mp.alloc(hi * hi * m)
+    mp.dispatch("n_conv8", [x1o, w1o, b1o, y1o, h1 * h1, m, h1, h1, h1, c // 4, 9, 3, 1, 1, 1, 1,
+                            2, *P.GELU_C, OFF_NONE], (1, 1, 1))
+    mp.dispatch("n_resize", [y1o, upo, 4 * h1 * h1, m, 2 * h1, h1, h1, float(np.float32(0.5)),
+                             float(np.float32(0.5))], (1, 1, 1))
+    mp.dispatch("n_conv8", [y1o if dependent else x2o, w2o, b2o, y2o, hi * hi, m, hi, hi, hi,
+                            c2 // 4, 9, 3, 1, 1, 1, 1, 0, *P.GELU_C, OFF_NONE], (1, 1, 1))
+    mp.output(y2o, hi * hi * m, (1, hi, hi, m))
+    mp.output(upo, 4 * h1 * h1 * m, (1, 2 * h1, 2 * h1, m))
+    mp.p.total_words = mp.words
+    sess = P.HipPlanSession(mp.p)
+    try:
+        got2, gotup = sess.run(None)
+        assert sess.launches() == (3 if dependent else 2)
+    finally:
+        sess.close()
+    assert_bitexact(got2, nhwc(ref2), "second conv")
+    assert_bitexact(gotup, nhwc(up), "upsampled first conv")
+
+
 DW_CASES = [
     # n, c, h, w, k, (sh, sw), (pt, pl, pb, pr), bias, act, residual
     (1, 16, 13, 12, 3, (1, 1), (1, 1, 1, 1), True, "none", False),
@@ -288,6 +336,54 @@ def test_plan_reduce_last_and_row_ops(gpu, oracle):
     assert np.all(m4[:, 1:] == 0.0)
     assert_bitexact(sub, oracle.binary_bcast(x, mean, rows, cp, 1, 0), "x - mean")
     assert_bitexact(div, oracle.binary_bcast(x, mean, rows, cp, 3, 0), "x / mean")
+
+
+@pytest.mark.parametrize("export_d", [False, True])
+def test_plan_layernorm_run_folds_into_one_launch(gpu, oracle, export_d):
+    """The nine dispatches PlanBuilder writes for a LayerNorm (n_reduce_last,
+    n_elem 8 / 9, n_reduce_last, n_elem 6 / 10 / 11, n_channel 0 / 1) run as
+    one LayerNorm launch when no intermediate is read elsewhere, and as nine
+    launches when one is (here x - mean, exported as a graph output); the
+    bits are the oracle's LayerNorm either way.  Rows 0 and 5 hold a huge
+    cancelling pair (their means take the sequential sum)."""
+    from qppocr_amd import plan as P
+    r = rng(13)
+    rows, cols, eps = 37, 256, 1e-6
+    x = (rnd(r, (rows, cols)) + 0.5).astype(np.float32)
+    x[0, 3], x[0, 7] = 1e15, -1e15
+    x[5, 9], x[5, 200] = -1e18, 1e18
+    g = (1.0 + rnd(r, (cols,), 0.1)).astype(np.float32)
+    bt = rnd(r, (cols,), 0.1)
+    mp = MiniPlan()
+    xo, go, bo = mp.static(x), mp.static(g), mp.static(bt)
+    eo = mp.static(np.array([eps], np.float32))
+    mo, vo, veo, so = (mp.alloc(rows * 4) for _ in range(4))
+    do, sqo, y0, y1, yo = (mp.alloc(rows * cols) for _ in range(5))
+    n = rows * cols
+    mp.dispatch("n_reduce_last", [xo, mo, rows, cols, cols, rows], (rows, 1, 1))
+    mp.dispatch("n_elem", [8, xo, mo, do, n, cols // 4, 0.0])
+    mp.dispatch("n_elem", [9, do, OFF_NONE, sqo, n, 0.0, 0.0])
+    mp.dispatch("n_reduce_last", [sqo, vo, rows, cols, cols, rows], (rows, 1, 1))
+    mp.dispatch("n_elem", [6, vo, eo, veo, 4 * rows, 0.0, 0.0])
+    mp.dispatch("n_elem", [10, veo, OFF_NONE, so, 4 * rows, 0.0, 0.0])
+    mp.dispatch("n_elem", [11, do, so, y0, n, cols // 4, 0.0])
+    mp.dispatch("n_channel", [0, y0, go, OFF_NONE, y1, n, cols, 0.0, 0.0, rows])
+    mp.dispatch("n_channel", [1, y1, bo, OFF_NONE, yo, n, cols, 0.0, 0.0, rows])
+    mp.output(yo, n, (rows, cols))
+    if export_d:
+        mp.output(do, n, (rows, cols))
+    mp.p.total_words = mp.words
+    sess = P.HipPlanSession(mp.p)
+    try:
+        outs = sess.run(None)
+        assert sess.launches() == (9 if export_d else 1)
+    finally:
+        sess.close()
+    ref = oracle.layernorm(x, g, bt, eps)
+    assert_bitexact(outs[0], ref, "plan LayerNorm")
+    if export_d:
+        mean = oracle.reduce_mean_last(x)
+        assert_bitexact(outs[1], oracle.binary_bcast(x, mean, rows, cols, 1, 0), "x - mean")
 
 
 ELEM_UNARY = [(0, None), (1, None), (2, (0.2, 0.5)), (2, (1.0 / 6.0, 0.5)), (3, (-0.5, 0.7)),
