@@ -230,13 +230,29 @@ struct ConvK {
   Act act;
 };
 
+// Whether the bias of output channel co at output row oy, column ox is
+// seeded into the chain (else added after it): bias_seeded's rule over the
+// GEMM the reference runs for the conv's kind (rule_kind 0: pointwise sgemm
+// over all P pixels; 1: one implicit GEMM per output row; 2: im2col tiles of
+// `tile` output rows).  32-bit arithmetic: the decoder keeps P N, and so
+// every index here, below 2^31.
+__device__ __forceinline__ bool conv_seeded_at(const ConvK& p, int co, int oy, int ox) {
+  const int N = (int)p.N, ow = (int)p.ow;
+  const bool mtail = co >= N - N % 4;
+  if (p.rule_kind == 0) {
+    const int P = (int)p.P, px = oy * ow + ox;
+    if (p.rule_path == 1) return px >= P - P % 32;
+    return P - (px & ~31) < 32 && mtail;
+  }
+  if (p.rule_kind == 1) return ow - (ox & ~31) < 32 && mtail;
+  const int tile = (int)p.tile, t0 = oy / tile * tile;
+  const int n = min(tile, (int)p.oh - t0) * ow, j = (oy - t0) * ow + ox;
+  return n - (j & ~31) < 32 && mtail;
+}
+
 __device__ __forceinline__ bool conv_seeded(const ConvK& p, int64_t co, int64_t px) {
-  if (p.rule_kind == 0) return bias_seeded(p.rule_path, co, px, p.N, p.P);
-  const int64_t oy = px / p.ow, ox = px - oy * p.ow;
-  if (p.rule_kind == 1) return bias_seeded(0, co, ox, p.N, p.ow);
-  const int64_t t0 = (oy / p.tile) * p.tile;
-  const int64_t rows = min(p.tile, p.oh - t0);
-  return bias_seeded(0, co, (oy - t0) * p.ow + ox, p.N, rows * p.ow);
+  const int oy = (int)px / (int)p.ow;
+  return conv_seeded_at(p, (int)co, oy, (int)px - oy * (int)p.ow);
 }
 
 constexpr int CONV_NB = 2;  // 16-pixel blocks per wave
@@ -598,25 +614,45 @@ __global__ __launch_bounds__(64) void plan_conv_dma_kernel(ConvK p) {
   }
 }
 
-// 3x3 convs with x-stride SW (the det neck and head over the NHWC arena):
-// a workgroup of NCB waves, one 16-channel output block each, owns 32
-// consecutive output pixels of one output row.  Per group of 4 input
-// channels it loads, once for all its waves, the 3 x (31 SW + 3) halo quads
-// those pixels read (slot r * HC + col: input row iy0 + r, column ix0 + col,
-// 0 outside the image) and the group's 36 weight rows (t * 4 + c) for all
-// its output blocks (past N: 0), by buffer->LDS loads; the B operand of tap
-// (ky, kx) and pixel j is then halo quad (ky, j * SW + kx).  Groups move
-// through a CONV_DMA_D-deep ring: before a group's steps each wave waits for
-// its own loads of that group, then a barrier (every wave's loads of it in,
-// every wave's reads of the previous buffer done) frees the previous buffer
-// for the refill.  Chain order (k = c * 9 + t within a group), bias rule and
-// epilogue are plan_conv_dma_kernel's, so the outputs are the same bits with
-// the halo loaded once instead of once per tap and per output block.
-template <int SW>
+// 3x3 convs with stride SW in both directions (the det neck and head over
+// the NHWC arena): a workgroup of 2 NCB waves owns 32 consecutive output
+// pixels of 2 output rows, wave w computing row w / NCB for the 16-channel
+// output block w % NCB.  A stage holds HALO_CG groups of 4 input channels:
+// per group the HR x HC halo quads the tile reads (input row iy0 + r, column
+// ix0 + col, 0 outside the image) and the group's 36 weight rows (t * 4 + c)
+// for all output blocks (past N: 0), loaded once for every wave by
+// buffer->LDS loads through a HALO_D-deep ring.  One stage ahead of its
+// steps, the waves copy a stage's halo quads into a channel-planar buffer
+// (word (cg * 4 + c) PL + r RP + col): every lane of one MFMA step reads the
+// same input channel, which the 16-byte quads would put on one bank in four;
+// the row and plane pitches place the rows one step reads on separate banks.
+// The weight rows are stored rotated: unit (t, c, block u) of 16 floats at
+// 4 (t NCB + u) + ((t + c + u) & 3), so the four k rows of a step (four
+// consecutive k, whose t + c runs through four consecutive values) are on
+// four different bank quarters.  Chain order (k = c * 9 + t within a group,
+// groups in order), bias rule and epilogue are plan_conv_dma_kernel's, so the
+// outputs are the same bits with the halo and weights loaded once per tile
+// instead of once per tap and output block.
+#define HALO_CG 2   // channel groups per stage
+#define HALO_D 4    // DMA ring depth
+#define HALO_LEAD 6 // steps the operand reads run ahead
+template <int SW, int NCB>
 struct HaloGeom {
+  static constexpr int W = 2 * NCB;                    // waves
+  static constexpr int HR = SW + 3;                    // halo rows (2 output rows)
   static constexpr int HC = 31 * SW + 3;               // halo columns
-  static constexpr int HQ = 3 * HC;                    // halo quads per group
-  static constexpr int HQP = (HQ + 63) / 64 * 64;      // their slots (whole loads)
+  static constexpr int HQ = HR * HC;                   // halo quads per group
+  static constexpr int HQP = (HALO_CG * HQ + 63) / 64 * 64;   // halo slots (whole loads)
+  static constexpr int WG = 144 * NCB;                 // weight quads per group
+  static constexpr int L = (HQP + HALO_CG * WG + 64 * W - 1) / (64 * W);   // loads per wave
+  static constexpr int BUF = L * 64 * W;               // float4 per ring stage
+  // planar pitches (words): a row RP, a channel plane PL; RP and PL - 2 RP
+  // are 16..47 mod 64 (stride 1) or 32 mod 64 (stride 2, 33-word row spans)
+  static constexpr int RP = SW == 1 ? 40 : 96;
+  static constexpr int PL = SW == 1 ? 176 : 480;
+  static constexpr int PW = HALO_CG * 4 * PL;          // planar words per stage
+  static_assert(PL >= HR * RP && RP >= HC, "planar pitches too small");
+  static constexpr size_t lds() { return (size_t)HALO_D * BUF * 16 + 2 * (size_t)PW * 4; }
 };
 
 // Up to four independent such convs of one batch count, one launch: conv m
@@ -633,48 +669,60 @@ struct HaloGroup {
 template <int SW, int NCB>
 __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x, int tile,
                                                     float4* ring) {
-  using G = HaloGeom<SW>;
-  constexpr int WC = 36 * 4 * NCB;                     // weight chunks per group
-  constexpr int L = (G::HQP + WC + 64 * NCB - 1) / (64 * NCB);   // loads per wave per group
-  constexpr int BUF = L * 64 * NCB;                    // float4 per group buffer
+  using G = HaloGeom<SW, NCB>;
+  constexpr int L = G::L;
+  float* planar = (float*)(ring + HALO_D * G::BUF);   // 2 x PW words
   const int b = blockIdx.y;
   const unsigned rn = real_n(p.arena);
   if (rn != 0 && (unsigned)b >= rn) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int N = (int)p.N, ow = (int)p.ow, P = (int)p.P;
-  const int oy = tile / tiles_x, ox0 = (tile - oy * tiles_x) * 32;
+  const int row = wave / NCB, ub = wave - row * NCB, co0 = ub * 16;
+  const int N = (int)p.N, ow = (int)p.ow, P = (int)p.P, oh = P / ow;
+  const int ty = tile / tiles_x, oy0 = 2 * ty, ox0 = (tile - ty * tiles_x) * 32;
+  const int oy = oy0 + row;
   const int li = lane & 15, kq = lane >> 4;
-  const int co0 = wave * 16;
   const int cin = (int)p.cin, iw = (int)p.iw, ih = (int)p.ih;
-  const int iy0 = oy * (int)p.sh - (int)p.pt, ix0 = ox0 * SW - (int)p.pl;
+  const int groups = cin / 4, stages = (groups + HALO_CG - 1) / HALO_CG;
+  const int iy0 = oy0 * SW - (int)p.pt, ix0 = ox0 * SW - (int)p.pl;
   const unsigned OOB = 0x80000000u;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.x + (size_t)b * ih * iw * cin), 0, ih * iw * cin * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.w, 0, 9 * cin * N * 4, 0x00020000);
   // this wave's loads: slots 64 (L wave + i) + lane; halo slots [0, HQP),
-  // weight slots [HQP, HQP + WC): every load is wholly one or the other
-  int off[L];
+  // weight slots [HQP, HQP + CG WG): every load is wholly one or the other.
+  // off: word offset at stage 0 (-1 reads 0); cg: the slot's channel group
+  int off[L], cgs[L];
 #pragma unroll
   for (int i = 0; i < L; i++) {
     const int s = 64 * (L * wave + i) + lane;
     off[i] = -1;
-    if (s < G::HQ) {
-      const int r = s / G::HC, col = s - r * G::HC, iy = iy0 + r, ix = ix0 + col;
-      if ((unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw) off[i] = (iy * iw + ix) * cin;
-    } else if (s >= G::HQP && s < G::HQP + WC) {
-      const int w = s - G::HQP, row = w / (4 * NCB), j = w - row * (4 * NCB);
-      const int t = row >> 2, c = row & 3;
-      if (4 * j < N) off[i] = (t * cin + c) * N + 4 * j;
+    cgs[i] = 0;
+    if (s < HALO_CG * G::HQ) {
+      const int cg = s / G::HQ, h = s - cg * G::HQ;
+      const int r = h / G::HC, col = h - r * G::HC, iy = iy0 + r, ix = ix0 + col;
+      cgs[i] = cg;
+      if ((unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw)
+        off[i] = (iy * iw + ix) * cin + 4 * cg;
+    } else if (s >= G::HQP && s < G::HQP + HALO_CG * G::WG) {
+      // rotated weight units: unit position up = 4 (t NCB + u) + ((t + c + u) & 3)
+      const int w = s - G::HQP, cg = w / G::WG, w2 = w - cg * G::WG;
+      const int up = w2 >> 2, qq = w2 & 3, tu = up >> 2;
+      const int t = tu / NCB, u = tu - t * NCB, c = ((up & 3) - t - u) & 3;
+      const int co = 16 * u + 4 * qq;
+      cgs[i] = cg;
+      if (co < N) off[i] = (t * cin + 4 * cg + c) * N + co;
     }
   }
-  auto issue = [&](int g) {
-    float4* buf = ring + (g % CONV_DMA_D) * BUF;
+  auto issue = [&](int st) {
+    float4* buf = ring + (st % HALO_D) * G::BUF;
 #pragma unroll
     for (int i = 0; i < L; i++) {
       const bool isx = 64 * (L * wave + i) < G::HQP;   // wave-uniform
-      const unsigned o = off[i] < 0 ? OOB : (unsigned)((off[i] + (isx ? 4 * g : 4 * g * N)) * 4);
+      const bool live = off[i] >= 0 && HALO_CG * st + cgs[i] < groups;
+      const unsigned o =
+          live ? (unsigned)((off[i] + (isx ? 4 * HALO_CG * st : 4 * HALO_CG * st * N)) * 4) : OOB;
       const unsigned m = __builtin_amdgcn_readfirstlane(
           (unsigned)(uintptr_t)(__attribute__((address_space(3))) float4*)(buf + 64 * (L * wave + i)));
 #pragma clang diagnostic push
@@ -685,45 +733,102 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
 #pragma clang diagnostic pop
     }
   };
+  // a stage's halo quads -> its planar buffer
+  auto to_planar = [&](int st) {
+    const float4* q = ring + (st % HALO_D) * G::BUF;
+    float* pb = planar + (st & 1) * G::PW;
+    for (int s = tid; s < HALO_CG * G::HQ; s += 64 * G::W) {
+      const int cg = s / G::HQ, h = s - cg * G::HQ, r = h / G::HC, col = h - r * G::HC;
+      const float4 v = q[s];
+      float* d = pb + cg * 4 * G::PL + r * G::RP + col;
+      d[0] = v.x;
+      d[G::PL] = v.y;
+      d[2 * G::PL] = v.z;
+      d[3 * G::PL] = v.w;
+    }
+  };
   f32x4 acc[2];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
-    const int ox = ox0 + 16 * j + li, px = oy * ow + ox;
+    const int ox = ox0 + 16 * j + li;
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       const int co = co0 + 4 * kq + v;
-      acc[j][v] = (p.bias && co < N && ox < ow && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
+      acc[j][v] = (p.bias && co < N && ox < ow && oy < oh && conv_seeded_at(p, co, oy, ox))
+                      ? p.bias[co]
+                      : 0.0f;
     }
   }
-  const int groups = cin / 4;
+  // the steps of the first NG channel groups of a stage (k = c * 9 + t
+  // within a group): every operand read from LDS first, then two MFMAs a
+  // step, the reads HALO_LEAD steps ahead of their use (left to itself the
+  // scheduler reads each step's operands just before its MFMAs)
+  auto steps = [&](auto ngc, int st) {
+    constexpr int NS = 9 * decltype(ngc)::value;
+    const float* pb = planar + (st & 1) * G::PW;
+    const float* wq = (const float*)(ring + (st % HALO_D) * G::BUF + G::HQP);
+    float av[NS], bv[NS][2];
 #pragma unroll
-  for (int g = 0; g < CONV_DMA_D - 1; g++)
-    if (g < groups) issue(g);
-  for (int g = 0; g < groups; g++) {
-    const int ahead = min(CONV_DMA_D - 2, groups - 1 - g);   // groups issued after g
-    switch (ahead) {
-      case 2: wait_vmcnt<2 * L>(); break;
-      case 1: wait_vmcnt<L>(); break;
-      default: wait_vmcnt<0>(); break;
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the previous buffer are back
-    __builtin_amdgcn_s_barrier();         // and every wave's; group g is in for all
-    __asm__ volatile("" ::: "memory");
-    if (g + CONV_DMA_D - 1 < groups) issue(g + CONV_DMA_D - 1);   // into the buffer of g - 1
-    const float* hq = (const float*)(ring + (g % CONV_DMA_D) * BUF);
-    const float* wq = hq + 4 * G::HQP;
-#pragma unroll
-    for (int u = 0; u < 9; u++) {
+    for (int s = 0; s < NS; s++) {
+      const int cg = s / 9, u = s - cg * 9;
       const int k = 4 * u + kq, c = k / 9, t = k - c * 9, ky = t / 3, kx = t - ky * 3;
-      const float a = wq[(4 * t + c) * (16 * NCB) + co0 + li];
+      av[s] = wq[4 * G::WG * cg + (4 * (t * NCB + ub) + ((t + c + ub) & 3)) * 16 + li];
 #pragma unroll
       for (int j = 0; j < 2; j++)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-            a, hq[(ky * G::HC + (16 * j + li) * SW + kx) * 4 + c], acc[j], 0, 0, 0);
+        bv[s][j] = pb[(cg * 4 + c) * G::PL + (row * SW + ky) * G::RP + (16 * j + li) * SW + kx];
     }
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s][j], acc[j], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3 * HALO_LEAD, 0);
+#pragma unroll
+    for (int s = HALO_LEAD; s < NS; s++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * HALO_LEAD, 0);
+  };
+  // ring: stage st computes from its weights (ring slot st) and planar copy,
+  // stage st + 1 is copied to planar, st + 2 and st + 3 are loading
+#pragma unroll
+  for (int st = 0; st < HALO_D - 1; st++)
+    if (st < stages) issue(st);
+  {
+    const int ahead = min(HALO_D - 2, stages - 1);   // stages issued after 0
+    if (ahead >= 2)
+      wait_vmcnt<2 * L>();
+    else if (ahead == 1)
+      wait_vmcnt<L>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();   // stage 0 is in for all
+    __asm__ volatile("" ::: "memory");
+    to_planar(0);
+  }
+  for (int st = 0; st < stages; st++) {
+    if (st + 1 < stages) {
+      if (st + 2 < stages)   // this wave's loads of st + 1 in; st + 2 may load
+        wait_vmcnt<L>();
+      else
+        wait_vmcnt<0>();
+    }
+    // every wave's: loads of st + 1 in, planar copy of st written, reads of
+    // the planar copy and ring slot of st - 1 done
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    if (st + HALO_D - 1 < stages) issue(st + HALO_D - 1);   // into the ring slot of st - 1
+    if (st + 1 < stages) to_planar(st + 1);
+    if (HALO_CG * st + HALO_CG <= groups)
+      steps(std::integral_constant<int, HALO_CG>{}, st);
+    else
+      steps(std::integral_constant<int, 1>{}, st);   // the odd last group
   }
   const int cob = co0 + 4 * kq;
-  if (cob >= N) return;
+  if (cob >= N || oy >= oh) return;
   const float* yres = p.res ? p.res + (size_t)b * P * N : nullptr;
   float* yb = p.y + (size_t)b * P * N;
 #pragma unroll
@@ -735,7 +840,7 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       float x = acc[j][v];
-      if (p.bias && !conv_seeded(p, cob + v, px)) x = x + p.bias[cob + v];
+      if (p.bias && !conv_seeded_at(p, cob + v, oy, ox)) x = x + p.bias[cob + v];
       x = act_apply(x, p.act);
       if (yres) x = x + yres[px * N + cob + v];
       o[v] = x;
@@ -745,19 +850,111 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
 }
 
 template <int SW, int NCB>
-__global__ __launch_bounds__(64 * NCB) void plan_conv_halo_kernel(ConvK p, int tiles_x) {
+__global__ __launch_bounds__(128 * NCB) void plan_conv_halo_kernel(ConvK p, int tiles_x) {
   extern __shared__ float4 ring[];
   plan_conv_halo_tile<SW, NCB>(p, tiles_x, (int)blockIdx.x, ring);
 }
 
 template <int SW, int NCB>
-__global__ __launch_bounds__(64 * NCB) void plan_conv_halo_group_kernel(HaloGroup g) {
+__global__ __launch_bounds__(128 * NCB) void plan_conv_halo_group_kernel(HaloGroup g) {
   extern __shared__ float4 ring[];
   const int t = (int)blockIdx.x;   // < start[HALO_GROUP_MAX]: the grid is the total
   int m = 0;
 #pragma unroll
   for (int i = 1; i < HALO_GROUP_MAX; i++) m += t >= g.start[i] ? 1 : 0;
   plan_conv_halo_tile<SW, NCB>(g.k[m], g.tiles_x[m], t - g.start[m], ring);
+}
+
+// ------------------------------------------------------ pointwise, small K
+// A 1x1 conv with K = 4 KS input channels (16 or 32: the det blocks' first
+// pointwise convs and the 32-channel lateral) over the NHWC rows as one GEMM,
+// rows = pixels (m = nb P), columns = channels: a wave owns 16 channels x 32
+// pixels.  Its 32 input rows arrive by 16-byte loads (consecutive lanes,
+// consecutive words) into a wave-private LDS area, read back per step in the
+// MFMA layout (lane (li, kq): x[px0 + 16 j + li][4 s + kq], row pitch K + 1
+// so the 16 rows of one read are on different banks); the weights
+// W[4 s + kq][co0 + li] come straight from memory.  The chain is KS
+// v_mfma_f32_16x16x4f32 in k order from +0, then + bias, the activation and
+// the residual: gemm_skinny_kernel's chain and epilogue for this shape.
+struct PwK {
+  const float* x; const float* w; const float* bias; const float* res; float* y;
+  int m, n;
+  Act act;
+};
+
+template <int KS>
+__global__ __launch_bounds__(256) void plan_pw_kernel(PwK p) {
+  constexpr int K = 4 * KS, RP = K + 1, Q = 32 * KS / 64;   // Q float4 loads per lane
+  __shared__ float tile[4][32 * RP];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wave = (int)blockIdx.x * 4 + wv;
+  const int li = lane & 15, kq = lane >> 4;
+  const int nco = (p.n + 15) >> 4;
+  const int pt = wave / nco, co0 = (wave - pt * nco) * 16, px0 = pt * 32;
+  if (px0 >= p.m) return;
+  const int N = p.n, M = p.m;
+  float* t = tile[wv];
+  // the 32 x K input rows: load q covers float4 q * 64 + lane (row r, quad c)
+  float4 xv[Q];
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    const int f = q * 64 + lane, r = f / KS, c = f - r * KS;
+    xv[q] = px0 + r < M ? ((const float4*)p.x)[(px0 + r) * KS + c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float a[KS];
+  const int co = co0 + li;
+#pragma unroll
+  for (int s = 0; s < KS; s++) a[s] = co < N ? p.w[(4 * s + kq) * N + co] : 0.0f;
+  // epilogue terms, their latency under the chain
+  const int cob = co0 + 4 * kq;
+  float bv[4], rv[2][4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) bv[v] = p.bias && cob < N ? p.bias[cob + v] : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int px = px0 + 16 * j + li;
+#pragma unroll
+    for (int v = 0; v < 4; v++) rv[j][v] = p.res && cob < N && px < M ? p.res[px * N + cob + v] : 0.0f;
+  }
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    const int f = q * 64 + lane, r = f / KS, c = f - r * KS;
+    float* d = t + r * RP + 4 * c;
+    d[0] = xv[q].x;
+    d[1] = xv[q].y;
+    d[2] = xv[q].z;
+    d[3] = xv[q].w;
+  }
+  // the area is this wave's alone: a wave-scope fence orders the writes
+  // before the reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  f32x4 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < KS; s++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], t[(16 * j + li) * RP + 4 * s + kq], acc[j],
+                                                    0, 0, 0);
+  if (cob >= N) return;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int px = px0 + 16 * j + li;
+    if (px >= M) continue;
+    float o[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float x = acc[j][v];
+      if (p.bias) x = x + bv[v];
+      x = act_apply(x, p.act);
+      if (p.res) x = x + rv[j][v];
+      o[v] = x;
+    }
+    *(float4*)(p.y + px * N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+  }
 }
 
 // ------------------------------------------------------------- depthwise
@@ -794,6 +991,67 @@ __global__ __launch_bounds__(256) void plan_dw_kernel(DwK p) {
   float4 o = act4(add4(acc, bv), p.act);
   if (p.res) o = add4(o, ((const float4*)p.res)[b * p.P * p.c4 + gid]);
   ((float4*)p.y)[b * p.P * p.c4 + gid] = o;
+}
+
+// The same depthwise with 4 adjacent output pixels of one channel quad per
+// thread (KH x KW taps, x-stride SW, any y-stride): the taps' weight quads
+// sit in registers and each input row's 3 SW + KW quads are read once for
+// the 4 outputs; threads run channel quads fastest (16-byte loads and stores
+// of consecutive lanes are contiguous).  Each output's chain is plan_dw_kernel's.
+template <int KH, int KW, int SW>
+__global__ __launch_bounds__(256) void plan_dw_px_kernel(DwK p) {
+  constexpr int NC = 3 * SW + KW;   // input columns a thread reads per row
+  const int64_t b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && b >= rn) return;
+  const int64_t ngx = (p.ow + 3) / 4;
+  const int64_t oh = p.P / p.ow;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= oh * ngx * p.c4) return;
+  const int64_t c4 = gid % p.c4, m = gid / p.c4;
+  const int64_t oy = m / ngx, ox0 = (m - oy * ngx) * 4;
+  const float4* xb = (const float4*)p.x + b * p.ih * p.iw * p.c4;
+  const float4* w4 = (const float4*)p.w;
+  float4 wv[KH * KW];
+#pragma unroll
+  for (int t = 0; t < KH * KW; t++) wv[t] = w4[t * p.c4 + c4];
+  float4 acc[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) acc[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int ky = 0; ky < KH; ky++) {
+    const int64_t iy = oy * p.sh - p.pt + ky;
+    const bool rok = iy >= 0 && iy < p.ih;
+    float4 xv[NC];
+#pragma unroll
+    for (int cc = 0; cc < NC; cc++) {
+      const int64_t ix = ox0 * SW - p.pl + cc;
+      xv[cc] = (rok && ix >= 0 && ix < p.iw) ? xb[(iy * p.iw + ix) * p.c4 + c4]
+                                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int kx = 0; kx < KW; kx++) {
+      const float4 w = wv[ky * KW + kx];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float4 x = xv[q * SW + kx];
+        acc[q].x = __builtin_fmaf(w.x, x.x, acc[q].x);
+        acc[q].y = __builtin_fmaf(w.y, x.y, acc[q].y);
+        acc[q].z = __builtin_fmaf(w.z, x.z, acc[q].z);
+        acc[q].w = __builtin_fmaf(w.w, x.w, acc[q].w);
+      }
+    }
+  }
+  // yc = acc + bv with bv = 0 when there is no bias (conv.rs:461-505)
+  const float4 bv = p.bias ? ((const float4*)p.bias)[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (ox0 + q >= p.ow) break;
+    const int64_t e = (oy * p.ow + ox0 + q) * p.c4 + c4;
+    float4 o = act4(add4(acc[q], bv), p.act);
+    if (p.res) o = add4(o, ((const float4*)p.res)[b * p.P * p.c4 + e]);
+    ((float4*)p.y)[b * p.P * p.c4 + e] = o;
+  }
 }
 
 // ------------------------------------------------------- conv transpose
@@ -1213,11 +1471,6 @@ int add_launch(qph_plan* pl, int dispatch, std::function<int(hipStream_t)> f) {
 
 struct PendingHw { uint32_t in, scratch; int64_t m, c, nb; };
 
-size_t halo_lds(int sw, int ncb) {
-  const int hqp = sw == 1 ? HaloGeom<1>::HQP : HaloGeom<2>::HQP;
-  const int l = (hqp + 144 * ncb + 64 * ncb - 1) / (64 * ncb);
-  return (size_t)CONV_DMA_D * l * 64 * ncb * 16;
-}
 
 // A 3x3 halo conv joins the open group (and launches with its first member,
 // earlier in the launch order) when: the group has room and the same
@@ -1252,7 +1505,7 @@ bool join_halo_group(Decoder& d, const ConvK& k, int tiles_x, int64_t oh, int sw
   const int i = h.n++;
   g.k[i] = k;
   g.tiles_x[i] = tiles_x;
-  g.start[i + 1] = g.start[i] + (int)(oh * tiles_x);
+  g.start[i + 1] = g.start[i] + (int)((oh + 1) / 2 * tiles_x);
   for (int j = i + 2; j <= HALO_GROUP_MAX; j++) g.start[j] = g.start[i + 1];
   h.reads = reads;
   for (const auto& r : rd) h.reads.push_back(r);
@@ -1322,6 +1575,20 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
         la.res = e.res == OFF_NONE ? nullptr : d.at(e.res);
         return add_launch(d.pl, d.idx, [la](hipStream_t s) { return launch_linear_nt(la, s); });
       }
+      if ((cin == 16 || cin == 32) && nb * P * N < (1ll << 31) && nb * P * cin < (1ll << 31) &&
+          e.y % 4 == 0 && (e.res == OFF_NONE || e.res % 4 == 0)) {
+        PwK k{x, wt, e.bias == OFF_NONE ? nullptr : d.at(e.bias),
+              e.res == OFF_NONE ? nullptr : d.at(e.res), d.at(e.y), (int)(nb * P), (int)N, e.act};
+        const int64_t waves = ((N + 15) / 16) * ((nb * P + 31) / 32);
+        const unsigned blocks = (unsigned)((waves + 3) / 4);
+        return add_launch(d.pl, d.idx, [k, blocks, cin](hipStream_t s) {
+          if (cin == 16)
+            hipLaunchKernelGGL(plan_pw_kernel<4>, dim3(blocks), dim3(256), 0, s, k);
+          else
+            hipLaunchKernelGGL(plan_pw_kernel<8>, dim3(blocks), dim3(256), 0, s, k);
+          return launch_check("plan_pw_kernel");
+        });
+      }
       GemmArgs g{};
       g.a = x; g.lda = cin; g.a_batch = 0;
       g.b = wt; g.ldb = N; g.b_batch = 0;
@@ -1354,7 +1621,7 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
   k.y = d.at(e.y);
   const int64_t lwaves = ((N + 15) / 16) * ((P + 31) / 32);
   // 3x3 convs with up to four 16-channel output blocks: the halo kernel
-  if (kh == 3 && kw == 3 && (sw == 1 || sw == 2) && N <= 64 && cin >= 8 &&
+  if (kh == 3 && kw == 3 && (sw == 1 || sw == 2) && sh == sw && N <= 64 && cin >= 8 &&
       9 * cin * N * 4 < (1ll << 31) && ih * iw * cin * 4 < (1ll << 31) &&
       oh * ((ow + 31) / 32) < (1ll << 31)) {
     const int tiles_x = (int)((ow + 31) / 32), ncb = (int)((N + 15) / 16);
@@ -1378,18 +1645,18 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
     d.halo.reads = rd;
     d.halo.writes = {wr};
     g->start[0] = 0;
-    for (int i = 1; i <= HALO_GROUP_MAX; i++) g->start[i] = (int)(oh * tiles_x);
-    const size_t lds = halo_lds((int)sw, ncb);
+    for (int i = 1; i <= HALO_GROUP_MAX; i++) g->start[i] = (int)((oh + 1) / 2 * tiles_x);
     const unsigned nbu = (unsigned)nb;
 #define QPH_HALO(S, C)                                                                      \
   if (sw == S && ncb == C)                                                                  \
-    return add_launch(d.pl, d.idx, [g, lds, nbu](hipStream_t s) {                           \
+    return add_launch(d.pl, d.idx, [g, nbu](hipStream_t s) {                                \
       const dim3 grid((unsigned)g->start[HALO_GROUP_MAX], nbu);                             \
+      const size_t lds = HaloGeom<S, C>::lds();                                             \
       if (g->start[1] == g->start[HALO_GROUP_MAX])                                          \
-        hipLaunchKernelGGL((plan_conv_halo_kernel<S, C>), grid, dim3(64 * C), lds, s,       \
+        hipLaunchKernelGGL((plan_conv_halo_kernel<S, C>), grid, dim3(128 * C), lds, s,      \
                            g->k[0], g->tiles_x[0]);                                         \
       else                                                                                  \
-        hipLaunchKernelGGL((plan_conv_halo_group_kernel<S, C>), grid, dim3(64 * C), lds, s, \
+        hipLaunchKernelGGL((plan_conv_halo_group_kernel<S, C>), grid, dim3(128 * C), lds, s,\
                            *g);                                                             \
       return launch_check("plan_conv_halo_kernel");                                         \
     });
@@ -1621,6 +1888,18 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       DwK k{pl->arena, d.at(w[0]), d.at(w[1]), w[2] == OFF_NONE ? nullptr : d.at(w[2]),
             e.res == OFF_NONE ? nullptr : d.at(e.res), d.at(e.y),
             P, C / 4, ow, iw, ih, taps, kw, sh, sw, pt, pl_, e.act};
+      const int64_t kh = taps / kw;
+      if (((kh == 3 && kw == 3) || (kh == 5 && kw == 5)) && (sw == 1 || sw == 2)) {
+        const int64_t threads = (P / ow) * ((ow + 3) / 4) * (C / 4);
+        return add_launch(pl, d.idx, [k, nb, threads, kh, sw](hipStream_t s) {
+          const dim3 grid(blocks_for(threads), (unsigned)nb);
+          if (kh == 3 && sw == 1) hipLaunchKernelGGL((plan_dw_px_kernel<3, 3, 1>), grid, dim3(256), 0, s, k);
+          else if (kh == 3) hipLaunchKernelGGL((plan_dw_px_kernel<3, 3, 2>), grid, dim3(256), 0, s, k);
+          else if (sw == 1) hipLaunchKernelGGL((plan_dw_px_kernel<5, 5, 1>), grid, dim3(256), 0, s, k);
+          else hipLaunchKernelGGL((plan_dw_px_kernel<5, 5, 2>), grid, dim3(256), 0, s, k);
+          return launch_check("plan_dw_px_kernel");
+        });
+      }
       return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
         hipLaunchKernelGGL(plan_dw_kernel, dim3(blocks_for(k.P * k.c4), (unsigned)nb), dim3(256), 0,
                            s, k);

@@ -87,6 +87,16 @@ CONV_CASES = [
     (1, 16, 10, 10, 8, 1, 1, (2, 2), (0, 0, 0, 0), True, "none", False),    # 1x1 stride 2: general
     (1, 8, 7, 8, 4, 2, 2, (1, 1), (0, 0, 1, 1), False, "none", False),      # SAME_UPPER 2x2, no bias
     (3, 20, 6, 6, 36, 3, 3, (1, 1), (1, 1, 1, 1), True, "gelu", False),     # N odd vec4 count: n_conv
+    # the 3x3 halo tiles (2 output rows, 2 channel groups a stage): stride 2
+    # with an odd row count; 4 output blocks, 5 stages through the 3-deep
+    # ring, 3 column tiles; stride 2 with 3 blocks, an odd group count, no bias
+    (1, 16, 21, 19, 24, 3, 3, (2, 2), (1, 1, 1, 1), True, "relu", False),
+    (2, 40, 13, 70, 64, 3, 3, (1, 1), (1, 1, 1, 1), True, "none", True),
+    (1, 28, 23, 66, 48, 3, 3, (2, 2), (1, 1, 1, 1), False, "gelu", False),
+    # pointwise with 16 input channels (register-operand kernel): batch 2,
+    # a row count off the 32-pixel tiles, residual; and without bias
+    (2, 16, 9, 13, 40, 1, 1, (1, 1), (0, 0, 0, 0), True, "relu", True),
+    (1, 16, 12, 12, 20, 1, 1, (1, 1), (0, 0, 0, 0), False, "none", False),
 ]
 
 
