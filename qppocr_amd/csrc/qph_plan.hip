@@ -42,6 +42,7 @@
 #include <functional>
 #include <memory>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "qph_internal.h"
@@ -621,20 +622,17 @@ __global__ __launch_bounds__(64) void plan_conv_dma_kernel(ConvK p) {
 // per group the HR x HC halo quads the tile reads (input row iy0 + r, column
 // ix0 + col, 0 outside the image) and the group's 36 weight rows (t * 4 + c)
 // for all output blocks (past N: 0), loaded once for every wave by
-// buffer->LDS loads through a HALO_D-deep ring.  One stage ahead of its
-// steps, the waves copy a stage's halo quads into a channel-planar buffer
-// (word (cg * 4 + c) PL + r RP + col): every lane of one MFMA step reads the
-// same input channel, which the 16-byte quads would put on one bank in four;
-// the row and plane pitches place the rows one step reads on separate banks.
-// The weight rows are stored rotated: unit (t, c, block u) of 16 floats at
-// 4 (t NCB + u) + ((t + c + u) & 3), so the four k rows of a step (four
-// consecutive k, whose t + c runs through four consecutive values) are on
-// four different bank quarters.  Chain order (k = c * 9 + t within a group,
+// buffer->LDS loads through a HALO_D-deep ring.  The weight rows are stored
+// rotated: unit (t, c, block u) of 16 floats at 4 (t NCB + u) + ((t + c + u)
+// & 3), so the four k rows of a step (four consecutive k, whose t + c runs
+// through four consecutive values) are on four different bank quarters.
+// (A channel-planar copy of the halo, which would do the same for the B
+// reads, measured no faster and its LDS cost a workgroup per CU.)  Chain order (k = c * 9 + t within a group,
 // groups in order), bias rule and epilogue are plan_conv_dma_kernel's, so the
 // outputs are the same bits with the halo and weights loaded once per tile
 // instead of once per tap and output block.
 #define HALO_CG 2   // channel groups per stage
-#define HALO_D 4    // DMA ring depth
+#define HALO_D 3    // DMA ring depth
 #define HALO_LEAD 6 // steps the operand reads run ahead
 template <int SW, int NCB>
 struct HaloGeom {
@@ -646,13 +644,7 @@ struct HaloGeom {
   static constexpr int WG = 144 * NCB;                 // weight quads per group
   static constexpr int L = (HQP + HALO_CG * WG + 64 * W - 1) / (64 * W);   // loads per wave
   static constexpr int BUF = L * 64 * W;               // float4 per ring stage
-  // planar pitches (words): a row RP, a channel plane PL; RP and PL - 2 RP
-  // are 16..47 mod 64 (stride 1) or 32 mod 64 (stride 2, 33-word row spans)
-  static constexpr int RP = SW == 1 ? 40 : 96;
-  static constexpr int PL = SW == 1 ? 176 : 480;
-  static constexpr int PW = HALO_CG * 4 * PL;          // planar words per stage
-  static_assert(PL >= HR * RP && RP >= HC, "planar pitches too small");
-  static constexpr size_t lds() { return (size_t)HALO_D * BUF * 16 + 2 * (size_t)PW * 4; }
+  static constexpr size_t lds() { return (size_t)HALO_D * BUF * 16; }
 };
 
 // Up to four independent such convs of one batch count, one launch: conv m
@@ -671,7 +663,6 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
                                                     float4* ring) {
   using G = HaloGeom<SW, NCB>;
   constexpr int L = G::L;
-  float* planar = (float*)(ring + HALO_D * G::BUF);   // 2 x PW words
   const int b = blockIdx.y;
   const unsigned rn = real_n(p.arena);
   if (rn != 0 && (unsigned)b >= rn) return;
@@ -733,20 +724,6 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
 #pragma clang diagnostic pop
     }
   };
-  // a stage's halo quads -> its planar buffer
-  auto to_planar = [&](int st) {
-    const float4* q = ring + (st % HALO_D) * G::BUF;
-    float* pb = planar + (st & 1) * G::PW;
-    for (int s = tid; s < HALO_CG * G::HQ; s += 64 * G::W) {
-      const int cg = s / G::HQ, h = s - cg * G::HQ, r = h / G::HC, col = h - r * G::HC;
-      const float4 v = q[s];
-      float* d = pb + cg * 4 * G::PL + r * G::RP + col;
-      d[0] = v.x;
-      d[G::PL] = v.y;
-      d[2 * G::PL] = v.z;
-      d[3 * G::PL] = v.w;
-    }
-  };
   f32x4 acc[2];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
@@ -765,8 +742,8 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
   // scheduler reads each step's operands just before its MFMAs)
   auto steps = [&](auto ngc, int st) {
     constexpr int NS = 9 * decltype(ngc)::value;
-    const float* pb = planar + (st & 1) * G::PW;
-    const float* wq = (const float*)(ring + (st % HALO_D) * G::BUF + G::HQP);
+    const float* hq = (const float*)(ring + (st % HALO_D) * G::BUF);
+    const float* wq = hq + 4 * G::HQP;
     float av[NS], bv[NS][2];
 #pragma unroll
     for (int s = 0; s < NS; s++) {
@@ -775,7 +752,7 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
       av[s] = wq[4 * G::WG * cg + (4 * (t * NCB + ub) + ((t + c + ub) & 3)) * 16 + li];
 #pragma unroll
       for (int j = 0; j < 2; j++)
-        bv[s][j] = pb[(cg * 4 + c) * G::PL + (row * SW + ky) * G::RP + (16 * j + li) * SW + kx];
+        bv[s][j] = hq[4 * (cg * G::HQ + (row * SW + ky) * G::HC + (16 * j + li) * SW + kx) + c];
     }
 #pragma unroll
     for (int s = 0; s < NS; s++)
@@ -790,38 +767,18 @@ __device__ __forceinline__ void plan_conv_halo_tile(const ConvK& p, int tiles_x,
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 2 * HALO_LEAD, 0);
   };
-  // ring: stage st computes from its weights (ring slot st) and planar copy,
-  // stage st + 1 is copied to planar, st + 2 and st + 3 are loading
 #pragma unroll
   for (int st = 0; st < HALO_D - 1; st++)
     if (st < stages) issue(st);
-  {
-    const int ahead = min(HALO_D - 2, stages - 1);   // stages issued after 0
-    if (ahead >= 2)
-      wait_vmcnt<2 * L>();
-    else if (ahead == 1)
+  for (int st = 0; st < stages; st++) {
+    if (st + 1 < stages)   // this wave's loads of st in; st + 1 may load
       wait_vmcnt<L>();
     else
       wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();   // stage 0 is in for all
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the previous buffer are back
+    __builtin_amdgcn_s_barrier();         // and every wave's; stage st is in for all
     __asm__ volatile("" ::: "memory");
-    to_planar(0);
-  }
-  for (int st = 0; st < stages; st++) {
-    if (st + 1 < stages) {
-      if (st + 2 < stages)   // this wave's loads of st + 1 in; st + 2 may load
-        wait_vmcnt<L>();
-      else
-        wait_vmcnt<0>();
-    }
-    // every wave's: loads of st + 1 in, planar copy of st written, reads of
-    // the planar copy and ring slot of st - 1 done
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-    if (st + HALO_D - 1 < stages) issue(st + HALO_D - 1);   // into the ring slot of st - 1
-    if (st + 1 < stages) to_planar(st + 1);
+    if (st + HALO_D - 1 < stages) issue(st + HALO_D - 1);   // into the buffer of st - 1
     if (HALO_CG * st + HALO_CG <= groups)
       steps(std::integral_constant<int, HALO_CG>{}, st);
     else
@@ -1188,6 +1145,28 @@ __global__ __launch_bounds__(256) void plan_transpose_nd_kernel(TransposeNK p) {
   int64_t src = 0;
   for (int d = 0; d < p.rank; d++) src = src * p.dims[d] + ic[d];
   p.y[i] = p.x[src];
+}
+
+// The same permutation in 32-bit index arithmetic (element count below
+// 2^31), V consecutive elements a thread: with V = 4 the innermost axis stays
+// innermost and is a multiple of 4 (the attention's head split and merge),
+// so 4 consecutive output elements are 4 consecutive input elements.  Axis d
+// of the output has od[d] units (of V elements) and input stride is[d] units.
+struct TransposeFastK { const float* x; float* y; unsigned units; int rank; unsigned od[5], is[5]; };
+template <int V>
+__global__ __launch_bounds__(256) void plan_transpose_fast_kernel(TransposeFastK p) {
+  using T = typename std::conditional<V == 4, float4, float>::type;
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= p.units) return;
+  unsigned rem = i, src = 0;
+#pragma unroll
+  for (int d = 4; d >= 0; d--) {
+    if (d >= p.rank) continue;
+    const unsigned c = rem % p.od[d];
+    rem /= p.od[d];
+    src += c * p.is[d];
+  }
+  ((T*)p.y)[i] = ((const T*)p.x)[src];
 }
 
 struct ConcatK { const float* arena; float* y; int64_t hw, outc4; int n; uint32_t src[8]; int64_t c4len[8]; };
@@ -2038,6 +2017,29 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       QPH_TRY(d.region(w[1], (uint64_t)k.total, false, "output"));
       k.x = d.at(w[0]);
       k.y = d.at(w[1]);
+      if (k.total < (1ll << 31)) {
+        const int r = k.rank;
+        const bool v4 = k.perm[r - 1] == r - 1 && k.dims[r - 1] % 4 == 0 && w[0] % 4 == 0 &&
+                        w[1] % 4 == 0;
+        const int V = v4 ? 4 : 1;
+        TransposeFastK f{};
+        f.x = k.x; f.y = k.y; f.rank = r; f.units = (unsigned)(k.total / V);
+        int64_t stride[5];
+        stride[r - 1] = 1;
+        for (int i = r - 2; i >= 0; i--) stride[i] = stride[i + 1] * k.dims[i + 1];
+        for (int i = 0; i < r; i++) {
+          f.od[i] = (unsigned)(k.dims[k.perm[i]] / (i == r - 1 ? V : 1));
+          f.is[i] = (unsigned)(stride[k.perm[i]] / (k.perm[i] == r - 1 ? 1 : V));
+        }
+        return add_launch(pl, d.idx, [f, v4](hipStream_t s) {
+          const dim3 grid((f.units + 255) / 256);
+          if (v4)
+            hipLaunchKernelGGL(plan_transpose_fast_kernel<4>, grid, dim3(256), 0, s, f);
+          else
+            hipLaunchKernelGGL(plan_transpose_fast_kernel<1>, grid, dim3(256), 0, s, f);
+          return launch_check("plan_transpose_fast_kernel");
+        });
+      }
       return add_launch(pl, d.idx, [k](hipStream_t s) {
         hipLaunchKernelGGL(plan_transpose_nd_kernel, dim3(blocks_for(k.total)), dim3(256), 0, s, k);
         return launch_check("plan_transpose_nd_kernel");
@@ -2081,7 +2083,12 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       // the first maximum of each row in the same pass when an
       // n_exit3_argmax of this output follows (after n_exit3 reads of it):
       // the softmax kernels take it from the probabilities they store
+      // When that argmax is the probabilities' only reader (no n_exit3 of
+      // them, no graph output in them: the rec plan's pairs exit), they are
+      // not stored at all, nor their padding columns (wide rows only, whose
+      // kernels take a null output).
       float* pairs = nullptr;
+      bool dead = false;
       for (int j = d.idx + 1; j < d.n_disp; j++) {
         const uint32_t* e3 = d.peek(j, PK_EXIT3, 6);
         const uint32_t* am = d.peek(j, PK_EXIT3_ARGMAX, 6);
@@ -2092,13 +2099,14 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
           QPH_TRY(d.region(am[1], (uint64_t)rows * 2, false, "pairs"));
           pairs = d.at(am[1]);
           d.skip[j] = 1;
+          dead = cols > 128 && d.only_readers(d.idx, w[1], (uint64_t)rows * cp, {j});
         }
         break;
       }
       PadColsK pk{y, rows, cols, cp};
       return add_launch(pl, d.idx, [=](hipStream_t s) {
-        QPH_TRY(launch_softmax_pitched(x, rows, cols, cp, y, cp, pairs, s));
-        if (cp == cols) return QPH_OK;
+        QPH_TRY(launch_softmax_pitched(x, rows, cols, cp, dead ? nullptr : y, cp, pairs, s));
+        if (dead || cp == cols) return QPH_OK;
         hipLaunchKernelGGL(plan_pad_cols_kernel, dim3(blocks_for(rows * (cp - cols))), dim3(256),
                            0, s, pk);
         return launch_check("plan_pad_cols_kernel");

@@ -508,6 +508,36 @@ def test_plan_softmax_and_argmax_exits(gpu, oracle, rows, cols):
     assert_bitexact(a, pairs, "pairs")
 
 
+@pytest.mark.parametrize("rows,cols", [(5, 18709), (4, 300)])
+def test_plan_softmax_pairs_only(gpu, oracle, rows, cols):
+    """n_softmax whose output only an n_exit3_argmax reads (the rec plan's
+    pairs exit): the pairs bit-exact, the probabilities left unwritten."""
+    from qppocr_amd import plan
+    r = rng(cols + 1)
+    cp = (cols + 3) // 4 * 4
+    x = np.zeros((rows, cp), np.float32)
+    x[:, :cols] = rnd(r, (rows, cols), 3.0)
+    ref = x[:, :cols].copy()
+    oracle.softmax_last_dim(ref, cols)
+    pairs = oracle.ctc_argmax(ref)
+    mp = MiniPlan()
+    xo = mp.static(x)
+    po = mp.static(np.full(rows * cp, 5.0, np.float32))
+    mp.dispatch("n_softmax", [xo, po, rows, cols, cp, rows], (rows, 1, 1))
+    ao = mp.alloc(rows * 2)
+    mp.dispatch("n_exit3_argmax", [po, ao, rows, cols, cp, rows], (rows, 1, 1))
+    mp.output(ao, rows * 2, (rows, 2))
+    mp.p.total_words = mp.words
+    s = plan.HipPlanSession(mp.p)
+    try:
+        (a,) = s.run(None)
+        left = s.read(po, rows * cp)
+    finally:
+        s.close()
+    assert_bitexact(a, pairs, "pairs")
+    assert np.all(left == 5.0)
+
+
 def test_plan_attn_mm(gpu, oracle):
     r = rng(77)
     b, heads, t, dh = 2, 3, 12, 8
@@ -559,6 +589,28 @@ def test_plan_entry_exit_and_concat(gpu, oracle):
     assert_bitexact(got[2], oracle.sigmoid_tensor(cat_ref), "exit sigmoid")
     assert_bitexact(got[3], cat_ref.reshape(n * 16, h * w).T, "transpose")
     assert_bitexact(got[4], cat_ref.transpose(2, 0, 3, 1), "transpose nd")
+
+
+@pytest.mark.parametrize("dims,perm", [
+    ((2, 5, 3, 4, 8), (2, 0, 3, 1, 4)),    # innermost axis kept, 4 | 8: 16-byte moves
+    ((3, 7, 12), (1, 0, 2)),
+    ((2, 3, 5, 6, 7), (4, 2, 0, 1, 3)),    # innermost axis moved: element moves
+    ((4, 9, 5), (2, 1, 0)),
+])
+def test_plan_transpose_nd_paths(gpu, oracle, dims, perm):
+    """n_transpose_nd against numpy's transpose on both of the kernel's paths."""
+    r = rng(sum(dims) * 7 + perm[0])
+    x = rnd(r, dims)
+    mp = MiniPlan()
+    xo = mp.static(x)
+    yo = mp.alloc(x.size)
+    dd = list(dims) + [1] * (5 - len(dims))
+    pp = list(perm) + [0] * (5 - len(perm))
+    mp.dispatch("n_transpose_nd", [xo, yo, x.size, len(dims), *dd, *pp])
+    ref = np.ascontiguousarray(x.transpose(perm))
+    mp.output(yo, x.size, ref.shape)
+    (got,) = mp.run()
+    assert_bitexact(got, ref, "transpose nd")
 
 
 # ------------------------------------------------------------------ fusion
