@@ -366,7 +366,8 @@ __global__ __launch_bounds__(256) void plan_conv_kernel(ConvK p) {
 }
 
 // The same conv for up to CONV_LDS_TAPS taps with the patch matrix staged in
-// LDS: a one-wave workgroup owns 16 output channels x 32 pixels; per group
+// LDS: a wave owns 16 output channels x 32 pixels (four independent waves a
+// workgroup, each with its own patch area); per group
 // of 4 input channels it stores, for each tap t and pixel j, the 16-byte
 // channel quad x[pixel(j, t)][4g .. 4g + 3] (0 outside the image) at
 // slot t * 32 + j, then runs that group's taps steps (k = c * taps + t within
@@ -375,15 +376,17 @@ __global__ __launch_bounds__(256) void plan_conv_kernel(ConvK p) {
 constexpr int CONV_LDS_TAPS = 16;
 constexpr int CONV_LDS_SLOTS = (CONV_LDS_TAPS * 32 + 63) / 64;  // quads per lane and group
 
-__global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
-  extern __shared__ float4 patch[];  // [taps][32]
+__global__ __launch_bounds__(256) void plan_conv_lds_kernel(ConvK p) {
+  extern __shared__ float4 patches[];  // per wave [taps][32]
   const int b = blockIdx.y;
   const unsigned rn = real_n(p.arena);
   if (rn != 0 && (unsigned)b >= rn) return;
-  const int lane = threadIdx.x;
-  const int wave = blockIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wave = (int)blockIdx.x * 4 + wv;
   const int N = (int)p.N, P = (int)p.P, ow = (int)p.ow;
   const int ncob = (N + 15) >> 4;
+  if (wave >= ncob * ((P + 31) >> 5)) return;
+  float4* patch = patches + wv * (int)p.taps * 32;
   const int co0 = (wave % ncob) * 16, px0 = (wave / ncob) * 32;
   const int li = lane & 15, kq = lane >> 4;
   const int co_a = co0 + li;
@@ -391,31 +394,72 @@ __global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
   const int cin = (int)p.cin, taps = (int)p.taps, kw = (int)p.kw;
   const int iw = (int)p.iw, ih = (int)p.ih;
   const float* xb = p.x + (size_t)b * ih * iw * cin;
+  // Index arithmetic without per-lane divisions: pixel px0 + r is output
+  // (oy0, ox0) walked r columns on (one wave-uniform division), a tap t is
+  // (t / kw, t % kw) walked from 0, and step u's k = 4 u + kq is walked by 4.
+  const int oy0 = px0 / ow, ox0 = px0 - oy0 * ow;
+  auto pixel = [&](int r, int& oy, int& ox) {
+    oy = oy0;
+    ox = ox0 + r;
+    while (ox >= ow) {
+      ox -= ow;
+      oy++;
+    }
+  };
   // the slots this lane fills: q = lane + 64 i -> (t = q / 32, j = q % 32);
   // their input word offsets (channel 0), -1 outside the image
   int soff[CONV_LDS_SLOTS];
+  {
+    int oy, ox;
+    pixel(lane & 31, oy, ox);
+    const bool pin = px0 + (lane & 31) < P;
 #pragma unroll
-  for (int i = 0; i < CONV_LDS_SLOTS; i++) {
-    const int q = lane + 64 * i;
-    const int t = q >> 5, px = px0 + (q & 31);
-    soff[i] = -1;
-    if (t < taps && px < P) {
-      const int oy = px / ow, ox = px - oy * ow;
-      const int iy = oy * (int)p.sh - (int)p.pt + t / kw, ix = ox * (int)p.sw - (int)p.pl + t % kw;
-      if ((unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw) soff[i] = (iy * iw + ix) * cin;
+    for (int i = 0; i < CONV_LDS_SLOTS; i++) {
+      const int t = 2 * i + (lane >> 5);
+      soff[i] = -1;
+      if (t < taps && pin) {
+        int ky = 0, kx = t;
+        while (kx >= kw) {
+          kx -= kw;
+          ky++;
+        }
+        const int iy = oy * (int)p.sh - (int)p.pt + ky, ix = ox * (int)p.sw - (int)p.pl + kx;
+        if ((unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw) soff[i] = (iy * iw + ix) * cin;
+      }
     }
   }
   f32x4 acc[2];
+  int poy[2], pox[2];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int px = px0 + 16 * j + li;
+    pixel(16 * j + li, poy[j], pox[j]);
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       const int co = co0 + 4 * kq + v;
-      acc[j][v] = (p.bias && co < N && px < P && conv_seeded(p, co, px)) ? p.bias[co] : 0.0f;
+      acc[j][v] = (p.bias && co < N && px < P && conv_seeded_at(p, co, poy[j], pox[j])) ? p.bias[co]
+                                                                                        : 0.0f;
     }
   }
   // step u of a group: k = 4 u + kq -> channel c_u = k / taps, tap t_u = k % taps
+  int cu[CONV_LDS_TAPS], tu[CONV_LDS_TAPS];
+  {
+    int c = 0, t = kq;
+    while (t >= taps) {
+      t -= taps;
+      c++;
+    }
+#pragma unroll
+    for (int u = 0; u < CONV_LDS_TAPS; u++) {
+      cu[u] = c;
+      tu[u] = t;
+      t += 4;
+      while (t >= taps) {
+        t -= taps;
+        c++;
+      }
+    }
+  }
   const int groups = cin / 4;
   float4 quad[CONV_LDS_SLOTS];
   float wa[CONV_LDS_TAPS] = {};
@@ -426,10 +470,8 @@ __global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int u = 0; u < CONV_LDS_TAPS; u++) {
-      if (u < taps) {  // wave-uniform
-        const int k = 4 * u + kq, c = k / taps, t = k - c * taps;
-        wa[u] = co_ok ? p.w[(t * cin + 4 * g + c) * N + co_a] : 0.0f;
-      }
+      if (u < taps)  // wave-uniform
+        wa[u] = co_ok ? p.w[(tu[u] * cin + 4 * g + cu[u]) * N + co_a] : 0.0f;
     }
   };
   load_group(0);
@@ -442,20 +484,25 @@ __global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
     float wc[CONV_LDS_TAPS];
 #pragma unroll
     for (int u = 0; u < CONV_LDS_TAPS; u++) wc[u] = wa[u];
-    __syncthreads();
+    // the patch area is this wave's alone: wave-scope fences order its
+    // writes before the reads below and those reads before the next writes
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (g + 1 < groups) load_group(g + 1);
 #pragma unroll
     for (int u = 0; u < CONV_LDS_TAPS; u++) {
       if (u < taps) {  // wave-uniform: the chain has exactly the group's terms
-        const int k = 4 * u + kq, c = k / taps, t = k - c * taps;
-        const float* row = (const float*)(patch + t * 32);
+        const float* row = (const float*)(patch + tu[u] * 32);
 #pragma unroll
         for (int j = 0; j < 2; j++)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(wc[u], row[(16 * j + li) * 4 + c], acc[j],
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(wc[u], row[(16 * j + li) * 4 + cu[u]], acc[j],
                                                         0, 0, 0);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   const int cob = co0 + 4 * kq;
   if (cob >= N) return;
@@ -469,7 +516,7 @@ __global__ __launch_bounds__(64) void plan_conv_lds_kernel(ConvK p) {
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       float x = acc[j][v];
-      if (p.bias && !conv_seeded(p, cob + v, px)) x = x + p.bias[cob + v];
+      if (p.bias && !conv_seeded_at(p, cob + v, poy[j], pox[j])) x = x + p.bias[cob + v];
       x = act_apply(x, p.act);
       if (yres) x = x + yres[px * N + cob + v];
       o[v] = x;
@@ -612,6 +659,123 @@ __global__ __launch_bounds__(64) void plan_conv_dma_kernel(ConvK p) {
       o[v] = x;
     }
     *(float4*)(yb + px * N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// The nets' stems: 3x3 convs over 4 (padded) input channels, stride SW, as
+// plan_conv_lds_kernel computes them (one group, k = c * 9 + t, the same
+// bias rule and epilogue) with the index arithmetic fixed at compile time:
+// a wave owns 32 pixels x 16 NCB output channels, its 9 x 32 patch quads in
+// its own LDS area; step u's k = 4 u + kq gives c = k / 9 = (57 k) >> 9 and
+// t = k - 9 c (exact for k < 64), a tap's row t / 3 = (11 t) >> 5.
+template <int SW, int NCB>
+__global__ __launch_bounds__(256) void plan_stem_kernel(ConvK p) {
+  __shared__ float4 patches[4][9 * 32];
+  const int b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && (unsigned)b >= rn) return;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wave = (int)blockIdx.x * 4 + wv;
+  const int N = (int)p.N, P = (int)p.P, ow = (int)p.ow;
+  const int ncob = (N + 16 * NCB - 1) / (16 * NCB);
+  if (wave >= ncob * ((P + 31) >> 5)) return;
+  float4* patch = patches[wv];
+  const int cb = wave % ncob, co0 = cb * 16 * NCB, px0 = (wave / ncob) * 32;
+  const int li = lane & 15, kq = lane >> 4;
+  const int iw = (int)p.iw, ih = (int)p.ih;
+  const float4* xb = (const float4*)p.x + (size_t)b * ih * iw;
+  const int oy0 = px0 / ow, ox0 = px0 - oy0 * ow;
+  auto pixel = [&](int r, int& oy, int& ox) {
+    oy = oy0;
+    ox = ox0 + r;
+    while (ox >= ow) {
+      ox -= ow;
+      oy++;
+    }
+  };
+  // patch slots q = lane + 64 i: tap t = 2 i + lane / 32, pixel r = lane % 32
+  float4 quad[5];
+  {
+    int oy, ox;
+    pixel(lane & 31, oy, ox);
+    const bool pin = px0 + (lane & 31) < P;
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+      const int t = 2 * i + (lane >> 5), ky = (t * 11) >> 5, kx = t - 3 * ky;
+      const int iy = oy * SW - (int)p.pt + ky, ix = ox * SW - (int)p.pl + kx;
+      const bool in = t < 9 && pin && (unsigned)iy < (unsigned)ih && (unsigned)ix < (unsigned)iw;
+      quad[i] = in ? xb[iy * iw + ix] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
+  float a[9][NCB];
+#pragma unroll
+  for (int u = 0; u < 9; u++) {
+    const int k = 4 * u + kq, c = (k * 57) >> 9, t = k - 9 * c;
+#pragma unroll
+    for (int nb = 0; nb < NCB; nb++) {
+      const int co = co0 + 16 * nb + li;
+      a[u][nb] = co < N ? p.w[(t * 4 + c) * N + co] : 0.0f;
+    }
+  }
+  f32x4 acc[NCB][2];
+  int poy[2], pox[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    pixel(16 * j + li, poy[j], pox[j]);
+    const bool pin = px0 + 16 * j + li < P;
+#pragma unroll
+    for (int nb = 0; nb < NCB; nb++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int co = co0 + 16 * nb + 4 * kq + v;
+        acc[nb][j][v] = (p.bias && co < N && pin && conv_seeded_at(p, co, poy[j], pox[j]))
+                            ? p.bias[co]
+                            : 0.0f;
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 5; i++) {
+    const int q = lane + 64 * i;
+    if (q < 9 * 32) patch[q] = quad[i];
+  }
+  // the patch area is this wave's alone: a wave-scope fence orders the
+  // writes before the reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int u = 0; u < 9; u++) {
+    const int k = 4 * u + kq, c = (k * 57) >> 9, t = k - 9 * c;
+    const float* row = (const float*)(patch + t * 32);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const float bv = row[(16 * j + li) * 4 + c];
+#pragma unroll
+      for (int nb = 0; nb < NCB; nb++)
+        acc[nb][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][nb], bv, acc[nb][j], 0, 0, 0);
+    }
+  }
+  const float* yres = p.res ? p.res + (size_t)b * P * N : nullptr;
+  float* yb = p.y + (size_t)b * P * N;
+#pragma unroll
+  for (int nb = 0; nb < NCB; nb++) {
+    const int cob = co0 + 16 * nb + 4 * kq;
+    if (cob >= N) continue;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int px = px0 + 16 * j + li;
+      if (px >= P) continue;
+      float o[4];
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        float x = acc[nb][j][v];
+        if (p.bias && !conv_seeded_at(p, cob + v, poy[j], pox[j])) x = x + p.bias[cob + v];
+        x = act_apply(x, p.act);
+        if (yres) x = x + yres[px * N + cob + v];
+        o[v] = x;
+      }
+      *(float4*)(yb + px * N + cob) = make_float4(o[0], o[1], o[2], o[3]);
+    }
   }
 }
 
@@ -1662,11 +1826,23 @@ int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
       return go(plan_conv_dma_kernel<9>, CONV_DMA_D * DmaGeom<9>::BUF * 16, s);
     });
   }
+  if (kh == 3 && kw == 3 && cin == 4 && sh == sw && (sw == 1 || sw == 2) && ih * iw < (1ll << 31)) {
+    const int64_t w2 = ((N + 31) / 32) * ((P + 31) / 32), w1 = ((N + 15) / 16) * ((P + 31) / 32);
+    return add_launch(d.pl, d.idx, [k, nb, sw, w1, w2](hipStream_t s) {
+      const bool two = k.N > 16;   // both 16-channel blocks in one wave
+      const dim3 grid((unsigned)(((two ? w2 : w1) + 3) / 4), (unsigned)nb);
+      if (sw == 1 && two) hipLaunchKernelGGL((plan_stem_kernel<1, 2>), grid, dim3(256), 0, s, k);
+      else if (sw == 1) hipLaunchKernelGGL((plan_stem_kernel<1, 1>), grid, dim3(256), 0, s, k);
+      else if (two) hipLaunchKernelGGL((plan_stem_kernel<2, 2>), grid, dim3(256), 0, s, k);
+      else hipLaunchKernelGGL((plan_stem_kernel<2, 1>), grid, dim3(256), 0, s, k);
+      return launch_check("plan_stem_kernel");
+    });
+  }
   if (taps <= CONV_LDS_TAPS) {
-    const size_t lds = (size_t)taps * 32 * 16;
+    const size_t lds = (size_t)4 * taps * 32 * 16;
     return add_launch(d.pl, d.idx, [k, lwaves, nb, lds](hipStream_t s) {
-      hipLaunchKernelGGL(plan_conv_lds_kernel, dim3((unsigned)lwaves, (unsigned)nb), dim3(64), lds,
-                         s, k);
+      hipLaunchKernelGGL(plan_conv_lds_kernel, dim3((unsigned)((lwaves + 3) / 4), (unsigned)nb),
+                         dim3(256), lds, s, k);
       return launch_check("plan_conv_lds_kernel");
     });
   }

@@ -97,6 +97,10 @@ CONV_CASES = [
     # a row count off the 32-pixel tiles, residual; and without bias
     (2, 16, 9, 13, 40, 1, 1, (1, 1), (0, 0, 0, 0), True, "relu", True),
     (1, 16, 12, 12, 20, 1, 1, (1, 1), (0, 0, 0, 0), False, "none", False),
+    # stems (3x3 over 4 padded channels): 32 outputs in one wave, stride 1,
+    # batch 2 + residual; 40 outputs (a partial second wave), stride 2
+    (2, 3, 11, 37, 32, 3, 3, (1, 1), (1, 1, 1, 1), True, "relu", True),
+    (1, 4, 20, 21, 40, 3, 3, (2, 2), (1, 1, 1, 1), False, "gelu", False),
 ]
 
 
