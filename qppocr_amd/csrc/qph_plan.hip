@@ -1285,6 +1285,57 @@ __global__ __launch_bounds__(256) void plan_resize_kernel(ResizeNK p) {
   ((float4*)p.y)[b * p.P * p.c4 + gid] = xb[(iy * p.iw + ix) * p.c4 + c4];
 }
 
+// plan_resize_kernel's nearest source row (or column) of output o
+__device__ __forceinline__ int resize_src(int o, int in, int out) {
+  const int i = (int)((float)o * (float)in / (float)out);
+  return i > in - 1 ? in - 1 : i;
+}
+
+// n_resize (nearest) followed by the n_elem add of its output and another
+// tensor, as one pass: y = a + resize(x) (the add commutes bitwise).  32-bit
+// indices (the decoder checks the sizes).
+struct ResizeAddK { const float4* x; const float4* a; float4* y; int P, c4, ow, oh, iw, ih; };
+__global__ __launch_bounds__(256) void plan_resize_add_kernel(ResizeAddK p) {
+  const int b = blockIdx.y;
+  const int gid = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (gid >= p.P * p.c4) return;
+  const int m = gid / p.c4, c4 = gid - m * p.c4;
+  const int oy = m / p.ow, ox = m - oy * p.ow;
+  const int iy = resize_src(oy, p.ih, p.oh), ix = resize_src(ox, p.iw, p.ow);
+  const float4 r = p.x[(b * p.ih * p.iw + iy * p.iw + ix) * p.c4 + c4];
+  const float4 v = p.a[b * p.P * p.c4 + gid];
+  p.y[b * p.P * p.c4 + gid] = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
+}
+
+// n_concat_c whose inputs may be n_resize outputs read through (input i
+// with ih[i] > 0 is the resize source of ih[i] x iw[i] pixels, mapped as
+// plan_resize_kernel maps it onto the oh x ow output).
+struct ConcatUpK {
+  float4* y;
+  int npx, outc4, n, oh, ow;
+  const float4* src[8];
+  int c4len[8], ih[8], iw[8];
+};
+__global__ __launch_bounds__(256) void plan_concat_up_kernel(ConcatUpK p) {
+  const int gid = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (gid >= p.npx * p.outc4) return;
+  const int pos = gid / p.outc4, c4 = gid - pos * p.outc4;
+  int acc = 0;
+  for (int i = 0; i < p.n; i++) {
+    if (c4 < acc + p.c4len[i]) {
+      int sp = pos;
+      if (p.ih[i] > 0) {
+        const int hw = p.oh * p.ow, b = pos / hw, r = pos - b * hw;
+        const int oy = r / p.ow, ox = r - oy * p.ow;
+        sp = (b * p.ih[i] + resize_src(oy, p.ih[i], p.oh)) * p.iw[i] + resize_src(ox, p.iw[i], p.ow);
+      }
+      p.y[gid] = p.src[i][sp * p.c4len[i] + (c4 - acc)];
+      return;
+    }
+    acc += p.c4len[i];
+  }
+}
+
 // ------------------------------------------------------ data movement
 struct Transpose2K { const float* x; float* y; int64_t r, c; };
 __global__ __launch_bounds__(256) void plan_transpose2_kernel(Transpose2K p) {
@@ -1426,6 +1477,10 @@ struct Decoder {
     std::vector<Span> reads, writes;  // the members' and the dispatches' between them
   };
   HaloOpen halo;
+  // n_resize dispatches a later n_concat_c reads through: output region ->
+  // source region and geometry
+  struct Resized { uint32_t out, src; int64_t nb, ih, iw, oh, ow, c4; };
+  std::vector<Resized> resized;
 
   std::string where() const {
     return "plan dispatch " + std::to_string(idx) + " (" + kname + ", params at word " +
@@ -1631,6 +1686,7 @@ bool join_halo_group(Decoder& d, const ConvK& k, int tiles_x, int64_t oh, int sw
   std::vector<Decoder::Span> reads = h.reads, writes = h.writes;
   for (int m = h.last + 1; m < d.idx; m++) {
     const qph_plan_dispatch& q = d.disp[m];
+    if (q.kernel == PK_RESIZE && d.skip[(size_t)m]) continue;   // read through by a concat
     const uint32_t* w = q.kernel == PK_RESIZE ? d.find(q.p_off, 9) : nullptr;
     if (!w || d.skip[(size_t)m]) return false;
     const uint64_t nbm = q.groups[1];
@@ -2153,6 +2209,47 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
         return fail(QPH_EINVAL, d.where() + ": bad resize geometry");
       QPH_TRY(d.region(w[0], (uint64_t)nb * ih * iw * C, true, "input"));
       QPH_TRY(d.region(w[1], (uint64_t)nb * P * C, true, "output"));
+      const uint32_t S = w[0], R = w[1];
+      const uint64_t len = (uint64_t)nb * P * C, slen = (uint64_t)nb * ih * iw * C;
+      const bool small = len < (1ull << 31) && slen < (1ull << 31);
+      auto hits = [](uint32_t o, uint32_t lo, uint64_t n) { return o >= lo && (uint64_t)o < lo + n; };
+      // (a) the next dispatch adds the resized map to another tensor of its
+      // size, and is its only reader: one pass (the FPN's top-down adds)
+      const uint32_t* e = d.peek(d.idx + 1, PK_ELEM, 7);
+      if (small && e && e[0] == 4 && e[4] == len && ((e[1] == R) != (e[2] == R)) &&
+          d.only_readers(d.idx, R, len, {d.idx + 1}) && !hits(e[3], S, slen) &&
+          !hits(S, e[3], len)) {
+        const uint32_t Y = e[1] == R ? e[2] : e[1];
+        QPH_TRY(d.region(Y, len, true, "addend"));
+        QPH_TRY(d.region(e[3], len, true, "sum"));
+        d.skip[(size_t)d.idx + 1] = 1;
+        ResizeAddK k{(const float4*)d.at(S), (const float4*)d.at(Y), (float4*)d.at(e[3]), (int)P,
+                     (int)(C / 4), (int)ow, (int)(P / ow), (int)iw, (int)ih};
+        return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
+          hipLaunchKernelGGL(plan_resize_add_kernel, dim3(blocks_for((int64_t)k.P * k.c4), (unsigned)nb),
+                             dim3(256), 0, s, k);
+          return launch_check("plan_resize_add_kernel");
+        });
+      }
+      // (b) a later n_concat_c is the only reader of the resized map, and
+      // nothing writes the source or the map before it: the concat reads the
+      // source through the same mapping (the det neck's upsampled maps)
+      for (int j = d.idx + 1; small && j < d.n_disp && j <= d.idx + 16; j++) {
+        if (d.wr[(size_t)j] != OFF_NONE && (hits(d.wr[(size_t)j], S, slen) || hits(d.wr[(size_t)j], R, len)))
+          break;
+        if (d.disp[j].kernel != PK_CONCAT_C || d.skip[(size_t)j]) continue;
+        const uint32_t* c = d.find(d.disp[j].p_off, 4);
+        if (!c || c[2] < 1 || c[2] > 8 || c[1] != (uint64_t)nb * P) break;
+        const uint32_t* cw = d.find(d.disp[j].p_off, 4 + 2 * c[2]);
+        bool reads = false;
+        for (uint32_t i = 0; cw && i < c[2]; i++) reads = reads || (cw[4 + 2 * i] == R && cw[5 + 2 * i] == C / 4);
+        if (reads && d.only_readers(d.idx, R, len, {j})) {
+          d.resized.push_back({R, S, nb, ih, iw, P / ow, ow, C / 4});
+          d.skip[(size_t)d.idx] = 1;
+          return QPH_OK;
+        }
+        break;
+      }
       ResizeNK k{d.at(w[0]), d.at(w[1]), P, C / 4, ow, P / ow, iw, ih};
       return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
         hipLaunchKernelGGL(plan_resize_kernel, dim3(blocks_for(k.P * k.c4), (unsigned)nb),
@@ -2240,6 +2337,31 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       if (sum != outc4) return fail(QPH_EINVAL, d.where() + ": input channels do not sum to the output's");
       QPH_TRY(d.region(w[0], (uint64_t)hw * outc4 * 4, true, "output"));
       k.y = d.at(w[0]);
+      // inputs that are n_resize outputs read through (see PK_RESIZE)
+      ConcatUpK u{};
+      bool up = false;
+      u.y = (float4*)k.y; u.npx = (int)hw; u.outc4 = (int)outc4; u.n = (int)n;
+      for (int i = 0; i < n; i++) {
+        u.src[i] = (const float4*)d.at(k.src[i]);
+        u.c4len[i] = (int)k.c4len[i];
+        for (const auto& r : d.resized) {
+          if (r.out != k.src[i]) continue;
+          if ((up && (u.oh != r.oh || u.ow != r.ow)) || r.nb * r.oh * r.ow != hw || r.c4 != k.c4len[i])
+            return fail(QPH_EINVAL, d.where() + ": read-through input geometry");
+          up = true;
+          u.oh = (int)r.oh; u.ow = (int)r.ow;
+          u.src[i] = (const float4*)d.at(r.src);
+          u.ih[i] = (int)r.ih; u.iw[i] = (int)r.iw;
+        }
+      }
+      if (up && hw * outc4 >= (1ll << 31))
+        return fail(QPH_EUNSUPPORTED, d.where() + ": read-through concat too large");
+      if (up)
+        return add_launch(pl, d.idx, [u](hipStream_t s) {
+          hipLaunchKernelGGL(plan_concat_up_kernel, dim3(blocks_for((int64_t)u.npx * u.outc4)), dim3(256),
+                             0, s, u);
+          return launch_check("plan_concat_up_kernel");
+        });
       return add_launch(pl, d.idx, [k](hipStream_t s) {
         hipLaunchKernelGGL(plan_concat_kernel, dim3(blocks_for(k.hw * k.outc4)), dim3(256), 0, s, k);
         return launch_check("plan_concat_kernel");

@@ -595,6 +595,54 @@ def test_plan_entry_exit_and_concat(gpu, oracle):
     assert_bitexact(got[4], cat_ref.transpose(2, 0, 3, 1), "transpose nd")
 
 
+def _resize_ref(x, oh, ow):
+    """plan_resize_kernel's nearest map on NHWC x [n, h, w, c]."""
+    n, h, w, c = x.shape
+    iy = np.minimum((np.arange(oh, dtype=np.float32) * np.float32(h) / np.float32(oh)).astype(np.int64), h - 1)
+    ix = np.minimum((np.arange(ow, dtype=np.float32) * np.float32(w) / np.float32(ow)).astype(np.int64), w - 1)
+    return x[:, iy][:, :, ix]
+
+
+@pytest.mark.parametrize("order,export_resized", [(0, False), (1, False), (0, True)])
+def test_plan_resize_fusions(gpu, oracle, order, export_resized):
+    """n_resize + n_elem add (either operand order) as one pass, and resizes
+    that only an n_concat_c reads, read through by it (the det neck); with
+    a resized map also exported, the resizes run as dispatched.  Every
+    output equals numpy's nearest resize, add and concat."""
+    from qppocr_amd import plan
+    r = rng(5 + order + 2 * export_resized)
+    n = 2
+    a = rnd(r, (n, 5, 7, 8))            # coarse map, 8 channels
+    y = rnd(r, (n, 10, 14, 8))          # fine lateral
+    c1 = rnd(r, (n, 3, 4, 4))           # concat inputs: two coarse, one full size
+    c2 = rnd(r, (n, 6, 7, 4))
+    c3 = rnd(r, (n, 12, 14, 4))
+    mp = MiniPlan()
+    ao, yo = mp.static(a), mp.static(y)
+    o1, o2, o3 = mp.static(c1), mp.static(c2), mp.static(c3)
+    ra = mp.alloc(n * 10 * 14 * 8)
+    mp.dispatch("n_resize", [ao, ra, 10 * 14, 8, 14, 7, 5, 0.5, 0.5], (1, n, 1))
+    so = mp.alloc(n * 10 * 14 * 8)
+    mp.dispatch("n_elem", [4, ra, yo, so, n * 10 * 14 * 8, 0.0, 0.0] if order == 0 else
+                [4, yo, ra, so, n * 10 * 14 * 8, 0.0, 0.0])
+    r1 = mp.alloc(n * 12 * 14 * 4)
+    mp.dispatch("n_resize", [o1, r1, 12 * 14, 4, 14, 4, 3, 0.25, 0.25], (1, n, 1))
+    r2 = mp.alloc(n * 12 * 14 * 4)
+    mp.dispatch("n_resize", [o2, r2, 12 * 14, 4, 14, 7, 6, 0.5, 0.5], (1, n, 1))
+    cat = mp.alloc(n * 12 * 14 * 12)
+    mp.dispatch("n_concat_c", [cat, n * 12 * 14, 3, 3, r1, 1, r2, 1, o3, 1])
+    mp.output(so, n * 10 * 14 * 8, (n, 10, 14, 8))
+    mp.output(cat, n * 12 * 14 * 12, (n, 12, 14, 12))
+    if export_resized:
+        mp.output(r1, n * 12 * 14 * 4, (n, 12, 14, 4))
+    got = mp.run()
+    assert_bitexact(got[0], _resize_ref(a, 10, 14) + y, "resize + add")
+    cat_ref = np.concatenate([_resize_ref(c1, 12, 14), _resize_ref(c2, 12, 14), c3], -1)
+    assert_bitexact(got[1], cat_ref, "concat of resized maps")
+    if export_resized:
+        assert_bitexact(got[2], _resize_ref(c1, 12, 14), "exported resize")
+
+
 @pytest.mark.parametrize("dims,perm", [
     ((2, 5, 3, 4, 8), (2, 0, 3, 1, 4)),    # innermost axis kept, 4 | 8: 16-byte moves
     ((3, 7, 12), (1, 0, 2)),
