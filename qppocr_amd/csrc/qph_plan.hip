@@ -1206,6 +1206,69 @@ __global__ __launch_bounds__(256) void plan_convt_kernel(ConvtK p) {
   ((float4*)p.y)[b * p.P * p.nv + gid] = act4(acc, p.act);
 }
 
+// The det head's tail: an n_convt (2x2, stride 2, CI -> CM channels) whose
+// output only a second such n_convt (CM -> at most 4 channels) reads, whose
+// output only an n_exit (NHWC -> NCHW, sigmoid or not) reads, in one pass.
+// A thread takes one pixel of the middle map: its CM channels by
+// plan_convt_kernel's chains (input channels ascending from +0, + bias, the
+// activation), then the 2 x 2 output pixels it feeds (the same chains over
+// the CM channels) through the exit into NCHW.  A block's threads share the
+// tap parity of their middle pixel (blockIdx.y), so every weight a chain
+// reads is the same for the whole block (scalar loads).
+struct ConvtPairK {
+  const float* x; const float* w1; const float* b1; const float* w2; const float* b2; float* y;
+  int h, w;          // input map; the middle map is 2h x 2w, the output 4h x 4w
+  int co2p, c_out;   // second conv's padded channels (weight pitch), exported channels
+  Act act1, act2;
+  int sigmoid;
+};
+template <int CI, int CM>
+__global__ __launch_bounds__(256) void plan_convt_pair_kernel(ConvtPairK p) {
+  const int b = blockIdx.z, py = blockIdx.y >> 1, px = blockIdx.y & 1;
+  const int t = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (t >= p.h * p.w) return;
+  const int i = t / p.w, j = t - i * p.w;
+  float xv[CI];
+  const float4* xr = (const float4*)(p.x + ((size_t)(b * p.h + i) * p.w + j) * CI);
+#pragma unroll
+  for (int q = 0; q < CI / 4; q++) {
+    const float4 v = xr[q];
+    xv[4 * q] = v.x;
+    xv[4 * q + 1] = v.y;
+    xv[4 * q + 2] = v.z;
+    xv[4 * q + 3] = v.w;
+  }
+  const float* w1 = p.w1 + (size_t)(py * 2 + px) * CI * CM;   // [tap][ci][CM]
+  float m[CM];
+#pragma unroll
+  for (int c = 0; c < CM; c++) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int ci = 0; ci < CI; ci++) acc = __builtin_fmaf(xv[ci], w1[ci * CM + c], acc);
+    if (p.b1) acc = acc + p.b1[c];
+    m[c] = act_apply(acc, p.act1);
+  }
+  const int H2 = 4 * p.h, W2 = 4 * p.w;
+  const int my = 2 * i + py, mx = 2 * j + px;
+#pragma unroll
+  for (int qy = 0; qy < 2; qy++)
+#pragma unroll
+    for (int qx = 0; qx < 2; qx++) {
+      const float* w2 = p.w2 + (size_t)(qy * 2 + qx) * CM * p.co2p;   // [tap][c][co2p]
+      const int oy = 2 * my + qy, ox = 2 * mx + qx;
+#pragma unroll
+      for (int o = 0; o < 4; o++) {
+        if (o >= p.c_out) break;
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CM; c++) acc = __builtin_fmaf(m[c], w2[c * p.co2p + o], acc);
+        if (p.b2) acc = acc + p.b2[o];
+        acc = act_apply(acc, p.act2);
+        p.y[((size_t)(b * p.c_out + o) * H2 + oy) * W2 + ox] = p.sigmoid ? sigmoid1(acc) : acc;
+      }
+    }
+}
+
 // ------------------------------------------------------------------ pool
 // pool2d.rs:94-259 on NHWC (see pool2d_kernel for the arithmetic)
 struct PoolNK {
@@ -2135,6 +2198,35 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       if (w[2] != OFF_NONE) QPH_TRY(d.region(w[2], (uint64_t)N, true, "bias"));
       ConvtK k{d.at(w[0]), d.at(w[1]), w[2] == OFF_NONE ? nullptr : d.at(w[2]), d.at(w[3]),
                P, N / 4, ow, iw, ih, cin, sh, sw, kw, act};
+      // a second 2x2 stride-2 conv-transpose and an n_exit after it, each
+      // the only reader of what it reads: one pass (plan_convt_pair_kernel)
+      const uint32_t* w2 = d.peek(d.idx + 1, PK_CONVT, 18);
+      const uint32_t* ex = d.peek(d.idx + 2, PK_EXIT, 8);
+      const bool twice = sh == 2 && sw == 2 && kw == 2 && P == 4 * ih * iw && ow == 2 * iw;
+      if (twice && cin == 24 && N == 24 && w2 && ex && w2[0] == w[3] && w2[9] == (uint32_t)N &&
+          w2[11] == 2 && w2[12] == 2 && w2[13] == 2 && w2[8] == (uint32_t)(2 * ih) &&
+          w2[7] == (uint32_t)ow && w2[4] == 16ull * ih * iw && w2[6] == 4ull * iw && w2[5] == 4 &&
+          d.disp[d.idx + 1].groups[1] == (uint32_t)nb && ex[0] == w2[3] && ex[2] == (uint32_t)nb &&
+          ex[4] == 4ull * ih && ex[5] == 4ull * iw && ex[6] == 4 && ex[3] >= 1 && ex[3] <= 4 &&
+          nb * 16 * ih * iw < (1ll << 31) && (w[0] % 4) == 0 &&
+          d.only_readers(d.idx, w[3], (uint64_t)nb * P * N, {d.idx + 1}) &&
+          d.only_readers(d.idx + 1, w2[3], (uint64_t)nb * w2[4] * 4, {d.idx + 2})) {
+        Act act2;
+        QPH_TRY(conv_act(d, w2[14], f32_of(w2[15]), f32_of(w2[16]), f32_of(w2[17]), &act2));
+        QPH_TRY(d.region(w2[1], 4ull * N * 4, true, "second weights"));
+        if (w2[2] != OFF_NONE) QPH_TRY(d.region(w2[2], 4, true, "second bias"));
+        QPH_TRY(d.region(ex[1], (uint64_t)nb * ex[3] * 16 * ih * iw, false, "output"));
+        d.skip[(size_t)d.idx + 1] = 1;
+        d.skip[(size_t)d.idx + 2] = 1;
+        ConvtPairK f{d.at(w[0]), d.at(w[1]), k.bias, d.at(w2[1]),
+                     w2[2] == OFF_NONE ? nullptr : d.at(w2[2]), d.at(ex[1]), (int)ih, (int)iw, 4,
+                     (int)ex[3], act, act2, ex[7] == 4};
+        return add_launch(pl, d.idx, [f, nb](hipStream_t s) {
+          const dim3 grid((unsigned)((f.h * f.w + 255) / 256), 4, (unsigned)nb);
+          hipLaunchKernelGGL((plan_convt_pair_kernel<24, 24>), grid, dim3(256), 0, s, f);
+          return launch_check("plan_convt_pair_kernel");
+        });
+      }
       return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
         hipLaunchKernelGGL(plan_convt_kernel, dim3(blocks_for(k.P * k.nv), (unsigned)nb), dim3(256),
                            0, s, k);

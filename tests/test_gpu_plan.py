@@ -246,6 +246,42 @@ def test_plan_convt(gpu, oracle, ci, co):
     assert_bitexact(mp.run()[0], nhwc(ref), "conv transpose")
 
 
+@pytest.mark.parametrize("sig", [True, False])
+def test_plan_convt_pair_exit_fused(gpu, oracle, sig):
+    """n_convt 24 -> 24, n_convt 24 -> 1 and the n_exit after them (the det
+    head's tail) run as one pass; bit-exact against the oracle's two
+    conv-transposes and sigmoid."""
+    from qppocr_amd import plan
+    r = rng(41 + sig)
+    n, h, w = 2, 5, 6
+    x = rnd(r, (n, 24, h, w))
+    w1 = rnd(r, (24, 24, 2, 2), 0.3)
+    w2 = rnd(r, (24, 1, 2, 2), 0.3)
+    t2 = oracle.convtranspose2d(oracle.convtranspose2d(x, w1), w2)
+    ref = oracle.sigmoid_tensor(t2) if sig else t2
+    mp = MiniPlan()
+    xo = mp.static(nhwc(x))
+    wo1 = mp.static(plan.repack_convt_w(w1, 24, 24, 2, 2))
+    wo2 = mp.static(plan.repack_convt_w(w2, 24, 1, 2, 2))
+    y1 = mp.alloc(n * 4 * h * w * 24)
+    mp.dispatch("n_convt", [xo, wo1, OFF_NONE, y1, 4 * h * w, 24, 2 * w, w, h, 24, 6, 2, 2, 2, 0,
+                            *plan.GELU_C], (1, n, 1))
+    y2 = mp.alloc(n * 16 * h * w * 4)
+    mp.dispatch("n_convt", [y1, wo2, OFF_NONE, y2, 16 * h * w, 4, 4 * w, 2 * w, 2 * h, 24, 6, 2, 2, 2,
+                            0, *plan.GELU_C], (1, n, 1))
+    out = mp.alloc(n * 16 * h * w)
+    mp.dispatch("n_exit", [y2, out, n, 1, 4 * h, 4 * w, 4, 4 if sig else 0])
+    mp.output(out, n * 16 * h * w, (n, 1, 4 * h, 4 * w))
+    mp.p.total_words = mp.words
+    s = plan.HipPlanSession(mp.p)
+    try:
+        assert s.launches() == 1
+        (got,) = s.run(None)
+    finally:
+        s.close()
+    assert_bitexact(got, ref, "conv-transpose pair + exit")
+
+
 def test_plan_real_n_skips_padded_batch_rows(gpu, oracle):
     """Word 0 (real_n) stops the conv at the real batch (plan.rs:587-593):
     the padded batch item's output keeps what the arena held."""
