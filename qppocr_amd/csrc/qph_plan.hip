@@ -1777,6 +1777,54 @@ bool join_halo_group(Decoder& d, const ConvK& k, int tiles_x, int64_t oh, int sw
   return true;
 }
 
+// The attention lowering PlanBuilder writes after the QKV projection
+// (plan.rs attention): n_transpose_nd of the [B, T, 3, H, dh] rows to
+// [3, B, H, T, dh]; q times the scale (n_elem 7); k transposed per head;
+// S = q k^T (n_attn_mm); P = softmax(S) over T; O = P v (n_attn_mm); O
+// back to [B, T, H, dh].  When the seven dispatches are exactly that and
+// every intermediate is read only inside them, one launch_attention (the
+// fused attention over the stored QKV rows: q scaled first, the score and
+// output chains over ascending k, the same softmax sequence) writes the
+// final rows.  Returns 1 when the pattern does not match (nothing decoded).
+int fuse_attention(Decoder& d, const uint32_t* w) {
+  const int i = d.idx;
+  const int64_t B = w[4], T = w[5], H = w[7], DH = w[8];
+  const uint64_t part = (uint64_t)B * H * T * DH;
+  const uint32_t t5 = w[1];
+  const uint32_t* e = d.peek(i + 1, PK_ELEM, 7);
+  const uint32_t* t2 = d.peek(i + 2, PK_TRANSPOSE_ND, 14);
+  const uint32_t* m1 = d.peek(i + 3, PK_ATTN_MM, 8);
+  const uint32_t* sm = d.peek(i + 4, PK_SOFTMAX, 6);
+  const uint32_t* m2 = d.peek(i + 5, PK_ATTN_MM, 8);
+  const uint32_t* t3 = d.peek(i + 6, PK_TRANSPOSE_ND, 14);
+  if (!e || !t2 || !m1 || !sm || !m2 || !t3) return 1;
+  const uint32_t* sc = d.find(e[2], 1);
+  auto perm4 = [&](const uint32_t* t, uint32_t a, uint32_t b, uint32_t c, uint32_t e4) {
+    return t[2] == part && t[3] == 4 && t[4] == B && t[5] == H && t[6] == T && t[7] == DH &&
+           t[9] == a && t[10] == b && t[11] == c && t[12] == e4;
+  };
+  const bool match =
+      sc && e[0] == 7 && e[1] == t5 && e[4] == part && t2[0] == t5 + part && perm4(t2, 0, 1, 3, 2) &&
+      m1[0] == e[3] && m1[1] == t2[1] && m1[3] == T && m1[4] == DH && m1[5] == T &&
+      m1[6] == (uint64_t)B * H && sm[0] == m1[2] && sm[2] == (uint64_t)B * H * T && sm[3] == T &&
+      sm[4] == T && m2[0] == sm[1] && m2[1] == t5 + 2 * part && m2[3] == T && m2[4] == T &&
+      m2[5] == DH && m2[6] == (uint64_t)B * H && t3[0] == m2[2] && perm4(t3, 0, 2, 1, 3) &&
+      d.only_readers(i, t5, 3 * part, {i + 1, i + 2, i + 5}) &&
+      d.only_readers(i + 1, e[3], part, {i + 3}) && d.only_readers(i + 2, t2[1], part, {i + 3}) &&
+      d.only_readers(i + 3, m1[2], (uint64_t)B * H * T * T, {i + 4}) &&
+      d.only_readers(i + 4, sm[1], (uint64_t)B * H * T * T, {i + 5}) &&
+      d.only_readers(i + 5, m2[2], part, {i + 6}) && B * H < (1ll << 31);
+  if (!match) return 1;
+  QPH_TRY(d.region(t3[1], part, false, "attention output"));
+  for (int j = i + 1; j <= i + 6; j++) d.skip[(size_t)j] = 1;
+  const float* qkv = d.at(w[0]);
+  float* y = d.at(t3[1]);
+  const float scale = f32_of(sc[0]);
+  return add_launch(d.pl, i, [=](hipStream_t s) {
+    return launch_attention(qkv, B, T, H, DH, scale, y, s);
+  });
+}
+
 int decode_conv(Decoder& d, const qph_plan_dispatch& q) {
   const uint32_t* w;
   QPH_TRY(d.params(21, &w));
@@ -2382,6 +2430,11 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       QPH_TRY(d.region(w[1], (uint64_t)k.total, false, "output"));
       k.x = d.at(w[0]);
       k.y = d.at(w[1]);
+      if (k.rank == 5 && k.perm[0] == 2 && k.perm[1] == 0 && k.perm[2] == 3 && k.perm[3] == 1 &&
+          k.perm[4] == 4 && k.dims[2] == 3) {
+        int rc = fuse_attention(d, w);
+        if (rc != 1) return rc;   // 1: not the attention pattern
+      }
       if (k.total < (1ll << 31)) {
         const int r = k.rank;
         const bool v4 = k.perm[r - 1] == r - 1 && k.dims[r - 1] % 4 == 0 && w[0] % 4 == 0 &&
