@@ -1216,6 +1216,7 @@ __global__ __launch_bounds__(256) void plan_convt_kernel(ConvtK p) {
 // tap parity of their middle pixel (blockIdx.y), so every weight a chain
 // reads is the same for the whole block (scalar loads).
 struct ConvtPairK {
+  const float* arena;
   const float* x; const float* w1; const float* b1; const float* w2; const float* b2; float* y;
   int h, w;          // input map; the middle map is 2h x 2w, the output 4h x 4w
   int co2p, c_out;   // second conv's padded channels (weight pitch), exported channels
@@ -1225,6 +1226,8 @@ struct ConvtPairK {
 template <int CI, int CM>
 __global__ __launch_bounds__(256) void plan_convt_pair_kernel(ConvtPairK p) {
   const int b = blockIdx.z, py = blockIdx.y >> 1, px = blockIdx.y & 1;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && (unsigned)b >= rn) return;
   const int t = (int)blockIdx.x * 256 + (int)threadIdx.x;
   if (t >= p.h * p.w) return;
   const int i = t / p.w, j = t - i * p.w;
@@ -1357,9 +1360,11 @@ __device__ __forceinline__ int resize_src(int o, int in, int out) {
 // n_resize (nearest) followed by the n_elem add of its output and another
 // tensor, as one pass: y = a + resize(x) (the add commutes bitwise).  32-bit
 // indices (the decoder checks the sizes).
-struct ResizeAddK { const float4* x; const float4* a; float4* y; int P, c4, ow, oh, iw, ih; };
+struct ResizeAddK { const float* arena; const float4* x; const float4* a; float4* y; int P, c4, ow, oh, iw, ih; };
 __global__ __launch_bounds__(256) void plan_resize_add_kernel(ResizeAddK p) {
   const int b = blockIdx.y;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && (unsigned)b >= rn) return;
   const int gid = (int)blockIdx.x * 256 + (int)threadIdx.x;
   if (gid >= p.P * p.c4) return;
   const int m = gid / p.c4, c4 = gid - m * p.c4;
@@ -2266,7 +2271,7 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
         QPH_TRY(d.region(ex[1], (uint64_t)nb * ex[3] * 16 * ih * iw, false, "output"));
         d.skip[(size_t)d.idx + 1] = 1;
         d.skip[(size_t)d.idx + 2] = 1;
-        ConvtPairK f{d.at(w[0]), d.at(w[1]), k.bias, d.at(w2[1]),
+        ConvtPairK f{pl->arena, d.at(w[0]), d.at(w[1]), k.bias, d.at(w2[1]),
                      w2[2] == OFF_NONE ? nullptr : d.at(w2[2]), d.at(ex[1]), (int)ih, (int)iw, 4,
                      (int)ex[3], act, act2, ex[7] == 4};
         return add_launch(pl, d.idx, [f, nb](hipStream_t s) {
@@ -2363,7 +2368,7 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
         QPH_TRY(d.region(Y, len, true, "addend"));
         QPH_TRY(d.region(e[3], len, true, "sum"));
         d.skip[(size_t)d.idx + 1] = 1;
-        ResizeAddK k{(const float4*)d.at(S), (const float4*)d.at(Y), (float4*)d.at(e[3]), (int)P,
+        ResizeAddK k{pl->arena, (const float4*)d.at(S), (const float4*)d.at(Y), (float4*)d.at(e[3]), (int)P,
                      (int)(C / 4), (int)ow, (int)(P / ow), (int)iw, (int)ih};
         return add_launch(pl, d.idx, [k, nb](hipStream_t s) {
           hipLaunchKernelGGL(plan_resize_add_kernel, dim3(blocks_for((int64_t)k.P * k.c4), (unsigned)nb),

@@ -305,6 +305,46 @@ def test_plan_real_n_skips_padded_batch_rows(gpu, oracle):
     assert np.all(got[2] == 7.0)
 
 
+def test_plan_real_n_in_fused_launches(gpu, oracle):
+    """real_n in the launches that take over several dispatches: the
+    resize + add pass and the conv-transpose pair + exit stop at the real
+    batch; the real items equal the oracle, the padded item's outputs keep
+    what the arena held."""
+    from qppocr_amd import plan
+    r = rng(17)
+    n, h, w = 3, 4, 5
+    a = rnd(r, (n, 2, 3, 8))
+    y = rnd(r, (n, 4, 6, 8))
+    x = rnd(r, (n, 24, h, w))
+    w1 = rnd(r, (24, 24, 2, 2), 0.3)
+    w2 = rnd(r, (24, 1, 2, 2), 0.3)
+    ref_t = oracle.sigmoid_tensor(oracle.convtranspose2d(oracle.convtranspose2d(x, w1), w2))
+    mp = MiniPlan()
+    ao, yo = mp.static(a), mp.static(y)
+    ra = mp.alloc(n * 4 * 6 * 8)
+    mp.dispatch("n_resize", [ao, ra, 4 * 6, 8, 6, 3, 2, 0.5, 0.5], (1, n, 1))
+    so = mp.static(np.full(n * 4 * 6 * 8, 7.0, np.float32))
+    mp.dispatch("n_elem", [4, ra, yo, so, n * 4 * 6 * 8, 0.0, 0.0])
+    xo = mp.static(nhwc(x))
+    wo1 = mp.static(plan.repack_convt_w(w1, 24, 24, 2, 2))
+    wo2 = mp.static(plan.repack_convt_w(w2, 24, 1, 2, 2))
+    t1 = mp.alloc(n * 4 * h * w * 24)
+    mp.dispatch("n_convt", [xo, wo1, OFF_NONE, t1, 4 * h * w, 24, 2 * w, w, h, 24, 6, 2, 2, 2, 0,
+                            *plan.GELU_C], (1, n, 1))
+    t2 = mp.alloc(n * 16 * h * w * 4)
+    mp.dispatch("n_convt", [t1, wo2, OFF_NONE, t2, 16 * h * w, 4, 4 * w, 2 * w, 2 * h, 24, 6, 2, 2, 2,
+                            0, *plan.GELU_C], (1, n, 1))
+    out = mp.static(np.full(n * 16 * h * w, 7.0, np.float32))
+    mp.dispatch("n_exit", [t2, out, n, 1, 4 * h, 4 * w, 4, 4])
+    mp.output(so, n * 4 * 6 * 8, (n, 4, 6, 8))
+    mp.output(out, n * 16 * h * w, (n, 1, 4 * h, 4 * w))
+    got_s, got_t = mp.run(real_n=2)
+    assert_bitexact(got_s[:2], (_resize_ref(a, 4, 6) + y)[:2], "resize + add, real items")
+    assert np.all(got_s[2] == 7.0)
+    assert_bitexact(got_t[:2], ref_t[:2], "conv-transpose pair, real items")
+    assert np.all(got_t[2] == 7.0)
+
+
 # -------------------------------------------------------- pool / resize / reductions
 
 POOL_CASES = [  # kh, kw, sh, sw, pads (t, l, b, r), max
