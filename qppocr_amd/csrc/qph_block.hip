@@ -580,6 +580,175 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   }
 }
 
+// Register-fed form of the same block, for the 16-byte path's shapes with
+// C = 4 NS channels (NS = 8, 16 or 32): the same tile (16 output pixels of a
+// row, a 64-channel slice of M) and the same arithmetic, with only the
+// depthwise outputs in LDS (C x 16 floats, at most 8 KB, where dwpw_kernel
+// stages the whole input halo and weight slice: 40-115 KB).  A workgroup
+// this small fits beside other kernels' workgroups on a CU, for instance
+// beside the rec head GEMM (144 KB of LDS a CU) when the det and rec graphs
+// run concurrently.
+//  - First, each lane loads its NS pointwise A operands W[k = 4 s + g][m]
+//    (the k-major repack, m = this wave's 16-channel block + l16) into
+//    registers; their latency runs under the depthwise phase.
+//  - Depthwise: task (channel ci, quarter part) computes the 4 outputs
+//    part * 4 .. + 3 of the tile for channel ci.  Its window is the KH input
+//    rows x 3 aligned 16-byte chunks starting 4 columns left of its first
+//    output's first tap (so the first tap sits SHIFT = 4 - KW / 2 words in),
+//    loaded straight into registers; a chunk is wholly inside or outside
+//    the image (width % 4 == 0), outside ones read 0 through the buffer
+//    range check, which is the zero padding.  The taps and bias come from
+//    memory.  Lanes 4 ci + part: one load instruction touches 16 channels'
+//    rows, four consecutive chunks each.  acc = fma(w, x, acc) over ky then
+//    kx from 0, + bias, activation; outputs past the image store 0.
+//  - One barrier; each wave then runs the chain of its 16 output channels
+//    over k = 4 s + g ascending on v_mfma_f32_16x16x4f32, the B operands
+//    read from LDS, and stores as dwpw_kernel does.
+#define DWPW_REG_MAXC 128
+
+template <int KH, int KW, int SW, int NS, int AK>
+__global__ __launch_bounds__(256) void dwpw_reg_kernel(DwPwK p) {
+  constexpr int C = 4 * NS;
+  constexpr int PX = 4;
+  constexpr int SHIFT = 4 - KW / 2;
+  constexpr int NC = SHIFT + (PX - 1) * SW + KW;
+  constexpr int NV = (NC + 3) / 4;
+  static_assert(C <= DWPW_REG_MAXC && NV == 3, "");
+  __shared__ __attribute__((aligned(16))) float t[C * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int img = blockIdx.z, slice = blockIdx.y;
+  const int oy = blockIdx.x / p.tiles_x;
+  const int ox0 = (blockIdx.x - oy * p.tiles_x) * 16;
+  const int mb = slice * 4 + wave;            // 16-channel block index
+  const unsigned OOB = 0x80000000u;
+
+  // pointwise A operands and this lane's four bias terms, issued first
+  float wa[NS];
+  {
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.wk, 0, C * p.mpad * 4, 0x00020000);
+    const int col = mb * 16 + l16;
+    const unsigned vo = col < p.mpad ? (unsigned)(lg * p.mpad + col) * 4u : OOB;
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+      wa[s] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(wr, vo, 16 * s * p.mpad, 0));
+  }
+  float bpre[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mb * 16 + 4 * lg + v;
+    bpre[v] = (p.bp && mo < p.m) ? p.bp[mo] : 0.0f;
+  }
+
+  // depthwise phase
+  {
+    const int64_t plane = (int64_t)p.h * p.w;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.x + (int64_t)img * C * plane), 0, (int)(C * plane * 4), 0x00020000);
+    const int iy0 = oy * p.sh - p.ph;
+#pragma unroll
+    for (int e0 = 0; e0 < 4 * C; e0 += 256) {
+      const int e = e0 + tid;
+      if (4 * C % 256 != 0 && e >= 4 * C) break;
+      const int ci = e >> 2, part = e & 3;
+      const int px0 = part * PX;
+      const int wx = (ox0 + px0) * SW - 4;    // window column 0 (a multiple of 4)
+      float r[KH][4 * NV];
+#pragma unroll
+      for (int ky = 0; ky < KH; ky++) {
+        const int iy = iy0 + ky;
+        const bool rok = iy >= 0 && iy < p.h;
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+          const int ix = wx + 4 * v;
+          const unsigned off =
+              rok && ix >= 0 && ix < p.w ? (unsigned)((ci * (int)plane + iy * p.w + ix) * 4) : OOB;
+          const f32x4 q =
+              __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+#pragma unroll
+          for (int j = 0; j < 4; j++) r[ky][4 * v + j] = q[j];
+        }
+      }
+      float wv[KH * KW];
+      const float* wp = p.wd + ci * KH * KW;
+#pragma unroll
+      for (int j = 0; j < KH * KW; j++) wv[j] = wp[j];
+      const float bdv = p.bd ? p.bd[ci] : 0.0f;
+      float acc[PX];
+#pragma unroll
+      for (int q = 0; q < PX; q++) acc[q] = 0.0f;
+#pragma unroll
+      for (int ky = 0; ky < KH; ky++)
+#pragma unroll
+        for (int kx = 0; kx < KW; kx++)
+#pragma unroll
+          for (int q = 0; q < PX; q++)
+            acc[q] = __builtin_fmaf(wv[ky * KW + kx], r[ky][SHIFT + q * SW + kx], acc[q]);
+      float o[PX];
+#pragma unroll
+      for (int q = 0; q < PX; q++) {
+        const float v = act_k<AK>(acc[q] + bdv, p.act_d);
+        o[q] = ox0 + px0 + q < p.ow ? v : 0.0f;
+      }
+      *(f32x4*)(t + ci * 16 + px0) = f32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+  __syncthreads();
+
+  // pointwise chain of this wave's 16 channels
+  if (mb * 16 >= p.m) return;
+  const int npx = p.oh * p.ow;
+  const int px = oy * p.ow + ox0 + l16;
+  const bool pok = ox0 + l16 < p.ow;
+  float bv[NS];
+#pragma unroll
+  for (int s = 0; s < NS; s++) bv[s] = t[(4 * s + lg) * 16 + l16];
+  f32x4 acc;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mb * 16 + 4 * lg + v;
+    float s0 = 0.0f;
+    if (p.bp && mo < p.m && pok && bias_seeded(p.seed_rule, mo, px, p.m, npx)) s0 = bpre[v];
+    acc[v] = s0;
+  }
+#pragma unroll
+  for (int s = 0; s < NS; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], bv[s], acc, 0, 0, 0);
+
+  float badd[4];
+  bool hadd[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mb * 16 + 4 * lg + v;
+    hadd[v] = p.bp && mo < p.m && pok && !bias_seeded(p.seed_rule, mo, px, p.m, npx);
+    badd[v] = hadd[v] ? bpre[v] : 0.0f;
+  }
+  if (!pok) return;
+  float r[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    r[v] = acc[v];
+    if (hadd[v]) r[v] = r[v] + badd[v];
+    r[v] = act_k<AK>(r[v], p.act_p);
+  }
+  const int mo0 = mb * 16 + 4 * lg;
+  if (p.trans_out && mo0 + 3 < p.m && p.m % 4 == 0 && ((uintptr_t)p.y & 15) == 0) {
+    *(f32x4*)(p.y + ((int64_t)img * npx + px) * p.m + mo0) = f32x4{r[0], r[1], r[2], r[3]};
+    return;
+  }
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int mo = mo0 + v;
+    if (mo >= p.m) continue;
+    if (p.trans_out)
+      p.y[((int64_t)img * npx + px) * p.m + mo] = r[v];
+    else
+      p.y[((int64_t)img * p.m + mo) * npx + px] = r[v];
+  }
+}
+
 // halo row pitch: 15 * sw + KW columns rounded up to 4 (16-byte rows)
 static int halo_ct(const DwPwArgs& a) { return (int)((15 * a.sw + a.kw + 3) / 4 * 4); }
 // halo per channel: KH rows, in one or two loads
@@ -600,9 +769,11 @@ static int64_t dwpw_lds_bytes(const DwPwArgs& a, int64_t halo) {
          4;
 }
 
+// (5x5 taps with x-stride 1 only: the 5x5 kernel instances are stride-1)
 bool dwpw_eligible(const DwPwArgs& a) {
-  return ((a.kh == 3 && a.kw == 3) || (a.kh == 5 && a.kw == 5)) && a.c > 0 &&
-         a.c <= DWPW_MAX_C && a.m > 0 && a.n <= 65535 && (a.sw == 1 || a.sw == 2) &&
+  return ((a.kh == 3 && a.kw == 3 && (a.sw == 1 || a.sw == 2)) ||
+          (a.kh == 5 && a.kw == 5 && a.sw == 1)) &&
+         a.c > 0 && a.c <= DWPW_MAX_C && a.m > 0 && a.n <= 65535 &&
          halo_per_c(a) <= 128 && halo_floats(a) <= DWPW_MAX_HALO &&
          dwpw_lds_bytes(a, halo_floats(a)) <= 160 * 1024 &&
          a.c * a.h * a.w * 4 < (int64_t)0x80000000 && a.oh * a.ow < (1ll << 30) &&
@@ -658,6 +829,25 @@ static bool dwpw_vec(const DwPwArgs& a) {
          (!a.bd || al(a.bd)) && al(a.wk);
 }
 
+// the register-fed form: the 16-byte path with C = 32, 64 or 128
+static bool dwpw_reg_ok(const DwPwArgs& a) { return a.c == 32 || a.c == 64 || a.c == 128; }
+
+template <int KH, int KW, int SW, int NS>
+static int launch_dwpw_reg_t(dim3 grid, const DwPwK& p, hipStream_t s) {
+  if (p.act_d.kind == 3 && p.act_p.kind == 3)
+    hipLaunchKernelGGL((dwpw_reg_kernel<KH, KW, SW, NS, 3>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((dwpw_reg_kernel<KH, KW, SW, NS, 0>), grid, dim3(256), 0, s, p);
+  return launch_check("dwpw_reg_kernel");
+}
+
+template <int KH, int KW, int SW>
+static int launch_dwpw_reg(int64_t c, dim3 grid, const DwPwK& p, hipStream_t s) {
+  if (c == 32) return launch_dwpw_reg_t<KH, KW, SW, 8>(grid, p, s);
+  if (c == 64) return launch_dwpw_reg_t<KH, KW, SW, 16>(grid, p, s);
+  return launch_dwpw_reg_t<KH, KW, SW, 32>(grid, p, s);
+}
+
 bool dwpw_stem_eligible(const DwPwArgs& a) {
   return a.stem && a.xin && a.wst && (a.c == 16 || a.c == 32) && a.kh == 3 && a.kw == 3 &&
          a.sh == 2 && a.sw == 2 && a.ph == 1 && a.pw == 1 && a.h == (a.hin - 1) / 2 + 1 &&
@@ -707,6 +897,11 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
     // cpad 16 -> 1 pixel per depthwise task, 32 -> 2
     if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true, false>(grid, lds, p, s);
     return launch_dwpw_t<3, 3, 2, 1, true, false>(grid, lds, p, s);
+  }
+  if (dwpw_vec(a) && dwpw_reg_ok(a)) {
+    if (a.kh == 5) return launch_dwpw_reg<5, 5, 1>(a.c, grid, p, s);
+    if (a.sw == 1) return launch_dwpw_reg<3, 3, 1>(a.c, grid, p, s);
+    return launch_dwpw_reg<3, 3, 2>(a.c, grid, p, s);
   }
   // the 16-byte path's halo: whole chunks, channels contiguous
   const int vch = a.kh == 5 ? VecGeom<5, 5, 1>::CH : a.sw == 1 ? VecGeom<3, 3, 1>::CH

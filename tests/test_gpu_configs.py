@@ -532,16 +532,21 @@ BLOCK_CASES = [
     (1, 64, 20, 42, 3, 1, 1, 64, "hs"),     # width % 4 != 0: one-word loads
     (1, 30, 20, 40, 3, 1, 1, 40, "hs"),     # channels % 4 != 0: one-word loads
     (1, 32, 20, 40, 3, 1, 0, 32, "hs"),     # no padding: one-word loads
+    (1, 32, 40, 64, 3, 1, 1, 32, "relu"),   # register-fed form, generic activations
+    (1, 64, 26, 36, 3, 2, 1, 128, "hs"),    # register-fed, stride 2, partial tile (18 wide)
+    (1, 64, 24, 48, 5, 2, 2, 64, "hs"),     # 5x5 stride 2: depthwise and 1x1 as two launches
 ]
 
 
 @pytest.mark.parametrize("case", BLOCK_CASES, ids=lambda c: "-".join(map(str, c)))
 def test_session_block_paths(gpu, oracle, case):
-    """Depthwise + 1x1 blocks fused into one launch, over both halo load
-    paths (16-byte chunks when the width and channel count are multiples
+    """Depthwise + 1x1 blocks fused into one launch: the register-fed form
+    (C = 32, 64, 128 on the 16-byte path) and both halo load paths of the
+    LDS form (16-byte chunks when the width and channel count are multiples
     of 4 and the padding is k // 2; one-word loads otherwise), 1 to 8
     pixels a depthwise task, 3x3 and 5x5, strides 1 and 2, partial tiles
-    and channel slices; bit-exact against the oracle."""
+    and channel slices, and a 5x5 stride-2 pair (not fused); bit-exact
+    against the oracle."""
     from qppocr_amd import nets
     from oracle import nets as onets
     n, c, h, w, k, st, pad, m, act = case
