@@ -581,7 +581,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
 }
 
 // Register-fed form of the same block, for the 16-byte path's shapes with
-// C = 4 NS channels (NS = 8, 16 or 32): the same tile (16 output pixels of a
+// C = 4 NS channels (NS = 4, 8, 16 or 32): the same tile (16 output pixels of a
 // row, a 64-channel slice of M) and the same arithmetic, with only the
 // depthwise outputs in LDS (C x 16 floats, at most 8 KB, where dwpw_kernel
 // stages the whole input halo and weight slice: 40-115 KB).  A workgroup
@@ -829,8 +829,10 @@ static bool dwpw_vec(const DwPwArgs& a) {
          (!a.bd || al(a.bd)) && al(a.wk);
 }
 
-// the register-fed form: the 16-byte path with C = 32, 64 or 128
-static bool dwpw_reg_ok(const DwPwArgs& a) { return a.c == 32 || a.c == 64 || a.c == 128; }
+// the register-fed form: the 16-byte path with C = 16, 32, 64 or 128
+static bool dwpw_reg_ok(const DwPwArgs& a) {
+  return a.c == 16 || a.c == 32 || a.c == 64 || a.c == 128;
+}
 
 template <int KH, int KW, int SW, int NS>
 static int launch_dwpw_reg_t(dim3 grid, const DwPwK& p, hipStream_t s) {
@@ -843,6 +845,7 @@ static int launch_dwpw_reg_t(dim3 grid, const DwPwK& p, hipStream_t s) {
 
 template <int KH, int KW, int SW>
 static int launch_dwpw_reg(int64_t c, dim3 grid, const DwPwK& p, hipStream_t s) {
+  if (c == 16) return launch_dwpw_reg_t<KH, KW, SW, 4>(grid, p, s);
   if (c == 32) return launch_dwpw_reg_t<KH, KW, SW, 8>(grid, p, s);
   if (c == 64) return launch_dwpw_reg_t<KH, KW, SW, 16>(grid, p, s);
   return launch_dwpw_reg_t<KH, KW, SW, 32>(grid, p, s);

@@ -527,7 +527,8 @@ BLOCK_CASES = [
     (1, 128, 40, 40, 3, 2, 1, 256, "hs"),   # det block 12: stride 2, four 64-channel slices
     (2, 64, 23, 44, 3, 1, 1, 96, "hs"),     # partial tiles and slice, odd height
     (1, 32, 30, 36, 3, 2, 1, 64, "hs"),     # stride 2, 2 px a task, partial tile
-    (1, 16, 17, 20, 3, 1, 1, 32, "relu"),   # 1 px a task, generic activations
+    (1, 16, 17, 20, 3, 1, 1, 32, "relu"),   # register-fed, C = 16, generic activations
+    (1, 16, 17, 22, 3, 1, 1, 32, "relu"),   # width % 4 != 0: one-word loads, 1 px a task
     (1, 64, 24, 48, 5, 1, 2, 64, "hs"),     # 5x5, 4 px a task
     (1, 64, 20, 42, 3, 1, 1, 64, "hs"),     # width % 4 != 0: one-word loads
     (1, 30, 20, 40, 3, 1, 1, 40, "hs"),     # channels % 4 != 0: one-word loads
