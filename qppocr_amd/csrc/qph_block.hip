@@ -27,7 +27,10 @@
 // With the stem in front (STEM, the first block of both nets: stem conv
 // 3 -> C, 3x3 stride 2 pad 1, then a 3x3 stride-2 pad-1 depthwise), the halo
 // is not loaded but computed: phase 1 brings the 3 x 7 x 67 input pixels the
-// tile's 3 x 33 stem outputs read, phase S runs the stem chains on
+// tile's 3 x 33 stem outputs read (3 x 11 x 67 for 5 x 33 when a workgroup
+// owns two output rows, as the launcher picks when one-row workgroups would
+// not all be resident at once; the stem row the two rows share is then
+// computed once), phase S runs the stem chains on
 // v_mfma_f32_16x16x4f32 (16 stem pixels x 16 channels a block, k = c*9 +
 // ky*3 + kx ascending after one leading 0 * 0 term, so each output is the
 // reference's chain acc = 0; acc = fma(w, x, acc) exactly; taps outside the
@@ -74,19 +77,29 @@ struct DwPwK {
   int xvec;          // stem input in 16-byte chunks (region column 0 one left)
 };
 
-// stem input region of a tile: 3 channels x 7 rows x 67 columns, rows 68
-// floats apart (a row arrives as a 64-lane load and a 3-lane load: only
-// active lanes write LDS; or, when the input width is a multiple of 4, as
-// 17 aligned 16-byte chunks starting one column further left); the stem
-// tile is 3 rows x 33 columns of stem outputs
-#define ST_RR 7
-#define ST_RP 68
-#define ST_IN (3 * ST_RR * ST_RP)
+// Stem tile of a launch whose workgroups own R output rows (R = 1 or 2):
+// the depthwise (3x3, stride 2) reads 2R + 1 stem rows x 33 stem columns,
+// which the stem (3x3, stride 2) computes from an input region of 3
+// channels x (4R + 3) rows x 67 columns, rows 68 floats apart (a row
+// arrives as a 64-lane load and a 3-lane load: only active lanes write LDS;
+// or, when the input width is a multiple of 4, as 17 aligned 16-byte chunks
+// starting one column further left).  The halo rows are CT = 36 floats
+// apart; a channel's pitch PCP holds its 2R + 1 rows and the spare words
+// where the pixels past the tile of the last 16-pixel block land, and is
+// 4 mod 64 (16 lanes reading 16 consecutive channels hit distinct banks).
+template <int R>
+struct StemGeom {
+  static constexpr int RR = 4 * R + 3;
+  static constexpr int RP = 68;
+  static constexpr int IN = 3 * RR * RP;
+  static constexpr int ROWS = 2 * R + 1;
+  static constexpr int PX = ROWS * 33;
+  static constexpr int PB = (PX + 15) / 16;
+  static constexpr int CT = 36;
+  static constexpr int PCP = R == 1 ? 132 : 196;
+  static_assert(ROWS * CT + (PB * 16 - PX) <= PCP && PCP % 64 == 4, "stem halo pitch");
+};
 #define ST_K 28            // 27 taps after one leading zero term
-#define ST_PX 99           // 3 x 33 stem outputs
-#define ST_PB 7            // 16-pixel blocks covering them
-#define ST_CT 36           // halo row pitch of the stem launch (3x3 stride 2)
-#define ST_PCP 132         // its channel pitch (3 rows of 36, rounded to 64, + 4)
 
 // Halo geometry of the 16-byte load path (VEC: left padding KW / 2, image
 // width a multiple of 4, 16-byte aligned tensors).  A halo row starts at the
@@ -113,18 +126,25 @@ __device__ __forceinline__ float act_k(float v, const Act& a) {
   else return act_apply(v, a);
 }
 
-template <int KH, int KW, int SW, int PX, bool STEM, int AK, bool VEC>
+template <int KH, int KW, int SW, int PX, bool STEM, int AK, bool VEC, int R>
 __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   static_assert(!(STEM && VEC), "the stem computes its halo");
+  static_assert(R == 1 || (STEM && R == 2), "two output rows a workgroup: stem launches only");
+  using SG = StemGeom<R>;
   extern __shared__ float lds[];
   float* halo = lds;                 // [c][KH][ct]
   float* wsl = lds + p.halo;         // [cpad][64]
-  float* t = wsl + p.wrows;          // [cpad][16]
-  float* wdl = t + p.cpad * 16;      // depthwise weights [c][KH*KW], then bias [c]
-  // STEM: input region [3][7][68], stem weights [c][27] (28 c floats of
-  // room), bias [c] (64 floats of room)
+  float* t = wsl + p.wrows;          // [cpad][R][16]
+  // depthwise weights [c][KH*KW], then bias [c]; STEM: after the halo (no
+  // weight slice), t aliasing the input region instead
+  float* wdl = STEM ? wsl : t + p.cpad * 16 * R;
+  // STEM: input region [3][4R + 3][68], stem weights [c][27] (28 c floats
+  // of room), bias [c] (64 floats of room)
   float* xin = wdl + p.wdl_pad + (p.c + 63) / 64 * 64;
-  float* wsm = xin + ST_IN;
+  // (phase 2 writes t only after the barrier that ends phase S, the last
+  // reader of the input region)
+  if constexpr (STEM) t = xin;
+  float* wsm = xin + SG::IN;
   float* bsm = wsm + ST_K * p.c;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -149,8 +169,11 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     for (int u = 0; u < WS; u++)
       wreg[u] = col < p.mpad ? p.wk[(4 * u + (lane >> 4)) * p.mpad + col] : 0.0f;
   }
-  const int oy = blockIdx.x / p.tiles_x;
-  const int ox0 = (blockIdx.x - oy * p.tiles_x) * 16;
+  // this workgroup's output rows oy .. oy + R - 1 (rows past the map are
+  // computed from zeros and not stored)
+  const int ob = blockIdx.x / p.tiles_x;
+  const int oy = ob * R;
+  const int ox0 = (blockIdx.x - ob * p.tiles_x) * 16;
   const int64_t plane = (int64_t)p.h * p.w;
   const unsigned OOB = 0x80000000u;
 
@@ -179,11 +202,11 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
       if (p.xvec) {
         // chunk q: region row q / 17 (channel, row), columns jx0 - 1 + 4 (q % 17)
         // .. + 3, wholly inside or outside the image (width % 4 == 0)
-        for (int q0 = wave * 64; q0 < 3 * ST_RR * 17; q0 += 256) {
+        for (int q0 = wave * 64; q0 < 3 * SG::RR * 17; q0 += 256) {
           const int q = q0 + lane, cr = q / 17, j = q - 17 * cr;
-          const int c = cr / ST_RR, iy = jy0 + cr - c * ST_RR, ix = jx0 - 1 + 4 * j;
+          const int c = cr / SG::RR, iy = jy0 + cr - c * SG::RR, ix = jx0 - 1 + 4 * j;
           const bool ok = iy >= 0 && iy < p.hin && ix >= 0 && ix < p.win;
-          if (q < 3 * ST_RR * 17)
+          if (q < 3 * SG::RR * 17)
             lds_load16(ir, xin + 4 * q0, ok ? (unsigned)(((c * p.hin + iy) * p.win + ix) * 4) : OOB, 0);
         }
         for (int base = wave * 256; base < nws; base += 1024)
@@ -194,8 +217,8 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
           lds_load16(sbr, bsm, (unsigned)lane * 16u, 0);
         }
       } else {
-        for (int cr = wave; cr < 3 * ST_RR; cr += 4) {
-          const int c = cr / ST_RR, rr = cr - c * ST_RR;
+        for (int cr = wave; cr < 3 * SG::RR; cr += 4) {
+          const int c = cr / SG::RR, rr = cr - c * SG::RR;
           const int iy = jy0 + rr;
 #pragma unroll
           for (int j = 0; j < 2; j++) {
@@ -203,7 +226,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
             const bool ok = iy >= 0 && iy < p.hin && ix >= 0 && ix < p.win;
             if (j == 0 || lane < 3)
               __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                  ir, (__attribute__((address_space(3))) void*)(xin + cr * ST_RP + 64 * j), 4,
+                  ir, (__attribute__((address_space(3))) void*)(xin + cr * SG::RP + 64 * j), 4,
                   ok ? (unsigned)(((c * p.hin + iy) * p.win + ix) * 4) : OOB, 0, 0, 0);
           }
         }
@@ -326,7 +349,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     for (int s = 0; s < ST_K / 4; s++) {
       const int k = 4 * s + lg - 1;
       const int c = k / 9, ky = (k - 9 * c) / 3, kx = k - 9 * c - 3 * ky;
-      koff[s] = k < 0 ? -1 : (c * ST_RR + ky) * ST_RP + kx + p.xvec;
+      koff[s] = k < 0 ? -1 : (c * SG::RR + ky) * SG::RP + kx + p.xvec;
     }
     // this lane's weights and bias of every channel block, read once:
     // weight (k', channel) = w[ch][k' - 1], 0 for the leading term (27
@@ -344,28 +367,28 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
       for (int s = 0; s < ST_K / 4; s++) bw[cb][s] = koff[s] >= 0 ? bw[cb][s] : 0.0f;
-    for (int pb = wave; pb < ST_PB; pb += 4) {
+    for (int pb = wave; pb < SG::PB; pb += 4) {
       const int q = pb * 16 + l16;
-      const bool qok = q < ST_PX;
-      const int qr = (q >= 33) + (q >= 66), qc = q - 33 * qr;
-      const int poff = 2 * qr * ST_RP + 2 * qc;
+      const bool qok = q < SG::PX;
+      const int qr = q / 33, qc = q - 33 * qr;
+      const int poff = 2 * qr * SG::RP + 2 * qc;
       // the input operands, one LDS round trip (the leading term and pixels
       // past the tile read word 0 and select 0)
       float a[ST_K / 4];
 #pragma unroll
       for (int s = 0; s < ST_K / 4; s++) a[s] = xin[koff[s] >= 0 && qok ? koff[s] + poff : 0];
       // this lane's four output pixels: halo offset, inside the stem map
-      // (outside: the depthwise's zero padding).  Pixels past the tile
-      // (block 6, row 3) land in the channel pitch's spare words
-      // (3 ST_CT + 12 < ST_PCP), which the depthwise never reads.
+      // (outside: the depthwise's zero padding).  Pixels past the tile (the
+      // last block's, in row 2R + 1) land in the channel pitch's spare
+      // words, which the depthwise never reads.
       int hoff[4];
       bool inmap[4];
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int qo = pb * 16 + 4 * lg + v;
-        const int ro = (qo >= 33) + (qo >= 66) + (qo >= 99), co = qo - 33 * ro;
+        const int ro = qo / 33, co = qo - 33 * ro;
         const int sy = sy0 + ro, sx = sx0 + co;
-        hoff[v] = ro * ST_CT + co;
+        hoff[v] = ro * SG::CT + co;
         inmap[v] = sy >= 0 && sy < p.h && sx >= 0 && sx < p.w;
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -384,7 +407,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         if (cb < ncb) {
-          float* hc = halo + (cb * 16 + l16) * ST_PCP;
+          float* hc = halo + (cb * 16 + l16) * SG::PCP;
 #pragma unroll
           for (int v = 0; v < 4; v++) {
             const float y = act_k<AK>(p.bst ? acc[cb][v] + bb[cb] : acc[cb][v], p.act_s);
@@ -396,8 +419,9 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     __syncthreads();
   }
 
-  // phase 2: depthwise outputs of every channel for the 16 pixels; task e =
-  // (part, channel): pixels part * PX .. part * PX + PX - 1 of channel ci
+  // phase 2: depthwise outputs of every channel for the 16 pixels of each of
+  // the R rows; task e = (part, channel): row rw = part / (16 / PX), pixels
+  // pp * PX .. pp * PX + PX - 1 of it (pp = part % (16 / PX)), channel ci
   const int npx = p.oh * p.ow;
   {
     // halo columns of a task's row, from its 16-byte aligned start (the
@@ -407,11 +431,12 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
     constexpr bool V4 = (PX * SW) % 4 == 0;  // row start 16-byte aligned
     constexpr int NV = (NC + 3) / 4;
     constexpr int NR = V4 ? 4 * NV : NC;
-    const int ntask = p.cpad * (16 / PX);
+    const int ntask = p.cpad * (16 / PX) * R;
     for (int e = tid; e < ntask; e += 256) {
       const int part = e / p.cpad;
       const int ci = e - part * p.cpad;
-      const int px0 = part * PX;
+      const int rw = R == 1 ? 0 : part / (16 / PX);
+      const int px0 = (part - rw * (16 / PX)) * PX;
       float acc[PX];
 #pragma unroll
       for (int q = 0; q < PX; q++) acc[q] = 0.0f;
@@ -420,7 +445,8 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         const float* wp = wdl + ci * KH * KW;
 #pragma unroll
         for (int j = 0; j < KH * KW; j++) wv[j] = wp[j];
-        const float* hp = halo + ci * (VEC ? VecGeom<KH, KW, SW>::PITCH : p.pcp) + px0 * SW;
+        const float* hp = halo + ci * (VEC ? VecGeom<KH, KW, SW>::PITCH : p.pcp) +
+                          rw * p.sh * (VEC ? VecGeom<KH, KW, SW>::CT : p.ct) + px0 * SW;
         // every row read before the first FMA (one LDS round trip)
         float r[KH][NR];
 #pragma unroll
@@ -468,7 +494,7 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         const float v = act_k<AK>(acc[q] + bdv, p.act_d);
         o[q] = (ci < p.c && ox0 + px0 + q < p.ow) ? v : 0.0f;
       }
-      float* tp = t + ci * 16 + px0;
+      float* tp = t + ci * 16 * R + rw * 16 + px0;
       if constexpr (PX % 4 == 0) {
 #pragma unroll
         for (int q = 0; q < PX; q += 4) *(f32x4*)(tp + q) = f32x4{o[q], o[q + 1], o[q + 2], o[q + 3]};
@@ -480,103 +506,106 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   }
   __syncthreads();
 
-  // phase 3: pointwise chain of this wave's 16 channels
+  // phase 3: pointwise chain of this wave's 16 channels, for each of the R rows
   const int l16 = lane & 15, lg = lane >> 4;
   const int mb = slice * 4 + wave;            // 16-channel block index
   if (mb * 16 >= p.m) return;
-  const int px = oy * p.ow + ox0 + l16;
-  const bool pok = ox0 + l16 < p.ow;
-  f32x4 acc;
+  for (int rw = 0; rw < R; rw++) {
+    const int px = (oy + rw) * p.ow + ox0 + l16;
+    const bool pok = ox0 + l16 < p.ow && oy + rw < p.oh;
+    f32x4 acc;
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    const int mo = mb * 16 + 4 * lg + v;
-    float s0 = 0.0f;
-    if (p.bp && mo < p.m && pok && bias_seeded(p.seed_rule, mo, px, p.m, npx)) s0 = bpre[v];
-    acc[v] = s0;
-  }
-  const float* al = wsl + lg * 64 + ((wave * 16 + l16) ^ (16 * lg));   // swizzled rows
-  const float* bl = t + lg * 16 + l16;
-  const int nsteps = p.cpad >> 2;
-  int s = 0;
-  if constexpr (STEM) {
+    for (int v = 0; v < 4; v++) {
+      const int mo = mb * 16 + 4 * lg + v;
+      float s0 = 0.0f;
+      if (p.bp && mo < p.m && pok && bias_seeded(p.seed_rule, mo, px, p.m, npx)) s0 = bpre[v];
+      acc[v] = s0;
+    }
+    const float* al = wsl + lg * 64 + ((wave * 16 + l16) ^ (16 * lg));   // swizzled rows
+    const float* bl = t + lg * 16 * R + rw * 16 + l16;
+    const int nsteps = p.cpad >> 2;
+    int s = 0;
+    if constexpr (STEM) {
 #pragma unroll
-    for (int u = 0; u < WS; u++)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wreg[u], bl[u * 64], acc, 0, 0, 0);
-    s = nsteps;
-  }
-  if (s + 4 <= nsteps) {
-    // groups of 4 steps in two register sets: the next group's operands
-    // are read before this group's MFMAs (a group past the end re-reads
-    // the current one: in bounds, unused)
-    float a0[4], b0[4], a1[4], b1[4];
-    auto ld = [&](float* a, float* b, const float* ap, const float* bp) {
+      for (int u = 0; u < WS; u++)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wreg[u], bl[u * 64 * R], acc, 0, 0, 0);
+      s = nsteps;
+    }
+    // (the LDS-fed chain below: R = 1 launches only)
+    if (!STEM && s + 4 <= nsteps) {
+      // groups of 4 steps in two register sets: the next group's operands
+      // are read before this group's MFMAs (a group past the end re-reads
+      // the current one: in bounds, unused)
+      float a0[4], b0[4], a1[4], b1[4];
+      auto ld = [&](float* a, float* b, const float* ap, const float* bp) {
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        a[u] = ap[u * 256];
-        b[u] = bp[u * 64];
+        for (int u = 0; u < 4; u++) {
+          a[u] = ap[u * 256];
+          b[u] = bp[u * 64];
+        }
+      };
+      auto mm = [&](const float* a, const float* b) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+      };
+      const float* ap = al;
+      const float* bp = bl;
+      ld(a0, b0, ap, bp);
+      for (; s + 8 <= nsteps; s += 8) {
+        ld(a1, b1, ap + 1024, bp + 256);
+        mm(a0, b0);
+        const int nx = s + 12 <= nsteps ? 2 : 1;
+        ld(a0, b0, ap + nx * 1024, bp + nx * 256);
+        mm(a1, b1);
+        // reads of the next group ahead of each group's MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        ap += 2048;
+        bp += 512;
       }
-    };
-    auto mm = [&](const float* a, const float* b) {
-#pragma unroll
-      for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
-    };
-    const float* ap = al;
-    const float* bp = bl;
-    ld(a0, b0, ap, bp);
-    for (; s + 8 <= nsteps; s += 8) {
-      ld(a1, b1, ap + 1024, bp + 256);
-      mm(a0, b0);
-      const int nx = s + 12 <= nsteps ? 2 : 1;
-      ld(a0, b0, ap + nx * 1024, bp + nx * 256);
-      mm(a1, b1);
-      // reads of the next group ahead of each group's MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      ap += 2048;
-      bp += 512;
+      if (s + 4 <= nsteps) {
+        mm(a0, b0);
+        s += 4;
+      }
     }
-    if (s + 4 <= nsteps) {
-      mm(a0, b0);
-      s += 4;
-    }
-  }
-  for (; s < nsteps; s++)
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(al[s * 256], bl[s * 64], acc, 0, 0, 0);
+    for (; !STEM && s < nsteps; s++)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(al[s * 256], bl[s * 64], acc, 0, 0, 0);
 
-  // epilogue: bias terms first, then finish and store
-  float badd[4];
-  bool hadd[4];
+    // epilogue: bias terms first, then finish and store
+    float badd[4];
+    bool hadd[4];
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    const int mo = mb * 16 + 4 * lg + v;
-    hadd[v] = p.bp && mo < p.m && pok && !bias_seeded(p.seed_rule, mo, px, p.m, npx);
-    badd[v] = hadd[v] ? bpre[v] : 0.0f;
-  }
-  if (!pok) return;
-  float r[4];
+    for (int v = 0; v < 4; v++) {
+      const int mo = mb * 16 + 4 * lg + v;
+      hadd[v] = p.bp && mo < p.m && pok && !bias_seeded(p.seed_rule, mo, px, p.m, npx);
+      badd[v] = hadd[v] ? bpre[v] : 0.0f;
+    }
+    if (!pok) continue;
+    float r[4];
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    r[v] = acc[v];
-    if (hadd[v]) r[v] = r[v] + badd[v];
-    r[v] = act_k<AK>(r[v], p.act_p);
-  }
-  const int mo0 = mb * 16 + 4 * lg;
-  // channel-last: this lane's four channels of the pixel are adjacent, one
-  // 16-byte store when they are all inside M and 16-byte aligned
-  if (p.trans_out && mo0 + 3 < p.m && p.m % 4 == 0 && ((uintptr_t)p.y & 15) == 0) {
-    *(f32x4*)(p.y + ((int64_t)img * npx + px) * p.m + mo0) = f32x4{r[0], r[1], r[2], r[3]};
-    return;
-  }
+    for (int v = 0; v < 4; v++) {
+      r[v] = acc[v];
+      if (hadd[v]) r[v] = r[v] + badd[v];
+      r[v] = act_k<AK>(r[v], p.act_p);
+    }
+    const int mo0 = mb * 16 + 4 * lg;
+    // channel-last: this lane's four channels of the pixel are adjacent, one
+    // 16-byte store when they are all inside M and 16-byte aligned
+    if (p.trans_out && mo0 + 3 < p.m && p.m % 4 == 0 && ((uintptr_t)p.y & 15) == 0) {
+      *(f32x4*)(p.y + ((int64_t)img * npx + px) * p.m + mo0) = f32x4{r[0], r[1], r[2], r[3]};
+      continue;
+    }
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    const int mo = mo0 + v;
-    if (mo >= p.m) continue;
-    if (p.trans_out)
-      p.y[((int64_t)img * npx + px) * p.m + mo] = r[v];
-    else
-      p.y[((int64_t)img * p.m + mo) * npx + px] = r[v];
+    for (int v = 0; v < 4; v++) {
+      const int mo = mo0 + v;
+      if (mo >= p.m) continue;
+      if (p.trans_out)
+        p.y[((int64_t)img * npx + px) * p.m + mo] = r[v];
+      else
+        p.y[((int64_t)img * p.m + mo) * npx + px] = r[v];
+    }
   }
 }
 
@@ -780,7 +809,7 @@ bool dwpw_eligible(const DwPwArgs& a) {
          (a.m + 31) / 32 * 32 * ((a.c + 3) / 4 * 4) * 4 < (1ll << 31);
 }
 
-template <int KH, int KW, int SW, int PX, bool STEM, int AK, bool VEC>
+template <int KH, int KW, int SW, int PX, bool STEM, int AK, bool VEC, int R>
 static int launch_dwpw_a(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
   // the widest halo row read of a task stays inside its row
   static_assert(VEC || (16 - PX) * SW + 4 * (((PX - 1) * SW + KW + 3) / 4) <=
@@ -792,16 +821,16 @@ static int launch_dwpw_a(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
                                  : VecGeom<KH, KW, SW>::SHIFT + (PX - 1) * SW + KW) <=
                             VecGeom<KH, KW, SW>::CT,
                 "depthwise row reads past the halo row");
-  QPH_TRY(allow_full_lds((const void*)dwpw_kernel<KH, KW, SW, PX, STEM, AK, VEC>));
-  hipLaunchKernelGGL((dwpw_kernel<KH, KW, SW, PX, STEM, AK, VEC>), grid, dim3(256), lds, s, p);
+  QPH_TRY(allow_full_lds((const void*)dwpw_kernel<KH, KW, SW, PX, STEM, AK, VEC, R>));
+  hipLaunchKernelGGL((dwpw_kernel<KH, KW, SW, PX, STEM, AK, VEC, R>), grid, dim3(256), lds, s, p);
   return launch_check("dwpw_kernel");
 }
 
-template <int KH, int KW, int SW, int PX, bool STEM = false, bool VEC = false>
+template <int KH, int KW, int SW, int PX, bool STEM = false, bool VEC = false, int R = 1>
 static int launch_dwpw_t(dim3 grid, size_t lds, const DwPwK& p, hipStream_t s) {
   const bool hs = p.act_d.kind == 3 && p.act_p.kind == 3 && (!STEM || p.act_s.kind == 3);
-  return hs ? launch_dwpw_a<KH, KW, SW, PX, STEM, 3, VEC>(grid, lds, p, s)
-            : launch_dwpw_a<KH, KW, SW, PX, STEM, 0, VEC>(grid, lds, p, s);
+  return hs ? launch_dwpw_a<KH, KW, SW, PX, STEM, 3, VEC, R>(grid, lds, p, s)
+            : launch_dwpw_a<KH, KW, SW, PX, STEM, 0, VEC, R>(grid, lds, p, s);
 }
 
 template <int KH, int KW, int SW, bool VEC>
@@ -888,18 +917,43 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
     p.hin = (int)a.hin; p.win = (int)a.win;
     auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     p.xvec = a.win % 4 == 0 && al16(a.xin) && al16(a.wst) && (!a.bst || al16(a.bst));
-    // the stem phase writes the halo with these pitches as constants (and
-    // parks the pixels past its tile in the spare words of each channel)
-    if (p.ct != ST_CT || p.pcp != ST_PCP || 3 * ST_CT + 13 > ST_PCP)
-      return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: halo pitch");
     if (p.cpad != 16 * px || p.slices != 1)
       return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: unsupported shape");
-    lds -= (size_t)p.wrows * 4;   // pointwise weights in registers
-    p.wrows = 0;
-    lds += (size_t)(ST_IN + ST_K * a.c + 64) * 4;
+    // the stem phase writes the halo with this row pitch as a constant
+    if (p.ct != StemGeom<1>::CT || StemGeom<2>::CT != StemGeom<1>::CT)
+      return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: halo pitch");
+    p.wrows = 0;   // pointwise weights in registers
+    // LDS of the launch at R output rows a workgroup (t inside the input
+    // region: cpad 16 R <= 1024 floats, below the region's 1428 / 2244)
+    auto stem_lds = [&](int pcp, int in, int r) -> size_t {
+      if (p.cpad * 16 * r > in) return SIZE_MAX;
+      return (size_t)(p.c * pcp + p.wdl_pad + (p.c + 63) / 64 * 64 + in + ST_K * p.c + 64) * 4;
+    };
+    const size_t lds1 = stem_lds(StemGeom<1>::PCP, StemGeom<1>::IN, 1);
+    const size_t lds2 = stem_lds(StemGeom<2>::PCP, StemGeom<2>::IN, 2);
+    if (lds1 > 160 * 1024 || lds2 > 160 * 1024)
+      return fail(QPH_EUNSUPPORTED, "stem + dw + pw block: LDS");
+    // two output rows a workgroup when one-row workgroups would not all be
+    // resident at once (by LDS): the stem row the two rows share is
+    // computed once and the launch has half the workgroups, so the rec
+    // stem (1920 one-row workgroups of 27 KB) runs in one round instead of
+    // two; the det stem (1600 of 17 KB) already fits and keeps one row
+    int cus = 0;
+    QPH_TRY(device_cus(nullptr, &cus));
+    const int64_t wg1 = (int64_t)p.tiles_x * a.oh * a.n;
+    const bool two = wg1 > (int64_t)(160 * 1024 / lds1) * cus;
+    const int R = two ? 2 : 1;
+    p.pcp = two ? StemGeom<2>::PCP : StemGeom<1>::PCP;
+    p.halo = p.c * p.pcp;
+    lds = two ? lds2 : lds1;
+    grid.x = (unsigned)(p.tiles_x * ceil_div(a.oh, R));
     // cpad 16 -> 1 pixel per depthwise task, 32 -> 2
-    if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true, false>(grid, lds, p, s);
-    return launch_dwpw_t<3, 3, 2, 1, true, false>(grid, lds, p, s);
+    if (two) {
+      if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true, false, 2>(grid, lds, p, s);
+      return launch_dwpw_t<3, 3, 2, 1, true, false, 2>(grid, lds, p, s);
+    }
+    if (px == 2) return launch_dwpw_t<3, 3, 2, 2, true, false, 1>(grid, lds, p, s);
+    return launch_dwpw_t<3, 3, 2, 1, true, false, 1>(grid, lds, p, s);
   }
   if (dwpw_vec(a) && dwpw_reg_ok(a)) {
     if (a.kh == 5) return launch_dwpw_reg<5, 5, 1>(a.c, grid, p, s);

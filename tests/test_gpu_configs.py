@@ -485,6 +485,8 @@ STEM_CASES = [
     (1, 48, 100, 32, 64, ("hs", "hs", "hs"), True, False),         # rec-like, partial last tile
     (1, 48, 100, 32, 64, ("hs", "hs", "hs"), True, True),          # stem output also an output: not fused
     (3, 7, 9, 16, 16, ("hs", "hs", "hs"), True, False),            # tiny maps
+    (1, 44, 64, 32, 64, ("hs", "hs", "hs"), True, False),          # odd output height: a tile's second row past the map
+    (2, 42, 70, 16, 32, ("relu", "hs", "relu"), True, False),      # odd output height, width % 4 != 0 (one-word loads)
 ]
 
 
