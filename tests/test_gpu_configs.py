@@ -487,6 +487,9 @@ STEM_CASES = [
     (3, 7, 9, 16, 16, ("hs", "hs", "hs"), True, False),            # tiny maps
     (1, 44, 64, 32, 64, ("hs", "hs", "hs"), True, False),          # odd output height: a tile's second row past the map
     (2, 42, 70, 16, 32, ("relu", "hs", "relu"), True, False),      # odd output height, width % 4 != 0 (one-word loads)
+    # enough workgroups that one-row tiles would not all be resident: two output rows a workgroup
+    (32, 44, 300, 32, 64, ("hs", "hs", "hs"), True, False),        # rec-like, odd output height, partial tiles
+    (16, 64, 640, 16, 32, ("hs", "hs", "hs"), True, False),        # det-like, 16 stem channels
 ]
 
 
@@ -569,6 +572,30 @@ def test_session_block_paths(gpu, oracle, case):
     got = sess.run(x)
     ref = onets.run_graph(g, x)
     assert_bitexact(got[0], ref[0], "block output")
+    sess.close()
+
+
+@pytest.mark.parametrize("m", [64, 30])
+def test_session_block_channel_last_out(gpu, oracle, m):
+    """A register-fed depthwise + 1x1 block (C = 64, 16-byte path) whose 1x1
+    conv stores channel-last: 16-byte stores of four channels when M % 4 == 0,
+    one word a channel otherwise; bit-exact against the oracle."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    r = nets.WeightRng(41 + m)
+    g = nets.Graph((2, 64, 20, 40))
+    wd = g.weight(r.kaiming((64, 1, 3, 3), 9))
+    bd = g.weight(r.normal((64,), 0.1))
+    t = g.conv(0, wd, bd, stride=(1, 1), pad=(1, 1, 1, 1), group=64, act=nets.ACT_HARDSWISH)
+    wp = g.weight(r.kaiming((m, 64, 1, 1), 64))
+    bp = g.weight(r.normal((m,), 0.1))
+    y = g.conv(t, wp, bp, act=nets.ACT_HARDSWISH, trans_out=True)
+    g.outputs = [y]
+    x = r.uniform((2, 64, 20, 40), -1.0, 1.0)
+    sess = nets.HipSession(g)
+    got = sess.run(x)
+    ref = onets.run_graph(g, x)
+    assert_bitexact(got[0], ref[0], "channel-last block output")
     sess.close()
 
 
