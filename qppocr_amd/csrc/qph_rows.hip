@@ -1213,8 +1213,9 @@ __global__ __launch_bounds__(512) void qkv_attention_kernel(const float* __restr
   f32x4 acc[3];
 #pragma unroll
   for (int i = 0; i < 3; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  // a wave's blocks j = wave + 8 i; past nblk it multiplies block 0 again
-  // (no branches in the chain; those results are never used)
+  // a wave's blocks j = wave + 8 i; a wave whose third block is past nblk
+  // runs the two-chain form of the slab loop (past nblk, a block index
+  // reads block 0: in bounds, never used)
   int arow[3], wrow[3];
 #pragma unroll
   for (int i = 0; i < 3; i++) {
@@ -1222,38 +1223,47 @@ __global__ __launch_bounds__(512) void qkv_attention_kernel(const float* __restr
     arow[i] = (16 * rb + l16) * 64 + lg;
     wrow[i] = (QA_ROWS + 16 * cb + l16) * 64 + lg;
   }
+  // the slab loop over NB of the wave's chains (every wave reaches every
+  // barrier whichever form it runs)
+  auto slabs = [&](auto nbc) {
+    constexpr int NB = decltype(nbc)::value;
 #pragma unroll
-  for (int kt = 0; kt < NK; kt++) {
-    __asm__ volatile("" ::: "memory");
-    if (kt + 1 < NK)
-      wait_vmcnt<5>();
-    else
-      wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-    const float* st = (kt & 1) ? st1 : st0;
-    float av[3][16], bv[3][16];
-#pragma unroll
-    for (int i = 0; i < 3; i++)
-#pragma unroll
-      for (int s4 = 0; s4 < 16; s4++) {
-        av[i][s4] = st[arow[i] + 4 * (s4 ^ l16)];
-        bv[i][s4] = st[wrow[i] + 4 * (s4 ^ l16)];
-      }
-#pragma unroll
-    for (int s4 = 0; s4 < 16; s4++)
-#pragma unroll
-      for (int i = 0; i < 3; i++)
-        acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][s4], bv[i][s4], acc[i], 0, 0, 0);
-    if (kt + 2 < NK) {
-      // every wave's reads of this stage done, then its refill
+    for (int kt = 0; kt < NK; kt++) {
+      __asm__ volatile("" ::: "memory");
+      if (kt + 1 < NK)
+        wait_vmcnt<5>();
+      else
+        wait_vmcnt<0>();
       __builtin_amdgcn_s_waitcnt(0xC07F);
       __builtin_amdgcn_s_barrier();
       __asm__ volatile("" ::: "memory");
-      issue(kt + 2, (kt & 1) ? st1 : st0);
+      const float* st = (kt & 1) ? st1 : st0;
+      float av[NB][16], bv[NB][16];
+#pragma unroll
+      for (int i = 0; i < NB; i++)
+#pragma unroll
+        for (int s4 = 0; s4 < 16; s4++) {
+          av[i][s4] = st[arow[i] + 4 * (s4 ^ l16)];
+          bv[i][s4] = st[wrow[i] + 4 * (s4 ^ l16)];
+        }
+#pragma unroll
+      for (int s4 = 0; s4 < 16; s4++)
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][s4], bv[i][s4], acc[i], 0, 0, 0);
+      if (kt + 2 < NK) {
+        // every wave's reads of this stage done, then its refill
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        issue(kt + 2, (kt & 1) ? st1 : st0);
+      }
     }
-  }
+  };
+  if (wave + 16 < nblk)
+    slabs(std::integral_constant<int, 3>{});
+  else
+    slabs(std::integral_constant<int, 2>{});
   __syncthreads();   // the stages are free: q, k, v go where they were
   float* sq = sm;                       // tp x LD (scaled q)
   float* sk = sq + QA_ROWS * LD;        // tp x LD
