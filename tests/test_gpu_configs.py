@@ -631,6 +631,37 @@ def test_session_channel_last_chain_px(gpu, oracle):
     sess.close()
 
 
+def test_session_channel_last_blocks_wide(gpu, oracle):
+    """Channel-last depthwise + 1x1 blocks over wide rows (105 and 53
+    columns), C = 64, 128, 256, x-stride 2 at C = 128, and a ReLU depthwise
+    next to the inline HardSigmoid + Mul; bit-exact against the oracle."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    r = nets.WeightRng(53)
+    g = nets.Graph((2, 3, 16, 420))
+    ws = g.weight(r.kaiming((32, 3, 3, 3), 27))
+    bs = g.weight(r.normal((32,), 0.1))
+    x = g.conv(0, ws, bs, stride=(2, 2), pad=(1, 1, 1, 1), act=nets.ACT_HARDSWISH)
+    blocks = [  # (dw stride, dw activation, cin, cout)
+        ((1, 1), nets.ACT_HARDSWISH, 32, 64), ((2, 2), nets.ACT_HARDSWISH, 64, 128),
+        ((1, 2), nets.ACT_RELU, 128, 256), ((1, 1), nets.ACT_HARDSWISH, 256, 256),
+    ]
+    for i, (st, act, cin, cout) in enumerate(blocks):
+        wd = g.weight(r.kaiming((cin, 1, 3, 3), 9))
+        bd = g.weight(r.normal((cin,), 0.1))
+        x = g.conv(x, wd, bd, stride=st, pad=(1, 1, 1, 1), group=cin, act=act)
+        wp = g.weight(r.kaiming((cout, cin, 1, 1), cin))
+        bp = g.weight(r.normal((cout,), 0.1))
+        x = g.conv(x, wp, bp, act=nets.ACT_HARDSWISH, trans_out=i == len(blocks) - 1)
+    g.outputs = [x]
+    xin = r.uniform((2, 3, 16, 420), -1.0, 1.0)
+    sess = nets.HipSession(g)
+    got = sess.run(xin)
+    ref = onets.run_graph(g, xin)
+    assert_bitexact(got[0], ref[0], "chain output")
+    sess.close()
+
+
 def test_session_channel_last_chain(gpu, oracle):
     """A chain of depthwise -> 1x1 blocks ending in a 1x1 conv that stores
     [n][pixels][M] runs channel-last (depthwise_cl_kernel + the 1x1 convs as
