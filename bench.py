@@ -13,12 +13,16 @@ step's top-2 logit gap is below 1e-4).  Beside it: rec_lines_per_s_bitexact_
 pairs, the graph with the separate head softmax whose pairs are bit-exact,
 and rec_lines_per_s_with_probs, that graph exporting the probability tensor
 too.
-The det and rec sessions run on two contexts (two streams), as a page
-pipeline runs the det of one page next to the rec of another: value = steps
-per second = det images per second with 32 recognised lines each, over the
-wall time of K steps with both streams busy.  det_img_per_s and
-rec_lines_per_s are the stage-isolated rates (HIP events around each
-session alone, on its own stream).
+The det and rec sessions run on contexts (streams) of their own, as a page
+pipeline runs the det of one page next to the rec of another, with
+--pages-in-flight pages (default 2) in flight at once: page i of the K timed
+steps runs on det and rec session pair i % P, each pair on two streams of
+its own (2 pages: 4 streams, the hardware queues a process gets here).
+value = steps per second = det images per second with 32 recognised lines
+each, over the wall time of the K steps; one_page_in_flight gives the same K
+steps on one det and one rec stream.  det_img_per_s and rec_lines_per_s are
+the stage-isolated rates (HIP events around each session alone, on its own
+stream).
 
 roofline: the dominant kernel, the fused rec head (GEMM 1280 x 18709 x
 256, 12.26 GFLOP of the step's 20.86, with the softmax / argmax epilogue),
@@ -624,6 +628,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--pages-in-flight", type=int, default=2,
+                    help="pages the timed headline keeps in flight, each on its own det and rec "
+                         "session (two streams a page; 2 fills the 4 hardware queues)")
     ap.add_argument("--cpu-rounds", type=int, default=5,
                     help="CPU baseline: least timed rounds (median) after one warm-up round; "
                          "more run until the leg's time floor is reached")
@@ -698,22 +705,37 @@ def main():
                               sync_all, args.plan_report)
         print(json.dumps({"plan_model": leg, "steps": args.steps, "warmup": args.warmup}))
         return
+    # the other pages in flight: a det and a rec session each, on contexts
+    # (streams) of their own.  Every context is created before any session:
+    # the HIP runtime hands hardware queues to streams in turn, and creating
+    # a session takes queues from the same rotation, so a context created
+    # after sessions can share a queue with an earlier stream and run behind it
+    P = max(1, args.pages_in_flight)
+    extra_ctx = [ops.new_context(0) for _ in range(2 * (P - 1))]
     det = nets.HipSession(det_g, ctx=ctx)
     rec = nets.HipSession(rec_g, ctx=ctx_rec)
+    pages = [(det, rec)]
+    for j in range(P - 1):
+        pages.append((nets.HipSession(det_g, ctx=extra_ctx[2 * j]),
+                      nets.HipSession(rec_g, ctx=extra_ctx[2 * j + 1])))
     # inputs resident in HBM: copied once, then every step reuses them
-    det.run(det_x, outputs=False)
-    rec.run(rec_x, outputs=False)
-    det.sync()
-    rec.sync()
+    for d, r in pages:
+        d.run(det_x, outputs=False)
+        r.run(rec_x, outputs=False)
+    for d, r in pages:
+        d.sync()
+        r.sync()
 
     def both_sync():
-        det.sync()
-        rec.sync()
+        for d, r in pages:
+            d.sync()
+            r.sync()
         torch.cuda.synchronize()
 
     for _ in range(args.warmup):
-        det.run(None, outputs=False)
-        rec.run(None, outputs=False)
+        for d, r in pages:
+            d.run(None, outputs=False)
+            r.run(None, outputs=False)
     both_sync()
 
     K = args.steps
@@ -731,7 +753,18 @@ def main():
     det_ms = stage_ms(det, stream)
     rec_ms = stage_ms(rec, stream_rec)
 
-    # the timed region: K steps, det and rec of each step on their streams
+    # the timed region: K steps (pages), det and rec of each on their
+    # streams, page i on session pair i % P: P pages in flight
+    both_sync()
+    t0 = time.perf_counter()
+    for i in range(K):
+        d, r = pages[i % P]
+        d.run(None, outputs=False)
+        r.run(None, outputs=False)
+    both_sync()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / K
+    # the same K steps with one page in flight (one det and one rec stream)
     both_sync()
     t0 = time.perf_counter()
     for i in range(K):
@@ -739,7 +772,13 @@ def main():
         rec.run(None, outputs=False)
     both_sync()
     t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / K
+    ms_step_one = (t1 - t0) * 1e3 / K
+    for d, r in pages[1:]:
+        d.close()
+        r.close()
+    for c in extra_ctx:
+        ops.close_context(c)
+    pages = pages[:1]
 
     # the same step with host buffers at the boundary, through the sessions'
     # pinned staging buffers (deferred runs): det input up and det map down,
@@ -832,6 +871,7 @@ def main():
         "data": "synthetic (seeded inputs, random-init weights)",
         "config": {"workload": "det 1x3x640x640 + rec 32x3x48x320 per step, "
                                "rec ending in the CTC (value, index) pairs",
+                   "pages_in_flight": P,
                    "det_gflop": round(det_flops / 1e9, 3), "rec_gflop": round(rec_flops / 1e9, 3)},
         "det_img_per_s": round(1e3 / det_ms, 2),
         "rec_lines_per_s": round(REC_BATCH * 1e3 / rec_ms, 1),
@@ -840,6 +880,8 @@ def main():
         "det_ms": round(det_ms, 4),
         "rec_ms": round(rec_ms, 4),
         "serial_ms_per_step": round(det_ms + rec_ms, 4),
+        "one_page_in_flight": {"value": round(1e3 / ms_step_one, 3),
+                               "ms_per_step": round(ms_step_one, 4)},
         "pcie_inclusive_img_per_s": round(1e3 / host_ms_step, 3),
         "roofline": {"bound": "mfma",
                      "kernel": "fused rec head: GEMM 1280x18709x256 + softmax/argmax epilogue "
