@@ -86,7 +86,9 @@ struct DwPwK {
 // starting one column further left).  The halo rows are CT = 36 floats
 // apart; a channel's pitch PCP holds its 2R + 1 rows and the spare words
 // where the pixels past the tile of the last 16-pixel block land, and is
-// 4 mod 64 (16 lanes reading 16 consecutive channels hit distinct banks).
+// 4 or 60 mod 64 (16 lanes reading 16 consecutive channels hit distinct
+// banks).  At one row, 124 floats keep a 16-channel det stem workgroup
+// within 16 KB of LDS (what the rec head GEMM leaves free on a CU).
 template <int R>
 struct StemGeom {
   static constexpr int RR = 4 * R + 3;
@@ -96,8 +98,8 @@ struct StemGeom {
   static constexpr int PX = ROWS * 33;
   static constexpr int PB = (PX + 15) / 16;
   static constexpr int CT = 36;
-  static constexpr int PCP = R == 1 ? 132 : 196;
-  static_assert(ROWS * CT + (PB * 16 - PX) <= PCP && PCP % 64 == 4, "stem halo pitch");
+  static constexpr int PCP = R == 1 ? 124 : 196;
+  static_assert(ROWS * CT + (PB * 16 - PX) <= PCP && (PCP % 64 == 4 || PCP % 64 == 60), "stem halo pitch");
 };
 #define ST_K 28            // 27 taps after one leading zero term
 
@@ -138,9 +140,9 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
   // depthwise weights [c][KH*KW], then bias [c]; STEM: after the halo (no
   // weight slice), t aliasing the input region instead
   float* wdl = STEM ? wsl : t + p.cpad * 16 * R;
-  // STEM: input region [3][4R + 3][68], stem weights [c][27] (28 c floats
-  // of room), bias [c] (64 floats of room)
-  float* xin = wdl + p.wdl_pad + (p.c + 63) / 64 * 64;
+  // STEM: depthwise bias [c] after its weights, input region [3][4R + 3][68],
+  // stem weights [c][27] (28 c floats of room), stem bias [c]
+  float* xin = wdl + p.wdl_pad + (STEM ? (p.c + 3) / 4 * 4 : (p.c + 63) / 64 * 64);
   // (phase 2 writes t only after the barrier that ends phase S, the last
   // reader of the input region)
   if constexpr (STEM) t = xin;
@@ -237,8 +239,9 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         if (p.bst && wave == 0) {
           const __amdgpu_buffer_rsrc_t sbr =
               __builtin_amdgcn_make_buffer_rsrc((void*)p.bst, 0, p.c * 4, 0x00020000);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(sbr, (__attribute__((address_space(3))) void*)bsm,
-                                                   4, (unsigned)lane * 4u, 0, 0, 0);
+          if (lane < p.c)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sbr, (__attribute__((address_space(3))) void*)bsm,
+                                                     4, (unsigned)lane * 4u, 0, 0, 0);
         }
       }
     } else if constexpr (VEC) {
@@ -324,9 +327,10 @@ __global__ __launch_bounds__(256) void dwpw_kernel(DwPwK p) {
         const __amdgpu_buffer_rsrc_t br =
             __builtin_amdgcn_make_buffer_rsrc((void*)p.bd, 0, p.c * 4, 0x00020000);
         for (int base = wave * 64; base < p.c; base += 256)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              br, (__attribute__((address_space(3))) void*)(wdl + p.wdl_pad + base), 4,
-              (unsigned)(base + lane) * 4u, 0, 0, 0);
+          if (base + lane < p.c)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                br, (__attribute__((address_space(3))) void*)(wdl + p.wdl_pad + base), 4,
+                (unsigned)(base + lane) * 4u, 0, 0, 0);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -927,7 +931,7 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s) {
     // region: cpad 16 R <= 1024 floats, below the region's 1428 / 2244)
     auto stem_lds = [&](int pcp, int in, int r) -> size_t {
       if (p.cpad * 16 * r > in) return SIZE_MAX;
-      return (size_t)(p.c * pcp + p.wdl_pad + (p.c + 63) / 64 * 64 + in + ST_K * p.c + 64) * 4;
+      return (size_t)(p.c * pcp + p.wdl_pad + (p.c + 3) / 4 * 4 + in + ST_K * p.c + (p.c + 3) / 4 * 4) * 4;
     };
     const size_t lds1 = stem_lds(StemGeom<1>::PCP, StemGeom<1>::IN, 1);
     const size_t lds2 = stem_lds(StemGeom<2>::PCP, StemGeom<2>::IN, 2);
