@@ -1081,13 +1081,14 @@ int launch_head_argmax(const float* x, int64_t m, int64_t k, const float* w, int
   g.bias = bias; g.bias_mode = bias ? 2 : 0;
   g.act = make_act(nullptr);
   g.part = part;
-  int occ = 0, cus = 0;
-  QPH_TRY(device_cus(nullptr, &cus));
-  QPH_TRY(kernel_occupancy((const void*)gemm_wave_kernel<WV_EPI_ARGMAX>, 64, &occ));
   const int mb = (int)ceil_div(m, 64), nb = (int)ceil_div(n, 64);
   const int ntiles = mb * nb;
   const int per_xcd = (ntiles + NUM_XCD - 1) / NUM_XCD;
-  const int wg_xcd = std::max(1, std::min(per_xcd, occ * cus / NUM_XCD));
+  // one tile a wave (not persistent): with pages in flight the other
+  // streams' kernels get CUs between the head's waves (two pages: 3477
+  // against 3421 steps/s with the persistent grid); alone on the GPU the
+  // persistent grid is ahead (one page in flight: 2877 against 2801)
+  const int wg_xcd = std::max(1, per_xcd);
   hipLaunchKernelGGL(gemm_wave_kernel<WV_EPI_ARGMAX>, dim3((unsigned)(wg_xcd * NUM_XCD)), dim3(64),
                      0, s, g, mb, nb, ntiles, per_xcd, wg_xcd);
   QPH_TRY(launch_check("gemm_wave_kernel<argmax>"));
