@@ -542,6 +542,17 @@ __global__ __launch_bounds__(256) void conv3x3_direct_group_kernel(DirectConvGro
 #define LC_DMA (LC_STAGE / 256)         // 16 loads per chunk, 4 per wave
 #define LC_LEAD 6                       // steps the operand reads run ahead
 
+// The det head's conv-transpose pair and sigmoid, run in the epilogue of the
+// 3x3 conv before it (CVT): w1 [24][24][2][2] and w2 [24][1][2][2] in their
+// ONNX layouts, y [n][1][4 oh][4 ow].
+struct ConvtEpi {
+  const float* w1;
+  const float* w2;
+  float* y;
+};
+#define CV_C 24    // channels of the conv output and of the first ConvT
+#define CV_HP 28   // LDS pitch of a pixel's 24 conv outputs (16-byte rows)
+
 struct LdsConvGroup {
   DirectConvK k[DIRECT_GROUP_MAX];
   int tiles_x[DIRECT_GROUP_MAX];
@@ -558,10 +569,11 @@ struct LdsConvGroup {
 // read from LDS before its MFMAs (so the reads' latency is paid once a chunk,
 // not once a step), and AK (0 none, 2 ReLU, -1 any kind through act_apply)
 // keeps the epilogue free of the generic activation switch.
-template <int AK, bool ONE>
+template <int AK, bool ONE, bool CVT = false>
 __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x, int tile,
                                               float* s0, float* s1, float* s2, float* s3,
-                                              int wave, int lane) {
+                                              int wave, int lane,
+                                              const ConvtEpi& cv = ConvtEpi{}) {
   // every parameter the loads depend on, fetched in one batch of scalar
   // loads (left alone, the compiler fetches them in dependent rounds as the
   // code first uses them, each round a full kernel-argument load latency)
@@ -641,6 +653,16 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
       const int co = mt * 16 + 4 * lg + v;
       bld[mt][v] = (p.bias && co < p.m) ? p.bias[co] : 0.0f;
     }
+  // CVT: this thread's share of the ConvT weights (w1 element tid + 256 j,
+  // w2 element tid), loaded before the chunks as the bias is; the epilogue
+  // stages them in LDS
+  float w1r[CVT ? 9 : 1], w2r = 0.0f;
+  if constexpr (CVT) {
+    const int tid = wave * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < 9; j++) w1r[j] = cv.w1[tid + 256 * j];
+    if (tid < 4 * CV_C) w2r = cv.w2[tid];
+  }
 
   __asm__ volatile("" ::: "memory");
   const int nch = p.c / LC_CC;   // ONE: exactly 4 (C = 32)
@@ -761,6 +783,81 @@ __device__ __forceinline__ void lds_conv_tile(const DirectConvK& p, int tiles_x,
     }
   }
 
+  if constexpr (CVT) {
+    // The conv outputs (bias, activation) of this wave's 16 pixels go to LDS,
+    // and the ConvT weights, in the two ring stages the last chunk did not
+    // use: every wave is past that chunk's barrier, so no wave reads them any
+    // more.  The first ConvT is then a 96 x 24 by 24 x 16 product per wave on
+    // the MFMAs: row 4 q + v of M tile mt is (tap q, channel 4 mt + v), so that
+    // lane (pixel l16, g) ends with the 24 intermediates of its pixel and tap
+    // q = g in its registers, each the chain over ci of fma(x[ci], w1[ci][co][q])
+    // from 0, in ci order (k = 4 s + g), as convt_pair_sigmoid_kernel chains it.
+    // The second ConvT (chain over co) and the sigmoid follow in the lane.
+    const int last = (nch - 1) % LC_NST;
+    float* fa = last == 0 ? s1 : s0;
+    float* fb = last == 2 ? s1 : s2;
+    float* hh = fa + wave * 16 * CV_HP;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int co = mt * 16 + 4 * lg + v;
+        float xv = acc[mt][v] + bterm[mt][v];
+        if constexpr (AK == 2)
+          xv = relu1(xv);
+        else if constexpr (AK < 0)
+          xv = act_apply(xv, p.act);
+        if (co < CV_C) hh[l16 * CV_HP + co] = xv;
+      }
+    // A operands in MFMA order [mt][s][lane]: lane g 16 + i of step s, tile mt
+    // holds w1[ci = 4 s + g][co = 4 mt + (i & 3)][q = i >> 2]
+    float* sa = fb;
+    float* sw2 = fb + 4 * CV_C * CV_C;  // [co][q2]
+    {
+      const int tid = wave * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < 9; j++) {
+        const int i = tid + 256 * j;   // (ci * 24 + co) * 4 + q
+        const int ci = i / (4 * CV_C), co = (i >> 2) % CV_C, q = i & 3;
+        sa[((co >> 2) * (CV_C / 4) + (ci >> 2)) * 64 + (ci & 3) * 16 + q * 4 + (co & 3)] = w1r[j];
+      }
+      if (tid < 4 * CV_C) sw2[tid] = w2r;
+    }
+    __syncthreads();
+    // every lane takes part in the products (an idle lane's A row would be
+    // lost to every pixel); only the stores are per pixel
+    float bx[CV_C / 4];
+#pragma unroll
+    for (int s = 0; s < CV_C / 4; s++) bx[s] = hh[l16 * CV_HP + 4 * s + lg];
+    f32x4 mid[CV_C / 4];
+#pragma unroll
+    for (int mt = 0; mt < CV_C / 4; mt++) {
+      mid[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < CV_C / 4; s++)
+        mid[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sa[(mt * (CV_C / 4) + s) * 64 + lane], bx[s],
+                                                       mid[mt], 0, 0, 0);
+    }
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int co = 0; co < CV_C; co++) {
+      const f32x4 wv = *(const f32x4*)(sw2 + co * 4);
+      const float mv = mid[co >> 2][co & 3];
+      o[0] = __builtin_fmaf(mv, wv[0], o[0]);
+      o[1] = __builtin_fmaf(mv, wv[1], o[1]);
+      o[2] = __builtin_fmaf(mv, wv[2], o[2]);
+      o[3] = __builtin_fmaf(mv, wv[3], o[3]);
+    }
+    if (!pval) return;
+    const int ky = lg >> 1, kx = lg & 1;
+    const int64_t ow4 = 4 * (int64_t)p.ow;
+    float* yo = cv.y + ((int64_t)img * 4 * p.oh + 4 * poy + 2 * ky) * ow4 + 4 * pox + 2 * kx;
+    yo[0] = sigmoid1(o[0]);
+    yo[1] = sigmoid1(o[1]);
+    yo[ow4] = sigmoid1(o[2]);
+    yo[ow4 + 1] = sigmoid1(o[3]);
+    return;
+  }
   // epilogue as in direct3x3_unit; every residual term is read before the
   // first store (a load after a store that may alias the output makes the
   // compiler wait for that store to complete, once per output)
@@ -808,6 +905,19 @@ __global__ __launch_bounds__(256) void conv3x3_lds_kernel(LdsConvGroup g) {
     lds_conv_tile<AK, false>(g.k[i], g.tiles_x[i], t - g.start[i], s0, s1, s2, nullptr, wave,
                              lane);
   }
+}
+
+// The det head: a 3x3 conv to 24 channels (lds_conv_tile, one conv) with the
+// conv-transpose pair and sigmoid after it in the epilogue; the conv output
+// never reaches HBM.
+template <int AK>
+__global__ __launch_bounds__(256) void conv3x3_lds_convt_kernel(DirectConvK k, int tiles_x,
+                                                                ConvtEpi cv) {
+  __shared__ __attribute__((aligned(16))) float s0[LC_STAGE], s1[LC_STAGE], s2[LC_STAGE];
+  static_assert(4 * 16 * CV_HP <= LC_STAGE && 4 * CV_C * CV_C + 4 * CV_C <= LC_STAGE, "");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+  lds_conv_tile<AK, false, true>(k, tiles_x, blockIdx.x, s0, s1, s2, nullptr, wave, lane, cv);
 }
 
 // One plain 32-channel conv (no residual, no upsampled store, no activation
@@ -902,6 +1012,35 @@ static int launch_lds3x3(const ConvArgs* a, int n, hipStream_t s) {
       hipLaunchKernelGGL((conv3x3_lds_kernel<-1, 4>), grid, dim3(256), 0, s, g);
   }
   return launch_check("conv3x3_lds_kernel");
+}
+
+// The conv of the det head with its conv-transpose pair (24 -> 24 -> 1, 2x2
+// stride 2 each) and sigmoid in one launch: a 3x3 conv to 24 channels that
+// lds_conv_tile takes, stored plainly (no residual, slot or upsample), ReLU
+// or no activation.
+bool conv3x3_convt_eligible(const ConvArgs& a) {
+  return lds3x3_eligible(a) && a.m == CV_C && !a.res && a.y_up == 1 &&
+         (a.y_ctotal == 0 || a.y_ctotal == a.m) && a.y_coff == 0 &&
+         (a.act.kind == 0 || a.act.kind == 2) && a.n * 16 * a.oh * a.ow < (1ll << 31);
+}
+
+int launch_conv3x3_convt(const ConvArgs& a, const float* w1, const float* w2, float* y,
+                         hipStream_t s) {
+  if (!a.wk || !conv3x3_convt_eligible(a))
+    return fail(QPH_EUNSUPPORTED, "conv + conv-transpose pair: unsupported shape");
+  DirectConvK k{};
+  direct_params(a, a.wk, k);
+  const int tiles_x = (int)ceil_div(a.ow, 32);
+  const int64_t total = (int64_t)tiles_x * ceil_div(a.oh, 2) * a.n;
+  if (total >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "conv: grid too large");
+  const ConvtEpi cv{w1, w2, y};
+  if (a.act.kind == 2)
+    hipLaunchKernelGGL(conv3x3_lds_convt_kernel<2>, dim3((unsigned)total), dim3(256), 0, s, k,
+                       tiles_x, cv);
+  else
+    hipLaunchKernelGGL(conv3x3_lds_convt_kernel<0>, dim3((unsigned)total), dim3(256), 0, s, k,
+                       tiles_x, cv);
+  return launch_check("conv3x3_lds_convt_kernel");
 }
 
 int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s) {

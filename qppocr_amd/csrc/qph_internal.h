@@ -297,6 +297,13 @@ int launch_dwpw(const DwPwArgs& a, hipStream_t s);
 // 3x3 convs the direct kernel takes; up to four independent ones in one launch
 bool direct3x3_eligible(const ConvArgs& a);
 int launch_dense_conv_group(const ConvArgs* a, int n, hipStream_t s);
+// A 3x3 conv to 24 channels with the det head's conv-transpose pair (w1
+// [24][24][2][2], w2 [24][1][2][2]) and sigmoid in its epilogue: y [n][1][4
+// oh][4 ow]; the conv output is never stored.  a as conv_dispatch plans it
+// (resident weights).
+bool conv3x3_convt_eligible(const ConvArgs& a);
+int launch_conv3x3_convt(const ConvArgs& a, const float* w1, const float* w2, float* y,
+                         hipStream_t s);
 int launch_depthwise(const ConvArgs& a, hipStream_t s);
 // depthwise conv with x and y channel-last ([n][h][w][c]); 3x3 and 5x5
 int launch_depthwise_cl(const ConvArgs& a, hipStream_t s);

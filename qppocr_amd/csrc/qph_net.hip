@@ -25,6 +25,7 @@ struct qph_net {
   std::vector<float*> wk;        // per node: resident repacked dense-conv weights (or NULL)
   std::vector<ConvArgs> plan;    // per node: launch arguments of a dense 3x3 conv
   std::vector<int> group_len;    // > 1: first of that many independent 3x3 convs, one launch
+  std::vector<bool> convt_fused; // 3x3 conv node i and its conv-transpose pair i + 1, one launch
   std::vector<DwPwArgs> dwpw;    // per node: fused depthwise + pointwise launch
   std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1, and i + 2 for a stem, with it)
   std::vector<float*> wt;        // per linear node: resident transposed weight Wt[N][K] (or NULL)
@@ -379,6 +380,37 @@ static void plan_conv_groups(qph_net* net) {
       if (j - i >= 2) net->group_len[i] = (int)(j - i);
     }
     i = j > i ? j : i + 1;
+  }
+}
+
+// A single 3x3 conv whose output only the conv-transpose pair after it reads
+// (the det head: conv 96 -> 24, ReLU, then ConvT -> ConvT -> Sigmoid): one
+// launch, the pair in the conv's epilogue (launch_conv3x3_convt).
+static void plan_conv_convt(qph_net* net) {
+  const size_t nn = net->nodes.size();
+  net->convt_fused.assign(nn, false);
+  std::vector<bool> grouped(nn, false);
+  for (size_t i = 0; i < nn; i++)
+    for (int k = 1; k < net->group_len[i] && i + (size_t)k < nn; k++) grouped[i + (size_t)k] = true;
+  std::vector<int> readers(net->tptr.size(), 0);
+  for (const qph_node& n : net->nodes) {
+    readers[(size_t)storage_of(net, n.in)]++;
+    if (n.in2 >= 0) readers[(size_t)storage_of(net, n.in2)]++;
+    if (n.in3 >= 0) readers[(size_t)storage_of(net, n.in3)]++;
+  }
+  for (int32_t o : net->outputs) readers[(size_t)storage_of(net, o)]++;
+  for (size_t i = 0; i + 1 < nn; i++) {
+    const qph_node& d = net->nodes[i];
+    const qph_node& q = net->nodes[i + 1];
+    if (d.op != QPH_OP_CONV || q.op != QPH_OP_CONVT_PAIR_SIG || !net->plan[i].wk) continue;
+    if (net->group_len[i] > 1 || grouped[i]) continue;
+    if (storage_of(net, d.out) != d.out || storage_of(net, q.in) != d.out ||
+        readers[(size_t)d.out] != 1)
+      continue;
+    const int64_t* xs = &net->shapes[4 * (size_t)q.in];
+    if (xs[1] != 24 || q.ws[1] != 24 || q.w2 < 0) continue;
+    if (!conv3x3_convt_eligible(net->plan[i])) continue;
+    net->convt_fused[i] = true;
   }
 }
 
@@ -754,6 +786,14 @@ static int run_all(qph_net* net) {
                                         net->head_part[i], net->tptr[r.out2], s);
       if (rc != QPH_OK) return fail(rc, node_name(i, q) + ": " + qph_last_error());
       step = 2;
+    } else if (net->convt_fused[i]) {
+      const qph_node& q = net->nodes[i + 1];
+      ConvArgs a = net->plan[i];
+      a.n = net->real_n;
+      const int rc = launch_conv3x3_convt(a, net->weights[q.w], net->weights[q.w2],
+                                          net->tptr[q.out], s);
+      if (rc != QPH_OK) return fail(rc, node_name(i, net->nodes[i]) + ": " + qph_last_error());
+      step = 2;
     } else if (net->fused[i]) {
       DwPwArgs f = net->dwpw[i];
       f.n = net->real_n;
@@ -1034,6 +1074,7 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
   if (spec->flags & QPH_NET_SEPARATE_LAUNCHES) {
     net->plan.assign(nn, ConvArgs{});
     net->group_len.assign(nn, 1);
+    net->convt_fused.assign(nn, false);
     net->cl_dw.assign(nn, false);
     net->cl_pw.assign(nn, false);
     net->cl_out.assign(nn, false);
@@ -1041,6 +1082,7 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     net->fused.assign(nn, false);
   } else {
     plan_conv_groups(net);
+    plan_conv_convt(net);
     plan_cl(net);
     rc = plan_dwpw(net);
     if (rc) return bail(rc);
@@ -1094,8 +1136,8 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
                          int32_t cap, int32_t* n_launches) {
   if (!net || !n_launches) return fail(QPH_EINVAL, "net_plan: NULL argument");
   // the stepping of run_all: one launch per plain node, one per fused
-  // block / dense group / fused head (the head is two kernels) / QKV linear
-  // + attention
+  // block / dense group / conv + conv-transpose pair / fused head (the head
+  // is two kernels) / QKV linear + attention
   int32_t n = 0;
   const size_t nn = net->nodes.size();
   for (size_t i = 0; i < nn; n++) {
@@ -1104,6 +1146,7 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
     if (net->group_len[i] > 1) step = (size_t)net->group_len[i];
     else if (net->head[i]) step = 2, nk = 2;
     else if (net->fused[i]) step = net->dwpw[i].stem ? 3 : 2;
+    else if (net->convt_fused[i]) step = 2;
     else if (net->qa_fused[i]) step = 2;
     if (n < cap) {
       if (first) first[n] = (int32_t)i;

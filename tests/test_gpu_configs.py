@@ -353,6 +353,58 @@ def test_session_fusion_rules(gpu, oracle):
     sess.close()
 
 
+CONVT_CASES = [
+    # batch, c, h, w, conv activation, conv output also a graph output, fused
+    (1, 96, 40, 64, "relu", False, True),    # the det head's shape, 12 chunks of 8 channels
+    (2, 8, 13, 20, "relu", False, True),     # one chunk, odd rows, a partial 32-column tile
+    (1, 16, 9, 44, "none", False, True),     # two chunks, no activation
+    (3, 24, 6, 36, "relu", False, True),     # three chunks
+    (1, 32, 10, 12, "relu", True, False),    # the conv output is read twice: two launches
+    (2, 40, 7, 18, "relu", False, False),    # width not a multiple of 4: the plain conv path
+]
+
+
+@pytest.mark.parametrize("case", CONVT_CASES, ids=lambda c: "x".join(map(str, c[:4])) + f"-{c[4]}{c[5]}")
+def test_session_conv_convt_pair(gpu, oracle, case):
+    """The det head (3x3 conv to 24 channels, ReLU, then ConvTranspose 2x2
+    24 -> 24, ConvTranspose 2x2 24 -> 1, Sigmoid; DBHead as the det graph
+    holds it) runs as one launch when only the pair reads the conv output:
+    bit-exact against the oracle's conv, ConvT, ConvT and sigmoid, and, with
+    real_n below the batch, the oracle's bits for the real items."""
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    n, c, h, w, act, shared, fused = case
+    r = nets.WeightRng(17)
+    g = nets.Graph((n, c, h, w))
+    wc = g.weight(r.kaiming((24, c, 3, 3), 9 * c))
+    bc = g.weight(r.normal((24,), 0.1))
+    kind = nets.ACT_RELU if act == "relu" else nets.ACT_NONE
+    t = g.conv(0, wc, bc, pad=(1, 1, 1, 1), act=kind)
+    w1 = g.weight(r.kaiming((24, 24, 2, 2), 24))
+    w2 = g.weight(r.kaiming((24, 1, 2, 2), 24))
+    y = g.convt_pair_sigmoid(t, w1, w2)
+    g.outputs = [y, t] if shared else [y]
+    x = r.normal((n, c, h, w), 1.0)
+    print(f"conv + ConvT pair {case}", flush=True)
+    sess = nets.HipSession(g)
+    launches = sess.plan()
+    assert ((0, 2, 1) in launches) == fused, launches
+    got = sess.run(x)
+    ref = onets.run_graph(g, x)
+    for i, (a, b) in enumerate(zip(got, ref)):
+        assert_bitexact(a, b, f"output {i}")
+    if n > 1:
+        x1 = r.normal((1, c, h, w), 1.0)
+        got1 = sess.run(x1)[0]
+        g1 = nets.Graph((1, c, h, w))
+        for arr in g.weights:
+            g1.weight(arr)
+        t1 = g1.conv(0, wc, bc, pad=(1, 1, 1, 1), act=kind)
+        g1.outputs = [g1.convt_pair_sigmoid(t1, w1, w2)]
+        assert_bitexact(got1, onets.run_graph(g1, x1)[0], "real_n 1")
+    sess.close()
+
+
 LINEAR_CASES = [
     # rows, k, n, layernorm in front, activation, residual, LN output also an output
     (1280, 256, 768, True, "none", False, False),   # rec QKV: 4 slabs
