@@ -89,6 +89,14 @@ typedef struct {
 #define QPH_ACT_HARDSWISH 3
 #define QPH_ACT_SIGMOID 4
 #define QPH_ACT_HARDSIGMOID 5  /* HardSigmoid node alone (alpha = c1, beta = c2): the SE gate */
+/* Clip node (executor.rs:779-807, activation.rs:221-229): m = x < c1 ? c1 : x,
+ * then c2 < m ? c2 : m (lo = c1, hi = c2; NaN passes through). */
+#define QPH_ACT_CLIP 6
+/* The Add / Clip / Mul / Div export form of hardswish, each node rounding
+ * to f32 as the reference's separate nodes do (elementwise.rs:350-363 for
+ * the scalar Add and Div): t = x + c1, t = clip(t, +0.0, c2), t = x * t,
+ * y = t / c3. */
+#define QPH_ACT_HARDSWISH_CLIP 7
 typedef struct {
   int32_t kind;
   float c1, c2, c3;
@@ -319,6 +327,10 @@ QPH_API int qph_db_mask(qph_ctx* ctx, const float* pred, int64_t h, int64_t w, f
                                   output size from the tensor table; y_ctotal/y_coff (bilinear) */
 #define QPH_OP_TRANSPOSE 13    /* rank-4 permutation ws = {perm0..3} */
 #define QPH_OP_COPY_SLOT 14    /* x -> channels [y_coff, y_coff + C) of y (a Concat slot) */
+#define QPH_OP_BINARY 15       /* y = x op in2 (same element count), or with in2 = -1 the
+                                  one-element broadcast: y = x op scale (ws[1] = 0) or
+                                  y = scale op x (ws[1] = 1); ws[0] = op: 0 Add, 1 Sub,
+                                  2 Mul, 3 Div (elementwise.rs:185-298, 350-363) */
 
 typedef struct {
   int32_t op;

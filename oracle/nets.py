@@ -26,7 +26,8 @@ from . import oracle as O
 OP_CONV, OP_CONVT_PAIR_SIG, OP_LINEAR, OP_LAYERNORM, OP_ATTENTION = 1, 2, 3, 4, 5
 OP_SOFTMAX_ARGMAX, OP_CONVT, OP_ACT = 6, 7, 8
 OP_GAP, OP_MUL_ADD_SCALE, OP_POOL, OP_RESIZE, OP_TRANSPOSE, OP_COPY_SLOT = 9, 10, 11, 12, 13, 14
-ACT_HARDSIGMOID = 5
+OP_BINARY = 15
+ACT_HARDSIGMOID, ACT_CLIP, ACT_HARDSWISH_CLIP = 5, 6, 7
 
 
 def _store(T, g, d, y):
@@ -44,7 +45,15 @@ def _store(T, g, d, y):
 
 
 def _act_nodes(y, act):
-    """The activation as the reference graph applies it after a Conv / MatMul."""
+    """The activation as the reference graph applies it after a Conv / MatMul
+    (act: a kind, or (kind, c1, c2, c3) for the parameterised Clip forms)."""
+    kind, c1, c2, c3 = act if isinstance(act, tuple) else (act, 0.0, 0.0, 0.0)
+    if kind == ACT_CLIP:                                 # Clip node
+        return O.clip_inplace(y.copy(), c1, c2)
+    if kind == ACT_HARDSWISH_CLIP:                       # Add, Clip, Mul, Div nodes
+        t = O.clip_inplace(O.binary_scalar(y, c1, 0), 0.0, c2)
+        return O.binary_scalar(O.binary_flat(y, t, 2), c3, 3)
+    act = kind
     if act == O.ACT_HARDSWISH:
         hs = O.hardsigmoid(y, O.HS_ALPHA, O.HS_BETA)
         return O.binary_flat(y, hs, 2)          # Mul node
@@ -142,6 +151,13 @@ def run_graph(g, x_in, keep=False):
             T[d["out"]] = O.convtranspose2d(x.reshape(g.shapes[d["inp"]]), W[d["w"]].reshape(d["ws"]))
         elif op == OP_ACT:
             T[d["out"]] = _act_nodes(x.copy(), d["act"])
+        elif op == OP_BINARY:                            # Add / Sub / Mul / Div node
+            opc, first = int(d["ws"][0]), bool(d["ws"][1])
+            if d["in2"] >= 0:
+                y = O.binary_flat(x, T[d["in2"]], opc)
+            else:
+                y = O.binary_scalar(x, d["scale"], opc, scalar_first=first)
+            T[d["out"]] = y.reshape(g.shapes[d["out"]])
         elif op == OP_GAP:
             T[d["out"]] = O.global_avg_pool(x.reshape(g.shapes[d["inp"]]))
         elif op == OP_MUL_ADD_SCALE:

@@ -64,6 +64,7 @@ def lib():
             "qpo_resize_nearest": ([P, I64, I64, I64, I64, I64, P], None),
             "qpo_binary_flat": ([P, P, I64, I], None),
             "qpo_binary_bcast": ([P, P, I64, I64, I, I], None),
+            "qpo_binary_scalar": ([P, I64, F, I, I, P], None),
             "qpo_reduce_mean_last": ([P, I64, I64, P], None),
             "qpo_sqrt_inplace": ([P, I64], None),
             "qpo_layernorm_chain": ([P, P, P, F, I64, I64, P], None),
@@ -254,6 +255,14 @@ def binary_flat(a, b, op):
     assert a.size == b.size
     lib().qpo_binary_flat(_p(a), _p(b), a.size, op)
     return a
+
+
+def binary_scalar(x, s, op, scalar_first=False):
+    """y = x op s, or s op x (the one-element broadcast of binary_op)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().qpo_binary_scalar(_p(x), x.size, float(np.float32(s)), op, int(bool(scalar_first)), _p(y))
+    return y
 
 
 def binary_bcast(a, b, rows, cols, op, bmode):

@@ -745,6 +745,19 @@ QPO_API void qpo_binary_flat(float* a, const float* b, int64_t n, int op) {
   for (int64_t i = 0; i < n; i++) a[i] = binop(op, a[i], b[i]);
 }
 
+/* y = x op s (scalar_first 0) or s op x: binary_op's one-element fast path
+ * (elementwise.rs:350-363; binary_scalar_bcast_scalar elementwise.rs:635-650,
+ * x86.rs:1241-1278), one IEEE op an element. */
+QPO_API void qpo_binary_scalar(const float* x, int64_t n, float s, int op, int scalar_first,
+                               float* y) {
+#pragma omp parallel
+  {
+    qpo_ftz();
+#pragma omp for schedule(static)
+    for (int64_t i = 0; i < n; i++) y[i] = scalar_first ? binop(op, s, x[i]) : binop(op, x[i], s);
+  }
+}
+
 /* a[R,C] op= b broadcast: bmode 0 = b[R] per row (a [R,C] op [R,1]),
  * 1 = b[C] per column (a [R,C] op [C]), 2 = scalar b[0].  The run paths of
  * binary_op_inplace (elementwise.rs:207-298, x86.rs:895-942). */

@@ -17,6 +17,9 @@ OP_CONV, OP_CONVT_PAIR_SIG, OP_LINEAR, OP_LAYERNORM, OP_ATTENTION = 1, 2, 3, 4, 
 OP_SOFTMAX_ARGMAX, OP_CONVT, OP_ACT = 6, 7, 8
 OP_GAP, OP_MUL_ADD_SCALE, OP_POOL, OP_RESIZE, OP_TRANSPOSE, OP_COPY_SLOT = 9, 10, 11, 12, 13, 14
 ACT_HARDSIGMOID = 5
+ACT_CLIP, ACT_HARDSWISH_CLIP = 6, 7
+OP_BINARY = 15
+BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = 0, 1, 2, 3
 RUN_UPLOAD, RUN_DOWNLOAD = 1, 2
 NET_SEPARATE_LAUNCHES = 1
 NET_FUSED_HEAD = 2

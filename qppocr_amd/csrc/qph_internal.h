@@ -61,7 +61,8 @@ namespace qph {
 int ctx_workspace(qph_ctx* ctx, size_t bytes, void** out);
 
 // Activation kinds (qph_act.kind): 0 none, 1 gelu(c1,c2,c3), 2 relu,
-// 3 hardswish(alpha=c1, beta=c2), 4 sigmoid, 5 hardsigmoid(alpha=c1, beta=c2).
+// 3 hardswish(alpha=c1, beta=c2), 4 sigmoid, 5 hardsigmoid(alpha=c1, beta=c2),
+// 6 clip(lo=c1, hi=c2), 7 the Add / Clip / Mul / Div hardswish (c1, c2, c3).
 
 // exp1: qppocr-kernels/src/activation.rs:28-47 (x86.rs:28-57).
 __device__ __forceinline__ float exp1(float x) {
@@ -108,6 +109,12 @@ __device__ __forceinline__ float hsig1(float x, float alpha, float beta) {
   return v < 0.0f ? 0.0f : (v > 1.0f ? 1.0f : v);
 }
 
+// clip: activation.rs:221-229, the comparison chain (NaN passes through).
+__device__ __forceinline__ float clip1(float v, float lo, float hi) {
+  const float m = v < lo ? lo : v;
+  return hi < m ? hi : m;
+}
+
 // sigmoid: activation.rs:196-201 (true division).
 __device__ __forceinline__ float sigmoid1(float x) { return 1.0f / (1.0f + exp1(-x)); }
 
@@ -128,6 +135,11 @@ __device__ __forceinline__ float act_apply(float v, const Act& a) {
     case 3: return v * hsig1(v, a.c1, a.c2);  // HardSigmoid node then Mul node
     case 4: return sigmoid1(v);
     case 5: return hsig1(v, a.c1, a.c2);      // HardSigmoid node alone (the SE gate)
+    case 6: return clip1(v, a.c1, a.c2);      // Clip node
+    case 7: {                                 // Add(c1), Clip(0, c2), Mul(x), Div(c3) nodes
+      const float t = clip1(v + a.c1, 0.0f, a.c2);
+      return (v * t) / a.c3;
+    }
     default: return v;
   }
 }
@@ -143,7 +155,7 @@ inline Act make_act(const qph_act* a) {
   return r;
 }
 
-inline bool act_valid(const qph_act* a) { return !a || (a->kind >= 0 && a->kind <= 5); }
+inline bool act_valid(const qph_act* a) { return !a || (a->kind >= 0 && a->kind <= 7); }
 
 // The conv the reference runs as a plain GEMM over X[C][H*W] (conv.rs:264):
 // 1x1, stride 1, one group; padding excluded (X is then not that matrix).
@@ -337,6 +349,10 @@ int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, 
 int launch_attention_generic(const float* qkv, int64_t batch, int64_t t, int64_t heads,
                              int64_t dh, float scale, float* out, hipStream_t s);
 int launch_elementwise_act(const float* x, float* y, int64_t n, const Act& a, hipStream_t s);
+// y = x op b (mode 0, same element count), x op sv (mode 1) or sv op x
+// (mode 2); op 0 add, 1 sub, 2 mul, 3 div
+int launch_binary_out(const float* x, const float* b, float sv, float* y, int64_t n, int op,
+                      int mode, hipStream_t s);
 int launch_resize_nearest(const float* x, int64_t nc, int64_t h, int64_t w, int64_t oh,
                           int64_t ow, float* y, hipStream_t s);
 int launch_binary(float* a, const float* b, int64_t rows, int64_t cols, int op, int bmode,

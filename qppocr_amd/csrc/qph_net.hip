@@ -26,6 +26,7 @@ struct qph_net {
   std::vector<ConvArgs> plan;    // per node: launch arguments of a dense 3x3 conv
   std::vector<int> group_len;    // > 1: first of that many independent 3x3 convs, one launch
   std::vector<bool> convt_fused; // 3x3 conv node i and its conv-transpose pair i + 1, one launch
+  std::vector<int> absorb_after; // nodes after node i done in its launch's epilogue (0 or 4)
   std::vector<DwPwArgs> dwpw;    // per node: fused depthwise + pointwise launch
   std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1, and i + 2 for a stem, with it)
   std::vector<float*> wt;        // per linear node: resident transposed weight Wt[N][K] (or NULL)
@@ -211,6 +212,10 @@ static int run_node(qph_net* net, size_t i) {
     }
     case QPH_OP_COPY_SLOT:
       return launch_copy_slot(x, y, xs[1], xs[2] * xs[3], xs[0] * xs[1], n.y_ctotal, n.y_coff, s);
+    case QPH_OP_BINARY:
+      return launch_binary_out(x, n.in2 >= 0 ? net->tptr[n.in2] : nullptr, n.scale, y,
+                               numel_of(net, n.in), (int)n.ws[0],
+                               n.in2 >= 0 ? 0 : (n.ws[1] ? 2 : 1), s);
     default:
       return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unknown op");
   }
@@ -329,6 +334,64 @@ static void plan_pitch(qph_net* net) {
     for (const qph_node& r : net->nodes)
       soft = soft || (r.in == t && r.op == QPH_OP_SOFTMAX_ARGMAX && r.ws[0] == nn);
     if (soft) net->pitch[(size_t)t] = (nn + 31) / 32 * 32;
+  }
+}
+
+// The Add / Clip / Mul / Div export form of hardswish after a conv or
+// linear with no activation, residual or placed output:
+//   X = P(...); T1 = X + a; T2 = Clip(T1, +0.0, hi); T3 = X * T2; Y = T3 / d
+// as the five consecutive nodes i .. i + 4, with X, T1, T2 and T3 read only
+// inside the chain: node i then writes Y with activation kind 7 (the same
+// four roundings in its epilogue) and the four nodes after it launch
+// nothing.  Rewrites node i before the other planners see it.
+static void plan_hardswish_clip(qph_net* net) {
+  const size_t nn = net->nodes.size(), nt = net->tptr.size();
+  net->absorb_after.assign(nn, 0);
+  std::vector<int> readers(nt, 0);
+  std::vector<bool> aliased(nt, false);
+  for (const qph_node& n : net->nodes)
+    for (int32_t t : {n.in, n.in2, n.in3})
+      if (t >= 0) readers[(size_t)t]++;
+  for (int32_t o : net->outputs) readers[(size_t)o] += 1000;
+  for (size_t t = 0; t < nt; t++)
+    if (net->alias[t] >= 0) aliased[t] = aliased[(size_t)net->alias[t]] = true;
+  auto plain = [&](int32_t t) { return t >= 0 && !aliased[(size_t)t]; };
+  for (size_t i = 0; i + 4 < nn; i++) {
+    qph_node& p = net->nodes[i];
+    const qph_node& a = net->nodes[i + 1];
+    const qph_node& c = net->nodes[i + 2];
+    const qph_node& m = net->nodes[i + 3];
+    const qph_node& d = net->nodes[i + 4];
+    if ((p.op != QPH_OP_CONV && p.op != QPH_OP_LINEAR) || p.act.kind != QPH_ACT_NONE ||
+        p.in2 >= 0 || p.y_ctotal || p.y_coff || (p.y_up && p.y_up != 1) || p.trans_out ||
+        net->head[i] || net->qa_fused[i])
+      continue;
+    const int32_t x = p.out;
+    if (a.op != QPH_OP_BINARY || a.ws[0] != 0 || a.in != x || a.in2 >= 0) continue;
+    if (c.op != QPH_OP_ACT || c.act.kind != QPH_ACT_CLIP || c.in != a.out ||
+        __builtin_bit_cast(uint32_t, c.act.c1) != 0u)
+      continue;
+    if (m.op != QPH_OP_BINARY || m.ws[0] != 2 || m.in2 < 0 ||
+        !((m.in == x && m.in2 == c.out) || (m.in == c.out && m.in2 == x)))
+      continue;
+    if (d.op != QPH_OP_BINARY || d.ws[0] != 3 || d.in != m.out || d.in2 >= 0 || d.ws[1] != 0)
+      continue;
+    const int32_t y = d.out;
+    if (!plain(x) || !plain(a.out) || !plain(c.out) || !plain(m.out) || !plain(y) ||
+        readers[(size_t)x] != 2 || readers[(size_t)a.out] != 1 || readers[(size_t)c.out] != 1 ||
+        readers[(size_t)m.out] != 1)
+      continue;
+    bool same = true;
+    for (int k = 0; k < 4; k++)
+      same = same && net->shapes[4 * (size_t)x + k] == net->shapes[4 * (size_t)y + k];
+    if (!same) continue;
+    p.act.kind = QPH_ACT_HARDSWISH_CLIP;
+    p.act.c1 = a.scale;
+    p.act.c2 = c.act.c2;
+    p.act.c3 = d.scale;
+    p.out = y;
+    net->absorb_after[i] = 4;
+    i += 4;
   }
 }
 
@@ -753,6 +816,19 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
       if (!n.y_ctotal) return fail(QPH_EINVAL, node_name(i, n) + ": copy slot needs y_ctotal");
       QPH_TRY(check_slot(net, i, n, xs[0], xs[1], xs[2], xs[3]));
       return QPH_OK;
+    case QPH_OP_BINARY:
+      // Pow (op 4) goes through libm powf on the reference's CPU path
+      // (elementwise.rs:32-34), with ulp-level differences across libms
+      if (n.ws[0] < 0 || n.ws[0] > 3)
+        return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": binary op must be Add, Sub, Mul or Div");
+      if (n.ws[1] != 0 && n.ws[1] != 1)
+        return fail(QPH_EINVAL, node_name(i, n) + ": ws[1] (scalar first) must be 0 or 1");
+      if ((n.in2 >= 0 && numel_of(net, n.in2) != numel_of(net, n.in)) ||
+          numel_of(net, n.out) != numel_of(net, n.in))
+        return fail(QPH_EINVAL, node_name(i, n) + ": binary operands and output differ in size");
+      if (n.y_ctotal || n.y_coff)
+        return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": binary op into a Concat slot");
+      return QPH_OK;
     default:
       return fail(QPH_EUNSUPPORTED, node_name(i, n) + ": unsupported op");
   }
@@ -814,6 +890,7 @@ static int run_all(qph_net* net) {
       const int rc = run_node(net, i);
       if (rc != QPH_OK) return fail(rc, node_name(i, net->nodes[i]) + ": " + qph_last_error());
     }
+    step += (size_t)net->absorb_after[i + step - 1];
     if (net->profiling)
       for (size_t k = i + 1; k < i + step; k++) QPH_TRY_HIP(hipEventRecord(net->ev[k], s));
     i += step;
@@ -1075,12 +1152,14 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     net->plan.assign(nn, ConvArgs{});
     net->group_len.assign(nn, 1);
     net->convt_fused.assign(nn, false);
+    net->absorb_after.assign(nn, 0);
     net->cl_dw.assign(nn, false);
     net->cl_pw.assign(nn, false);
     net->cl_out.assign(nn, false);
     net->dwpw.assign(nn, DwPwArgs{});
     net->fused.assign(nn, false);
   } else {
+    plan_hardswish_clip(net);
     plan_conv_groups(net);
     plan_conv_convt(net);
     plan_cl(net);
@@ -1137,7 +1216,8 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
   if (!net || !n_launches) return fail(QPH_EINVAL, "net_plan: NULL argument");
   // the stepping of run_all: one launch per plain node, one per fused
   // block / dense group / conv + conv-transpose pair / fused head (the head
-  // is two kernels) / QKV linear + attention
+  // is two kernels) / QKV linear + attention, each also covering the
+  // elementwise nodes folded into its epilogue
   int32_t n = 0;
   const size_t nn = net->nodes.size();
   for (size_t i = 0; i < nn; n++) {
@@ -1148,6 +1228,7 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
     else if (net->fused[i]) step = net->dwpw[i].stem ? 3 : 2;
     else if (net->convt_fused[i]) step = 2;
     else if (net->qa_fused[i]) step = 2;
+    step += (size_t)net->absorb_after[i + step - 1];
     if (n < cap) {
       if (first) first[n] = (int32_t)i;
       if (nodes) nodes[n] = (int32_t)step;

@@ -1448,6 +1448,79 @@ int launch_binary(float* a, const float* b, int64_t rows, int64_t cols, int op, 
   return launch_check("binary_kernel");
 }
 
+// y = x op b element for element (mode 0), x op scalar (mode 1) or scalar
+// op x (mode 2): binary_op's same-shape pass and its one-element fast path
+// (elementwise.rs:185-298, 350-363; x86.rs:1241-1278), one IEEE op each.
+// Four elements a thread by 16-byte accesses when every pointer allows.
+template <int OP, int MODE, bool V4>
+__global__ __launch_bounds__(256) void binary_out_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ b, float sv,
+                                                         float* __restrict__ y, int64_t n) {
+  auto op = [&](float a, float c) {
+    if constexpr (OP == 0) return a + c;
+    else if constexpr (OP == 1) return a - c;
+    else if constexpr (OP == 2) return a * c;
+    else return a / c;
+  };
+  auto one = [&](float xv, float bv) {
+    if constexpr (MODE == 0) return op(xv, bv);
+    else if constexpr (MODE == 1) return op(xv, sv);
+    else return op(sv, xv);
+  };
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if constexpr (V4) {
+    for (; 4 * i < n; i += stride) {
+      const f32x4 xv = *(const f32x4*)(x + 4 * i);
+      f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (MODE == 0) bv = *(const f32x4*)(b + 4 * i);
+      f32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; q++) o[q] = one(xv[q], bv[q]);
+      *(f32x4*)(y + 4 * i) = o;
+    }
+  } else {
+    for (; i < n; i += stride) y[i] = one(x[i], MODE == 0 ? b[i] : 0.0f);
+  }
+}
+
+template <int OP, int MODE>
+static void launch_binary_out_t(const float* x, const float* b, float sv, float* y, int64_t n,
+                                bool v4, hipStream_t s) {
+  const int64_t items = v4 ? n / 4 : n;
+  const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>((items + 255) / 256, 16384));
+  if (v4)
+    hipLaunchKernelGGL((binary_out_kernel<OP, MODE, true>), dim3(blocks), dim3(256), 0, s, x, b,
+                       sv, y, n);
+  else
+    hipLaunchKernelGGL((binary_out_kernel<OP, MODE, false>), dim3(blocks), dim3(256), 0, s, x, b,
+                       sv, y, n);
+}
+
+template <int OP>
+static void launch_binary_out_m(const float* x, const float* b, float sv, float* y, int64_t n,
+                                int mode, bool v4, hipStream_t s) {
+  if (mode == 0) launch_binary_out_t<OP, 0>(x, b, sv, y, n, v4, s);
+  else if (mode == 1) launch_binary_out_t<OP, 1>(x, b, sv, y, n, v4, s);
+  else launch_binary_out_t<OP, 2>(x, b, sv, y, n, v4, s);
+}
+
+int launch_binary_out(const float* x, const float* b, float sv, float* y, int64_t n, int op,
+                      int mode, hipStream_t s) {
+  if (op < 0 || op > 3 || mode < 0 || mode > 2 || (mode == 0 && !b))
+    return fail(QPH_EINVAL, "binary: op 0..3 and mode 0..2 (mode 0 needs b)");
+  if (n <= 0) return QPH_OK;
+  auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  const bool v4 = n % 4 == 0 && al(x) && al(y) && (mode != 0 || al(b));
+  switch (op) {
+    case 0: launch_binary_out_m<0>(x, b, sv, y, n, mode, v4, s); break;
+    case 1: launch_binary_out_m<1>(x, b, sv, y, n, mode, v4, s); break;
+    case 2: launch_binary_out_m<2>(x, b, sv, y, n, mode, v4, s); break;
+    default: launch_binary_out_m<3>(x, b, sv, y, n, mode, v4, s); break;
+  }
+  return launch_check("binary_out_kernel");
+}
+
 // reduce_mean over the last axis (shape.rs:510-560): f64 sum, / cols, to f32.
 // Row r's element j is x[(r / rpg) * gstride + (r % rpg) * rstride + j * estride]
 // (contiguous rows: rpg = rows, rstride = cols, estride = 1); its mean goes

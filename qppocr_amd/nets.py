@@ -33,10 +33,12 @@ import math
 import numpy as np
 
 from . import _lib
-from ._lib import (ACT_GELU, ACT_HARDSIGMOID, ACT_HARDSWISH, ACT_NONE, ACT_RELU, NET_FUSED_HEAD,
+from ._lib import (ACT_CLIP, ACT_GELU, ACT_HARDSIGMOID, ACT_HARDSWISH, ACT_HARDSWISH_CLIP,
+                   ACT_NONE, ACT_RELU, BIN_ADD, BIN_DIV, BIN_MUL, NET_FUSED_HEAD,
                    NET_SEPARATE_LAUNCHES, Act,
                    ConvParams, Node, NetSpec,
-                   OP_ACT, OP_ATTENTION, OP_CONV, OP_CONVT, OP_CONVT_PAIR_SIG, OP_COPY_SLOT,
+                   OP_ACT, OP_ATTENTION, OP_BINARY, OP_CONV, OP_CONVT, OP_CONVT_PAIR_SIG,
+                   OP_COPY_SLOT,
                    OP_GAP, OP_LAYERNORM, OP_LINEAR, OP_MUL_ADD_SCALE, OP_POOL, OP_RESIZE,
                    OP_SOFTMAX_ARGMAX, OP_TRANSPOSE, check)
 
@@ -48,6 +50,8 @@ LN_EPS = 1e-6
 
 
 def _act(kind):
+    if isinstance(kind, tuple):          # (kind, c1, c2, c3): the Clip forms
+        return Act(*kind)
     if kind in (ACT_HARDSWISH, ACT_HARDSIGMOID):
         return Act(kind, *HS)
     if kind == ACT_GELU:
@@ -164,6 +168,26 @@ class Graph:
         d.update(kw)
         self.nodes.append(d)
         return out
+
+    def act(self, x, act):
+        """A standalone activation node (act: a kind or (kind, c1, c2, c3))."""
+        return self._node(OP_ACT, x, self.tensor(self.lshapes[x]), act=act)
+
+    def clip(self, x, lo, hi):
+        """Clip node (executor.rs:779-807): lo / hi as the node's min / max."""
+        return self.act(x, (ACT_CLIP, float(lo), float(hi), 0.0))
+
+    def binary(self, x, op, other=-1, scalar=0.0, scalar_first=False):
+        """Add / Sub / Mul / Div node: x op other (same element count), or with
+        other = -1 the one-element broadcast x op scalar (scalar op x when
+        scalar_first)."""
+        return self._node(OP_BINARY, x, self.tensor(self.lshapes[x]), in2=other,
+                          ws=(int(op), int(bool(scalar_first)), 0, 0), scale=float(scalar))
+
+    def hardswish_clip(self, x):
+        """The Add(3) / Clip(0, 6) / Mul / Div(6) export form of hardswish."""
+        t = self.clip(self.binary(x, BIN_ADD, scalar=3.0), 0.0, 6.0)
+        return self.binary(self.binary(x, BIN_MUL, other=t), BIN_DIV, scalar=6.0)
 
     def global_avg_pool(self, x):
         """GlobalAveragePool [N, C, H, W] -> [N, C, 1, 1] (pool2d.rs:10-29)."""

@@ -110,6 +110,42 @@ def test_activations_vs_f64(oracle):
     assert (cl.view(np.uint32) == want.view(np.uint32)).all()
 
 
+def test_binary_scalar_both_orders(oracle):
+    """The one-element broadcast of binary_op (elementwise.rs:350-363): each
+    op is the IEEE single op with the scalar on the side asked for (a
+    swapped Sub or Div operand fails), as numpy's float32 ops give it."""
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 2, 4099).astype(np.float32)
+    x[::9] = 0.0
+    s = np.float32(-1.375)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        for op, f in enumerate((np.add, np.subtract, np.multiply, np.divide)):
+            for first in (False, True):
+                got = oracle.binary_scalar(x, s, op, scalar_first=first)
+                want = f(s, x) if first else f(x, s)
+                assert want.dtype == np.float32
+                assert (got.view(np.uint32) == want.view(np.uint32)).all(), (op, first)
+    assert not (oracle.binary_scalar(x, s, 1, True) == oracle.binary_scalar(x, s, 1, False)).all()
+
+
+def test_hardswish_clip_chain_order(oracle):
+    """The oracle executor runs the Add(3) / Clip(0, 6) / Mul / Div(6) form as
+    four nodes, each rounding to f32: (x * clip(x + 3)) / 6, which differs
+    from x * (clip(x + 3) / 6) and from the HardSigmoid + Mul form on some
+    inputs, so the order of the roundings is what is checked."""
+    from oracle import nets as onets
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 3, 20000).astype(np.float32)
+    y = onets._act_nodes(x.copy(), (onets.ACT_HARDSWISH_CLIP, 3.0, 6.0, 6.0))
+    t = np.minimum(np.maximum(x + np.float32(3), np.float32(0)), np.float32(6))
+    want = (x * t) / np.float32(6)
+    assert (y == want).all()
+    other = x * (t / np.float32(6))
+    assert (y != other).any()
+    hs = onets._act_nodes(x.copy(), oracle.ACT_HARDSWISH)
+    assert (y != hs).any()
+
+
 def test_softmax_invariants(oracle):
     tol = GOLD["activation_tolerances"]
     rng = XorShift(int(GOLD["rng"]["kernels_seed"], 16))
