@@ -321,7 +321,8 @@ QPH_API int qph_db_mask(qph_ctx* ctx, const float* pred, int64_t h, int64_t w, f
 #define QPH_OP_CONVT 7         /* x -> y; w [Ci, Co, 2, 2] */
 #define QPH_OP_ACT 8           /* x -> y; act */
 #define QPH_OP_GAP 9           /* GlobalAveragePool: x [N,C,H,W] -> y [N,C,1,1] */
-#define QPH_OP_MUL_ADD_SCALE 10 /* y = in * in3 (gate [C] or [N,C]) + in2; y_ctotal/y_coff */
+#define QPH_OP_MUL_ADD_SCALE 10 /* y = in * in3 (gate [C] or [N,C]) + in2 (in2 = -1: the
+                                  gate Mul alone); y_ctotal/y_coff */
 #define QPH_OP_POOL 11         /* ws = {max?, 0, kh, kw}; cp strides and pads; y_ctotal/y_coff */
 #define QPH_OP_RESIZE 12       /* ws = {mode 0 nearest | 1 bilinear, align_corners, 0, 0};
                                   output size from the tensor table; y_ctotal/y_coff (bilinear) */

@@ -164,6 +164,11 @@ def run_graph(g, x_in, keep=False):
             n, c, h, w = g.shapes[d["inp"]]
             gate = T[d["in3"]].reshape(-1)
             f = x.reshape(n, c, h, w)
+            if d["in2"] < 0:            # the gate Mul node alone (no residual)
+                gb = np.tile(gate, n) if gate.size == c else gate
+                y = O.binary_bcast(f.reshape(n * c, h * w), gb, n * c, h * w, 2, 0)
+                _store(T, g, d, y.reshape(n, c, h, w))
+                continue
             r = T[d["in2"]].reshape(n, c, h, w)
             if gate.size == c:
                 y = O.mul_add_scale(f, gate, r)

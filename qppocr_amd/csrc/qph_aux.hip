@@ -23,7 +23,9 @@ __device__ __forceinline__ int64_t out_plane(int64_t p, int64_t c, int64_t ctot,
 // mul_add_scale (qppocr-kernels/src/elementwise.rs:134-179):
 // out = f * gate[plane % gmod] + r, the Mul and the Add each rounded; gmod =
 // c for a per-channel gate, n * c for one gate per batch item and channel
-// (the reference's Mul-then-Add fallback, the same two roundings).
+// (the reference's Mul-then-Add fallback, the same two roundings).  With r
+// NULL, out = f * gate alone: the gate Mul of an SE block without a
+// residual (binary_op's inner-run path, elementwise.rs:366-420).
 __global__ __launch_bounds__(256) void mul_add_scale_kernel(const float* __restrict__ f,
                                                             const float* __restrict__ gate,
                                                             const float* __restrict__ r,
@@ -37,20 +39,20 @@ __global__ __launch_bounds__(256) void mul_add_scale_kernel(const float* __restr
   for (int64_t p = blockIdx.y; p < planes; p += gridDim.y) {
     const float g = gate[p % gmod];
     const float* fp = f + p * hw;
-    const float* rp = r + p * hw;
+    const float* rp = r ? r + p * hw : nullptr;
     float* op = out + out_plane(p, c, ctot, coff) * hw;
     float fv[4], rv[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int64_t e = e0 + u * 256;
       fv[u] = e < hw ? fp[e] : 0.0f;
-      rv[u] = e < hw ? rp[e] : 0.0f;
+      rv[u] = (r && e < hw) ? rp[e] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int64_t e = e0 + u * 256;
       const float v = fv[u] * g;
-      if (e < hw) op[e] = v + rv[u];
+      if (e < hw) op[e] = r ? v + rv[u] : v;
     }
   }
 }

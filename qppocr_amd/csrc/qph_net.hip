@@ -777,9 +777,10 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
       return QPH_OK;
     case QPH_OP_MUL_ADD_SCALE: {
       QPH_TRY(check_tensor(net, n.in3, false, i, n, "gate"));
-      if (n.in2 < 0) return fail(QPH_EINVAL, node_name(i, n) + ": MulAddScale without residual");
+      // in2 = -1: the gate Mul alone (an SE block without a residual)
       const int64_t g = numel_of(net, n.in3);
-      if (numel_of(net, n.in2) != numel_of(net, n.in) || (g != xs[1] && g != xs[0] * xs[1]))
+      if ((n.in2 >= 0 && numel_of(net, n.in2) != numel_of(net, n.in)) ||
+          (g != xs[1] && g != xs[0] * xs[1]))
         return fail(QPH_EINVAL, node_name(i, n) + ": MulAddScale shapes");
       QPH_TRY(check_slot(net, i, n, xs[0], xs[1], xs[2], xs[3]));
       return QPH_OK;

@@ -195,8 +195,9 @@ class Graph:
         return self._node(OP_GAP, x, self.tensor((n, c, 1, 1)))
 
     def mul_add_scale(self, feature, gate, residual, out=None, y_ctotal=0, y_coff=0):
-        """MulAddScale (optimize.rs:429-497): feature * gate + residual; out /
-        y_ctotal / y_coff place it in a Concat slot."""
+        """MulAddScale (optimize.rs:429-497): feature * gate + residual (residual
+        -1: the gate Mul alone); out / y_ctotal / y_coff place it in a Concat
+        slot."""
         n, c, h, w = self.shapes[feature]
         out = self.tensor((n, c, h, w)) if out is None else out
         return self._node(OP_MUL_ADD_SCALE, feature, out, in2=residual, in3=gate,
@@ -419,6 +420,76 @@ def build_rec(seed=3, batch=32, w=320, h=48, probs=True, fused_head=False):
     x_in, r = rec_input(seed, batch, h, w)
     g = build_rec_graph(rec_weights(r), batch, w, h, probs, fused_head)
     return g, x_in
+
+
+# ------------------------------------------------------------------- cls
+
+CLS_H, CLS_W = 48, 192   # the cls canvas (PipelineConfig cls_height / cls_width, config.rs:156)
+CLS_BLOCKS = [  # (dw kernel, stride, cin, cout, SE gate on the depthwise output)
+    (3, 1, 16, 32, False), (3, 2, 32, 64, False), (3, 1, 64, 64, False),
+    (3, 2, 64, 128, False), (3, 1, 128, 128, False), (5, 2, 128, 256, True),
+    (5, 1, 256, 256, True),
+]
+CLS_LAST = 1280          # the 1x1 conv after the last GlobalAveragePool
+CLS_CLASSES = 2          # 0 and 180 degrees
+
+
+def cls_input(seed, batch=32, h=CLS_H, w=CLS_W):
+    r = WeightRng(seed)
+    x = r.uniform((batch, 3, h, w), -1.0, 1.0)
+    return x, r
+
+
+def cls_weights(r):
+    """All cls weights in graph order (shape-independent of the batch)."""
+    ws = [r.kaiming((16, 3, 3, 3), 27), r.normal((16,), 0.1)]
+    for k, _, cin, cout, se in CLS_BLOCKS:
+        ws += [r.kaiming((cin, 1, k, k), k * k), r.normal((cin,), 0.1)]
+        if se:
+            ws += [r.kaiming((cin // 4, cin, 1, 1), cin), r.normal((cin // 4,), 0.1),
+                   r.kaiming((cin, cin // 4, 1, 1), cin // 4), r.normal((cin,), 0.1)]
+        ws += [r.kaiming((cout, cin, 1, 1), cin), r.normal((cout,), 0.1)]
+    c = CLS_BLOCKS[-1][3]
+    ws += [r.kaiming((CLS_LAST, c, 1, 1), c), r.normal((CLS_LAST,), 0.1),
+           r.kaiming((CLS_LAST, CLS_CLASSES), CLS_LAST), r.normal((CLS_CLASSES,), 0.1)]
+    return ws
+
+
+def build_cls_graph(weights, batch, h=CLS_H, w=CLS_W):
+    """Text-line orientation classifier (the engine's cls stage,
+    qppocr-core/src/pipeline/engine.rs:1294-1380) on [batch, 3, h, w]: a
+    PP-LCNet-style backbone (stem conv 3x3 s2 + hardswish; depthwise +
+    pointwise blocks, the last two with an SE gate on the depthwise output:
+    GlobalAveragePool, 1x1 + ReLU, 1x1 + HardSigmoid, Mul), then
+    GlobalAveragePool, a 1x1 conv to 1280 + hardswish, the linear to 2
+    classes and the row softmax: [batch, 2] probabilities."""
+    it = iter(weights)
+    g = Graph((batch, 3, h, w))
+    nw = lambda: g.weight(next(it))  # noqa: E731
+    ws, bs = nw(), nw()
+    x = g.conv(0, ws, bs, stride=(2, 2), pad=(1, 1, 1, 1), act=ACT_HARDSWISH)
+    for k, s, cin, cout, se in CLS_BLOCKS:
+        wd, bd = nw(), nw()
+        x = g.conv(x, wd, bd, stride=(s, s), pad=(k // 2,) * 4, group=cin, act=ACT_HARDSWISH)
+        if se:
+            w1, b1, w2, b2 = nw(), nw(), nw(), nw()
+            gp = g.global_avg_pool(x)
+            gate = g.conv(g.conv(gp, w1, b1, act=ACT_RELU), w2, b2, act=ACT_HARDSIGMOID)
+            x = g.mul_add_scale(x, gate, -1)
+        wp, bp = nw(), nw()
+        x = g.conv(x, wp, bp, act=ACT_HARDSWISH)
+    wl, bl = nw(), nw()
+    x = g.conv(g.global_avg_pool(x), wl, bl, act=ACT_HARDSWISH)
+    wf, bf = nw(), nw()
+    logits = g.linear(x, wf, bf)
+    probs, _ = g.softmax_argmax(logits, CLS_CLASSES)
+    g.outputs = [probs]
+    return g
+
+
+def build_cls(seed=5, batch=32, h=CLS_H, w=CLS_W):
+    x_in, r = cls_input(seed, batch, h, w)
+    return build_cls_graph(cls_weights(r), batch, h, w), x_in
 
 
 def node_cost(g, d):

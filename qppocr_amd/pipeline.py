@@ -23,6 +23,26 @@ BUCKET = 160
 MAX_BATCH = 64
 
 
+CLS_THRESH = 0.9       # PipelineConfig cls_thresh (config.rs:158)
+CLS_PER_DEVICE = 32    # lines per cls forward on a device session (engine.rs:1313-1319)
+
+
+def cls_batches(n_lines, per=CLS_PER_DEVICE):
+    """The cls stage's batches (engine.rs:1321-1324): consecutive runs of at
+    most `per` lines, not padded (a shorter last batch runs at its own size;
+    on a HipSession of `per` items that is real_n = its size)."""
+    return [(b, min(b + per, n_lines)) for b in range(0, n_lines, per)]
+
+
+def cls_decisions(probs, thresh=CLS_THRESH):
+    """Per line (engine.rs:1375-1380): flip the crop by 180 degrees when
+    p1 > p0 and p1 >= thresh; the line's confidence is max(p0, p1).
+    probs: [n, 2] float32.  Returns (flip bool [n], confidence float32 [n])."""
+    p = np.asarray(probs, dtype=np.float32).reshape(-1, 2)
+    p0, p1 = p[:, 0], p[:, 1]
+    return (p1 > p0) & (p1 >= np.float32(thresh)), np.maximum(p0, p1)
+
+
 def ctc_decode_pairs(pairs, t_len):
     """Greedy CTC collapse of (val, idx-bits) pairs over the first t_len
     steps (qppocr-core/src/pipeline/rec.rs:82-115): a step emits its index

@@ -83,6 +83,30 @@ def test_cfg4_rec_net(gpu, oracle):
     sess.close()
 
 
+def test_cls_net(gpu, oracle):
+    """The cls stage's net (engine.rs:1294-1380) over a 42-line page in the
+    stage's batches of 32 (cls_batches): the second batch of 10 lines runs on
+    the same 32-item session through real_n.  Probabilities bit-exact against
+    the oracle's run of a net of the batch's own size, and the same flip
+    decisions (cls_decisions)."""
+    from qppocr_amd import nets, pipeline
+    from oracle import nets as onets
+    r = nets.WeightRng(5)
+    cw = nets.cls_weights(r)
+    x42 = r.uniform((42, 3, nets.CLS_H, nets.CLS_W), -1.0, 1.0)
+    print("cls 32x3x48x192 net, lines 0..32 then real_n 10", flush=True)
+    sess = nets.HipSession(nets.build_cls_graph(cw, 32))
+    for b, e in pipeline.cls_batches(42):
+        (probs,) = sess.run(x42[b:e])
+        (ref,) = onets.run_graph(nets.build_cls_graph(cw, e - b), x42[b:e])
+        assert probs.shape == ref.shape
+        assert_bitexact(probs, ref, f"cls probabilities, lines {b}..{e}")
+        flip, conf = pipeline.cls_decisions(probs)
+        flip_r, conf_r = pipeline.cls_decisions(ref)
+        assert (flip == flip_r).all() and (conf == conf_r).all()
+    sess.close()
+
+
 def test_rec_pairs_only_and_deferred_runs(gpu, oracle):
     """The rec graph with the pairs-only head (rec_argmax_pairs,
     device.rs:160-165) gives the same pairs as the full graph and the

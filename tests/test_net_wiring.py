@@ -1,4 +1,4 @@
-"""The det and rec graphs' wiring, pinned independently of qppocr_amd/nets.py.
+"""The det, rec and cls graphs' wiring, pinned independently of qppocr_amd/nets.py.
 
 The GPU sessions and the CPU oracle both consume the node list nets.py
 builds, so a wiring mistake there (FPN order, a residual source, pre-LN
@@ -6,7 +6,9 @@ placement, the QKV head split) would pass every parity test.  Here a plain
 torch float64 forward of each architecture, written from the workload
 description alone (det: stem, 11 dw+pw blocks, FPN with 1x1 laterals, nearest
 2x top-down adds, 3x3 smoothing, upsample + concat, DB head; rec: stem, 4
-dw+pw blocks, two pre-LN encoder blocks, head + softmax), consumes the weight
+dw+pw blocks, two pre-LN encoder blocks, head + softmax; cls: stem, 7 dw+pw
+blocks with SE gates in the last two, pooled 1280 conv, 2-way linear +
+softmax), consumes the weight
 list in its documented creation order and must agree with the oracle running
 nets.py's graph.  Variants of the f64 forward with one plausible wiring
 mistake each must disagree, so the comparison can see such mistakes.
@@ -127,6 +129,36 @@ def rec_f64(weights, x, heads=8, dh=32, mistake=None):
     return logits, torch.softmax(logits, -1)
 
 
+CLS_BLOCKS = [(3, 1, 16, 32, False), (3, 2, 32, 64, False), (3, 1, 64, 64, False),
+              (3, 2, 64, 128, False), (3, 1, 128, 128, False), (5, 2, 128, 256, True),
+              (5, 1, 256, 256, True)]
+
+
+def cls_f64(weights, x, mistake=None):
+    """Cls forward: stem conv3x3 s2 3->16 + hardswish; blocks of dw(k, s, pad
+    k/2) + hardswish, then (the last two) an SE gate on the dw output (global
+    mean, 1x1 C->C/4 + ReLU, 1x1 C/4->C + hardsigmoid(x/6 + 1/2), multiply),
+    then 1x1 + hardswish; global mean, 1x1 -> 1280 + hardswish, linear
+    1280 -> 2, softmax.  Returns (logits, probs)."""
+    it = iter(weights)
+    w = lambda: next(it)  # noqa: E731
+    h = _hswish(_conv(_t(x), w(), w(), 2, (1, 1, 1, 1)))
+    for k, s, cin, _, se in CLS_BLOCKS:
+        inp = h
+        h = _hswish(_conv(h, w(), w(), s, (k // 2,) * 4, groups=cin))
+        if se:
+            src = inp if mistake == "se_on_input" else h
+            gp = src.mean((2, 3), keepdim=True)
+            gt = torch.relu(_conv(gp, w(), w()))
+            gt = torch.clamp(_conv(gt, w(), w()) * HS_ALPHA + HS_BETA, 0.0, 1.0)
+            h = h * gt
+        h = _hswish(_conv(h, w(), w()))
+    last = _conv(h.mean((2, 3), keepdim=True), w(), w())
+    last = last if mistake == "head_no_act" else _hswish(last)
+    logits = last.reshape(last.shape[0], -1) @ _t(w()) + _t(w())
+    return logits, torch.softmax(logits, -1)
+
+
 def _close(got, ref, rel):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
@@ -178,3 +210,29 @@ def test_rec_f64_forward_sees_wiring_mistakes(rec_case, mistake):
     g, x, logits, _ = rec_case
     wrong, _ = rec_f64(g.weights, x, mistake=mistake)
     assert not _close(logits.reshape(wrong.shape), wrong.numpy(), 1e-3)
+
+
+@pytest.fixture(scope="module")
+def cls_case(oracle):
+    from qppocr_amd import nets
+    from oracle import nets as onets
+    g, x = nets.build_cls(5, 3)
+    outs, T = onets.run_graph(g, x, keep=True)
+    return g, x, T[g.nodes[-2]["out"]], outs[0]
+
+
+def test_cls_graph_matches_independent_f64_forward(cls_case):
+    g, x, logits, probs = cls_case
+    ref_logits, ref_probs = cls_f64(g.weights, x)
+    assert logits.reshape(ref_logits.shape).shape == (3, 2)
+    assert _close(logits.reshape(ref_logits.shape), ref_logits.numpy(), 1e-5)
+    assert np.abs(probs.reshape(ref_probs.shape) - ref_probs.numpy()).max() < 1e-5
+
+
+@pytest.mark.parametrize("mistake", ["se_on_input", "head_no_act"])
+def test_cls_f64_forward_sees_wiring_mistakes(cls_case, mistake):
+    g, x, logits, _ = cls_case
+    wrong, _ = cls_f64(g.weights, x, mistake=mistake)
+    # the net's two logits move little with its input (a global mean ends the
+    # backbone); the correct wiring agrees to ~1e-7, the SE mistake is ~5e-4 off
+    assert not _close(logits.reshape(wrong.shape), wrong.numpy(), 1e-4)

@@ -72,3 +72,22 @@ def test_rec_session_hooks():
     assert not s.prefers_host_parallelism()
     assert s.bucket_grain() == 64 and s.batch_grain() == 64 and s.rec_chunk() == 64
     assert s.rec_argmax_pairs()
+
+
+def test_cls_batches_and_decisions():
+    """The cls stage's batching (consecutive runs of 32 lines, the last one
+    shorter and not padded; engine.rs:1313-1324) and decision rule (flip when
+    p1 > p0 and p1 >= cls_thresh 0.9; confidence max(p0, p1);
+    engine.rs:1375-1380)."""
+    from qppocr_amd import pipeline
+    assert pipeline.cls_batches(42) == [(0, 32), (32, 42)]
+    assert pipeline.cls_batches(32) == [(0, 32)]
+    assert pipeline.cls_batches(0) == []
+    assert pipeline.cls_batches(5, per=2) == [(0, 2), (2, 4), (4, 5)]
+    p = np.array([[0.05, 0.95], [0.5, 0.5], [0.1, 0.9], [0.95, 0.05], [0.2, 0.8],
+                  [0.9, 0.9]], dtype=np.float32)
+    flip, conf = pipeline.cls_decisions(p)
+    assert flip.tolist() == [True, False, True, False, False, False]
+    assert conf.dtype == np.float32
+    assert (conf == np.array([0.95, 0.5, 0.9, 0.95, 0.8, 0.9], dtype=np.float32)).all()
+    assert pipeline.cls_decisions(p, thresh=0.96)[0].tolist() == [False] * 6
