@@ -50,6 +50,8 @@ rounds, run until each leg has taken 2 s, 5 s for the headline's det and rec):
   cfg3 det 640^2 / cfg4 rec 32x320: the headline's stage rates, with the
     per-kernel-class roofline fractions from per-node event times.
   cfg5: det 1536^2 + 128 rec lines in width buckets (page wall time).
+  cls (beside the five): the orientation classifier on a full batch of 32
+    lines of 3x48x192 (graph replays), lines/s.
 
 aux: the operators around the nets -- page resize, det input normalisation,
 rec line packing, the DB mask, the SE block's pool and gate, MaxPool,
@@ -494,6 +496,36 @@ def aux_specs(torch, lib, ctx):
     return specs
 
 
+def bench_cls(nets, lib, torch, ctx, replays, cpu_rounds, O):
+    """The cls stage's net (the orientation classifier of engine.rs:1294-1380)
+    on a full batch of 32 lines of 3x48x192: HIP events around graph replays
+    on the session's stream; the CPU oracle beside it."""
+    g, x = nets.build_cls(5, 32)
+    sess = nets.HipSession(g, ctx=ctx)
+    sess.run(x, outputs=False)
+    for _ in range(3):
+        sess.run(None, outputs=False)
+    sess.sync()
+    st = torch.cuda.ExternalStream(lib.qph_ctx_stream(ctx))
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(replays):
+        sess.run(None, outputs=False)
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / replays
+    out = {"workload": "cls 32x3x48x192 (seed 5), probabilities", "lines_per_s": round(32e3 / ms, 1),
+           "ms": round(ms, 4), "gflop": round(nets.flops(g) / 1e9, 4),
+           "launches": len(sess.plan()), "method": f"HIP events over {replays} graph replays"}
+    sess.close()
+    if O is not None:
+        from oracle import nets as onets
+        s, n = cpu_sample(lambda: onets.run_graph(g, x), cpu_rounds, CPU_CONFIG_MIN_S)
+        out["cpu_baseline"] = {"lines_per_s": round(32 / s, 2), "rounds": n}
+    return out
+
+
 def bench_aux(ops, replays, O=None, cpu_rounds=5):
     """Device time per launch of the operators around the nets (aux_specs),
     cache-cold: R buffer sets (R x set bytes > COLD_BYTES) whose launches are
@@ -923,6 +955,7 @@ def main():
         cfgs["cfg5"], mixed_data = time_mixed_page(max(3, K // 5), 2)
         cfgs["cfg5"]["engine_batching"], _ = time_mixed_page(max(3, K // 5), 2, engine=True,
                                                              data=mixed_data)
+        cfgs["cls"] = bench_cls(nets, lib, torch, ctx, max(3, K // 2), args.cpu_rounds, O)
 
     if O is not None:
         det_s, det_n = cpu_sample(lambda: onets.run_graph(det_g, det_x), args.cpu_rounds,

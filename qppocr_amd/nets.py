@@ -546,7 +546,11 @@ def node_cost(g, d):
         n, c = g.shapes[d["inp"]][:2]
         return 0, (g.numel(d["inp"]) + n * c) * f32, "hbm"
     if op == OP_MUL_ADD_SCALE:
-        return 0, (3 * g.numel(d["inp"]) + g.numel(d["in3"])) * f32, "hbm"
+        tensors = 3 if d["in2"] >= 0 else 2
+        return 0, (tensors * g.numel(d["inp"]) + g.numel(d["in3"])) * f32, "hbm"
+    if op == OP_BINARY:
+        tensors = 3 if d["in2"] >= 0 else 2
+        return 0, tensors * g.numel(d["inp"]) * f32, "hbm"
     if op in (OP_POOL, OP_RESIZE, OP_COPY_SLOT):
         n = g.shapes[d["inp"]][0]
         c = g.shapes[d["inp"]][1]
