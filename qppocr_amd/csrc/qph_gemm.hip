@@ -338,15 +338,13 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
 // wait for them.  The loads are inline asm, so the compiler adds no waits
 // of its own for the stages.
 template <int MBW, int NST>
-__global__ __launch_bounds__(64) void gemm_pw_kernel(GemmArgs g, int mgroups) {
-  extern __shared__ float pw_lds[];
+__device__ __forceinline__ void pw_tile(const GemmArgs& g, int mgroups, int blk, int64_t bt,
+                                        float* pw_lds) {
   constexpr int STAGE = 256 * (1 + MBW);   // floats: X slab, then W slab
   constexpr int PER = 1 + MBW;             // loads per slab
   const int lane = threadIdx.x;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int blk = blockIdx.x;
   const int mg = blk % mgroups, pg = blk / mgroups;
-  const int64_t bt = blockIdx.z;
   const int64_t n0 = (int64_t)pg * 16, m0 = (int64_t)mg * (16 * MBW);
   const int64_t M = g.m, N = g.n;
   const unsigned OOB = 0x80000000u;
@@ -474,6 +472,34 @@ __global__ __launch_bounds__(64) void gemm_pw_kernel(GemmArgs g, int mgroups) {
     }
 }
 
+template <int MBW, int NST>
+__global__ __launch_bounds__(64) void gemm_pw_kernel(GemmArgs g, int mgroups) {
+  extern __shared__ float pw_lds[];
+  pw_tile<MBW, NST>(g, mgroups, blockIdx.x, blockIdx.z, pw_lds);
+}
+
+// Up to three independent pointwise GEMMs in one launch, one 16-row block a
+// wave (the FPN laterals of the coarse levels, which no longer wait on one
+// another): workgroups [start[i], start[i + 1]) take GEMM i.  The branches
+// keep each GEMM's arguments in the kernel-argument segment.
+struct PwGroup {
+  GemmArgs g[3];
+  int mgroups[3];
+  int start[3];
+};
+
+template <int NST>
+__global__ __launch_bounds__(64) void gemm_pw_group_kernel(PwGroup p) {
+  extern __shared__ float pw_lds[];
+  const int b = blockIdx.x;
+  if (b >= p.start[2])
+    pw_tile<1, NST>(p.g[2], p.mgroups[2], b - p.start[2], blockIdx.z, pw_lds);
+  else if (b >= p.start[1])
+    pw_tile<1, NST>(p.g[1], p.mgroups[1], b - p.start[1], blockIdx.z, pw_lds);
+  else
+    pw_tile<1, NST>(p.g[0], p.mgroups[0], b, blockIdx.z, pw_lds);
+}
+
 // The pointwise kernel takes K a multiple of 16, M <= 128, 16-byte aligned
 // rows of both operands, N a multiple of 4 and offsets within 31 bits.
 static bool pw_eligible(const GemmArgs& g) {
@@ -482,6 +508,84 @@ static bool pw_eligible(const GemmArgs& g) {
          g.a_batch % 4 == 0 && g.b_batch % 4 == 0 && (uintptr_t)g.a % 16 == 0 &&
          (uintptr_t)g.b % 16 == 0 && g.k * g.ldb * 4 < (1ll << 31) &&
          g.m * g.lda * 4 < (1ll << 31) && g.ldb >= g.n && g.lda >= g.k;
+}
+
+bool pw_group_eligible(const GemmArgs& g) {
+  return pw_eligible(g) && !g.res && g.batch >= 1 && g.batch <= 65535 &&
+         (double)ceil_div(g.n, 16) * (double)ceil_div(g.m, 16) < (double)(1 << 29);
+}
+
+int launch_pw_group(const GemmArgs* g, int n, hipStream_t s) {
+  if (n < 1 || n > 3) return fail(QPH_EINVAL, "pointwise group: 1 to 3 GEMMs");
+  PwGroup p{};
+  int64_t total = 0;
+  bool deep = false;
+  for (int i = 0; i < n; i++) {
+    if (!pw_group_eligible(g[i]) || g[i].batch != g[0].batch)
+      return fail(QPH_EUNSUPPORTED, "pointwise group: a GEMM the group kernel does not take");
+    p.g[i] = g[i];
+    p.mgroups[i] = (int)ceil_div(g[i].m, 16);
+    p.start[i] = (int)total;
+    total += ceil_div(g[i].n, 16) * p.mgroups[i];
+    deep = deep || g[i].k > 32;
+  }
+  for (int i = n; i < 3; i++) p.start[i] = (int)total;
+  if (total >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "pointwise group: grid too large");
+  const dim3 grid((unsigned)total, 1, (unsigned)g[0].batch);
+  const size_t lds = (size_t)(deep ? 4 : 2) * 256 * 2 * 4;
+  if (deep)
+    hipLaunchKernelGGL(gemm_pw_group_kernel<4>, grid, dim3(64), lds, s, p);
+  else
+    hipLaunchKernelGGL(gemm_pw_group_kernel<2>, grid, dim3(64), lds, s, p);
+  return launch_check("gemm_pw_group_kernel");
+}
+
+// FPN top-down over the level-3 maps of every batch item: in4 = t4 + up2(in5)
+// and in3 = t3 + up2(in4), each Add rounded as the laterals' residual
+// epilogues round it.  A lane takes four consecutive level-3 elements of
+// one row (w3 is a multiple of 4): the level-4 values t4 + in5 of their
+// columns, in3 = t3 + that, and in4 stored by the even-position elements.
+__global__ __launch_bounds__(256) void fpn_topdown_kernel(const float* __restrict__ t4,
+                                                          const float* __restrict__ in5,
+                                                          const float* __restrict__ t3,
+                                                          float* __restrict__ in4,
+                                                          float* __restrict__ in3, int h3, int w3,
+                                                          int total) {
+  const int e0 = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
+  if (e0 >= total) return;
+  const int hw3 = h3 * w3, w4 = w3 >> 1, w5 = w3 >> 2, hw4 = hw3 >> 2, hw5 = hw3 >> 4;
+  const int plane = e0 / hw3, r = e0 - plane * hw3;
+  const int y = r / w3, x = r - y * w3;
+  const float* a4 = t4 + (int64_t)plane * hw4 + (y >> 1) * w4;
+  const float* a5 = in5 + (int64_t)plane * hw5 + (y >> 2) * w5;
+  const f32x4 a3 = *(const f32x4*)(t3 + (int64_t)plane * hw3 + r);
+  f32x4 o;
+  float v4[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    v4[u] = a4[(x + u) >> 1] + a5[(x + u) >> 2];
+    o[u] = a3[u] + v4[u];
+  }
+  *(f32x4*)(in3 + (int64_t)plane * hw3 + r) = o;
+  if (!(y & 1)) {
+    float* d4 = in4 + (int64_t)plane * hw4 + (y >> 1) * w4 + (x >> 1);
+    d4[0] = v4[0];
+    d4[1] = v4[2];
+  }
+}
+
+int launch_fpn_topdown(const float* t4, const float* in5, const float* t3, float* in4, float* in3,
+                       int64_t n, int64_t c, int64_t h3, int64_t w3, hipStream_t s) {
+  if (h3 % 4 || w3 % 4 || h3 <= 0 || w3 <= 0)
+    return fail(QPH_EINVAL, "fpn top-down: level-3 sides must be multiples of 4");
+  const int64_t total = n * c * h3 * w3;
+  if (total <= 0) return QPH_OK;
+  if (total >= (1ll << 31)) return fail(QPH_EUNSUPPORTED, "fpn top-down: maps too large");
+  const auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  if (!al(t3) || !al(in3)) return fail(QPH_EUNSUPPORTED, "fpn top-down: level-3 maps not 16-byte aligned");
+  hipLaunchKernelGGL(fpn_topdown_kernel, dim3((unsigned)ceil_div(total, 1024)), dim3(256), 0, s,
+                     t4, in5, t3, in4, in3, (int)h3, (int)w3, (int)total);
+  return launch_check("fpn_topdown_kernel");
 }
 
 template <int MBW>

@@ -187,6 +187,21 @@ struct GemmArgs {
   float* part;                                     // fused head: per-block argmax partials
 };
 int launch_gemm(const GemmArgs& g, hipStream_t s);
+// The GEMM of a pointwise (1x1, stride 1, no padding, one group) conv of x
+// [n][C][H][W] with w [M][C]: everything but residual, placement and store
+// layout (plain rows), as conv_dispatch sets it up.
+void pointwise_gemm_args(const float* x, const int64_t xs[4], const float* w,
+                         const int64_t ws[4], const float* bias, const Act& a, float* y,
+                         GemmArgs* out);
+// Up to three pointwise GEMMs (no residual) that each take one-block
+// pointwise tiles, as one launch (pw_group_eligible says which can).
+bool pw_group_eligible(const GemmArgs& g);
+int launch_pw_group(const GemmArgs* g, int n, hipStream_t s);
+// FPN top-down on the level-3 maps: in4 = t4 + up2(in5), in3 = t3 + up2(in4)
+// (nearest 2x, each Add rounded, as the laterals' residual epilogues do);
+// per batch item c planes of h3 x w3 (in4 h3/2 x w3/2, in5 h3/4 x w3/4).
+int launch_fpn_topdown(const float* t4, const float* in5, const float* t3, float* in4, float* in3,
+                       int64_t n, int64_t c, int64_t h3, int64_t w3, hipStream_t s);
 // The rec head with the softmax-argmax fused into the GEMM (pairs only):
 // (max, first index, exp1 sum) per row and 64-column block into part
 // (head_argmax_part_floats floats), then the pairs.  Values within ~1e-6

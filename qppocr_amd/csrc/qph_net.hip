@@ -27,6 +27,9 @@ struct qph_net {
   std::vector<int> group_len;    // > 1: first of that many independent 3x3 convs, one launch
   std::vector<bool> convt_fused; // 3x3 conv node i and its conv-transpose pair i + 1, one launch
   std::vector<int> absorb_after; // nodes after node i done in its launch's epilogue (0 or 4)
+  std::vector<bool> fpn;         // node i starts four FPN laterals run as three launches
+  std::vector<float*> fpn_tmp;   // per such node: the raw level-4 and level-3 laterals
+  std::vector<float*> fpn_t4, fpn_t3;
   std::vector<DwPwArgs> dwpw;    // per node: fused depthwise + pointwise launch
   std::vector<bool> fused;       // node i runs dwpw[i] (and node i + 1, and i + 2 for a stem, with it)
   std::vector<float*> wt;        // per linear node: resident transposed weight Wt[N][K] (or NULL)
@@ -838,6 +841,100 @@ static int validate_node(qph_net* net, size_t i, const int64_t* wsizes, int32_t 
 // Every node in order, fused launches where planned.  With profiling on,
 // an event precedes each node; the nodes a fused launch covers after its
 // first get their events right after it (so their time reads 0).
+// The FPN top-down laterals: four consecutive 1x1 convs to the same M with
+// no activation, L5 = conv(C5), L4 = conv(C4) + up2(L5), L3 = conv(C3) +
+// up2(L4), L2 = conv(C2) + up2(L3), each a plain single-node launch.  The
+// three coarse GEMMs do not depend on one another without their residuals:
+// one grouped launch computes conv(C5) into L5 and conv(C4), conv(C3) into
+// net-owned buffers, one elementwise pass forms L4 and L3 (the same Adds),
+// and L2 runs as before.  Three launches instead of four, the coarse GEMMs
+// side by side instead of one after another.  (L2's GEMM forming its
+// residual from the raw laterals itself, with the elementwise pass in its
+// launch, made two launches but a slower step with two pages in flight.)
+static int plan_fpn(qph_net* net) {
+  const size_t nn = net->nodes.size();
+  net->fpn.assign(nn, false);
+  // nodes that start a single-node launch in run_all's stepping
+  std::vector<bool> single(nn, false);
+  for (size_t i = 0; i < nn;) {
+    size_t step = 1;
+    if (net->group_len[i] > 1) step = (size_t)net->group_len[i];
+    else if (net->head[i] || net->convt_fused[i] || net->qa_fused[i]) step = 2;
+    else if (net->fused[i]) step = net->dwpw[i].stem ? 3 : 2;
+    step += (size_t)net->absorb_after[i + step - 1];
+    single[i] = step == 1 && !net->cl_dw[i] && !net->cl_pw[i] && !net->cl_out[i];
+    i += step;
+  }
+  auto lateral = [&](size_t i) {
+    const qph_node& n = net->nodes[i];
+    return n.op == QPH_OP_CONV && single[i] && conv_is_pointwise(n.ws, n.cp) &&
+           n.cp.group == 1 && n.act.kind == QPH_ACT_NONE && !n.y_ctotal && !n.y_coff &&
+           (!n.y_up || n.y_up == 1) && !n.trans_out && n.bias >= 0 &&
+           storage_of(net, n.out) == n.out && net->alias[(size_t)n.out] < 0;
+  };
+  for (size_t i = 0; i + 3 < nn; i++) {
+    bool ok = true;
+    for (size_t k = 0; k < 4 && ok; k++) ok = lateral(i + k);
+    if (!ok) continue;
+    const qph_node* q[4] = {&net->nodes[i], &net->nodes[i + 1], &net->nodes[i + 2],
+                            &net->nodes[i + 3]};
+    if (q[0]->in2 >= 0) continue;
+    for (int k = 1; k < 4 && ok; k++)
+      ok = q[k]->in2 == q[k - 1]->out && q[k]->res_up == 2 && q[k]->ws[0] == q[0]->ws[0];
+    if (!ok) continue;
+    const int64_t* s3 = &net->shapes[4 * (size_t)q[2]->out];
+    if (s3[2] % 4 || s3[3] % 4) continue;
+    // the grouped GEMMs at the full batch take the pointwise group kernel
+    for (int k = 0; k < 3 && ok; k++) {
+      GemmArgs g{};
+      const qph_node& n = *q[k];
+      Act a = make_act(&n.act);
+      pointwise_gemm_args(net->tptr[n.in], &net->shapes_full[4 * (size_t)n.in],
+                          net->weights[n.w], n.ws, net->weights[n.bias], a, net->tptr[n.out], &g);
+      ok = pw_group_eligible(g);
+    }
+    if (!ok) continue;
+    float* t4 = nullptr;
+    float* t3 = nullptr;
+    QPH_TRY(hip_check(hipMalloc((void**)&t4, (size_t)numel_of(net, q[1]->out) * 4), "hipMalloc(fpn)"));
+    net->fpn_tmp.push_back(t4);
+    QPH_TRY(hip_check(hipMalloc((void**)&t3, (size_t)numel_of(net, q[2]->out) * 4), "hipMalloc(fpn)"));
+    net->fpn_tmp.push_back(t3);
+    net->fpn[i] = true;
+    net->fpn_t4.resize(nn, nullptr);
+    net->fpn_t3.resize(nn, nullptr);
+    net->fpn_t4[i] = t4;
+    net->fpn_t3[i] = t3;
+    i += 3;
+  }
+  return QPH_OK;
+}
+
+static int run_fpn(qph_net* net, size_t i) {
+  hipStream_t s = net->ctx->stream;
+  const qph_node* q[4] = {&net->nodes[i], &net->nodes[i + 1], &net->nodes[i + 2],
+                          &net->nodes[i + 3]};
+  float* t4 = net->fpn_t4[i];
+  float* t3 = net->fpn_t3[i];
+  float* outs[3] = {net->tptr[q[0]->out], t4, t3};
+  GemmArgs g[3];
+  for (int k = 0; k < 3; k++) {
+    const qph_node& n = *q[k];
+    Act a = make_act(&n.act);
+    pointwise_gemm_args(net->tptr[n.in], &net->shapes[4 * (size_t)n.in], net->weights[n.w], n.ws,
+                        net->weights[n.bias], a, outs[k], &g[k]);
+  }
+  int rc = launch_pw_group(g, 3, s);
+  if (rc != QPH_OK) return fail(rc, node_name(i, *q[0]) + ": " + qph_last_error());
+  const int64_t* s3 = &net->shapes[4 * (size_t)q[2]->out];
+  rc = launch_fpn_topdown(t4, net->tptr[q[0]->out], t3, net->tptr[q[1]->out],
+                          net->tptr[q[2]->out], s3[0], s3[1], s3[2], s3[3], s);
+  if (rc != QPH_OK) return fail(rc, node_name(i + 1, *q[1]) + ": " + qph_last_error());
+  rc = run_node(net, i + 3);
+  if (rc != QPH_OK) return fail(rc, node_name(i + 3, *q[3]) + ": " + qph_last_error());
+  return QPH_OK;
+}
+
 static int run_all(qph_net* net) {
   hipStream_t s = net->ctx->stream;
   const size_t nn = net->nodes.size();
@@ -863,6 +960,9 @@ static int run_all(qph_net* net) {
                                         net->head_part[i], net->tptr[r.out2], s);
       if (rc != QPH_OK) return fail(rc, node_name(i, q) + ": " + qph_last_error());
       step = 2;
+    } else if (net->fpn[i]) {
+      QPH_TRY(run_fpn(net, i));
+      step = 4;
     } else if (net->convt_fused[i]) {
       const qph_node& q = net->nodes[i + 1];
       ConvArgs a = net->plan[i];
@@ -976,6 +1076,8 @@ static void release(qph_net* net) {
   for (float* p : net->wk)
     if (p) (void)hipFree(p);
   for (float* p : net->head_part)
+    if (p) (void)hipFree(p);
+  for (float* p : net->fpn_tmp)
     if (p) (void)hipFree(p);
   for (float* p : net->wt)
     if (p) (void)hipFree(p);
@@ -1154,6 +1256,7 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     net->group_len.assign(nn, 1);
     net->convt_fused.assign(nn, false);
     net->absorb_after.assign(nn, 0);
+    net->fpn.assign(nn, false);
     net->cl_dw.assign(nn, false);
     net->cl_pw.assign(nn, false);
     net->cl_out.assign(nn, false);
@@ -1165,6 +1268,8 @@ QPH_API int qph_net_create(qph_ctx* ctx, const qph_net_spec* spec,
     plan_conv_convt(net);
     plan_cl(net);
     rc = plan_dwpw(net);
+    if (rc) return bail(rc);
+    rc = plan_fpn(net);
     if (rc) return bail(rc);
   }
   rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
@@ -1218,7 +1323,8 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
   // the stepping of run_all: one launch per plain node, one per fused
   // block / dense group / conv + conv-transpose pair / fused head (the head
   // is two kernels) / QKV linear + attention, each also covering the
-  // elementwise nodes folded into its epilogue
+  // elementwise nodes folded into its epilogue; the four FPN laterals are
+  // three kernels
   int32_t n = 0;
   const size_t nn = net->nodes.size();
   for (size_t i = 0; i < nn; n++) {
@@ -1229,6 +1335,7 @@ QPH_API int qph_net_plan(qph_net* net, int32_t* first, int32_t* nodes, int32_t* 
     else if (net->fused[i]) step = net->dwpw[i].stem ? 3 : 2;
     else if (net->convt_fused[i]) step = 2;
     else if (net->qa_fused[i]) step = 2;
+    else if (net->fpn[i]) step = 4, nk = 3;
     step += (size_t)net->absorb_after[i + step - 1];
     if (n < cap) {
       if (first) first[n] = (int32_t)i;

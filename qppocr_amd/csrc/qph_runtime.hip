@@ -306,6 +306,27 @@ int kernel_occupancy(const void* fn, int block, int* occ) {
   return QPH_OK;
 }
 
+// The GEMM of a pointwise conv (the reference's 1x1 branch, conv.rs:264-460):
+// Y[n][M][HW] = W[M][C] X[n][C][HW] over the batch, column-major-free rows,
+// with the reference's bias placement rule; no residual, plain store.
+void pointwise_gemm_args(const float* x, const int64_t xs[4], const float* w,
+                         const int64_t ws[4], const float* bias, const Act& a, float* y,
+                         GemmArgs* out) {
+  const int64_t n = xs[0], c = xs[1], hw = xs[2] * xs[3], m = ws[0];
+  GemmArgs gm{};
+  gm.a = w; gm.lda = c; gm.a_batch = 0;
+  gm.b = x; gm.ldb = hw; gm.b_batch = c * hw;
+  gm.c = y; gm.ldc = hw; gm.c_batch = m * hw;
+  gm.m = m; gm.n = hw; gm.k = c; gm.batch = n;
+  gm.bias = bias; gm.bias_mode = bias ? 1 : 0;
+  // 1x1 path of conv.rs:370-460: N > 1 runs the serial panel kernel per
+  // chunk; N == 1 runs sgemm_res, whose rule depends on the shape.
+  const double fl = (double)m * (double)hw * (double)c;
+  gm.seed_rule = (n > 1 || fl < 2e5 || (hw + 31) / 32 >= 2) ? 0 : 1;
+  gm.act = a;
+  *out = gm;
+}
+
 // Validates a conv node and launches its kernel.  wk: resident k-major
 // repacked weights of a dense conv (NULL: repacked into the context scratch).
 int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float* w,
@@ -348,20 +369,8 @@ int conv_dispatch(qph_ctx* ctx, const float* x, const int64_t xs[4], const float
     if (!plain_out) return fail(QPH_EUNSUPPORTED, "conv2d 1x1: channel-slice output not supported");
     if (trans && res_up) return fail(QPH_EUNSUPPORTED, "conv2d 1x1: trans_out with res_up");
     GemmArgs gm{};
-    gm.a = w; gm.lda = c; gm.a_batch = 0;
-    gm.b = x; gm.ldb = h * wd; gm.b_batch = c * h * wd;
-    gm.c = y;
+    pointwise_gemm_args(x, xs, w, ws, bias, a, y, &gm);
     gm.ldc = trans ? m : oh * ow;
-    gm.c_batch = m * oh * ow;
-    gm.m = m; gm.n = oh * ow; gm.k = c; gm.batch = n;
-    gm.bias = bias; gm.bias_mode = bias ? 1 : 0;
-    // 1x1 path of conv.rs:370-460: N > 1 runs the serial panel kernel per
-    // chunk; N == 1 runs sgemm_res, whose rule depends on the shape.
-    {
-      double fl = (double)m * (double)(oh * ow) * (double)c;
-      gm.seed_rule = (n > 1 || fl < 2e5 || (oh * ow + 31) / 32 >= 2) ? 0 : 1;
-    }
-    gm.act = a;
     gm.res = res;
     gm.ldr = res_up ? (oh / 2) * (ow / 2) : oh * ow;
     gm.r_batch = m * gm.ldr;

@@ -429,6 +429,61 @@ def test_session_conv_convt_pair(gpu, oracle, case):
     sess.close()
 
 
+FPN_CASES = [
+    # batch, level-2 side (h, w), channels of C2..C5, M, a lateral with ReLU (not fused)
+    (1, (32, 40), (16, 32, 48, 64), 32, False),
+    (2, (16, 32), (32, 64, 128, 256), 96, False),
+    (1, (32, 40), (16, 32, 48, 64), 32, True),
+]
+
+
+@pytest.mark.parametrize("case", FPN_CASES, ids=lambda c: f"n{c[0]}-{c[1][0]}x{c[1][1]}-m{c[3]}-{int(c[4])}")
+def test_session_fpn_laterals(gpu, oracle, case):
+    """The det FPN's four 1x1 laterals with their nearest-2x top-down Adds
+    (L5 = conv(C5), Lk = conv(Ck) + up2(Lk+1)) run as the grouped coarse
+    GEMMs, the top-down pass and the fine lateral: one plan entry of four
+    nodes and three kernels; every level bit-exact against the oracle, and
+    with real_n 1 on a batch of 2 the oracle's one-item bits."""
+    from qppocr_amd import nets
+    from qppocr_amd._lib import ACT_RELU
+    from oracle import nets as onets
+    n, (h, w), cs, m, relu = case
+
+    def build(batch, r):
+        g = nets.Graph((batch, cs[0], h, w))
+        feats = [0]
+        for k in range(1, 4):
+            wc = g.weight(r.kaiming((cs[k], cs[k - 1], 3, 3), 9 * cs[k - 1]))
+            bc = g.weight(r.normal((cs[k],), 0.1))
+            feats.append(g.conv(feats[-1], wc, bc, stride=(2, 2), pad=(1, 1, 1, 1)))
+        lat = -1
+        outs = []
+        for k in (3, 2, 1, 0):
+            wl = g.weight(r.kaiming((m, cs[k], 1, 1), cs[k]))
+            bl = g.weight(r.normal((m,), 0.1))
+            act = ACT_RELU if (relu and k == 1) else nets.ACT_NONE
+            lat = g.conv(feats[k], wl, bl, residual=lat, res_up=2 if lat >= 0 else 0, act=act)
+            outs.append(lat)
+        g.outputs = outs
+        return g
+
+    g = build(n, nets.WeightRng(31))
+    x = nets.WeightRng(32).normal((n, cs[0], h, w), 1.0)
+    print(f"fpn laterals {case}", flush=True)
+    sess = nets.HipSession(g)
+    assert ((3, 4, 3) in sess.plan()) == (not relu), sess.plan()
+    got = sess.run(x)
+    ref = onets.run_graph(g, x)
+    for lvl, (a, b) in enumerate(zip(got, ref)):
+        assert_bitexact(a, b, f"level {5 - lvl}")
+    if n > 1:
+        got1 = sess.run(x[:1])
+        ref1 = onets.run_graph(build(1, nets.WeightRng(31)), x[:1])
+        for lvl, (a, b) in enumerate(zip(got1, ref1)):
+            assert_bitexact(a, b, f"real_n 1 level {5 - lvl}")
+    sess.close()
+
+
 LINEAR_CASES = [
     # rows, k, n, layernorm in front, activation, residual, LN output also an output
     (1280, 256, 768, True, "none", False, False),   # rec QKV: 4 slabs
