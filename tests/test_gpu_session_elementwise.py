@@ -14,7 +14,10 @@ from conftest import assert_bitexact
 pytestmark = pytest.mark.gpu
 
 
-def _run(g, x):
+def _run(g, x, build1=None):
+    """Runs g on x through the session and the oracle (bit-exact, and a
+    replay); with build1 (the same graph at batch 1), also real_n 1 against
+    the oracle's one-item graph."""
     from qppocr_amd import nets
     from oracle import nets as onets
     sess = nets.HipSession(g)
@@ -26,6 +29,11 @@ def _run(g, x):
     again = sess.run(x)
     for i, (a, b) in enumerate(zip(again, got)):
         assert_bitexact(a, b, f"replay output {i}")
+    if build1 is not None:
+        got1 = sess.run(x[:1])
+        ref1 = onets.run_graph(build1(), x[:1])
+        for i, (a, b) in enumerate(zip(got1, ref1)):
+            assert_bitexact(a, b, f"real_n 1 output {i}")
     sess.close()
     return launches
 
@@ -35,21 +43,25 @@ def test_session_binary_nodes(gpu, oracle, shape):
     """Every op in both operand orders, scalar and same-shape, including
     zero divisors (signed infinities), on a 16-byte and a ragged size."""
     from qppocr_amd import nets
-    r = nets.WeightRng(21)
-    g = nets.Graph(shape)
-    x = r.normal(shape, 1.5)
+
+    def build(n):
+        g = nets.Graph((n,) + shape[1:])
+        outs = []
+        for op in range(4):
+            outs.append(g.binary(0, op, scalar=0.375))
+            outs.append(g.binary(0, op, scalar=-1.25, scalar_first=True))
+        prod = g.binary(outs[0], 2, other=outs[3])
+        outs.append(prod)
+        outs.append(g.binary(prod, 1, other=0))
+        outs.append(g.binary(0, 3, other=outs[6]))
+        g.outputs = outs
+        return g
+
+    g = build(shape[0])
+    x = nets.WeightRng(21).normal(shape, 1.5)
     x.flat[::7] = 0.0
-    outs = []
-    for op in range(4):
-        outs.append(g.binary(0, op, scalar=0.375))
-        outs.append(g.binary(0, op, scalar=-1.25, scalar_first=True))
-    prod = g.binary(outs[0], 2, other=outs[3])
-    outs.append(prod)
-    outs.append(g.binary(prod, 1, other=0))
-    outs.append(g.binary(0, 3, other=outs[6]))
-    g.outputs = outs
     print(f"binary nodes {shape}", flush=True)
-    launches = _run(g, x)
+    launches = _run(g, x, (lambda: build(1)) if shape[0] > 1 else None)
     assert len(launches) == len(g.nodes)
 
 
@@ -95,31 +107,36 @@ def test_session_hardswish_clip_fold(gpu, oracle, case):
     four roundings), five otherwise; bit-exact either way."""
     from qppocr_amd import nets
     prod, shared, separate = case
-    r = nets.WeightRng(23)
     shape = (2, 16, 14, 20)
-    g = nets.Graph(shape)
-    x = r.normal(shape, 3.0)
-    if prod == "conv3x3":
-        w = g.weight(r.kaiming((24, 16, 3, 3), 144))
-        b = g.weight(r.normal((24,), 0.1))
-        t = g.conv(0, w, b, pad=(1, 1, 1, 1))
-    elif prod == "conv1x1":
-        w = g.weight(r.kaiming((32, 16, 1, 1), 16))
-        b = g.weight(r.normal((32,), 0.1))
-        t = g.conv(0, w, b)
-    elif prod == "depthwise":
-        w = g.weight(r.kaiming((16, 1, 3, 3), 9))
-        b = g.weight(r.normal((16,), 0.1))
-        t = g.conv(0, w, b, stride=(2, 2), pad=(1, 1, 1, 1), group=16)
-    else:
-        w = g.weight(r.kaiming((20, 48), 20))
-        b = g.weight(r.normal((48,), 0.1))
-        t = g.linear(0, w, b)
-    y = g.hardswish_clip(t)
-    g.outputs = [y, t] if shared else [y]
-    if separate:
-        g.flags |= nets.NET_SEPARATE_LAUNCHES
+
+    def build(n):
+        r = nets.WeightRng(23)
+        g = nets.Graph((n,) + shape[1:])
+        if prod == "conv3x3":
+            w = g.weight(r.kaiming((24, 16, 3, 3), 144))
+            b = g.weight(r.normal((24,), 0.1))
+            t = g.conv(0, w, b, pad=(1, 1, 1, 1))
+        elif prod == "conv1x1":
+            w = g.weight(r.kaiming((32, 16, 1, 1), 16))
+            b = g.weight(r.normal((32,), 0.1))
+            t = g.conv(0, w, b)
+        elif prod == "depthwise":
+            w = g.weight(r.kaiming((16, 1, 3, 3), 9))
+            b = g.weight(r.normal((16,), 0.1))
+            t = g.conv(0, w, b, stride=(2, 2), pad=(1, 1, 1, 1), group=16)
+        else:
+            w = g.weight(r.kaiming((20, 48), 20))
+            b = g.weight(r.normal((48,), 0.1))
+            t = g.linear(0, w, b)
+        y = g.hardswish_clip(t)
+        g.outputs = [y, t] if shared else [y]
+        if separate:
+            g.flags |= nets.NET_SEPARATE_LAUNCHES
+        return g
+
+    g = build(2)
+    x = nets.WeightRng(24).normal(shape, 3.0)
     print(f"hardswish clip form after {case}", flush=True)
-    launches = _run(g, x)
+    launches = _run(g, x, lambda: build(1))
     assert ((0, 5, 1) in launches) == (not shared and not separate), launches
     assert len(launches) == (1 if (0, 5, 1) in launches else 5)
