@@ -226,6 +226,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
   const int lg = lane >> 4, l16 = lane & 15;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t bz = blockIdx.z;
+  if (g.rn && *g.rn != 0 && bz >= (int64_t)*g.rn * g.rn_per) return;   // past the real batch
   const int64_t i0 = (int64_t)blockIdx.y * 32;
   const int64_t j0 = (int64_t)blockIdx.x * 32;
   const float* A = g.a + bz * g.a_batch;
@@ -342,6 +343,7 @@ __device__ __forceinline__ void pw_tile(const GemmArgs& g, int mgroups, int blk,
                                         float* pw_lds) {
   constexpr int STAGE = 256 * (1 + MBW);   // floats: X slab, then W slab
   constexpr int PER = 1 + MBW;             // loads per slab
+  if (g.rn && *g.rn != 0 && bt >= (int64_t)*g.rn * g.rn_per) return;   // past the real batch
   const int lane = threadIdx.x;
   const int l16 = lane & 15, lg = lane >> 4;
   const int mg = blk % mgroups, pg = blk / mgroups;

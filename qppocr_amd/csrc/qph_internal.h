@@ -185,6 +185,9 @@ struct GemmArgs {
   int64_t up_w, up_cw;                             // output / coarse image width (res_up)
   int trans_out;                                   // store C^T: c[j*ldc + i]
   float* part;                                     // fused head: per-block argmax partials
+  // real-batch early exit (plan path): batch items bz >= *rn * rn_per are
+  // skipped when rn is set and *rn != 0 (the pointwise and skinny kernels)
+  const unsigned* rn; int64_t rn_per;
 };
 int launch_gemm(const GemmArgs& g, hipStream_t s);
 // The GEMM of a pointwise (1x1, stride 1, no padding, one group) conv of x
@@ -357,8 +360,10 @@ int launch_argmax(const float* probs, int64_t rows, int64_t cols, float* pairs, 
 int launch_argmax_pitched(const float* probs, int64_t rows, int64_t cols, int64_t ld,
                           float* pairs, hipStream_t s);
 // logits rows ld floats apart, probabilities rows ldo floats apart (either may be NULL)
+// rn (plan path): rows >= *rn * rpb are skipped when *rn != 0
 int launch_softmax_pitched(const float* logits, int64_t rows, int64_t cols, int64_t ld,
-                           float* probs, int64_t ldo, float* pairs, hipStream_t s);
+                           float* probs, int64_t ldo, float* pairs, hipStream_t s,
+                           const unsigned* rn = nullptr, int64_t rpb = 0);
 int launch_attention(const float* qkv, int64_t batch, int64_t t, int64_t heads, int64_t dh,
                      float scale, float* out, hipStream_t s);
 int launch_attention_generic(const float* qkv, int64_t batch, int64_t t, int64_t heads,
@@ -378,9 +383,11 @@ int launch_mask_pairs(float* pairs, int64_t batch, int64_t t, const int32_t* t_v
 int launch_reduce_mean(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t s);
 // row r's element j at x[(r / rpg) * gstride + (r % rpg) * rstride + j * estride],
 // its mean to out[r * ostride] (ostride 4: the row's other three words set to 0)
+// rn (plan path): rows >= *rn * rpb are skipped when *rn != 0
 int launch_reduce_mean_rows(const float* x, int64_t rows, int64_t cols, int64_t rpg,
                             int64_t gstride, int64_t rstride, int64_t estride, float* out,
-                            int64_t ostride, hipStream_t s);
+                            int64_t ostride, hipStream_t s, const unsigned* rn = nullptr,
+                            int64_t rpb = 0);
 
 // qph_aux.hip.  ctot / coff: the output is channels [coff, coff + c) of a
 // tensor with ctot channels (ctot = c, coff = 0 for a plain output).

@@ -31,9 +31,10 @@
 //    n_exit3_argmax the first strict maximum (rec.rs:46-54).
 //  - n_attn_mm: the batched MatMul's k-ascending fma chains (shape.rs:568-698).
 // Real-batch early exit: word 0 of the arena holds real_n (plan.rs:587-593);
-// the entry, exit3, pool, depthwise, conv and channel kernels skip batch
-// rows past it as the reference's kernels do; the GEMM-based dispatches
-// compute the padded rows too (never read).
+// the entry, exit3, pool, depthwise, conv, channel, softmax, row-mean
+// (n_reduce_last, n_reduce_hw/fin) and batched-matmul (n_attn_mm) launches
+// skip batch rows past it as the reference's kernels do; the pointwise
+// GEMM dispatches compute the padded rows too (never read).
 
 #include <hip/hip_runtime.h>
 
@@ -1469,12 +1470,16 @@ __global__ __launch_bounds__(256) void plan_concat_kernel(ConcatK p) {
 }
 
 // pad columns [cols, cpad) of rows x cpad set to 0 (n_softmax.comp's tail)
-struct PadColsK { float* y; int64_t rows, cols, cpad; };
+// the softmax output's pad columns (n_softmax.comp writes them in the row's
+// pass, so rows past the real batch keep theirs)
+struct PadColsK { const float* arena; float* y; int64_t rows, cols, cpad, rpb; };
 __global__ __launch_bounds__(256) void plan_pad_cols_kernel(PadColsK p) {
   const int64_t w = p.cpad - p.cols;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= p.rows * w) return;
   const int64_t r = i / w;
+  const unsigned rn = real_n(p.arena);
+  if (rn != 0 && r >= (int64_t)rn * p.rpb) return;
   p.y[r * p.cpad + p.cols + (i - r * w)] = 0.0f;
 }
 
@@ -2328,8 +2333,9 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       pending.erase(it);
       // GlobalAveragePool: channel c of image b is the mean over the P
       // pixels x[(b * P + p) * C + c]
+      const unsigned* rn = (const unsigned*)d.at(0);
       return add_launch(pl, d.idx, [=](hipStream_t s) {
-        return launch_reduce_mean_rows(x, nb * c, m, c, m * c, 1, c, y, 1, s);
+        return launch_reduce_mean_rows(x, nb * c, m, c, m * c, 1, c, y, 1, s, rn, c);
       });
     }
     case PK_REDUCE_LAST: {
@@ -2343,8 +2349,10 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       QPH_TRY(d.region(w[1], (uint64_t)rows * 4, false, "output"));
       const float* x = d.at(w[0]);
       float* y = d.at(w[1]);
+      const unsigned* rn = (const unsigned*)d.at(0);
+      const int64_t rpb = w[5];
       return add_launch(pl, d.idx, [=](hipStream_t s) {
-        return launch_reduce_mean_rows(x, rows, cols, rows, 0, cp, 1, y, 4, s);
+        return launch_reduce_mean_rows(x, rows, cols, rows, 0, cp, 1, y, 4, s, rn, rpb);
       });
     }
     case PK_RESIZE: {
@@ -2551,9 +2559,12 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
         }
         break;
       }
-      PadColsK pk{y, rows, cols, cp};
+      const unsigned* rn = (const unsigned*)d.at(0);
+      const int64_t rpb = w[5];
+      PadColsK pk{d.at(0), y, rows, cols, cp, rpb};
       return add_launch(pl, d.idx, [=](hipStream_t s) {
-        QPH_TRY(launch_softmax_pitched(x, rows, cols, cp, dead ? nullptr : y, cp, pairs, s));
+        QPH_TRY(launch_softmax_pitched(x, rows, cols, cp, dead ? nullptr : y, cp, pairs, s, rn,
+                                       rpb));
         if (dead || cp == cols) return QPH_OK;
         hipLaunchKernelGGL(plan_pad_cols_kernel, dim3(blocks_for(rows * (cp - cols))), dim3(256),
                            0, s, pk);
@@ -2575,6 +2586,8 @@ int decode(Decoder& d, const qph_plan_dispatch& q, std::vector<PendingHw>& pendi
       g.m = m; g.n = n; g.k = kk; g.batch = batch;
       g.bias = nullptr; g.bias_mode = 0; g.seed_rule = 0;
       g.act = make_act(nullptr);
+      // batch items past real_n x heads skipped (n_attn_mm.comp)
+      g.rn = (const unsigned*)d.at(0); g.rn_per = w[7];
       return add_launch(pl, d.idx, [g](hipStream_t s) { return launch_gemm(g, s); });
     }
     default:

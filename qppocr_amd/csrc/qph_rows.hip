@@ -202,15 +202,25 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
 // exponentials are then recomputed from the logits where the probabilities
 // would have been read back; exp1 is deterministic, so the values are the
 // same).  pairs may be NULL.
+// A row past the real batch (rn set and *rn != 0: rows >= *rn * rpb, the
+// plan model's word 0) returns at once in every softmax kernel.
+__device__ __forceinline__ bool past_real(const unsigned* rn, int64_t rpb, int64_t row) {
+  if (!rn) return false;
+  const unsigned r = *rn;
+  return r != 0 && row >= (int64_t)r * rpb;
+}
+
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* logits, int64_t cols,
                                                            int64_t ld, float* probs, int64_t ldo,
-                                                           float* pairs) {
+                                                           float* pairs, const unsigned* rn,
+                                                           int64_t rpb) {
   __shared__ float buf[2][SM_CHUNK];
   __shared__ float part[16];
   __shared__ float red[8];
   __shared__ int redi[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
+  if (past_real(rn, rpb, row)) return;
   const float* xr = logits + row * ld;
   float* pr = probs + row * ldo;
 
@@ -376,7 +386,8 @@ __device__ __forceinline__ float block_max_512(float v, float* red) {
 }
 
 __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, int cols, int ld,
-                                                          float* probs, int ldo, float* pairs) {
+                                                          float* probs, int ldo, float* pairs,
+                                                          const unsigned* rn, int64_t rpb) {
   __shared__ __attribute__((aligned(16))) float win[2][8 * SM_WIN_PITCH];
   __shared__ float part[16];
   __shared__ float red[8];
@@ -384,6 +395,7 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t row = blockIdx.x;
+  if (past_real(rn, rpb, row)) return;
   const int nu = (cols - tid + 511) >> 9;   // this thread's elements: u < nu
   // row to registers (out-of-range reads give 0 and are never used)
   float e[SM_REG_PER_THREAD];
@@ -524,7 +536,8 @@ __global__ __launch_bounds__(512) void softmax_reg_kernel(const float* logits, i
 #define SM_LDS_PER_THREAD 38            // ceil(SM_LDS_MAX_COLS / 512)
 
 __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, int cols, int ld,
-                                                          float* probs, int ldo, float* pairs) {
+                                                          float* probs, int ldo, float* pairs,
+                                                          const unsigned* rn, int64_t rpb) {
   __shared__ __attribute__((aligned(16))) float tr[8 * SM_TP];
   __shared__ float tail[8];
   __shared__ float red[8];
@@ -533,6 +546,7 @@ __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, i
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t row = blockIdx.x;
+  if (past_real(rn, rpb, row)) return;
   const int nu = (cols - tid + 511) >> 9;   // this thread's elements: u < nu
   float e[SM_LDS_PER_THREAD];
   {
@@ -651,10 +665,11 @@ __global__ __launch_bounds__(512) void softmax_lds_kernel(const float* logits, i
 #define SM_SMALL_MAX_COLS 128
 __global__ __launch_bounds__(256) void softmax_small_kernel(const float* logits, int64_t rows,
                                                             int cols, int64_t ld, float* probs,
-                                                            int64_t ldo, float* pairs) {
+                                                            int64_t ldo, float* pairs,
+                                                            const unsigned* rn, int64_t rpb) {
   const int j = threadIdx.x & 7;
   const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
-  const bool live = row < rows;
+  const bool live = row < rows && !past_real(rn, rpb, row);
   const float* xr = logits + (live ? row : 0) * ld;
   float* pr = probs + (live ? row : 0) * ldo;
   const int q = cols >= 8 ? cols / 8 : 0;  // full groups of eight
@@ -741,27 +756,28 @@ __global__ __launch_bounds__(256) void softmax_small_kernel(const float* logits,
 
 // logits rows ld floats apart (ld >= cols); probs rows ldo floats apart.
 int launch_softmax_pitched(const float* logits, int64_t rows, int64_t cols, int64_t ld,
-                           float* probs, int64_t ldo, float* pairs, hipStream_t s) {
+                           float* probs, int64_t ldo, float* pairs, hipStream_t s,
+                           const unsigned* rn, int64_t rpb) {
   if (rows > (1ll << 31)) return fail(QPH_EUNSUPPORTED, "softmax: too many rows");
   if (ld < cols || ldo < cols) return fail(QPH_EINVAL, "softmax: row pitch below the row width");
   if (probs == logits && ldo != ld) return fail(QPH_EINVAL, "softmax: in place with two pitches");
   if (cols <= SM_SMALL_MAX_COLS && probs) {
     hipLaunchKernelGGL(softmax_small_kernel, dim3(ceil_div(rows, 32)), dim3(256), 0, s, logits,
-                       rows, (int)cols, ld, probs, ldo, pairs);
+                       rows, (int)cols, ld, probs, ldo, pairs, rn, rpb);
     return launch_check("softmax_small_kernel");
   }
   if (cols <= SM_LDS_MAX_COLS && ld < (1ll << 31) && ldo < (1ll << 31)) {
     hipLaunchKernelGGL(softmax_lds_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
-                       (int)cols, (int)ld, probs, (int)ldo, pairs);
+                       (int)cols, (int)ld, probs, (int)ldo, pairs, rn, rpb);
     return launch_check("softmax_lds_kernel");
   }
   if (cols <= SM_REG_MAX_COLS && ld < (1ll << 31) && ldo < (1ll << 31)) {
     hipLaunchKernelGGL(softmax_reg_kernel, dim3((unsigned)rows), dim3(512), 0, s, logits,
-                       (int)cols, (int)ld, probs, (int)ldo, pairs);
+                       (int)cols, (int)ld, probs, (int)ldo, pairs, rn, rpb);
     return launch_check("softmax_reg_kernel");
   }
   hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols,
-                     ld, probs, ldo, pairs);
+                     ld, probs, ldo, pairs, rn, rpb);
   return launch_check("softmax_rows_kernel");
 }
 
@@ -1531,12 +1547,14 @@ struct MeanRows {
   int64_t rows, cols, rpg, gstride, rstride, estride;
   float* out;
   int64_t ostride;
+  const unsigned* rn;   // plan path: rows >= *rn * rpb skipped when *rn != 0
+  int64_t rpb;
 };
 
 __global__ __launch_bounds__(256) void reduce_mean_kernel(MeanRows p) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= p.rows) return;
+  if (row >= p.rows || past_real(p.rn, p.rpb, row)) return;
   const int64_t cols = p.cols, es = p.estride;
   const float* xr = p.x + (row / p.rpg) * p.gstride + (row % p.rpg) * p.rstride;
   double s = 0.0, sa = 0.0;
@@ -1575,6 +1593,7 @@ __global__ __launch_bounds__(256) void reduce_mean_wg_kernel(MeanRows p) {
   __shared__ int le[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
+  if (past_real(p.rn, p.rpb, row)) return;
   const int64_t cols = p.cols, es = p.estride;
   const float* xr = p.x + (row / p.rpg) * p.gstride + (row % p.rpg) * p.rstride;
   double s = 0.0, sa = 0.0;
@@ -1643,10 +1662,10 @@ __global__ __launch_bounds__(256) void reduce_mean_wg_kernel(MeanRows p) {
 
 int launch_reduce_mean_rows(const float* x, int64_t rows, int64_t cols, int64_t rpg,
                             int64_t gstride, int64_t rstride, int64_t estride, float* out,
-                            int64_t ostride, hipStream_t s) {
+                            int64_t ostride, hipStream_t s, const unsigned* rn, int64_t rpb) {
   if (rows >= (1ll << 33)) return fail(QPH_EUNSUPPORTED, "reduce_mean: too many rows");
   if (rows <= 0 || cols <= 0 || rpg <= 0) return fail(QPH_EINVAL, "reduce_mean: empty rows");
-  MeanRows p{x, rows, cols, rpg, gstride, rstride, estride, out, ostride};
+  MeanRows p{x, rows, cols, rpg, gstride, rstride, estride, out, ostride, rn, rpb};
   if (cols >= 1024 && rows < (1ll << 31)) {
     const bool vec = estride == 1 && (uintptr_t)x % 16 == 0 && gstride % 4 == 0 &&
                      rstride % 4 == 0;

@@ -633,6 +633,77 @@ def test_plan_attn_mm(gpu, oracle):
     assert_bitexact(mp.run()[0], ref, "batched matmul")
 
 
+@pytest.mark.parametrize("kind", ["softmax30", "softmax18709", "softmax20000", "softmax25001",
+                                  "reduce_last", "gap", "attn_qk", "attn_pv"])
+def test_plan_real_n_row_kernels(gpu, oracle, kind):
+    """Word 0 (real_n) also stops the softmax, the row means (n_reduce_last,
+    n_reduce_hw + n_reduce_fin) and the batched matmul (n_attn_mm) at the
+    real batch, as n_softmax / n_reduce_last / n_reduce_fin / n_attn_mm.comp
+    exit early: 3 batch items, real_n 1; the real rows bit-exact, the
+    padded items' outputs keep what the arena held."""
+    O = oracle
+    r = rng(len(kind))
+    mp = MiniPlan()
+    n = 3
+    S = 5.0
+    if kind.startswith("softmax"):
+        cols = int(kind[7:])
+        rpb = 2
+        rows = n * rpb
+        cp = (cols + 3) // 4 * 4
+        x = np.zeros((rows, cp), np.float32)
+        x[:, :cols] = rnd(r, (rows, cols), 3.0)
+        ref = x[:rpb, :cols].copy()
+        O.softmax_last_dim(ref, cols)
+        xo = mp.static(x)
+        yo = mp.static(np.full(rows * cp, S, np.float32))
+        mp.dispatch("n_softmax", [xo, yo, rows, cols, cp, rpb], (rows, 1, 1))
+        mp.output(yo, rows * cp, (rows, cp))
+        got = mp.run(real_n=1)[0]
+        assert_bitexact(got[:rpb, :cols], ref, "real rows")
+        assert np.all(got[rpb:] == S)
+    elif kind == "reduce_last":
+        rpb, cols, cp = 12, 30, 32
+        rows = n * rpb
+        x = np.zeros((rows, cp), np.float32)
+        x[:, :cols] = rnd(r, (rows, cols)) + 1.0
+        mean = O.reduce_mean_last(x[:rpb, :cols])
+        xo = mp.static(x)
+        mo = mp.static(np.full(rows * 4, S, np.float32))
+        mp.dispatch("n_reduce_last", [xo, mo, rows, cols, cp, rpb], (rows, 1, 1))
+        mp.output(mo, rows * 4, (rows, 4))
+        got = mp.run(real_n=1)[0]
+        assert_bitexact(got[:rpb, 0], mean, "real row means")
+        assert np.all(got[rpb:] == S)
+    elif kind == "gap":
+        c, h, w = 20, 33, 35
+        x = rnd(r, (n, c, h, w)) + 3.0
+        ref = O.global_avg_pool(x[:1]).reshape(1, c)
+        xo = mp.static(nhwc(x))
+        scratch = mp.alloc(n * ((h * w + 1023) // 1024) * c)
+        yo = mp.static(np.full(n * c, S, np.float32))
+        mp.dispatch("n_reduce_hw", [xo, scratch, h * w, c], ((h * w + 1023) // 1024, n, 1))
+        mp.dispatch("n_reduce_fin", [scratch, yo, (h * w + 1023) // 1024, c, h * w], (n, 1, 1))
+        mp.output(yo, n * c, (n, c))
+        got = mp.run(real_n=1)[0]
+        assert_bitexact(got[:1], ref, "real image")
+        assert np.all(got[1:] == S)
+    else:
+        heads, t, dh = 3, 12, 32 if kind == "attn_qk" else 8
+        kk, nn = (dh, t) if kind == "attn_qk" else (t, dh)
+        a = rnd(r, (n, heads, t, kk))
+        bm = rnd(r, (n, heads, kk, nn))
+        ref = O.matmul(a[:1], bm[:1])
+        ao = mp.static(a)
+        bo = mp.static(bm)
+        yo = mp.static(np.full(n * heads * t * nn, S, np.float32))
+        mp.dispatch("n_attn_mm", [ao, bo, yo, t, kk, nn, n * heads, heads], (1, n * heads * t, 1))
+        mp.output(yo, n * heads * t * nn, (n, heads, t, nn))
+        got = mp.run(real_n=1)[0]
+        assert_bitexact(got[:1], ref, "real batch item")
+        assert np.all(got[1:] == S)
+
+
 # ------------------------------------------------------------- data movement
 
 def test_plan_entry_exit_and_concat(gpu, oracle):
