@@ -95,6 +95,7 @@ HSW_CASES = [
     ("conv1x1", False, False),
     ("depthwise", False, False),
     ("linear", False, False),
+    ("dwpw", False, False),       # depthwise + 1x1 block: the fold rides on the block's launch
     ("conv3x3", True, False),
     ("conv3x3", False, True),
 ]
@@ -124,6 +125,13 @@ def test_session_hardswish_clip_fold(gpu, oracle, case):
             w = g.weight(r.kaiming((16, 1, 3, 3), 9))
             b = g.weight(r.normal((16,), 0.1))
             t = g.conv(0, w, b, stride=(2, 2), pad=(1, 1, 1, 1), group=16)
+        elif prod == "dwpw":
+            wd = g.weight(r.kaiming((16, 1, 3, 3), 9))
+            bd = g.weight(r.normal((16,), 0.1))
+            d = g.conv(0, wd, bd, pad=(1, 1, 1, 1), group=16, act=nets.ACT_HARDSWISH)
+            w = g.weight(r.kaiming((32, 16, 1, 1), 16))
+            b = g.weight(r.normal((32,), 0.1))
+            t = g.conv(d, w, b)
         else:
             w = g.weight(r.kaiming((20, 48), 20))
             b = g.weight(r.normal((48,), 0.1))
@@ -138,5 +146,8 @@ def test_session_hardswish_clip_fold(gpu, oracle, case):
     x = nets.WeightRng(24).normal(shape, 3.0)
     print(f"hardswish clip form after {case}", flush=True)
     launches = _run(g, x, lambda: build(1))
+    if prod == "dwpw":   # one launch: the block (two nodes) and the four folded nodes
+        assert launches == [(0, 6, 1)], launches
+        return
     assert ((0, 5, 1) in launches) == (not shared and not separate), launches
     assert len(launches) == (1 if (0, 5, 1) in launches else 5)
