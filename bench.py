@@ -22,7 +22,9 @@ value = steps per second = det images per second with 32 recognised lines
 each, over the wall time of the K steps; one_page_in_flight gives the same K
 steps on one det and one rec stream.  det_img_per_s and rec_lines_per_s are
 the stage-isolated rates (HIP events around each session alone, on its own
-stream).
+stream).  Defaults: K = 200 timed steps (about 60 ms) after W = 20 warm-up
+steps; the per-config, cls and aux legs take their repetitions from
+min(K, 50).
 
 roofline: the dominant kernel, the fused rec head (GEMM 1280 x 18709 x
 256, 12.26 GFLOP of the step's 20.86, with the softmax / argmax epilogue),
@@ -657,8 +659,8 @@ def cpu_mixed_page(data, rounds):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--pages-in-flight", type=int, default=2,
                     help="pages the timed headline keeps in flight, each on its own det and rec "
@@ -697,7 +699,7 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
     if args.aux_only:
-        print(json.dumps({"aux": bench_aux(ops, max(3, args.steps // 5))}))
+        print(json.dumps({"aux": bench_aux(ops, max(3, min(args.steps, 50) // 5))}))
         return
     ctx = ops.context(0)           # det stream
     ctx_rec = ops.new_context(0)   # rec stream
@@ -940,7 +942,7 @@ def main():
 
     cfgs = {}
     if not args.no_configs:
-        reps = max(3, K // 5)
+        reps = max(3, min(K, 50) // 5)
         cfgs["cfg1"] = bench_cfg1(nets, ops, configs, ctx, reps, args.cpu_rounds, O)
         cfgs.update(bench_cfg2(nets, ops, configs, ctx, reps, args.cpu_rounds, O))
     cfgs["cfg3"] = {"workload": "det 1x3x640x640 (seed 2)", "img_per_s": result["det_img_per_s"],
@@ -952,10 +954,10 @@ def main():
                     "classes": class_fractions(nets, rec_g, node_ms)}
     mixed_data = None
     if not args.no_configs:
-        cfgs["cfg5"], mixed_data = time_mixed_page(max(3, K // 5), 2)
-        cfgs["cfg5"]["engine_batching"], _ = time_mixed_page(max(3, K // 5), 2, engine=True,
+        cfgs["cfg5"], mixed_data = time_mixed_page(max(3, min(K, 50) // 5), 2)
+        cfgs["cfg5"]["engine_batching"], _ = time_mixed_page(max(3, min(K, 50) // 5), 2, engine=True,
                                                              data=mixed_data)
-        cfgs["cls"] = bench_cls(nets, lib, torch, ctx, max(3, K // 2), args.cpu_rounds, O)
+        cfgs["cls"] = bench_cls(nets, lib, torch, ctx, max(3, min(K, 50) // 2), args.cpu_rounds, O)
 
     if O is not None:
         det_s, det_n = cpu_sample(lambda: onets.run_graph(det_g, det_x), args.cpu_rounds,
@@ -980,7 +982,7 @@ def main():
         }
     result["configs"] = cfgs
     if not args.no_configs:
-        result["aux"] = bench_aux(ops, max(3, K // 5), O, args.cpu_rounds)
+        result["aux"] = bench_aux(ops, max(3, min(K, 50) // 5), O, args.cpu_rounds)
     print(json.dumps(result))
     det.close()
     rec.close()
