@@ -798,7 +798,10 @@ __global__ __launch_bounds__(256) void plan_stem_kernel(ConvK p) {
 // instead of once per tap and output block.
 #define HALO_CG 2   // channel groups per stage
 #define HALO_D 3    // DMA ring depth
-#define HALO_LEAD 6 // steps the operand reads run ahead
+// steps the operand reads run ahead: with the waves of several workgroups
+// interleaving on each SIMD, two measured faster than three or six (the det
+// head conv 30.7 -> 29.5 us, the neck group 38.6 -> 37.8 us, trace medians)
+#define HALO_LEAD 2
 template <int SW, int NCB>
 struct HaloGeom {
   static constexpr int W = 2 * NCB;                    // waves
